@@ -1,0 +1,232 @@
+"""Shrimp forward benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds T]
+
+Workload: ShrimpNet(channels=128, heads=8, trunk "CCACCACCACCA") serve forward
+(forward_policy_value: policy logits + value logits) at B=512 positions,
+Npad=256 (S=264), bf16 kernels, seeded random-init weights, seeded synthetic
+positions (shrimp.synthetic "cfg4": 10-80 stones, support radius 4, L256
+capped). Inputs are device-resident before timing. One step = one forward.
+
+Prints one JSON line with the metric, the per-kernel roofline of the
+dominant kernel (the trunk hex conv, timed live with HIP events on the
+launch stream), the attention kernel's figures, and the CPU baseline (the
+oracle's fp32 eager forward on a bounded sample, rank 0 only).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT), str(ROOT / "hexo-bot_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "Shrimp fwd positions/sec @B=512 bf16 on 1 MI355X; attn/conv % MFMA peak"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+B, NPAD, C, H, LAYOUT = 512, 256, 128, 8, "CCACCACCACCA"
+
+
+def _events_time(fn, reps, stream):
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def kernel_timings(net, inputs, reps=50):
+    """Re-launch the trunk conv (ConvBlock conv1: conv + LN + ReLU + mask) and
+    the attention kernel of block 0 on the forward's own buffers; average
+    duration per launch from HIP events on the launch stream."""
+
+    import torch
+
+    from shrimp import ops
+    from shrimp.geometry import CELL_LUT_M
+
+    rt = net.hip_runtime()
+    rt.keep_buffers = True
+    net.forward_policy_value(*inputs)
+    L = rt.last
+    rt.keep_buffers = False
+    P = L["P"]
+    b, n, s = L["B"], L["N"], L["S"]
+    cells = L["seq"][:, 8:]
+    k = P.convs[0]
+    stream = torch.cuda.current_stream()
+
+    def conv():
+        ops.launch_conv(
+            x=cells, x_sb=s * C, x_sn=C, idx=L["idx"], taps=7, idx_stride=7, mask8=L["mask8"],
+            wpack=k.w1, bias=k.b1, B=b, N=n, cin_pad=C, cout=C, ln_w=k.ln1w, ln_b=k.ln1b,
+            eps=k.eps1, relu=True, out=L["y1"], o_sb=n * C, o_sn=C, stream=L["stream"],
+        )
+
+    a = P.attn[0]
+    qkv = L["qkv"]
+
+    def attn():
+        ops.launch_attn(
+            q=qkv[0], k=qkv[1], v=qkv[2], qkv_sb=H * s * P.dpad, qkv_sh=s * P.dpad,
+            seq_lens=L["seq_lens"], o=L["att"], o_sb=s * C, o_sh=P.d, o_sr=C, B=b, S=s, H=H,
+            d=P.d, dpad=P.dpad, coords=L["coords32"], mask8=L["mask8"], btab=a.btab,
+            lut_m=CELL_LUT_M, n_tokens=8, stream=L["stream"],
+        )
+
+    conv()
+    attn()
+    conv_ms = _events_time(conv, reps, stream)
+    attn_ms = _events_time(attn, reps, stream)
+    seq_lens = L["seq_lens"].cpu().to(torch.float64)
+    valid_rows = int(L["mask8"].sum().item())
+    return {
+        "conv_ms": conv_ms,
+        "conv_flops": 2.0 * 7 * C * C * b * n,
+        "conv_flops_valid": 2.0 * 7 * C * C * valid_rows,
+        "conv_bytes": b * n * C * 2 * 2 + b * n * 7 * 4 + 7 * C * C * 2,
+        "attn_ms": attn_ms,
+        "attn_flops": float(4 * P.d * H * (seq_lens ** 2).sum().item()),
+        "attn_bytes": float(4 * 2 * P.d * H * seq_lens.sum().item()),
+    }
+
+
+def cpu_baseline(batch, seconds: float):
+    """Oracle fp32 eager forward (the reference CPU path, restated) on a
+    bounded sample of the same workload; positions/s on the host cores."""
+
+    import torch
+
+    from oracle import forward as ofwd
+    from oracle import weights
+
+    threads = int(os.environ.get("SHRIMP_CPU_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    sample = 8
+    sd = weights.make_state_dict(C, H, LAYOUT, seed=0, mode="fresh")
+    args = [batch[k][:sample] for k in ("feats", "nbr", "mask", "coords")]
+    ofwd.forward_policy_value(sd, LAYOUT, H, *args, dtype=torch.float32)
+    runs = 0
+    t0 = time.perf_counter()
+    while True:
+        ofwd.forward_policy_value(sd, LAYOUT, H, *args, dtype=torch.float32)
+        runs += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {
+        "value": round(sample * runs / el, 3),
+        "unit": "positions/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{runs} forwards x {sample} cfg4 positions (fp32 eager oracle, {el:.1f} s)",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            "bench.py measures one MI355X: the Shrimp forward shards by position with no "
+            "collective, and this build runs single-GPU only (--gpus 1).",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from shrimp import _lib, synthetic
+    from shrimp.model import ShrimpNet
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    net = ShrimpNet(channels=C, attention_heads=H, trunk_layout=LAYOUT).to(dev).eval()
+    batch = synthetic.position_batch("cfg4", B)
+    inputs = (
+        batch["feats"].to(dev, torch.float16),
+        batch["nbr"].to(dev, torch.int32),
+        batch["mask"].to(dev),
+        batch["coords"].to(dev, torch.int32),
+    )
+    for _ in range(args.warmup):
+        net.forward_policy_value(*inputs)
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    t0 = time.perf_counter()
+    ms = _events_time(lambda: net.forward_policy_value(*inputs), args.steps, stream)
+    torch.cuda.synchronize(dev)
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    kt = kernel_timings(net, inputs)
+
+    conv_tflops = kt["conv_flops"] / (kt["conv_ms"] * 1e-3) / 1e12
+    attn_tflops = kt["attn_flops"] / (kt["attn_ms"] * 1e-3) / 1e12
+    traffic = None
+    tfile = ROOT / "profiles" / "conv_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
+    line = {
+        "metric": METRIC,
+        "value": round(B / (ms * 1e-3), 1),
+        "unit": "positions/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "wall_ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "shrimp_forward_policy_value_cfg4",
+            "positions": B, "npad": NPAD, "seq_len": NPAD + 8, "channels": C, "heads": H,
+            "trunk": LAYOUT, "support_radius": 4, "generator": "l256 seed 20261205",
+        },
+        "roofline": {
+            "kernel": "hex_conv_kernel<128,4,LN|RELU> (ConvBlock conv1, B=512 x 256 rows)",
+            "bound": "mfma",
+            "achieved": round(conv_tflops, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(conv_tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic,
+            "launch_ms": round(kt["conv_ms"], 5),
+            "flops_per_launch": kt["conv_flops"],
+        },
+        "attention": {
+            "kernel": "attn_kernel<16,2,coords> (block 0)",
+            "launch_ms": round(kt["attn_ms"], 5),
+            "tflops": round(attn_tflops, 2),
+            "mfma_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+            "hbm_gbs_algorithmic": round(kt["attn_bytes"] / (kt["attn_ms"] * 1e-3) / 1e9, 1),
+        },
+        "forward_tflops_padded": round(1.425e9 * B / (ms * 1e-3) / 1e12, 2),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(batch, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

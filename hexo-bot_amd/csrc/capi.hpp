@@ -1,0 +1,30 @@
+// Host-side helpers shared by the C-ABI entry points: per-thread error text,
+// launch checking and argument validation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "shrimp_hip.h"
+
+namespace shrimp {
+
+int set_error(int code, const char* fmt, ...);
+
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(SHRIMP_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return SHRIMP_OK;
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace shrimp
+
+#define SHRIMP_REQUIRE(cond, ...)                                 \
+  do {                                                            \
+    if (!(cond)) return ::shrimp::set_error(SHRIMP_EINVAL, __VA_ARGS__); \
+  } while (0)

@@ -1,0 +1,105 @@
+// Shared device helpers for the Shrimp gfx950 kernels.
+//
+// Conventions used by every kernel in this directory:
+//  * wave64; MFMA operands follow the CDNA lane layouts: for a 16x16xK tile
+//    lane l supplies row/col (l % 16) and the K slice owned by lane group
+//    (l / 16); the 16x16 f32 result gives lane l rows 4*(l/16)+j (j=0..3) of
+//    column (l % 16).
+//  * activations are bf16, accumulation and all statistics fp32.
+//  * gathered reads go through buffer resources: an offset past the record
+//    count returns zeros, so a missing neighbour (index >= N) is a zero row
+//    by construction and no gathered read can leave its buffer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
+
+#define SHRIMP_DEV __device__ __forceinline__
+
+// Buffer resource word 3 for gfx9-family raw buffers (no format conversion).
+#define SHRIMP_RSRC_W3 0x00020000
+
+// Offset used for "absent" rows: far past any record count.
+#define SHRIMP_OOB_OFFSET 0x7FFFFF00u
+
+SHRIMP_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           SHRIMP_RSRC_W3);
+}
+
+SHRIMP_DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+}
+SHRIMP_DEV u32x2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 0);
+}
+SHRIMP_DEV unsigned buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0);
+}
+
+// ---- bf16 <-> f32 -----------------------------------------------------------
+
+SHRIMP_DEV float bf16_lo(unsigned w) { return __uint_as_float(w << 16); }
+SHRIMP_DEV float bf16_hi(unsigned w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// Round-to-nearest-even pack of two floats into one dword of bf16 (lo, hi);
+// lowers to v_cvt_pk_bf16_f32 on gfx950.
+SHRIMP_DEV unsigned pack_bf16x2(float lo, float hi) {
+  bf16x2 v;
+  v.x = (__bf16)lo;
+  v.y = (__bf16)hi;
+  return __builtin_bit_cast(unsigned, v);
+}
+
+SHRIMP_DEV unsigned short f32_to_bf16_bits(float f) {
+  __bf16 b = (__bf16)f;
+  return __builtin_bit_cast(unsigned short, b);
+}
+
+SHRIMP_DEV float bf16_bits_to_f32(unsigned short h) {
+  return __uint_as_float(((unsigned)h) << 16);
+}
+
+// ---- MFMA wrappers -------------------------------------------------------------
+
+SHRIMP_DEV f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+SHRIMP_DEV f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                   __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+}
+
+// ---- cross-lane -----------------------------------------------------------------
+
+SHRIMP_DEV float xor_shfl(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+// Sum over the 4 lane groups (l/16 = 0..3) sharing the same l % 16.
+SHRIMP_DEV float sum_lane_groups(float v) {
+  v += xor_shfl(v, 16);
+  v += xor_shfl(v, 32);
+  return v;
+}
+SHRIMP_DEV float max_lane_groups(float v) {
+  v = fmaxf(v, xor_shfl(v, 16));
+  v = fmaxf(v, xor_shfl(v, 32));
+  return v;
+}
+
+SHRIMP_DEV float wave_sum(float v) {
+  for (int m = 32; m >= 1; m >>= 1) v += xor_shfl(v, m);
+  return v;
+}
+
+// erf-based GELU (torch.nn.functional.gelu default, approximate='none').
+SHRIMP_DEV float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }

@@ -1,0 +1,420 @@
+// Small per-position kernels around the Shrimp forward: input preparation,
+// token rows, the trunk tail (final LayerNorm + pooled value head), serve
+// decode, and the pair / ray index builders. One workgroup per position; all
+// are bandwidth-trivial next to the conv and attention kernels.
+#include "capi.hpp"
+#include "common.hpp"
+
+namespace shrimp {
+
+__device__ __forceinline__ int64_t load_index(const void* p, int dt, int64_t i) {
+  switch (dt) {
+    case SHRIMP_DT_I64: return static_cast<const int64_t*>(p)[i];
+    case SHRIMP_DT_I32: return static_cast<const int32_t*>(p)[i];
+    case SHRIMP_DT_U16: {
+      const unsigned v = static_cast<const uint16_t*>(p)[i];
+      return v == 0xFFFFu ? -1 : (int64_t)v;
+    }
+    default: return -1;
+  }
+}
+
+__device__ __forceinline__ float load_feat(const void* p, int dt, int64_t i) {
+  switch (dt) {
+    case SHRIMP_DT_F32: return static_cast<const float*>(p)[i];
+    case SHRIMP_DT_F16: return (float)static_cast<const _Float16*>(p)[i];
+    case SHRIMP_DT_BF16: return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+    default: return 0.f;
+  }
+}
+
+// ---- input preparation (model.py:861-863, 884-892; batching.py:264-276) --------
+__global__ __launch_bounds__(256) void prep_kernel(const void* nbr, int nbr_dt, const void* mask,
+                                                   const void* coords, int coords_dt,
+                                                   const void* feats, int feats_dt, int nfeat,
+                                                   int N, int n_tokens, int32_t* idx,
+                                                   uint8_t* mask8, int32_t* coords32,
+                                                   int32_t* seq_lens, uint8_t* seq_mask,
+                                                   uint16_t* xin) {
+  const int b = blockIdx.x;
+  const int64_t base = (int64_t)b * N;
+  if (seq_mask)
+    for (int t = threadIdx.x; t < n_tokens; t += blockDim.x)
+      seq_mask[(int64_t)b * (n_tokens + N) + t] = 1;
+  int last = 0;  // 1 + index of the last live cell
+  for (int n = threadIdx.x; n < N; n += blockDim.x) {
+    const int64_t r = base + n;
+    const bool live = static_cast<const uint8_t*>(mask)[r] != 0;
+    if (live) last = n + 1;
+    if (mask8) mask8[r] = live ? 1 : 0;
+    if (seq_mask) seq_mask[(int64_t)b * (n_tokens + N) + n_tokens + n] = live ? 1 : 0;
+    if (idx) {
+      idx[r * 7] = n;
+#pragma unroll
+      for (int k = 0; k < 6; ++k) {
+        const int64_t j = load_index(nbr, nbr_dt, r * 6 + k);
+        idx[r * 7 + 1 + k] = (j >= 0 && j < N) ? (int32_t)j : N;
+      }
+    }
+    if (coords32) {
+      coords32[r * 2] = (int32_t)load_index(coords, coords_dt, r * 2);
+      coords32[r * 2 + 1] = (int32_t)load_index(coords, coords_dt, r * 2 + 1);
+    }
+    if (xin) {
+#pragma unroll 4
+      for (int f = 0; f < 32; f += 2) {
+        const float v0 = f < nfeat ? load_feat(feats, feats_dt, r * nfeat + f) : 0.f;
+        const float v1 = f + 1 < nfeat ? load_feat(feats, feats_dt, r * nfeat + f + 1) : 0.f;
+        reinterpret_cast<unsigned*>(xin + r * 32)[f / 2] = pack_bf16x2(v0, v1);
+      }
+    }
+  }
+  if (seq_lens) {
+    __shared__ int red[256];
+    red[threadIdx.x] = last;
+    __syncthreads();
+    for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+      if ((int)threadIdx.x < s) red[threadIdx.x] = max(red[threadIdx.x], red[threadIdx.x + s]);
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) seq_lens[b] = n_tokens + red[0];
+  }
+}
+
+__global__ void fill_tokens_kernel(const float* __restrict__ tokens, int n_tokens, int C,
+                                   uint16_t* __restrict__ seq, int64_t seq_sb) {
+  const int b = blockIdx.x;
+  for (int i = threadIdx.x; i < n_tokens * C; i += blockDim.x)
+    seq[(int64_t)b * seq_sb + i] = f32_to_bf16_bits(tokens[i]);
+}
+
+// ---- trunk tail + value heads (model.py:927-935, 990-1002) --------------------
+// Dynamic LDS: vin[3C] (value input), mlin[3C] (moves-left input), hid[C].
+__global__ __launch_bounds__(256) void tail_kernel(const shrimp_tail_args a) {
+  extern __shared__ float sm[];
+  const int C = a.C;
+  float* vin = sm;            // [T0 | T1 | pooled]
+  float* mlin = sm + 3 * C;   // [T4 | T5 | pooled]
+  float* hid = sm + 6 * C;    // [C]
+  float* pool = sm + 7 * C;   // [4][C] per-wave partial sums
+  __shared__ int cnt_w[4];
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int S = a.S, nt = a.n_tokens, N = S - nt;
+  const uint16_t* seq = static_cast<const uint16_t*>(a.seq) + (int64_t)b * a.s_sb;
+  uint16_t* outs = static_cast<uint16_t*>(a.out_seq) + (int64_t)b * a.s_sb;
+  const int per = (C + 63) / 64;  // channels per lane (<= 4)
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  int cnt = 0;
+  for (int row = wave; row < S; row += 4) {
+    float x[4];
+    float s = 0.f;
+    for (int u = 0; u < per; ++u) {
+      const int c = lane + 64 * u;
+      x[u] = c < C ? bf16_bits_to_f32(seq[(int64_t)row * C + c]) : 0.f;
+      s += x[u];
+    }
+    const float mean = wave_sum(s) / C;
+    float q = 0.f;
+    for (int u = 0; u < per; ++u) {
+      const int c = lane + 64 * u;
+      x[u] = c < C ? x[u] - mean : 0.f;
+      q += x[u] * x[u];
+    }
+    const float rstd = rsqrtf(wave_sum(q) / C + a.eps);
+    const bool is_cell = row >= nt;
+    const bool live = !is_cell || a.mask[(int64_t)b * N + (row - nt)] != 0;
+    if (is_cell && live) ++cnt;
+    for (int u = 0; u < per; ++u) {
+      const int c = lane + 64 * u;
+      if (c >= C) continue;
+      float y = x[u] * rstd * a.ln_w[c] + a.ln_b[c];
+      if (!live) y = 0.f;
+      outs[(int64_t)row * C + c] = f32_to_bf16_bits(y);
+      if (is_cell) acc[u] += y;
+      if (row == 0) vin[c] = y;
+      if (row == 1) vin[C + c] = y;
+      if (row == 4) mlin[c] = y;
+      if (row == 5) mlin[C + c] = y;
+    }
+  }
+  for (int u = 0; u < per; ++u) {
+    const int c = lane + 64 * u;
+    if (c < C) pool[wave * C + c] = acc[u];
+  }
+  if (lane == 0) cnt_w[wave] = cnt;
+  __syncthreads();
+  const int count = max(1, cnt_w[0] + cnt_w[1] + cnt_w[2] + cnt_w[3]);
+  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    const float p = (pool[c] + pool[C + c] + pool[2 * C + c] + pool[3 * C + c]) / (float)count;
+    vin[2 * C + c] = p;
+    mlin[2 * C + c] = p;
+  }
+  __syncthreads();
+  // value_reduction (C x 3C) + ReLU, then value_head (bins x C)
+  for (int pass = 0; pass < 2; ++pass) {
+    const float* rw = pass == 0 ? a.vr_w : a.mr_w;
+    const float* rb = pass == 0 ? a.vr_b : a.mr_b;
+    const float* hw = pass == 0 ? a.vh_w : a.mh_w;
+    const float* hb = pass == 0 ? a.vh_b : a.mh_b;
+    float* dst = pass == 0 ? a.value : a.moves_left;
+    const float* in = pass == 0 ? vin : mlin;
+    if (dst == nullptr) continue;
+    for (int o = wave; o < C; o += 4) {
+      float s = 0.f;
+      for (int k = lane; k < 3 * C; k += 64) s += rw[(int64_t)o * 3 * C + k] * in[k];
+      s = wave_sum(s);
+      if (lane == 0) hid[o] = fmaxf(s + rb[o], 0.f);
+    }
+    __syncthreads();
+    for (int o = wave; o < a.bins; o += 4) {
+      float s = 0.f;
+      for (int k = lane; k < C; k += 64) s += hw[(int64_t)o * C + k] * hid[k];
+      s = wave_sum(s);
+      if (lane == 0) dst[(int64_t)b * a.bins + o] = s + hb[o];
+    }
+    __syncthreads();
+  }
+}
+
+// ---- serve decode (inference.py:998-1042, losses.py:40-60) ---------------------
+__device__ float block_reduce(float v, bool is_max, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float o = __shfl_xor(v, m, 64);
+    v = is_max ? fmaxf(v, o) : v + o;
+  }
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+  return r;
+}
+
+__device__ float decode_expectation(const float* logits, int bins, float* red) {
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < bins; i += blockDim.x) mx = fmaxf(mx, logits[i]);
+  mx = block_reduce(mx, true, red);
+  float se = 0.f, sv = 0.f;
+  const float step = 2.0f / (float)(bins - 1);
+  for (int i = threadIdx.x; i < bins; i += blockDim.x) {
+    const float e = expf(logits[i] - mx);
+    const float bin = (2 * i < bins) ? -1.0f + step * i : 1.0f - step * (bins - 1 - i);
+    se += e;
+    sv += e * bin;
+  }
+  se = block_reduce(se, false, red);
+  sv = block_reduce(sv, false, red);
+  const float v = sv / se;
+  return fminf(fmaxf(v, -1.0f), 1.0f);
+}
+
+__global__ __launch_bounds__(256) void decode_kernel(const float* value_logits,
+                                                     const float* ml_logits, const float* policy,
+                                                     int64_t pol_sb, const int32_t* legal,
+                                                     const int64_t* out_off, int bins,
+                                                     float ml_cap, float* value, float* ml,
+                                                     float* priors, float* logits_out) {
+  __shared__ float red[8];
+  const int b = blockIdx.x;
+  const float v = decode_expectation(value_logits + (int64_t)b * bins, bins, red);
+  if (threadIdx.x == 0) value[b] = v;
+  if (ml_logits != nullptr) {
+    const float u = decode_expectation(ml_logits + (int64_t)b * bins, bins, red);
+    if (threadIdx.x == 0) ml[b] = (u + 1.0f) * 0.5f * ml_cap;
+  }
+  // The legal prefix never extends past the row (pol_sb == Npad here).
+  const int L = max(0, min(legal[b], (int)pol_sb));
+  const float* row = policy + (int64_t)b * pol_sb;
+  float* dst = priors + out_off[b];
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < L; i += blockDim.x) mx = fmaxf(mx, row[i]);
+  mx = block_reduce(mx, true, red);
+  float se = 0.f;
+  for (int i = threadIdx.x; i < L; i += blockDim.x) se += expf(row[i] - mx);
+  se = block_reduce(se, false, red);
+  const float inv = 1.0f / se;
+  for (int i = threadIdx.x; i < L; i += blockDim.x) {
+    dst[i] = expf(row[i] - mx) * inv;
+    if (logits_out != nullptr) logits_out[out_off[b] + i] = row[i];
+  }
+}
+
+// ---- pair index (model.py:762-792) ------------------------------------------------
+__global__ void pair_kernel(const int32_t* coords, const uint8_t* mask, const uint8_t* lut,
+                            int M, int N, int nt, int r_ct, int r_tc, int r_tt, int pad_row,
+                            uint8_t* pair) {
+  const int b = blockIdx.y;
+  const int i = blockIdx.x;  // query row
+  const int S = nt + N;
+  const int W = 2 * M + 1;
+  for (int j = threadIdx.x; j < S; j += blockDim.x) {
+    int row;
+    const bool qt = i < nt, kt = j < nt;
+    if (qt && kt) row = r_tt;
+    else if (qt) row = r_tc;
+    else if (kt) row = r_ct;
+    else {
+      const int64_t ci = (int64_t)b * N + (i - nt), cj = (int64_t)b * N + (j - nt);
+      int dq = coords[cj * 2] - coords[ci * 2];
+      int dr = coords[cj * 2 + 1] - coords[ci * 2 + 1];
+      dq = dq < -M ? -M : (dq > M ? M : dq);
+      dr = dr < -M ? -M : (dr > M ? M : dr);
+      row = lut[(dq + M) * W + (dr + M)];
+    }
+    if (!kt && mask[(int64_t)b * N + (j - nt)] == 0) row = pad_row;
+    pair[((int64_t)b * S + i) * S + j] = (uint8_t)row;
+  }
+}
+
+// ---- ray gather index (hexfield_eq/_triton_ray.py:221-281) ------------------------
+// Per position: an LDS open-addressing table of live cells keyed by packed
+// (q, r), then one probe per (cell, slot). Coordinates must satisfy
+// |q|, |r| < 2^14; cells outside that domain are never matched.
+#define RAY_TABLE 4096
+__device__ __forceinline__ unsigned ray_key(int q, int r) {
+  if (q <= -16384 || q >= 16384 || r <= -16384 || r >= 16384) return 0u;
+  return ((unsigned)(q + 16384) << 15 | (unsigned)(r + 16384)) + 1u;
+}
+__device__ __forceinline__ unsigned ray_hash(unsigned k) { return (k * 2654435761u) >> 20; }
+
+__global__ __launch_bounds__(256) void ray_index_kernel(const int32_t* coords, const uint8_t* mask,
+                                                        int N, int32_t* idx) {
+  __shared__ unsigned keys[RAY_TABLE];
+  __shared__ int vals[RAY_TABLE];
+  const int b = blockIdx.x;
+  for (int i = threadIdx.x; i < RAY_TABLE; i += blockDim.x) keys[i] = 0u;
+  __syncthreads();
+  for (int n = threadIdx.x; n < N; n += blockDim.x) {
+    const int64_t r = (int64_t)b * N + n;
+    if (!mask[r]) continue;
+    const unsigned k = ray_key(coords[r * 2], coords[r * 2 + 1]);
+    if (k == 0u) continue;
+    unsigned h = ray_hash(k) & (RAY_TABLE - 1);
+    for (int probe = 0; probe < RAY_TABLE; ++probe) {
+      const unsigned prev = atomicCAS(&keys[h], 0u, k);
+      if (prev == 0u || prev == k) {
+        vals[h] = n;
+        break;
+      }
+      h = (h + 1) & (RAY_TABLE - 1);
+    }
+  }
+  __syncthreads();
+  const int ax_q[3] = {1, 0, 1}, ax_r[3] = {0, 1, -1};
+  for (int i = threadIdx.x; i < N * 32; i += blockDim.x) {
+    const int n = i >> 5;
+    const int s = i & 31;
+    const int64_t r = (int64_t)b * N + n;
+    int out = N;
+    if (s == 0) {
+      out = n;
+    } else if (s < 31) {
+      const int t = s - 1;
+      const int axis = t / 10, dir = (t % 10) / 5, k = t % 5 + 1;
+      const int sgn = dir == 0 ? 1 : -1;
+      const unsigned key =
+          ray_key(coords[r * 2] + sgn * k * ax_q[axis], coords[r * 2 + 1] + sgn * k * ax_r[axis]);
+      if (key != 0u) {
+        unsigned h = ray_hash(key) & (RAY_TABLE - 1);
+        for (int probe = 0; probe < RAY_TABLE; ++probe) {
+          const unsigned kk = keys[h];
+          if (kk == key) {
+            out = vals[h];
+            break;
+          }
+          if (kk == 0u) break;
+          h = (h + 1) & (RAY_TABLE - 1);
+        }
+      }
+    }
+    idx[r * 32 + s] = out;
+  }
+}
+
+}  // namespace shrimp
+
+using namespace shrimp;
+
+extern "C" int shrimp_prep_inputs(const void* nbr, int nbr_dt, const void* mask, const void* coords,
+                                  int coords_dt, const void* feats, int feats_dt, int nfeat, int B,
+                                  int N, int n_tokens, int32_t* idx, uint8_t* mask8,
+                                  int32_t* coords32, int32_t* seq_lens, uint8_t* seq_mask,
+                                  void* xin, void* stream) {
+  SHRIMP_REQUIRE(B >= 0 && N > 0, "prep_inputs: bad shape (%d, %d)", B, N);
+  if (B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(mask != nullptr, "prep_inputs: mask required");
+  SHRIMP_REQUIRE(!idx || (nbr && (nbr_dt == SHRIMP_DT_I64 || nbr_dt == SHRIMP_DT_I32 ||
+                                  nbr_dt == SHRIMP_DT_U16)),
+                 "prep_inputs: nbr dtype");
+  SHRIMP_REQUIRE(!coords32 || (coords && (coords_dt == SHRIMP_DT_I64 || coords_dt == SHRIMP_DT_I32)),
+                 "prep_inputs: coords dtype");
+  SHRIMP_REQUIRE(!xin || (feats && nfeat > 0 && nfeat <= 32 &&
+                          (feats_dt == SHRIMP_DT_F32 || feats_dt == SHRIMP_DT_F16 ||
+                           feats_dt == SHRIMP_DT_BF16)),
+                 "prep_inputs: feats dtype / width");
+  hipLaunchKernelGGL(prep_kernel, dim3(B), dim3(256), 0, as_stream(stream), nbr, nbr_dt, mask,
+                     coords, coords_dt, feats, feats_dt, nfeat, N, n_tokens, idx, mask8, coords32,
+                     seq_lens, seq_mask, static_cast<uint16_t*>(xin));
+  return check_launch("prep_inputs");
+}
+
+extern "C" int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void* seq,
+                                  int64_t seq_sb, int B, void* stream) {
+  SHRIMP_REQUIRE(tokens && seq, "fill_tokens: null pointer");
+  if (B == 0 || n_tokens == 0) return SHRIMP_OK;
+  hipLaunchKernelGGL(fill_tokens_kernel, dim3(B), dim3(256), 0, as_stream(stream), tokens,
+                     n_tokens, C, static_cast<uint16_t*>(seq), seq_sb);
+  return check_launch("fill_tokens");
+}
+
+extern "C" int shrimp_trunk_tail(const shrimp_tail_args* a, void* stream) {
+  SHRIMP_REQUIRE(a != nullptr, "trunk_tail: null args");
+  if (a->B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(a->seq && a->mask && a->ln_w && a->ln_b && a->out_seq, "trunk_tail: null pointer");
+  SHRIMP_REQUIRE(a->C > 0 && a->C <= 256, "trunk_tail: C %d outside (0, 256]", a->C);
+  SHRIMP_REQUIRE(a->n_tokens >= 6 && a->S > a->n_tokens, "trunk_tail: needs >= 6 tokens");
+  SHRIMP_REQUIRE(!a->value || (a->vr_w && a->vr_b && a->vh_w && a->vh_b), "trunk_tail: value head");
+  SHRIMP_REQUIRE(!a->moves_left || (a->mr_w && a->mr_b && a->mh_w && a->mh_b),
+                 "trunk_tail: moves-left head");
+  const size_t smem = (size_t)(7 * a->C + 4 * a->C) * sizeof(float);
+  hipLaunchKernelGGL(tail_kernel, dim3(a->B), dim3(256), smem, as_stream(stream), *a);
+  return check_launch("trunk_tail");
+}
+
+extern "C" int shrimp_decode(const float* value_logits, const float* ml_logits,
+                             const float* policy, int64_t pol_sb, const int32_t* legal,
+                             const int64_t* out_off, int B, int bins, float ml_cap, float* value,
+                             float* ml, float* priors, float* logits_out, void* stream) {
+  if (B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(value_logits && policy && legal && out_off && value && priors,
+                 "decode: null pointer");
+  SHRIMP_REQUIRE(!ml_logits || ml, "decode: ml output missing");
+  SHRIMP_REQUIRE(bins >= 2, "decode: bins %d", bins);
+  hipLaunchKernelGGL(decode_kernel, dim3(B), dim3(256), 0, as_stream(stream), value_logits,
+                     ml_logits, policy, pol_sb, legal, out_off, bins, ml_cap, value, ml, priors,
+                     logits_out);
+  return check_launch("decode");
+}
+
+extern "C" int shrimp_build_pair_u8(const int32_t* coords, const uint8_t* mask, const uint8_t* lut,
+                                    int lut_m, int B, int N, int n_tokens, int row_ct, int row_tc,
+                                    int row_tt, int pad_row, uint8_t* pair, void* stream) {
+  if (B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(coords && mask && lut && pair, "build_pair_u8: null pointer");
+  dim3 grid(n_tokens + N, B);
+  hipLaunchKernelGGL(pair_kernel, grid, dim3(256), 0, as_stream(stream), coords, mask, lut, lut_m,
+                     N, n_tokens, row_ct, row_tc, row_tt, pad_row, pair);
+  return check_launch("build_pair_u8");
+}
+
+extern "C" int shrimp_build_ray_index(const int32_t* coords, const uint8_t* mask, int B, int N,
+                                      int32_t* idx, void* stream) {
+  if (B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(coords && mask && idx, "build_ray_index: null pointer");
+  SHRIMP_REQUIRE(N > 0 && 2 * N <= RAY_TABLE, "build_ray_index: N %d exceeds %d", N, RAY_TABLE / 2);
+  hipLaunchKernelGGL(ray_index_kernel, dim3(B), dim3(256), 0, as_stream(stream), coords, mask, N,
+                     idx);
+  return check_launch("build_ray_index");
+}

@@ -1,0 +1,152 @@
+"""ctypes binding of ``libshrimp_hip.so`` (the C ABI in ``include/shrimp_hip.h``).
+
+The library is built in-tree (``hexo-bot_amd/shrimp/_lib/``) by
+``__graft_entry__.build()`` / ``make -C hexo-bot_amd/csrc``. There is no
+fallback: if the library is missing every GPU entry point raises, naming the
+build step.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_DIR = Path(__file__).resolve().parent / "_lib"
+LIB_PATH = LIB_DIR / "libshrimp_hip.so"
+
+DT_BF16, DT_F32, DT_F16, DT_I64, DT_I32, DT_U16, DT_U8 = range(7)
+LIN_PLAIN, LIN_GELU, LIN_RESID, LIN_QKV = range(4)
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+
+
+class ConvArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", _vp), ("x_sb", _i64), ("x_sn", _i64),
+        ("idx", _vp), ("taps", _i32), ("idx_stride", _i32),
+        ("mask", _vp), ("w", _vp), ("bias", _vp),
+        ("ln_w", _vp), ("ln_b", _vp), ("eps", _f32), ("relu", _i32),
+        ("resid", _vp), ("r_sb", _i64), ("r_sn", _i64), ("gamma", _vp),
+        ("head_w", _vp), ("head_b", _vp), ("head_out", _vp),
+        ("out", _vp), ("o_sb", _i64), ("o_sn", _i64),
+        ("B", _i32), ("N", _i32), ("cin_pad", _i32), ("cout", _i32),
+    ]
+
+
+class LinearArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", _vp), ("x_sr", _i64), ("w", _vp), ("bias", _vp),
+        ("ln_w", _vp), ("ln_b", _vp), ("eps", _f32), ("mode", _i32),
+        ("resid", _vp), ("r_sr", _i64), ("gamma", _vp), ("mask", _vp),
+        ("out", _vp), ("o_sr", _i64),
+        ("rows", _i32), ("in_features", _i32), ("out_features", _i32),
+        ("B", _i32), ("S", _i32), ("H", _i32), ("dpad", _i32),
+    ]
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp), ("k", _vp), ("v", _vp), ("qkv_sb", _i64), ("qkv_sh", _i64),
+        ("seq_lens", _vp),
+        ("pair", _vp), ("p_sb", _i64), ("p_sq", _i64), ("table2", _vp), ("table_rows", _i32),
+        ("coords", _vp), ("mask", _vp), ("btab", _vp), ("lut_m", _i32), ("n_tokens", _i32),
+        ("o", _vp), ("o_sb", _i64), ("o_sh", _i64), ("o_sr", _i64),
+        ("B", _i32), ("S", _i32), ("H", _i32), ("d", _i32), ("dpad", _i32),
+    ]
+
+
+class TailArgs(ctypes.Structure):
+    _fields_ = [
+        ("seq", _vp), ("s_sb", _i64), ("mask", _vp), ("ln_w", _vp), ("ln_b", _vp),
+        ("eps", _f32), ("out_seq", _vp),
+        ("vr_w", _vp), ("vr_b", _vp), ("vh_w", _vp), ("vh_b", _vp), ("value", _vp),
+        ("mr_w", _vp), ("mr_b", _vp), ("mh_w", _vp), ("mh_b", _vp), ("moves_left", _vp),
+        ("B", _i32), ("S", _i32), ("n_tokens", _i32), ("C", _i32), ("bins", _i32),
+    ]
+
+
+# Exported symbols and their ctypes signatures; tests check every one of them
+# against the header and the built library.
+SIGNATURES: dict = {
+    "shrimp_last_error": (ctypes.c_char_p, []),
+    "shrimp_abi_version": (ctypes.c_int, []),
+    "shrimp_conv_wpack_bytes": (ctypes.c_size_t, [ctypes.c_int] * 3),
+    "shrimp_pack_conv_weight": (ctypes.c_int, [_vp, _vp] + [ctypes.c_int] * 4 + [_vp]),
+    "shrimp_linear_wpack_bytes": (ctypes.c_size_t, [ctypes.c_int] * 2),
+    "shrimp_pack_linear_weight": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp]),
+    "shrimp_hex_conv": (ctypes.c_int, [ctypes.POINTER(ConvArgs), _vp]),
+    "shrimp_linear": (ctypes.c_int, [ctypes.POINTER(LinearArgs), _vp]),
+    "shrimp_attn": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _vp]),
+    "shrimp_attn_bias_table": (
+        ctypes.c_int,
+        [_vp, ctypes.c_int, ctypes.c_int, _vp] + [ctypes.c_int] * 4 + [_vp, _vp],
+    ),
+    "shrimp_prep_inputs": (
+        ctypes.c_int,
+        [_vp, ctypes.c_int, _vp, _vp, ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int,
+         ctypes.c_int, ctypes.c_int, ctypes.c_int] + [_vp] * 7,
+    ),
+    "shrimp_fill_tokens": (
+        ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _i64, ctypes.c_int, _vp]
+    ),
+    "shrimp_trunk_tail": (ctypes.c_int, [ctypes.POINTER(TailArgs), _vp]),
+    "shrimp_decode": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _i64, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_float]
+        + [_vp] * 5,
+    ),
+    "shrimp_build_pair_u8": (
+        ctypes.c_int, [_vp, _vp, _vp] + [ctypes.c_int] * 8 + [_vp, _vp]
+    ),
+    "shrimp_build_ray_index": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+}
+
+_LIB = None
+
+
+class HipLibraryMissing(RuntimeError):
+    pass
+
+
+def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
+    """Load (once) and return the library, with every signature bound."""
+
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise HipLibraryMissing(
+            f"{p} is not built: run `python -c 'import __graft_entry__ as g; g.build()'` "
+            "(or `make -C hexo-bot_amd/csrc`) before using the shrimp HIP forward"
+        )
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().shrimp_last_error()
+        raise RuntimeError(f"{what} failed ({status}): {msg.decode() if msg else ''}")
+
+
+def ptr(t) -> int | None:
+    """Device address of a tensor (None for None)."""
+
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device=None) -> int:
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream

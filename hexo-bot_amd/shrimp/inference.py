@@ -1,0 +1,177 @@
+"""ShrimpEvaluator — the serve side of the ABI-1 wire protocol on MI355X.
+
+Restates ``packages/shrimp/python/shrimp/inference.py``: payload validation
+(:509-531), padding-aware grouping ``plan_groups`` (:201-223), per-group pack
+(:865-892), the forward, and the decode (:998-1042) into the reply bytes
+(:806-863). The Rust caller (``payload.rs:108-160`` builds the payload,
+``:164-289`` parses the reply) is unchanged.
+
+Payload: ``abi`` == 1, ``shape`` (B, T), ``node_feats`` f16 T x 15,
+``node_qr`` i16 T x 2, ``node_row_offsets`` (B+1), ``nbr`` u16 T x 6 with
+0xFFFF = absent, ``legal_counts`` i32 B, ``request_moves_left``,
+``request_logits``. Rows arrive sorted by support size, descending.
+
+Reply: ``values_bytes`` f32 x B in [-1, 1]; ``priors_bytes`` f32 x sum(L),
+the softmax over each row's legal prefix, rows in order; optional
+``moves_left_bytes`` f32 x B and ``priors_logits_bytes`` f32 x sum(L).
+
+Per group the forward and the decode (``shrimp_decode``: binned value,
+moves-left, legal-prefix softmax and the flat gather in one kernel) run on
+the current stream; ``result`` performs the only device-to-host copy.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import torch
+
+from . import _lib
+from .constants import MOVES_LEFT_CAP, NUM_FEATURES, NUM_TOKENS, VALUE_BINS
+from .model import ShrimpNet
+
+NBR_SENTINEL = 0xFFFF
+PAIR_CEILING = float(os.environ.get("SHRIMP_PAIR_CEILING", 0) or 3.8e7)
+QUANT_NODES = 64
+WASTE_FRACTION = float(os.environ.get("SHRIMP_WASTE_FRACTION", 0) or 0.18)
+
+
+def _ceil_quant(n: int) -> int:
+    return max(QUANT_NODES, -(-int(n) // QUANT_NODES) * QUANT_NODES)
+
+
+def plan_groups(sizes) -> list:
+    """(start, end, pad_to) groups over size-descending rows: a group is
+    anchored at its first (largest) row, padded to the 64-quantized anchor, and
+    stops growing when B * (pad_to + 8)^2 would pass PAIR_CEILING or the next
+    row is smaller than the anchor by more than max(64, WASTE_FRACTION * pad_to)
+    (inference.py:201-223)."""
+
+    n = len(sizes)
+    groups = []
+    start = 0
+    while start < n:
+        pad_to = _ceil_quant(int(sizes[start]))
+        floor = pad_to - max(QUANT_NODES, int(WASTE_FRACTION * pad_to))
+        end = start + 1
+        while end < n:
+            if (end - start + 1) * (pad_to + NUM_TOKENS) ** 2 > PAIR_CEILING:
+                break
+            if int(sizes[end]) < floor:
+                break
+            end += 1
+        groups.append((start, end, pad_to))
+        start = end
+    return groups
+
+
+class ShrimpEvaluator:
+    def __init__(self, model: ShrimpNet, device="cuda"):
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise RuntimeError(
+                "ShrimpEvaluator of the MI355X build serves on a ROCm device only "
+                f"(got {self.device})"
+            )
+        self.model = model.to(self.device).eval()
+
+    def __call__(self, payload: dict) -> dict:
+        return self.evaluate_payload(payload)
+
+    @torch.no_grad()
+    def evaluate_payload(self, payload: dict) -> dict:
+        return self.result(self.submit_payload(payload))
+
+    def perf_trace_report(self):
+        return None
+
+    @staticmethod
+    def _parse(payload: dict):
+        if int(payload["abi"]) != 1:
+            raise ValueError(f"unsupported shrimp ABI {payload['abi']}")
+        b, total = (int(x) for x in payload["shape"])
+        offsets = np.asarray(payload["node_row_offsets"], dtype=np.int64)
+        if offsets.shape[0] != b + 1 or int(offsets[-1]) != total:
+            raise ValueError("node_row_offsets inconsistent with shape")
+        legal = np.frombuffer(payload["legal_counts"], dtype=np.int32)
+        if legal.shape[0] != b:
+            raise ValueError("legal_counts byte count mismatch")
+        feats = np.frombuffer(payload["node_feats"], dtype=np.float16)
+        if feats.shape[0] != total * NUM_FEATURES:
+            raise ValueError("node_feats byte count mismatch")
+        qr = np.frombuffer(payload["node_qr"], dtype=np.int16)
+        nbr = np.frombuffer(payload["nbr"], dtype=np.uint16)
+        if qr.shape[0] != total * 2 or nbr.shape[0] != total * 6:
+            raise ValueError("node_qr / nbr byte count mismatch")
+        return (b, total, offsets, legal, feats.reshape(total, NUM_FEATURES),
+                qr.reshape(total, 2), nbr.reshape(total, 6))
+
+    @torch.no_grad()
+    def submit_payload(self, payload: dict) -> dict:
+        b, total, offsets, legal, feats, qr, nbr = self._parse(payload)
+        request_ml = bool(payload.get("request_moves_left", False))
+        request_logits = bool(payload.get("request_logits", False))
+        dev = self.device
+        sizes = offsets[1:] - offsets[:-1]
+        legal64 = legal.astype(np.int64)
+        flat_off = np.zeros(b + 1, dtype=np.int64)
+        np.cumsum(legal64, out=flat_off[1:])
+        values = torch.empty(b, dtype=torch.float32, device=dev)
+        ml = torch.empty(b, dtype=torch.float32, device=dev) if request_ml else None
+        priors = torch.empty(int(flat_off[-1]), dtype=torch.float32, device=dev)
+        logits = torch.empty_like(priors) if request_logits else None
+        d_legal = torch.from_numpy(legal.copy()).to(dev, non_blocking=True)
+        d_off = torch.from_numpy(flat_off[:-1].copy()).to(dev, non_blocking=True)
+        lib = _lib.load()
+        stream = _lib.stream_handle(dev)
+        for start, end, pad_to in plan_groups(sizes):
+            g = end - start
+            p_feats = np.zeros((g, pad_to, NUM_FEATURES), dtype=np.float16)
+            p_nbr = np.full((g, pad_to, 6), NBR_SENTINEL, dtype=np.uint16)
+            p_mask = np.zeros((g, pad_to), dtype=np.bool_)
+            p_coords = np.zeros((g, pad_to, 2), dtype=np.int32)
+            for k in range(g):
+                o = int(offsets[start + k])
+                n = int(sizes[start + k])
+                p_feats[k, :n] = feats[o:o + n]
+                p_nbr[k, :n] = nbr[o:o + n]
+                p_mask[k, :n] = True
+                p_coords[k, :n] = qr[o:o + n]
+            d_feats = torch.from_numpy(p_feats).pin_memory().to(dev, non_blocking=True)
+            d_nbr = torch.from_numpy(p_nbr).pin_memory().to(dev, non_blocking=True)
+            d_mask = torch.from_numpy(p_mask).pin_memory().to(dev, non_blocking=True)
+            d_coords = torch.from_numpy(p_coords).pin_memory().to(dev, non_blocking=True)
+            out = self.model.forward_policy_value(
+                d_feats, d_nbr, d_mask, d_coords, request_moves_left=request_ml
+            )
+            pol = out["policy"]
+            _lib.check(
+                lib.shrimp_decode(
+                    out["value"].data_ptr(),
+                    out["moves_left"].data_ptr() if request_ml else None,
+                    pol.data_ptr(), pol.stride(0),
+                    d_legal[start:].data_ptr(), d_off[start:].data_ptr(), g, VALUE_BINS,
+                    float(MOVES_LEFT_CAP), values[start:].data_ptr(),
+                    ml[start:].data_ptr() if request_ml else None,
+                    priors.data_ptr(), logits.data_ptr() if request_logits else None, stream,
+                ),
+                "decode",
+            )
+        return {
+            "b": b, "request_ml": request_ml, "request_logits": request_logits,
+            "values_gpu": values, "ml_gpu": ml, "priors_gpu": priors, "logits_gpu": logits,
+        }
+
+    @torch.no_grad()
+    def result(self, handle: dict) -> dict:
+        reply = {
+            "values_bytes": handle["values_gpu"].cpu().numpy().astype(np.float32, copy=False).tobytes(),
+            "priors_bytes": handle["priors_gpu"].cpu().numpy().astype(np.float32, copy=False).tobytes(),
+        }
+        if handle["request_ml"]:
+            reply["moves_left_bytes"] = handle["ml_gpu"].cpu().numpy().tobytes()
+        if handle["request_logits"]:
+            reply["priors_logits_bytes"] = handle["logits_gpu"].cpu().numpy().tobytes()
+        return reply

@@ -1,0 +1,269 @@
+"""Launch helpers over the C ABI and the reference's operator names.
+
+``shrimp::hex_conv``, ``shrimp::hex_conv_ln`` and ``shrimp::attn_pair`` are
+registered with the signatures of the reference's serve ops
+(``packages/shrimp/python/shrimp/_triton_conv.py:93-128,198-239``,
+``_triton_attn.py:132-171``), each with a fake kernel, so code written against
+the reference can call ``torch.ops.shrimp.*`` unchanged. They run the gfx950
+kernels of ``libshrimp_hip.so`` and return bfloat16 (the reference returns
+float16; MI355X computes these paths in bf16). Inputs must live on a ROCm
+device; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .constants import (
+    BIAS_CELL_TOKEN_ROW,
+    BIAS_TOKEN_CELL_ROW,
+    BIAS_TOKEN_TOKEN_ROW,
+    NUM_TOKENS,
+)
+from .geometry import CELL_LUT_M
+
+
+def require_device(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(
+            f"{what}: the shrimp MI355X build runs on a ROCm device only "
+            f"(got a {t.device} tensor)"
+        )
+
+
+def cin_pad_of(c: int) -> int:
+    return -(-int(c) // 32) * 32
+
+
+# ---- weight packing ------------------------------------------------------------------
+
+
+def pack_conv_weight(weight: torch.Tensor, cin_pad: int | None = None) -> torch.Tensor:
+    """(T, cin, cout) conv weight -> packed bf16 MFMA fragments (uint8 bytes)."""
+
+    require_device(weight, "pack_conv_weight")
+    t, cin, cout = weight.shape
+    cp = cin_pad_of(cin) if cin_pad is None else int(cin_pad)
+    lib = _lib.load()
+    w32 = weight.detach().to(torch.float32).contiguous()
+    out = torch.empty(lib.shrimp_conv_wpack_bytes(t, cp, cout), dtype=torch.uint8, device=weight.device)
+    _lib.check(
+        lib.shrimp_pack_conv_weight(w32.data_ptr(), out.data_ptr(), t, cin, cp, cout,
+                                    _lib.stream_handle(weight.device)),
+        "pack_conv_weight",
+    )
+    return out
+
+
+def pack_linear_weight(weight: torch.Tensor) -> torch.Tensor:
+    """nn.Linear weight (out, in) -> packed bf16 MFMA fragments (uint8 bytes)."""
+
+    require_device(weight, "pack_linear_weight")
+    n_out, n_in = weight.shape
+    lib = _lib.load()
+    w32 = weight.detach().to(torch.float32).contiguous()
+    out = torch.empty(lib.shrimp_linear_wpack_bytes(n_in, n_out), dtype=torch.uint8, device=weight.device)
+    _lib.check(
+        lib.shrimp_pack_linear_weight(w32.data_ptr(), out.data_ptr(), n_in, n_out,
+                                      _lib.stream_handle(weight.device)),
+        "pack_linear_weight",
+    )
+    return out
+
+
+def attn_bias_table(table: torch.Tensor, lut_u8: torch.Tensor, lut_m: int = CELL_LUT_M) -> torch.Tensor:
+    """Per-block (BIAS_ROWS, H) table -> ((2M+1)^2 + 3, H) fp32 LUT-indexed
+    table with log2(e) folded in (the layout the coords-mode kernel reads)."""
+
+    require_device(table, "attn_bias_table")
+    rows, h = table.shape
+    w = 2 * lut_m + 1
+    t32 = table.detach().to(torch.float32).contiguous()
+    out = torch.empty((w * w + 3, h), dtype=torch.float32, device=table.device)
+    _lib.check(
+        _lib.load().shrimp_attn_bias_table(
+            t32.data_ptr(), rows, h, lut_u8.data_ptr(), lut_m, BIAS_CELL_TOKEN_ROW,
+            BIAS_TOKEN_CELL_ROW, BIAS_TOKEN_TOKEN_ROW, out.data_ptr(),
+            _lib.stream_handle(table.device),
+        ),
+        "attn_bias_table",
+    )
+    return out
+
+
+# ---- raw launches ----------------------------------------------------------------------
+
+
+def launch_conv(
+    *, x, x_sb, x_sn, idx, taps, idx_stride, mask8, wpack, bias, B, N, cin_pad, cout,
+    ln_w=None, ln_b=None, eps=1e-5, relu=False, resid=None, r_sb=0, r_sn=0, gamma=None,
+    head_w=None, head_b=None, head_out=None, out=None, o_sb=0, o_sn=0, stream=None,
+):
+    a = _lib.ConvArgs(
+        x=x.data_ptr(), x_sb=x_sb, x_sn=x_sn, idx=idx.data_ptr(), taps=taps,
+        idx_stride=idx_stride, mask=mask8.data_ptr(), w=wpack.data_ptr(), bias=bias.data_ptr(),
+        ln_w=_lib.ptr(ln_w), ln_b=_lib.ptr(ln_b), eps=float(eps), relu=int(bool(relu)),
+        resid=_lib.ptr(resid), r_sb=r_sb, r_sn=r_sn, gamma=_lib.ptr(gamma),
+        head_w=_lib.ptr(head_w), head_b=_lib.ptr(head_b), head_out=_lib.ptr(head_out),
+        out=_lib.ptr(out), o_sb=o_sb, o_sn=o_sn, B=B, N=N, cin_pad=cin_pad, cout=cout,
+    )
+    s = _lib.stream_handle() if stream is None else stream
+    _lib.check(_lib.load().shrimp_hex_conv(ctypes_ref(a), s), "hex_conv")
+
+
+def launch_linear(
+    *, x, x_sr, wpack, bias, rows, n_in, n_out, mode, out, o_sr=0, ln_w=None, ln_b=None,
+    eps=1e-5, resid=None, r_sr=0, gamma=None, mask=None, B=0, S=0, H=0, dpad=0, stream=None,
+):
+    a = _lib.LinearArgs(
+        x=x.data_ptr(), x_sr=x_sr, w=wpack.data_ptr(), bias=bias.data_ptr(),
+        ln_w=_lib.ptr(ln_w), ln_b=_lib.ptr(ln_b), eps=float(eps), mode=mode,
+        resid=_lib.ptr(resid), r_sr=r_sr, gamma=_lib.ptr(gamma), mask=_lib.ptr(mask),
+        out=out.data_ptr(), o_sr=o_sr, rows=rows, in_features=n_in, out_features=n_out,
+        B=B, S=S, H=H, dpad=dpad,
+    )
+    s = _lib.stream_handle() if stream is None else stream
+    _lib.check(_lib.load().shrimp_linear(ctypes_ref(a), s), "linear")
+
+
+def launch_attn(
+    *, q, k, v, qkv_sb, qkv_sh, seq_lens, o, o_sb, o_sh, o_sr, B, S, H, d, dpad,
+    pair=None, p_sb=0, p_sq=0, table2=None, coords=None, mask8=None, btab=None,
+    lut_m=CELL_LUT_M, n_tokens=NUM_TOKENS, stream=None,
+):
+    a = _lib.AttnArgs(
+        q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), qkv_sb=qkv_sb, qkv_sh=qkv_sh,
+        seq_lens=seq_lens.data_ptr(), pair=_lib.ptr(pair), p_sb=p_sb, p_sq=p_sq,
+        table2=_lib.ptr(table2), table_rows=0 if table2 is None else int(table2.shape[0]),
+        coords=_lib.ptr(coords), mask=_lib.ptr(mask8), btab=_lib.ptr(btab), lut_m=lut_m,
+        n_tokens=n_tokens, o=o.data_ptr(), o_sb=o_sb, o_sh=o_sh, o_sr=o_sr,
+        B=B, S=S, H=H, d=d, dpad=dpad,
+    )
+    s = _lib.stream_handle() if stream is None else stream
+    _lib.check(_lib.load().shrimp_attn(ctypes_ref(a), s), "attn")
+
+
+def ctypes_ref(struct):
+    import ctypes
+
+    return ctypes.byref(struct)
+
+
+# ---- the reference operator ABI -----------------------------------------------------------
+
+
+def _bf16_rows(x: torch.Tensor, cin_pad: int) -> torch.Tensor:
+    """x (B, N, C) -> contiguous bf16 (B, N, cin_pad) (zero channel padding)."""
+
+    b, n, c = x.shape
+    xb = x.to(torch.bfloat16)
+    if c == cin_pad:
+        return xb.contiguous()
+    out = torch.zeros((b, n, cin_pad), dtype=torch.bfloat16, device=x.device)
+    out[..., :c] = xb
+    return out
+
+
+def _conv_common(x, gather_idx, mask, weight, bias, ln_weight, ln_bias, eps, relu):
+    require_device(x, "shrimp::hex_conv")
+    b, n, c = x.shape
+    t = weight.shape[0]
+    cout = weight.shape[-1]
+    cp = cin_pad_of(c)
+    xb = _bf16_rows(x, cp)
+    idx = gather_idx.to(torch.int32).contiguous()
+    m8 = mask.to(torch.uint8).contiguous()
+    wp = pack_conv_weight(weight, cp)
+    out = torch.empty((b, n, cout), dtype=torch.bfloat16, device=x.device)
+    launch_conv(
+        x=xb, x_sb=n * cp, x_sn=cp, idx=idx, taps=t, idx_stride=idx.shape[-1], mask8=m8,
+        wpack=wp, bias=bias.to(torch.float32).contiguous(), B=b, N=n, cin_pad=cp, cout=cout,
+        ln_w=None if ln_weight is None else ln_weight.to(torch.float32).contiguous(),
+        ln_b=None if ln_bias is None else ln_bias.to(torch.float32).contiguous(),
+        eps=eps, relu=relu, out=out, o_sb=n * cout, o_sn=cout,
+    )
+    return out
+
+
+@torch.library.custom_op("shrimp::hex_conv", mutates_args=())
+def hex_conv(
+    x: torch.Tensor,
+    gather_idx: torch.Tensor,
+    mask: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor,
+) -> torch.Tensor:
+    """out[b, i] = mask * (sum_t x[b, gather_idx[b, i, t]] @ weight[t] + bias);
+    gather_idx entries outside [0, N) (the reference's Npad sentinel) read as
+    zero rows."""
+
+    return _conv_common(x, gather_idx, mask, weight, bias, None, None, 1e-5, False)
+
+
+@hex_conv.register_fake
+def _hex_conv_fake(x, gather_idx, mask, weight, bias):
+    return x.new_empty((x.shape[0], x.shape[1], weight.shape[-1]), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("shrimp::hex_conv_ln", mutates_args=())
+def hex_conv_ln(
+    x: torch.Tensor,
+    gather_idx: torch.Tensor,
+    mask: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor,
+    ln_weight: torch.Tensor,
+    ln_bias: torch.Tensor,
+    eps: float,
+    relu: bool,
+) -> torch.Tensor:
+    """hex_conv followed by LayerNorm over the output channels (fp32 stats on
+    the accumulator), optional ReLU and the row mask."""
+
+    return _conv_common(x, gather_idx, mask, weight, bias, ln_weight, ln_bias, eps, relu)
+
+
+@hex_conv_ln.register_fake
+def _hex_conv_ln_fake(x, gather_idx, mask, weight, bias, ln_weight, ln_bias, eps, relu):
+    return x.new_empty((x.shape[0], x.shape[1], weight.shape[-1]), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("shrimp::attn_pair", mutates_args=())
+def attn_pair(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    pair: torch.Tensor,
+    table2: torch.Tensor,
+    seq_lens: torch.Tensor,
+) -> torch.Tensor:
+    """softmax(q k^T / sqrt(D) + table2[pair[b, i, j], h]) v over keys
+    j < seq_lens[b]; q/k/v (B, H, S, D). Query rows >= seq_lens[b] are 0."""
+
+    require_device(q, "shrimp::attn_pair")
+    b, h, s, d = q.shape
+    dpad = max(16, -(-d // 16) * 16)
+
+    def prep(t):
+        t = t.to(torch.bfloat16)
+        if dpad != d:
+            t = torch.nn.functional.pad(t, (0, dpad - d))
+        return t.contiguous()
+
+    qb, kb, vb = prep(q), prep(k), prep(v)
+    pr = pair.to(torch.uint8).contiguous()
+    tab = table2.to(torch.float32).contiguous()
+    sl = seq_lens.to(torch.int32).contiguous()
+    out = torch.empty((b, h, s, d), dtype=torch.bfloat16, device=q.device)
+    launch_attn(
+        q=qb, k=kb, v=vb, qkv_sb=h * s * dpad, qkv_sh=s * dpad, seq_lens=sl,
+        o=out, o_sb=h * s * d, o_sh=s * d, o_sr=d, B=b, S=s, H=h, d=d, dpad=dpad,
+        pair=pr, p_sb=s * s, p_sq=s, table2=tab, n_tokens=0,
+    )
+    return out
+
+
+@attn_pair.register_fake
+def _attn_pair_fake(q, k, v, pair, table2, seq_lens):
+    return q.new_empty(q.shape, dtype=torch.bfloat16)

@@ -1,0 +1,292 @@
+"""HipForward: the serve forward of ShrimpNet as a fixed sequence of gfx950
+kernel launches on the current HIP stream.
+
+Device layout of one batch (B positions, N = Npad cells, S = N + 8 rows):
+
+    seq   (B, S, C)  bf16  residual stream; rows 0..7 are the summary tokens,
+                           rows 8.. the cells (the reference's cat([tokens, x]),
+                           model.py:921-926, kept in place instead of re-built)
+    y1    (B, N, C)  bf16  first conv of a ConvBlock
+    qkv   (3, B, H, S, dpad) bf16 head-major projections
+    att   (B, S, C)  bf16  attention output, heads concatenated
+    hid   (B, S, 2C) bf16  MLP hidden
+    seqf  (B, S, C)  bf16  after the final LayerNorm (cells masked)
+
+Kernel sequence (reference lines in model.py):
+    prep_inputs          gather_idx / mask / coords / seq_lens / padded feats  :861-892
+    hex_conv  (stem)     conv + LN + ReLU + mask                               :865
+    per 'C': hex_conv x2 conv1+LN+ReLU+mask -> y1; conv2+LN+mask, ReLU(x+g*y)  :395-422
+    per 'A': linear(QKV, LN1) -> attn -> linear(out_proj, residual)
+             -> linear(fc1, LN2, GELU) -> linear(fc2, residual)                :448-514
+    trunk_tail           final LN, pooled mean, value / moves-left heads       :927-935, 990-1002
+    hex_conv  (policy)   conv + ReLU + Linear(C,1) + mask                      :1011-1020
+Weights are packed once into MFMA fragment order (bf16) and re-packed when
+any parameter changes (tracked through tensor version counters).
+"""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import torch
+
+from . import _lib
+from .constants import NUM_TOKENS, VALUE_BINS
+from .geometry import CELL_LUT_M
+from .ops import (
+    attn_bias_table,
+    launch_attn,
+    launch_conv,
+    launch_linear,
+    pack_conv_weight,
+    pack_linear_weight,
+    require_device,
+)
+
+_NBR_DT = {
+    torch.int64: _lib.DT_I64,
+    torch.int32: _lib.DT_I32,
+    torch.uint16: _lib.DT_U16,
+}
+_FEAT_DT = {
+    torch.float32: _lib.DT_F32,
+    torch.float16: _lib.DT_F16,
+    torch.bfloat16: _lib.DT_BF16,
+}
+_COORD_DT = {torch.int64: _lib.DT_I64, torch.int32: _lib.DT_I32}
+
+
+def head_dim_pad(d: int) -> int:
+    return max(16, -(-d // 16) * 16)
+
+
+class HipForward:
+    def __init__(self, net) -> None:
+        self.net = net
+        self._packed = None
+        self._key = None
+        # When set, the device buffers of the last forward stay referenced in
+        # ``self.last`` (used to re-launch single kernels for timing).
+        self.keep_buffers = False
+        self.last = None
+
+    def invalidate(self) -> None:
+        self._packed = None
+        self._key = None
+
+    def _param_key(self, device) -> tuple:
+        return (str(device),) + tuple(
+            (p.data_ptr(), p._version) for p in self.net.parameters()
+        )
+
+    def weights(self, device: torch.device) -> SimpleNamespace:
+        key = self._param_key(device)
+        if self._packed is not None and key == self._key:
+            return self._packed
+        self._packed = self._pack(device)
+        self._key = key
+        return self._packed
+
+    @torch.no_grad()
+    def _pack(self, device: torch.device) -> SimpleNamespace:
+        net = self.net
+
+        def f32(t):
+            return t.detach().to(device=device, dtype=torch.float32).contiguous()
+
+        def conv_w(conv, cin_pad=None):
+            return pack_conv_weight(conv.weight.detach().to(device), cin_pad)
+
+        def lin_w(lin):
+            return pack_linear_weight(lin.weight.detach().to(device))
+
+        c = net.channels
+        P = SimpleNamespace()
+        P.C, P.H = c, net.heads
+        P.d = c // P.H
+        P.dpad = head_dim_pad(P.d)
+        P.layout = net.trunk_layout
+        P.stem = SimpleNamespace(
+            w=conv_w(net.stem, 32), b=f32(net.stem.bias), lnw=f32(net.stem_ln.weight),
+            lnb=f32(net.stem_ln.bias), eps=net.stem_ln.eps,
+        )
+        P.convs = []
+        for blk in net.conv_blocks:
+            P.convs.append(
+                SimpleNamespace(
+                    w1=conv_w(blk.conv1), b1=f32(blk.conv1.bias), ln1w=f32(blk.ln1.weight),
+                    ln1b=f32(blk.ln1.bias), eps1=blk.ln1.eps,
+                    w2=conv_w(blk.conv2), b2=f32(blk.conv2.bias), ln2w=f32(blk.ln2.weight),
+                    ln2b=f32(blk.ln2.bias), eps2=blk.ln2.eps, gamma=f32(blk.ls.gamma),
+                )
+            )
+        lut = net._cell_bias_lut_u8.to(device)
+        P.lut = lut
+        P.attn = []
+        for i, blk in enumerate(net.attn_blocks):
+            at = blk.attn
+            qkv_w = torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight], 0)
+            qkv_b = torch.cat([at.q_proj.bias, at.k_proj.bias, at.v_proj.bias], 0)
+            P.attn.append(
+                SimpleNamespace(
+                    ln1w=f32(blk.ln1.weight), ln1b=f32(blk.ln1.bias), eps1=blk.ln1.eps,
+                    qkv_w=pack_linear_weight(qkv_w.detach().to(device)), qkv_b=f32(qkv_b),
+                    out_w=lin_w(at.out_proj), out_b=f32(at.out_proj.bias),
+                    ln2w=f32(blk.ln2.weight), ln2b=f32(blk.ln2.bias), eps2=blk.ln2.eps,
+                    fc1_w=lin_w(blk.fc1), fc1_b=f32(blk.fc1.bias),
+                    fc2_w=lin_w(blk.fc2), fc2_b=f32(blk.fc2.bias),
+                    g_attn=f32(blk.ls_attn.gamma), g_mlp=f32(blk.ls_mlp.gamma),
+                    btab=attn_bias_table(net.bias_tables[i].detach().to(device), lut, CELL_LUT_M),
+                )
+            )
+        P.tokens = f32(net.tokens)
+        P.lnf = SimpleNamespace(w=f32(net.ln_final.weight), b=f32(net.ln_final.bias),
+                                eps=net.ln_final.eps)
+        P.value = SimpleNamespace(
+            rw=f32(net.value_reduction.weight), rb=f32(net.value_reduction.bias),
+            hw=f32(net.value_head.weight), hb=f32(net.value_head.bias),
+        )
+        P.ml = SimpleNamespace(
+            rw=f32(net.ml_reduction.weight), rb=f32(net.ml_reduction.bias),
+            hw=f32(net.moves_left_head.weight), hb=f32(net.moves_left_head.bias),
+        )
+        P.policy = SimpleNamespace(
+            w=conv_w(net.policy_conv), b=f32(net.policy_conv.bias),
+            hw=f32(net.policy_head.weight.reshape(-1)), hb=f32(net.policy_head.bias.reshape(-1)),
+        )
+        return P
+
+    @torch.no_grad()
+    def forward(self, feats, nbr, mask, coords, *, request_moves_left: bool = False) -> dict:
+        require_device(feats, "ShrimpNet.forward_policy_value")
+        dev = feats.device
+        B, N, F = feats.shape
+        P = self.weights(dev)
+        C, H, d, dpad = P.C, P.H, P.d, P.dpad
+        S = N + NUM_TOKENS
+        if nbr.dtype not in _NBR_DT or feats.dtype not in _FEAT_DT or coords.dtype not in _COORD_DT:
+            raise TypeError(
+                f"unsupported dtypes feats={feats.dtype} nbr={nbr.dtype} coords={coords.dtype}"
+            )
+        if tuple(nbr.shape) != (B, N, 6) or tuple(mask.shape) != (B, N) or tuple(coords.shape) != (B, N, 2):
+            raise ValueError("feats/nbr/mask/coords shapes disagree")
+        lib = _lib.load()
+        st = _lib.stream_handle(dev)
+        feats_c = feats.contiguous()
+        nbr_c = nbr.contiguous()
+        mask_c = mask.contiguous()
+        if mask_c.dtype not in (torch.bool, torch.uint8):
+            mask_c = mask_c.to(torch.bool)
+        coords_c = coords.contiguous()
+
+        i32, u8, bf = torch.int32, torch.uint8, torch.bfloat16
+        idx = torch.empty((B, N, 7), dtype=i32, device=dev)
+        mask8 = torch.empty((B, N), dtype=u8, device=dev)
+        coords32 = torch.empty((B, N, 2), dtype=i32, device=dev)
+        seq_lens = torch.empty((B,), dtype=i32, device=dev)
+        seq_mask = torch.empty((B, S), dtype=u8, device=dev)
+        xin = torch.empty((B, N, 32), dtype=bf, device=dev)
+        _lib.check(
+            lib.shrimp_prep_inputs(
+                nbr_c.data_ptr(), _NBR_DT[nbr_c.dtype], mask_c.data_ptr(), coords_c.data_ptr(),
+                _COORD_DT[coords_c.dtype], feats_c.data_ptr(), _FEAT_DT[feats_c.dtype], F, B, N,
+                NUM_TOKENS, idx.data_ptr(), mask8.data_ptr(), coords32.data_ptr(),
+                seq_lens.data_ptr(), seq_mask.data_ptr(), xin.data_ptr(), st,
+            ),
+            "prep_inputs",
+        )
+        seq = torch.empty((B, S, C), dtype=bf, device=dev)
+        _lib.check(
+            lib.shrimp_fill_tokens(P.tokens.data_ptr(), NUM_TOKENS, C, seq.data_ptr(), S * C, B, st),
+            "fill_tokens",
+        )
+        cells = seq[:, NUM_TOKENS:]
+        y1 = torch.empty((B, N, C), dtype=bf, device=dev)
+        qkv = (torch.zeros if d != dpad else torch.empty)((3, B, H, S, dpad), dtype=bf, device=dev)
+        att = torch.empty((B, S, C), dtype=bf, device=dev)
+        hid = torch.empty((B, S, 2 * C), dtype=bf, device=dev)
+
+        conv_common = dict(idx=idx, taps=7, idx_stride=7, mask8=mask8, B=B, N=N, stream=st)
+        launch_conv(
+            x=xin, x_sb=N * 32, x_sn=32, wpack=P.stem.w, bias=P.stem.b, cin_pad=32, cout=C,
+            ln_w=P.stem.lnw, ln_b=P.stem.lnb, eps=P.stem.eps, relu=True,
+            out=cells, o_sb=S * C, o_sn=C, **conv_common,
+        )
+        ci = ai = 0
+        rows = B * S
+        for kind in P.layout:
+            if kind == "C":
+                k = P.convs[ci]
+                ci += 1
+                launch_conv(
+                    x=cells, x_sb=S * C, x_sn=C, wpack=k.w1, bias=k.b1, cin_pad=C, cout=C,
+                    ln_w=k.ln1w, ln_b=k.ln1b, eps=k.eps1, relu=True,
+                    out=y1, o_sb=N * C, o_sn=C, **conv_common,
+                )
+                launch_conv(
+                    x=y1, x_sb=N * C, x_sn=C, wpack=k.w2, bias=k.b2, cin_pad=C, cout=C,
+                    ln_w=k.ln2w, ln_b=k.ln2b, eps=k.eps2, relu=False,
+                    resid=cells, r_sb=S * C, r_sn=C, gamma=k.gamma,
+                    out=cells, o_sb=S * C, o_sn=C, **conv_common,
+                )
+            else:
+                a = P.attn[ai]
+                ai += 1
+                launch_linear(
+                    x=seq, x_sr=C, wpack=a.qkv_w, bias=a.qkv_b, rows=rows, n_in=C, n_out=3 * C,
+                    mode=_lib.LIN_QKV, out=qkv, ln_w=a.ln1w, ln_b=a.ln1b, eps=a.eps1,
+                    B=B, S=S, H=H, dpad=dpad, stream=st,
+                )
+                launch_attn(
+                    q=qkv[0], k=qkv[1], v=qkv[2], qkv_sb=H * S * dpad, qkv_sh=S * dpad,
+                    seq_lens=seq_lens, o=att, o_sb=S * C, o_sh=d, o_sr=C, B=B, S=S, H=H, d=d,
+                    dpad=dpad, coords=coords32, mask8=mask8, btab=a.btab, lut_m=CELL_LUT_M,
+                    n_tokens=NUM_TOKENS, stream=st,
+                )
+                launch_linear(
+                    x=att, x_sr=C, wpack=a.out_w, bias=a.out_b, rows=rows, n_in=C, n_out=C,
+                    mode=_lib.LIN_RESID, out=seq, o_sr=C, resid=seq, r_sr=C, gamma=a.g_attn,
+                    mask=seq_mask, stream=st,
+                )
+                launch_linear(
+                    x=seq, x_sr=C, wpack=a.fc1_w, bias=a.fc1_b, rows=rows, n_in=C, n_out=2 * C,
+                    mode=_lib.LIN_GELU, out=hid, o_sr=2 * C, ln_w=a.ln2w, ln_b=a.ln2b,
+                    eps=a.eps2, stream=st,
+                )
+                launch_linear(
+                    x=hid, x_sr=2 * C, wpack=a.fc2_w, bias=a.fc2_b, rows=rows, n_in=2 * C,
+                    n_out=C, mode=_lib.LIN_RESID, out=seq, o_sr=C, resid=seq, r_sr=C,
+                    gamma=a.g_mlp, mask=seq_mask, stream=st,
+                )
+
+        seqf = torch.empty((B, S, C), dtype=bf, device=dev)
+        value = torch.empty((B, VALUE_BINS), dtype=torch.float32, device=dev)
+        ml = torch.empty((B, VALUE_BINS), dtype=torch.float32, device=dev) if request_moves_left else None
+        tail = _lib.TailArgs(
+            seq=seq.data_ptr(), s_sb=S * C, mask=mask8.data_ptr(), ln_w=P.lnf.w.data_ptr(),
+            ln_b=P.lnf.b.data_ptr(), eps=float(P.lnf.eps), out_seq=seqf.data_ptr(),
+            vr_w=P.value.rw.data_ptr(), vr_b=P.value.rb.data_ptr(), vh_w=P.value.hw.data_ptr(),
+            vh_b=P.value.hb.data_ptr(), value=value.data_ptr(),
+            mr_w=P.ml.rw.data_ptr(), mr_b=P.ml.rb.data_ptr(), mh_w=P.ml.hw.data_ptr(),
+            mh_b=P.ml.hb.data_ptr(), moves_left=_lib.ptr(ml),
+            B=B, S=S, n_tokens=NUM_TOKENS, C=C, bins=VALUE_BINS,
+        )
+        import ctypes
+
+        _lib.check(lib.shrimp_trunk_tail(ctypes.byref(tail), st), "trunk_tail")
+        policy = torch.empty((B, N), dtype=torch.float32, device=dev)
+        launch_conv(
+            x=seqf[:, NUM_TOKENS:], x_sb=S * C, x_sn=C, wpack=P.policy.w, bias=P.policy.b,
+            cin_pad=C, cout=C, relu=True, head_w=P.policy.hw, head_b=P.policy.hb,
+            head_out=policy, **conv_common,
+        )
+        out = {"policy": policy, "value": value}
+        if request_moves_left:
+            out["moves_left"] = ml
+        if self.keep_buffers:
+            self.last = dict(
+                P=P, B=B, N=N, S=S, idx=idx, mask8=mask8, coords32=coords32, seq_lens=seq_lens,
+                seq_mask=seq_mask, seq=seq, y1=y1, qkv=qkv, att=att, hid=hid, seqf=seqf,
+                stream=st,
+            )
+        return out

@@ -1,0 +1,276 @@
+/*
+ * shrimp_hip.h — C ABI of the MI355X (gfx950) Shrimp forward kernels.
+ *
+ * Every entry point:
+ *   - takes plain device pointers (non-owning), sizes and a hipStream_t passed
+ *     as `void* stream` (NULL = the null stream);
+ *   - allocates nothing, never synchronises the host, and only enqueues work
+ *     on `stream`, so it can be captured into a HIP graph;
+ *   - returns 0 on success or a negative status; the message of the last
+ *     failure on the calling thread is available from shrimp_last_error().
+ *
+ * Shapes: B positions, N padded cells per position (Npad), S = n_tokens + N
+ * sequence rows, C channels, H heads, d = C / H head dim.
+ * Activations are bf16 with fp32 accumulation; element strides are given in
+ * elements (not bytes).
+ */
+#ifndef SHRIMP_HIP_H
+#define SHRIMP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SHRIMP_ABI_VERSION 1
+
+/* Status codes. */
+#define SHRIMP_OK 0
+#define SHRIMP_EINVAL (-1)   /* bad argument / unsupported shape */
+#define SHRIMP_ELAUNCH (-2)  /* HIP launch error */
+
+/* Element types for the few entry points that accept several. */
+#define SHRIMP_DT_BF16 0
+#define SHRIMP_DT_F32 1
+#define SHRIMP_DT_F16 2
+#define SHRIMP_DT_I64 3
+#define SHRIMP_DT_I32 4
+#define SHRIMP_DT_U16 5
+#define SHRIMP_DT_U8 6
+
+const char* shrimp_last_error(void);
+int shrimp_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Weight packing (device -> device). MFMA operands are read in fragment
+ * order: for K-step ks (32 rows of K) and output block nb (16 outputs), 64
+ * lanes x 8 bf16, lane l holding W[k = 32*ks + 8*(l/16) + e][n = 16*nb + l%16].
+ *
+ * Conv weights (HexNodeConv.weight, (T, cin, cout) fp32, model.py:338) are
+ * packed with K = T * cin_pad (tap-major, zero rows for cin <= c < cin_pad).
+ * Linear weights (nn.Linear.weight, (out, in) fp32) use K = in, n = out.
+ * ---------------------------------------------------------------------- */
+size_t shrimp_conv_wpack_bytes(int taps, int cin_pad, int cout);
+int shrimp_pack_conv_weight(const float* w, void* packed, int taps, int cin, int cin_pad,
+                            int cout, void* stream);
+size_t shrimp_linear_wpack_bytes(int in_features, int out_features);
+int shrimp_pack_linear_weight(const float* w, void* packed, int in_features, int out_features,
+                              void* stream);
+
+/* ------------------------------------------------------------------------
+ * Gather-GEMM hex / ray-tap convolution with fused epilogue.
+ *
+ * Replaces shrimp::hex_conv (packages/shrimp/python/shrimp/_triton_conv.py:93-122),
+ * shrimp::hex_conv_ln (_triton_conv.py:198-231), the materialized
+ * HexNodeConv.forward (model.py:346-370), ConvBlock.forward (model.py:395-422)
+ * and the policy head ShrimpNet._policy_logits (model.py:1011-1020).
+ *
+ *   acc[r, n] = bias[n] + sum_t sum_c x[b, idx[r, t], c] * W[t, c, n]
+ *   y = acc; if ln_w: y = LayerNorm(y) * ln_w + ln_b (fp32 stats, eps)
+ *   if relu: y = max(y, 0); y = mask[r] ? y : 0
+ *   residual (resid != NULL): out = max(resid[r, n] + gamma[n] * y, 0)
+ *   head (head_w != NULL): head_out[r] = mask[r] ? sum_n max(acc,0)*head_w[n] + head_b[0] : 0
+ *                          (no activation store)
+ *   else out = y.
+ * idx values outside [0, N) read as zero rows (the Npad sentinel of the
+ * reference). x, resid and out are bf16 with strides (per position, per row);
+ * out may alias resid (each row reads only its own residual row); out must not
+ * alias x.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* x;
+  int64_t x_sb, x_sn;
+  const int32_t* idx; /* (B, N, idx_stride) */
+  int32_t taps, idx_stride;
+  const uint8_t* mask; /* (B, N) */
+  const void* w;       /* packed, taps * cin_pad x cout */
+  const float* bias;   /* (cout) */
+  const float* ln_w;   /* (cout) or NULL */
+  const float* ln_b;
+  float eps;
+  int32_t relu;
+  const void* resid;
+  int64_t r_sb, r_sn;
+  const float* gamma;  /* LayerScale (cout), required with resid */
+  const float* head_w; /* (cout) or NULL */
+  const float* head_b; /* (1) */
+  float* head_out;     /* (B, N) fp32 */
+  void* out;
+  int64_t o_sb, o_sn;
+  int32_t B, N, cin_pad, cout;
+} shrimp_conv_args;
+
+int shrimp_hex_conv(const shrimp_conv_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Dense row GEMM with fused prologue / epilogue (the nn.Linear calls of
+ * RelPosAttention / AttnBlock, model.py:448-514, and the value heads,
+ * model.py:990-1002):
+ *   a = ln_w ? LayerNorm(x[r]) * ln_w + ln_b : x[r]       (x bf16, K = in)
+ *   y = a @ W^T + bias                                      (fp32 acc)
+ *   mode PLAIN: out = y (bf16)          mode GELU: out = gelu_erf(y)
+ *   mode RESID: out[r] = resid[r] + gamma * (mask[r] ? y : 0)   (out may alias resid)
+ *   mode QKV:  y split into q/k/v, heads, stored to qkv (3, B, H, S, dpad)
+ * Rows r = (b, s) over B positions x S rows; x, out, resid strides per row
+ * are given in elements; mask is per (b, s) (seq mask) or NULL.
+ * ---------------------------------------------------------------------- */
+#define SHRIMP_LIN_PLAIN 0
+#define SHRIMP_LIN_GELU 1
+#define SHRIMP_LIN_RESID 2
+#define SHRIMP_LIN_QKV 3
+
+typedef struct {
+  const void* x;
+  int64_t x_sr;
+  const void* w; /* packed, in x out */
+  const float* bias;
+  const float* ln_w; /* (in) or NULL */
+  const float* ln_b;
+  float eps;
+  int32_t mode;
+  const void* resid;
+  int64_t r_sr;
+  const float* gamma;
+  const uint8_t* mask; /* (rows) or NULL */
+  void* out;
+  int64_t o_sr;
+  int32_t rows, in_features, out_features;
+  /* QKV mode */
+  int32_t B, S, H, dpad;
+} shrimp_linear_args;
+
+int shrimp_linear(const shrimp_linear_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused relative-position-biased, key-masked attention (online softmax).
+ *
+ * Replaces shrimp::attn_pair (packages/shrimp/python/shrimp/_triton_attn.py:132-167)
+ * and the materialized / flex bias paths of RelPosAttention (model.py:448-492,
+ * build_attn_bias :718-760, _build_pair_u8 :762-792):
+ *   score[i, j] = q_i . k_j / sqrt(d) + bias(i, j, h);  out_i = softmax_j(score) v
+ *   keys j >= seq_lens[b] are skipped.
+ * Bias sources:
+ *   pair mode (pair != NULL):   bias = table2[pair[b, i, j], h], table2 (rows, H)
+ *                               fp32; the reference's pad row (-3e4) masks keys.
+ *   coords mode (pair == NULL): rows < n_tokens are tokens; for cells
+ *       pos = (clamp(dq,-M,M)+M)*(2M+1) + clamp(dr,-M,M)+M with (dq,dr) =
+ *       coords[key] - coords[query], bias = btab[pos, h];
+ *       btab rows (2M+1)^2 .. +2 hold (cell q, token k), (token q, cell k),
+ *       (token q, token k); keys whose mask is 0 get weight exactly 0.
+ *   btab is produced by shrimp_attn_bias_table (with log2(e) folded in).
+ * q, k, v: (B, H, S, dpad) bf16 with head-dim zero padding; o element
+ * (b, h, s, e) at o[b*o_sb + h*o_sh + s*o_sr + e], e < d (o_sh = d, o_sr = C
+ * gives the (B, S, C) layout out_proj reads; o_sh = S*d, o_sr = d gives
+ * (B, H, S, d)). Query rows >= seq_lens[b] store 0.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t qkv_sb, qkv_sh; /* elements between positions / heads; rows are dpad apart */
+  const int32_t* seq_lens; /* (B) */
+  /* pair mode */
+  const uint8_t* pair;
+  int64_t p_sb, p_sq;
+  const float* table2; /* (table_rows, H) raw (log2e not folded) */
+  int32_t table_rows;
+  /* coords mode */
+  const int32_t* coords; /* (B, S - n_tokens, 2) */
+  const uint8_t* mask;   /* (B, S - n_tokens) */
+  const float* btab;     /* ((2M+1)^2 + 3, H), log2e folded */
+  int32_t lut_m, n_tokens;
+  void* o;
+  int64_t o_sb, o_sh, o_sr;
+  int32_t B, S, H, d, dpad;
+} shrimp_attn_args;
+
+int shrimp_attn(const shrimp_attn_args* a, void* stream);
+
+/* btab[pos, h] = log2(e) * table[lut[pos], h] for pos < (2M+1)^2 and the 3
+ * token rows from table rows tok_rows[0..2]; table (rows, H) fp32. */
+int shrimp_attn_bias_table(const float* table, int table_rows, int H, const uint8_t* lut,
+                           int lut_m, int tok_row_ct, int tok_row_tc, int tok_row_tt,
+                           float* btab, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Index preparation (model.py:861-863, 884-892, 905; batching.py:264-276):
+ * one pass per position over the padded batch.
+ *   nbr (B, N, 6) of dtype nbr_dt (i64 / i32 with sentinel N, or u16 with
+ *   0xFFFF) -> idx (B, N, 7) int32, tap 0 = self, missing = N
+ *   mask (B, N) bool/u8 -> mask8; coords (B, N, 2) i64/i32 -> coords32
+ *   seq_lens[b] = n_tokens + (last live cell + 1)
+ *   seq_mask (B, n_tokens + N) u8: 1 for token rows, mask for cell rows
+ *   feats (B, N, F) of feats_dt -> xin (B, N, 32) bf16 zero-padded (if feats)
+ * Any output pointer may be NULL to skip it.
+ * ---------------------------------------------------------------------- */
+int shrimp_prep_inputs(const void* nbr, int nbr_dt, const void* mask, const void* coords,
+                       int coords_dt, const void* feats, int feats_dt, int nfeat, int B, int N,
+                       int n_tokens, int32_t* idx, uint8_t* mask8, int32_t* coords32,
+                       int32_t* seq_lens, uint8_t* seq_mask, void* xin, void* stream);
+
+/* seq[b, t, :] = tokens[t, :] (bf16) for t < n_tokens; seq rows are C apart,
+ * positions seq_sb apart. */
+int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void* seq, int64_t seq_sb, int B,
+                       void* stream);
+
+/* ------------------------------------------------------------------------
+ * Trunk tail + value head (model.py:927-935, 990-1002):
+ *   seq_f = LayerNorm(seq) (all S rows, fp32 stats), cell rows * mask -> out_seq (bf16)
+ *   pooled = masked mean of the normalized cells (count clamped to 1)
+ *   value = value_head(relu(value_reduction([T0, T1, pooled])))  -> value (B, 65) fp32
+ *   moves_left likewise from [T4, T5, pooled] when ml_* are non-NULL.
+ * Linear weights here are fp32 (out, in) as stored by nn.Linear.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* seq; /* (B, S, C) bf16 */
+  int64_t s_sb;
+  const uint8_t* mask; /* (B, N) */
+  const float* ln_w;
+  const float* ln_b;
+  float eps;
+  void* out_seq; /* (B, S, C) bf16 */
+  const float* vr_w; const float* vr_b; /* (C, 3C), (C) */
+  const float* vh_w; const float* vh_b; /* (bins, C), (bins) */
+  float* value;                         /* (B, bins) */
+  const float* mr_w; const float* mr_b;
+  const float* mh_w; const float* mh_b;
+  float* moves_left;
+  int32_t B, S, n_tokens, C, bins;
+} shrimp_tail_args;
+
+int shrimp_trunk_tail(const shrimp_tail_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Serve decode (inference.py:998-1042, losses.py:40-60):
+ *   value[b] = clamp(sum softmax(value_logits[b]) * linspace(-1,1,bins), -1, 1)
+ *   ml[b]    = (clamp(...) + 1) / 2 * ml_cap                  (if ml_logits)
+ *   priors[out_off[b] + i] = softmax(policy[b, :legal[b]])_i  (fp32)
+ *     (policy rows are pol_sb apart and pol_sb long; legal[b] is clamped to it)
+ *   logits_out[out_off[b] + i] = policy[b, i]                  (if logits_out)
+ * ---------------------------------------------------------------------- */
+int shrimp_decode(const float* value_logits, const float* ml_logits, const float* policy,
+                  int64_t pol_sb, const int32_t* legal, const int64_t* out_off, int B, int bins,
+                  float ml_cap, float* value, float* ml, float* priors, float* logits_out,
+                  void* stream);
+
+/* ------------------------------------------------------------------------
+ * Index builders kept for the reference operator ABI and its tests.
+ *   pair (B, S, S) u8 (model.py:762-792): rows from the (2M+1)^2 LUT for
+ *     cell pairs (key - query offset), token rows, pad keys -> pad_row.
+ *   ray gather index (B, N, 32) int32 (hexfield_eq/_triton_ray.py:221-281):
+ *     slot 0 = self, slot 1 + axis*10 + dir*5 + (k-1) = live cell at
+ *     coords + dir_sign * k * axis (axes Q, R, QR), slot 31 = N.
+ * ---------------------------------------------------------------------- */
+int shrimp_build_pair_u8(const int32_t* coords, const uint8_t* mask, const uint8_t* lut,
+                         int lut_m, int B, int N, int n_tokens, int row_ct, int row_tc,
+                         int row_tt, int pad_row, uint8_t* pair, void* stream);
+int shrimp_build_ray_index(const int32_t* coords, const uint8_t* mask, int B, int N,
+                           int32_t* idx, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SHRIMP_HIP_H */

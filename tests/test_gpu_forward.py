@@ -1,0 +1,137 @@
+"""Full serve forward on the GPU against the reference goldens and the CPU
+oracle. Tolerance: policy logits, value logits and decoded value within
+2e-2 absolute (bf16 path vs the fp32 reference)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode as odec
+from oracle import forward as ofwd
+from oracle import weights
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 2e-2
+
+
+def _net(c, h, layout, seed, mode="parity"):
+    from shrimp.model import ShrimpNet
+
+    net = ShrimpNet(channels=c, attention_heads=h, trunk_layout=layout)
+    net.load_state_dict(weights.make_state_dict(c, h, layout, seed=seed, mode=mode))
+    return net.to(DEV).eval()
+
+
+def _run(net, feats, nbr, mask, coords, ml=True):
+    t = lambda a: torch.as_tensor(a).to(DEV)
+    out = net.forward_policy_value(t(feats), t(nbr), t(mask), t(coords), request_moves_left=ml)
+    return {k: v.cpu().double() for k, v in out.items()}
+
+
+def _check(out, want, mask, what):
+    for key in ("policy", "value", "moves_left"):
+        if key not in want:
+            continue
+        w = torch.as_tensor(want[key]).double()
+        err = (out[key] - w).abs().max().item()
+        print(f"{what} {key}: max abs err {err:.3e} (|ref| max {w.abs().max().item():.3f})", flush=True)
+        assert err <= TOL, f"{what}/{key}: {err}"
+    v_got = odec.decode_value(out["value"])
+    v_want = odec.decode_value(torch.as_tensor(want["value"]).double())
+    assert (v_got - v_want).abs().max().item() <= TOL
+    assert (out["policy"][~torch.as_tensor(mask)] == 0).all()
+
+
+@pytest.mark.parametrize("name,mode", [("forward_cfg0", "parity"), ("forward_cfg0", "fresh"),
+                                       ("forward_cfg4", "parity")])
+def test_forward_matches_reference_golden(golden, name, mode):
+    g = golden(name)
+    c, h = (int(x) for x in g["arch"])
+    net = _net(c, h, str(g["layout"]), int(g[f"{mode}_seed"]), mode)
+    out = _run(net, g["feats"], g["nbr"], g["mask"], g["coords"])
+    want = {k: g[f"{mode}_{k}"] for k in ("policy", "value", "moves_left")}
+    _check(out, want, g["mask"], f"{name}/{mode}")
+
+
+@pytest.fixture(scope="module")
+def cfg4_batch():
+    from shrimp import synthetic
+
+    return synthetic.position_batch("cfg4", 32, seed=77)
+
+
+def test_forward_cfg4_matches_oracle(cfg4_batch):
+    b = cfg4_batch
+    layout = "CCACCACCACCA"
+    net = _net(128, 8, layout, seed=5)
+    out = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+    want = ofwd.forward_policy_value(
+        weights.make_state_dict(128, 8, layout, seed=5), layout, 8, b["feats"], b["nbr"],
+        b["mask"], b["coords"], request_moves_left=True, dtype=torch.float32,
+    )
+    _check(out, want, b["mask"], "cfg4 B=32")
+
+
+def test_forward_feature_and_index_dtypes(cfg4_batch):
+    """f16 features + int32 nbr/coords (the evaluator wire types) give the
+    same result as f32 + int64 up to the f16 rounding of the features."""
+
+    b = cfg4_batch
+    net = _net(128, 8, "CCACCACCACCA", seed=5)
+    a = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+    c = _run(net, b["feats"].half(), b["nbr"].int(), b["mask"], b["coords"].int())
+    assert (a["policy"] - c["policy"]).abs().max().item() <= TOL
+
+
+def test_rows_are_independent_of_batch(cfg4_batch):
+    """padded == single-row (tests/test_shrimp_model.py:139-164): a row's
+    outputs do not depend on the rest of the batch (bit-exact here)."""
+
+    b = cfg4_batch
+    net = _net(128, 8, "CCACCACCACCA", seed=5)
+    full = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+    sub = [3, 17, 30]
+    part = _run(net, b["feats"][sub], b["nbr"][sub], b["mask"][sub], b["coords"][sub])
+    for key in ("policy", "value", "moves_left"):
+        assert torch.equal(full[key][sub], part[key]), key
+
+
+def test_evaluator_matches_reference_reply(golden):
+    from shrimp.inference import ShrimpEvaluator
+
+    g = golden("evaluator_cfg0")
+    payload = {
+        "abi": 1, "shape": tuple(int(x) for x in g["shape"]),
+        "node_feats": g["node_feats"].tobytes(), "node_qr": g["node_qr"].tobytes(),
+        "node_row_offsets": g["node_row_offsets"].tolist(), "nbr": g["nbr"].tobytes(),
+        "legal_counts": g["legal_counts"].tobytes(),
+        "request_moves_left": True, "request_logits": True,
+    }
+    ev = ShrimpEvaluator(_net(32, 4, "CCA", int(g["wseed"])), DEV)
+    reply = ev.evaluate_payload(payload)
+    for key, gk, tol in (("values_bytes", "values", TOL), ("priors_bytes", "priors", 5e-3),
+                         ("moves_left_bytes", "moves_left", 209 * TOL),
+                         ("priors_logits_bytes", "priors_logits", TOL)):
+        got = np.frombuffer(reply[key], np.float32)
+        assert got.shape == g[gk].shape, key
+        err = np.abs(got - g[gk]).max()
+        print(f"evaluator {key}: max abs err {err:.3e}", flush=True)
+        assert err <= tol, key
+
+
+def test_full_size_cfg4_properties():
+    """Config 4 at its real shape (B=512, Npad=256): finite outputs, pad
+    logits exactly zero, and rows equal to a sub-batch run."""
+
+    from shrimp import synthetic
+
+    b = synthetic.position_batch("cfg4", 512)
+    net = _net(128, 8, "CCACCACCACCA", seed=9)
+    out = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+    assert torch.isfinite(out["policy"]).all() and torch.isfinite(out["value"]).all()
+    assert (out["policy"][~b["mask"]] == 0).all()
+    sub = [0, 255, 511]
+    part = _run(net, b["feats"][sub], b["nbr"][sub], b["mask"][sub], b["coords"][sub])
+    assert torch.equal(out["policy"][sub], part["policy"])
+    assert torch.equal(out["value"][sub], part["value"])

@@ -1,0 +1,312 @@
+"""Operator-level parity of the gfx950 kernels against the CPU oracle.
+
+Inputs are rounded to bf16 before the oracle sees them, so the comparison
+measures the kernels' own arithmetic (fp32 accumulation, bf16 output):
+tolerance |got - want| <= 2e-2 + 1e-2 * |want| for bf16 outputs; integer
+tables are bit-exact."""
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode as odec
+from oracle import forward as ofwd
+from oracle import tables
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def bf(x):
+    return torch.as_tensor(x).to(torch.bfloat16).to(torch.float64)
+
+
+def close(got, want, atol=2e-2, rtol=1e-2, what=""):
+    got = got.detach().to("cpu", torch.float64)
+    want = want.detach().to("cpu", torch.float64)
+    err = (got - want).abs() - rtol * want.abs()
+    worst = err.max().item()
+    assert worst <= atol, f"{what}: max excess error {worst}"
+
+
+@pytest.fixture(scope="module")
+def conv_case():
+    from shrimp import synthetic
+
+    return synthetic.conv_inputs(6, channels=128)
+
+
+def _gidx(batch):
+    return torch.from_numpy(tables.gather_index(batch["nbr"].numpy()))
+
+
+@pytest.mark.parametrize("epi", ["plain", "ln_relu", "ln"])
+def test_hex_conv_ops(conv_case, epi):
+    torch.manual_seed(0)
+    b = conv_case["batch"]
+    x = torch.from_numpy(conv_case["x"])
+    w = torch.from_numpy(conv_case["w"])
+    bias = torch.from_numpy(conv_case["bias"])
+    gidx = _gidx(b)
+    mask = b["mask"]
+    lnw = torch.rand(128) + 0.5
+    lnb = torch.randn(128) * 0.1
+    if epi == "plain":
+        got = torch.ops.shrimp.hex_conv(x.to(DEV), gidx.to(DEV), mask.to(DEV), w.to(DEV), bias.to(DEV))
+        want = ofwd.hex_conv(bf(x), gidx, mask, bf(w), bias.double())
+    else:
+        relu = epi == "ln_relu"
+        got = torch.ops.shrimp.hex_conv_ln(
+            x.to(DEV), gidx.to(DEV), mask.to(DEV), w.to(DEV), bias.to(DEV), lnw.to(DEV),
+            lnb.to(DEV), 1e-5, relu,
+        )
+        want = ofwd.hex_conv_ln(bf(x), gidx, mask, bf(w), bias.double(), lnw.double(),
+                                lnb.double(), 1e-5, relu)
+    assert got.dtype == torch.bfloat16 and got.shape == want.shape
+    close(got, want, what=epi)
+    assert (got.cpu()[~mask] == 0).all()
+
+
+@pytest.mark.parametrize("c", [32, 64, 96, 192, 256])
+def test_hex_conv_widths(c):
+    from shrimp import synthetic
+
+    case = synthetic.conv_inputs(2, channels=c)
+    b = case["batch"]
+    x, w, bias = (torch.from_numpy(case[k]) for k in ("x", "w", "bias"))
+    gidx = _gidx(b)
+    got = torch.ops.shrimp.hex_conv(x.to(DEV), gidx.to(DEV), b["mask"].to(DEV), w.to(DEV), bias.to(DEV))
+    want = ofwd.hex_conv(bf(x), gidx, b["mask"], bf(w), bias.double())
+    close(got, want, what=f"C={c}")
+
+
+def test_conv_residual_and_head_epilogues(conv_case):
+    from shrimp import ops
+
+    b = conv_case["batch"]
+    B, N = b["mask"].shape
+    x = torch.from_numpy(conv_case["x"])
+    w = torch.from_numpy(conv_case["w"])
+    bias = torch.from_numpy(conv_case["bias"])
+    gidx = _gidx(b)
+    mask = b["mask"]
+    g = torch.rand(128) * 0.5 + 0.5
+    lnw = torch.rand(128) + 0.5
+    lnb = torch.randn(128) * 0.1
+    resid = torch.randn(B, N, 128) * mask[..., None]
+    xd = x.to(DEV, torch.bfloat16).contiguous()
+    idx = gidx.to(DEV, torch.int32).contiguous()
+    m8 = mask.to(DEV, torch.uint8)
+    wp = ops.pack_conv_weight(w.to(DEV))
+    out = resid.to(DEV, torch.bfloat16).contiguous()
+    resid_bf = bf(resid)
+    ops.launch_conv(
+        x=xd, x_sb=N * 128, x_sn=128, idx=idx, taps=7, idx_stride=7, mask8=m8, wpack=wp,
+        bias=bias.to(DEV), B=B, N=N, cin_pad=128, cout=128, ln_w=lnw.to(DEV), ln_b=lnb.to(DEV),
+        resid=out, r_sb=N * 128, r_sn=128, gamma=g.to(DEV), out=out, o_sb=N * 128, o_sn=128,
+    )
+    y = ofwd.hex_conv_ln(bf(x), gidx, mask, bf(w), bias.double(), lnw.double(), lnb.double(), 1e-5, False)
+    want = torch.relu(resid_bf + g.double() * y)
+    close(out, want, what="residual")
+
+    hw = torch.randn(128) * 0.1
+    hb = torch.randn(1)
+    head = torch.empty(B, N, device=DEV)
+    ops.launch_conv(
+        x=xd, x_sb=N * 128, x_sn=128, idx=idx, taps=7, idx_stride=7, mask8=m8, wpack=wp,
+        bias=bias.to(DEV), B=B, N=N, cin_pad=128, cout=128, relu=True, head_w=hw.to(DEV),
+        head_b=hb.to(DEV), head_out=head,
+    )
+    yc = torch.relu(ofwd.hex_conv(bf(x), gidx, mask, bf(w), bias.double()))
+    want = (yc @ hw.double() + hb.double()) * mask.double()
+    close(head, want, atol=1e-2, rtol=1e-3, what="head")
+    assert (head.cpu()[~mask] == 0).all()
+
+
+def test_prep_pair_and_ray_index_exact(golden):
+    from shrimp import _lib
+
+    g = golden("pair")
+    coords = torch.from_numpy(g["coords"])
+    mask = torch.from_numpy(g["mask"])
+    B, N = mask.shape
+    nbr = torch.from_numpy(golden("forward_cfg0")["nbr"])
+    lib = _lib.load()
+    idx = torch.empty(B, N, 7, dtype=torch.int32, device=DEV)
+    m8 = torch.empty(B, N, dtype=torch.uint8, device=DEV)
+    c32 = torch.empty(B, N, 2, dtype=torch.int32, device=DEV)
+    sl = torch.empty(B, dtype=torch.int32, device=DEV)
+    sm = torch.empty(B, N + 8, dtype=torch.uint8, device=DEV)
+    nb = nbr.to(DEV)
+    md = mask.to(DEV)
+    cd = coords.to(DEV)
+    _lib.check(lib.shrimp_prep_inputs(nb.data_ptr(), _lib.DT_I64, md.data_ptr(), cd.data_ptr(),
+                                      _lib.DT_I64, None, 0, 0, B, N, 8, idx.data_ptr(), m8.data_ptr(),
+                                      c32.data_ptr(), sl.data_ptr(), sm.data_ptr(), None,
+                                      _lib.stream_handle()), "prep")
+    np.testing.assert_array_equal(idx.cpu().numpy(), tables.gather_index(nbr.numpy()))
+    np.testing.assert_array_equal(sl.cpu().numpy(), tables.seq_lens(mask.numpy()))
+    np.testing.assert_array_equal(c32.cpu().numpy(), coords.numpy())
+    np.testing.assert_array_equal(sm.cpu().numpy()[:, 8:], mask.numpy())
+    assert (sm.cpu().numpy()[:, :8] == 1).all()
+
+    lut = torch.from_numpy(tables.cell_lut()).to(DEV)
+    pair = torch.empty(B, N + 8, N + 8, dtype=torch.uint8, device=DEV)
+    _lib.check(lib.shrimp_build_pair_u8(c32.data_ptr(), m8.data_ptr(), lut.data_ptr(), 17, B, N, 8,
+                                        234, 235, 236, 237, pair.data_ptr(), _lib.stream_handle()),
+               "pair")
+    np.testing.assert_array_equal(pair.cpu().numpy(), g["pair_u8"])
+
+    ridx = torch.empty(B, N, 32, dtype=torch.int32, device=DEV)
+    _lib.check(lib.shrimp_build_ray_index(c32.data_ptr(), m8.data_ptr(), B, N, ridx.data_ptr(),
+                                          _lib.stream_handle()), "ray")
+    np.testing.assert_array_equal(ridx.cpu().numpy(), golden("ray_index")["idx"])
+
+
+def test_raytap_conv_31_taps():
+    from shrimp import _lib, ops, synthetic
+
+    case = synthetic.raytap_inputs(4, channels=128)
+    b = case["batch"]
+    B, N = b["mask"].shape
+    coords = b["coords"].to(torch.int32)
+    mask = b["mask"]
+    ridx = torch.from_numpy(tables.ray_index(coords.numpy(), mask.numpy()))
+    x, w, bias = (torch.from_numpy(case[k]) for k in ("x", "w", "bias"))
+    lib = _lib.load()
+    c32 = coords.to(DEV).contiguous()
+    m8 = mask.to(DEV, torch.uint8)
+    idx = torch.empty(B, N, 32, dtype=torch.int32, device=DEV)
+    _lib.check(lib.shrimp_build_ray_index(c32.data_ptr(), m8.data_ptr(), B, N, idx.data_ptr(),
+                                          _lib.stream_handle()), "ray")
+    assert torch.equal(idx.cpu(), ridx)
+    out = torch.empty(B, N, 128, dtype=torch.bfloat16, device=DEV)
+    ops.launch_conv(
+        x=x.to(DEV, torch.bfloat16).contiguous(), x_sb=N * 128, x_sn=128, idx=idx, taps=31,
+        idx_stride=32, mask8=m8, wpack=ops.pack_conv_weight(w.to(DEV)), bias=bias.to(DEV),
+        B=B, N=N, cin_pad=128, cout=128, out=out, o_sb=N * 128, o_sn=128,
+    )
+    want = ofwd.raytap_conv(bf(x), ridx, mask, bf(w), bias.double())
+    close(out, want, what="raytap")
+
+
+@pytest.mark.parametrize("mode", ["qkv", "gelu", "resid", "plain"])
+@pytest.mark.parametrize("c", [32, 128])
+def test_linear_modes(mode, c):
+    from shrimp import _lib, ops
+
+    torch.manual_seed(1)
+    B, S, H = 3, 40, 4 if c == 32 else 8
+    d = c // H
+    dpad = max(16, -(-d // 16) * 16)
+    rows = B * S
+    n_in = 2 * c if mode == "resid" else c
+    n_out = {"qkv": 3 * c, "gelu": 2 * c, "resid": c, "plain": c}[mode]
+    x = torch.randn(rows, n_in)
+    w = torch.randn(n_out, n_in) * 0.1
+    bias = torch.randn(n_out) * 0.1
+    lnw = torch.rand(n_in) + 0.5
+    lnb = torch.randn(n_in) * 0.1
+    use_ln = mode in ("qkv", "gelu")
+    xd = x.to(DEV, torch.bfloat16).contiguous()
+    wp = ops.pack_linear_weight(w.to(DEV))
+    xin = bf(x)
+    if use_ln:
+        xin = torch.nn.functional.layer_norm(xin, (n_in,), lnw.double(), lnb.double(), 1e-5)
+        xin = bf(xin)  # the kernel feeds normalised rows to MFMA in bf16
+    y = xin @ bf(w).T + bias.double()
+    kw = dict(x=xd, x_sr=n_in, wpack=wp, bias=bias.to(DEV), rows=rows, n_in=n_in, n_out=n_out)
+    if use_ln:
+        kw.update(ln_w=lnw.to(DEV), ln_b=lnb.to(DEV), eps=1e-5)
+    if mode == "qkv":
+        out = torch.zeros(3, B, H, S, dpad, dtype=torch.bfloat16, device=DEV)
+        ops.launch_linear(mode=_lib.LIN_QKV, out=out, B=B, S=S, H=H, dpad=dpad, **kw)
+        want = y.reshape(B, S, 3, H, d).permute(2, 0, 3, 1, 4)
+        close(out[..., :d], want, what="qkv")
+        assert (out[..., d:] == 0).all()
+    elif mode == "gelu":
+        out = torch.empty(rows, n_out, dtype=torch.bfloat16, device=DEV)
+        ops.launch_linear(mode=_lib.LIN_GELU, out=out, o_sr=n_out, **kw)
+        close(out, torch.nn.functional.gelu(y), what="gelu")
+    elif mode == "resid":
+        res = torch.randn(rows, n_out)
+        g = torch.rand(n_out)
+        m = (torch.rand(rows) > 0.3)
+        out = res.to(DEV, torch.bfloat16).contiguous()
+        ops.launch_linear(mode=_lib.LIN_RESID, out=out, o_sr=n_out, resid=out, r_sr=n_out,
+                          gamma=g.to(DEV), mask=m.to(DEV, torch.uint8), **kw)
+        close(out, bf(res) + g.double() * y * m.double()[:, None], what="resid")
+    else:
+        out = torch.empty(rows, n_out, dtype=torch.bfloat16, device=DEV)
+        ops.launch_linear(mode=_lib.LIN_PLAIN, out=out, o_sr=n_out, **kw)
+        close(out, y, what="plain")
+
+
+@pytest.mark.parametrize("d", [16, 32, 64])
+def test_attn_pair_op(d):
+    torch.manual_seed(2)
+    B, H, S = 3, 4, 70
+    q, k, v = (torch.randn(B, H, S, d) for _ in range(3))
+    rows = 238
+    table2 = torch.randn(rows, H) * 0.5
+    table2[rows - 1] = -3.0e4
+    pair = torch.randint(0, rows - 1, (B, S, S), dtype=torch.uint8)
+    pair[1, :, 50:60] = rows - 1  # pad keys inside the bound
+    lens = torch.tensor([70, 61, 23], dtype=torch.int32)
+    got = torch.ops.shrimp.attn_pair(q.to(DEV), k.to(DEV), v.to(DEV), pair.to(DEV),
+                                     table2.to(DEV), lens.to(DEV))
+    want = ofwd.attn_pair(bf(q), bf(k), bf(v), pair, table2.double(), lens)
+    close(got, want, atol=1e-2, what=f"attn d={d}")
+
+
+def test_attn_offset_table_cfg2():
+    from shrimp import ops, synthetic
+
+    case = synthetic.attention_inputs(4, heads=8, d=16)
+    q, k, v = (torch.from_numpy(case[n]) for n in ("q", "k", "v"))
+    B, H, S, d = q.shape
+    table = torch.from_numpy(case["table"])  # (33*33, H)
+    btab = torch.cat([table, torch.zeros(3, H)]) * (1.0 / math.log(2.0))
+    coords = torch.from_numpy(case["coords"])
+    mask = torch.from_numpy(case["mask"])
+    lens = torch.from_numpy(case["lens"])
+    out = torch.empty(B, H, S, d, dtype=torch.bfloat16, device=DEV)
+    qd, kd, vd = (t.to(DEV, torch.bfloat16).contiguous() for t in (q, k, v))
+    ops.launch_attn(
+        q=qd, k=kd, v=vd, qkv_sb=H * S * d, qkv_sh=S * d, seq_lens=lens.to(DEV), o=out,
+        o_sb=H * S * d, o_sh=S * d, o_sr=d, B=B, S=S, H=H, d=d, dpad=16,
+        coords=coords.to(DEV, torch.int32).contiguous(), mask8=mask.to(DEV, torch.uint8),
+        btab=btab.to(DEV).contiguous(), lut_m=16, n_tokens=0,
+    )
+    want = ofwd.attn_offset_table(bf(q), bf(k), bf(v), coords, mask, table.double(), 16)
+    close(out, want, atol=1e-2, what="cfg2 attention")
+
+
+def test_decode_kernel(golden):
+    from shrimp import _lib
+
+    g = golden("decode")
+    logits = torch.from_numpy(g["logits"])
+    B = logits.shape[0]
+    pol = torch.randn(B, 50)
+    legal = torch.randint(1, 50, (B,), dtype=torch.int32)
+    off = torch.zeros(B, dtype=torch.int64)
+    off[1:] = torch.cumsum(legal.to(torch.int64), 0)[:-1]
+    total = int(legal.sum())
+    vals = torch.empty(B, device=DEV)
+    ml = torch.empty(B, device=DEV)
+    pri = torch.empty(total, device=DEV)
+    lg = torch.empty(total, device=DEV)
+    ld, pd = logits.to(DEV), pol.to(DEV)
+    _lib.check(_lib.load().shrimp_decode(
+        ld.data_ptr(), ld.data_ptr(), pd.data_ptr(), 50, legal.to(DEV).data_ptr(),
+        off.to(DEV).data_ptr(), B, 65, 209.0, vals.data_ptr(), ml.data_ptr(), pri.data_ptr(),
+        lg.data_ptr(), _lib.stream_handle()), "decode")
+    assert np.allclose(vals.cpu().numpy(), g["value"], atol=1e-6)
+    assert np.allclose(ml.cpu().numpy(), g["moves_left"], atol=1e-3)
+    want = torch.cat([torch.softmax(pol[i, : legal[i]].double(), 0) for i in range(B)])
+    assert torch.allclose(pri.cpu().double(), want, atol=1e-6)
+    assert torch.equal(lg.cpu(), torch.cat([pol[i, : legal[i]] for i in range(B)]))

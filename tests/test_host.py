@@ -1,0 +1,110 @@
+"""Host-side shrimp modules against the reference's golden outputs and the
+reference tests' invariants (tests/test_shrimp_geometry.py,
+tests/test_shrimp_support.py)."""
+
+import random
+
+import numpy as np
+import pytest
+
+from shrimp import constants as C
+from shrimp import features, geometry, support
+from shrimp.batching import collate_rows
+from shrimp.inference import plan_groups
+
+from oracle import tables
+
+
+def _facts(stones, owners):
+    from shrimp.synthetic import facts_from_stones
+
+    return facts_from_stones([tuple(s) for s in stones], owners)
+
+
+def test_support_and_features_match_reference(golden):
+    g = golden("support_features")
+    so = np.concatenate([[0], np.cumsum(g["n_stones"])])
+    no = np.concatenate([[0], np.cumsum(g["n_nodes"])])
+    for p in range(len(g["n_stones"])):
+        stones = g["stones"][so[p]:so[p + 1]].tolist()
+        owners = g["owners"][so[p]:so[p + 1]]
+        facts = _facts(stones, owners)
+        sup, feats = features.build_position(facts, radius=int(g["radius"][p]))
+        sl = slice(no[p], no[p + 1])
+        np.testing.assert_array_equal(sup.coords, g["coords"][sl])
+        np.testing.assert_array_equal(sup.nbr, g["nbr"][sl])
+        np.testing.assert_array_equal(sup.dist, g["dist"][sl])
+        assert [sup.legal_count, sup.stone_count, sup.halo_count] == g["counts"][p].tolist()
+        np.testing.assert_array_equal(feats, g["feats"][sl])
+
+
+def test_geometry_invariants():
+    rng = random.Random(13)
+    for _ in range(500):
+        dq, dr = rng.randint(-30, 30), rng.randint(-30, 30)
+        assert geometry.hex_dist(dq, dr) == (abs(dq) + abs(dr) + abs(dq + dr)) // 2
+        assert geometry.rel_bias_index(dq, dr) == tables.rel_bias_row(dq, dr)
+        for sym in range(12):
+            tq, tr = geometry.apply_d6(sym, dq, dr)
+            assert geometry.apply_d6(geometry.d6_inverse(sym), tq, tr) == (dq, dr)
+            assert geometry.hex_dist(tq, tr) == geometry.hex_dist(dq, dr)
+    d = C.DIRECTIONS
+    for i in range(6):
+        assert geometry.rot60(*d[i]) == d[(i + 1) % 6]
+        assert geometry.reflect(*d[i]) == d[5 - i]
+    for _ in range(200):
+        q, r = rng.randint(-2000, 2000), rng.randint(-2000, 2000)
+        assert geometry.unpack_action_id(geometry.pack_action_id(q, r)) == (q, r)
+    np.testing.assert_array_equal(geometry.cell_bias_lut(), tables.cell_lut())
+
+
+def test_support_invariants():
+    sup = support.build_support([])
+    assert sup.num_nodes == 7 and sup.legal_count == 1
+    rng = random.Random(3)
+    stones = list({(rng.randint(-6, 6), rng.randint(-6, 6)) for _ in range(15)})
+    sup = support.build_support(stones, radius=4)
+    n = sup.num_nodes
+    for i in range(n):
+        for k in range(6):
+            j = sup.nbr[i, k]
+            if j >= 0:
+                assert sup.nbr[j, (k + 3) % 6] == i
+    lg, st, ha = sup.segments()
+    for seg in (lg, st, ha):
+        rows = [tuple(sup.coords[i]) for i in seg]
+        assert rows == sorted(rows)
+    assert all(sup.dist[i] == 5 for i in ha)
+    with pytest.raises(support.SupportContractError):
+        support.build_support(stones, radius=4, expected_legal=[(100, 100)])
+
+
+def test_collate_pad_conventions():
+    rows = [features.build_position(_facts([(0, 0), (1, 0)], [0, 1]), radius=4)]
+    batch = collate_rows(rows, pad_to=128)
+    n = rows[0][0].num_nodes
+    assert batch["feats"].shape == (1, 128, 15)
+    assert (batch["nbr"][0, n:] == 128).all()
+    assert (batch["nbr"][0, :n] <= 128).all()
+    assert batch["mask"][0, :n].all() and not batch["mask"][0, n:].any()
+    with pytest.raises(ValueError):
+        collate_rows(rows, pad_to=n - 1)
+
+
+def test_plan_groups_matches_reference(golden):
+    g = golden("decode")
+    assert plan_groups(g["sizes"]) == [tuple(x) for x in g["groups"].tolist()]
+
+
+def test_synthetic_l256_generator():
+    from shrimp import synthetic
+
+    batch = synthetic.position_batch("cfg4", 24)
+    assert batch["feats"].shape == (24, 256, 15)
+    for facts, sup, _ in batch["rows"]:
+        assert sup.num_nodes <= 256
+        assert len(facts.records) >= 10
+    again = synthetic.position_batch("cfg4", 24)
+    assert np.array_equal(batch["feats"].numpy(), again["feats"].numpy())
+    spec = synthetic.position_batch("cfg4_spec", 4)
+    assert spec["feats"].shape[1] % 64 == 0 and spec["feats"].shape[1] > 256

@@ -1,0 +1,88 @@
+"""The C-ABI library: it loads, exports every symbol include/shrimp_hip.h
+declares, its struct layouts match the ctypes mirrors, and argument checks
+fail with a message before any device work (no GPU needed)."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from shrimp import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "shrimp_hip.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(shrimp_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} not built; run __graft_entry__.build()")
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    declared = _declared_functions()
+    assert declared, "no declarations parsed"
+    assert set(declared) == set(_lib.SIGNATURES), set(declared) ^ set(_lib.SIGNATURES)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_version(lib):
+    assert lib.shrimp_abi_version() == 1
+
+
+def test_struct_layouts_match_c(tmp_path):
+    exe = tmp_path / "abi_layout"
+    subprocess.run(
+        ["gcc", "-std=c99", f"-I{ROOT / 'include'}", str(ROOT / "tests" / "abi_layout.c"), "-o", str(exe)],
+        check=True,
+    )
+    lines = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    mirrors = {
+        "shrimp_conv_args": _lib.ConvArgs,
+        "shrimp_linear_args": _lib.LinearArgs,
+        "shrimp_attn_args": _lib.AttnArgs,
+        "shrimp_tail_args": _lib.TailArgs,
+    }
+    seen = 0
+    for line in filter(None, lines):
+        key, val = line.split()
+        sname, field = key.split(".")
+        cls = mirrors[sname]
+        if field == "__size__":
+            assert ctypes.sizeof(cls) == int(val), sname
+        else:
+            assert getattr(cls, field).offset == int(val), key
+        seen += 1
+    names = {f for cls in mirrors.values() for f, _ in cls._fields_}
+    assert seen == len(mirrors) + sum(len(c._fields_) for c in mirrors.values())
+    assert names
+
+
+def test_bad_arguments_fail_with_message(lib):
+    a = _lib.ConvArgs(B=1, N=4, cin_pad=33, cout=128, taps=7, idx_stride=7,
+                      x=1, idx=1, mask=1, w=1, bias=1, out=1, x_sn=64)
+    rc = lib.shrimp_hex_conv(ctypes.byref(a), None)
+    assert rc == -1
+    assert b"cin_pad" in lib.shrimp_last_error()
+    la = _lib.LinearArgs(rows=4, in_features=100, out_features=128, x=1, w=1, bias=1, out=1,
+                         x_sr=100, o_sr=128, mode=0)
+    assert lib.shrimp_linear(ctypes.byref(la), None) == -1
+    aa = _lib.AttnArgs(B=1, S=8, H=2, d=6, dpad=16, q=1, k=1, v=1, o=1, seq_lens=1)
+    assert lib.shrimp_attn(ctypes.byref(aa), None) == -1
+    assert b"head dim" in lib.shrimp_last_error()
+    assert lib.shrimp_build_ray_index(1, 1, 1, 5000, 1, None) == -1
+
+
+def test_missing_library_raises(tmp_path):
+    with pytest.raises(_lib.HipLibraryMissing):
+        _lib.load(tmp_path / "nope.so")
