@@ -300,11 +300,13 @@ def test_decode_kernel(golden):
     ml = torch.empty(B, device=DEV)
     pri = torch.empty(total, device=DEV)
     lg = torch.empty(total, device=DEV)
-    ld, pd = logits.to(DEV), pol.to(DEV)
+    # keep every device tensor referenced until the kernel has run
+    ld, pd, legd, offd = logits.to(DEV), pol.to(DEV), legal.to(DEV), off.to(DEV)
     _lib.check(_lib.load().shrimp_decode(
-        ld.data_ptr(), ld.data_ptr(), pd.data_ptr(), 50, legal.to(DEV).data_ptr(),
-        off.to(DEV).data_ptr(), B, 65, 209.0, vals.data_ptr(), ml.data_ptr(), pri.data_ptr(),
-        lg.data_ptr(), _lib.stream_handle()), "decode")
+        ld.data_ptr(), ld.data_ptr(), pd.data_ptr(), 50, legd.data_ptr(), offd.data_ptr(), B,
+        65, 209.0, vals.data_ptr(), ml.data_ptr(), pri.data_ptr(), lg.data_ptr(),
+        _lib.stream_handle()), "decode")
+    torch.cuda.synchronize()
     assert np.allclose(vals.cpu().numpy(), g["value"], atol=1e-6)
     assert np.allclose(ml.cpu().numpy(), g["moves_left"], atol=1e-3)
     want = torch.cat([torch.softmax(pol[i, : legal[i]].double(), 0) for i in range(B)])
