@@ -29,6 +29,129 @@ namespace shrimp {
 
 enum : int { KEY_CELL = 0, KEY_TOKEN = 1, KEY_DEAD = 2 };
 
+// Max over the 4 lane groups (l / 16) that share l % 16, on VALU lane swaps.
+SHRIMP_DEV float max_groups_swap(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const unsigned v = __float_as_uint(y);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+struct AttnLds {
+  unsigned short* Ks;  // [HG][SP][DP] key-major
+  unsigned short* Vt;  // [HG][DP][SP] dim-major
+  int2* kqr;           // [SP] key coordinates
+  int* kcls;           // [SP] KEY_CELL / KEY_TOKEN / KEY_DEAD
+  int* blk_gen;        // [SP / 16] 1 if the 16-key block holds a token or dead key
+  float* tab;          // [npos][HG] bias columns, log2(e) folded
+};
+
+struct AttnQuery {
+  int query, qq, qr;
+  bool qtok, qv;
+};
+
+// One chunk of NBK 16-key blocks for all HG heads of one 16-query block.
+// GENERAL handles token rows/columns, dead keys and the key bound; the fast
+// path assumes every key of the chunk is a live cell and the query is a cell.
+template <int DP, int HG, bool PAIR, int NBK, bool GENERAL>
+SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds& s, const AttnQuery& qi,
+                           int kb0, int L, int SP, int lr, int lg, float qk_scale, int npos,
+                           const u32x2 (&qf)[HG][DP / 16], float (&m)[HG], float (&l)[HG],
+                           f32x4 (&o)[HG][DP / 16]) {
+  constexpr int KD = DP / 16;
+  const int M = a.lut_m;
+  const int W = 2 * M + 1;
+  f32x4 sc4[HG][NBK];
+#pragma unroll
+  for (int kb = 0; kb < NBK; ++kb)
+#pragma unroll
+    for (int h = 0; h < HG; ++h) {
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) {
+        const u32x2 kf = *reinterpret_cast<const u32x2*>(
+            s.Ks + (h * SP + (kb0 + kb) * 16 + lr) * DP + kd * 16 + lg * 4);
+        acc = mfma16x16x16(kf, qf[h][kd], acc);
+      }
+      sc4[h][kb] = acc;
+    }
+  int pos[NBK][4];
+  bool live[NBK][4];
+#pragma unroll
+  for (int kb = 0; kb < NBK; ++kb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int key = (kb0 + kb) * 16 + lg * 4 + j;
+      live[kb][j] = true;
+      if (PAIR) {
+        if (GENERAL) live[kb][j] = key < L;
+        const uint8_t* prow = a.pair + (int64_t)blockIdx.y * a.p_sb + (int64_t)qi.query * a.p_sq;
+        const int p = (live[kb][j] && qi.qv) ? (int)prow[key] : 0;
+        pos[kb][j] = p < npos ? p : npos - 1;
+      } else {
+        const int2 kk = s.kqr[key];
+        const int dq = min(max(kk.x - qi.qq, -M), M);
+        const int dr = min(max(kk.y - qi.qr, -M), M);
+        int p = (dq + M) * W + (dr + M);
+        if (GENERAL) {
+          const int cls = s.kcls[key];
+          live[kb][j] = cls != KEY_DEAD;
+          const int tp = qi.qtok ? W * W + 2 : W * W;  // key token: (token q | cell q)
+          const int cp = qi.qtok ? W * W + 1 : p;      // key cell
+          p = cls == KEY_TOKEN ? tp : cp;
+        }
+        pos[kb][j] = p;
+      }
+    }
+#pragma unroll
+  for (int h = 0; h < HG; ++h) {
+    float sc[NBK][4];
+    float mx = SHRIMP_NEG_BIG;
+#pragma unroll
+    for (int kb = 0; kb < NBK; ++kb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float v = sc4[h][kb][j] * qk_scale + s.tab[pos[kb][j] * HG + h];
+        if (GENERAL) v = live[kb][j] ? v : SHRIMP_NEG_BIG;
+        sc[kb][j] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = max_groups_swap(mx);
+    const float mnew = fmaxf(m[h], mx);
+    const float alpha = __builtin_amdgcn_exp2f(m[h] - mnew);
+    m[h] = mnew;
+    float ps = 0.f;
+    u32x2 pf[NBK];
+#pragma unroll
+    for (int kb = 0; kb < NBK; ++kb) {
+      float p[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        p[j] = __builtin_amdgcn_exp2f(sc[kb][j] - mnew);
+        if (GENERAL) p[j] = live[kb][j] ? p[j] : 0.f;
+        ps += p[j];
+      }
+      pf[kb].x = pack_bf16x2(p[0], p[1]);
+      pf[kb].y = pack_bf16x2(p[2], p[3]);
+    }
+    l[h] = l[h] * alpha + ps;
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) {
+      f32x4 acc = o[h][kd] * alpha;
+#pragma unroll
+      for (int kb = 0; kb < NBK; ++kb) {
+        const u32x2 vf = *reinterpret_cast<const u32x2*>(
+            s.Vt + (h * DP + kd * 16 + lr) * SP + (kb0 + kb) * 16 + lg * 4);
+        acc = mfma16x16x16(vf, pf[kb], acc);
+      }
+      o[h][kd] = acc;
+    }
+  }
+}
+
 template <int DP, int HG, bool PAIR>
 __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, float qk_scale,
                                                    uint32_t qkv_bytes, int npos) {
@@ -44,12 +167,13 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   const int nt = a.n_tokens;
   const int NC = S - nt;
 
-  unsigned short* Ks = reinterpret_cast<unsigned short*>(smem);  // [HG][SP][DP]
-  unsigned short* Vt = Ks + HG * SP * DP;                         // [HG][DP][SP]
-  int* kq = reinterpret_cast<int*>(Vt + HG * DP * SP);            // [SP]
-  int* kr = kq + SP;
-  int* kc = kr + SP;
-  float* tab = reinterpret_cast<float*>(kc + SP);  // [npos][HG]
+  AttnLds s;
+  s.Ks = reinterpret_cast<unsigned short*>(smem);
+  s.Vt = s.Ks + HG * SP * DP;
+  s.kqr = reinterpret_cast<int2*>(s.Vt + HG * DP * SP);
+  s.kcls = reinterpret_cast<int*>(s.kqr + SP);
+  s.blk_gen = s.kcls + SP;
+  s.tab = reinterpret_cast<float*>(s.blk_gen + SP / 16);
 
   const int tid = threadIdx.x;
   const __amdgpu_buffer_rsrc_t qrs = make_rsrc(a.q, qkv_bytes);
@@ -67,9 +191,9 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     const uint32_t off =
         key < L ? (uint32_t)((pos_base + (int64_t)(h0 + h) * a.qkv_sh + key * DP + ch * 8) * 2)
                 : SHRIMP_OOB_OFFSET;
-    *reinterpret_cast<u32x4*>(Ks + (h * SP + key) * DP + ch * 8) = buf_load16(krs, off);
+    *reinterpret_cast<u32x4*>(s.Ks + (h * SP + key) * DP + ch * 8) = buf_load16(krs, off);
   }
-  // ---- stage V^T (dim-major), two keys per dword --------------------------------
+  // ---- stage V^T (dim-major), keys (2k, 2k+1) packed per dword -------------------
   for (int i = tid; i < HG * (LP / 2) * CH; i += 256) {
     const int h = i / ((LP / 2) * CH);
     const int rem = i - h * (LP / 2) * CH;
@@ -82,13 +206,13 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const int d = ch * 8 + 2 * w;
-      Vt[(h * DP + d) * SP + key] = (unsigned short)(v0[w] & 0xFFFF);
-      Vt[(h * DP + d) * SP + key + 1] = (unsigned short)(v1[w] & 0xFFFF);
-      Vt[(h * DP + d + 1) * SP + key] = (unsigned short)(v0[w] >> 16);
-      Vt[(h * DP + d + 1) * SP + key + 1] = (unsigned short)(v1[w] >> 16);
+      unsigned* lo = reinterpret_cast<unsigned*>(s.Vt + (h * DP + d) * SP + key);
+      unsigned* hi = reinterpret_cast<unsigned*>(s.Vt + (h * DP + d + 1) * SP + key);
+      *lo = (v0[w] & 0xFFFFu) | (v1[w] << 16);
+      *hi = (v0[w] >> 16) | (v1[w] & 0xFFFF0000u);
     }
   }
-  // ---- key classes / coordinates -------------------------------------------------
+  // ---- key classes / coordinates / per-block flags ---------------------------------
   if (!PAIR) {
     for (int key = tid; key < LP; key += 256) {
       int q = 0, r = 0, cls = KEY_DEAD;
@@ -100,16 +224,24 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
         r = a.coords[cell * 2 + 1];
         cls = a.mask[cell] ? KEY_CELL : KEY_DEAD;
       }
-      kq[key] = q;
-      kr[key] = r;
-      kc[key] = cls;
+      s.kqr[key] = make_int2(q, r);
+      s.kcls[key] = cls;
     }
+  }
+  for (int blk = tid; blk < LP / 16; blk += 256) {
+    int gen = 0;
+    for (int j = 0; j < 16; ++j) {
+      const int key = blk * 16 + j;
+      if (key >= L || key < nt) gen = 1;
+      else if (!PAIR && !a.mask[(int64_t)b * NC + (key - nt)]) gen = 1;
+    }
+    s.blk_gen[blk] = gen;
   }
   // ---- bias columns of this head group --------------------------------------------
   for (int i = tid; i < npos * HG; i += 256) {
     const int pos = i / HG;
     const int h = i - pos * HG;
-    tab[i] = PAIR ? a.table2[pos * a.H + h0 + h] * SHRIMP_LOG2E : a.btab[pos * a.H + h0 + h];
+    s.tab[i] = PAIR ? a.table2[pos * a.H + h0 + h] * SHRIMP_LOG2E : a.btab[pos * a.H + h0 + h];
   }
   __syncthreads();
 
@@ -117,27 +249,29 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   const int wave = tid >> 6;
   const int lr = lane & 15;
   const int lg = lane >> 4;
-  const int M = a.lut_m;
-  const int W = 2 * M + 1;
-  const int pos_ct = W * W, pos_tc = W * W + 1, pos_tt = W * W + 2;
+  const int nkb = LP / 16;
 
   for (int qb = wave; qb * 16 < L; qb += 4) {
-    const int query = qb * 16 + lr;
-    const bool qv = query < L;
+    AttnQuery qi;
+    qi.query = qb * 16 + lr;
+    qi.qv = qi.query < L;
+    qi.qtok = qi.query < nt;
+    qi.qq = 0;
+    qi.qr = 0;
+    if (!PAIR) {
+      const int2 qc = s.kqr[qi.query];
+      qi.qq = qc.x;
+      qi.qr = qc.y;
+    }
+    const bool qgen = qb * 16 < nt;  // wave-uniform
     u32x2 qf[HG][KD];
 #pragma unroll
     for (int h = 0; h < HG; ++h)
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd) {
-        const int64_t e = pos_base + (int64_t)(h0 + h) * a.qkv_sh + query * DP + kd * 16 + lg * 4;
-        qf[h][kd] = buf_load8(qrs, qv ? (uint32_t)(e * 2) : SHRIMP_OOB_OFFSET);
+        const int64_t e = pos_base + (int64_t)(h0 + h) * a.qkv_sh + qi.query * DP + kd * 16 + lg * 4;
+        qf[h][kd] = buf_load8(qrs, qi.qv ? (uint32_t)(e * 2) : SHRIMP_OOB_OFFSET);
       }
-    const bool qtok = query < nt;
-    int qq = 0, qr = 0;
-    if (!PAIR) {
-      qq = kq[query];
-      qr = kr[query];
-    }
     float m[HG], l[HG];
     f32x4 o[HG][KD];
 #pragma unroll
@@ -148,74 +282,22 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
       for (int kd = 0; kd < KD; ++kd) o[h][kd] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    for (int kb = 0; kb < LP / 16; ++kb) {
-      const int key0 = kb * 16 + lg * 4;
-      int pos[4];
-      bool live[4];
-      if (PAIR) {
-        const uint8_t* prow = a.pair + (int64_t)b * a.p_sb + (int64_t)query * a.p_sq;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int key = key0 + j;
-          live[j] = key < L;
-          int p = (live[j] && qv) ? (int)prow[key] : 0;
-          pos[j] = p < npos ? p : npos - 1;
-        }
+    int kb = 0;
+    while (kb < nkb) {
+      if (nkb - kb >= 4) {
+        const bool gen = qgen || (s.blk_gen[kb] | s.blk_gen[kb + 1] | s.blk_gen[kb + 2] |
+                                  s.blk_gen[kb + 3]);
+        if (gen)
+          attn_chunk<DP, HG, PAIR, 4, true>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, qf, m, l, o);
+        else
+          attn_chunk<DP, HG, PAIR, 4, false>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, qf, m, l, o);
+        kb += 4;
       } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int key = key0 + j;
-          const int cls = kc[key];
-          live[j] = cls != KEY_DEAD;
-          if (cls == KEY_TOKEN) {
-            pos[j] = qtok ? pos_tt : pos_ct;
-          } else {
-            int dq = kq[key] - qq;
-            int dr = kr[key] - qr;
-            dq = dq < -M ? -M : (dq > M ? M : dq);
-            dr = dr < -M ? -M : (dr > M ? M : dr);
-            pos[j] = qtok ? pos_tc : (dq + M) * W + (dr + M);
-          }
-        }
-      }
-#pragma unroll
-      for (int h = 0; h < HG; ++h) {
-        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kd = 0; kd < KD; ++kd) {
-          const u32x2 kf =
-              *reinterpret_cast<const u32x2*>(Ks + (h * SP + kb * 16 + lr) * DP + kd * 16 + lg * 4);
-          s = mfma16x16x16(kf, qf[h][kd], s);
-        }
-        float sc[4];
-        float mx = SHRIMP_NEG_BIG;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          sc[j] = live[j] ? s[j] * qk_scale + tab[pos[j] * HG + h] : SHRIMP_NEG_BIG;
-          mx = fmaxf(mx, sc[j]);
-        }
-        mx = max_lane_groups(mx);
-        const float mnew = fmaxf(m[h], mx);
-        const float alpha = __builtin_amdgcn_exp2f(m[h] - mnew);
-        float p[4];
-        float ps = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          p[j] = live[j] ? __builtin_amdgcn_exp2f(sc[j] - mnew) : 0.f;
-          ps += p[j];
-        }
-        l[h] = l[h] * alpha + ps;
-        m[h] = mnew;
-        u32x2 pf;
-        pf.x = pack_bf16x2(p[0], p[1]);
-        pf.y = pack_bf16x2(p[2], p[3]);
-#pragma unroll
-        for (int kd = 0; kd < KD; ++kd) {
-          o[h][kd] *= alpha;
-          const u32x2 vf =
-              *reinterpret_cast<const u32x2*>(Vt + (h * DP + kd * 16 + lr) * SP + kb * 16 + lg * 4);
-          o[h][kd] = mfma16x16x16(vf, pf, o[h][kd]);
-        }
+        if (qgen || s.blk_gen[kb])
+          attn_chunk<DP, HG, PAIR, 1, true>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, qf, m, l, o);
+        else
+          attn_chunk<DP, HG, PAIR, 1, false>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, qf, m, l, o);
+        kb += 1;
       }
     }
 
@@ -223,9 +305,9 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     for (int h = 0; h < HG; ++h) {
       const float lt = sum_lane_groups(l[h]);
       const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-      if (!qv) continue;
+      if (!qi.qv) continue;
       unsigned short* orow = static_cast<unsigned short*>(a.o) + (int64_t)b * a.o_sb +
-                             (int64_t)(h0 + h) * a.o_sh + (int64_t)query * a.o_sr;
+                             (int64_t)(h0 + h) * a.o_sh + (int64_t)qi.query * a.o_sr;
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd) {
         const int e = kd * 16 + lg * 4;
@@ -254,7 +336,8 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
 
 static size_t attn_smem_bytes(int DP, int HG, int S, int npos) {
   const int SP = (S + 15) & ~15;
-  return (size_t)2 * HG * SP * DP * 2 + (size_t)3 * SP * 4 + (size_t)npos * HG * 4;
+  return (size_t)2 * HG * SP * DP * 2 + (size_t)SP * (8 + 4) + (size_t)(SP / 16) * 4 +
+         (size_t)npos * HG * 4;
 }
 
 template <int DP, int HG, bool PAIR>

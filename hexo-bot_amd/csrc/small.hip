@@ -103,20 +103,23 @@ __global__ __launch_bounds__(256) void tail_kernel(const shrimp_tail_args a) {
   const int S = a.S, nt = a.n_tokens, N = S - nt;
   const uint16_t* seq = static_cast<const uint16_t*>(a.seq) + (int64_t)b * a.s_sb;
   uint16_t* outs = static_cast<uint16_t*>(a.out_seq) + (int64_t)b * a.s_sb;
-  const int per = (C + 63) / 64;  // channels per lane (<= 4)
+  // C <= 256: each lane owns channels lane + 64u, u < 4 (fully unrolled so
+  // the per-lane arrays stay in registers).
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   int cnt = 0;
   for (int row = wave; row < S; row += 4) {
     float x[4];
     float s = 0.f;
-    for (int u = 0; u < per; ++u) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
       const int c = lane + 64 * u;
       x[u] = c < C ? bf16_bits_to_f32(seq[(int64_t)row * C + c]) : 0.f;
       s += x[u];
     }
     const float mean = wave_sum(s) / C;
     float q = 0.f;
-    for (int u = 0; u < per; ++u) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
       const int c = lane + 64 * u;
       x[u] = c < C ? x[u] - mean : 0.f;
       q += x[u] * x[u];
@@ -125,7 +128,8 @@ __global__ __launch_bounds__(256) void tail_kernel(const shrimp_tail_args a) {
     const bool is_cell = row >= nt;
     const bool live = !is_cell || a.mask[(int64_t)b * N + (row - nt)] != 0;
     if (is_cell && live) ++cnt;
-    for (int u = 0; u < per; ++u) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
       const int c = lane + 64 * u;
       if (c >= C) continue;
       float y = x[u] * rstd * a.ln_w[c] + a.ln_b[c];
@@ -138,7 +142,8 @@ __global__ __launch_bounds__(256) void tail_kernel(const shrimp_tail_args a) {
       if (row == 5) mlin[C + c] = y;
     }
   }
-  for (int u = 0; u < per; ++u) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
     const int c = lane + 64 * u;
     if (c < C) pool[wave * C + c] = acc[u];
   }
