@@ -82,7 +82,8 @@ def kernel_timings(net, inputs, reps=50):
         ops.launch_attn(
             q=qkv[0], k=qkv[1], v=qkv[2], qkv_sb=H * s * P.dpad, qkv_sh=s * P.dpad,
             seq_lens=L["seq_lens"], o=L["att"], o_sb=s * C, o_sh=P.d, o_sr=C, B=b, S=s, H=H,
-            d=P.d, dpad=P.dpad, coords=L["coords32"], mask8=L["mask8"], btab=a.btab,
+            d=P.d, dpad=P.dpad, coords=L["coords32"], mask8=L["mask8"], btab=a.btab_xtab[0],
+            xtab=a.btab_xtab[1],
             lut_m=CELL_LUT_M, n_tokens=8, stream=L["stream"],
         )
 

@@ -5,20 +5,28 @@
 // 677-760) and the serve kernel's key bound (_triton_attn.py:59-130):
 // keys >= seq_lens[b] are never visited, pad keys inside it get weight 0.
 //
-// One workgroup = one position x HG heads; K (key-major) and V (transposed,
-// dim-major) of those heads, the per-key coordinates and the heads' bias
-// columns are staged in LDS once, then each wave walks 16-query blocks.
-// Everything is kept in the "transposed" MFMA orientation so no value ever
-// changes lanes:
-//   S^T = K Q^T  (v_mfma_f32_16x16x16_bf16): lane l holds keys 4*(l/16)+j of
-//                query l%16 — exactly the B operand layout of P^T below;
-//   O^T += V^T P^T: lane l holds dims 4*(l/16)+j of query l%16, so the online
-//                softmax rescale uses the lane's own running max.
-// The bias row of a cell pair is computed in-kernel from coordinates through
-// the clamped offset LUT (coords mode) or read from the reference's uint8
-// pair tensor (pair mode); the pair index is computed once and reused by the
-// HG heads. Softmax runs in base 2 with log2(e) folded into the scale and the
-// staged bias table; statistics are fp32.
+// One workgroup = one position x HG heads. K (key-major) and V (dim-major) of
+// those heads, per-key coordinates and the heads' bias tables are staged in
+// LDS once; each wave then walks 16-query blocks over 16-key blocks. All
+// products stay in the "transposed" MFMA orientation so no value changes
+// lanes:
+//   S^T = K Q^T   (16x16x16): lane l holds keys 4*(l/16)+j of query l%16,
+//                 which is the B-operand layout of P^T;
+//   O^T += V^T P^T (16x16x32 over two key blocks): lane l holds dims
+//                 4*(l/16)+j of query l%16, so the online-softmax rescale uses
+//                 the lane's own running max;
+//   row sums: one more MFMA of P^T against a constant ones row of "V^T".
+// Key chunks take one of three bias paths (chosen per wave, uniformly):
+//   LINEAR  all keys live cells and the position's coordinate span <= 26:
+//           the offset LUT needs no clamping, so the bias index is
+//           kkey[key] - qkey[query] into an unclamped 53x53 fp16 table
+//           (the reference also rounds the table to fp16, model.py:741);
+//   CLAMP   all keys live cells, wider positions: clamped LUT index into the
+//           fp32 table in global memory (L1/L2 resident);
+//   GENERAL token rows / columns, dead keys, the key bound (and the pair
+//           tensor of the reference operator ABI).
+// Softmax runs in base 2 with log2(e) folded into scale and tables; scores,
+// statistics and accumulators are fp32, P enters the MFMAs as bf16.
 #include "capi.hpp"
 #include "common.hpp"
 
@@ -28,6 +36,11 @@ namespace shrimp {
 #define SHRIMP_NEG_BIG (-1.0e30f)
 
 enum : int { KEY_CELL = 0, KEY_TOKEN = 1, KEY_DEAD = 2 };
+enum : int { PATH_GENERAL = 0, PATH_CLAMP = 1, PATH_LINEAR = 2 };
+
+// Unclamped offset table: offsets with |dq|, |dr| <= XD.
+constexpr int XD = SHRIMP_ATTN_XD;
+constexpr int XW = 2 * XD + 1;
 
 // Max over the 4 lane groups (l / 16) that share l % 16, on VALU lane swaps.
 SHRIMP_DEV float max_groups_swap(float x) {
@@ -39,29 +52,34 @@ SHRIMP_DEV float max_groups_swap(float x) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+SHRIMP_DEV int clampi(int x, int m) { return min(max(x, -m), m); }
+
+template <int HG>
 struct AttnLds {
-  unsigned short* Ks;  // [HG][SP][DP] key-major
-  unsigned short* Vt;  // [HG][DP][SP] dim-major
+  unsigned short* Ks;  // [HG][KD][SP/16] K fragments (256 bf16 each)
+  unsigned short* Vt;  // [HG][KD][SP/16] V fragments (256 bf16 each)
   int2* kqr;           // [SP] key coordinates
+  int* kkey;           // [SP] q*XW + r + XD*XW + XD (linear offset code)
   int* kcls;           // [SP] KEY_CELL / KEY_TOKEN / KEY_DEAD
-  int* blk_gen;        // [SP / 16] 1 if the 16-key block holds a token or dead key
-  float* tab;          // [npos][HG] bias columns, log2(e) folded
+  int* blk_gen;        // [SP / 16] 1 if the block holds a token or dead key
+  float* tab;          // pair mode: [rows][HG] fp32 (log2e folded)
+  _Float16* xtab;      // coords mode: [XW*XW][HG] unclamped offset table, fp16
 };
 
 struct AttnQuery {
-  int query, qq, qr;
+  int query, qq, qr, qkey;
   bool qtok, qv;
 };
 
-// One chunk of NBK 16-key blocks for all HG heads of one 16-query block.
-// GENERAL handles token rows/columns, dead keys and the key bound; the fast
-// path assumes every key of the chunk is a live cell and the query is a cell.
-template <int DP, int HG, bool PAIR, int NBK, bool GENERAL>
-SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds& s, const AttnQuery& qi,
+// One chunk of NBK 16-key blocks (NBK in {1, 2, 4}) for the HG heads of one
+// 16-query block.
+template <int DP, int HG, bool PAIR, int NBK, int PATH>
+SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, const AttnQuery& qi,
                            int kb0, int L, int SP, int lr, int lg, float qk_scale, int npos,
                            const u32x2 (&qf)[HG][DP / 16], float (&m)[HG], float (&l)[HG],
                            f32x4 (&o)[HG][DP / 16]) {
   constexpr int KD = DP / 16;
+  const int NKB = SP / 16;
   const int M = a.lut_m;
   const int W = 2 * M + 1;
   f32x4 sc4[HG][NBK];
@@ -73,12 +91,13 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds& s, const At
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd) {
         const u32x2 kf = *reinterpret_cast<const u32x2*>(
-            s.Ks + (h * SP + (kb0 + kb) * 16 + lr) * DP + kd * 16 + lg * 4);
+            s.Ks + ((h * KD + kd) * NKB + kb0 + kb) * 256 + (lg * 16 + lr) * 4);
         acc = mfma16x16x16(kf, qf[h][kd], acc);
       }
       sc4[h][kb] = acc;
     }
-  int pos[NBK][4];
+  // Bias of every (key, head) of the chunk, fp32, log2e folded.
+  float bias[NBK][4][HG];
   bool live[NBK][4];
 #pragma unroll
   for (int kb = 0; kb < NBK; ++kb)
@@ -87,25 +106,42 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds& s, const At
       const int key = (kb0 + kb) * 16 + lg * 4 + j;
       live[kb][j] = true;
       if (PAIR) {
-        if (GENERAL) live[kb][j] = key < L;
+        if (PATH == PATH_GENERAL) live[kb][j] = key < L;
         const uint8_t* prow = a.pair + (int64_t)blockIdx.y * a.p_sb + (int64_t)qi.query * a.p_sq;
-        const int p = (live[kb][j] && qi.qv) ? (int)prow[key] : 0;
-        pos[kb][j] = p < npos ? p : npos - 1;
+        int p = (live[kb][j] && qi.qv) ? (int)prow[key] : 0;
+        p = p < npos ? p : npos - 1;
+#pragma unroll
+        for (int h = 0; h < HG; ++h) bias[kb][j][h] = s.tab[p * HG + h];
+      } else if (PATH == PATH_LINEAR) {
+        const int p = s.kkey[key] - qi.qkey;
+        if (HG == 2) {
+          const unsigned w = reinterpret_cast<const unsigned*>(s.xtab)[p];
+          bias[kb][j][0] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xFFFFu));
+          bias[kb][j][HG - 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> 16));
+        } else {
+#pragma unroll
+          for (int h = 0; h < HG; ++h) bias[kb][j][h] = (float)s.xtab[p * HG + h];
+        }
       } else {
         const int2 kk = s.kqr[key];
-        const int dq = min(max(kk.x - qi.qq, -M), M);
-        const int dr = min(max(kk.y - qi.qr, -M), M);
-        int p = (dq + M) * W + (dr + M);
-        if (GENERAL) {
+        const int p = (clampi(kk.x - qi.qq, M) + M) * W + (clampi(kk.y - qi.qr, M) + M);
+        if (PATH == PATH_CLAMP) {
+#pragma unroll
+          for (int h = 0; h < HG; ++h) bias[kb][j][h] = a.btab[p * a.H + blockIdx.x * HG + h];
+        } else {
           const int cls = s.kcls[key];
           live[kb][j] = cls != KEY_DEAD;
-          const int tp = qi.qtok ? W * W + 2 : W * W;  // key token: (token q | cell q)
+          const int tp = qi.qtok ? W * W + 2 : W * W;  // key token: (token | cell) query
           const int cp = qi.qtok ? W * W + 1 : p;      // key cell
-          p = cls == KEY_TOKEN ? tp : cp;
+          const int pp = cls == KEY_TOKEN ? tp : cp;
+#pragma unroll
+          for (int h = 0; h < HG; ++h) bias[kb][j][h] = a.btab[pp * a.H + blockIdx.x * HG + h];
         }
-        pos[kb][j] = p;
       }
     }
+  // Constant A fragment: row 0 of "V^T" is all ones, so P^T times it gives the
+  // per-query sum of P in accumulator row 0 (lane group 0, element 0).
+  const unsigned one2 = lr == 0 ? 0x3F803F80u : 0u;
 #pragma unroll
   for (int h = 0; h < HG; ++h) {
     float sc[NBK][4];
@@ -114,8 +150,8 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds& s, const At
     for (int kb = 0; kb < NBK; ++kb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float v = sc4[h][kb][j] * qk_scale + s.tab[pos[kb][j] * HG + h];
-        if (GENERAL) v = live[kb][j] ? v : SHRIMP_NEG_BIG;
+        float v = fmaf(sc4[h][kb][j], qk_scale, bias[kb][j][h]);
+        if (PATH == PATH_GENERAL) v = live[kb][j] ? v : SHRIMP_NEG_BIG;
         sc[kb][j] = v;
         mx = fmaxf(mx, v);
       }
@@ -123,7 +159,6 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds& s, const At
     const float mnew = fmaxf(m[h], mx);
     const float alpha = __builtin_amdgcn_exp2f(m[h] - mnew);
     m[h] = mnew;
-    float ps = 0.f;
     u32x2 pf[NBK];
 #pragma unroll
     for (int kb = 0; kb < NBK; ++kb) {
@@ -131,24 +166,43 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds& s, const At
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         p[j] = __builtin_amdgcn_exp2f(sc[kb][j] - mnew);
-        if (GENERAL) p[j] = live[kb][j] ? p[j] : 0.f;
-        ps += p[j];
+        if (PATH == PATH_GENERAL) p[j] = live[kb][j] ? p[j] : 0.f;
       }
       pf[kb].x = pack_bf16x2(p[0], p[1]);
       pf[kb].y = pack_bf16x2(p[2], p[3]);
     }
-    l[h] = l[h] * alpha + ps;
+    f32x4 lacc = f32x4{l[h] * alpha, 0.f, 0.f, 0.f};
+    f32x4 acc[KD];
 #pragma unroll
-    for (int kd = 0; kd < KD; ++kd) {
-      f32x4 acc = o[h][kd] * alpha;
+    for (int kd = 0; kd < KD; ++kd) acc[kd] = o[h][kd] * alpha;
+    if (NBK == 1) {
+      const u32x2 ones = u32x2{one2, one2};
+      lacc = mfma16x16x16(ones, pf[0], lacc);
 #pragma unroll
-      for (int kb = 0; kb < NBK; ++kb) {
+      for (int kd = 0; kd < KD; ++kd) {
         const u32x2 vf = *reinterpret_cast<const u32x2*>(
-            s.Vt + (h * DP + kd * 16 + lr) * SP + (kb0 + kb) * 16 + lg * 4);
-        acc = mfma16x16x16(vf, pf[kb], acc);
+            s.Vt + ((h * KD + kd) * NKB + kb0) * 256 + (lg * 16 + lr) * 4);
+        acc[kd] = mfma16x16x16(vf, pf[0], acc[kd]);
       }
-      o[h][kd] = acc;
+    } else {
+      const u32x4 ones = u32x4{one2, one2, one2, one2};
+#pragma unroll
+      for (int kp = 0; kp < NBK; kp += 2) {
+        // k slots 0-3 of lane group g: keys 4g..4g+3 of block kp; 4-7: of kp+1.
+        const u32x4 pp = u32x4{pf[kp].x, pf[kp].y, pf[kp + 1].x, pf[kp + 1].y};
+        lacc = mfma16x16x32(ones, pp, lacc);
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd) {
+          const unsigned short* vf = s.Vt + ((h * KD + kd) * NKB + kb0 + kp) * 256 + (lg * 16 + lr) * 4;
+          const u32x2 v0 = *reinterpret_cast<const u32x2*>(vf);
+          const u32x2 v1 = *reinterpret_cast<const u32x2*>(vf + 256);
+          acc[kd] = mfma16x16x32(u32x4{v0.x, v0.y, v1.x, v1.y}, pp, acc[kd]);
+        }
+      }
     }
+    l[h] = lacc[0];
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) o[h][kd] = acc[kd];
   }
 }
 
@@ -156,6 +210,7 @@ template <int DP, int HG, bool PAIR>
 __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, float qk_scale,
                                                    uint32_t qkv_bytes, int npos) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  __shared__ int span_red[16];
   constexpr int KD = DP / 16;
   const int b = blockIdx.y;
   const int h0 = blockIdx.x * HG;
@@ -167,13 +222,18 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   const int nt = a.n_tokens;
   const int NC = S - nt;
 
-  AttnLds s;
+  const int NKB = SP / 16;
+  AttnLds<HG> s;
   s.Ks = reinterpret_cast<unsigned short*>(smem);
   s.Vt = s.Ks + HG * SP * DP;
   s.kqr = reinterpret_cast<int2*>(s.Vt + HG * DP * SP);
-  s.kcls = reinterpret_cast<int*>(s.kqr + SP);
+  s.kkey = reinterpret_cast<int*>(s.kqr + SP);
+  s.kcls = s.kkey + SP;
   s.blk_gen = s.kcls + SP;
-  s.tab = reinterpret_cast<float*>(s.blk_gen + SP / 16);
+  int* q_gen = s.blk_gen + NKB;
+  float* tail = reinterpret_cast<float*>(q_gen + NKB);
+  s.tab = tail;
+  s.xtab = reinterpret_cast<_Float16*>(tail);
 
   const int tid = threadIdx.x;
   const __amdgpu_buffer_rsrc_t qrs = make_rsrc(a.q, qkv_bytes);
@@ -181,38 +241,83 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(a.v, qkv_bytes);
   const int64_t pos_base = (int64_t)b * a.qkv_sb;
 
-  // ---- stage K (key-major) ---------------------------------------------------
+  // ---- stage K and V in MFMA fragment order -----------------------------------
+  // K fragment (h, kd, kb): lane (lr, lg) holds K[kb*16 + lr][kd*16 + 4lg .. +3];
+  // V fragment (h, kd, kb): lane (lr, lg) holds V[kb*16 + 4lg .. +3][kd*16 + lr].
+  // A wave's fragment read is then one contiguous 512-byte LDS block.
+  // Global loads are issued U at a time per thread before their LDS stores.
   constexpr int CH = DP / 8;
-  for (int i = tid; i < HG * LP * CH; i += 256) {
-    const int h = i / (LP * CH);
-    const int rem = i - h * LP * CH;
-    const int key = rem / CH;
-    const int ch = rem - key * CH;
-    const uint32_t off =
-        key < L ? (uint32_t)((pos_base + (int64_t)(h0 + h) * a.qkv_sh + key * DP + ch * 8) * 2)
-                : SHRIMP_OOB_OFFSET;
-    *reinterpret_cast<u32x4*>(s.Ks + (h * SP + key) * DP + ch * 8) = buf_load16(krs, off);
-  }
-  // ---- stage V^T (dim-major), keys (2k, 2k+1) packed per dword -------------------
-  for (int i = tid; i < HG * (LP / 2) * CH; i += 256) {
-    const int h = i / ((LP / 2) * CH);
-    const int rem = i - h * (LP / 2) * CH;
-    const int kp = rem / CH;
-    const int ch = rem - kp * CH;
-    const int key = 2 * kp;
-    const int64_t e0 = pos_base + (int64_t)(h0 + h) * a.qkv_sh + key * DP + ch * 8;
-    const u32x4 v0 = buf_load16(vrs, key < L ? (uint32_t)(e0 * 2) : SHRIMP_OOB_OFFSET);
-    const u32x4 v1 = buf_load16(vrs, key + 1 < L ? (uint32_t)((e0 + DP) * 2) : SHRIMP_OOB_OFFSET);
+  constexpr int U = 4;
+  {
+    const int total = HG * LP * CH;
+    for (int base = tid; base < total; base += 256 * U) {
+      u32x4 v[U];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const int d = ch * 8 + 2 * w;
-      unsigned* lo = reinterpret_cast<unsigned*>(s.Vt + (h * DP + d) * SP + key);
-      unsigned* hi = reinterpret_cast<unsigned*>(s.Vt + (h * DP + d + 1) * SP + key);
-      *lo = (v0[w] & 0xFFFFu) | (v1[w] << 16);
-      *hi = (v0[w] >> 16) | (v1[w] & 0xFFFF0000u);
+      for (int u = 0; u < U; ++u) {
+        const int i = base + u * 256;
+        const int h = i / (LP * CH);
+        const int rem = i - h * LP * CH;
+        const int key = rem / CH;
+        const int ch = rem - key * CH;
+        const bool ok = i < total && key < L;
+        v[u] = buf_load16(krs, ok ? (uint32_t)((pos_base + (int64_t)(h0 + h) * a.qkv_sh +
+                                               key * DP + ch * 8) * 2)
+                                  : SHRIMP_OOB_OFFSET);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = base + u * 256;
+        if (i >= total) break;
+        const int h = i / (LP * CH);
+        const int rem = i - h * LP * CH;
+        const int key = rem / CH;
+        const int ch = rem - key * CH;
+        const int kd = ch >> 1;
+        const int g0 = (ch & 1) * 2;  // lane group of dims ch*8 .. +3
+        unsigned short* f = s.Ks + ((h * KD + kd) * NKB + key / 16) * 256 + (key & 15) * 4;
+        *reinterpret_cast<u32x2*>(f + g0 * 64) = u32x2{v[u][0], v[u][1]};
+        *reinterpret_cast<u32x2*>(f + (g0 + 1) * 64) = u32x2{v[u][2], v[u][3]};
+      }
     }
   }
-  // ---- key classes / coordinates / per-block flags ---------------------------------
+  {
+    const int total = HG * (LP / 2) * CH;
+    for (int base = tid; base < total; base += 256 * U) {
+      u32x4 v0[U], v1[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = base + u * 256;
+        const int h = i / ((LP / 2) * CH);
+        const int rem = i - h * (LP / 2) * CH;
+        const int key = 2 * (rem / CH);
+        const int ch = rem - (key / 2) * CH;
+        const int64_t e0 = pos_base + (int64_t)(h0 + h) * a.qkv_sh + key * DP + ch * 8;
+        v0[u] = buf_load16(vrs, (i < total && key < L) ? (uint32_t)(e0 * 2) : SHRIMP_OOB_OFFSET);
+        v1[u] = buf_load16(vrs, (i < total && key + 1 < L) ? (uint32_t)((e0 + DP) * 2)
+                                                           : SHRIMP_OOB_OFFSET);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = base + u * 256;
+        if (i >= total) break;
+        const int h = i / ((LP / 2) * CH);
+        const int rem = i - h * (LP / 2) * CH;
+        const int key = 2 * (rem / CH);
+        const int ch = rem - (key / 2) * CH;
+        // keys (key, key+1) are j, j+1 of lane group (key % 16) / 4
+        unsigned short* f = s.Vt + ((h * KD + (ch >> 1)) * NKB + key / 16) * 256 +
+                            ((key & 15) >> 2) * 64 + (key & 3);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int lrd = (ch & 1) * 8 + 2 * w;  // dim within the 16-dim block
+          *reinterpret_cast<unsigned*>(f + lrd * 4) = (v0[u][w] & 0xFFFFu) | (v1[u][w] << 16);
+          *reinterpret_cast<unsigned*>(f + (lrd + 1) * 4) = (v0[u][w] >> 16) | (v1[u][w] & 0xFFFF0000u);
+        }
+      }
+    }
+  }
+  // ---- key classes, coordinates, span of the live cells ----------------------------
+  int qmin = 1 << 30, qmax = -(1 << 30), rmin = 1 << 30, rmax = -(1 << 30);
   if (!PAIR) {
     for (int key = tid; key < LP; key += 256) {
       int q = 0, r = 0, cls = KEY_DEAD;
@@ -223,25 +328,98 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
         q = a.coords[cell * 2];
         r = a.coords[cell * 2 + 1];
         cls = a.mask[cell] ? KEY_CELL : KEY_DEAD;
+        if (cls == KEY_CELL) {
+          qmin = min(qmin, q);
+          qmax = max(qmax, q);
+          rmin = min(rmin, r);
+          rmax = max(rmax, r);
+        }
       }
       s.kqr[key] = make_int2(q, r);
       s.kcls[key] = cls;
     }
   }
+  // ---- bias tables of this head group -------------------------------------------------
+  if (PAIR) {
+    for (int i = tid; i < npos * HG; i += 256) {
+      const int pos = i / HG;
+      const int h = i - pos * HG;
+      s.tab[i] = a.table2[pos * a.H + h0 + h] * SHRIMP_LOG2E;
+    }
+  } else if (a.xtab != nullptr) {
+    const unsigned short* xg = static_cast<const unsigned short*>(a.xtab);
+    if (HG == 2) {
+      constexpr int UX = 12;
+      for (int base = tid; base < XW * XW; base += 256 * UX) {
+        unsigned v[UX];
+#pragma unroll
+        for (int u = 0; u < UX; ++u) {
+          const int x = base + u * 256;
+          v[u] = x < XW * XW ? *reinterpret_cast<const unsigned*>(xg + (int64_t)x * a.H + h0) : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < UX; ++u) {
+          const int x = base + u * 256;
+          if (x < XW * XW) reinterpret_cast<unsigned*>(s.xtab)[x] = v[u];
+        }
+      }
+    } else {
+      for (int i = tid; i < XW * XW * HG; i += 256) {
+        const int x = i / HG;
+        reinterpret_cast<unsigned short*>(s.xtab)[i] = xg[(int64_t)x * a.H + h0 + (i - x * HG)];
+      }
+    }
+  }
+  // Coordinate span of the live cells (block-wide min / max).
+  bool linear_ok = false;
+  int safe_q = 0, safe_r = 0;
+  if (!PAIR) {
+    for (int m = 32; m >= 1; m >>= 1) {
+      qmin = min(qmin, __shfl_xor(qmin, m, 64));
+      qmax = max(qmax, __shfl_xor(qmax, m, 64));
+      rmin = min(rmin, __shfl_xor(rmin, m, 64));
+      rmax = max(rmax, __shfl_xor(rmax, m, 64));
+    }
+    if ((tid & 63) == 0) {
+      const int w = tid >> 6;
+      span_red[w * 4 + 0] = qmin;
+      span_red[w * 4 + 1] = qmax;
+      span_red[w * 4 + 2] = rmin;
+      span_red[w * 4 + 3] = rmax;
+    }
+  }
+  __syncthreads();
+  // Per-block flags, from the staged key classes: key blocks with a token, a
+  // dead key or keys past the bound; query blocks with a token or dead query.
   for (int blk = tid; blk < LP / 16; blk += 256) {
-    int gen = 0;
+    int kg = 0, qg = 0;
     for (int j = 0; j < 16; ++j) {
       const int key = blk * 16 + j;
-      if (key >= L || key < nt) gen = 1;
-      else if (!PAIR && !a.mask[(int64_t)b * NC + (key - nt)]) gen = 1;
+      const bool special = PAIR ? false : s.kcls[key] != KEY_CELL;
+      if (key >= L) kg = 1;
+      else if (special || key < nt) kg = qg = 1;
     }
-    s.blk_gen[blk] = gen;
+    s.blk_gen[blk] = kg;
+    q_gen[blk] = qg;
   }
-  // ---- bias columns of this head group --------------------------------------------
-  for (int i = tid; i < npos * HG; i += 256) {
-    const int pos = i / HG;
-    const int h = i - pos * HG;
-    s.tab[i] = PAIR ? a.table2[pos * a.H + h0 + h] * SHRIMP_LOG2E : a.btab[pos * a.H + h0 + h];
+  if (!PAIR) {
+    int q0 = span_red[0], q1 = span_red[1], r0 = span_red[2], r1 = span_red[3];
+    for (int w = 1; w < 4; ++w) {
+      q0 = min(q0, span_red[w * 4 + 0]);
+      q1 = max(q1, span_red[w * 4 + 1]);
+      r0 = min(r0, span_red[w * 4 + 2]);
+      r1 = max(r1, span_red[w * 4 + 3]);
+    }
+    // an empty cell set gives q1 < q0: nothing is indexed linearly then anyway
+    linear_ok = a.xtab != nullptr && (q1 - q0) <= XD && (r1 - r0) <= XD;
+    // queries past the bound borrow (q0, r0): offsets to live cells stay in range
+    safe_q = q0;
+    safe_r = r0;
+    // Linear offset code: (dq, dr) -> (dq + XD) * XW + (dr + XD) = kkey - qkey.
+    for (int key = tid; key < LP; key += 256) {
+      const int2 kk = s.kqr[key];
+      s.kkey[key] = kk.x * XW + kk.y + XD * XW + XD;
+    }
   }
   __syncthreads();
 
@@ -258,12 +436,15 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     qi.qtok = qi.query < nt;
     qi.qq = 0;
     qi.qr = 0;
+    qi.qkey = 0;
     if (!PAIR) {
       const int2 qc = s.kqr[qi.query];
-      qi.qq = qc.x;
-      qi.qr = qc.y;
+      qi.qq = qi.qv ? qc.x : safe_q;
+      qi.qr = qi.qv ? qc.y : safe_r;
+      qi.qkey = qi.qq * XW + qi.qr;
     }
-    const bool qgen = qb * 16 < nt;  // wave-uniform
+    // token or dead queries in this block: general path (wave-uniform)
+    const bool qgen = q_gen[qb] != 0;
     u32x2 qf[HG][KD];
 #pragma unroll
     for (int h = 0; h < HG; ++h)
@@ -282,28 +463,38 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
       for (int kd = 0; kd < KD; ++kd) o[h][kd] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
+#define SHRIMP_CHUNK(NB, P) \
+  attn_chunk<DP, HG, PAIR, NB, P>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, qf, m, l, o)
     int kb = 0;
     while (kb < nkb) {
-      if (nkb - kb >= 4) {
-        const bool gen = qgen || (s.blk_gen[kb] | s.blk_gen[kb + 1] | s.blk_gen[kb + 2] |
-                                  s.blk_gen[kb + 3]);
-        if (gen)
-          attn_chunk<DP, HG, PAIR, 4, true>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, qf, m, l, o);
-        else
-          attn_chunk<DP, HG, PAIR, 4, false>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, qf, m, l, o);
-        kb += 4;
-      } else {
-        if (qgen || s.blk_gen[kb])
-          attn_chunk<DP, HG, PAIR, 1, true>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, qf, m, l, o);
-        else
-          attn_chunk<DP, HG, PAIR, 1, false>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, qf, m, l, o);
+      if (qgen || s.blk_gen[kb]) {
+        SHRIMP_CHUNK(1, PATH_GENERAL);
         kb += 1;
+        continue;
       }
+      int run = 1;  // consecutive fast blocks starting at kb (up to 4)
+      while (run < 4 && kb + run < nkb && !s.blk_gen[kb + run]) ++run;
+      if (PAIR) {
+        if (run == 4) SHRIMP_CHUNK(4, PATH_CLAMP);
+        else if (run >= 2) SHRIMP_CHUNK(2, PATH_CLAMP);
+        else SHRIMP_CHUNK(1, PATH_CLAMP);
+      } else if (linear_ok) {
+        if (run == 4) SHRIMP_CHUNK(4, PATH_LINEAR);
+        else if (run >= 2) SHRIMP_CHUNK(2, PATH_LINEAR);
+        else SHRIMP_CHUNK(1, PATH_LINEAR);
+      } else {
+        if (run == 4) SHRIMP_CHUNK(4, PATH_CLAMP);
+        else if (run >= 2) SHRIMP_CHUNK(2, PATH_CLAMP);
+        else SHRIMP_CHUNK(1, PATH_CLAMP);
+      }
+      kb += run == 4 ? 4 : (run >= 2 ? 2 : 1);
     }
+#undef SHRIMP_CHUNK
 
 #pragma unroll
     for (int h = 0; h < HG; ++h) {
-      const float lt = sum_lane_groups(l[h]);
+      // the row sum sits in lane group 0; broadcast it to the query's lanes
+      const float lt = __shfl(l[h], lr, 64);
       const float inv = lt > 0.f ? 1.0f / lt : 0.f;
       if (!qi.qv) continue;
       unsigned short* orow = static_cast<unsigned short*>(a.o) + (int64_t)b * a.o_sb +
@@ -334,16 +525,17 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   }
 }
 
-static size_t attn_smem_bytes(int DP, int HG, int S, int npos) {
-  const int SP = (S + 15) & ~15;
-  return (size_t)2 * HG * SP * DP * 2 + (size_t)SP * (8 + 4) + (size_t)(SP / 16) * 4 +
-         (size_t)npos * HG * 4;
+// LDS bytes of one workgroup; npos = pair-table rows (pair mode only).
+static size_t attn_smem_bytes(int DP, int HG, int S, int npos, bool pair) {
+  const size_t SP = (size_t)((S + 15) & ~15);
+  size_t bytes = 2 * HG * SP * DP * 2 + SP * (8 + 4 + 4) + (SP / 16) * 8;
+  bytes += pair ? (size_t)npos * HG * 4 : (size_t)XW * XW * HG * 2;
+  return bytes;
 }
 
 template <int DP, int HG, bool PAIR>
 static int launch_attn(const shrimp_attn_args* a, float qk_scale, uint32_t qkv_bytes, int npos,
-                       hipStream_t st) {
-  const size_t smem = attn_smem_bytes(DP, HG, a->S, npos);
+                       size_t smem, hipStream_t st) {
   dim3 grid(a->H / HG, a->B);
   hipLaunchKernelGGL((attn_kernel<DP, HG, PAIR>), grid, dim3(256), smem, st, *a, qk_scale,
                      qkv_bytes, npos);
@@ -355,14 +547,15 @@ static const size_t kAttnSmemCap = 64 * 1024;
 
 template <bool PAIR>
 static int dispatch_attn(const shrimp_attn_args* a, float qk_scale, uint32_t qkv_bytes, int npos,
-                         hipStream_t st) {
-#define SHRIMP_ATTN_DP(DPV)                                                          \
-  if (a->dpad == DPV) {                                                              \
-    if (a->H % 2 == 0 && attn_smem_bytes(DPV, 2, a->S, npos) <= kAttnSmemCap)        \
-      return launch_attn<DPV, 2, PAIR>(a, qk_scale, qkv_bytes, npos, st);            \
-    if (attn_smem_bytes(DPV, 1, a->S, npos) <= kAttnSmemCap)                          \
-      return launch_attn<DPV, 1, PAIR>(a, qk_scale, qkv_bytes, npos, st);            \
-    return set_error(SHRIMP_EINVAL, "attn: sequence %d too long for LDS staging", a->S); \
+                         int tab_rows, hipStream_t st) {
+#define SHRIMP_ATTN_DP(DPV)                                                                \
+  if (a->dpad == DPV) {                                                                    \
+    const size_t s2 = attn_smem_bytes(DPV, 2, a->S, tab_rows, PAIR);                       \
+    const size_t s1 = attn_smem_bytes(DPV, 1, a->S, tab_rows, PAIR);                       \
+    if (a->H % 2 == 0 && s2 <= kAttnSmemCap)                                               \
+      return launch_attn<DPV, 2, PAIR>(a, qk_scale, qkv_bytes, npos, s2, st);             \
+    if (s1 <= kAttnSmemCap) return launch_attn<DPV, 1, PAIR>(a, qk_scale, qkv_bytes, npos, s1, st); \
+    return set_error(SHRIMP_EINVAL, "attn: sequence %d too long for LDS staging", a->S);   \
   }
   SHRIMP_ATTN_DP(16)
   SHRIMP_ATTN_DP(32)
@@ -386,13 +579,29 @@ __global__ void attn_bias_table_kernel(const float* __restrict__ table, int tabl
   btab[i] = table[row * H + h] * SHRIMP_LOG2E;
 }
 
+// xtab[x, h] = fp16(btab[clamped LUT position of (dq, dr), h]), x over the
+// unclamped (2 XD + 1)^2 offsets.
+__global__ void attn_xtab_kernel(const float* __restrict__ btab, int H, int M,
+                                 unsigned short* __restrict__ xtab) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= XW * XW * H) return;
+  const int x = i / H;
+  const int h = i - x * H;
+  const int dq = x / XW - XD;
+  const int dr = x - (x / XW) * XW - XD;
+  const int W = 2 * M + 1;
+  const int pos = (clampi(dq, M) + M) * W + (clampi(dr, M) + M);
+  xtab[i] = __builtin_bit_cast(unsigned short, (_Float16)btab[pos * H + h]);
+}
+
 }  // namespace shrimp
 
 using namespace shrimp;
 
 extern "C" int shrimp_attn_bias_table(const float* table, int table_rows, int H,
                                       const uint8_t* lut, int lut_m, int tok_row_ct,
-                                      int tok_row_tc, int tok_row_tt, float* btab, void* stream) {
+                                      int tok_row_tc, int tok_row_tt, float* btab, void* xtab,
+                                      void* stream) {
   SHRIMP_REQUIRE(table && lut && btab, "attn_bias_table: null pointer");
   SHRIMP_REQUIRE(table_rows > 0 && H > 0 && lut_m >= 0, "attn_bias_table: bad sizes");
   const int w = 2 * lut_m + 1;
@@ -400,6 +609,11 @@ extern "C" int shrimp_attn_bias_table(const float* table, int table_rows, int H,
   hipLaunchKernelGGL(attn_bias_table_kernel, dim3((total + 255) / 256), dim3(256), 0,
                      as_stream(stream), table, table_rows, H, lut, w * w, tok_row_ct, tok_row_tc,
                      tok_row_tt, btab);
+  if (xtab != nullptr) {
+    const int nx = XW * XW * H;
+    hipLaunchKernelGGL(attn_xtab_kernel, dim3((nx + 255) / 256), dim3(256), 0, as_stream(stream),
+                       btab, H, lut_m, static_cast<unsigned short*>(xtab));
+  }
   return check_launch("attn_bias_table");
 }
 
@@ -420,10 +634,11 @@ extern "C" int shrimp_attn(const shrimp_attn_args* a, void* stream) {
   hipStream_t st = as_stream(stream);
   if (a->pair != nullptr) {
     SHRIMP_REQUIRE(a->table2 && a->table_rows > 0, "attn: pair mode needs table2");
-    return dispatch_attn<true>(a, qk_scale, (uint32_t)(extent * 2), a->table_rows, st);
+    return dispatch_attn<true>(a, qk_scale, (uint32_t)(extent * 2), a->table_rows,
+                               a->table_rows, st);
   }
-  SHRIMP_REQUIRE(a->btab && a->lut_m >= 0, "attn: coords mode needs btab");
+  SHRIMP_REQUIRE(a->btab && a->lut_m >= 0 && a->lut_m <= 64, "attn: coords mode needs btab");
   SHRIMP_REQUIRE(a->n_tokens == a->S || (a->coords && a->mask), "attn: coords mode needs coords and mask");
   const int w = 2 * a->lut_m + 1;
-  return dispatch_attn<false>(a, qk_scale, (uint32_t)(extent * 2), w * w + 3, st);
+  return dispatch_attn<false>(a, qk_scale, (uint32_t)(extent * 2), w * w + 3, w * w, st);
 }

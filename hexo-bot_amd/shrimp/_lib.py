@@ -53,7 +53,8 @@ class AttnArgs(ctypes.Structure):
         ("q", _vp), ("k", _vp), ("v", _vp), ("qkv_sb", _i64), ("qkv_sh", _i64),
         ("seq_lens", _vp),
         ("pair", _vp), ("p_sb", _i64), ("p_sq", _i64), ("table2", _vp), ("table_rows", _i32),
-        ("coords", _vp), ("mask", _vp), ("btab", _vp), ("lut_m", _i32), ("n_tokens", _i32),
+        ("coords", _vp), ("mask", _vp), ("btab", _vp), ("xtab", _vp), ("lut_m", _i32),
+        ("n_tokens", _i32),
         ("o", _vp), ("o_sb", _i64), ("o_sh", _i64), ("o_sr", _i64),
         ("B", _i32), ("S", _i32), ("H", _i32), ("d", _i32), ("dpad", _i32),
     ]
@@ -83,7 +84,7 @@ SIGNATURES: dict = {
     "shrimp_attn": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _vp]),
     "shrimp_attn_bias_table": (
         ctypes.c_int,
-        [_vp, ctypes.c_int, ctypes.c_int, _vp] + [ctypes.c_int] * 4 + [_vp, _vp],
+        [_vp, ctypes.c_int, ctypes.c_int, _vp] + [ctypes.c_int] * 4 + [_vp, _vp, _vp],
     ),
     "shrimp_prep_inputs": (
         ctypes.c_int,

@@ -72,24 +72,30 @@ def pack_linear_weight(weight: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def attn_bias_table(table: torch.Tensor, lut_u8: torch.Tensor, lut_m: int = CELL_LUT_M) -> torch.Tensor:
-    """Per-block (BIAS_ROWS, H) table -> ((2M+1)^2 + 3, H) fp32 LUT-indexed
-    table with log2(e) folded in (the layout the coords-mode kernel reads)."""
+ATTN_XD = 26  # SHRIMP_ATTN_XD of the C ABI
+
+
+def attn_bias_table(table: torch.Tensor, lut_u8: torch.Tensor, lut_m: int = CELL_LUT_M):
+    """Per-block (BIAS_ROWS, H) table -> (btab, xtab): btab ((2M+1)^2 + 3, H)
+    fp32, the LUT-indexed table with log2(e) folded in; xtab ((2 XD + 1)^2, H)
+    fp16, the same values indexed by unclamped offsets (|dq|, |dr| <= XD)."""
 
     require_device(table, "attn_bias_table")
     rows, h = table.shape
     w = 2 * lut_m + 1
+    xw = 2 * ATTN_XD + 1
     t32 = table.detach().to(torch.float32).contiguous()
-    out = torch.empty((w * w + 3, h), dtype=torch.float32, device=table.device)
+    btab = torch.empty((w * w + 3, h), dtype=torch.float32, device=table.device)
+    xtab = torch.empty((xw * xw, h), dtype=torch.float16, device=table.device)
     _lib.check(
         _lib.load().shrimp_attn_bias_table(
             t32.data_ptr(), rows, h, lut_u8.data_ptr(), lut_m, BIAS_CELL_TOKEN_ROW,
-            BIAS_TOKEN_CELL_ROW, BIAS_TOKEN_TOKEN_ROW, out.data_ptr(),
+            BIAS_TOKEN_CELL_ROW, BIAS_TOKEN_TOKEN_ROW, btab.data_ptr(), xtab.data_ptr(),
             _lib.stream_handle(table.device),
         ),
         "attn_bias_table",
     )
-    return out
+    return btab, xtab
 
 
 # ---- raw launches ----------------------------------------------------------------------
@@ -129,14 +135,15 @@ def launch_linear(
 
 def launch_attn(
     *, q, k, v, qkv_sb, qkv_sh, seq_lens, o, o_sb, o_sh, o_sr, B, S, H, d, dpad,
-    pair=None, p_sb=0, p_sq=0, table2=None, coords=None, mask8=None, btab=None,
+    pair=None, p_sb=0, p_sq=0, table2=None, coords=None, mask8=None, btab=None, xtab=None,
     lut_m=CELL_LUT_M, n_tokens=NUM_TOKENS, stream=None,
 ):
     a = _lib.AttnArgs(
         q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), qkv_sb=qkv_sb, qkv_sh=qkv_sh,
         seq_lens=seq_lens.data_ptr(), pair=_lib.ptr(pair), p_sb=p_sb, p_sq=p_sq,
         table2=_lib.ptr(table2), table_rows=0 if table2 is None else int(table2.shape[0]),
-        coords=_lib.ptr(coords), mask=_lib.ptr(mask8), btab=_lib.ptr(btab), lut_m=lut_m,
+        coords=_lib.ptr(coords), mask=_lib.ptr(mask8), btab=_lib.ptr(btab),
+        xtab=_lib.ptr(xtab), lut_m=lut_m,
         n_tokens=n_tokens, o=o.data_ptr(), o_sb=o_sb, o_sh=o_sh, o_sr=o_sr,
         B=B, S=S, H=H, d=d, dpad=dpad,
     )

@@ -69,6 +69,9 @@ class HipForward:
         # ``self.last`` (used to re-launch single kernels for timing).
         self.keep_buffers = False
         self.last = None
+        # The unclamped offset table lets the attention kernel index biases
+        # linearly for compact positions; off forces the clamped LUT path.
+        self.use_linear_bias = True
 
     def invalidate(self) -> None:
         self._packed = None
@@ -136,7 +139,8 @@ class HipForward:
                     fc1_w=lin_w(blk.fc1), fc1_b=f32(blk.fc1.bias),
                     fc2_w=lin_w(blk.fc2), fc2_b=f32(blk.fc2.bias),
                     g_attn=f32(blk.ls_attn.gamma), g_mlp=f32(blk.ls_mlp.gamma),
-                    btab=attn_bias_table(net.bias_tables[i].detach().to(device), lut, CELL_LUT_M),
+                    btab_xtab=attn_bias_table(net.bias_tables[i].detach().to(device), lut,
+                                              CELL_LUT_M),
                 )
             )
         P.tokens = f32(net.tokens)
@@ -240,7 +244,8 @@ class HipForward:
                 launch_attn(
                     q=qkv[0], k=qkv[1], v=qkv[2], qkv_sb=H * S * dpad, qkv_sh=S * dpad,
                     seq_lens=seq_lens, o=att, o_sb=S * C, o_sh=d, o_sr=C, B=B, S=S, H=H, d=d,
-                    dpad=dpad, coords=coords32, mask8=mask8, btab=a.btab, lut_m=CELL_LUT_M,
+                    dpad=dpad, coords=coords32, mask8=mask8, btab=a.btab_xtab[0],
+                    xtab=a.btab_xtab[1] if self.use_linear_bias else None, lut_m=CELL_LUT_M,
                     n_tokens=NUM_TOKENS, stream=st,
                 )
                 launch_linear(

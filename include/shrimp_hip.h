@@ -160,6 +160,9 @@ int shrimp_linear(const shrimp_linear_args* a, void* stream);
  *       btab rows (2M+1)^2 .. +2 hold (cell q, token k), (token q, cell k),
  *       (token q, token k); keys whose mask is 0 get weight exactly 0.
  *   btab is produced by shrimp_attn_bias_table (with log2(e) folded in).
+ *   xtab (optional, same source): the LUT re-indexed without clamping over
+ *       |dq|, |dr| <= SHRIMP_ATTN_XD, fp16 [(2 XD + 1)^2][H]; positions whose
+ *       live cells span <= XD in q and r then index it linearly.
  * q, k, v: (B, H, S, dpad) bf16 with head-dim zero padding; o element
  * (b, h, s, e) at o[b*o_sb + h*o_sh + s*o_sr + e], e < d (o_sh = d, o_sr = C
  * gives the (B, S, C) layout out_proj reads; o_sh = S*d, o_sr = d gives
@@ -180,6 +183,7 @@ typedef struct {
   const int32_t* coords; /* (B, S - n_tokens, 2) */
   const uint8_t* mask;   /* (B, S - n_tokens) */
   const float* btab;     /* ((2M+1)^2 + 3, H), log2e folded */
+  const void* xtab;      /* ((2 XD + 1)^2, H) fp16, log2e folded, or NULL */
   int32_t lut_m, n_tokens;
   void* o;
   int64_t o_sb, o_sh, o_sr;
@@ -188,11 +192,15 @@ typedef struct {
 
 int shrimp_attn(const shrimp_attn_args* a, void* stream);
 
+#define SHRIMP_ATTN_XD 26
+
 /* btab[pos, h] = log2(e) * table[lut[pos], h] for pos < (2M+1)^2 and the 3
- * token rows from table rows tok_rows[0..2]; table (rows, H) fp32. */
+ * token rows from table rows tok_rows[0..2]; table (rows, H) fp32.
+ * xtab (if not NULL) [x, h] = fp16(btab[clamped pos of (dq, dr)], h) with
+ * x = (dq + XD) * (2 XD + 1) + dr + XD. */
 int shrimp_attn_bias_table(const float* table, int table_rows, int H, const uint8_t* lut,
                            int lut_m, int tok_row_ct, int tok_row_tc, int tok_row_tt,
-                           float* btab, void* stream);
+                           float* btab, void* xtab, void* stream);
 
 /* ------------------------------------------------------------------------
  * Index preparation (model.py:861-863, 884-892, 905; batching.py:264-276):

@@ -33,7 +33,7 @@ int main(void) {
   F(shrimp_attn_args, qkv_sb); F(shrimp_attn_args, qkv_sh); F(shrimp_attn_args, seq_lens);
   F(shrimp_attn_args, pair); F(shrimp_attn_args, p_sb); F(shrimp_attn_args, p_sq);
   F(shrimp_attn_args, table2); F(shrimp_attn_args, table_rows); F(shrimp_attn_args, coords);
-  F(shrimp_attn_args, mask); F(shrimp_attn_args, btab); F(shrimp_attn_args, lut_m);
+  F(shrimp_attn_args, mask); F(shrimp_attn_args, btab); F(shrimp_attn_args, xtab); F(shrimp_attn_args, lut_m);
   F(shrimp_attn_args, n_tokens); F(shrimp_attn_args, o); F(shrimp_attn_args, o_sb);
   F(shrimp_attn_args, o_sh); F(shrimp_attn_args, o_sr); F(shrimp_attn_args, B);
   F(shrimp_attn_args, S); F(shrimp_attn_args, H); F(shrimp_attn_args, d);

@@ -84,6 +84,22 @@ def test_forward_feature_and_index_dtypes(cfg4_batch):
     assert (a["policy"] - c["policy"]).abs().max().item() <= TOL
 
 
+def test_linear_and_clamped_bias_paths_agree(cfg4_batch):
+    """The attention kernel's unclamped-table path (compact positions) and its
+    clamped-LUT path give the same forward up to fp16-vs-fp32 table rounding."""
+
+    b = cfg4_batch
+    net = _net(128, 8, "CCACCACCACCA", seed=5)
+    lin = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+    net.hip_runtime().use_linear_bias = False
+    try:
+        clamp = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+    finally:
+        net.hip_runtime().use_linear_bias = True
+    for key in ("policy", "value"):
+        assert (lin[key] - clamp[key]).abs().max().item() <= 1e-2, key
+
+
 def test_rows_are_independent_of_batch(cfg4_batch):
     """padded == single-row (tests/test_shrimp_model.py:139-164): a row's
     outputs do not depend on the rest of the batch (bit-exact here)."""
