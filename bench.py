@@ -87,10 +87,42 @@ def kernel_timings(net, inputs, reps=50):
             lut_m=CELL_LUT_M, n_tokens=8, stream=L["stream"],
         )
 
+    from shrimp import _lib
+
+    rows = b * s
+    seq, hid = L["seq"], L["hid"]
+
+    def lin(mode, x, x_sr, w, bias, n_in, n_out, out, o_sr, **kw):
+        return lambda: ops.launch_linear(
+            x=x, x_sr=x_sr, wpack=w, bias=bias, rows=rows, n_in=n_in, n_out=n_out, mode=mode,
+            out=out, o_sr=o_sr, stream=L["stream"], **kw)
+
+    # Timing re-launches write into the forward's scratch buffers only (never
+    # back into seq): residual modes target a copy.
+    seq_copy = seq.clone()
+    linears = {
+        "qkv": (lin(_lib.LIN_QKV, seq, C, a.qkv_w, a.qkv_b, C, 3 * C, qkv[0], 0, ln_w=a.ln1w,
+                    ln_b=a.ln1b, B=b, S=s, H=H, dpad=P.dpad), rows * C * 3 * C * 2.0,
+                rows * (C + 3 * C) * 2.0),
+        "out_proj": (lin(_lib.LIN_RESID, L["att"], C, a.out_w, a.out_b, C, C, seq_copy, C,
+                         resid=seq_copy, r_sr=C, gamma=a.g_attn, mask=L["seq_mask"]),
+                     rows * C * C * 2.0, rows * 3 * C * 2.0),
+        "fc1": (lin(_lib.LIN_GELU, seq, C, a.fc1_w, a.fc1_b, C, 2 * C, hid, 2 * C, ln_w=a.ln2w,
+                    ln_b=a.ln2b), rows * C * 2 * C * 2.0, rows * 3 * C * 2.0),
+        "fc2": (lin(_lib.LIN_RESID, hid, 2 * C, a.fc2_w, a.fc2_b, 2 * C, C, seq_copy, C,
+                    resid=seq_copy, r_sr=C, gamma=a.g_mlp, mask=L["seq_mask"]),
+                rows * 2 * C * C * 2.0, rows * 4 * C * 2.0),
+    }
     conv()
     attn()
     conv_ms = _events_time(conv, reps, stream)
     attn_ms = _events_time(attn, reps, stream)
+    extra = {}
+    for name, (fn, flops, nbytes) in linears.items():
+        fn()
+        ms = _events_time(fn, reps, stream)
+        extra[name] = {"ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                       "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
     seq_lens = L["seq_lens"].cpu().to(torch.float64)
     valid_rows = int(L["mask8"].sum().item())
     return {
@@ -101,6 +133,7 @@ def kernel_timings(net, inputs, reps=50):
         "attn_ms": attn_ms,
         "attn_flops": float(4 * P.d * H * (seq_lens ** 2).sum().item()),
         "attn_bytes": float(4 * 2 * P.d * H * seq_lens.sum().item()),
+        "linears": extra,
     }
 
 
@@ -221,6 +254,7 @@ def main() -> int:
             "mfma_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
             "hbm_gbs_algorithmic": round(kt["attn_bytes"] / (kt["attn_ms"] * 1e-3) / 1e9, 1),
         },
+        "linears_block0": kt["linears"],
         "forward_tflops_padded": round(1.425e9 * B / (ms * 1e-3) / 1e12, 2),
     }
     if not args.no_cpu:

@@ -89,94 +89,153 @@ __global__ void fill_tokens_kernel(const float* __restrict__ tokens, int n_token
 }
 
 // ---- trunk tail + value heads (model.py:927-935, 990-1002) --------------------
-// Dynamic LDS: vin[3C] (value input), mlin[3C] (moves-left input), hid[C].
-__global__ __launch_bounds__(256) void tail_kernel(const shrimp_tail_args a) {
-  extern __shared__ float sm[];
-  const int C = a.C;
-  float* vin = sm;            // [T0 | T1 | pooled]
-  float* mlin = sm + 3 * C;   // [T4 | T5 | pooled]
-  float* hid = sm + 6 * C;    // [C]
-  float* pool = sm + 7 * C;   // [4][C] per-wave partial sums
+// Pass 1, one workgroup per position: final LayerNorm of every row (cells
+// masked), written to out_seq; the value-head inputs [T0 | T1 | pooled] and
+// [T4 | T5 | pooled] go to the workspace (B, 6C) fp32. Each wave keeps four
+// rows in flight; a lane owns channel pairs (2 lane + 128 u, +1).
+__global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a) {
+  __shared__ float pool_w[4][256];
   __shared__ int cnt_w[4];
   const int b = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int S = a.S, nt = a.n_tokens, N = S - nt;
+  const int C = a.C, S = a.S, nt = a.n_tokens, N = S - nt;
   const uint16_t* seq = static_cast<const uint16_t*>(a.seq) + (int64_t)b * a.s_sb;
   uint16_t* outs = static_cast<uint16_t*>(a.out_seq) + (int64_t)b * a.s_sb;
-  // C <= 256: each lane owns channels lane + 64u, u < 4 (fully unrolled so
-  // the per-lane arrays stay in registers).
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float* vin = a.workspace + (int64_t)b * 6 * C;
+  float lw[2][2], lb[2][2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int c = 2 * lane + 128 * u + e;
+      lw[u][e] = c < C ? a.ln_w[c] : 0.f;
+      lb[u][e] = c < C ? a.ln_b[c] : 0.f;
+    }
+  float acc[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
   int cnt = 0;
-  for (int row = wave; row < S; row += 4) {
-    float x[4];
-    float s = 0.f;
+  for (int row0 = wave * 4; row0 < S; row0 += 16) {
+    unsigned raw[4][2];
+    bool live[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = lane + 64 * u;
-      x[u] = c < C ? bf16_bits_to_f32(seq[(int64_t)row * C + c]) : 0.f;
-      s += x[u];
+    for (int r = 0; r < 4; ++r) {
+      const int row = row0 + r;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int c = 2 * lane + 128 * u;
+        raw[r][u] = (row < S && c < C)
+                        ? *reinterpret_cast<const unsigned*>(seq + (int64_t)row * C + c)
+                        : 0u;
+      }
+      live[r] = row < S && (row < nt || a.mask[(int64_t)b * N + (row - nt)] != 0);
     }
-    const float mean = wave_sum(s) / C;
-    float q = 0.f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = lane + 64 * u;
-      x[u] = c < C ? x[u] - mean : 0.f;
-      q += x[u] * x[u];
-    }
-    const float rstd = rsqrtf(wave_sum(q) / C + a.eps);
-    const bool is_cell = row >= nt;
-    const bool live = !is_cell || a.mask[(int64_t)b * N + (row - nt)] != 0;
-    if (is_cell && live) ++cnt;
+    for (int r = 0; r < 4; ++r) {
+      const int row = row0 + r;
+      if (row >= S) break;  // wave-uniform
+      float x[2][2];
+      float sum = 0.f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = lane + 64 * u;
-      if (c >= C) continue;
-      float y = x[u] * rstd * a.ln_w[c] + a.ln_b[c];
-      if (!live) y = 0.f;
-      outs[(int64_t)row * C + c] = f32_to_bf16_bits(y);
-      if (is_cell) acc[u] += y;
-      if (row == 0) vin[c] = y;
-      if (row == 1) vin[C + c] = y;
-      if (row == 4) mlin[c] = y;
-      if (row == 5) mlin[C + c] = y;
+      for (int u = 0; u < 2; ++u) {
+        x[u][0] = bf16_lo(raw[r][u]);
+        x[u][1] = bf16_hi(raw[r][u]);
+        sum += x[u][0] + x[u][1];
+      }
+      const float mean = wave_sum(sum) / C;
+      float q = 0.f;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int c = 2 * lane + 128 * u + e;
+          x[u][e] = c < C ? x[u][e] - mean : 0.f;
+          q += x[u][e] * x[u][e];
+        }
+      const float rstd = rsqrtf(wave_sum(q) / C + a.eps);
+      const bool is_cell = row >= nt;
+      if (is_cell && live[r]) ++cnt;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int c = 2 * lane + 128 * u;
+        if (c >= C) continue;
+        float y0 = x[u][0] * rstd * lw[u][0] + lb[u][0];
+        float y1 = x[u][1] * rstd * lw[u][1] + lb[u][1];
+        if (!live[r]) y0 = y1 = 0.f;
+        *reinterpret_cast<unsigned*>(outs + (int64_t)row * C + c) = pack_bf16x2(y0, y1);
+        if (is_cell) {
+          acc[u][0] += y0;
+          acc[u][1] += y1;
+        }
+        // token rows 0, 1 feed the value head, rows 4, 5 the moves-left head
+        const int slot = row == 0 ? 0 : row == 1 ? 1 : row == 4 ? 3 : row == 5 ? 4 : -1;
+        if (slot >= 0) {
+          vin[slot * C + c] = y0;
+          vin[slot * C + c + 1] = y1;
+        }
+      }
     }
   }
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int c = lane + 64 * u;
-    if (c < C) pool[wave * C + c] = acc[u];
-  }
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int c = 2 * lane + 128 * u + e;
+      if (c < C) pool_w[wave][c] = acc[u][e];
+    }
   if (lane == 0) cnt_w[wave] = cnt;
   __syncthreads();
-  const int count = max(1, cnt_w[0] + cnt_w[1] + cnt_w[2] + cnt_w[3]);
+  const float inv = 1.0f / (float)max(1, cnt_w[0] + cnt_w[1] + cnt_w[2] + cnt_w[3]);
   for (int c = threadIdx.x; c < C; c += blockDim.x) {
-    const float p = (pool[c] + pool[C + c] + pool[2 * C + c] + pool[3 * C + c]) / (float)count;
+    const float p = (pool_w[0][c] + pool_w[1][c] + pool_w[2][c] + pool_w[3][c]) * inv;
     vin[2 * C + c] = p;
-    mlin[2 * C + c] = p;
+    vin[5 * C + c] = p;
   }
-  __syncthreads();
-  // value_reduction (C x 3C) + ReLU, then value_head (bins x C)
+}
+
+// Pass 2: value / moves-left heads for 4 positions per workgroup; weights are
+// transposed (k-major) so a wave's weight load covers 64 consecutive outputs.
+constexpr int kHeadPos = 4;
+__global__ __launch_bounds__(256) void value_head_kernel(const shrimp_tail_args a) {
+  extern __shared__ float hs[];
+  const int C = a.C, bins = a.bins;
+  float* in = hs;                   // [kHeadPos][3C]
+  float* hid = hs + kHeadPos * 3 * C;  // [kHeadPos][C]
+  const int b0 = blockIdx.x * kHeadPos;
+  const int np = min(kHeadPos, a.B - b0);
   for (int pass = 0; pass < 2; ++pass) {
-    const float* rw = pass == 0 ? a.vr_w : a.mr_w;
+    const float* rwt = pass == 0 ? a.vr_w : a.mr_w;
     const float* rb = pass == 0 ? a.vr_b : a.mr_b;
-    const float* hw = pass == 0 ? a.vh_w : a.mh_w;
+    const float* hwt = pass == 0 ? a.vh_w : a.mh_w;
     const float* hb = pass == 0 ? a.vh_b : a.mh_b;
     float* dst = pass == 0 ? a.value : a.moves_left;
-    const float* in = pass == 0 ? vin : mlin;
-    if (dst == nullptr) continue;
-    for (int o = wave; o < C; o += 4) {
-      float s = 0.f;
-      for (int k = lane; k < 3 * C; k += 64) s += rw[(int64_t)o * 3 * C + k] * in[k];
-      s = wave_sum(s);
-      if (lane == 0) hid[o] = fmaxf(s + rb[o], 0.f);
+    if (dst == nullptr) continue;  // uniform
+    for (int i = threadIdx.x; i < kHeadPos * 3 * C; i += blockDim.x) {
+      const int p = i / (3 * C), k = i - p * 3 * C;
+      in[i] = p < np ? a.workspace[(int64_t)(b0 + p) * 6 * C + pass * 3 * C + k] : 0.f;
     }
     __syncthreads();
-    for (int o = wave; o < a.bins; o += 4) {
-      float s = 0.f;
-      for (int k = lane; k < C; k += 64) s += hw[(int64_t)o * C + k] * hid[k];
-      s = wave_sum(s);
-      if (lane == 0) dst[(int64_t)b * a.bins + o] = s + hb[o];
+    for (int o = threadIdx.x; o < C; o += blockDim.x) {
+      float s[kHeadPos] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+      for (int k = 0; k < 3 * C; ++k) {
+        const float w = rwt[(int64_t)k * C + o];
+#pragma unroll
+        for (int p = 0; p < kHeadPos; ++p) s[p] += w * in[p * 3 * C + k];
+      }
+#pragma unroll
+      for (int p = 0; p < kHeadPos; ++p) hid[p * C + o] = fmaxf(s[p] + rb[o], 0.f);
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < bins; o += blockDim.x) {
+      float s[kHeadPos] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+      for (int k = 0; k < C; ++k) {
+        const float w = hwt[(int64_t)k * bins + o];
+#pragma unroll
+        for (int p = 0; p < kHeadPos; ++p) s[p] += w * hid[p * C + k];
+      }
+#pragma unroll
+      for (int p = 0; p < kHeadPos; ++p)
+        if (p < np) dst[(int64_t)(b0 + p) * bins + o] = s[p] + hb[o];
     }
     __syncthreads();
   }
@@ -377,15 +436,23 @@ extern "C" int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void
 extern "C" int shrimp_trunk_tail(const shrimp_tail_args* a, void* stream) {
   SHRIMP_REQUIRE(a != nullptr, "trunk_tail: null args");
   if (a->B == 0) return SHRIMP_OK;
-  SHRIMP_REQUIRE(a->seq && a->mask && a->ln_w && a->ln_b && a->out_seq, "trunk_tail: null pointer");
-  SHRIMP_REQUIRE(a->C > 0 && a->C <= 256, "trunk_tail: C %d outside (0, 256]", a->C);
+  SHRIMP_REQUIRE(a->seq && a->mask && a->ln_w && a->ln_b && a->out_seq && a->workspace,
+                 "trunk_tail: null pointer");
+  SHRIMP_REQUIRE(a->C > 0 && a->C <= 256 && a->C % 2 == 0, "trunk_tail: C %d outside (0, 256]",
+                 a->C);
+  SHRIMP_REQUIRE(a->s_sb % 2 == 0, "trunk_tail: position stride must be even");
   SHRIMP_REQUIRE(a->n_tokens >= 6 && a->S > a->n_tokens, "trunk_tail: needs >= 6 tokens");
   SHRIMP_REQUIRE(!a->value || (a->vr_w && a->vr_b && a->vh_w && a->vh_b), "trunk_tail: value head");
   SHRIMP_REQUIRE(!a->moves_left || (a->mr_w && a->mr_b && a->mh_w && a->mh_b),
                  "trunk_tail: moves-left head");
-  const size_t smem = (size_t)(7 * a->C + 4 * a->C) * sizeof(float);
-  hipLaunchKernelGGL(tail_kernel, dim3(a->B), dim3(256), smem, as_stream(stream), *a);
-  return check_launch("trunk_tail");
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(final_ln_kernel, dim3(a->B), dim3(256), 0, st, *a);
+  if (int rc = check_launch("trunk_tail/ln")) return rc;
+  if (!a->value && !a->moves_left) return SHRIMP_OK;
+  const size_t smem = (size_t)kHeadPos * 4 * a->C * sizeof(float);
+  hipLaunchKernelGGL(value_head_kernel, dim3((a->B + kHeadPos - 1) / kHeadPos), dim3(256), smem,
+                     st, *a);
+  return check_launch("trunk_tail/heads");
 }
 
 extern "C" int shrimp_decode(const float* value_logits, const float* ml_logits,

@@ -66,6 +66,7 @@ class TailArgs(ctypes.Structure):
         ("eps", _f32), ("out_seq", _vp),
         ("vr_w", _vp), ("vr_b", _vp), ("vh_w", _vp), ("vh_b", _vp), ("value", _vp),
         ("mr_w", _vp), ("mr_b", _vp), ("mh_w", _vp), ("mh_b", _vp), ("moves_left", _vp),
+        ("workspace", _vp),
         ("B", _i32), ("S", _i32), ("n_tokens", _i32), ("C", _i32), ("bins", _i32),
     ]
 

@@ -146,13 +146,14 @@ class HipForward:
         P.tokens = f32(net.tokens)
         P.lnf = SimpleNamespace(w=f32(net.ln_final.weight), b=f32(net.ln_final.bias),
                                 eps=net.ln_final.eps)
+        # head weights transposed (k-major) for the tail kernel
         P.value = SimpleNamespace(
-            rw=f32(net.value_reduction.weight), rb=f32(net.value_reduction.bias),
-            hw=f32(net.value_head.weight), hb=f32(net.value_head.bias),
+            rw=f32(net.value_reduction.weight.t()), rb=f32(net.value_reduction.bias),
+            hw=f32(net.value_head.weight.t()), hb=f32(net.value_head.bias),
         )
         P.ml = SimpleNamespace(
-            rw=f32(net.ml_reduction.weight), rb=f32(net.ml_reduction.bias),
-            hw=f32(net.moves_left_head.weight), hb=f32(net.moves_left_head.bias),
+            rw=f32(net.ml_reduction.weight.t()), rb=f32(net.ml_reduction.bias),
+            hw=f32(net.moves_left_head.weight.t()), hb=f32(net.moves_left_head.bias),
         )
         P.policy = SimpleNamespace(
             w=conv_w(net.policy_conv), b=f32(net.policy_conv.bias),
@@ -267,13 +268,14 @@ class HipForward:
         seqf = torch.empty((B, S, C), dtype=bf, device=dev)
         value = torch.empty((B, VALUE_BINS), dtype=torch.float32, device=dev)
         ml = torch.empty((B, VALUE_BINS), dtype=torch.float32, device=dev) if request_moves_left else None
+        tail_ws = torch.empty((B, 6 * C), dtype=torch.float32, device=dev)
         tail = _lib.TailArgs(
             seq=seq.data_ptr(), s_sb=S * C, mask=mask8.data_ptr(), ln_w=P.lnf.w.data_ptr(),
             ln_b=P.lnf.b.data_ptr(), eps=float(P.lnf.eps), out_seq=seqf.data_ptr(),
             vr_w=P.value.rw.data_ptr(), vr_b=P.value.rb.data_ptr(), vh_w=P.value.hw.data_ptr(),
             vh_b=P.value.hb.data_ptr(), value=value.data_ptr(),
             mr_w=P.ml.rw.data_ptr(), mr_b=P.ml.rb.data_ptr(), mh_w=P.ml.hw.data_ptr(),
-            mh_b=P.ml.hb.data_ptr(), moves_left=_lib.ptr(ml),
+            mh_b=P.ml.hb.data_ptr(), moves_left=_lib.ptr(ml), workspace=tail_ws.data_ptr(),
             B=B, S=S, n_tokens=NUM_TOKENS, C=C, bins=VALUE_BINS,
         )
         import ctypes

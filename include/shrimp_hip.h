@@ -228,8 +228,10 @@ int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void* seq, int6
  *   seq_f = LayerNorm(seq) (all S rows, fp32 stats), cell rows * mask -> out_seq (bf16)
  *   pooled = masked mean of the normalized cells (count clamped to 1)
  *   value = value_head(relu(value_reduction([T0, T1, pooled])))  -> value (B, 65) fp32
- *   moves_left likewise from [T4, T5, pooled] when ml_* are non-NULL.
- * Linear weights here are fp32 (out, in) as stored by nn.Linear.
+ *   moves_left likewise from [T4, T5, pooled] when moves_left is non-NULL.
+ * Head weights are fp32 and TRANSPOSED relative to nn.Linear.weight:
+ *   vr_w / mr_w (3C, C) = reduction.weight^T, vh_w / mh_w (C, bins) = head.weight^T.
+ * workspace: caller-provided (B, 6C) fp32 scratch (the head inputs).
  * ---------------------------------------------------------------------- */
 typedef struct {
   const void* seq; /* (B, S, C) bf16 */
@@ -239,12 +241,13 @@ typedef struct {
   const float* ln_b;
   float eps;
   void* out_seq; /* (B, S, C) bf16 */
-  const float* vr_w; const float* vr_b; /* (C, 3C), (C) */
-  const float* vh_w; const float* vh_b; /* (bins, C), (bins) */
+  const float* vr_w; const float* vr_b; /* (3C, C)^T layout, (C) */
+  const float* vh_w; const float* vh_b; /* (C, bins)^T layout, (bins) */
   float* value;                         /* (B, bins) */
   const float* mr_w; const float* mr_b;
   const float* mh_w; const float* mh_b;
   float* moves_left;
+  float* workspace; /* (B, 6C) */
   int32_t B, S, n_tokens, C, bins;
 } shrimp_tail_args;
 

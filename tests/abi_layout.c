@@ -44,7 +44,8 @@ int main(void) {
   F(shrimp_tail_args, out_seq); F(shrimp_tail_args, vr_w); F(shrimp_tail_args, vr_b);
   F(shrimp_tail_args, vh_w); F(shrimp_tail_args, vh_b); F(shrimp_tail_args, value);
   F(shrimp_tail_args, mr_w); F(shrimp_tail_args, mr_b); F(shrimp_tail_args, mh_w);
-  F(shrimp_tail_args, mh_b); F(shrimp_tail_args, moves_left); F(shrimp_tail_args, B);
+  F(shrimp_tail_args, mh_b); F(shrimp_tail_args, moves_left); F(shrimp_tail_args, workspace);
+  F(shrimp_tail_args, B);
   F(shrimp_tail_args, S); F(shrimp_tail_args, n_tokens); F(shrimp_tail_args, C);
   F(shrimp_tail_args, bins);
   return 0;
