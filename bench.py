@@ -176,6 +176,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run 5 plain device copies of this many MiB (the "
+                         "calibration kernel for HBM traffic counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -190,8 +193,17 @@ def main() -> int:
     from shrimp import _lib, synthetic
     from shrimp.model import ShrimpNet
 
-    _lib.load()
     dev = torch.device("cuda:0")
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib << 20
+        src = torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        print(json.dumps({"copy_probe_bytes": n, "reps": 5}), flush=True)
+        return 0
+    _lib.load()
     torch.manual_seed(0)
     net = ShrimpNet(channels=C, attention_heads=H, trunk_layout=LAYOUT).to(dev).eval()
     batch = synthetic.position_batch("cfg4", B)
