@@ -90,7 +90,7 @@ def kernel_timings(net, inputs, reps=50):
     from shrimp import _lib
 
     rows = b * s
-    seq, hid = L["seq"], L["hid"]
+    seq = L["seq"]
 
     def lin(mode, x, x_sr, w, bias, n_in, n_out, out, o_sr, **kw):
         return lambda: ops.launch_linear(
@@ -104,15 +104,27 @@ def kernel_timings(net, inputs, reps=50):
         "qkv": (lin(_lib.LIN_QKV, seq, C, a.qkv_w, a.qkv_b, C, 3 * C, qkv[0], 0, ln_w=a.ln1w,
                     ln_b=a.ln1b, B=b, S=s, H=H, dpad=P.dpad), rows * C * 3 * C * 2.0,
                 rows * (C + 3 * C) * 2.0),
-        "out_proj": (lin(_lib.LIN_RESID, L["att"], C, a.out_w, a.out_b, C, C, seq_copy, C,
-                         resid=seq_copy, r_sr=C, gamma=a.g_attn, mask=L["seq_mask"]),
-                     rows * C * C * 2.0, rows * 3 * C * 2.0),
-        "fc1": (lin(_lib.LIN_GELU, seq, C, a.fc1_w, a.fc1_b, C, 2 * C, hid, 2 * C, ln_w=a.ln2w,
-                    ln_b=a.ln2b), rows * C * 2 * C * 2.0, rows * 3 * C * 2.0),
-        "fc2": (lin(_lib.LIN_RESID, hid, 2 * C, a.fc2_w, a.fc2_b, 2 * C, C, seq_copy, C,
-                    resid=seq_copy, r_sr=C, gamma=a.g_mlp, mask=L["seq_mask"]),
-                rows * 2 * C * C * 2.0, rows * 4 * C * 2.0),
     }
+    if P.fused_mlp:
+        linears["attn_mlp"] = (
+            lambda: ops.launch_attn_mlp(
+                x=L["att"], x_sr=C, seq=seq_copy, s_sr=C, mask=L["seq_mask"], out_w=a.out_w,
+                out_b=a.out_b, g_attn=a.g_attn, ln_w=a.ln2w, ln_b=a.ln2b, eps=a.eps2,
+                fc1_w=a.fc1_w_il, fc1_b=a.fc1_b, fc2_w=a.fc2_w_il, fc2_b=a.fc2_b, g_mlp=a.g_mlp,
+                rows=rows, C=C, hidden=2 * C, stream=L["stream"]),
+            rows * (C * C + 4 * C * C) * 2.0, rows * 3 * C * 2.0)
+    else:
+        hid = L["hid"]
+        linears.update({
+            "out_proj": (lin(_lib.LIN_RESID, L["att"], C, a.out_w, a.out_b, C, C, seq_copy, C,
+                             resid=seq_copy, r_sr=C, gamma=a.g_attn, mask=L["seq_mask"]),
+                         rows * C * C * 2.0, rows * 3 * C * 2.0),
+            "fc1": (lin(_lib.LIN_GELU, seq, C, a.fc1_w, a.fc1_b, C, 2 * C, hid, 2 * C,
+                        ln_w=a.ln2w, ln_b=a.ln2b), rows * C * 2 * C * 2.0, rows * 3 * C * 2.0),
+            "fc2": (lin(_lib.LIN_RESID, hid, 2 * C, a.fc2_w, a.fc2_b, 2 * C, C, seq_copy, C,
+                        resid=seq_copy, r_sr=C, gamma=a.g_mlp, mask=L["seq_mask"]),
+                    rows * 2 * C * C * 2.0, rows * 4 * C * 2.0),
+        })
     conv()
     attn()
     conv_ms = _events_time(conv, reps, stream)
@@ -266,7 +278,7 @@ def main() -> int:
             "mfma_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
             "hbm_gbs_algorithmic": round(kt["attn_bytes"] / (kt["attn_ms"] * 1e-3) / 1e9, 1),
         },
-        "linears_block0": kt["linears"],
+        "block0_row_kernels": kt["linears"],
         "forward_tflops_padded": round(1.425e9 * B / (ms * 1e-3) / 1e12, 2),
     }
     if not args.no_cpu:

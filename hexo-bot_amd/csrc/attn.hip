@@ -42,16 +42,6 @@ enum : int { PATH_GENERAL = 0, PATH_CLAMP = 1, PATH_LINEAR = 2 };
 constexpr int XD = SHRIMP_ATTN_XD;
 constexpr int XW = 2 * XD + 1;
 
-// Max over the 4 lane groups (l / 16) that share l % 16, on VALU lane swaps.
-SHRIMP_DEV float max_groups_swap(float x) {
-  const unsigned u = __float_as_uint(x);
-  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const unsigned v = __float_as_uint(y);
-  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-
 SHRIMP_DEV int clampi(int x, int m) { return min(max(x, -m), m); }
 
 template <int HG>

@@ -22,6 +22,15 @@ inline int check_launch(const char* what) {
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Largest dynamic LDS allocation one workgroup may request on the current
+// device (queried once per device).
+int max_lds_per_block();
+
+// Conv kernel selection: 0 = automatic (LDS-staged when the position fits,
+// else global gather), 1 = always the global-gather kernel, 2 = LDS-staged,
+// 3 = big-tile LDS kernel for the 128-channel 7-tap shape (else as 0).
+extern int g_conv_variant;
+
 }  // namespace shrimp
 
 #define SHRIMP_REQUIRE(cond, ...)                                 \

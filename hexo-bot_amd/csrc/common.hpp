@@ -96,6 +96,26 @@ SHRIMP_DEV float max_lane_groups(float v) {
   return v;
 }
 
+// Sum / max over the 4 lane groups on VALU lane swaps (v_permlane16_swap,
+// v_permlane32_swap) instead of LDS-routed shuffles. Every lane of a group
+// gets the bit-identical result (the pair sums are commutative).
+SHRIMP_DEV float sum_groups_swap(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const unsigned v = __float_as_uint(y);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+SHRIMP_DEV float max_groups_swap(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const unsigned v = __float_as_uint(y);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 SHRIMP_DEV float wave_sum(float v) {
   for (int m = 32; m >= 1; m >>= 1) v += xor_shfl(v, m);
   return v;

@@ -25,6 +25,142 @@ namespace shrimp {
 
 enum : int { EPI_LN = 1, EPI_RELU = 2, EPI_RESID = 4, EPI_HEAD = 8 };
 
+// Bias / LayerNorm / ReLU / mask / residual / head epilogue on the fp32
+// accumulators of MB row blocks. rb, rn: position and cell index of this
+// lane's row in block mb; rv: row exists.
+// PRE (kernels with registers to spare): the per-channel parameters of this
+// lane's channels are loaded once into registers (they would otherwise be
+// re-read after every store, which the compiler must assume may alias them).
+// The row masks are loaded up front and the residual rows of block mb+1 are
+// requested before block mb's math.
+template <int COUT, int MB, int EPI, bool PRE>
+SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16][MB],
+                              const int (&rb)[MB], const int (&rn)[MB], const bool (&rv)[MB],
+                              int lg) {
+  constexpr int NB = COUT / 16;
+  constexpr bool LN = (EPI & EPI_LN) != 0, RESID = (EPI & EPI_RESID) != 0;
+  constexpr bool HEAD = (EPI & EPI_HEAD) != 0;
+  constexpr int PN = PRE ? NB : 1;
+  const int N = a.N;
+  f32x4 pb[PN], pw[LN ? PN : 1], pl[LN ? PN : 1], pg[RESID ? PN : 1], ph[HEAD ? PN : 1];
+  auto prm = [&](const float* p, int nb) { return *reinterpret_cast<const f32x4*>(p + nb * 16 + lg * 4); };
+  if constexpr (PRE) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      pb[nb] = prm(a.bias, nb);
+      if constexpr (LN) {
+        pw[nb] = prm(a.ln_w, nb);
+        pl[nb] = prm(a.ln_b, nb);
+      }
+      if constexpr (RESID) pg[nb] = prm(a.gamma, nb);
+      if constexpr (HEAD) ph[nb] = prm(a.head_w, nb);
+    }
+  }
+  auto P_b = [&](int nb) { if constexpr (PRE) return pb[nb]; else return prm(a.bias, nb); };
+  auto P_w = [&](int nb) { if constexpr (PRE) return pw[nb % (LN ? NB : 1)]; else return prm(a.ln_w, nb); };
+  auto P_l = [&](int nb) { if constexpr (PRE) return pl[nb % (LN ? NB : 1)]; else return prm(a.ln_b, nb); };
+  auto P_g = [&](int nb) { if constexpr (PRE) return pg[nb % (RESID ? NB : 1)]; else return prm(a.gamma, nb); };
+  auto P_h = [&](int nb) { if constexpr (PRE) return ph[nb % (HEAD ? NB : 1)]; else return prm(a.head_w, nb); };
+  bool live[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) live[mb] = rv[mb] && a.mask[(int64_t)rb[mb] * N + rn[mb]] != 0;
+  const float hb = HEAD ? a.head_b[0] : 0.f;
+
+  auto resid_row = [&](int mb, u32x2 (&r)[NB]) {
+    if constexpr (RESID) {
+      const unsigned short* rp = static_cast<const unsigned short*>(a.resid) +
+                                 (int64_t)rb[mb] * a.r_sb + (int64_t)rn[mb] * a.r_sn + lg * 4;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        r[nb] = rv[mb] ? *reinterpret_cast<const u32x2*>(rp + nb * 16) : u32x2{0u, 0u};
+    }
+  };
+  u32x2 rcur[RESID ? NB : 1], rnext[RESID ? NB : 1];
+  if constexpr (RESID) resid_row(0, rcur);
+
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    if constexpr (RESID) {
+      if (mb + 1 < MB) resid_row(mb + 1, rnext);
+    }
+    float v[NB][4];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const f32x4 bb = P_b(nb);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[nb][j] = acc[nb][mb][j] + bb[j];
+    }
+    if constexpr (LN) {
+      float s = 0.f;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s += v[nb][j];
+      const float mean = sum_groups_swap(s) * (1.0f / COUT);
+      float q = 0.f;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[nb][j] -= mean;
+          q += v[nb][j] * v[nb][j];
+        }
+      const float rstd = rsqrtf(sum_groups_swap(q) * (1.0f / COUT) + a.eps);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const f32x4 gw = P_w(nb), gb = P_l(nb);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[nb][j] = v[nb][j] * rstd * gw[j] + gb[j];
+      }
+    }
+    if (EPI & EPI_RELU) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[nb][j] = fmaxf(v[nb][j], 0.f);
+    }
+    if constexpr (HEAD) {
+      float h = 0.f;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const f32x4 hw = P_h(nb);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) h += v[nb][j] * hw[j];
+      }
+      h = sum_groups_swap(h);
+      if (rv[mb] && lg == 0) a.head_out[(int64_t)rb[mb] * N + rn[mb]] = live[mb] ? h + hb : 0.f;
+      continue;
+    }
+    if (rv[mb]) {
+      unsigned short* op = static_cast<unsigned short*>(a.out) + (int64_t)rb[mb] * a.o_sb +
+                           (int64_t)rn[mb] * a.o_sn + lg * 4;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = live[mb] ? v[nb][j] : 0.f;
+        if constexpr (RESID) {
+          const u32x2 rw = rcur[nb];
+          const f32x4 g = P_g(nb);
+          o[0] = fmaxf(bf16_lo(rw.x) + g[0] * o[0], 0.f);
+          o[1] = fmaxf(bf16_hi(rw.x) + g[1] * o[1], 0.f);
+          o[2] = fmaxf(bf16_lo(rw.y) + g[2] * o[2], 0.f);
+          o[3] = fmaxf(bf16_hi(rw.y) + g[3] * o[3], 0.f);
+        }
+        u32x2 pk;
+        pk.x = pack_bf16x2(o[0], o[1]);
+        pk.y = pack_bf16x2(o[2], o[3]);
+        *reinterpret_cast<u32x2*>(op + nb * 16) = pk;
+      }
+    }
+    if constexpr (RESID) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) rcur[nb] = rnext[nb];
+    }
+  }
+}
+
+// Global-gather variant: any N, any cin_pad; rows fetched from HBM / L2 per tap.
 template <int COUT, int MB, int EPI>
 __global__ __launch_bounds__(256, 2) void hex_conv_kernel(const shrimp_conv_args a,
                                                           uint32_t x_bytes, uint32_t w_bytes) {
@@ -104,91 +240,324 @@ __global__ __launch_bounds__(256, 2) void hex_conv_kernel(const shrimp_conv_args
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = mfma16x16x32(wc[nb], xc[mb], acc[nb][mb]);
   }
+  conv_epilogue<COUT, MB, EPI, false>(a, acc, rb, rn, rv, lg);
+}
 
-  // ---- epilogue ------------------------------------------------------------
+// LDS-staged variant: one workgroup per position. The position's N rows
+// (cin_pad = CIN channels) are copied once into LDS, plus one zero row at
+// index N that stands for every absent neighbour, and all taps gather from
+// there, so HBM sees each row once (the global variant re-fetches a row per
+// tap once the rows of all resident positions exceed the L2).
+// Row j occupies bytes [j*2*CIN, (j+1)*2*CIN); its 16-byte chunk c is stored
+// at chunk slot c ^ (j % (CIN/8)), so the 16 lanes of an MFMA lane group,
+// reading the same chunk of 16 different rows, mostly hit distinct banks.
+template <int COUT, int MB, int EPI, int CIN>
+__global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_args a,
+                                                              uint32_t w_bytes) {
+  constexpr int NB = COUT / 16;
+  constexpr int ROWB = CIN * 2;
+  constexpr int CPR = CIN / 8;
+  constexpr int KC = CIN / 32;
+  constexpr int TILE = 4 * MB * 16;
+  static_assert((CPR & (CPR - 1)) == 0, "chunks per row must be a power of two");
+  extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int lr = lane & 15;
+  const int lg = lane >> 4;
+  const int N = a.N;
+  const int b = blockIdx.x;
+
+  // ---- stage rows 0..N-1 and the zero row N --------------------------------
+  {
+    const unsigned short* xb = static_cast<const unsigned short*>(a.x) + (int64_t)b * a.x_sb;
+    const int total = (N + 1) * CPR;
+    constexpr int U = 8;
+    for (int c0 = threadIdx.x; c0 < total; c0 += 256 * U) {
+      u32x4 v[U];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    float v[NB][4];
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * 256;
+        const int row = c / CPR;
+        const int ch = c & (CPR - 1);
+        v[u] = u32x4{0u, 0u, 0u, 0u};
+        if (row < N) v[u] = *reinterpret_cast<const u32x4*>(xb + (int64_t)row * a.x_sn + ch * 8);
+      }
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const f32x4 bb = *reinterpret_cast<const f32x4*>(a.bias + nb * 16 + lg * 4);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[nb][j] = acc[nb][mb][j] + bb[j];
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * 256;
+        const int row = c / CPR;
+        const int ch = c & (CPR - 1);
+        if (c < total)
+          *reinterpret_cast<u32x4*>(xs + row * ROWB + ((ch ^ (row & (CPR - 1))) << 4)) = v[u];
+      }
     }
-    if (EPI & EPI_LN) {
-      float s = 0.f;
+  }
+  __syncthreads();
+
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, w_bytes);
+  const int* idxb = a.idx + (int64_t)b * N * a.idx_stride;
+  const int taps = a.taps;
+  const int nsteps = taps * KC;
+
+  for (int tile0 = 0; tile0 < N; tile0 += TILE) {
+    const int row_base = tile0 + wave * MB * 16;
+    if (row_base >= N) break;
+    int rb[MB], rn[MB];
+    bool rv[MB];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+    for (int mb = 0; mb < MB; ++mb) {
+      rb[mb] = b;
+      rn[mb] = row_base + mb * 16 + lr;
+      rv[mb] = rn[mb] < N;
+    }
+    // Neighbour row of tap t (N for absent) -> swizzled LDS row address.
+    auto tap_rows = [&](int t, int (&j)[MB]) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s += v[nb][j];
-      const float mean = sum_lane_groups(s) * (1.0f / COUT);
-      float q = 0.f;
+      for (int mb = 0; mb < MB; ++mb) {
+        int v = rv[mb] ? idxb[rn[mb] * a.idx_stride + t] : N;
+        j[mb] = (v >= 0 && v < N) ? v : N;
+      }
+    };
+    auto row_addr = [&](int j) -> uint32_t {
+      return (uint32_t)(j * ROWB) | ((uint32_t)(j & (CPR - 1)) << 4);
+    };
+
+    f32x4 acc[NB][MB];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[nb][j] -= mean;
-          q += v[nb][j] * v[nb][j];
+      for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    int jn[MB];
+    uint32_t sw[MB];
+    tap_rows(0, jn);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) sw[mb] = row_addr(jn[mb]);
+    if (taps > 1) tap_rows(1, jn);
+
+    u32x4 xf[MB], wf[NB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      xf[mb] = *reinterpret_cast<const u32x4*>(xs + (sw[mb] ^ ((uint32_t)lg << 4)));
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) wf[nb] = buf_load16(wr, (uint32_t)((nb * 64 + lane) * 16));
+
+    int t = 0, kc = 0;
+    for (int s = 0; s < nsteps; ++s) {
+      u32x4 xc[MB], wc[NB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) xc[mb] = xf[mb];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) wc[nb] = wf[nb];
+      if (s + 1 < nsteps) {
+        if (++kc == KC) {
+          kc = 0;
+          ++t;
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) sw[mb] = row_addr(jn[mb]);
+          if (t + 1 < taps) tap_rows(t + 1, jn);
         }
-      const float rstd = rsqrtf(sum_lane_groups(q) * (1.0f / COUT) + a.eps);
+        const uint32_t cs = (uint32_t)(kc * 4 + lg) << 4;
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const f32x4 gw = *reinterpret_cast<const f32x4*>(a.ln_w + nb * 16 + lg * 4);
-        const f32x4 gb = *reinterpret_cast<const f32x4*>(a.ln_b + nb * 16 + lg * 4);
+        for (int mb = 0; mb < MB; ++mb)
+          xf[mb] = *reinterpret_cast<const u32x4*>(xs + (sw[mb] ^ cs));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[nb][j] = v[nb][j] * rstd * gw[j] + gb[j];
+        for (int nb = 0; nb < NB; ++nb)
+          wf[nb] = buf_load16(wr, (uint32_t)((((s + 1) * NB + nb) * 64 + lane) * 16));
       }
-    }
-    if (EPI & EPI_RELU) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[nb][j] = fmaxf(v[nb][j], 0.f);
+        for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = mfma16x16x32(wc[nb], xc[mb], acc[nb][mb]);
     }
-    const bool live = rv[mb] && a.mask[(int64_t)rb[mb] * N + rn[mb]] != 0;
-    if (EPI & EPI_HEAD) {
-      float h = 0.f;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const f32x4 hw = *reinterpret_cast<const f32x4*>(a.head_w + nb * 16 + lg * 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) h += v[nb][j] * hw[j];
-      }
-      h = sum_lane_groups(h);
-      if (rv[mb] && lg == 0) a.head_out[(int64_t)rb[mb] * N + rn[mb]] = live ? h + a.head_b[0] : 0.f;
-      continue;
-    }
-    if (!rv[mb]) continue;
-    const int64_t obase = (int64_t)rb[mb] * a.o_sb + (int64_t)rn[mb] * a.o_sn + lg * 4;
-    const int64_t rbase = (int64_t)rb[mb] * a.r_sb + (int64_t)rn[mb] * a.r_sn + lg * 4;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      float o[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = live ? v[nb][j] : 0.f;
-      if (EPI & EPI_RESID) {
-        const u32x2 rw =
-            *reinterpret_cast<const u32x2*>(static_cast<const unsigned short*>(a.resid) + rbase + nb * 16);
-        const f32x4 g = *reinterpret_cast<const f32x4*>(a.gamma + nb * 16 + lg * 4);
-        o[0] = fmaxf(bf16_lo(rw.x) + g[0] * o[0], 0.f);
-        o[1] = fmaxf(bf16_hi(rw.x) + g[1] * o[1], 0.f);
-        o[2] = fmaxf(bf16_lo(rw.y) + g[2] * o[2], 0.f);
-        o[3] = fmaxf(bf16_hi(rw.y) + g[3] * o[3], 0.f);
-      }
-      u32x2 pk;
-      pk.x = pack_bf16x2(o[0], o[1]);
-      pk.y = pack_bf16x2(o[2], o[3]);
-      *reinterpret_cast<u32x2*>(static_cast<unsigned short*>(a.out) + obase + nb * 16) = pk;
-    }
+    conv_epilogue<COUT, MB, EPI, false>(a, acc, rb, rn, rv, lg);
   }
 }
 
+// Big-tile variant for the trunk shape (cin_pad = cout = 128, 7 taps, N <= 512):
+// one workgroup per position with ceil(N/128) waves, each wave owning 128 rows
+// x all 128 output channels (8 x 8 MFMA tiles, 256 fp32 accumulators held in
+// AGPRs, so one wave per SIMD). Every weight fragment feeds 8 MFMAs and every
+// gathered row fragment 8, which keeps both the L1 (weights) and the LDS (rows)
+// well under their bandwidth at full MFMA rate.
+// The K loop runs channel-chunk-major (kc = 32-channel chunk, then the 7 taps),
+// and rows are staged one chunk ahead: chunk kc+1 is loaded from HBM into
+// registers while the MFMAs of chunk kc run, then written to LDS behind a
+// barrier.
+constexpr int BIG_MAX_N = 512;
+
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_args a,
+                                                              uint32_t w_bytes) {
+  constexpr int COUT = 128, CIN = 128, ROWB = CIN * 2, CPR = CIN / 8, KC = CIN / 32;
+  constexpr int T = 7, MB = 8, NB = COUT / 16;
+  // Staging: chunk kc of every row is N x 4 pieces of 16 bytes; with
+  // ceil(N/128) waves that is at most SU = 8 pieces per thread, spread over
+  // the 7 tap steps of the previous chunk (piece u is loaded at step u*T/SU
+  // and written to LDS one step later).
+  constexpr int SU = 8;
+  extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nthr = blockDim.x;
+  const int lr = lane & 15;
+  const int lg = lane >> 4;
+  const int N = a.N;
+  const int b = blockIdx.x;
+  const unsigned short* xb = static_cast<const unsigned short*>(a.x) + (int64_t)b * a.x_sb;
+  const int pieces = N * 4;
+
+  auto piece_load = [&](int kc, int u) -> u32x4 {
+    const int c = u * nthr + (int)threadIdx.x;
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (c < pieces)
+      v = *reinterpret_cast<const u32x4*>(xb + (int64_t)(c >> 2) * a.x_sn + (kc * 4 + (c & 3)) * 8);
+    return v;
+  };
+  auto piece_store = [&](int kc, int u, u32x4 v) {
+    const int c = u * nthr + (int)threadIdx.x;
+    const int row = c >> 2;
+    const int ch = kc * 4 + (c & 3);
+    if (c < pieces) *reinterpret_cast<u32x4*>(xs + row * ROWB + ((ch ^ (row & (CPR - 1))) << 4)) = v;
+  };
+
+  // Prologue: request the neighbour indices of all taps, chunk 0 of the rows
+  // and the first weight fragments together, then write LDS.
+  const int row0 = wave * (MB * 16);
+  int rn[MB], rb[MB];
+  bool rv[MB];
+  const int* idxb = a.idx + (int64_t)b * N * a.idx_stride;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    rb[mb] = b;
+    rn[mb] = row0 + mb * 16 + lr;
+    rv[mb] = rn[mb] < N;
+  }
+  int jr[T][MB];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) jr[t][mb] = rv[mb] ? idxb[rn[mb] * a.idx_stride + t] : N;
+  u32x4 v0[SU];
+#pragma unroll
+  for (int u = 0; u < SU; ++u) v0[u] = piece_load(0, u);
+
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, w_bytes);
+  auto wload = [&](int s, u32x4 (&w)[NB]) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) w[nb] = buf_load16(wr, (uint32_t)(((s * NB + nb) * 64 + lane) * 16));
+  };
+  u32x4 wf[NB];
+  wload(0, wf);
+
+  // Zero row N (all chunks), then chunk 0.
+  for (int c = threadIdx.x; c < CPR; c += nthr)
+    *reinterpret_cast<u32x4*>(xs + N * ROWB + c * 16) = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int u = 0; u < SU; ++u) piece_store(0, u, v0[u]);
+
+  // Neighbour rows as 16-bit swizzled row addresses in 16-byte units:
+  // (j * ROWB + (j % CPR) * 16) / 16 = j * 16 + j % 16; two per register.
+  uint32_t sw2[T][MB / 2];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int m2 = 0; m2 < MB / 2; ++m2) {
+      uint32_t pk = 0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int j = jr[t][2 * m2 + h];
+        const int jj = (j >= 0 && j < N) ? j : N;
+        pk |= (uint32_t)(jj * (ROWB / 16) + (jj & (CPR - 1))) << (16 * h);
+      }
+      sw2[t][m2] = pk;
+    }
+
+  auto xload = [&](int t, int kc, u32x4 (&x)[MB]) {
+    const uint32_t cs = (uint32_t)(kc * 4 + lg);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const uint32_t v = (sw2[t][mb >> 1] >> (16 * (mb & 1))) & 0xFFFFu;
+      x[mb] = *reinterpret_cast<const u32x4*>(xs + ((v ^ cs) << 4));
+    }
+  };
+
+  f32x4 acc[NB][MB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  __syncthreads();
+
+  // Every wave owns rows (waves = ceil(N / 128)), so no wave skips the MFMAs;
+  // the chunk loop is fully unrolled so that no value crosses a branch.
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    const bool more = kc + 1 < KC;
+    u32x4 xf[MB];
+    xload(0, kc, xf);
+    u32x4 pv[2];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      // staging of chunk kc + 1: pieces [u0, u1) load now, store next step
+      const int u0 = (t * SU) / T, u1 = ((t + 1) * SU) / T;
+      u32x4 nv[2];
+      if (more) {
+#pragma unroll
+        for (int u = u0; u < u1; ++u) nv[u - u0] = piece_load(kc + 1, u);
+        if (t > 0) {
+          const int p0 = ((t - 1) * SU) / T, p1 = (t * SU) / T;
+#pragma unroll
+          for (int u = p0; u < p1; ++u) piece_store(kc + 1, u, pv[u - p0]);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) pv[i] = nv[i];
+      }
+      u32x4 xc[MB], wc[NB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) xc[mb] = xf[mb];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) wc[nb] = wf[nb];
+      if (t + 1 < T) {
+        xload(t + 1, kc, xf);
+        wload((t + 1) * KC + kc, wf);
+      } else if (more) {
+        wload(kc + 1, wf);
+      }
+      // Keep the next step's loads ahead of this step's MFMAs (the scheduler
+      // would otherwise sink them next to their uses).
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = mfma16x16x32(wc[nb], xc[mb], acc[nb][mb]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (more) {
+      constexpr int p0 = ((T - 1) * SU) / T;
+#pragma unroll
+      for (int u = p0; u < SU; ++u) piece_store(kc + 1, u, pv[u - p0]);
+      __syncthreads();
+    }
+  }
+  conv_epilogue<COUT, MB, EPI, true>(a, acc, rb, rn, rv, lg);
+}
+
 // ---- weight packing ------------------------------------------------------------
-// Fragment f = (ks * NB + nb) * 64 + lane holds 8 bf16:
-//   W[k = 32*ks + 8*(lane/16) + e][n = 16*nb + lane%16],  k = t*cin_pad + c.
+// Fragment f = (ks * NB + nb) * 64 + lane holds 8 bf16, element e:
+//   W[k][n = 16*nb + lane%16] with
+//   k = 32*ks + 8*(lane/16) + e                    (standard order), or
+//   k = 32*ks + 16*(e/4) + 4*(lane/16) + e%4       (interleaved order: the
+//       K-slice a lane holds is the 4 + 4 channels it owns in the output
+//       fragments of the previous 16x16 MFMA product),
+// and for convolutions k = t*cin_pad + c.
 __global__ void pack_weight_kernel(const float* __restrict__ src, unsigned short* __restrict__ dst,
                                    int K, int NOUT, int cin, int cin_pad, int64_t s_t,
-                                   int64_t s_c, int64_t s_n) {
+                                   int64_t s_c, int64_t s_n, int interleaved) {
   const int NB = NOUT / 16;
   const int64_t frags = (int64_t)(K / 32) * NB * 64;
   const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -199,7 +568,8 @@ __global__ void pack_weight_kernel(const float* __restrict__ src, unsigned short
   const int n = nb * 16 + (lane & 15);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const int k = ks * 32 + (lane >> 4) * 8 + e;
+    const int k = interleaved ? ks * 32 + (e >> 2) * 16 + (lane >> 4) * 4 + (e & 3)
+                              : ks * 32 + (lane >> 4) * 8 + e;
     const int t = k / cin_pad;
     const int c = k - t * cin_pad;
     const float v = (c < cin) ? src[t * s_t + c * s_c + n * s_n] : 0.f;
@@ -208,7 +578,29 @@ __global__ void pack_weight_kernel(const float* __restrict__ src, unsigned short
 }
 
 template <int COUT, int MB, int EPI>
-static int launch_conv(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, hipStream_t st) {
+static int launch_conv(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, size_t lds,
+                       hipStream_t st) {
+  if (COUT == 128 && lds && a->cin_pad == 128 && a->taps == 7 && a->N <= BIG_MAX_N &&
+      g_conv_variant == 3) {
+    const int waves = (a->N + 127) / 128;
+    hipLaunchKernelGGL((hex_conv_big_kernel<EPI>), dim3(a->B), dim3(64 * waves), lds, st, *a, wb);
+    return check_launch("hex_conv");
+  }
+  if (lds) {
+    switch (a->cin_pad) {
+#define SHRIMP_CONV_LDS(CINV)                                                               \
+  case CINV:                                                                                \
+    hipLaunchKernelGGL((hex_conv_lds_kernel<COUT, MB, EPI, CINV>), dim3(a->B), dim3(256), lds, \
+                       st, *a, wb);                                                         \
+    return check_launch("hex_conv");
+      SHRIMP_CONV_LDS(32)
+      SHRIMP_CONV_LDS(64)
+      SHRIMP_CONV_LDS(128)
+#undef SHRIMP_CONV_LDS
+      default:
+        break;
+    }
+  }
   const int rows = a->B * a->N;
   const int per_block = 4 * MB * 16;
   const int grid = (rows + per_block - 1) / per_block;
@@ -217,18 +609,29 @@ static int launch_conv(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, hipS
 }
 
 template <int EPI>
-static int dispatch_cout(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, hipStream_t st) {
+static int dispatch_cout(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, size_t lds,
+                         hipStream_t st) {
   switch (a->cout) {
-    case 32: return launch_conv<32, 4, EPI>(a, xb, wb, st);
-    case 64: return launch_conv<64, 4, EPI>(a, xb, wb, st);
-    case 96: return launch_conv<96, 4, EPI>(a, xb, wb, st);
-    case 128: return launch_conv<128, 4, EPI>(a, xb, wb, st);
-    case 192: return launch_conv<192, 2, EPI>(a, xb, wb, st);
-    case 256: return launch_conv<256, 1, EPI>(a, xb, wb, st);
+    case 32: return launch_conv<32, 4, EPI>(a, xb, wb, lds, st);
+    case 64: return launch_conv<64, 4, EPI>(a, xb, wb, lds, st);
+    case 96: return launch_conv<96, 4, EPI>(a, xb, wb, lds, st);
+    case 128: return launch_conv<128, 4, EPI>(a, xb, wb, lds, st);
+    case 192: return launch_conv<192, 2, EPI>(a, xb, wb, lds, st);
+    case 256: return launch_conv<256, 1, EPI>(a, xb, wb, lds, st);
     default: return set_error(SHRIMP_EINVAL, "hex_conv: unsupported cout %d", a->cout);
   }
 }
 
+// LDS bytes the staged variant needs, or 0 when the global-gather variant
+// runs instead (cin_pad without a staged instance, unaligned rows, or a
+// position too large for one workgroup's LDS).
+static size_t conv_lds_bytes(const shrimp_conv_args* a) {
+  if (a->cin_pad != 32 && a->cin_pad != 64 && a->cin_pad != 128) return 0;
+  if ((reinterpret_cast<uintptr_t>(a->x) & 15) != 0 || a->x_sb % 8 != 0 || a->x_sn % 8 != 0)
+    return 0;
+  const size_t bytes = (size_t)(a->N + 1) * a->cin_pad * 2;
+  return bytes <= (size_t)max_lds_per_block() ? bytes : 0;
+}
 }  // namespace shrimp
 
 using namespace shrimp;
@@ -253,12 +656,12 @@ extern "C" int shrimp_pack_conv_weight(const float* w, void* packed, int taps, i
   const int grid = (int)((frags + 255) / 256);
   hipLaunchKernelGGL(pack_weight_kernel, dim3(grid), dim3(256), 0, as_stream(stream), w,
                      static_cast<unsigned short*>(packed), K, cout, cin, cin_pad,
-                     (int64_t)cin * cout, (int64_t)cout, (int64_t)1);
+                     (int64_t)cin * cout, (int64_t)cout, (int64_t)1, 0);
   return check_launch("pack_conv_weight");
 }
 
-extern "C" int shrimp_pack_linear_weight(const float* w, void* packed, int in_features,
-                                         int out_features, void* stream) {
+static int pack_linear(const float* w, void* packed, int in_features, int out_features,
+                       void* stream, int interleaved) {
   SHRIMP_REQUIRE(w && packed, "pack_linear_weight: null pointer");
   SHRIMP_REQUIRE(in_features % 32 == 0 && out_features % 16 == 0,
                  "pack_linear_weight: shape (%d -> %d) needs in %% 32 == 0, out %% 16 == 0",
@@ -267,8 +670,19 @@ extern "C" int shrimp_pack_linear_weight(const float* w, void* packed, int in_fe
   const int grid = (int)((frags + 255) / 256);
   hipLaunchKernelGGL(pack_weight_kernel, dim3(grid), dim3(256), 0, as_stream(stream), w,
                      static_cast<unsigned short*>(packed), in_features, out_features,
-                     in_features, in_features, (int64_t)0, (int64_t)1, (int64_t)in_features);
+                     in_features, in_features, (int64_t)0, (int64_t)1, (int64_t)in_features,
+                     interleaved);
   return check_launch("pack_linear_weight");
+}
+
+extern "C" int shrimp_pack_linear_weight(const float* w, void* packed, int in_features,
+                                         int out_features, void* stream) {
+  return pack_linear(w, packed, in_features, out_features, stream, 0);
+}
+
+extern "C" int shrimp_pack_linear_weight_il(const float* w, void* packed, int in_features,
+                                            int out_features, void* stream) {
+  return pack_linear(w, packed, in_features, out_features, stream, 1);
 }
 
 extern "C" int shrimp_hex_conv(const shrimp_conv_args* a, void* stream) {
@@ -301,17 +715,19 @@ extern "C" int shrimp_hex_conv(const shrimp_conv_args* a, void* stream) {
   const uint32_t xb = (uint32_t)(x_extent * 2);
   const uint32_t wb = (uint32_t)shrimp_conv_wpack_bytes(a->taps, a->cin_pad, a->cout);
   hipStream_t st = as_stream(stream);
+  const size_t lds = g_conv_variant == 1 ? 0 : conv_lds_bytes(a);
   if (head) {
     SHRIMP_REQUIRE(a->relu, "hex_conv: head epilogue expects relu");
-    return dispatch_cout<EPI_HEAD | EPI_RELU>(a, xb, wb, st);
+    return dispatch_cout<EPI_HEAD | EPI_RELU>(a, xb, wb, lds, st);
   }
   if (resid) {
     SHRIMP_REQUIRE(ln && !a->relu, "hex_conv: residual epilogue is LN (no relu) + residual");
-    return dispatch_cout<EPI_LN | EPI_RESID>(a, xb, wb, st);
+    return dispatch_cout<EPI_LN | EPI_RESID>(a, xb, wb, lds, st);
   }
   if (ln) {
-    return a->relu ? dispatch_cout<EPI_LN | EPI_RELU>(a, xb, wb, st)
-                   : dispatch_cout<EPI_LN>(a, xb, wb, st);
+    return a->relu ? dispatch_cout<EPI_LN | EPI_RELU>(a, xb, wb, lds, st)
+                   : dispatch_cout<EPI_LN>(a, xb, wb, lds, st);
   }
-  return a->relu ? dispatch_cout<EPI_RELU>(a, xb, wb, st) : dispatch_cout<0>(a, xb, wb, st);
+  return a->relu ? dispatch_cout<EPI_RELU>(a, xb, wb, lds, st)
+                 : dispatch_cout<0>(a, xb, wb, lds, st);
 }

@@ -9,15 +9,15 @@ Device layout of one batch (B positions, N = Npad cells, S = N + 8 rows):
     y1    (B, N, C)  bf16  first conv of a ConvBlock
     qkv   (3, B, H, S, dpad) bf16 head-major projections
     att   (B, S, C)  bf16  attention output, heads concatenated
-    hid   (B, S, 2C) bf16  MLP hidden
+    hid   (B, S, 2C) bf16  MLP hidden (unfused MLP path only)
     seqf  (B, S, C)  bf16  after the final LayerNorm (cells masked)
 
 Kernel sequence (reference lines in model.py):
     prep_inputs          gather_idx / mask / coords / seq_lens / padded feats  :861-892
     hex_conv  (stem)     conv + LN + ReLU + mask                               :865
     per 'C': hex_conv x2 conv1+LN+ReLU+mask -> y1; conv2+LN+mask, ReLU(x+g*y)  :395-422
-    per 'A': linear(QKV, LN1) -> attn -> linear(out_proj, residual)
-             -> linear(fc1, LN2, GELU) -> linear(fc2, residual)                :448-514
+    per 'A': linear(QKV, LN1) -> attn -> attn_mlp (out_proj, residual, LN2,
+             fc1, GELU, fc2, residual; three linear launches when C != 128)   :448-514
     trunk_tail           final LN, pooled mean, value / moves-left heads       :927-935, 990-1002
     hex_conv  (policy)   conv + ReLU + Linear(C,1) + mask                      :1011-1020
 Weights are packed once into MFMA fragment order (bf16) and re-packed when
@@ -36,6 +36,7 @@ from .geometry import CELL_LUT_M
 from .ops import (
     attn_bias_table,
     launch_attn,
+    launch_attn_mlp,
     launch_conv,
     launch_linear,
     pack_conv_weight,
@@ -72,6 +73,9 @@ class HipForward:
         # The unclamped offset table lets the attention kernel index biases
         # linearly for compact positions; off forces the clamped LUT path.
         self.use_linear_bias = True
+        # Fused out_proj + MLP kernel where it applies; off runs the three
+        # linear kernels (used to check one against the other).
+        self.use_fused_mlp = True
 
     def invalidate(self) -> None:
         self._packed = None
@@ -100,8 +104,8 @@ class HipForward:
         def conv_w(conv, cin_pad=None):
             return pack_conv_weight(conv.weight.detach().to(device), cin_pad)
 
-        def lin_w(lin):
-            return pack_linear_weight(lin.weight.detach().to(device))
+        def lin_w(lin, interleaved=False):
+            return pack_linear_weight(lin.weight.detach().to(device), interleaved)
 
         c = net.channels
         P = SimpleNamespace()
@@ -125,6 +129,9 @@ class HipForward:
             )
         lut = net._cell_bias_lut_u8.to(device)
         P.lut = lut
+        # out_proj + MLP run as one fused kernel when its weights fit one
+        # workgroup's LDS (C = 128, hidden = 2C)
+        P.fused_mlp = c == 128 and all(b.fc1.out_features == 2 * c for b in net.attn_blocks)
         P.attn = []
         for i, blk in enumerate(net.attn_blocks):
             at = blk.attn
@@ -138,6 +145,8 @@ class HipForward:
                     ln2w=f32(blk.ln2.weight), ln2b=f32(blk.ln2.bias), eps2=blk.ln2.eps,
                     fc1_w=lin_w(blk.fc1), fc1_b=f32(blk.fc1.bias),
                     fc2_w=lin_w(blk.fc2), fc2_b=f32(blk.fc2.bias),
+                    fc1_w_il=lin_w(blk.fc1, True) if P.fused_mlp else None,
+                    fc2_w_il=lin_w(blk.fc2, True) if P.fused_mlp else None,
                     g_attn=f32(blk.ls_attn.gamma), g_mlp=f32(blk.ls_mlp.gamma),
                     btab_xtab=attn_bias_table(net.bias_tables[i].detach().to(device), lut,
                                               CELL_LUT_M),
@@ -209,7 +218,8 @@ class HipForward:
         y1 = torch.empty((B, N, C), dtype=bf, device=dev)
         qkv = (torch.zeros if d != dpad else torch.empty)((3, B, H, S, dpad), dtype=bf, device=dev)
         att = torch.empty((B, S, C), dtype=bf, device=dev)
-        hid = torch.empty((B, S, 2 * C), dtype=bf, device=dev)
+        fused = P.fused_mlp and self.use_fused_mlp
+        hid = None if fused else torch.empty((B, S, 2 * C), dtype=bf, device=dev)
 
         conv_common = dict(idx=idx, taps=7, idx_stride=7, mask8=mask8, B=B, N=N, stream=st)
         launch_conv(
@@ -249,6 +259,14 @@ class HipForward:
                     xtab=a.btab_xtab[1] if self.use_linear_bias else None, lut_m=CELL_LUT_M,
                     n_tokens=NUM_TOKENS, stream=st,
                 )
+                if fused:
+                    launch_attn_mlp(
+                        x=att, x_sr=C, seq=seq, s_sr=C, mask=seq_mask, out_w=a.out_w,
+                        out_b=a.out_b, g_attn=a.g_attn, ln_w=a.ln2w, ln_b=a.ln2b, eps=a.eps2,
+                        fc1_w=a.fc1_w_il, fc1_b=a.fc1_b, fc2_w=a.fc2_w_il, fc2_b=a.fc2_b,
+                        g_mlp=a.g_mlp, rows=rows, C=C, hidden=2 * C, stream=st,
+                    )
+                    continue
                 launch_linear(
                     x=att, x_sr=C, wpack=a.out_w, bias=a.out_b, rows=rows, n_in=C, n_out=C,
                     mode=_lib.LIN_RESID, out=seq, o_sr=C, resid=seq, r_sr=C, gamma=a.g_attn,

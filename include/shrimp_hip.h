@@ -43,6 +43,17 @@ extern "C" {
 const char* shrimp_last_error(void);
 int shrimp_abi_version(void);
 
+/* Tuning / test switches (no counterpart in the reference).
+ * shrimp_conv_variant: 0 = automatic conv kernel choice (a position's rows
+ * staged in LDS when they fit), 1 = always gather rows from global memory,
+ * 2 = LDS-staged rows, 3 = LDS-staged rows with 128x128 tiles per wave for
+ * the 128-channel 7-tap conv; other values only query. Returns the previous
+ * setting. Process-wide.
+ * shrimp_max_lds_per_block: LDS bytes one workgroup may allocate on the
+ * current device (the staged conv needs (N + 1) * cin_pad * 2). */
+int shrimp_conv_variant(int variant);
+int shrimp_max_lds_per_block(void);
+
 /* ------------------------------------------------------------------------
  * Weight packing (device -> device). MFMA operands are read in fragment
  * order: for K-step ks (32 rows of K) and output block nb (16 outputs), 64
@@ -58,6 +69,11 @@ int shrimp_pack_conv_weight(const float* w, void* packed, int taps, int cin, int
 size_t shrimp_linear_wpack_bytes(int in_features, int out_features);
 int shrimp_pack_linear_weight(const float* w, void* packed, int in_features, int out_features,
                               void* stream);
+/* Same fragments with the interleaved K order (lane l holds
+ * k = 32*ks + 16*(e/4) + 4*(l/16) + e%4), the input order of the fc1 / fc2
+ * weights of shrimp_attn_mlp. */
+int shrimp_pack_linear_weight_il(const float* w, void* packed, int in_features, int out_features,
+                                 void* stream);
 
 /* ------------------------------------------------------------------------
  * Gather-GEMM hex / ray-tap convolution with fused epilogue.
@@ -142,6 +158,40 @@ typedef struct {
 } shrimp_linear_args;
 
 int shrimp_linear(const shrimp_linear_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused attention-block tail (AttnBlock.forward after the attention core,
+ * model.py:508-514; replaces the out_proj / fc1 / fc2 nn.Linear calls and
+ * the two LayerScale residuals):
+ *   s1  = bf16(seq + g_attn * (mask ? x @ Wo^T + bo : 0))
+ *   h   = bf16(gelu_erf(LN2(s1) @ W1^T + b1))
+ *   seq = bf16(s1 + g_mlp * (mask ? h @ W2^T + b2 : 0))        (in place)
+ * x: attention output rows (bf16), seq: residual stream rows (bf16), both
+ * with element row strides; mask: per-row live flag. out_w packed in the
+ * standard order, fc1_w / fc2_w in the interleaved order. C = 128, hidden =
+ * 256 (the whole weight set is held in one workgroup's LDS).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* x;
+  int64_t x_sr;
+  void* seq;
+  int64_t s_sr;
+  const uint8_t* mask; /* (rows) */
+  const void* out_w;   /* packed (C -> C), standard order */
+  const float* out_b;
+  const float* g_attn; /* LayerScale after attention (C) */
+  const float* ln_w;   /* LN2 (C) */
+  const float* ln_b;
+  float eps;
+  const void* fc1_w;   /* packed (C -> hidden), interleaved order */
+  const float* fc1_b;
+  const void* fc2_w;   /* packed (hidden -> C), interleaved order */
+  const float* fc2_b;
+  const float* g_mlp;  /* LayerScale after the MLP (C) */
+  int32_t rows, C, hidden;
+} shrimp_mlp_args;
+
+int shrimp_attn_mlp(const shrimp_mlp_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
  * Fused relative-position-biased, key-masked attention (online softmax).

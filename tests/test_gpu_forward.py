@@ -100,6 +100,25 @@ def test_linear_and_clamped_bias_paths_agree(cfg4_batch):
         assert (lin[key] - clamp[key]).abs().max().item() <= 1e-2, key
 
 
+def test_fused_and_unfused_mlp_paths_agree(cfg4_batch):
+    """The fused attention-block MLP kernel and the three separate linear
+    kernels give the same forward up to fp32 summation order and the GELU's
+    erf evaluation (|error| <= 1.5e-7)."""
+
+    b = cfg4_batch
+    net = _net(128, 8, "CCACCACCACCA", seed=5)
+    fused = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+    net.hip_runtime().use_fused_mlp = False
+    try:
+        plain = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+    finally:
+        net.hip_runtime().use_fused_mlp = True
+    for key in ("policy", "value", "moves_left"):
+        err = (fused[key] - plain[key]).abs().max().item()
+        print(f"fused vs unfused {key}: {err:.3e}", flush=True)
+        assert err <= 1e-2, key
+
+
 def test_rows_are_independent_of_batch(cfg4_batch):
     """padded == single-row (tests/test_shrimp_model.py:139-164): a row's
     outputs do not depend on the rest of the batch (bit-exact here)."""

@@ -32,6 +32,22 @@ def close(got, want, atol=2e-2, rtol=1e-2, what=""):
     assert worst <= atol, f"{what}: max excess error {worst}"
 
 
+@pytest.fixture(params=[0, 1, 2, 3], ids=["auto", "global", "staged", "bigtile"])
+def conv_variant(request):
+    """Runs a conv test with the automatic kernel choice, with the
+    global-gather kernel forced, with the LDS-staged kernel forced and with
+    the big-tile staged kernel (128 -> 128 channels, 7 taps) selected."""
+
+    from shrimp import _lib
+
+    lib = _lib.load()
+    prev = lib.shrimp_conv_variant(request.param)
+    try:
+        yield request.param
+    finally:
+        lib.shrimp_conv_variant(prev)
+
+
 @pytest.fixture(scope="module")
 def conv_case():
     from shrimp import synthetic
@@ -44,7 +60,7 @@ def _gidx(batch):
 
 
 @pytest.mark.parametrize("epi", ["plain", "ln_relu", "ln"])
-def test_hex_conv_ops(conv_case, epi):
+def test_hex_conv_ops(conv_case, epi, conv_variant):
     torch.manual_seed(0)
     b = conv_case["batch"]
     x = torch.from_numpy(conv_case["x"])
@@ -71,7 +87,7 @@ def test_hex_conv_ops(conv_case, epi):
 
 
 @pytest.mark.parametrize("c", [32, 64, 96, 192, 256])
-def test_hex_conv_widths(c):
+def test_hex_conv_widths(c, conv_variant):
     from shrimp import synthetic
 
     case = synthetic.conv_inputs(2, channels=c)
@@ -83,7 +99,7 @@ def test_hex_conv_widths(c):
     close(got, want, what=f"C={c}")
 
 
-def test_conv_residual_and_head_epilogues(conv_case):
+def test_conv_residual_and_head_epilogues(conv_case, conv_variant):
     from shrimp import ops
 
     b = conv_case["batch"]
@@ -126,6 +142,63 @@ def test_conv_residual_and_head_epilogues(conv_case):
     assert (head.cpu()[~mask] == 0).all()
 
 
+@pytest.mark.parametrize("c", [32, 128])
+def test_hex_conv_multi_tile_positions(c, conv_variant):
+    """Spec-variant positions (Npad = ceil64(max N) > 256: several row tiles
+    per position in the staged kernel, N not a multiple of the tile)."""
+
+    from shrimp import synthetic
+
+    b = synthetic.position_batch("cfg4_spec", 3, seed=11)
+    B, N = b["mask"].shape
+    assert N > 256
+    rng = np.random.default_rng(5)
+    x = torch.from_numpy(rng.standard_normal((B, N, c), dtype=np.float32))
+    w = torch.from_numpy(rng.standard_normal((7, c, 128), dtype=np.float32) / np.sqrt(7 * c))
+    bias = torch.from_numpy(rng.standard_normal(128, dtype=np.float32) * 0.02)
+    gidx = _gidx(b)
+    got = torch.ops.shrimp.hex_conv(x.to(DEV), gidx.to(DEV), b["mask"].to(DEV), w.to(DEV), bias.to(DEV))
+    want = ofwd.hex_conv(bf(x), gidx, b["mask"], bf(w), bias.double())
+    close(got, want, what=f"N={N} C={c}")
+
+
+def test_conv_variants_agree_at_full_shape():
+    """At config 1's real shape (B=512, Npad=256): the global-gather and the
+    staged kernels issue the same MFMA sequence on the same operands
+    (bit-identical outputs); the big-tile kernel sums the same products in
+    another order (channel chunk before tap), so it agrees to fp32 rounding:
+    at most one bf16 ulp on a few elements."""
+
+    from shrimp import _lib, synthetic
+
+    case = synthetic.conv_inputs(512, channels=128)
+    b = case["batch"]
+    x, w, bias = (torch.from_numpy(case[k]).to(DEV) for k in ("x", "w", "bias"))
+    gidx, mask = _gidx(b).to(DEV), b["mask"].to(DEV)
+    lnw = torch.rand(128, device=DEV) + 0.5
+    lnb = torch.randn(128, device=DEV) * 0.1
+    lib = _lib.load()
+    outs = []
+    for v in (3, 1, 2):
+        prev = lib.shrimp_conv_variant(v)
+        try:
+            outs.append(torch.ops.shrimp.hex_conv_ln(x, gidx, mask, w, bias, lnw, lnb, 1e-5, True))
+        finally:
+            lib.shrimp_conv_variant(prev)
+    assert torch.equal(outs[1], outs[2])
+    a, c = outs[0].float(), outs[1].float()
+    diff = (a - c).abs()
+    # one bf16 ulp of the larger value, plus 1e-5 absolute for outputs at the
+    # ReLU edge (fp32 reordering moves the LayerNorm output by ~1e-6 there)
+    ulp = torch.maximum(a.abs(), c.abs()) * 2.0 ** -7 + 1e-5
+    frac = (diff > 0).float().mean().item()
+    print(f"big-tile vs global: max diff {diff.max().item():.3e}, {frac:.4f} of outputs differ, "
+          f"worst / allowed {(diff / ulp).max().item():.3f}", flush=True)
+    assert (diff <= ulp).all()
+    assert frac < 0.05
+    print(f"max LDS per block: {lib.shrimp_max_lds_per_block()} bytes", flush=True)
+
+
 def test_prep_pair_and_ray_index_exact(golden):
     from shrimp import _lib
 
@@ -166,7 +239,7 @@ def test_prep_pair_and_ray_index_exact(golden):
     np.testing.assert_array_equal(ridx.cpu().numpy(), golden("ray_index")["idx"])
 
 
-def test_raytap_conv_31_taps():
+def test_raytap_conv_31_taps(conv_variant):
     from shrimp import _lib, ops, synthetic
 
     case = synthetic.raytap_inputs(4, channels=128)
@@ -243,6 +316,45 @@ def test_linear_modes(mode, c):
         out = torch.empty(rows, n_out, dtype=torch.bfloat16, device=DEV)
         ops.launch_linear(mode=_lib.LIN_PLAIN, out=out, o_sr=n_out, **kw)
         close(out, y, what="plain")
+
+
+@pytest.mark.parametrize("rows", [1, 37, 4096 + 5])
+def test_attn_mlp_fused(rows):
+    """Fused out_proj + LayerScale residual + LN2 + fc1 + GELU(erf) + fc2 +
+    residual (C=128) against a float64 restatement with the kernel's bf16
+    rounding points (s1 and the hidden layer stored as bf16). Row counts
+    cover a single row, a ragged block and several blocks per wave."""
+
+    from shrimp import ops
+
+    torch.manual_seed(2)
+    c, hdim = 128, 256
+    x = torch.randn(rows, c)
+    seq = torch.randn(rows, c)
+    m = torch.rand(rows) > 0.25
+    wo, bo = torch.randn(c, c) * 0.08, torch.randn(c) * 0.1
+    w1, b1 = torch.randn(hdim, c) * 0.08, torch.randn(hdim) * 0.1
+    w2, b2 = torch.randn(c, hdim) * 0.06, torch.randn(c) * 0.1
+    ga, gm = torch.rand(c) * 0.5 + 0.25, torch.rand(c) * 0.5 + 0.25
+    lnw, lnb = torch.rand(c) + 0.5, torch.randn(c) * 0.1
+
+    s1 = bf(bf(seq) + ga.double() * ((bf(x) @ bf(wo).T + bo.double()) * m.double()[:, None]))
+    hn = bf(torch.nn.functional.layer_norm(s1, (c,), lnw.double(), lnb.double(), 1e-5))
+    hid = bf(torch.nn.functional.gelu(hn @ bf(w1).T + b1.double()))
+    want = s1 + gm.double() * ((hid @ bf(w2).T + b2.double()) * m.double()[:, None])
+
+    seq_d = seq.to(DEV, torch.bfloat16).contiguous()
+    ops.launch_attn_mlp(
+        x=x.to(DEV, torch.bfloat16).contiguous(), x_sr=c, seq=seq_d, s_sr=c,
+        mask=m.to(DEV, torch.uint8), out_w=ops.pack_linear_weight(wo.to(DEV)), out_b=bo.to(DEV),
+        g_attn=ga.to(DEV), ln_w=lnw.to(DEV), ln_b=lnb.to(DEV), eps=1e-5,
+        fc1_w=ops.pack_linear_weight(w1.to(DEV), True), fc1_b=b1.to(DEV),
+        fc2_w=ops.pack_linear_weight(w2.to(DEV), True), fc2_b=b2.to(DEV), g_mlp=gm.to(DEV),
+        rows=rows, C=c, hidden=hdim,
+    )
+    close(seq_d, want, what=f"attn_mlp rows={rows}")
+    # masked rows keep their residual exactly (bf16 of seq)
+    assert torch.equal(seq_d.cpu()[~m].double(), bf(seq)[~m])
 
 
 @pytest.mark.parametrize("d", [16, 32, 64])
