@@ -108,10 +108,8 @@ def kernel_timings(net, inputs, reps=50):
     if P.fused_mlp:
         linears["attn_mlp"] = (
             lambda: ops.launch_attn_mlp(
-                x=L["att"], x_sr=C, seq=seq_copy, s_sr=C, mask=L["seq_mask"], out_w=a.out_w,
-                out_b=a.out_b, g_attn=a.g_attn, ln_w=a.ln2w, ln_b=a.ln2b, eps=a.eps2,
-                fc1_w=a.fc1_w_il, fc1_b=a.fc1_b, fc2_w=a.fc2_w_il, fc2_b=a.fc2_b, g_mlp=a.g_mlp,
-                rows=rows, C=C, hidden=2 * C, stream=L["stream"]),
+                x=L["att"], x_sr=C, seq=seq_copy, s_sr=C, mask=L["seq_mask"], packed=a.mlp,
+                eps=a.eps2, rows=rows, C=C, hidden=2 * C, stream=L["stream"]),
             rows * (C * C + 4 * C * C) * 2.0, rows * 3 * C * 2.0)
     else:
         hid = L["hid"]

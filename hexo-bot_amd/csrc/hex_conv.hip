@@ -551,9 +551,9 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
 // Fragment f = (ks * NB + nb) * 64 + lane holds 8 bf16, element e:
 //   W[k][n = 16*nb + lane%16] with
 //   k = 32*ks + 8*(lane/16) + e                    (standard order), or
-//   k = 32*ks + 16*(e/4) + 4*(lane/16) + e%4       (interleaved order: the
-//       K-slice a lane holds is the 4 + 4 channels it owns in the output
-//       fragments of the previous 16x16 MFMA product),
+//   k = 32*ks + 16*(e/4) + 4*(lane/16) + e%4       (interleaved order, used by
+//       the fused MLP: the K-slice a lane holds is the 4 + 4 channels it owns
+//       in the output fragments of the previous 16x16 MFMA product),
 // and for convolutions k = t*cin_pad + c.
 __global__ void pack_weight_kernel(const float* __restrict__ src, unsigned short* __restrict__ dst,
                                    int K, int NOUT, int cin, int cin_pad, int64_t s_t,
@@ -678,11 +678,6 @@ static int pack_linear(const float* w, void* packed, int in_features, int out_fe
 extern "C" int shrimp_pack_linear_weight(const float* w, void* packed, int in_features,
                                          int out_features, void* stream) {
   return pack_linear(w, packed, in_features, out_features, stream, 0);
-}
-
-extern "C" int shrimp_pack_linear_weight_il(const float* w, void* packed, int in_features,
-                                            int out_features, void* stream) {
-  return pack_linear(w, packed, in_features, out_features, stream, 1);
 }
 
 extern "C" int shrimp_hex_conv(const shrimp_conv_args* a, void* stream) {

@@ -5,16 +5,26 @@
 //   h   = GELU_erf(LN2(s1) . W1^T + b1)                   (fc1, hidden 2C)
 //   seq = s1 + g_mlp * (m * (h . W2^T + b2))              (fc2, LayerScale)
 //
-// with s1 and h rounded to bf16 where the unfused kernels store them.
+// The per-channel factors are folded into the weights once, at pack time
+// (shrimp_pack_attn_mlp):
+//   Wo' = diag(g_attn) Wo,  bo' = g_attn * bo
+//   W1' = W1 diag(ln_w),    b1' = b1 + W1 ln_b
+//   W2' = diag(g_mlp) W2,   b2' = g_mlp * b2
+// so per row the kernel computes
+//   s1 = seq + (att . Wo'^T + bo'),  n = (s1 - mean) * rstd,
+//   h = GELU(n . W1'^T + b1'),       seq = bf16(s1) + (h . W2'^T + b2')
+// with n and h in bf16 as MFMA inputs. Rows with m = 0 are left untouched
+// (their updates are multiplied by 0), so the math runs unmasked and only
+// live rows store.
 //
-// Layout: one persistent workgroup per CU keeps the three packed weight
-// matrices in LDS (C = 128: 32 + 64 + 64 KiB = the whole 160 KiB), and each
-// of its 8 waves streams blocks of 16 rows through the three products without
-// leaving registers: a product's output fragment (lane l: channels
+// Layout: one persistent workgroup per CU keeps the packed fragments of the
+// three matrices in LDS (C = 128: 32 + 64 + 64 KiB = the whole 160 KiB); each
+// of its 12 waves streams blocks of 16 rows through the three products
+// without leaving registers: a product's output fragment (lane l: channels
 // 16 nb + 4 (l/16) + j of row l % 16) is directly the next product's input
-// fragment for K-step ks = nb / 2, because fc1 and fc2 are packed with that
-// interleaved K order (shrimp_pack_linear_weight_il). Only att and seq touch
-// HBM: 3 x 256 bytes per row.
+// fragment for K-step nb / 2, because W1' and W2' are packed with that
+// interleaved K order. The biases enter as the accumulators' initial values.
+// Only att and seq touch HBM: 3 x 256 bytes per row.
 #include <algorithm>
 
 #include "capi.hpp"
@@ -22,20 +32,30 @@
 
 namespace shrimp {
 
+// Weight fragment packer shared with the conv / linear packers (hex_conv.hip).
+__global__ void pack_weight_kernel(const float* __restrict__ src, unsigned short* __restrict__ dst,
+                                   int K, int NOUT, int cin, int cin_pad, int64_t s_t,
+                                   int64_t s_c, int64_t s_n, int interleaved);
+
 namespace {
 
 constexpr int MC = 128;           // channels
 constexpr int MH = 2 * MC;        // hidden width
-constexpr int MWAVES = 8;         // waves per workgroup (2 per SIMD)
+constexpr int MWAVES = 12;        // waves per workgroup (3 per SIMD)
 constexpr uint32_t WO_OFF = 0;                        // out_proj fragments
 constexpr uint32_t W1_OFF = MC * MC * 2;              // fc1 fragments
 constexpr uint32_t W2_OFF = W1_OFF + MC * MH * 2;     // fc2 fragments
 constexpr uint32_t W_LDS = W2_OFF + MH * MC * 2;      // 163840 bytes
+constexpr uint32_t BO_OFF = W_LDS;                    // folded biases (fp32) after the fragments
+constexpr uint32_t B1_OFF = BO_OFF + MC * 4;
+constexpr uint32_t B2_OFF = B1_OFF + MH * 4;
+constexpr uint32_t PACK_BYTES = B2_OFF + MC * 4;
 
 // GELU with erf from Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7 on erf):
 //   erfc(z) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2),
-//   t = 1 / (1 + p z), z = |x| / sqrt(2) >= 0,
-// GELU(x) = x * Phi(x), Phi(x) = 1 - erfc(z) / 2 for x >= 0, erfc(z) / 2 else.
+//   t = 1 / (1 + p z), z = |x| / sqrt(2) >= 0.
+// With h = erfc(z) / 2: GELU(x) = x (1 - h) for x >= 0 and x h for x < 0,
+// i.e. GELU(x) = max(x, 0) - |x| h.
 SHRIMP_DEV float gelu_as(float x) {
   constexpr float p = 0.3275911f * 0.70710678118654752f;  // p / sqrt(2), applied to |x|
   constexpr float a1 = 0.5f * 0.254829592f, a2 = 0.5f * -0.284496736f, a3 = 0.5f * 1.421413741f;
@@ -47,10 +67,8 @@ SHRIMP_DEV float gelu_as(float x) {
   q = fmaf(q, t, a3);
   q = fmaf(q, t, a2);
   q = fmaf(q, t, a1);
-  q *= t;                                                  // erfc(z) / 2 before the exp factor
-  const float h = q * __builtin_amdgcn_exp2f(nh * (x * x));  // erfc(z) / 2
-  const float phi = x >= 0.f ? 1.0f - h : h;
-  return x * phi;
+  const float h = (q * t) * __builtin_amdgcn_exp2f(nh * (x * x));  // erfc(z) / 2
+  return fmaf(-ax, h, fmaxf(x, 0.f));
 }
 
 SHRIMP_DEV u32x4 lds_frag(const unsigned char* wl, uint32_t base, int ks, int nb, int nbt,
@@ -58,50 +76,40 @@ SHRIMP_DEV u32x4 lds_frag(const unsigned char* wl, uint32_t base, int ks, int nb
   return *reinterpret_cast<const u32x4*>(wl + base + (uint32_t)(((ks * nbt + nb) * 64 + lane) * 16));
 }
 
-template <int MB>
-SHRIMP_DEV void mlp_rows(const shrimp_mlp_args& a, const unsigned char* wl,
-                         __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t sr, int row0,
-                         int lane) {
-  constexpr int KS1 = MC / 32, NB1 = MC / 16, NBH = MH / 16, KT = MH / 32, NB2 = MC / 16;
-  const int lr = lane & 15, lg = lane >> 4;
-  const float* __restrict__ ob = a.out_b;
-  const float* __restrict__ ga = a.g_attn;
-  const float* __restrict__ lw = a.ln_w;
-  const float* __restrict__ lb = a.ln_b;
-  const float* __restrict__ b1 = a.fc1_b;
-  const float* __restrict__ b2 = a.fc2_b;
-  const float* __restrict__ gm = a.g_mlp;
+// Attention-output fragments (out_proj input) of one 16-row block; rows at
+// or past `rows` read as zeros.
+SHRIMP_DEV void load_x(const shrimp_mlp_args& a, __amdgpu_buffer_rsrc_t xr, int row, int lg,
+                       u32x4 (&xf)[MC / 32]) {
+  const uint32_t xo =
+      row < a.rows ? (uint32_t)((int64_t)row * a.x_sr * 2) + (uint32_t)(lg * 16) : SHRIMP_OOB_OFFSET;
+#pragma unroll
+  for (int ks = 0; ks < MC / 32; ++ks) xf[ks] = buf_load16(xr, xo + ks * 64);
+}
 
-  int r[MB];
-  bool rv[MB];
-  float live[MB];
-  u32x4 xf[MB][KS1];
+// One block of 16 rows (lane: row lane % 16, channel group lane / 16).
+SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, const float* bias,
+                          __amdgpu_buffer_rsrc_t sr, const u32x4 (&xf)[MC / 32], int row,
+                          int lane) {
+  constexpr int KS1 = MC / 32, NB1 = MC / 16, NBH = MH / 16, KT = MH / 32, NB2 = MC / 16;
+  const int lg = lane >> 4;
+  const bool store = row < a.rows && a.mask[row] != 0;
+  const float* bo = bias;
+  const float* b1 = bias + MC;
+  const float* b2 = bias + MC + MH;
+
+  // accumulators start at the biases; residual rows (bf16) requested alongside
+  f32x4 acc[NB1];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    r[mb] = row0 + mb * 16 + lr;
-    rv[mb] = r[mb] < a.rows;
-    const uint32_t off = rv[mb] ? (uint32_t)((int64_t)r[mb] * a.x_sr * 2) + (uint32_t)(lg * 16)
-                                : SHRIMP_OOB_OFFSET;
+  for (int nb = 0; nb < NB1; ++nb) acc[nb] = *reinterpret_cast<const f32x4*>(bo + nb * 16 + lg * 4);
+  u32x2 sin[NB1];
+  {
+    const uint32_t so =
+        row < a.rows ? (uint32_t)((int64_t)row * a.s_sr * 2) + (uint32_t)(lg * 8) : SHRIMP_OOB_OFFSET;
 #pragma unroll
-    for (int ks = 0; ks < KS1; ++ks) xf[mb][ks] = buf_load16(xr, off + ks * 64);
-  }
-  // residual rows (bf16, 4 channels per 16-channel block)
-  u32x2 sp[MB][NB1];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    live[mb] = (rv[mb] && a.mask[r[mb]] != 0) ? 1.f : 0.f;
-    const uint32_t off = rv[mb] ? (uint32_t)((int64_t)r[mb] * a.s_sr * 2) + (uint32_t)(lg * 8)
-                                : SHRIMP_OOB_OFFSET;
-#pragma unroll
-    for (int nb = 0; nb < NB1; ++nb) sp[mb][nb] = buf_load8(sr, off + nb * 32);
+    for (int nb = 0; nb < NB1; ++nb) sin[nb] = buf_load8(sr, so + nb * 32);
   }
 
   // ---- out_proj ----------------------------------------------------------
-  f32x4 acc[MB][NB1];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NB1; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
   // (scheduling barriers keep the weight-fragment reads next to their MFMAs;
   // hoisted all at once they would not fit in registers)
 #pragma unroll
@@ -110,120 +118,101 @@ SHRIMP_DEV void mlp_rows(const shrimp_mlp_args& a, const unsigned char* wl,
 #pragma unroll
     for (int ks = 0; ks < KS1; ++ks) w[ks] = lds_frag(wl, WO_OFF, ks, nb, NB1, lane);
 #pragma unroll
-    for (int ks = 0; ks < KS1; ++ks)
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[mb][nb] = mfma16x16x32(w[ks], xf[mb][ks], acc[mb][nb]);
+    for (int ks = 0; ks < KS1; ++ks) acc[nb] = mfma16x16x32(w[ks], xf[ks], acc[nb]);
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // ---- residual 1 (bf16 s1), LayerNorm 2 -> fc1 input fragments ------------
-  u32x4 hf[MB][KS1];
+  // ---- residual 1, LayerNorm 2 (affine folded into W1', b1') ---------------
+  // s1 is kept as bf16 for the second residual; LayerNorm reads its fp32 value.
+  u32x2 sp[NB1];
+  float v[NB1][4];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    float v[NB1][4];
-#pragma unroll
-    for (int nb = 0; nb < NB1; ++nb) {
-      __builtin_amdgcn_sched_barrier(0);
-      const int c = nb * 16 + lg * 4;
-      const f32x4 bb = *reinterpret_cast<const f32x4*>(ob + c);
-      const f32x4 g = *reinterpret_cast<const f32x4*>(ga + c);
-      const float o0 = bf16_lo(sp[mb][nb].x) + g[0] * (live[mb] * (acc[mb][nb][0] + bb[0]));
-      const float o1 = bf16_hi(sp[mb][nb].x) + g[1] * (live[mb] * (acc[mb][nb][1] + bb[1]));
-      const float o2 = bf16_lo(sp[mb][nb].y) + g[2] * (live[mb] * (acc[mb][nb][2] + bb[2]));
-      const float o3 = bf16_hi(sp[mb][nb].y) + g[3] * (live[mb] * (acc[mb][nb][3] + bb[3]));
-      sp[mb][nb].x = pack_bf16x2(o0, o1);
-      sp[mb][nb].y = pack_bf16x2(o2, o3);
-      v[nb][0] = bf16_lo(sp[mb][nb].x);
-      v[nb][1] = bf16_hi(sp[mb][nb].x);
-      v[nb][2] = bf16_lo(sp[mb][nb].y);
-      v[nb][3] = bf16_hi(sp[mb][nb].y);
-    }
-    float s = 0.f;
-#pragma unroll
-    for (int nb = 0; nb < NB1; ++nb)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s += v[nb][j];
-    const float mean = sum_groups_swap(s) * (1.0f / MC);
-    float q = 0.f;
-#pragma unroll
-    for (int nb = 0; nb < NB1; ++nb)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[nb][j] -= mean;
-        q += v[nb][j] * v[nb][j];
-      }
-    const float rstd = rsqrtf(sum_groups_swap(q) * (1.0f / MC) + a.eps);
-    unsigned hp[NB1][2];
-#pragma unroll
-    for (int nb = 0; nb < NB1; ++nb) {
-      __builtin_amdgcn_sched_barrier(0);
-      const int c = nb * 16 + lg * 4;
-      const f32x4 gw = *reinterpret_cast<const f32x4*>(lw + c);
-      const f32x4 gb = *reinterpret_cast<const f32x4*>(lb + c);
-      hp[nb][0] = pack_bf16x2(v[nb][0] * rstd * gw[0] + gb[0], v[nb][1] * rstd * gw[1] + gb[1]);
-      hp[nb][1] = pack_bf16x2(v[nb][2] * rstd * gw[2] + gb[2], v[nb][3] * rstd * gw[3] + gb[3]);
-    }
-#pragma unroll
-    for (int ks = 0; ks < KS1; ++ks)
-      hf[mb][ks] = u32x4{hp[2 * ks][0], hp[2 * ks][1], hp[2 * ks + 1][0], hp[2 * ks + 1][1]};
+  for (int nb = 0; nb < NB1; ++nb) {
+    v[nb][0] = acc[nb][0] + bf16_lo(sin[nb].x);
+    v[nb][1] = acc[nb][1] + bf16_hi(sin[nb].x);
+    v[nb][2] = acc[nb][2] + bf16_lo(sin[nb].y);
+    v[nb][3] = acc[nb][3] + bf16_hi(sin[nb].y);
+    sp[nb].x = pack_bf16x2(v[nb][0], v[nb][1]);
+    sp[nb].y = pack_bf16x2(v[nb][2], v[nb][3]);
   }
+  float s = 0.f;
+#pragma unroll
+  for (int nb = 0; nb < NB1; ++nb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s += v[nb][j];
+  const float mean = sum_groups_swap(s) * (1.0f / MC);
+  float q = 0.f;
+#pragma unroll
+  for (int nb = 0; nb < NB1; ++nb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[nb][j] -= mean;
+      q = fmaf(v[nb][j], v[nb][j], q);
+    }
+  const float rstd = rsqrtf(sum_groups_swap(q) * (1.0f / MC) + a.eps);
+  u32x4 hf[KS1];
+#pragma unroll
+  for (int ks = 0; ks < KS1; ++ks) {
+    const int n0 = 2 * ks, n1 = 2 * ks + 1;
+    hf[ks] = u32x4{pack_bf16x2(v[n0][0] * rstd, v[n0][1] * rstd),
+                   pack_bf16x2(v[n0][2] * rstd, v[n0][3] * rstd),
+                   pack_bf16x2(v[n1][0] * rstd, v[n1][1] * rstd),
+                   pack_bf16x2(v[n1][2] * rstd, v[n1][3] * rstd)};
+  }
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- fc1 -> GELU -> fc2, one 32-wide hidden slice at a time ---------------
-  f32x4 acc2[MB][NB2];
+  f32x4 acc2[NB2];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+  for (int nb = 0; nb < NB2; ++nb) acc2[nb] = *reinterpret_cast<const f32x4*>(b2 + nb * 16 + lg * 4);
+  f32x4 bh[2];
 #pragma unroll
-    for (int nb = 0; nb < NB2; ++nb) acc2[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
+  for (int hh = 0; hh < 2; ++hh) bh[hh] = *reinterpret_cast<const f32x4*>(b1 + hh * 16 + lg * 4);
+#pragma unroll
   for (int kt = 0; kt < KT; ++kt) {
-    f32x4 ah[MB][2];
+    f32x4 ah[2];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) ah[mb][0] = ah[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int hh = 0; hh < 2; ++hh) {
+      u32x4 w[KS1];
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
+      for (int ks = 0; ks < KS1; ++ks) w[ks] = lds_frag(wl, W1_OFF, ks, 2 * kt + hh, NBH, lane);
+      ah[hh] = bh[hh];
 #pragma unroll
-      for (int ks = 0; ks < KS1; ++ks) {
-        const u32x4 w = lds_frag(wl, W1_OFF, ks, 2 * kt + hh, NBH, lane);
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) ah[mb][hh] = mfma16x16x32(w, hf[mb][ks], ah[mb][hh]);
-      }
-    const f32x4 bh0 = *reinterpret_cast<const f32x4*>(b1 + (2 * kt) * 16 + lg * 4);
-    const f32x4 bh1 = *reinterpret_cast<const f32x4*>(b1 + (2 * kt + 1) * 16 + lg * 4);
-    u32x4 gf[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      gf[mb][0] = pack_bf16x2(gelu_as(ah[mb][0][0] + bh0[0]), gelu_as(ah[mb][0][1] + bh0[1]));
-      gf[mb][1] = pack_bf16x2(gelu_as(ah[mb][0][2] + bh0[2]), gelu_as(ah[mb][0][3] + bh0[3]));
-      gf[mb][2] = pack_bf16x2(gelu_as(ah[mb][1][0] + bh1[0]), gelu_as(ah[mb][1][1] + bh1[1]));
-      gf[mb][3] = pack_bf16x2(gelu_as(ah[mb][1][2] + bh1[2]), gelu_as(ah[mb][1][3] + bh1[3]));
+      for (int ks = 0; ks < KS1; ++ks) ah[hh] = mfma16x16x32(w[ks], hf[ks], ah[hh]);
     }
+    // next slice's fc1 biases; fc2 fragments in two halves, the first half's
+    // LDS reads overlapping the GELU
+    if (kt + 1 < KT) {
 #pragma unroll
-    for (int nb = 0; nb < NB2; ++nb) {
-      const u32x4 w = lds_frag(wl, W2_OFF, kt, nb, NB2, lane);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc2[mb][nb] = mfma16x16x32(w, gf[mb], acc2[mb][nb]);
+      for (int hh = 0; hh < 2; ++hh)
+        bh[hh] = *reinterpret_cast<const f32x4*>(b1 + (2 * kt + 2 + hh) * 16 + lg * 4);
     }
+    u32x4 w2[NB2 / 2];
+#pragma unroll
+    for (int nb = 0; nb < NB2 / 2; ++nb) w2[nb] = lds_frag(wl, W2_OFF, kt, nb, NB2, lane);
+    u32x4 gf;
+    gf[0] = pack_bf16x2(gelu_as(ah[0][0]), gelu_as(ah[0][1]));
+    gf[1] = pack_bf16x2(gelu_as(ah[0][2]), gelu_as(ah[0][3]));
+    gf[2] = pack_bf16x2(gelu_as(ah[1][0]), gelu_as(ah[1][1]));
+    gf[3] = pack_bf16x2(gelu_as(ah[1][2]), gelu_as(ah[1][3]));
+#pragma unroll
+    for (int nb = 0; nb < NB2 / 2; ++nb) acc2[nb] = mfma16x16x32(w2[nb], gf, acc2[nb]);
+#pragma unroll
+    for (int nb = 0; nb < NB2 / 2; ++nb) w2[nb] = lds_frag(wl, W2_OFF, kt, NB2 / 2 + nb, NB2, lane);
+#pragma unroll
+    for (int nb = 0; nb < NB2 / 2; ++nb)
+      acc2[NB2 / 2 + nb] = mfma16x16x32(w2[nb], gf, acc2[NB2 / 2 + nb]);
     __builtin_amdgcn_sched_barrier(0);
   }
 
   // ---- residual 2 -> seq ----------------------------------------------------
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    if (!rv[mb]) continue;
-    unsigned short* op = static_cast<unsigned short*>(a.seq) + (int64_t)r[mb] * a.s_sr + lg * 4;
+  if (store) {
+    unsigned short* op = static_cast<unsigned short*>(a.seq) + (int64_t)row * a.s_sr + lg * 4;
 #pragma unroll
     for (int nb = 0; nb < NB2; ++nb) {
-      __builtin_amdgcn_sched_barrier(0);
-      const int c = nb * 16 + lg * 4;
-      const f32x4 bb = *reinterpret_cast<const f32x4*>(b2 + c);
-      const f32x4 g = *reinterpret_cast<const f32x4*>(gm + c);
-      const float o0 = bf16_lo(sp[mb][nb].x) + g[0] * (live[mb] * (acc2[mb][nb][0] + bb[0]));
-      const float o1 = bf16_hi(sp[mb][nb].x) + g[1] * (live[mb] * (acc2[mb][nb][1] + bb[1]));
-      const float o2 = bf16_lo(sp[mb][nb].y) + g[2] * (live[mb] * (acc2[mb][nb][2] + bb[2]));
-      const float o3 = bf16_hi(sp[mb][nb].y) + g[3] * (live[mb] * (acc2[mb][nb][3] + bb[3]));
       u32x2 pk;
-      pk.x = pack_bf16x2(o0, o1);
-      pk.y = pack_bf16x2(o2, o3);
+      pk.x = pack_bf16x2(acc2[nb][0] + bf16_lo(sp[nb].x), acc2[nb][1] + bf16_hi(sp[nb].x));
+      pk.y = pack_bf16x2(acc2[nb][2] + bf16_lo(sp[nb].y), acc2[nb][3] + bf16_hi(sp[nb].y));
       *reinterpret_cast<u32x2*>(op + nb * 16) = pk;
     }
   }
@@ -238,42 +227,112 @@ __global__ __launch_bounds__(MWAVES * 64, 1) void attn_mlp_kernel(const shrimp_m
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
 
-  // All three weight matrices into LDS (16-byte chunks, fragment order kept).
+  // The packed fragments of all three matrices into LDS (16-byte chunks).
   {
-    const __amdgpu_buffer_rsrc_t r0 = make_rsrc(a.out_w, W1_OFF);
-    const __amdgpu_buffer_rsrc_t r1 = make_rsrc(a.fc1_w, W2_OFF - W1_OFF);
-    const __amdgpu_buffer_rsrc_t r2 = make_rsrc(a.fc2_w, W_LDS - W2_OFF);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.packed, W_LDS);
     constexpr int CHUNKS = W_LDS / 16;
-    constexpr int PER = CHUNKS / (MWAVES * 64);
-    static_assert(CHUNKS % (MWAVES * 64) == 0, "weight chunks must tile the workgroup");
+    constexpr int PER = (CHUNKS + MWAVES * 64 - 1) / (MWAVES * 64);
     u32x4 v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) v[i] = buf_load16(wr, (uint32_t)(i * MWAVES * 64 + threadIdx.x) * 16);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const uint32_t off = (uint32_t)(i * MWAVES * 64 + threadIdx.x) * 16;
-      v[i] = off < W1_OFF ? buf_load16(r0, off)
-                          : (off < W2_OFF ? buf_load16(r1, off - W1_OFF) : buf_load16(r2, off - W2_OFF));
+      if (off < W_LDS) *reinterpret_cast<u32x4*>(wl + off) = v[i];
     }
-#pragma unroll
-    for (int i = 0; i < PER; ++i)
-      *reinterpret_cast<u32x4*>(wl + (uint32_t)(i * MWAVES * 64 + threadIdx.x) * 16) = v[i];
   }
   __syncthreads();
 
+  const float* bias = reinterpret_cast<const float*>(static_cast<const unsigned char*>(a.packed) + BO_OFF);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes);
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.seq, s_bytes);
-  // Contiguous, balanced range of 16-row blocks per wave.
+  // Contiguous, balanced range of 16-row blocks per wave; the next block's
+  // attention rows are requested before the current block's math.
   const int64_t nblk = (a.rows + 15) / 16;
   const int64_t tw = (int64_t)gridDim.x * MWAVES;
   const int64_t gw = (int64_t)blockIdx.x * MWAVES + wave;
-  int blk = (int)(gw * nblk / tw);
+  const int begin = (int)(gw * nblk / tw);
   const int end = (int)((gw + 1) * nblk / tw);
-  for (; blk + 2 <= end; blk += 2) mlp_rows<2>(a, wl, xr, sr, blk * 16, lane);
-  if (blk < end) mlp_rows<1>(a, wl, xr, sr, blk * 16, lane);
+  const int lr = lane & 15, lg = lane >> 4;
+  u32x4 cur[MC / 32], nxt[MC / 32];
+  if (begin < end) load_x(a, xr, begin * 16 + lr, lg, nxt);
+  for (int blk = begin; blk < end; ++blk) {
+#pragma unroll
+    for (int ks = 0; ks < MC / 32; ++ks) cur[ks] = nxt[ks];
+    // rows past this wave's range read as zeros (offset past the resource)
+    const int nrow = blk + 1 < end ? (blk + 1) * 16 + lr : a.rows;
+    load_x(a, xr, nrow, lg, nxt);
+    mlp_block(a, wl, bias, sr, cur, blk * 16 + lr, lane);
+  }
+}
+
+// ---- packing: fold the per-channel factors, then fragment order -----------
+__global__ void attn_mlp_bias_kernel(const shrimp_mlp_weights w, float* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < MC) {
+    out[i] = w.g_attn[i] * w.out_b[i];                                  // bo'
+  } else if (i < MC + MH) {
+    const int n = i - MC;
+    float s = w.fc1_b[n];
+    for (int k = 0; k < MC; ++k) s = fmaf(w.fc1_w[(int64_t)n * MC + k], w.ln_b[k], s);
+    out[i] = s;                                                         // b1'
+  } else if (i < MC + MH + MC) {
+    const int n = i - MC - MH;
+    out[i] = w.g_mlp[n] * w.fc2_b[n];                                   // b2'
+  }
+}
+
+// scaled[n][k] = rs[n] * src[n][k] * cs[k] (rs / cs may be NULL = 1)
+__global__ void scale_rows_cols_kernel(const float* __restrict__ src, const float* __restrict__ rs,
+                                       const float* __restrict__ cs, int n_out, int n_in,
+                                       float* __restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)n_out * n_in) return;
+  const int n = (int)(i / n_in), k = (int)(i - (int64_t)n * n_in);
+  float v = src[i];
+  if (rs) v *= rs[n];
+  if (cs) v *= cs[k];
+  dst[i] = v;
 }
 
 }  // namespace shrimp
 
 using namespace shrimp;
+
+extern "C" size_t shrimp_attn_mlp_pack_bytes(int C, int hidden) {
+  return (C == MC && hidden == MH) ? (size_t)PACK_BYTES : 0;
+}
+
+extern "C" int shrimp_pack_attn_mlp(const shrimp_mlp_weights* w, void* packed, void* scratch,
+                                    void* stream) {
+  SHRIMP_REQUIRE(w && packed && scratch, "pack_attn_mlp: null pointer");
+  SHRIMP_REQUIRE(w->C == MC && w->hidden == MH,
+                 "pack_attn_mlp: fused kernel covers C=%d, hidden=%d (got %d, %d)", MC, MH, w->C,
+                 w->hidden);
+  SHRIMP_REQUIRE(w->out_w && w->out_b && w->g_attn && w->ln_w && w->ln_b && w->fc1_w &&
+                     w->fc1_b && w->fc2_w && w->fc2_b && w->g_mlp,
+                 "pack_attn_mlp: null weight pointer");
+  hipStream_t st = as_stream(stream);
+  unsigned char* pk = static_cast<unsigned char*>(packed);
+  float* tmp = static_cast<float*>(scratch);  // MC * MH floats
+  struct Part {
+    const float* src; const float* rs; const float* cs; int n_out, n_in; uint32_t off; int il;
+  } parts[3] = {{w->out_w, w->g_attn, nullptr, MC, MC, WO_OFF, 0},
+                {w->fc1_w, nullptr, w->ln_w, MH, MC, W1_OFF, 1},
+                {w->fc2_w, w->g_mlp, nullptr, MC, MH, W2_OFF, 1}};
+  for (const Part& p : parts) {
+    const int64_t n = (int64_t)p.n_out * p.n_in;
+    hipLaunchKernelGGL(scale_rows_cols_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       p.src, p.rs, p.cs, p.n_out, p.n_in, tmp);
+    const int64_t frags = (int64_t)(p.n_in / 32) * (p.n_out / 16) * 64;
+    hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)((frags + 255) / 256)), dim3(256), 0, st,
+                       tmp, reinterpret_cast<unsigned short*>(pk + p.off), p.n_in, p.n_out, p.n_in,
+                       p.n_in, (int64_t)0, (int64_t)1, (int64_t)p.n_in, p.il);
+  }
+  hipLaunchKernelGGL(attn_mlp_bias_kernel, dim3((MC + MH + MC + 255) / 256), dim3(256), 0, st, *w,
+                     reinterpret_cast<float*>(pk + BO_OFF));
+  return check_launch("pack_attn_mlp");
+}
 
 extern "C" int shrimp_attn_mlp(const shrimp_mlp_args* a, void* stream) {
   SHRIMP_REQUIRE(a != nullptr, "attn_mlp: null args");
@@ -282,9 +341,7 @@ extern "C" int shrimp_attn_mlp(const shrimp_mlp_args* a, void* stream) {
   SHRIMP_REQUIRE(a->C == MC && a->hidden == MH,
                  "attn_mlp: fused kernel covers C=%d, hidden=%d (got C=%d, hidden=%d)", MC, MH,
                  a->C, a->hidden);
-  SHRIMP_REQUIRE(a->x && a->seq && a->mask && a->out_w && a->out_b && a->g_attn && a->ln_w &&
-                     a->ln_b && a->fc1_w && a->fc1_b && a->fc2_w && a->fc2_b && a->g_mlp,
-                 "attn_mlp: null pointer");
+  SHRIMP_REQUIRE(a->x && a->seq && a->mask && a->packed, "attn_mlp: null pointer");
   SHRIMP_REQUIRE(a->x_sr >= MC && a->x_sr % 8 == 0 && a->s_sr >= MC && a->s_sr % 8 == 0,
                  "attn_mlp: row strides must be >= C and multiples of 8");
   const int64_t xe = ((int64_t)(a->rows - 1) * a->x_sr + MC) * 2;

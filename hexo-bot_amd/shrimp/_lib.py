@@ -71,12 +71,18 @@ class TailArgs(ctypes.Structure):
     ]
 
 
+class MlpWeights(ctypes.Structure):
+    _fields_ = [
+        ("out_w", _vp), ("out_b", _vp), ("g_attn", _vp), ("ln_w", _vp), ("ln_b", _vp),
+        ("fc1_w", _vp), ("fc1_b", _vp), ("fc2_w", _vp), ("fc2_b", _vp), ("g_mlp", _vp),
+        ("C", _i32), ("hidden", _i32),
+    ]
+
+
 class MlpArgs(ctypes.Structure):
     _fields_ = [
         ("x", _vp), ("x_sr", _i64), ("seq", _vp), ("s_sr", _i64), ("mask", _vp),
-        ("out_w", _vp), ("out_b", _vp), ("g_attn", _vp), ("ln_w", _vp), ("ln_b", _vp),
-        ("eps", _f32), ("fc1_w", _vp), ("fc1_b", _vp), ("fc2_w", _vp), ("fc2_b", _vp),
-        ("g_mlp", _vp), ("rows", _i32), ("C", _i32), ("hidden", _i32),
+        ("packed", _vp), ("eps", _f32), ("rows", _i32), ("C", _i32), ("hidden", _i32),
     ]
 
 
@@ -91,10 +97,11 @@ SIGNATURES: dict = {
     "shrimp_pack_conv_weight": (ctypes.c_int, [_vp, _vp] + [ctypes.c_int] * 4 + [_vp]),
     "shrimp_linear_wpack_bytes": (ctypes.c_size_t, [ctypes.c_int] * 2),
     "shrimp_pack_linear_weight": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp]),
-    "shrimp_pack_linear_weight_il": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp]),
     "shrimp_hex_conv": (ctypes.c_int, [ctypes.POINTER(ConvArgs), _vp]),
     "shrimp_linear": (ctypes.c_int, [ctypes.POINTER(LinearArgs), _vp]),
     "shrimp_attn_mlp": (ctypes.c_int, [ctypes.POINTER(MlpArgs), _vp]),
+    "shrimp_attn_mlp_pack_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
+    "shrimp_pack_attn_mlp": (ctypes.c_int, [ctypes.POINTER(MlpWeights), _vp, _vp, _vp]),
     "shrimp_attn": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _vp]),
     "shrimp_attn_bias_table": (
         ctypes.c_int,

@@ -56,21 +56,44 @@ def pack_conv_weight(weight: torch.Tensor, cin_pad: int | None = None) -> torch.
     return out
 
 
-def pack_linear_weight(weight: torch.Tensor, interleaved: bool = False) -> torch.Tensor:
-    """nn.Linear weight (out, in) -> packed bf16 MFMA fragments (uint8 bytes);
-    ``interleaved`` selects the K order of the fused MLP's fc1 / fc2."""
+def pack_linear_weight(weight: torch.Tensor) -> torch.Tensor:
+    """nn.Linear weight (out, in) -> packed bf16 MFMA fragments (uint8 bytes)."""
 
     require_device(weight, "pack_linear_weight")
     n_out, n_in = weight.shape
     lib = _lib.load()
     w32 = weight.detach().to(torch.float32).contiguous()
     out = torch.empty(lib.shrimp_linear_wpack_bytes(n_in, n_out), dtype=torch.uint8, device=weight.device)
-    fn = lib.shrimp_pack_linear_weight_il if interleaved else lib.shrimp_pack_linear_weight
     _lib.check(
-        fn(w32.data_ptr(), out.data_ptr(), n_in, n_out, _lib.stream_handle(weight.device)),
+        lib.shrimp_pack_linear_weight(w32.data_ptr(), out.data_ptr(), n_in, n_out,
+                                      _lib.stream_handle(weight.device)),
         "pack_linear_weight",
     )
     return out
+
+
+def pack_attn_mlp(out_w, out_b, g_attn, ln_w, ln_b, fc1_w, fc1_b, fc2_w, fc2_b, g_mlp):
+    """AttnBlock out_proj / LN2 / fc1 / fc2 / LayerScale parameters -> the
+    fused MLP kernel's packed weights (per-channel factors folded in), or
+    None when the shape has no fused kernel (C != 128 or hidden != 2C)."""
+
+    require_device(out_w, "pack_attn_mlp")
+    c = int(out_w.shape[0])
+    hidden = int(fc1_w.shape[0])
+    lib = _lib.load()
+    nbytes = lib.shrimp_attn_mlp_pack_bytes(c, hidden)
+    if nbytes == 0:
+        return None
+    dev = out_w.device
+    ts = [t.detach().to(device=dev, dtype=torch.float32).contiguous()
+          for t in (out_w, out_b, g_attn, ln_w, ln_b, fc1_w, fc1_b, fc2_w, fc2_b, g_mlp)]
+    w = _lib.MlpWeights(*[t.data_ptr() for t in ts], C=c, hidden=hidden)
+    packed = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    scratch = torch.empty(c * hidden, dtype=torch.float32, device=dev)
+    _lib.check(lib.shrimp_pack_attn_mlp(ctypes_ref(w), packed.data_ptr(), scratch.data_ptr(),
+                                        _lib.stream_handle(dev)), "pack_attn_mlp")
+    torch.cuda.current_stream(dev).synchronize()  # ts / scratch die with this frame
+    return packed
 
 
 ATTN_XD = 26  # SHRIMP_ATTN_XD of the C ABI
@@ -134,18 +157,12 @@ def launch_linear(
     _lib.check(_lib.load().shrimp_linear(ctypes_ref(a), s), "linear")
 
 
-def launch_attn_mlp(
-    *, x, x_sr, seq, s_sr, mask, out_w, out_b, g_attn, ln_w, ln_b, eps, fc1_w, fc1_b, fc2_w,
-    fc2_b, g_mlp, rows, C, hidden, stream=None,
-):
+def launch_attn_mlp(*, x, x_sr, seq, s_sr, mask, packed, eps, rows, C, hidden, stream=None):
     """Fused out_proj + residual + LN2 + fc1 + GELU + fc2 + residual, seq in place."""
 
     a = _lib.MlpArgs(
         x=x.data_ptr(), x_sr=x_sr, seq=seq.data_ptr(), s_sr=s_sr, mask=mask.data_ptr(),
-        out_w=out_w.data_ptr(), out_b=out_b.data_ptr(), g_attn=g_attn.data_ptr(),
-        ln_w=ln_w.data_ptr(), ln_b=ln_b.data_ptr(), eps=float(eps), fc1_w=fc1_w.data_ptr(),
-        fc1_b=fc1_b.data_ptr(), fc2_w=fc2_w.data_ptr(), fc2_b=fc2_b.data_ptr(),
-        g_mlp=g_mlp.data_ptr(), rows=rows, C=C, hidden=hidden,
+        packed=packed.data_ptr(), eps=float(eps), rows=rows, C=C, hidden=hidden,
     )
     s = _lib.stream_handle() if stream is None else stream
     _lib.check(_lib.load().shrimp_attn_mlp(ctypes_ref(a), s), "attn_mlp")

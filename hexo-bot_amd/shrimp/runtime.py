@@ -39,6 +39,7 @@ from .ops import (
     launch_attn_mlp,
     launch_conv,
     launch_linear,
+    pack_attn_mlp,
     pack_conv_weight,
     pack_linear_weight,
     require_device,
@@ -104,8 +105,8 @@ class HipForward:
         def conv_w(conv, cin_pad=None):
             return pack_conv_weight(conv.weight.detach().to(device), cin_pad)
 
-        def lin_w(lin, interleaved=False):
-            return pack_linear_weight(lin.weight.detach().to(device), interleaved)
+        def lin_w(lin):
+            return pack_linear_weight(lin.weight.detach().to(device))
 
         c = net.channels
         P = SimpleNamespace()
@@ -129,9 +130,6 @@ class HipForward:
             )
         lut = net._cell_bias_lut_u8.to(device)
         P.lut = lut
-        # out_proj + MLP run as one fused kernel when its weights fit one
-        # workgroup's LDS (C = 128, hidden = 2C)
-        P.fused_mlp = c == 128 and all(b.fc1.out_features == 2 * c for b in net.attn_blocks)
         P.attn = []
         for i, blk in enumerate(net.attn_blocks):
             at = blk.attn
@@ -145,13 +143,17 @@ class HipForward:
                     ln2w=f32(blk.ln2.weight), ln2b=f32(blk.ln2.bias), eps2=blk.ln2.eps,
                     fc1_w=lin_w(blk.fc1), fc1_b=f32(blk.fc1.bias),
                     fc2_w=lin_w(blk.fc2), fc2_b=f32(blk.fc2.bias),
-                    fc1_w_il=lin_w(blk.fc1, True) if P.fused_mlp else None,
-                    fc2_w_il=lin_w(blk.fc2, True) if P.fused_mlp else None,
+                    # out_proj + MLP as one fused kernel where its weights fit
+                    # one workgroup's LDS (C = 128, hidden = 2C); else None
+                    mlp=pack_attn_mlp(at.out_proj.weight, at.out_proj.bias, blk.ls_attn.gamma,
+                                      blk.ln2.weight, blk.ln2.bias, blk.fc1.weight, blk.fc1.bias,
+                                      blk.fc2.weight, blk.fc2.bias, blk.ls_mlp.gamma),
                     g_attn=f32(blk.ls_attn.gamma), g_mlp=f32(blk.ls_mlp.gamma),
                     btab_xtab=attn_bias_table(net.bias_tables[i].detach().to(device), lut,
                                               CELL_LUT_M),
                 )
             )
+        P.fused_mlp = all(a.mlp is not None for a in P.attn)
         P.tokens = f32(net.tokens)
         P.lnf = SimpleNamespace(w=f32(net.ln_final.weight), b=f32(net.ln_final.bias),
                                 eps=net.ln_final.eps)
@@ -261,10 +263,8 @@ class HipForward:
                 )
                 if fused:
                     launch_attn_mlp(
-                        x=att, x_sr=C, seq=seq, s_sr=C, mask=seq_mask, out_w=a.out_w,
-                        out_b=a.out_b, g_attn=a.g_attn, ln_w=a.ln2w, ln_b=a.ln2b, eps=a.eps2,
-                        fc1_w=a.fc1_w_il, fc1_b=a.fc1_b, fc2_w=a.fc2_w_il, fc2_b=a.fc2_b,
-                        g_mlp=a.g_mlp, rows=rows, C=C, hidden=2 * C, stream=st,
+                        x=att, x_sr=C, seq=seq, s_sr=C, mask=seq_mask, packed=a.mlp,
+                        eps=a.eps2, rows=rows, C=C, hidden=2 * C, stream=st,
                     )
                     continue
                 launch_linear(

@@ -69,11 +69,6 @@ int shrimp_pack_conv_weight(const float* w, void* packed, int taps, int cin, int
 size_t shrimp_linear_wpack_bytes(int in_features, int out_features);
 int shrimp_pack_linear_weight(const float* w, void* packed, int in_features, int out_features,
                               void* stream);
-/* Same fragments with the interleaved K order (lane l holds
- * k = 32*ks + 16*(e/4) + 4*(l/16) + e%4), the input order of the fc1 / fc2
- * weights of shrimp_attn_mlp. */
-int shrimp_pack_linear_weight_il(const float* w, void* packed, int in_features, int out_features,
-                                 void* stream);
 
 /* ------------------------------------------------------------------------
  * Gather-GEMM hex / ray-tap convolution with fused epilogue.
@@ -161,36 +156,49 @@ int shrimp_linear(const shrimp_linear_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
  * Fused attention-block tail (AttnBlock.forward after the attention core,
- * model.py:508-514; replaces the out_proj / fc1 / fc2 nn.Linear calls and
- * the two LayerScale residuals):
- *   s1  = bf16(seq + g_attn * (mask ? x @ Wo^T + bo : 0))
+ * model.py:508-514; replaces the out_proj / fc1 / fc2 nn.Linear calls, LN2
+ * and the two LayerScale residuals):
+ *   s1  = seq + g_attn * (mask ? x @ Wo^T + bo : 0)
  *   h   = bf16(gelu_erf(LN2(s1) @ W1^T + b1))
- *   seq = bf16(s1 + g_mlp * (mask ? h @ W2^T + b2 : 0))        (in place)
+ *   seq = bf16(bf16(s1) + g_mlp * (mask ? h @ W2^T + b2 : 0))   (in place)
  * x: attention output rows (bf16), seq: residual stream rows (bf16), both
- * with element row strides; mask: per-row live flag. out_w packed in the
- * standard order, fc1_w / fc2_w in the interleaved order. C = 128, hidden =
- * 256 (the whole weight set is held in one workgroup's LDS).
+ * with element row strides; mask: per-row live flag (rows with mask 0 are
+ * not written: their update is 0). C = 128, hidden = 256: the packed weights
+ * (160 KiB of fragments) fill one workgroup's LDS.
+ *
+ * shrimp_pack_attn_mlp folds g_attn into Wo / bo, LN2's affine into W1 / b1
+ * and g_mlp into W2 / b2, then writes MFMA fragments and the folded biases to
+ * `packed` (shrimp_attn_mlp_pack_bytes bytes; 0 = unsupported shape).
+ * `scratch` is a device buffer of C * hidden floats used during packing.
+ * Weights are nn.Linear layouts (out, in), fp32.
  * ---------------------------------------------------------------------- */
+typedef struct {
+  const float* out_w;  /* (C, C) */
+  const float* out_b;  /* (C) */
+  const float* g_attn; /* (C) LayerScale after attention */
+  const float* ln_w;   /* (C) LN2 */
+  const float* ln_b;   /* (C) */
+  const float* fc1_w;  /* (hidden, C) */
+  const float* fc1_b;  /* (hidden) */
+  const float* fc2_w;  /* (C, hidden) */
+  const float* fc2_b;  /* (C) */
+  const float* g_mlp;  /* (C) LayerScale after the MLP */
+  int32_t C, hidden;
+} shrimp_mlp_weights;
+
 typedef struct {
   const void* x;
   int64_t x_sr;
   void* seq;
   int64_t s_sr;
-  const uint8_t* mask; /* (rows) */
-  const void* out_w;   /* packed (C -> C), standard order */
-  const float* out_b;
-  const float* g_attn; /* LayerScale after attention (C) */
-  const float* ln_w;   /* LN2 (C) */
-  const float* ln_b;
-  float eps;
-  const void* fc1_w;   /* packed (C -> hidden), interleaved order */
-  const float* fc1_b;
-  const void* fc2_w;   /* packed (hidden -> C), interleaved order */
-  const float* fc2_b;
-  const float* g_mlp;  /* LayerScale after the MLP (C) */
+  const uint8_t* mask;  /* (rows) */
+  const void* packed;   /* shrimp_pack_attn_mlp output */
+  float eps;            /* LN2 epsilon */
   int32_t rows, C, hidden;
 } shrimp_mlp_args;
 
+size_t shrimp_attn_mlp_pack_bytes(int C, int hidden);
+int shrimp_pack_attn_mlp(const shrimp_mlp_weights* w, void* packed, void* scratch, void* stream);
 int shrimp_attn_mlp(const shrimp_mlp_args* a, void* stream);
 
 /* ------------------------------------------------------------------------

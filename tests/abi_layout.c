@@ -48,13 +48,15 @@ int main(void) {
   F(shrimp_tail_args, B);
   F(shrimp_tail_args, S); F(shrimp_tail_args, n_tokens); F(shrimp_tail_args, C);
   F(shrimp_tail_args, bins);
+  Z(shrimp_mlp_weights);
+  F(shrimp_mlp_weights, out_w); F(shrimp_mlp_weights, out_b); F(shrimp_mlp_weights, g_attn);
+  F(shrimp_mlp_weights, ln_w); F(shrimp_mlp_weights, ln_b); F(shrimp_mlp_weights, fc1_w);
+  F(shrimp_mlp_weights, fc1_b); F(shrimp_mlp_weights, fc2_w); F(shrimp_mlp_weights, fc2_b);
+  F(shrimp_mlp_weights, g_mlp); F(shrimp_mlp_weights, C); F(shrimp_mlp_weights, hidden);
   Z(shrimp_mlp_args);
   F(shrimp_mlp_args, x); F(shrimp_mlp_args, x_sr); F(shrimp_mlp_args, seq);
-  F(shrimp_mlp_args, s_sr); F(shrimp_mlp_args, mask); F(shrimp_mlp_args, out_w);
-  F(shrimp_mlp_args, out_b); F(shrimp_mlp_args, g_attn); F(shrimp_mlp_args, ln_w);
-  F(shrimp_mlp_args, ln_b); F(shrimp_mlp_args, eps); F(shrimp_mlp_args, fc1_w);
-  F(shrimp_mlp_args, fc1_b); F(shrimp_mlp_args, fc2_w); F(shrimp_mlp_args, fc2_b);
-  F(shrimp_mlp_args, g_mlp); F(shrimp_mlp_args, rows); F(shrimp_mlp_args, C);
+  F(shrimp_mlp_args, s_sr); F(shrimp_mlp_args, mask); F(shrimp_mlp_args, packed);
+  F(shrimp_mlp_args, eps); F(shrimp_mlp_args, rows); F(shrimp_mlp_args, C);
   F(shrimp_mlp_args, hidden);
   return 0;
 }

@@ -321,9 +321,12 @@ def test_linear_modes(mode, c):
 @pytest.mark.parametrize("rows", [1, 37, 4096 + 5])
 def test_attn_mlp_fused(rows):
     """Fused out_proj + LayerScale residual + LN2 + fc1 + GELU(erf) + fc2 +
-    residual (C=128) against a float64 restatement with the kernel's bf16
-    rounding points (s1 and the hidden layer stored as bf16). Row counts
-    cover a single row, a ragged block and several blocks per wave."""
+    residual (C=128) against a float64 restatement of AttnBlock's tail with
+    the kernel's bf16 points (MFMA inputs, s1 kept as bf16 for the second
+    residual). The kernel folds the LayerScales and LN2's affine into the
+    weights before rounding them to bf16, so the reference rounds the folded
+    weights the same way. Row counts cover a single row, a ragged block and
+    several blocks per wave; masked rows must keep their residual exactly."""
 
     from shrimp import ops
 
@@ -338,23 +341,34 @@ def test_attn_mlp_fused(rows):
     ga, gm = torch.rand(c) * 0.5 + 0.25, torch.rand(c) * 0.5 + 0.25
     lnw, lnb = torch.rand(c) + 0.5, torch.randn(c) * 0.1
 
-    s1 = bf(bf(seq) + ga.double() * ((bf(x) @ bf(wo).T + bo.double()) * m.double()[:, None]))
-    hn = bf(torch.nn.functional.layer_norm(s1, (c,), lnw.double(), lnb.double(), 1e-5))
-    hid = bf(torch.nn.functional.gelu(hn @ bf(w1).T + b1.double()))
-    want = s1 + gm.double() * ((hid @ bf(w2).T + b2.double()) * m.double()[:, None])
+    d = lambda t: t.double()
+    s1 = bf(seq) + (bf(x) @ bf(ga[:, None] * wo).T + d(ga * bo)) * d(m)[:, None]
+    n = bf(torch.nn.functional.layer_norm(s1, (c,), None, None, 1e-5))
+    hid = bf(torch.nn.functional.gelu(n @ bf(w1 * lnw[None, :]).T + d(b1) + d(w1) @ d(lnb)))
+    want = bf(s1) + (hid @ bf(gm[:, None] * w2).T + d(gm * b2)) * d(m)[:, None]
+    # the same block in the model's own terms (unfolded fp64): within bf16 noise
+    s1u = d(seq) + d(ga) * ((d(x) @ d(wo).T + d(bo)) * d(m)[:, None])
+    hu = torch.nn.functional.gelu(
+        torch.nn.functional.layer_norm(s1u, (c,), d(lnw), d(lnb), 1e-5) @ d(w1).T + d(b1))
+    model = s1u + d(gm) * ((hu @ d(w2).T + d(b2)) * d(m)[:, None])
 
     seq_d = seq.to(DEV, torch.bfloat16).contiguous()
-    ops.launch_attn_mlp(
-        x=x.to(DEV, torch.bfloat16).contiguous(), x_sr=c, seq=seq_d, s_sr=c,
-        mask=m.to(DEV, torch.uint8), out_w=ops.pack_linear_weight(wo.to(DEV)), out_b=bo.to(DEV),
-        g_attn=ga.to(DEV), ln_w=lnw.to(DEV), ln_b=lnb.to(DEV), eps=1e-5,
-        fc1_w=ops.pack_linear_weight(w1.to(DEV), True), fc1_b=b1.to(DEV),
-        fc2_w=ops.pack_linear_weight(w2.to(DEV), True), fc2_b=b2.to(DEV), g_mlp=gm.to(DEV),
-        rows=rows, C=c, hidden=hdim,
-    )
+    g = lambda t: t.to(DEV)
+    packed = ops.pack_attn_mlp(g(wo), g(bo), g(ga), g(lnw), g(lnb), g(w1), g(b1), g(w2), g(b2), g(gm))
+    ops.launch_attn_mlp(x=x.to(DEV, torch.bfloat16).contiguous(), x_sr=c, seq=seq_d, s_sr=c,
+                        mask=m.to(DEV, torch.uint8), packed=packed, eps=1e-5, rows=rows, C=c,
+                        hidden=hdim)
     close(seq_d, want, what=f"attn_mlp rows={rows}")
-    # masked rows keep their residual exactly (bf16 of seq)
+    close(seq_d, model, atol=5e-2, rtol=2e-2, what=f"attn_mlp vs model rows={rows}")
     assert torch.equal(seq_d.cpu()[~m].double(), bf(seq)[~m])
+
+
+def test_attn_mlp_pack_rejects_other_shapes():
+    from shrimp import ops
+
+    z = lambda *s: torch.zeros(*s, device=DEV)
+    assert ops.pack_attn_mlp(z(64, 64), z(64), z(64), z(64), z(64), z(128, 64), z(128),
+                             z(64, 128), z(64), z(64)) is None
 
 
 @pytest.mark.parametrize("d", [16, 32, 64])
