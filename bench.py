@@ -100,11 +100,12 @@ def kernel_timings(net, inputs, reps=50):
     # Timing re-launches write into the forward's scratch buffers only (never
     # back into seq): residual modes target a copy.
     seq_copy = seq.clone()
-    linears = {
-        "qkv": (lin(_lib.LIN_QKV, seq, C, a.qkv_w, a.qkv_b, C, 3 * C, qkv[0], 0, ln_w=a.ln1w,
-                    ln_b=a.ln1b, B=b, S=s, H=H, dpad=P.dpad), rows * C * 3 * C * 2.0,
-                rows * (C + 3 * C) * 2.0),
-    }
+    qkv_fn = (lambda: ops.launch_attn_qkv(
+        x=seq, x_sr=C, qkv=qkv[0], packed=a.qkv, eps=a.eps1, rows=rows, B=b, S=s, H=H, C=C,
+        dpad=P.dpad, stream=L["stream"])) if P.fused_qkv else lin(
+            _lib.LIN_QKV, seq, C, a.qkv_w, a.qkv_b, C, 3 * C, qkv[0], 0, ln_w=a.ln1w,
+            ln_b=a.ln1b, B=b, S=s, H=H, dpad=P.dpad)
+    linears = {"qkv": (qkv_fn, rows * C * 3 * C * 2.0, rows * (C + 3 * C) * 2.0)}
     if P.fused_mlp:
         linears["attn_mlp"] = (
             lambda: ops.launch_attn_mlp(

@@ -71,6 +71,13 @@ class TailArgs(ctypes.Structure):
     ]
 
 
+class QkvArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", _vp), ("x_sr", _i64), ("qkv", _vp), ("packed", _vp), ("eps", _f32),
+        ("rows", _i32), ("B", _i32), ("S", _i32), ("H", _i32), ("C", _i32), ("dpad", _i32),
+    ]
+
+
 class MlpWeights(ctypes.Structure):
     _fields_ = [
         ("out_w", _vp), ("out_b", _vp), ("g_attn", _vp), ("ln_w", _vp), ("ln_b", _vp),
@@ -99,6 +106,9 @@ SIGNATURES: dict = {
     "shrimp_pack_linear_weight": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp]),
     "shrimp_hex_conv": (ctypes.c_int, [ctypes.POINTER(ConvArgs), _vp]),
     "shrimp_linear": (ctypes.c_int, [ctypes.POINTER(LinearArgs), _vp]),
+    "shrimp_attn_qkv": (ctypes.c_int, [ctypes.POINTER(QkvArgs), _vp]),
+    "shrimp_attn_qkv_pack_bytes": (ctypes.c_size_t, [ctypes.c_int]),
+    "shrimp_pack_attn_qkv": (ctypes.c_int, [_vp] * 6 + [ctypes.c_int, _vp]),
     "shrimp_attn_mlp": (ctypes.c_int, [ctypes.POINTER(MlpArgs), _vp]),
     "shrimp_attn_mlp_pack_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
     "shrimp_pack_attn_mlp": (ctypes.c_int, [ctypes.POINTER(MlpWeights), _vp, _vp, _vp]),

@@ -72,6 +72,28 @@ def pack_linear_weight(weight: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def pack_attn_qkv(qkv_w, qkv_b, ln_w, ln_b):
+    """(3C, C) q/k/v weights + biases and LN1's affine -> the fused QKV
+    kernel's packed weights, or None when C has no fused kernel."""
+
+    require_device(qkv_w, "pack_attn_qkv")
+    c = int(qkv_w.shape[1])
+    lib = _lib.load()
+    nbytes = lib.shrimp_attn_qkv_pack_bytes(c)
+    if nbytes == 0:
+        return None
+    dev = qkv_w.device
+    ts = [t.detach().to(device=dev, dtype=torch.float32).contiguous()
+          for t in (qkv_w, qkv_b, ln_w, ln_b)]
+    packed = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    scratch = torch.empty(3 * c * c, dtype=torch.float32, device=dev)
+    _lib.check(lib.shrimp_pack_attn_qkv(*[t.data_ptr() for t in ts], packed.data_ptr(),
+                                        scratch.data_ptr(), c, _lib.stream_handle(dev)),
+               "pack_attn_qkv")
+    torch.cuda.current_stream(dev).synchronize()
+    return packed
+
+
 def pack_attn_mlp(out_w, out_b, g_attn, ln_w, ln_b, fc1_w, fc1_b, fc2_w, fc2_b, g_mlp):
     """AttnBlock out_proj / LN2 / fc1 / fc2 / LayerScale parameters -> the
     fused MLP kernel's packed weights (per-channel factors folded in), or
@@ -155,6 +177,15 @@ def launch_linear(
     )
     s = _lib.stream_handle() if stream is None else stream
     _lib.check(_lib.load().shrimp_linear(ctypes_ref(a), s), "linear")
+
+
+def launch_attn_qkv(*, x, x_sr, qkv, packed, eps, rows, B, S, H, C, dpad, stream=None):
+    """LN1 + q/k/v projection into the head-major (3, B, H, S, dpad) layout."""
+
+    a = _lib.QkvArgs(x=x.data_ptr(), x_sr=x_sr, qkv=qkv.data_ptr(), packed=packed.data_ptr(),
+                     eps=float(eps), rows=rows, B=B, S=S, H=H, C=C, dpad=dpad)
+    s = _lib.stream_handle() if stream is None else stream
+    _lib.check(_lib.load().shrimp_attn_qkv(ctypes_ref(a), s), "attn_qkv")
 
 
 def launch_attn_mlp(*, x, x_sr, seq, s_sr, mask, packed, eps, rows, C, hidden, stream=None):

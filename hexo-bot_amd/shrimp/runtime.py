@@ -16,7 +16,7 @@ Kernel sequence (reference lines in model.py):
     prep_inputs          gather_idx / mask / coords / seq_lens / padded feats  :861-892
     hex_conv  (stem)     conv + LN + ReLU + mask                               :865
     per 'C': hex_conv x2 conv1+LN+ReLU+mask -> y1; conv2+LN+mask, ReLU(x+g*y)  :395-422
-    per 'A': linear(QKV, LN1) -> attn -> attn_mlp (out_proj, residual, LN2,
+    per 'A': attn_qkv (LN1, q/k/v) -> attn -> attn_mlp (out_proj, residual, LN2,
              fc1, GELU, fc2, residual; three linear launches when C != 128)   :448-514
     trunk_tail           final LN, pooled mean, value / moves-left heads       :927-935, 990-1002
     hex_conv  (policy)   conv + ReLU + Linear(C,1) + mask                      :1011-1020
@@ -37,9 +37,11 @@ from .ops import (
     attn_bias_table,
     launch_attn,
     launch_attn_mlp,
+    launch_attn_qkv,
     launch_conv,
     launch_linear,
     pack_attn_mlp,
+    pack_attn_qkv,
     pack_conv_weight,
     pack_linear_weight,
     require_device,
@@ -77,6 +79,9 @@ class HipForward:
         # Fused out_proj + MLP kernel where it applies; off runs the three
         # linear kernels (used to check one against the other).
         self.use_fused_mlp = True
+        # LN1 + q/k/v kernel with LN1 folded into its weights where it
+        # applies; off runs the linear kernel's QKV mode.
+        self.use_fused_qkv = True
 
     def invalidate(self) -> None:
         self._packed = None
@@ -139,6 +144,10 @@ class HipForward:
                 SimpleNamespace(
                     ln1w=f32(blk.ln1.weight), ln1b=f32(blk.ln1.bias), eps1=blk.ln1.eps,
                     qkv_w=pack_linear_weight(qkv_w.detach().to(device)), qkv_b=f32(qkv_b),
+                    # LN1 + q/k/v as one kernel with LN1 folded into the
+                    # weights where it applies (C = 128); else None
+                    qkv=pack_attn_qkv(qkv_w.to(device), qkv_b.to(device), blk.ln1.weight,
+                                      blk.ln1.bias),
                     out_w=lin_w(at.out_proj), out_b=f32(at.out_proj.bias),
                     ln2w=f32(blk.ln2.weight), ln2b=f32(blk.ln2.bias), eps2=blk.ln2.eps,
                     fc1_w=lin_w(blk.fc1), fc1_b=f32(blk.fc1.bias),
@@ -154,6 +163,7 @@ class HipForward:
                 )
             )
         P.fused_mlp = all(a.mlp is not None for a in P.attn)
+        P.fused_qkv = all(a.qkv is not None for a in P.attn)
         P.tokens = f32(net.tokens)
         P.lnf = SimpleNamespace(w=f32(net.ln_final.weight), b=f32(net.ln_final.bias),
                                 eps=net.ln_final.eps)
@@ -249,11 +259,15 @@ class HipForward:
             else:
                 a = P.attn[ai]
                 ai += 1
-                launch_linear(
-                    x=seq, x_sr=C, wpack=a.qkv_w, bias=a.qkv_b, rows=rows, n_in=C, n_out=3 * C,
-                    mode=_lib.LIN_QKV, out=qkv, ln_w=a.ln1w, ln_b=a.ln1b, eps=a.eps1,
-                    B=B, S=S, H=H, dpad=dpad, stream=st,
-                )
+                if P.fused_qkv and self.use_fused_qkv:
+                    launch_attn_qkv(x=seq, x_sr=C, qkv=qkv, packed=a.qkv, eps=a.eps1, rows=rows,
+                                    B=B, S=S, H=H, C=C, dpad=dpad, stream=st)
+                else:
+                    launch_linear(
+                        x=seq, x_sr=C, wpack=a.qkv_w, bias=a.qkv_b, rows=rows, n_in=C,
+                        n_out=3 * C, mode=_lib.LIN_QKV, out=qkv, ln_w=a.ln1w, ln_b=a.ln1b,
+                        eps=a.eps1, B=B, S=S, H=H, dpad=dpad, stream=st,
+                    )
                 launch_attn(
                     q=qkv[0], k=qkv[1], v=qkv[2], qkv_sb=H * S * dpad, qkv_sh=S * dpad,
                     seq_lens=seq_lens, o=att, o_sb=S * C, o_sh=d, o_sr=C, B=B, S=S, H=H, d=d,

@@ -155,6 +155,32 @@ typedef struct {
 int shrimp_linear(const shrimp_linear_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Fused LayerNorm + q/k/v projection (RelPosAttention.forward q_proj /
+ * k_proj / v_proj on AttnBlock's ln1, model.py:448-492, 508-514; replaces
+ * shrimp_linear's QKV mode for C = 128):
+ *   n = LN1(x[r]) ;  [q | k | v] = n @ Wqkv^T + bqkv   -> qkv (3, B, H, S, dpad)
+ * with rows r = (b, s). The padding lanes d..dpad of qkv are not written.
+ * shrimp_pack_attn_qkv folds LN1's affine into the weights (W diag(ln_w),
+ * b + W ln_b) and writes MFMA fragments and the folded bias to `packed`
+ * (shrimp_attn_qkv_pack_bytes(C) bytes; 0 = unsupported C). qkv_w is the
+ * (3C, C) concatenation of q_proj / k_proj / v_proj weights (fp32), qkv_b
+ * their biases; `scratch` holds 3C * C floats during packing.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* x; /* (rows, x_sr) bf16 */
+  int64_t x_sr;
+  void* qkv;     /* (3, B, H, S, dpad) bf16 */
+  const void* packed;
+  float eps;     /* LN1 epsilon */
+  int32_t rows, B, S, H, C, dpad;
+} shrimp_qkv_args;
+
+size_t shrimp_attn_qkv_pack_bytes(int C);
+int shrimp_pack_attn_qkv(const float* qkv_w, const float* qkv_b, const float* ln_w,
+                         const float* ln_b, void* packed, void* scratch, int C, void* stream);
+int shrimp_attn_qkv(const shrimp_qkv_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
  * Fused attention-block tail (AttnBlock.forward after the attention core,
  * model.py:508-514; replaces the out_proj / fc1 / fc2 nn.Linear calls, LN2
  * and the two LayerScale residuals):

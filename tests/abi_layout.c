@@ -48,6 +48,11 @@ int main(void) {
   F(shrimp_tail_args, B);
   F(shrimp_tail_args, S); F(shrimp_tail_args, n_tokens); F(shrimp_tail_args, C);
   F(shrimp_tail_args, bins);
+  Z(shrimp_qkv_args);
+  F(shrimp_qkv_args, x); F(shrimp_qkv_args, x_sr); F(shrimp_qkv_args, qkv);
+  F(shrimp_qkv_args, packed); F(shrimp_qkv_args, eps); F(shrimp_qkv_args, rows);
+  F(shrimp_qkv_args, B); F(shrimp_qkv_args, S); F(shrimp_qkv_args, H); F(shrimp_qkv_args, C);
+  F(shrimp_qkv_args, dpad);
   Z(shrimp_mlp_weights);
   F(shrimp_mlp_weights, out_w); F(shrimp_mlp_weights, out_b); F(shrimp_mlp_weights, g_attn);
   F(shrimp_mlp_weights, ln_w); F(shrimp_mlp_weights, ln_b); F(shrimp_mlp_weights, fc1_w);

@@ -101,18 +101,20 @@ def test_linear_and_clamped_bias_paths_agree(cfg4_batch):
 
 
 def test_fused_and_unfused_mlp_paths_agree(cfg4_batch):
-    """The fused attention-block MLP kernel and the three separate linear
-    kernels give the same forward up to fp32 summation order and the GELU's
-    erf evaluation (|error| <= 1.5e-7)."""
+    """The fused LN1 + q/k/v and attention-block MLP kernels (per-channel
+    factors folded into bf16 weights) and the separate linear kernels give the
+    same forward up to bf16 rounding points, fp32 summation order and the
+    GELU's erf evaluation (|error| <= 1.5e-7)."""
 
     b = cfg4_batch
     net = _net(128, 8, "CCACCACCACCA", seed=5)
     fused = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
-    net.hip_runtime().use_fused_mlp = False
+    rt = net.hip_runtime()
+    rt.use_fused_mlp = rt.use_fused_qkv = False
     try:
         plain = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
     finally:
-        net.hip_runtime().use_fused_mlp = True
+        rt.use_fused_mlp = rt.use_fused_qkv = True
     for key in ("policy", "value", "moves_left"):
         err = (fused[key] - plain[key]).abs().max().item()
         print(f"fused vs unfused {key}: {err:.3e}", flush=True)

@@ -363,6 +363,34 @@ def test_attn_mlp_fused(rows):
     assert torch.equal(seq_d.cpu()[~m].double(), bf(seq)[~m])
 
 
+@pytest.mark.parametrize("h,dpad", [(8, 16), (4, 32), (2, 64)])
+def test_attn_qkv_fused(h, dpad):
+    """LN1 + q/k/v projection (C=128) into the head-major layout against a
+    float64 restatement; LN1's affine is folded into the bf16 weights the same
+    way the packer folds it. Padding lanes past d are never written."""
+
+    from shrimp import ops
+
+    torch.manual_seed(3)
+    c, B, S = 128, 3, 45
+    rows, d = B * S, c // h
+    x = torch.randn(rows, c) * 2 + 0.5
+    w, b = torch.randn(3 * c, c) * 0.08, torch.randn(3 * c) * 0.1
+    lnw, lnb = torch.rand(c) + 0.5, torch.randn(c) * 0.1
+    n = bf(torch.nn.functional.layer_norm(bf(x), (c,), None, None, 1e-5))
+    y = n @ bf(w * lnw[None, :]).T + (b.double() + w.double() @ lnb.double())
+    want = y.reshape(B, S, 3, h, d).permute(2, 0, 3, 1, 4)
+    model = (torch.nn.functional.layer_norm(bf(x), (c,), lnw.double(), lnb.double(), 1e-5)
+             @ w.double().T + b.double()).reshape(B, S, 3, h, d).permute(2, 0, 3, 1, 4)
+    out = torch.full((3, B, h, S, dpad), 7.0, dtype=torch.bfloat16, device=DEV)
+    packed = ops.pack_attn_qkv(w.to(DEV), b.to(DEV), lnw.to(DEV), lnb.to(DEV))
+    ops.launch_attn_qkv(x=x.to(DEV, torch.bfloat16).contiguous(), x_sr=c, qkv=out,
+                        packed=packed, eps=1e-5, rows=rows, B=B, S=S, H=h, C=c, dpad=dpad)
+    close(out[..., :d], want, what=f"qkv H={h}")
+    close(out[..., :d], model, atol=4e-2, rtol=2e-2, what=f"qkv vs model H={h}")
+    assert (out[..., d:].float() == 7.0).all()
+
+
 def test_attn_mlp_pack_rejects_other_shapes():
     from shrimp import ops
 

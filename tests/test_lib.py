@@ -52,6 +52,7 @@ def test_struct_layouts_match_c(tmp_path):
         "shrimp_linear_args": _lib.LinearArgs,
         "shrimp_attn_args": _lib.AttnArgs,
         "shrimp_tail_args": _lib.TailArgs,
+        "shrimp_qkv_args": _lib.QkvArgs,
         "shrimp_mlp_weights": _lib.MlpWeights,
         "shrimp_mlp_args": _lib.MlpArgs,
     }
