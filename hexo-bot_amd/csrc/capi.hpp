@@ -26,9 +26,10 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // device (queried once per device).
 int max_lds_per_block();
 
-// Conv kernel selection: 0 = automatic (LDS-staged when the position fits,
-// else global gather), 1 = always the global-gather kernel, 2 = LDS-staged,
-// 3 = big-tile LDS kernel for the 128-channel 7-tap shape (else as 0).
+// Conv kernel selection: 0 = automatic (big-tile LDS kernel for the
+// 128-channel 7-tap shape, else LDS-staged when the position fits, else
+// global gather), 1 = always the global-gather kernel, 2 = LDS-staged
+// (no big tiles), 3 = as 0.
 extern int g_conv_variant;
 
 }  // namespace shrimp

@@ -28,18 +28,23 @@ enum : int { EPI_LN = 1, EPI_RELU = 2, EPI_RESID = 4, EPI_HEAD = 8 };
 // Bias / LayerNorm / ReLU / mask / residual / head epilogue on the fp32
 // accumulators of MB row blocks. rb, rn: position and cell index of this
 // lane's row in block mb; rv: row exists.
-// PRE (kernels with registers to spare): the per-channel parameters of this
-// lane's channels are loaded once into registers (they would otherwise be
-// re-read after every store, which the compiler must assume may alias them).
+// Per-channel parameters (PSRC): PS_GLOBAL reads them where used; PS_REGS
+// loads this lane's channels once into registers (re-reading after a store
+// would wait, since the compiler must assume the store may alias them);
+// PS_LDS reads them from an LDS copy at `lp` laid out [bias | ln_w | ln_b |
+// gamma or head_w], COUT floats each.
 // The row masks are loaded up front and the residual rows of block mb+1 are
 // requested before block mb's math.
-template <int COUT, int MB, int EPI, bool PRE>
+enum : int { PS_GLOBAL = 0, PS_REGS = 1, PS_LDS = 2 };
+
+template <int COUT, int MB, int EPI, int PSRC>
 SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16][MB],
                               const int (&rb)[MB], const int (&rn)[MB], const bool (&rv)[MB],
-                              int lg) {
+                              int lg, const float* lp = nullptr) {
   constexpr int NB = COUT / 16;
   constexpr bool LN = (EPI & EPI_LN) != 0, RESID = (EPI & EPI_RESID) != 0;
   constexpr bool HEAD = (EPI & EPI_HEAD) != 0;
+  constexpr bool PRE = PSRC == PS_REGS;
   constexpr int PN = PRE ? NB : 1;
   const int N = a.N;
   f32x4 pb[PN], pw[LN ? PN : 1], pl[LN ? PN : 1], pg[RESID ? PN : 1], ph[HEAD ? PN : 1];
@@ -56,11 +61,17 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
       if constexpr (HEAD) ph[nb] = prm(a.head_w, nb);
     }
   }
-  auto P_b = [&](int nb) { if constexpr (PRE) return pb[nb]; else return prm(a.bias, nb); };
-  auto P_w = [&](int nb) { if constexpr (PRE) return pw[nb % (LN ? NB : 1)]; else return prm(a.ln_w, nb); };
-  auto P_l = [&](int nb) { if constexpr (PRE) return pl[nb % (LN ? NB : 1)]; else return prm(a.ln_b, nb); };
-  auto P_g = [&](int nb) { if constexpr (PRE) return pg[nb % (RESID ? NB : 1)]; else return prm(a.gamma, nb); };
-  auto P_h = [&](int nb) { if constexpr (PRE) return ph[nb % (HEAD ? NB : 1)]; else return prm(a.head_w, nb); };
+  // ri: index into the register copy (0 when that array is a placeholder)
+  auto pick = [&](int slot, const float* g, const f32x4* r, int nb, int ri) -> f32x4 {
+    if constexpr (PSRC == PS_LDS) return prm(lp + slot * COUT, nb);
+    else if constexpr (PRE) return r[ri];
+    else return prm(g, nb);
+  };
+  auto P_b = [&](int nb) { return pick(0, a.bias, pb, nb, nb); };
+  auto P_w = [&](int nb) { return pick(1, a.ln_w, pw, nb, LN && PRE ? nb : 0); };
+  auto P_l = [&](int nb) { return pick(2, a.ln_b, pl, nb, LN && PRE ? nb : 0); };
+  auto P_g = [&](int nb) { return pick(3, a.gamma, pg, nb, RESID && PRE ? nb : 0); };
+  auto P_h = [&](int nb) { return pick(3, a.head_w, ph, nb, HEAD && PRE ? nb : 0); };
   bool live[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) live[mb] = rv[mb] && a.mask[(int64_t)rb[mb] * N + rn[mb]] != 0;
@@ -240,7 +251,7 @@ __global__ __launch_bounds__(256, 2) void hex_conv_kernel(const shrimp_conv_args
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = mfma16x16x32(wc[nb], xc[mb], acc[nb][mb]);
   }
-  conv_epilogue<COUT, MB, EPI, false>(a, acc, rb, rn, rv, lg);
+  conv_epilogue<COUT, MB, EPI, PS_GLOBAL>(a, acc, rb, rn, rv, lg);
 }
 
 // LDS-staged variant: one workgroup per position. The position's N rows
@@ -372,7 +383,7 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = mfma16x16x32(wc[nb], xc[mb], acc[nb][mb]);
     }
-    conv_epilogue<COUT, MB, EPI, false>(a, acc, rb, rn, rv, lg);
+    conv_epilogue<COUT, MB, EPI, PS_GLOBAL>(a, acc, rb, rn, rv, lg);
   }
 }
 
@@ -382,50 +393,56 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
 // AGPRs, so one wave per SIMD). Every weight fragment feeds 8 MFMAs and every
 // gathered row fragment 8, which keeps both the L1 (weights) and the LDS (rows)
 // well under their bandwidth at full MFMA rate.
-// The K loop runs channel-chunk-major (kc = 32-channel chunk, then the 7 taps),
-// and rows are staged one chunk ahead: chunk kc+1 is loaded from HBM into
-// registers while the MFMAs of chunk kc run, then written to LDS behind a
-// barrier.
+//
+// Rows are staged by buffer-to-LDS DMA (no registers, no LDS store
+// instructions), channel-chunk-major: chunk kc (32 channels, 64 bytes) of row r
+// sits at kc * NR * 64 + r * 64, its four 16-byte pieces swizzled as slot
+// s = piece ^ ((r >> 2) & 3), so the 16 lanes of an MFMA lane group reading
+// one piece of 16 different rows hit distinct banks. One DMA instruction
+// fills 16 rows of one chunk; rows >= N (the zero row N for absent neighbours
+// and the padding up to NR = ceil((N+1)/16)*16) read past the buffer and land
+// as zeros. The K loop runs chunk-major (kc, then the 7 taps); chunk kc+1 is
+// requested while chunk kc's MFMAs run, always after the step's weight
+// prefetch (vmcnt retires in issue order, so a weight wait never waits for
+// an HBM row load), and a barrier publishes it at the chunk boundary.
 constexpr int BIG_MAX_N = 512;
+
+SHRIMP_DEV int big_rows_padded(int N) { return ((N + 1 + 15) / 16) * 16; }
+
+typedef __attribute__((address_space(3))) void lds_void_t;
 
 template <int EPI>
 __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_args a,
-                                                              uint32_t w_bytes) {
-  constexpr int COUT = 128, CIN = 128, ROWB = CIN * 2, CPR = CIN / 8, KC = CIN / 32;
+                                                              uint32_t x_bytes, uint32_t w_bytes) {
+  constexpr int COUT = 128, CIN = 128, KC = CIN / 32;
   constexpr int T = 7, MB = 8, NB = COUT / 16;
-  // Staging: chunk kc of every row is N x 4 pieces of 16 bytes; with
-  // ceil(N/128) waves that is at most SU = 8 pieces per thread, spread over
-  // the 7 tap steps of the previous chunk (piece u is loaded at step u*T/SU
-  // and written to LDS one step later).
-  constexpr int SU = 8;
   extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int nthr = blockDim.x;
+  const int nw = blockDim.x >> 6;
   const int lr = lane & 15;
   const int lg = lane >> 4;
   const int N = a.N;
+  const int NR = big_rows_padded(N);
+  const int groups = NR / 16;  // DMA instructions per chunk
   const int b = blockIdx.x;
-  const unsigned short* xb = static_cast<const unsigned short*>(a.x) + (int64_t)b * a.x_sb;
-  const int pieces = N * 4;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes);
+  const uint32_t xbase = (uint32_t)((int64_t)b * a.x_sb * 2);
 
-  auto piece_load = [&](int kc, int u) -> u32x4 {
-    const int c = u * nthr + (int)threadIdx.x;
-    u32x4 v = u32x4{0u, 0u, 0u, 0u};
-    if (c < pieces)
-      v = *reinterpret_cast<const u32x4*>(xb + (int64_t)(c >> 2) * a.x_sn + (kc * 4 + (c & 3)) * 8);
-    return v;
-  };
-  auto piece_store = [&](int kc, int u, u32x4 v) {
-    const int c = u * nthr + (int)threadIdx.x;
-    const int row = c >> 2;
-    const int ch = kc * 4 + (c & 3);
-    if (c < pieces) *reinterpret_cast<u32x4*>(xs + row * ROWB + ((ch ^ (row & (CPR - 1))) << 4)) = v;
+  // DMA of chunk kc, rows [16 g, 16 g + 16): lane -> row 16 g + lane / 4, slot lane % 4.
+  auto dma = [&](int kc, int g) {
+    const int r = g * 16 + (lane >> 2);
+    const int piece = (lane & 3) ^ ((r >> 2) & 3);
+    const uint32_t off = r < N ? xbase + (uint32_t)(r * a.x_sn * 2) + (uint32_t)((kc * 4 + piece) * 16)
+                               : SHRIMP_OOB_OFFSET;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        xr, (lds_void_t*)(xs + (kc * NR + g * 16) * 64), 16, off, 0, 0, 0);
   };
 
-  // Prologue: request the neighbour indices of all taps, chunk 0 of the rows
-  // and the first weight fragments together, then write LDS.
+  // Prologue: chunk 0 by DMA, the neighbour indices of all taps, the first
+  // weight fragments and the epilogue parameters, then one barrier.
+  for (int g = wave; g < groups; g += nw) dma(0, g);
   const int row0 = wave * (MB * 16);
   int rn[MB], rb[MB];
   bool rv[MB];
@@ -441,9 +458,6 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
   for (int t = 0; t < T; ++t)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) jr[t][mb] = rv[mb] ? idxb[rn[mb] * a.idx_stride + t] : N;
-  u32x4 v0[SU];
-#pragma unroll
-  for (int u = 0; u < SU; ++u) v0[u] = piece_load(0, u);
 
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, w_bytes);
   auto wload = [&](int s, u32x4 (&w)[NB]) {
@@ -453,14 +467,18 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
   u32x4 wf[NB];
   wload(0, wf);
 
-  // Zero row N (all chunks), then chunk 0.
-  for (int c = threadIdx.x; c < CPR; c += nthr)
-    *reinterpret_cast<u32x4*>(xs + N * ROWB + c * 16) = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int u = 0; u < SU; ++u) piece_store(0, u, v0[u]);
+  // epilogue parameters after the rows: [bias | ln_w | ln_b | gamma or head_w]
+  float* lp = reinterpret_cast<float*>(xs + KC * NR * 64);
+  {
+    const float* src[4] = {a.bias, a.ln_w, a.ln_b, (EPI & EPI_HEAD) ? a.head_w : a.gamma};
+    for (int i = threadIdx.x; i < 4 * COUT; i += blockDim.x) {
+      const float* sp = src[i / COUT];
+      lp[i] = sp ? sp[i % COUT] : 0.f;
+    }
+  }
 
-  // Neighbour rows as 16-bit swizzled row addresses in 16-byte units:
-  // (j * ROWB + (j % CPR) * 16) / 16 = j * 16 + j % 16; two per register.
+  // Neighbour rows as 16-bit row addresses within a chunk region:
+  // j * 64 | ((j >> 2) & 3) << 4 (the piece swizzle); two per register.
   uint32_t sw2[T][MB / 2];
 #pragma unroll
   for (int t = 0; t < T; ++t)
@@ -471,17 +489,18 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
       for (int h = 0; h < 2; ++h) {
         const int j = jr[t][2 * m2 + h];
         const int jj = (j >= 0 && j < N) ? j : N;
-        pk |= (uint32_t)(jj * (ROWB / 16) + (jj & (CPR - 1))) << (16 * h);
+        pk |= (uint32_t)(jj * 64 + (((jj >> 2) & 3) << 4)) << (16 * h);
       }
       sw2[t][m2] = pk;
     }
 
   auto xload = [&](int t, int kc, u32x4 (&x)[MB]) {
-    const uint32_t cs = (uint32_t)(kc * 4 + lg);
+    const uint32_t kbase = (uint32_t)(kc * NR * 64);
+    const uint32_t ls = (uint32_t)lg << 4;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       const uint32_t v = (sw2[t][mb >> 1] >> (16 * (mb & 1))) & 0xFFFFu;
-      x[mb] = *reinterpret_cast<const u32x4*>(xs + ((v ^ cs) << 4));
+      x[mb] = *reinterpret_cast<const u32x4*>(xs + kbase + (v ^ ls));
     }
   };
 
@@ -491,32 +510,19 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   // Every wave owns rows (waves = ceil(N / 128)), so no wave skips the MFMAs;
   // the chunk loop is fully unrolled so that no value crosses a branch.
+  const int mine = (groups - wave + nw - 1) / nw;  // DMA groups of this wave per chunk
 #pragma unroll
   for (int kc = 0; kc < KC; ++kc) {
     const bool more = kc + 1 < KC;
     u32x4 xf[MB];
     xload(0, kc, xf);
-    u32x4 pv[2];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      // staging of chunk kc + 1: pieces [u0, u1) load now, store next step
-      const int u0 = (t * SU) / T, u1 = ((t + 1) * SU) / T;
-      u32x4 nv[2];
-      if (more) {
-#pragma unroll
-        for (int u = u0; u < u1; ++u) nv[u - u0] = piece_load(kc + 1, u);
-        if (t > 0) {
-          const int p0 = ((t - 1) * SU) / T, p1 = (t * SU) / T;
-#pragma unroll
-          for (int u = p0; u < p1; ++u) piece_store(kc + 1, u, pv[u - p0]);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) pv[i] = nv[i];
-      }
       u32x4 xc[MB], wc[NB];
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) xc[mb] = xf[mb];
@@ -528,6 +534,11 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
       } else if (more) {
         wload(kc + 1, wf);
       }
+      if (more) {
+        // this wave's DMA groups i in [i0, i1) of chunk kc + 1
+        const int i0 = (t * mine) / T, i1 = ((t + 1) * mine) / T;
+        for (int i = i0; i < i1; ++i) dma(kc + 1, wave + i * nw);
+      }
       // Keep the next step's loads ahead of this step's MFMAs (the scheduler
       // would otherwise sink them next to their uses).
       __builtin_amdgcn_sched_barrier(0);
@@ -538,13 +549,11 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
       __builtin_amdgcn_sched_barrier(0);
     }
     if (more) {
-      constexpr int p0 = ((T - 1) * SU) / T;
-#pragma unroll
-      for (int u = p0; u < SU; ++u) piece_store(kc + 1, u, pv[u - p0]);
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA of chunk kc + 1 has landed
       __syncthreads();
     }
   }
-  conv_epilogue<COUT, MB, EPI, true>(a, acc, rb, rn, rv, lg);
+  conv_epilogue<COUT, MB, EPI, PS_LDS>(a, acc, rb, rn, rv, lg, lp);
 }
 
 // ---- weight packing ------------------------------------------------------------
@@ -581,9 +590,15 @@ template <int COUT, int MB, int EPI>
 static int launch_conv(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, size_t lds,
                        hipStream_t st) {
   if (COUT == 128 && lds && a->cin_pad == 128 && a->taps == 7 && a->N <= BIG_MAX_N &&
-      g_conv_variant == 3) {
+      (g_conv_variant == 0 || g_conv_variant == 3)) {
     const int waves = (a->N + 127) / 128;
-    hipLaunchKernelGGL((hex_conv_big_kernel<EPI>), dim3(a->B), dim3(64 * waves), lds, st, *a, wb);
+    const int nr = ((a->N + 1 + 15) / 16) * 16;
+    const size_t big_lds = (size_t)nr * 256 + 4 * 128 * sizeof(float);
+    if (big_lds <= (size_t)max_lds_per_block()) {
+      hipLaunchKernelGGL((hex_conv_big_kernel<EPI>), dim3(a->B), dim3(64 * waves), big_lds, st, *a,
+                         xb, wb);
+      return check_launch("hex_conv");
+    }
     return check_launch("hex_conv");
   }
   if (lds) {

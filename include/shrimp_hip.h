@@ -45,10 +45,10 @@ int shrimp_abi_version(void);
 
 /* Tuning / test switches (no counterpart in the reference).
  * shrimp_conv_variant: 0 = automatic conv kernel choice (a position's rows
- * staged in LDS when they fit), 1 = always gather rows from global memory,
- * 2 = LDS-staged rows, 3 = LDS-staged rows with 128x128 tiles per wave for
- * the 128-channel 7-tap conv; other values only query. Returns the previous
- * setting. Process-wide.
+ * staged in LDS when they fit, 128x128 tiles per wave for the 128-channel
+ * 7-tap conv), 1 = always gather rows from global memory, 2 = LDS-staged
+ * rows with small tiles, 3 = same as 0; other values only query. Returns
+ * the previous setting. Process-wide.
  * shrimp_max_lds_per_block: LDS bytes one workgroup may allocate on the
  * current device (the staged conv needs (N + 1) * cin_pad * 2). */
 int shrimp_conv_variant(int variant);
