@@ -91,153 +91,181 @@ __global__ void fill_tokens_kernel(const float* __restrict__ tokens, int n_token
 // ---- trunk tail + value heads (model.py:927-935, 990-1002) --------------------
 // Pass 1, one workgroup per position: final LayerNorm of every row (cells
 // masked), written to out_seq; the value-head inputs [T0 | T1 | pooled] and
-// [T4 | T5 | pooled] go to the workspace (B, 6C) fp32. Each wave keeps four
-// rows in flight; a lane owns channel pairs (2 lane + 128 u, +1).
+// [T4 | T5 | pooled] go to the workspace (B, 6C) fp32.
+// A row is handled by TPR = C / 8 lanes (16 bytes each), 256 / TPR rows per
+// pass, four passes in flight; row statistics reduce over the TPR lanes.
+template <int TPR>
 __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a) {
-  __shared__ float pool_w[4][256];
-  __shared__ int cnt_w[4];
+  constexpr int RPP = 256 / TPR;  // rows per pass
+  constexpr int U = 4;            // passes in flight
+  extern __shared__ float fl[];   // [RPP][C] pooled partial sums, then [RPP] counts
   const int b = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int C = a.C, S = a.S, nt = a.n_tokens, N = S - nt;
+  const int t = threadIdx.x;
+  const int sub = t % TPR;         // 8-channel chunk of this lane
+  const int rs = t / TPR;          // row slot
+  const int c0 = sub * 8;
+  const bool cv = c0 < C;
   const uint16_t* seq = static_cast<const uint16_t*>(a.seq) + (int64_t)b * a.s_sb;
   uint16_t* outs = static_cast<uint16_t*>(a.out_seq) + (int64_t)b * a.s_sb;
   float* vin = a.workspace + (int64_t)b * 6 * C;
-  float lw[2][2], lb[2][2];
+  float w[8], bb[8], pool[8];
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int c = 2 * lane + 128 * u + e;
-      lw[u][e] = c < C ? a.ln_w[c] : 0.f;
-      lb[u][e] = c < C ? a.ln_b[c] : 0.f;
-    }
-  float acc[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+  for (int e = 0; e < 8; ++e) {
+    w[e] = cv ? a.ln_w[c0 + e] : 0.f;
+    bb[e] = cv ? a.ln_b[c0 + e] : 0.f;
+    pool[e] = 0.f;
+  }
   int cnt = 0;
-  for (int row0 = wave * 4; row0 < S; row0 += 16) {
-    unsigned raw[4][2];
-    bool live[4];
+  const float invc = 1.0f / (float)C;
+  for (int r0 = 0; r0 < S; r0 += U * RPP) {
+    u32x4 raw[U];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = row0 + r;
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int c = 2 * lane + 128 * u;
-        raw[r][u] = (row < S && c < C)
-                        ? *reinterpret_cast<const unsigned*>(seq + (int64_t)row * C + c)
-                        : 0u;
-      }
-      live[r] = row < S && (row < nt || a.mask[(int64_t)b * N + (row - nt)] != 0);
+    for (int u = 0; u < U; ++u) {
+      const int row = r0 + u * RPP + rs;
+      raw[u] = (row < S && cv) ? *reinterpret_cast<const u32x4*>(seq + (int64_t)row * C + c0)
+                               : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = row0 + r;
-      if (row >= S) break;  // wave-uniform
-      float x[2][2];
-      float sum = 0.f;
+    for (int u = 0; u < U; ++u) {
+      const int row = r0 + u * RPP + rs;
+      float x[8];
+      float s = 0.f;
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        x[u][0] = bf16_lo(raw[r][u]);
-        x[u][1] = bf16_hi(raw[r][u]);
-        sum += x[u][0] + x[u][1];
+      for (int e = 0; e < 4; ++e) {
+        x[2 * e] = bf16_lo(raw[u][e]);
+        x[2 * e + 1] = bf16_hi(raw[u][e]);
+        s += x[2 * e] + x[2 * e + 1];
       }
-      const float mean = wave_sum(sum) / C;
+#pragma unroll
+      for (int m = 1; m < TPR; m <<= 1) s += __shfl_xor(s, m, 64);
+      const float mean = s * invc;
       float q = 0.f;
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int e = 0; e < 8; ++e) {
+        x[e] = cv ? x[e] - mean : 0.f;
+        q = fmaf(x[e], x[e], q);
+      }
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int c = 2 * lane + 128 * u + e;
-          x[u][e] = c < C ? x[u][e] - mean : 0.f;
-          q += x[u][e] * x[u][e];
-        }
-      const float rstd = rsqrtf(wave_sum(q) / C + a.eps);
-      const bool is_cell = row >= nt;
-      if (is_cell && live[r]) ++cnt;
+      for (int m = 1; m < TPR; m <<= 1) q += __shfl_xor(q, m, 64);
+      const float rstd = rsqrtf(q * invc + a.eps);
+      if (row >= S || !cv) continue;
+      const bool cell = row >= nt;
+      const bool live = !cell || a.mask[(int64_t)b * N + (row - nt)] != 0;
+      float y[8];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int c = 2 * lane + 128 * u;
-        if (c >= C) continue;
-        float y0 = x[u][0] * rstd * lw[u][0] + lb[u][0];
-        float y1 = x[u][1] * rstd * lw[u][1] + lb[u][1];
-        if (!live[r]) y0 = y1 = 0.f;
-        *reinterpret_cast<unsigned*>(outs + (int64_t)row * C + c) = pack_bf16x2(y0, y1);
-        if (is_cell) {
-          acc[u][0] += y0;
-          acc[u][1] += y1;
-        }
+      for (int e = 0; e < 8; ++e) y[e] = live ? fmaf(x[e] * rstd, w[e], bb[e]) : 0.f;
+      *reinterpret_cast<u32x4*>(outs + (int64_t)row * C + c0) =
+          u32x4{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]),
+                pack_bf16x2(y[6], y[7])};
+      if (cell) {
+        if (live && sub == 0) ++cnt;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pool[e] += y[e];
+      } else {
         // token rows 0, 1 feed the value head, rows 4, 5 the moves-left head
         const int slot = row == 0 ? 0 : row == 1 ? 1 : row == 4 ? 3 : row == 5 ? 4 : -1;
         if (slot >= 0) {
-          vin[slot * C + c] = y0;
-          vin[slot * C + c + 1] = y1;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vin[slot * C + c0 + e] = y[e];
         }
       }
     }
   }
+  float* red = fl;                 // [RPP][C]
+  float* cred = fl + RPP * C;      // [RPP]
+  if (cv) {
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int c = 2 * lane + 128 * u + e;
-      if (c < C) pool_w[wave][c] = acc[u][e];
-    }
-  if (lane == 0) cnt_w[wave] = cnt;
+    for (int e = 0; e < 8; ++e) red[rs * C + c0 + e] = pool[e];
+  }
+  if (sub == 0) cred[rs] = (float)cnt;
   __syncthreads();
-  const float inv = 1.0f / (float)max(1, cnt_w[0] + cnt_w[1] + cnt_w[2] + cnt_w[3]);
-  for (int c = threadIdx.x; c < C; c += blockDim.x) {
-    const float p = (pool_w[0][c] + pool_w[1][c] + pool_w[2][c] + pool_w[3][c]) * inv;
-    vin[2 * C + c] = p;
-    vin[5 * C + c] = p;
+  float total = 0.f;
+  for (int i = 0; i < RPP; ++i) total += cred[i];
+  const float inv = 1.0f / fmaxf(1.f, total);
+  for (int c = t; c < C; c += blockDim.x) {
+    float p = 0.f;
+    for (int i = 0; i < RPP; ++i) p += red[i * C + c];
+    vin[2 * C + c] = p * inv;
+    vin[5 * C + c] = p * inv;
   }
 }
 
-// Pass 2: value / moves-left heads for 4 positions per workgroup; weights are
-// transposed (k-major) so a wave's weight load covers 64 consecutive outputs.
+// Pass 2: one head (value or moves-left, blockIdx.y) for kHeadPos positions
+// per workgroup: hid = relu(in @ Wr + br) (in = [T | T' | pooled], 3C),
+// out = hid @ Wh + bh. Weights are transposed (k-major) so consecutive lanes
+// read consecutive outputs; the K range is split over the idle threads and
+// reduced through LDS.
 constexpr int kHeadPos = 4;
 __global__ __launch_bounds__(256) void value_head_kernel(const shrimp_tail_args a) {
   extern __shared__ float hs[];
-  const int C = a.C, bins = a.bins;
-  float* in = hs;                   // [kHeadPos][3C]
-  float* hid = hs + kHeadPos * 3 * C;  // [kHeadPos][C]
+  const int C = a.C, bins = a.bins, K1 = 3 * C;
+  const int head = blockIdx.y;
+  const float* rwt = head == 0 ? a.vr_w : a.mr_w;
+  const float* rb = head == 0 ? a.vr_b : a.mr_b;
+  const float* hwt = head == 0 ? a.vh_w : a.mh_w;
+  const float* hb = head == 0 ? a.vh_b : a.mh_b;
+  float* dst = head == 0 ? a.value : a.moves_left;
+  if (dst == nullptr) return;  // uniform
   const int b0 = blockIdx.x * kHeadPos;
   const int np = min(kHeadPos, a.B - b0);
-  for (int pass = 0; pass < 2; ++pass) {
-    const float* rwt = pass == 0 ? a.vr_w : a.mr_w;
-    const float* rb = pass == 0 ? a.vr_b : a.mr_b;
-    const float* hwt = pass == 0 ? a.vh_w : a.mh_w;
-    const float* hb = pass == 0 ? a.vh_b : a.mh_b;
-    float* dst = pass == 0 ? a.value : a.moves_left;
-    if (dst == nullptr) continue;  // uniform
-    for (int i = threadIdx.x; i < kHeadPos * 3 * C; i += blockDim.x) {
-      const int p = i / (3 * C), k = i - p * 3 * C;
-      in[i] = p < np ? a.workspace[(int64_t)(b0 + p) * 6 * C + pass * 3 * C + k] : 0.f;
-    }
-    __syncthreads();
-    for (int o = threadIdx.x; o < C; o += blockDim.x) {
+  const int t = threadIdx.x;
+  const int ks1 = 256 / C;         // K slices, layer 1
+  const int ks2 = 256 / bins;      // K slices, layer 2
+  float* in = hs;                              // [kHeadPos][K1]
+  float* red = in + kHeadPos * K1;             // [ks1][kHeadPos][C]
+  float* hid = red + ks1 * kHeadPos * C;       // [kHeadPos][C]
+  float* red2 = hid + kHeadPos * C;            // [ks2][kHeadPos][bins]
+  for (int i = t; i < kHeadPos * K1; i += blockDim.x) {
+    const int p = i / K1, k = i - p * K1;
+    in[i] = p < np ? a.workspace[(int64_t)(b0 + p) * 6 * C + head * K1 + k] : 0.f;
+  }
+  __syncthreads();
+  {
+    const int o = t % C, ks = t / C;
+    if (ks < ks1) {
+      const int k0 = ks * K1 / ks1, k1 = (ks + 1) * K1 / ks1;
       float s[kHeadPos] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
-      for (int k = 0; k < 3 * C; ++k) {
+      for (int k = k0; k < k1; ++k) {
         const float w = rwt[(int64_t)k * C + o];
 #pragma unroll
-        for (int p = 0; p < kHeadPos; ++p) s[p] += w * in[p * 3 * C + k];
+        for (int p = 0; p < kHeadPos; ++p) s[p] = fmaf(w, in[p * K1 + k], s[p]);
       }
 #pragma unroll
-      for (int p = 0; p < kHeadPos; ++p) hid[p * C + o] = fmaxf(s[p] + rb[o], 0.f);
+      for (int p = 0; p < kHeadPos; ++p) red[(ks * kHeadPos + p) * C + o] = s[p];
     }
-    __syncthreads();
-    for (int o = threadIdx.x; o < bins; o += blockDim.x) {
+  }
+  __syncthreads();
+  for (int i = t; i < kHeadPos * C; i += blockDim.x) {
+    const int p = i / C, o = i - p * C;
+    float s = rb[o];
+    for (int ks = 0; ks < ks1; ++ks) s += red[(ks * kHeadPos + p) * C + o];
+    hid[i] = fmaxf(s, 0.f);
+  }
+  __syncthreads();
+  {
+    const int o = t % bins, ks = t / bins;
+    if (ks < ks2) {
+      const int k0 = ks * C / ks2, k1 = (ks + 1) * C / ks2;
       float s[kHeadPos] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
-      for (int k = 0; k < C; ++k) {
+      for (int k = k0; k < k1; ++k) {
         const float w = hwt[(int64_t)k * bins + o];
 #pragma unroll
-        for (int p = 0; p < kHeadPos; ++p) s[p] += w * hid[p * C + k];
+        for (int p = 0; p < kHeadPos; ++p) s[p] = fmaf(w, hid[p * C + k], s[p]);
       }
 #pragma unroll
-      for (int p = 0; p < kHeadPos; ++p)
-        if (p < np) dst[(int64_t)(b0 + p) * bins + o] = s[p] + hb[o];
+      for (int p = 0; p < kHeadPos; ++p) red2[(ks * kHeadPos + p) * bins + o] = s[p];
     }
-    __syncthreads();
+  }
+  __syncthreads();
+  for (int i = t; i < kHeadPos * bins; i += blockDim.x) {
+    const int p = i / bins, o = i - p * bins;
+    if (p >= np) continue;
+    float s = hb[o];
+    for (int ks = 0; ks < ks2; ++ks) s += red2[(ks * kHeadPos + p) * bins + o];
+    dst[(int64_t)(b0 + p) * bins + o] = s;
   }
 }
 
@@ -445,13 +473,24 @@ extern "C" int shrimp_trunk_tail(const shrimp_tail_args* a, void* stream) {
   SHRIMP_REQUIRE(!a->value || (a->vr_w && a->vr_b && a->vh_w && a->vh_b), "trunk_tail: value head");
   SHRIMP_REQUIRE(!a->moves_left || (a->mr_w && a->mr_b && a->mh_w && a->mh_b),
                  "trunk_tail: moves-left head");
+  SHRIMP_REQUIRE(a->C % 8 == 0 && a->C <= 256 && a->s_sb % 8 == 0,
+                 "trunk_tail: C %d must be a multiple of 8 (<= 256), position stride of 8", a->C);
+  SHRIMP_REQUIRE(a->bins > 0 && a->bins <= 256, "trunk_tail: bins %d", a->bins);
   hipStream_t st = as_stream(stream);
-  hipLaunchKernelGGL(final_ln_kernel, dim3(a->B), dim3(256), 0, st, *a);
+  const int tpr = a->C / 8;
+  const size_t lsm = (size_t)(256 / ((tpr <= 4) ? 4 : (tpr <= 8) ? 8 : (tpr <= 16) ? 16 : 32)) *
+                     (a->C + 1) * sizeof(float);
+  if (tpr <= 4) hipLaunchKernelGGL(final_ln_kernel<4>, dim3(a->B), dim3(256), lsm, st, *a);
+  else if (tpr <= 8) hipLaunchKernelGGL(final_ln_kernel<8>, dim3(a->B), dim3(256), lsm, st, *a);
+  else if (tpr <= 16) hipLaunchKernelGGL(final_ln_kernel<16>, dim3(a->B), dim3(256), lsm, st, *a);
+  else hipLaunchKernelGGL(final_ln_kernel<32>, dim3(a->B), dim3(256), lsm, st, *a);
   if (int rc = check_launch("trunk_tail/ln")) return rc;
   if (!a->value && !a->moves_left) return SHRIMP_OK;
-  const size_t smem = (size_t)kHeadPos * 4 * a->C * sizeof(float);
-  hipLaunchKernelGGL(value_head_kernel, dim3((a->B + kHeadPos - 1) / kHeadPos), dim3(256), smem,
-                     st, *a);
+  const int ks1 = 256 / a->C, ks2 = 256 / a->bins;
+  const size_t smem = ((size_t)kHeadPos * 3 * a->C + (size_t)ks1 * kHeadPos * a->C +
+                       (size_t)kHeadPos * a->C + (size_t)ks2 * kHeadPos * a->bins) * sizeof(float);
+  hipLaunchKernelGGL(value_head_kernel, dim3((a->B + kHeadPos - 1) / kHeadPos, 2), dim3(256),
+                     smem, st, *a);
   return check_launch("trunk_tail/heads");
 }
 
