@@ -17,14 +17,17 @@
 //                 the lane's own running max;
 //   row sums: one more MFMA of P^T against a constant ones row of "V^T".
 // Key chunks take one of three bias paths (chosen per wave, uniformly):
-//   LINEAR  all keys live cells and the position's coordinate span <= 26:
-//           the offset LUT needs no clamping, so the bias index is
-//           kkey[key] - qkey[query] into an unclamped 53x53 fp16 table
-//           (the reference also rounds the table to fp16, model.py:741);
+//   LINEAR  positions whose live cells span <= 26 in q and r: the offset LUT
+//           needs no clamping, so the bias is read at byte offset
+//           kkey[key] - qkey[query] of an unclamped 53x53 fp16 table (the
+//           reference also rounds the table to fp16, model.py:741). Token
+//           and dead keys carry the offset code of a live cell, token
+//           queries that of a live cell; blocks holding them (flagged per
+//           chunk) then select the token biases / drop dead keys per lane;
 //   CLAMP   all keys live cells, wider positions: clamped LUT index into the
 //           fp32 table in global memory (L1/L2 resident);
-//   GENERAL token rows / columns, dead keys, the key bound (and the pair
-//           tensor of the reference operator ABI).
+//   GENERAL token rows / columns, dead keys and the key bound of wider
+//           positions (and the pair tensor of the reference operator ABI).
 // Softmax runs in base 2 with log2(e) folded into scale and tables; scores,
 // statistics and accumulators are fp32, P enters the MFMAs as bf16.
 #include "capi.hpp"
@@ -49,21 +52,27 @@ struct AttnLds {
   unsigned short* Ks;  // [HG][KD][SP/16] K fragments (256 bf16 each)
   unsigned short* Vt;  // [HG][KD][SP/16] V fragments (256 bf16 each)
   int2* kqr;           // [SP] key coordinates
-  int* kkey;           // [SP] q*XW + r + XD*XW + XD (linear offset code)
+  int* kkey;           // [SP] byte offset code (q*XW + r + XD*XW + XD) * 2 HG
   int* kcls;           // [SP] KEY_CELL / KEY_TOKEN / KEY_DEAD
   int* blk_gen;        // [SP / 16] 1 if the block holds a token or dead key
+  float* tokb;         // [3][HG] biases of (cell query, token key), (token query,
+                       // cell key), (token, token), log2e folded
   float* tab;          // pair mode: [rows][HG] fp32 (log2e folded)
   _Float16* xtab;      // coords mode: [XW*XW][HG] unclamped offset table, fp16
 };
 
 struct AttnQuery {
-  int query, qq, qr, qkey;
+  int query, qq, qr, qkey;  // qkey: byte offset code (q*XW + r) * 2 HG
   bool qtok, qv;
 };
 
+
+
 // One chunk of NBK 16-key blocks (NBK in {1, 2, 4}) for the HG heads of one
 // 16-query block.
-template <int DP, int HG, bool PAIR, int NBK, int PATH>
+// SEL (LINEAR path): the chunk holds token queries, token keys or dead keys;
+// their biases are selected per lane and dead keys dropped.
+template <int DP, int HG, bool PAIR, int NBK, int PATH, bool SEL = false>
 SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, const AttnQuery& qi,
                            int kb0, int L, int SP, int lr, int lg, float qk_scale, int npos,
                            const u32x2 (&qf)[HG][DP / 16], float (&m)[HG], float (&l)[HG],
@@ -103,14 +112,25 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
 #pragma unroll
         for (int h = 0; h < HG; ++h) bias[kb][j][h] = s.tab[p * HG + h];
       } else if (PATH == PATH_LINEAR) {
-        const int p = s.kkey[key] - qi.qkey;
+        const char* xp = reinterpret_cast<const char*>(s.xtab) + (s.kkey[key] - qi.qkey);
         if (HG == 2) {
-          const unsigned w = reinterpret_cast<const unsigned*>(s.xtab)[p];
+          const unsigned w = *reinterpret_cast<const unsigned*>(xp);
           bias[kb][j][0] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xFFFFu));
           bias[kb][j][HG - 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> 16));
         } else {
 #pragma unroll
-          for (int h = 0; h < HG; ++h) bias[kb][j][h] = (float)s.xtab[p * HG + h];
+          for (int h = 0; h < HG; ++h) bias[kb][j][h] = (float)reinterpret_cast<const _Float16*>(xp)[h];
+        }
+        if (SEL) {
+          const int cls = s.kcls[key];
+          const bool ktok = cls == KEY_TOKEN;
+          live[kb][j] = cls != KEY_DEAD;
+#pragma unroll
+          for (int h = 0; h < HG; ++h) {
+            const float tk = qi.qtok ? s.tokb[2 * HG + h] : s.tokb[h];
+            const float ck = qi.qtok ? s.tokb[HG + h] : bias[kb][j][h];
+            bias[kb][j][h] = ktok ? tk : ck;
+          }
         }
       } else {
         const int2 kk = s.kqr[key];
@@ -141,7 +161,7 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float v = fmaf(sc4[h][kb][j], qk_scale, bias[kb][j][h]);
-        if (PATH == PATH_GENERAL) v = live[kb][j] ? v : SHRIMP_NEG_BIG;
+        if (PATH == PATH_GENERAL || SEL) v = live[kb][j] ? v : SHRIMP_NEG_BIG;
         sc[kb][j] = v;
         mx = fmaxf(mx, v);
       }
@@ -156,7 +176,7 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         p[j] = __builtin_amdgcn_exp2f(sc[kb][j] - mnew);
-        if (PATH == PATH_GENERAL) p[j] = live[kb][j] ? p[j] : 0.f;
+        if (PATH == PATH_GENERAL || SEL) p[j] = live[kb][j] ? p[j] : 0.f;
       }
       pf[kb].x = pack_bf16x2(p[0], p[1]);
       pf[kb].y = pack_bf16x2(p[2], p[3]);
@@ -221,7 +241,8 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   s.kcls = s.kkey + SP;
   s.blk_gen = s.kcls + SP;
   int* q_gen = s.blk_gen + NKB;
-  float* tail = reinterpret_cast<float*>(q_gen + NKB);
+  s.tokb = reinterpret_cast<float*>(q_gen + NKB);
+  float* tail = s.tokb + 3 * HG;
   s.tab = tail;
   s.xtab = reinterpret_cast<_Float16*>(tail);
 
@@ -330,6 +351,10 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     }
   }
   // ---- bias tables of this head group -------------------------------------------------
+  if (!PAIR && tid < 3 * HG) {
+    const int W2 = (2 * a.lut_m + 1) * (2 * a.lut_m + 1);
+    s.tokb[tid] = a.btab[(W2 + tid / HG) * a.H + h0 + tid % HG];
+  }
   if (PAIR) {
     for (int i = tid; i < npos * HG; i += 256) {
       const int pos = i / HG;
@@ -400,15 +425,19 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
       r0 = min(r0, span_red[w * 4 + 2]);
       r1 = max(r1, span_red[w * 4 + 3]);
     }
-    // an empty cell set gives q1 < q0: nothing is indexed linearly then anyway
-    linear_ok = a.xtab != nullptr && (q1 - q0) <= XD && (r1 - r0) <= XD;
+    // LINEAR needs at least one live cell (its code stands in for token and
+    // dead keys); an empty cell set gives q1 < q0 and takes the general path.
+    linear_ok = a.xtab != nullptr && q0 <= q1 && (q1 - q0) <= XD && (r1 - r0) <= XD;
     // queries past the bound borrow (q0, r0): offsets to live cells stay in range
     safe_q = q0;
     safe_r = r0;
-    // Linear offset code: (dq, dr) -> (dq + XD) * XW + (dr + XD) = kkey - qkey.
+    // Linear offset code, in bytes of the (XW*XW, HG) fp16 table:
+    // (dq, dr) -> ((dq + XD) * XW + (dr + XD)) * 2 HG = kkey - qkey. Token and
+    // dead keys take the code of the live cell (q0, r0), so every LINEAR read
+    // stays inside the table; their biases are selected afterwards.
     for (int key = tid; key < LP; key += 256) {
-      const int2 kk = s.kqr[key];
-      s.kkey[key] = kk.x * XW + kk.y + XD * XW + XD;
+      const int2 kk = s.kcls[key] == KEY_CELL ? s.kqr[key] : make_int2(q0, r0);
+      s.kkey[key] = (kk.x * XW + kk.y + XD * XW + XD) * 2 * HG;
     }
   }
   __syncthreads();
@@ -429,9 +458,10 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     qi.qkey = 0;
     if (!PAIR) {
       const int2 qc = s.kqr[qi.query];
-      qi.qq = qi.qv ? qc.x : safe_q;
-      qi.qr = qi.qv ? qc.y : safe_r;
-      qi.qkey = qi.qq * XW + qi.qr;
+      const bool qcell = qi.qv && !qi.qtok;
+      qi.qq = qcell ? qc.x : safe_q;
+      qi.qr = qcell ? qc.y : safe_r;
+      qi.qkey = (qi.qq * XW + qi.qr) * 2 * HG;
     }
     // token or dead queries in this block: general path (wave-uniform)
     const bool qgen = q_gen[qb] != 0;
@@ -455,8 +485,35 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
 
 #define SHRIMP_CHUNK(NB, P) \
   attn_chunk<DP, HG, PAIR, NB, P>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, qf, m, l, o)
+#define SHRIMP_CHUNK_SEL(NB) \
+  attn_chunk<DP, HG, PAIR, NB, PATH_LINEAR, true>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, \
+                                                   qf, m, l, o)
     int kb = 0;
-    while (kb < nkb) {
+    if (!PAIR && linear_ok) {
+      // LINEAR everywhere: a token-query block selects in every chunk; else
+      // blocks with token / dead keys run alone with selects and the others
+      // in runs of up to 4.
+      while (kb < nkb) {
+        if (qgen) {
+          const int run = min(4, nkb - kb);
+          if (run == 4) SHRIMP_CHUNK_SEL(4);
+          else if (run >= 2) SHRIMP_CHUNK_SEL(2);
+          else SHRIMP_CHUNK_SEL(1);
+          kb += run == 4 ? 4 : (run >= 2 ? 2 : 1);
+        } else if (s.blk_gen[kb]) {
+          SHRIMP_CHUNK_SEL(1);
+          kb += 1;
+        } else {
+          int run = 1;
+          while (run < 4 && kb + run < nkb && !s.blk_gen[kb + run]) ++run;
+          if (run == 4) SHRIMP_CHUNK(4, PATH_LINEAR);
+          else if (run >= 2) SHRIMP_CHUNK(2, PATH_LINEAR);
+          else SHRIMP_CHUNK(1, PATH_LINEAR);
+          kb += run == 4 ? 4 : (run >= 2 ? 2 : 1);
+        }
+      }
+    }
+    while (!(!PAIR && linear_ok) && kb < nkb) {
       if (qgen || s.blk_gen[kb]) {
         SHRIMP_CHUNK(1, PATH_GENERAL);
         kb += 1;
@@ -468,10 +525,6 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
         if (run == 4) SHRIMP_CHUNK(4, PATH_CLAMP);
         else if (run >= 2) SHRIMP_CHUNK(2, PATH_CLAMP);
         else SHRIMP_CHUNK(1, PATH_CLAMP);
-      } else if (linear_ok) {
-        if (run == 4) SHRIMP_CHUNK(4, PATH_LINEAR);
-        else if (run >= 2) SHRIMP_CHUNK(2, PATH_LINEAR);
-        else SHRIMP_CHUNK(1, PATH_LINEAR);
       } else {
         if (run == 4) SHRIMP_CHUNK(4, PATH_CLAMP);
         else if (run >= 2) SHRIMP_CHUNK(2, PATH_CLAMP);
@@ -480,6 +533,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
       kb += run == 4 ? 4 : (run >= 2 ? 2 : 1);
     }
 #undef SHRIMP_CHUNK
+#undef SHRIMP_CHUNK_SEL
 
 #pragma unroll
     for (int h = 0; h < HG; ++h) {
@@ -518,7 +572,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
 // LDS bytes of one workgroup; npos = pair-table rows (pair mode only).
 static size_t attn_smem_bytes(int DP, int HG, int S, int npos, bool pair) {
   const size_t SP = (size_t)((S + 15) & ~15);
-  size_t bytes = 2 * HG * SP * DP * 2 + SP * (8 + 4 + 4) + (SP / 16) * 8;
+  size_t bytes = 2 * HG * SP * DP * 2 + SP * (8 + 4 + 4) + (SP / 16) * 8 + 3 * HG * 4;
   bytes += pair ? (size_t)npos * HG * 4 : (size_t)XW * XW * HG * 2;
   return bytes;
 }
