@@ -55,6 +55,7 @@ struct AttnLds {
   int* kkey;           // [SP] byte offset code (q*XW + r + XD*XW + XD) * 2 HG
   int* kcls;           // [SP] KEY_CELL / KEY_TOKEN / KEY_DEAD
   int* blk_gen;        // [SP / 16] 1 if the block holds a token or dead key
+  int* blk_dead;       // [SP / 16] 1 if the block holds a dead key (or keys past the bound)
   float* tokb;         // [3][HG] biases of (cell query, token key), (token query,
                        // cell key), (token, token), log2e folded
   float* tab;          // pair mode: [rows][HG] fp32 (log2e folded)
@@ -70,9 +71,17 @@ struct AttnQuery {
 
 // One chunk of NBK 16-key blocks (NBK in {1, 2, 4}) for the HG heads of one
 // 16-query block.
-// SEL (LINEAR path): the chunk holds token queries, token keys or dead keys;
-// their biases are selected per lane and dead keys dropped.
-template <int DP, int HG, bool PAIR, int NBK, int PATH, bool SEL = false>
+// LINEAR-path exceptions of a chunk (FL bits, compile time):
+//   FL_QTOK  the query block holds token queries: their biases toward cell
+//            keys are selected per lane;
+//   FL_KTOK  the chunk's first key block holds the token keys;
+//   FL_DEAD  the chunk holds dead keys: their V rows are staged as zeros and
+//            the row-sum MFMA weighs keys by liveness, so they drop out of
+//            both the output and the normaliser (their scores only enter the
+//            running maximum, which any finite value keeps exact).
+enum : int { FL_QTOK = 1, FL_KTOK = 2, FL_DEAD = 4 };
+
+template <int DP, int HG, bool PAIR, int NBK, int PATH, int FL = 0>
 SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, const AttnQuery& qi,
                            int kb0, int L, int SP, int lr, int lg, float qk_scale, int npos,
                            const u32x2 (&qf)[HG][DP / 16], float (&m)[HG], float (&l)[HG],
@@ -98,6 +107,15 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
   // Bias of every (key, head) of the chunk, fp32, log2e folded.
   float bias[NBK][4][HG];
   bool live[NBK][4];
+  // this lane's biases toward token keys and (token queries) cell keys
+  float tkb[HG], ckb[HG];
+  if (FL & (FL_QTOK | FL_KTOK)) {
+#pragma unroll
+    for (int h = 0; h < HG; ++h) {
+      tkb[h] = qi.qtok ? s.tokb[2 * HG + h] : s.tokb[h];
+      ckb[h] = s.tokb[HG + h];
+    }
+  }
 #pragma unroll
   for (int kb = 0; kb < NBK; ++kb)
 #pragma unroll
@@ -121,16 +139,14 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
 #pragma unroll
           for (int h = 0; h < HG; ++h) bias[kb][j][h] = (float)reinterpret_cast<const _Float16*>(xp)[h];
         }
-        if (SEL) {
-          const int cls = s.kcls[key];
-          const bool ktok = cls == KEY_TOKEN;
-          live[kb][j] = cls != KEY_DEAD;
+        if (FL & FL_QTOK) {
 #pragma unroll
-          for (int h = 0; h < HG; ++h) {
-            const float tk = qi.qtok ? s.tokb[2 * HG + h] : s.tokb[h];
-            const float ck = qi.qtok ? s.tokb[HG + h] : bias[kb][j][h];
-            bias[kb][j][h] = ktok ? tk : ck;
-          }
+          for (int h = 0; h < HG; ++h) bias[kb][j][h] = qi.qtok ? ckb[h] : bias[kb][j][h];
+        }
+        if ((FL & FL_KTOK) && kb == 0) {
+          const bool ktok = key < a.n_tokens;
+#pragma unroll
+          for (int h = 0; h < HG; ++h) bias[kb][j][h] = ktok ? tkb[h] : bias[kb][j][h];
         }
       } else {
         const int2 kk = s.kqr[key];
@@ -152,6 +168,14 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
   // Constant A fragment: row 0 of "V^T" is all ones, so P^T times it gives the
   // per-query sum of P in accumulator row 0 (lane group 0, element 0).
   const unsigned one2 = lr == 0 ? 0x3F803F80u : 0u;
+  // FL_DEAD: row 0 of the ones fragment carries 1 for live keys only.
+  // live2(key): bf16 pair (1 or 0 for keys key, key + 1) in row 0's lanes.
+  auto live2 = [&](int key) -> unsigned {
+    if (lr != 0) return 0u;
+    const unsigned lo = s.kcls[key] != KEY_DEAD ? 0x3F80u : 0u;
+    const unsigned hi = s.kcls[key + 1] != KEY_DEAD ? 0x3F80u : 0u;
+    return lo | (hi << 16);
+  };
 #pragma unroll
   for (int h = 0; h < HG; ++h) {
     float sc[NBK][4];
@@ -161,7 +185,7 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float v = fmaf(sc4[h][kb][j], qk_scale, bias[kb][j][h]);
-        if (PATH == PATH_GENERAL || SEL) v = live[kb][j] ? v : SHRIMP_NEG_BIG;
+        if (PATH == PATH_GENERAL) v = live[kb][j] ? v : SHRIMP_NEG_BIG;
         sc[kb][j] = v;
         mx = fmaxf(mx, v);
       }
@@ -176,7 +200,7 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         p[j] = __builtin_amdgcn_exp2f(sc[kb][j] - mnew);
-        if (PATH == PATH_GENERAL || SEL) p[j] = live[kb][j] ? p[j] : 0.f;
+        if (PATH == PATH_GENERAL) p[j] = live[kb][j] ? p[j] : 0.f;
       }
       pf[kb].x = pack_bf16x2(p[0], p[1]);
       pf[kb].y = pack_bf16x2(p[2], p[3]);
@@ -186,7 +210,11 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
 #pragma unroll
     for (int kd = 0; kd < KD; ++kd) acc[kd] = o[h][kd] * alpha;
     if (NBK == 1) {
-      const u32x2 ones = u32x2{one2, one2};
+      u32x2 ones = u32x2{one2, one2};
+      if (FL & FL_DEAD) {
+        const int k0 = kb0 * 16 + lg * 4;
+        ones = u32x2{live2(k0), live2(k0 + 2)};
+      }
       lacc = mfma16x16x16(ones, pf[0], lacc);
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd) {
@@ -195,11 +223,15 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
         acc[kd] = mfma16x16x16(vf, pf[0], acc[kd]);
       }
     } else {
-      const u32x4 ones = u32x4{one2, one2, one2, one2};
 #pragma unroll
       for (int kp = 0; kp < NBK; kp += 2) {
         // k slots 0-3 of lane group g: keys 4g..4g+3 of block kp; 4-7: of kp+1.
         const u32x4 pp = u32x4{pf[kp].x, pf[kp].y, pf[kp + 1].x, pf[kp + 1].y};
+        u32x4 ones = u32x4{one2, one2, one2, one2};
+        if (FL & FL_DEAD) {
+          const int k0 = (kb0 + kp) * 16 + lg * 4;
+          ones = u32x4{live2(k0), live2(k0 + 2), live2(k0 + 16), live2(k0 + 18)};
+        }
         lacc = mfma16x16x32(ones, pp, lacc);
 #pragma unroll
         for (int kd = 0; kd < KD; ++kd) {
@@ -241,7 +273,8 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   s.kcls = s.kkey + SP;
   s.blk_gen = s.kcls + SP;
   int* q_gen = s.blk_gen + NKB;
-  s.tokb = reinterpret_cast<float*>(q_gen + NKB);
+  s.blk_dead = q_gen + NKB;
+  s.tokb = reinterpret_cast<float*>(s.blk_dead + NKB);
   float* tail = s.tokb + 3 * HG;
   s.tab = tail;
   s.xtab = reinterpret_cast<_Float16*>(tail);
@@ -303,9 +336,12 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
         const int key = 2 * (rem / CH);
         const int ch = rem - (key / 2) * CH;
         const int64_t e0 = pos_base + (int64_t)(h0 + h) * a.qkv_sh + key * DP + ch * 8;
-        v0[u] = buf_load16(vrs, (i < total && key < L) ? (uint32_t)(e0 * 2) : SHRIMP_OOB_OFFSET);
-        v1[u] = buf_load16(vrs, (i < total && key + 1 < L) ? (uint32_t)((e0 + DP) * 2)
-                                                           : SHRIMP_OOB_OFFSET);
+        // dead keys (past the bound, or masked cells) stage zero V rows
+        const bool l0 = i < total && key < L && (PAIR || key < nt || a.mask[(int64_t)b * NC + key - nt]);
+        const bool l1 = i < total && key + 1 < L &&
+                        (PAIR || key + 1 < nt || a.mask[(int64_t)b * NC + key + 1 - nt]);
+        v0[u] = buf_load16(vrs, l0 ? (uint32_t)(e0 * 2) : SHRIMP_OOB_OFFSET);
+        v1[u] = buf_load16(vrs, l1 ? (uint32_t)((e0 + DP) * 2) : SHRIMP_OOB_OFFSET);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -407,15 +443,17 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   // Per-block flags, from the staged key classes: key blocks with a token, a
   // dead key or keys past the bound; query blocks with a token or dead query.
   for (int blk = tid; blk < LP / 16; blk += 256) {
-    int kg = 0, qg = 0;
+    int kg = 0, qg = 0, kd = 0;
     for (int j = 0; j < 16; ++j) {
       const int key = blk * 16 + j;
       const bool special = PAIR ? false : s.kcls[key] != KEY_CELL;
-      if (key >= L) kg = 1;
+      if (key >= L) kg = kd = 1;
       else if (special || key < nt) kg = qg = 1;
+      if (!PAIR && key < L && s.kcls[key] == KEY_DEAD) kd = 1;
     }
     s.blk_gen[blk] = kg;
     q_gen[blk] = qg;
+    s.blk_dead[blk] = kd;
   }
   if (!PAIR) {
     int q0 = span_red[0], q1 = span_red[1], r0 = span_red[2], r1 = span_red[3];
@@ -427,7 +465,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     }
     // LINEAR needs at least one live cell (its code stands in for token and
     // dead keys); an empty cell set gives q1 < q0 and takes the general path.
-    linear_ok = a.xtab != nullptr && q0 <= q1 && (q1 - q0) <= XD && (r1 - r0) <= XD;
+    linear_ok = a.xtab != nullptr && nt <= 16 && q0 <= q1 && (q1 - q0) <= XD && (r1 - r0) <= XD;
     // queries past the bound borrow (q0, r0): offsets to live cells stay in range
     safe_q = q0;
     safe_r = r0;
@@ -485,32 +523,40 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
 
 #define SHRIMP_CHUNK(NB, P) \
   attn_chunk<DP, HG, PAIR, NB, P>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, qf, m, l, o)
-#define SHRIMP_CHUNK_SEL(NB) \
-  attn_chunk<DP, HG, PAIR, NB, PATH_LINEAR, true>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, \
-                                                   qf, m, l, o)
+#define SHRIMP_CHUNK_FL(NB, F) \
+  attn_chunk<DP, HG, PAIR, NB, PATH_LINEAR, F>(a, s, qi, kb, L, SP, lr, lg, qk_scale, npos, \
+                                                qf, m, l, o)
+#define SHRIMP_CHUNK_FLS(NB)                          \
+  switch (fl) {                                       \
+    case 0: SHRIMP_CHUNK_FL(NB, 0); break;            \
+    case 1: SHRIMP_CHUNK_FL(NB, 1); break;            \
+    case 2: SHRIMP_CHUNK_FL(NB, 2); break;            \
+    case 3: SHRIMP_CHUNK_FL(NB, 3); break;            \
+    case 4: SHRIMP_CHUNK_FL(NB, 4); break;            \
+    case 5: SHRIMP_CHUNK_FL(NB, 5); break;            \
+    case 6: SHRIMP_CHUNK_FL(NB, 6); break;            \
+    default: SHRIMP_CHUNK_FL(NB, 7); break;           \
+  }
     int kb = 0;
     if (!PAIR && linear_ok) {
-      // LINEAR everywhere: a token-query block selects in every chunk; else
-      // blocks with token / dead keys run alone with selects and the others
-      // in runs of up to 4.
+      // LINEAR everywhere, in runs of four key blocks from block 0; each
+      // chunk's exceptions (token queries, token keys in block 0, dead keys)
+      // pick a compile-time variant.
+      const int qtokb = qb * 16 < nt ? FL_QTOK : 0;
       while (kb < nkb) {
-        if (qgen) {
-          const int run = min(4, nkb - kb);
-          if (run == 4) SHRIMP_CHUNK_SEL(4);
-          else if (run >= 2) SHRIMP_CHUNK_SEL(2);
-          else SHRIMP_CHUNK_SEL(1);
-          kb += run == 4 ? 4 : (run >= 2 ? 2 : 1);
-        } else if (s.blk_gen[kb]) {
-          SHRIMP_CHUNK_SEL(1);
-          kb += 1;
+        const int run = min(4, nkb - kb);
+        const int nb = run == 4 ? 4 : (run >= 2 ? 2 : 1);
+        int dead = 0;
+        for (int i = 0; i < nb; ++i) dead |= s.blk_dead[kb + i];
+        const int fl = qtokb | (kb == 0 && nt > 0 ? FL_KTOK : 0) | (dead ? FL_DEAD : 0);
+        if (nb == 4) {
+          SHRIMP_CHUNK_FLS(4)
+        } else if (nb == 2) {
+          SHRIMP_CHUNK_FLS(2)
         } else {
-          int run = 1;
-          while (run < 4 && kb + run < nkb && !s.blk_gen[kb + run]) ++run;
-          if (run == 4) SHRIMP_CHUNK(4, PATH_LINEAR);
-          else if (run >= 2) SHRIMP_CHUNK(2, PATH_LINEAR);
-          else SHRIMP_CHUNK(1, PATH_LINEAR);
-          kb += run == 4 ? 4 : (run >= 2 ? 2 : 1);
+          SHRIMP_CHUNK_FLS(1)
         }
+        kb += nb;
       }
     }
     while (!(!PAIR && linear_ok) && kb < nkb) {
@@ -533,7 +579,8 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
       kb += run == 4 ? 4 : (run >= 2 ? 2 : 1);
     }
 #undef SHRIMP_CHUNK
-#undef SHRIMP_CHUNK_SEL
+#undef SHRIMP_CHUNK_FL
+#undef SHRIMP_CHUNK_FLS
 
 #pragma unroll
     for (int h = 0; h < HG; ++h) {
@@ -572,7 +619,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
 // LDS bytes of one workgroup; npos = pair-table rows (pair mode only).
 static size_t attn_smem_bytes(int DP, int HG, int S, int npos, bool pair) {
   const size_t SP = (size_t)((S + 15) & ~15);
-  size_t bytes = 2 * HG * SP * DP * 2 + SP * (8 + 4 + 4) + (SP / 16) * 8 + 3 * HG * 4;
+  size_t bytes = 2 * HG * SP * DP * 2 + SP * (8 + 4 + 4) + (SP / 16) * 12 + 3 * HG * 4;
   bytes += pair ? (size_t)npos * HG * 4 : (size_t)XW * XW * HG * 2;
   return bytes;
 }
