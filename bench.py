@@ -260,7 +260,7 @@ def main() -> int:
             "trunk": LAYOUT, "support_radius": 4, "generator": "l256 seed 20261205",
         },
         "roofline": {
-            "kernel": "hex_conv_kernel<128,4,LN|RELU> (ConvBlock conv1, B=512 x 256 rows)",
+            "kernel": "hex_conv_big_kernel<LN|RELU> (ConvBlock conv1, B=512 x 256 rows)",
             "bound": "mfma",
             "achieved": round(conv_tflops, 2),
             "peak": PEAK_BF16_TFLOPS,
@@ -272,6 +272,7 @@ def main() -> int:
         },
         "attention": {
             "kernel": "attn_kernel<16,2,coords> (block 0)",
+            "bound": "valu (d=16: one exp + ~6 VALU per score vs 64 MFMA flops)",
             "launch_ms": round(kt["attn_ms"], 5),
             "tflops": round(attn_tflops, 2),
             "mfma_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
