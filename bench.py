@@ -48,9 +48,11 @@ def _events_time(fn, reps, stream):
 
 
 def kernel_timings(net, inputs, reps=50):
-    """Re-launch the trunk conv (ConvBlock conv1: conv + LN + ReLU + mask) and
-    the attention kernel of block 0 on the forward's own buffers; average
-    duration per launch from HIP events on the launch stream."""
+    """Re-launch single kernels of the forward on its own buffers (ConvBlock 0
+    as one launch, its conv1 alone, the attention kernel and the row kernels
+    of attention block 0); average duration per launch from HIP events on the
+    launch stream. Re-launches write into copies, never into the forward's
+    residual stream."""
 
     import torch
 
@@ -73,6 +75,17 @@ def kernel_timings(net, inputs, reps=50):
             x=cells, x_sb=s * C, x_sn=C, idx=L["idx"], taps=7, idx_stride=7, mask8=L["mask8"],
             wpack=k.w1, bias=k.b1, B=b, N=n, cin_pad=C, cout=C, ln_w=k.ln1w, ln_b=k.ln1b,
             eps=k.eps1, relu=True, out=L["y1"], o_sb=n * C, o_sn=C, stream=L["stream"],
+        )
+
+    # same (position, row) strides as `cells` (a clone of the view would be compact)
+    cells_out = L["seq"].clone()[:, 8:]
+
+    def block():
+        ops.launch_conv_block(
+            x=cells, x_sb=s * C, x_sn=C, idx=L["idx"], idx_stride=7, mask8=L["mask8"], B=b, N=n,
+            C=C, w1=k.w1, b1=k.b1, ln1_w=k.ln1w, ln1_b=k.ln1b, eps1=k.eps1, w2=k.w2, b2=k.b2,
+            ln2_w=k.ln2w, ln2_b=k.ln2b, eps2=k.eps2, gamma=k.gamma, out=cells_out,
+            o_sb=s * C, o_sn=C, stream=L["stream"],
         )
 
     a = P.attn[0]
@@ -125,8 +138,10 @@ def kernel_timings(net, inputs, reps=50):
                     rows * 2 * C * C * 2.0, rows * 4 * C * 2.0),
         })
     conv()
+    block()
     attn()
     conv_ms = _events_time(conv, reps, stream)
+    block_ms = _events_time(block, reps, stream)
     attn_ms = _events_time(attn, reps, stream)
     extra = {}
     for name, (fn, flops, nbytes) in linears.items():
@@ -137,6 +152,9 @@ def kernel_timings(net, inputs, reps=50):
     seq_lens = L["seq_lens"].cpu().to(torch.float64)
     valid_rows = int(L["mask8"].sum().item())
     return {
+        "block_ms": block_ms,
+        "block_flops": 2 * 2.0 * 7 * C * C * b * n,
+        "block_bytes": b * n * C * 2 * 2 + b * n * 7 * 4 + b * n + 2 * 7 * C * C * 2,
         "conv_ms": conv_ms,
         "conv_flops": 2.0 * 7 * C * C * b * n,
         "conv_flops_valid": 2.0 * 7 * C * C * valid_rows,
@@ -234,10 +252,11 @@ def main() -> int:
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     kt = kernel_timings(net, inputs)
 
+    block_tflops = kt["block_flops"] / (kt["block_ms"] * 1e-3) / 1e12
     conv_tflops = kt["conv_flops"] / (kt["conv_ms"] * 1e-3) / 1e12
     attn_tflops = kt["attn_flops"] / (kt["attn_ms"] * 1e-3) / 1e12
     traffic = None
-    tfile = ROOT / "profiles" / "conv_traffic.json"
+    tfile = ROOT / "profiles" / "block_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
     line = {
@@ -260,15 +279,23 @@ def main() -> int:
             "trunk": LAYOUT, "support_radius": 4, "generator": "l256 seed 20261205",
         },
         "roofline": {
-            "kernel": "hex_conv_big_kernel<LN|RELU> (ConvBlock conv1, B=512 x 256 rows)",
+            "kernel": "hex_block_kernel (ConvBlock 0: conv1 + LN + ReLU, conv2 + LN + "
+                      "LayerScale residual + ReLU; B=512 x 256 rows)",
             "bound": "mfma",
-            "achieved": round(conv_tflops, 2),
+            "achieved": round(block_tflops, 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(conv_tflops / PEAK_BF16_TFLOPS, 4),
+            "frac": round(block_tflops / PEAK_BF16_TFLOPS, 4),
             "traffic": traffic,
+            "algorithmic_bytes": kt["block_bytes"],
+            "launch_ms": round(kt["block_ms"], 5),
+            "flops_per_launch": kt["block_flops"],
+        },
+        "single_conv": {
+            "kernel": "hex_conv_big_kernel<LN|RELU> (ConvBlock 0 conv1 alone)",
             "launch_ms": round(kt["conv_ms"], 5),
-            "flops_per_launch": kt["conv_flops"],
+            "tflops": round(conv_tflops, 2),
+            "mfma_frac": round(conv_tflops / PEAK_BF16_TFLOPS, 4),
         },
         "attention": {
             "kernel": "attn_kernel<16,2,coords> (block 0)",

@@ -32,20 +32,25 @@ enum : int { EPI_LN = 1, EPI_RELU = 2, EPI_RESID = 4, EPI_HEAD = 8 };
 // loads this lane's channels once into registers (re-reading after a store
 // would wait, since the compiler must assume the store may alias them);
 // PS_LDS reads them from an LDS copy at `lp` laid out [bias | ln_w | ln_b |
-// gamma or head_w], COUT floats each.
-// The row masks are loaded up front and the residual rows of block mb+1 are
-// requested before block mb's math.
+// gamma or head_w | zeros], COUT floats each. With LDS parameters a masked
+// row gets LayerNorm scale 0 and its ln_b from the zero slot, so the
+// LayerNorm itself yields exact zeros and no per-value select is needed.
+// The residual rows are requested RD blocks ahead of their use.
+// `store(mb, nb, u32x2)` receives 4 packed bf16 channels 16 nb + 4 lg .. + 3
+// of row block mb, for rows that exist.
 enum : int { PS_GLOBAL = 0, PS_REGS = 1, PS_LDS = 2 };
 
-template <int COUT, int MB, int EPI, int PSRC>
+template <int COUT, int MB, int EPI, int PSRC, typename Store>
 SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16][MB],
                               const int (&rb)[MB], const int (&rn)[MB], const bool (&rv)[MB],
-                              int lg, const float* lp = nullptr) {
+                              int lg, const float* lp, Store&& store) {
   constexpr int NB = COUT / 16;
   constexpr bool LN = (EPI & EPI_LN) != 0, RESID = (EPI & EPI_RESID) != 0;
-  constexpr bool HEAD = (EPI & EPI_HEAD) != 0;
+  constexpr bool HEAD = (EPI & EPI_HEAD) != 0, RELU = (EPI & EPI_RELU) != 0;
   constexpr bool PRE = PSRC == PS_REGS;
+  constexpr bool LNMASK = LN && PSRC == PS_LDS;  // masking folded into the LayerNorm
   constexpr int PN = PRE ? NB : 1;
+  constexpr int RD = MB < 3 ? MB : 3;  // residual prefetch depth (row blocks)
   const int N = a.N;
   f32x4 pb[PN], pw[LN ? PN : 1], pl[LN ? PN : 1], pg[RESID ? PN : 1], ph[HEAD ? PN : 1];
   auto prm = [&](const float* p, int nb) { return *reinterpret_cast<const f32x4*>(p + nb * 16 + lg * 4); };
@@ -86,14 +91,14 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
         r[nb] = rv[mb] ? *reinterpret_cast<const u32x2*>(rp + nb * 16) : u32x2{0u, 0u};
     }
   };
-  u32x2 rcur[RESID ? NB : 1], rnext[RESID ? NB : 1];
-  if constexpr (RESID) resid_row(0, rcur);
+  u32x2 rbuf[RESID ? RD : 1][RESID ? NB : 1];
+  if constexpr (RESID) {
+#pragma unroll
+    for (int i = 0; i < RD; ++i) resid_row(i, rbuf[i]);
+  }
 
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
-    if constexpr (RESID) {
-      if (mb + 1 < MB) resid_row(mb + 1, rnext);
-    }
     float v[NB][4];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -116,21 +121,27 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
           v[nb][j] -= mean;
           q += v[nb][j] * v[nb][j];
         }
-      const float rstd = rsqrtf(sum_groups_swap(q) * (1.0f / COUT) + a.eps);
+      float rstd = rsqrtf(sum_groups_swap(q) * (1.0f / COUT) + a.eps);
+      int bslot = 2;
+      if constexpr (LNMASK) {
+        rstd = live[mb] ? rstd : 0.f;
+        bslot = live[mb] ? 2 : 4;
+      }
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const f32x4 gw = P_w(nb), gb = P_l(nb);
+        const f32x4 gw = P_w(nb);
+        const f32x4 gb = LNMASK ? prm(lp + bslot * COUT, nb) : P_l(nb);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[nb][j] = v[nb][j] * rstd * gw[j] + gb[j];
+        for (int j = 0; j < 4; ++j) v[nb][j] = fmaf(v[nb][j] * rstd, gw[j], gb[j]);
       }
     }
-    if (EPI & EPI_RELU) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[nb][j] = fmaxf(v[nb][j], 0.f);
-    }
     if constexpr (HEAD) {
+      if constexpr (RELU) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[nb][j] = fmaxf(v[nb][j], 0.f);
+      }
       float h = 0.f;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
@@ -142,32 +153,65 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
       if (rv[mb] && lg == 0) a.head_out[(int64_t)rb[mb] * N + rn[mb]] = live[mb] ? h + hb : 0.f;
       continue;
     }
+    // ReLU and the row mask in one clamp: med3(v, 0, +inf) = relu(v), med3(v, 0, 0) = 0.
+    const float cap = live[mb] ? __builtin_inff() : 0.f;
     if (rv[mb]) {
-      unsigned short* op = static_cast<unsigned short*>(a.out) + (int64_t)rb[mb] * a.o_sb +
-                           (int64_t)rn[mb] * a.o_sn + lg * 4;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         float o[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = live[mb] ? v[nb][j] : 0.f;
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (LNMASK) o[j] = v[nb][j];
+          else if constexpr (RELU && !RESID) o[j] = __builtin_amdgcn_fmed3f(v[nb][j], 0.f, cap);
+          else o[j] = live[mb] ? v[nb][j] : 0.f;
+        }
         if constexpr (RESID) {
-          const u32x2 rw = rcur[nb];
+          const u32x2 rw = rbuf[mb % RD][nb];
           const f32x4 g = P_g(nb);
-          o[0] = fmaxf(bf16_lo(rw.x) + g[0] * o[0], 0.f);
-          o[1] = fmaxf(bf16_hi(rw.x) + g[1] * o[1], 0.f);
-          o[2] = fmaxf(bf16_lo(rw.y) + g[2] * o[2], 0.f);
-          o[3] = fmaxf(bf16_hi(rw.y) + g[3] * o[3], 0.f);
+          o[0] = fmaxf(fmaf(g[0], o[0], bf16_lo(rw.x)), 0.f);
+          o[1] = fmaxf(fmaf(g[1], o[1], bf16_hi(rw.x)), 0.f);
+          o[2] = fmaxf(fmaf(g[2], o[2], bf16_lo(rw.y)), 0.f);
+          o[3] = fmaxf(fmaf(g[3], o[3], bf16_hi(rw.y)), 0.f);
+        } else if constexpr (LNMASK && RELU) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = fmaxf(o[j], 0.f);
         }
         u32x2 pk;
         pk.x = pack_bf16x2(o[0], o[1]);
         pk.y = pack_bf16x2(o[2], o[3]);
-        *reinterpret_cast<u32x2*>(op + nb * 16) = pk;
+        store(mb, nb, pk);
       }
     }
     if constexpr (RESID) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) rcur[nb] = rnext[nb];
+      if (mb + RD < MB) resid_row(mb + RD, rbuf[mb % RD]);
     }
+  }
+}
+
+// Store functor of the epilogue: rows of `a.out` (bf16, strides o_sb / o_sn).
+template <int MB>
+struct GlobalRowStore {
+  unsigned short* p[MB];
+  SHRIMP_DEV GlobalRowStore(const shrimp_conv_args& a, const int (&rb)[MB], const int (&rn)[MB],
+                            int lg) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      p[mb] = static_cast<unsigned short*>(a.out) + (int64_t)rb[mb] * a.o_sb +
+              (int64_t)rn[mb] * a.o_sn + lg * 4;
+  }
+  SHRIMP_DEV void operator()(int mb, int nb, u32x2 pk) const {
+    *reinterpret_cast<u32x2*>(p[mb] + nb * 16) = pk;
+  }
+};
+
+template <int COUT, int MB, int EPI, int PSRC>
+SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16][MB],
+                              const int (&rb)[MB], const int (&rn)[MB], const bool (&rv)[MB],
+                              int lg, const float* lp = nullptr) {
+  if constexpr ((EPI & EPI_HEAD) != 0) {
+    conv_epilogue<COUT, MB, EPI, PSRC>(a, acc, rb, rn, rv, lg, lp, [](int, int, u32x2) {});
+  } else {
+    conv_epilogue<COUT, MB, EPI, PSRC>(a, acc, rb, rn, rv, lg, lp, GlobalRowStore<MB>(a, rb, rn, lg));
   }
 }
 
@@ -406,138 +450,137 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
 // prefetch (vmcnt retires in issue order, so a weight wait never waits for
 // an HBM row load), and a barrier publishes it at the chunk boundary.
 constexpr int BIG_MAX_N = 512;
+constexpr int BIG_PARAMS = 5 * 128;  // floats: [bias | ln_w | ln_b | gamma or head_w | zeros]
 
-SHRIMP_DEV int big_rows_padded(int N) { return ((N + 1 + 15) / 16) * 16; }
+__host__ __device__ inline int big_rows_padded(int N) { return ((N + 1 + 15) / 16) * 16; }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int EPI>
-__global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_args a,
-                                                              uint32_t x_bytes, uint32_t w_bytes) {
-  constexpr int COUT = 128, CIN = 128, KC = CIN / 32;
-  constexpr int T = 7, MB = 8, NB = COUT / 16;
-  extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
+// Per-wave state of a big-tile workgroup (position b, rows 128 wave .. + 127).
+struct BigTile {
+  int lane, wave, nw, lg, N, NR, groups, mine, b;
+  __amdgpu_buffer_rsrc_t xr;
+  uint32_t xbase, xsn2;
+  int rb[8], rn[8];
+  bool rv[8];
+  uint32_t sw2[7][4];  // neighbour row addresses, two 16-bit values per register
+};
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int nw = blockDim.x >> 6;
-  const int lr = lane & 15;
-  const int lg = lane >> 4;
-  const int N = a.N;
-  const int NR = big_rows_padded(N);
-  const int groups = NR / 16;  // DMA instructions per chunk
-  const int b = blockIdx.x;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes);
-  const uint32_t xbase = (uint32_t)((int64_t)b * a.x_sb * 2);
-
-  // DMA of chunk kc, rows [16 g, 16 g + 16): lane -> row 16 g + lane / 4, slot lane % 4.
-  auto dma = [&](int kc, int g) {
-    const int r = g * 16 + (lane >> 2);
-    const int piece = (lane & 3) ^ ((r >> 2) & 3);
-    const uint32_t off = r < N ? xbase + (uint32_t)(r * a.x_sn * 2) + (uint32_t)((kc * 4 + piece) * 16)
+// DMA of chunk kc, rows [16 g, 16 g + 16): lane -> row 16 g + lane / 4, slot lane % 4.
+SHRIMP_DEV void big_dma(unsigned char* xs, const BigTile& t, int kc, int g) {
+  const int r = g * 16 + (t.lane >> 2);
+  const int piece = (t.lane & 3) ^ ((r >> 2) & 3);
+  const uint32_t off = r < t.N ? t.xbase + (uint32_t)r * t.xsn2 + (uint32_t)((kc * 4 + piece) * 16)
                                : SHRIMP_OOB_OFFSET;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        xr, (lds_void_t*)(xs + (kc * NR + g * 16) * 64), 16, off, 0, 0, 0);
-  };
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(t.xr, (lds_void_t*)(xs + (kc * t.NR + g * 16) * 64), 16,
+                                           off, 0, 0, 0);
+}
 
-  // Prologue: chunk 0 by DMA, the neighbour indices of all taps, the first
-  // weight fragments and the epilogue parameters, then one barrier.
-  for (int g = wave; g < groups; g += nw) dma(0, g);
-  const int row0 = wave * (MB * 16);
-  int rn[MB], rb[MB];
-  bool rv[MB];
-  const int* idxb = a.idx + (int64_t)b * N * a.idx_stride;
+// Requests chunk 0 by DMA and turns the neighbour indices of this wave's rows
+// into swizzled 16-bit LDS row addresses j * 64 | ((j >> 2) & 3) << 4.
+SHRIMP_DEV void big_setup(BigTile& t, const shrimp_conv_args& a, unsigned char* xs,
+                          uint32_t x_bytes) {
+  constexpr int T = 7, MB = 8;
+  t.lane = threadIdx.x & 63;
+  t.wave = threadIdx.x >> 6;
+  t.nw = blockDim.x >> 6;
+  t.lg = t.lane >> 4;
+  t.N = a.N;
+  t.NR = big_rows_padded(a.N);
+  t.groups = t.NR / 16;
+  t.mine = (t.groups - t.wave + t.nw - 1) / t.nw;
+  t.b = blockIdx.x;
+  t.xr = make_rsrc(a.x, x_bytes);
+  t.xbase = (uint32_t)((int64_t)t.b * a.x_sb * 2);
+  t.xsn2 = (uint32_t)(a.x_sn * 2);
+  for (int g = t.wave; g < t.groups; g += t.nw) big_dma(xs, t, 0, g);
+  const int row0 = t.wave * (MB * 16);
+  const int* idxb = a.idx + (int64_t)t.b * t.N * a.idx_stride;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
-    rb[mb] = b;
-    rn[mb] = row0 + mb * 16 + lr;
-    rv[mb] = rn[mb] < N;
+    t.rb[mb] = t.b;
+    t.rn[mb] = row0 + mb * 16 + (t.lane & 15);
+    t.rv[mb] = t.rn[mb] < t.N;
   }
   int jr[T][MB];
 #pragma unroll
-  for (int t = 0; t < T; ++t)
+  for (int tp = 0; tp < T; ++tp)
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) jr[t][mb] = rv[mb] ? idxb[rn[mb] * a.idx_stride + t] : N;
-
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, w_bytes);
-  auto wload = [&](int s, u32x4 (&w)[NB]) {
+    for (int mb = 0; mb < MB; ++mb) jr[tp][mb] = t.rv[mb] ? idxb[t.rn[mb] * a.idx_stride + tp] : t.N;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) w[nb] = buf_load16(wr, (uint32_t)(((s * NB + nb) * 64 + lane) * 16));
-  };
-  u32x4 wf[NB];
-  wload(0, wf);
-
-  // epilogue parameters after the rows: [bias | ln_w | ln_b | gamma or head_w]
-  float* lp = reinterpret_cast<float*>(xs + KC * NR * 64);
-  {
-    const float* src[4] = {a.bias, a.ln_w, a.ln_b, (EPI & EPI_HEAD) ? a.head_w : a.gamma};
-    for (int i = threadIdx.x; i < 4 * COUT; i += blockDim.x) {
-      const float* sp = src[i / COUT];
-      lp[i] = sp ? sp[i % COUT] : 0.f;
-    }
-  }
-
-  // Neighbour rows as 16-bit row addresses within a chunk region:
-  // j * 64 | ((j >> 2) & 3) << 4 (the piece swizzle); two per register.
-  uint32_t sw2[T][MB / 2];
-#pragma unroll
-  for (int t = 0; t < T; ++t)
+  for (int tp = 0; tp < T; ++tp)
 #pragma unroll
     for (int m2 = 0; m2 < MB / 2; ++m2) {
       uint32_t pk = 0;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int j = jr[t][2 * m2 + h];
-        const int jj = (j >= 0 && j < N) ? j : N;
+        const int j = jr[tp][2 * m2 + h];
+        const int jj = (j >= 0 && j < t.N) ? j : t.N;
         pk |= (uint32_t)(jj * 64 + (((jj >> 2) & 3) << 4)) << (16 * h);
       }
-      sw2[t][m2] = pk;
+      t.sw2[tp][m2] = pk;
     }
+}
 
-  auto xload = [&](int t, int kc, u32x4 (&x)[MB]) {
-    const uint32_t kbase = (uint32_t)(kc * NR * 64);
-    const uint32_t ls = (uint32_t)lg << 4;
+// Epilogue parameters of one conv into LDS: [bias | ln_w | ln_b | extra | zeros].
+SHRIMP_DEV void big_params(float* lp, const float* bias, const float* ln_w, const float* ln_b,
+                           const float* extra) {
+  const float* src[4] = {bias, ln_w, ln_b, extra};
+  for (int i = threadIdx.x; i < BIG_PARAMS; i += blockDim.x) {
+    const float* sp = i < 4 * 128 ? src[i / 128] : nullptr;
+    lp[i] = sp ? sp[i % 128] : 0.f;
+  }
+}
+
+// Weight fragments of k-step s (8 output blocks).
+SHRIMP_DEV void big_wload(__amdgpu_buffer_rsrc_t wr, int s, int lane, u32x4 (&w)[8]) {
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) w[nb] = buf_load16(wr, (uint32_t)(((s * 8 + nb) * 64 + lane) * 16));
+}
+
+// One 7-tap, 128 -> 128 conv over the rows in LDS: acc += sum_t W_t^T X[idx_t]^T.
+// On entry wf holds k-step 0 of `wr`; with NEXT, on exit it holds k-step 0 of
+// `wnext`. With STAGE, chunks 1..3 are still to be requested: chunk kc+1 is
+// spread over the 7 tap steps of chunk kc and a barrier publishes it.
+template <bool STAGE, bool NEXT>
+SHRIMP_DEV void big_pass(f32x4 (&acc)[8][8], u32x4 (&wf)[8], const BigTile& t,
+                         unsigned char* xs, __amdgpu_buffer_rsrc_t wr,
+                         __amdgpu_buffer_rsrc_t wnext) {
+  constexpr int KC = 4, T = 7, MB = 8, NB = 8;
+  auto xload = [&](int tp, int kc, u32x4 (&x)[MB]) {
+    const uint32_t kbase = (uint32_t)(kc * t.NR * 64);
+    const uint32_t ls = (uint32_t)t.lg << 4;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      const uint32_t v = (sw2[t][mb >> 1] >> (16 * (mb & 1))) & 0xFFFFu;
+      const uint32_t v = (t.sw2[tp][mb >> 1] >> (16 * (mb & 1))) & 0xFFFFu;
       x[mb] = *reinterpret_cast<const u32x4*>(xs + kbase + (v ^ ls));
     }
   };
-
-  f32x4 acc[NB][MB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  // Every wave owns rows (waves = ceil(N / 128)), so no wave skips the MFMAs;
-  // the chunk loop is fully unrolled so that no value crosses a branch.
-  const int mine = (groups - wave + nw - 1) / nw;  // DMA groups of this wave per chunk
+  // The chunk loop is fully unrolled so that no value crosses a branch.
 #pragma unroll
   for (int kc = 0; kc < KC; ++kc) {
     const bool more = kc + 1 < KC;
     u32x4 xf[MB];
     xload(0, kc, xf);
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
+    for (int tp = 0; tp < T; ++tp) {
       u32x4 xc[MB], wc[NB];
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) xc[mb] = xf[mb];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) wc[nb] = wf[nb];
-      if (t + 1 < T) {
-        xload(t + 1, kc, xf);
-        wload((t + 1) * KC + kc, wf);
+      if (tp + 1 < T) {
+        xload(tp + 1, kc, xf);
+        big_wload(wr, (tp + 1) * KC + kc, t.lane, wf);
       } else if (more) {
-        wload(kc + 1, wf);
+        big_wload(wr, kc + 1, t.lane, wf);
+      } else if (NEXT) {
+        big_wload(wnext, 0, t.lane, wf);
       }
-      if (more) {
+      if (STAGE && more) {
         // this wave's DMA groups i in [i0, i1) of chunk kc + 1
-        const int i0 = (t * mine) / T, i1 = ((t + 1) * mine) / T;
-        for (int i = i0; i < i1; ++i) dma(kc + 1, wave + i * nw);
+        const int i0 = (tp * t.mine) / T, i1 = ((tp + 1) * t.mine) / T;
+        for (int i = i0; i < i1; ++i) big_dma(xs, t, kc + 1, t.wave + i * t.nw);
       }
       // Keep the next step's loads ahead of this step's MFMAs (the scheduler
       // would otherwise sink them next to their uses).
@@ -548,12 +591,99 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
         for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = mfma16x16x32(wc[nb], xc[mb], acc[nb][mb]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (more) {
+    if (STAGE && more) {
       __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA of chunk kc + 1 has landed
       __syncthreads();
     }
   }
-  conv_epilogue<COUT, MB, EPI, PS_LDS>(a, acc, rb, rn, rv, lg, lp);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_args a,
+                                                              uint32_t x_bytes, uint32_t w_bytes) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
+  BigTile t;
+  big_setup(t, a, xs, x_bytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, w_bytes);
+  u32x4 wf[8];
+  big_wload(wr, 0, t.lane, wf);
+  float* lp = reinterpret_cast<float*>(xs + 4 * t.NR * 64);
+  big_params(lp, a.bias, a.ln_w, a.ln_b, (EPI & EPI_HEAD) ? a.head_w : a.gamma);
+  f32x4 acc[8][8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  big_pass<true, false>(acc, wf, t, xs, wr, wr);
+  conv_epilogue<128, 8, EPI, PS_LDS>(a, acc, t.rb, t.rn, t.rv, t.lg, lp);
+}
+
+// ConvBlock in one launch (ConvBlock.forward, model.py:395-422):
+//   y1  = relu(LN1(conv1(x))) * m          -> written into LDS over x's rows
+//   out = relu(x + gamma * LN2(conv2(y1)) * m)
+// conv1 stages x and runs as the big-tile conv; after a barrier its epilogue
+// writes y1 (bf16, masked rows zero) into the same LDS layout, and conv2
+// gathers from there, so y1 never reaches HBM. The zero row N stays zero.
+// `c2.resid` is x and `c2.out` may alias it: a lane reads the residual
+// elements it later overwrites, and a position only touches its own rows.
+__global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_args c1,
+                                                           const shrimp_conv_args c2,
+                                                           uint32_t x_bytes, uint32_t w_bytes) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
+  BigTile t;
+  big_setup(t, c1, xs, x_bytes);
+  const __amdgpu_buffer_rsrc_t wr1 = make_rsrc(c1.w, w_bytes);
+  const __amdgpu_buffer_rsrc_t wr2 = make_rsrc(c2.w, w_bytes);
+  u32x4 wf[8];
+  big_wload(wr1, 0, t.lane, wf);
+  float* lp1 = reinterpret_cast<float*>(xs + 4 * t.NR * 64);
+  float* lp2 = lp1 + BIG_PARAMS;
+  big_params(lp1, c1.bias, c1.ln_w, c1.ln_b, nullptr);
+  big_params(lp2, c2.bias, c2.ln_w, c2.ln_b, c2.gamma);
+  f32x4 acc[8][8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  big_pass<true, true>(acc, wf, t, xs, wr1, wr2);
+  __syncthreads();  // every wave is done reading x from LDS
+  {
+    const uint32_t nr64 = (uint32_t)t.NR * 64;
+    const uint32_t lo = (uint32_t)(t.lg & 1) * 8;
+    uint32_t row[8], swz[8];
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      row[mb] = (uint32_t)t.rn[mb] * 64;
+      swz[mb] = (uint32_t)((t.rn[mb] >> 2) & 3);
+    }
+    const int lg = t.lg;
+    conv_epilogue<128, 8, EPI_LN | EPI_RELU, PS_LDS>(
+        c1, acc, t.rb, t.rn, t.rv, t.lg, lp1, [&](int mb, int nb, u32x2 pk) {
+          const uint32_t piece = (uint32_t)((nb & 1) * 2 + (lg >> 1));
+          const uint32_t addr = (uint32_t)(nb >> 1) * nr64 + row[mb] + ((piece ^ swz[mb]) << 4) + lo;
+          *reinterpret_cast<u32x2*>(xs + addr) = pk;
+        });
+  }
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  __syncthreads();  // y1 is complete
+  // Hide the per-lane addresses from the optimizer: otherwise it keeps conv1's
+  // LDS row and weight offsets alive (spilled) for reuse by conv2 instead of
+  // recomputing them.
+#pragma unroll
+  for (int tp = 0; tp < 7; ++tp)
+#pragma unroll
+    for (int m2 = 0; m2 < 4; ++m2) asm volatile("" : "+v"(t.sw2[tp][m2]));
+  asm volatile("" : "+v"(t.lane));
+  t.lg = t.lane >> 4;
+  big_pass<false, false>(acc, wf, t, xs, wr2, wr2);
+  conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(c2, acc, t.rb, t.rn, t.rv, t.lg, lp2);
 }
 
 // ---- weight packing ------------------------------------------------------------
@@ -592,14 +722,12 @@ static int launch_conv(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, size
   if (COUT == 128 && lds && a->cin_pad == 128 && a->taps == 7 && a->N <= BIG_MAX_N &&
       (g_conv_variant == 0 || g_conv_variant == 3)) {
     const int waves = (a->N + 127) / 128;
-    const int nr = ((a->N + 1 + 15) / 16) * 16;
-    const size_t big_lds = (size_t)nr * 256 + 4 * 128 * sizeof(float);
+    const size_t big_lds = (size_t)big_rows_padded(a->N) * 256 + BIG_PARAMS * sizeof(float);
     if (big_lds <= (size_t)max_lds_per_block()) {
       hipLaunchKernelGGL((hex_conv_big_kernel<EPI>), dim3(a->B), dim3(64 * waves), big_lds, st, *a,
                          xb, wb);
       return check_launch("hex_conv");
     }
-    return check_launch("hex_conv");
   }
   if (lds) {
     switch (a->cin_pad) {
@@ -740,4 +868,53 @@ extern "C" int shrimp_hex_conv(const shrimp_conv_args* a, void* stream) {
   }
   return a->relu ? dispatch_cout<EPI_RELU>(a, xb, wb, lds, st)
                  : dispatch_cout<0>(a, xb, wb, lds, st);
+}
+
+extern "C" int shrimp_conv_block_supported(int taps, int N, int cin_pad, int cout) {
+  if (taps != 7 || cin_pad != 128 || cout != 128 || N <= 0 || N > BIG_MAX_N) return 0;
+  if (g_conv_variant != 0 && g_conv_variant != 3) return 0;
+  const size_t lds = (size_t)big_rows_padded(N) * 256 + 2 * BIG_PARAMS * sizeof(float);
+  return lds <= (size_t)max_lds_per_block() ? 1 : 0;
+}
+
+extern "C" int shrimp_conv_block(const shrimp_conv_args* c1, const shrimp_conv_args* c2,
+                                 void* stream) {
+  SHRIMP_REQUIRE(c1 != nullptr && c2 != nullptr, "conv_block: null args");
+  SHRIMP_REQUIRE(c1->B >= 0 && c1->N > 0, "conv_block: bad B/N (%d, %d)", c1->B, c1->N);
+  SHRIMP_REQUIRE(shrimp_conv_block_supported(c1->taps, c1->N, c1->cin_pad, c1->cout) &&
+                     c2->cin_pad == 128 && c2->cout == 128,
+                 "conv_block: no fused kernel for taps %d, N %d, %d -> %d channels", c1->taps,
+                 c1->N, c1->cin_pad, c1->cout);
+  if (c1->B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(c1->x && c1->idx && c1->mask && c1->w && c1->bias && c2->w && c2->bias,
+                 "conv_block: null input pointer");
+  SHRIMP_REQUIRE(c1->idx_stride >= 7, "conv_block: idx_stride %d < 7", c1->idx_stride);
+  SHRIMP_REQUIRE(c1->ln_w && c1->ln_b && c1->relu && !c1->resid && !c1->head_w,
+                 "conv_block: conv1 must be conv + LN + ReLU");
+  SHRIMP_REQUIRE(c2->ln_w && c2->ln_b && !c2->relu && c2->gamma && !c2->head_w && c2->out,
+                 "conv_block: conv2 must be conv + LN + LayerScale residual");
+  SHRIMP_REQUIRE(c2->resid == c1->x && c2->r_sb == c1->x_sb && c2->r_sn == c1->x_sn,
+                 "conv_block: the residual must be the block input");
+  SHRIMP_REQUIRE((reinterpret_cast<uintptr_t>(c1->x) & 15) == 0 && c1->x_sn >= 128 &&
+                     c1->x_sn % 8 == 0 && c1->x_sb % 8 == 0,
+                 "conv_block: x rows must be 16-byte aligned");
+  SHRIMP_REQUIRE(c2->o_sn % 4 == 0 && c2->o_sb % 4 == 0, "conv_block: output strides %% 4");
+  const int64_t x_extent =
+      (int64_t)(c1->B - 1) * c1->x_sb + (int64_t)(c1->N - 1) * c1->x_sn + c1->cin_pad;
+  SHRIMP_REQUIRE(x_extent * 2 < (int64_t)0x7FFF0000, "conv_block: activation buffer too large");
+  shrimp_conv_args a2 = *c2;
+  a2.x = c1->x;
+  a2.x_sb = c1->x_sb;
+  a2.x_sn = c1->x_sn;
+  a2.idx = c1->idx;
+  a2.taps = 7;
+  a2.idx_stride = c1->idx_stride;
+  a2.mask = c1->mask;
+  a2.B = c1->B;
+  a2.N = c1->N;
+  const int waves = (c1->N + 127) / 128;
+  const size_t lds = (size_t)big_rows_padded(c1->N) * 256 + 2 * BIG_PARAMS * sizeof(float);
+  hipLaunchKernelGGL(hex_block_kernel, dim3(c1->B), dim3(64 * waves), lds, as_stream(stream), *c1,
+                     a2, (uint32_t)(x_extent * 2), (uint32_t)shrimp_conv_wpack_bytes(7, 128, 128));
+  return check_launch("conv_block");
 }

@@ -105,6 +105,8 @@ SIGNATURES: dict = {
     "shrimp_linear_wpack_bytes": (ctypes.c_size_t, [ctypes.c_int] * 2),
     "shrimp_pack_linear_weight": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp]),
     "shrimp_hex_conv": (ctypes.c_int, [ctypes.POINTER(ConvArgs), _vp]),
+    "shrimp_conv_block_supported": (ctypes.c_int, [ctypes.c_int] * 4),
+    "shrimp_conv_block": (ctypes.c_int, [ctypes.POINTER(ConvArgs), ctypes.POINTER(ConvArgs), _vp]),
     "shrimp_linear": (ctypes.c_int, [ctypes.POINTER(LinearArgs), _vp]),
     "shrimp_attn_qkv": (ctypes.c_int, [ctypes.POINTER(QkvArgs), _vp]),
     "shrimp_attn_qkv_pack_bytes": (ctypes.c_size_t, [ctypes.c_int]),

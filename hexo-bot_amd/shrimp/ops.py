@@ -147,11 +147,29 @@ def attn_bias_table(table: torch.Tensor, lut_u8: torch.Tensor, lut_m: int = CELL
 # ---- raw launches ----------------------------------------------------------------------
 
 
+def _check_rows(name, t, sb, sn, B, N, width):
+    """Refuses a launch whose (position, row) strides or extent disagree with the
+    tensor the pointer comes from: the kernels address rows by these strides."""
+
+    if (t.dim() != 3 or t.stride(2) != 1 or t.stride(0) != sb or t.stride(1) != sn
+            or t.shape[0] < B or t.shape[1] < N or t.shape[2] < width):
+        raise ValueError(
+            f"{name}: tensor {tuple(t.shape)} with strides {t.stride()} does not hold "
+            f"(B={B}, N={N}, width={width}) rows at strides ({sb}, {sn})")
+
+
 def launch_conv(
     *, x, x_sb, x_sn, idx, taps, idx_stride, mask8, wpack, bias, B, N, cin_pad, cout,
     ln_w=None, ln_b=None, eps=1e-5, relu=False, resid=None, r_sb=0, r_sn=0, gamma=None,
     head_w=None, head_b=None, head_out=None, out=None, o_sb=0, o_sn=0, stream=None,
 ):
+    _check_rows("hex_conv x", x, x_sb, x_sn, B, N, cin_pad)
+    if out is not None:
+        _check_rows("hex_conv out", out, o_sb, o_sn, B, N, cout)
+    if resid is not None:
+        _check_rows("hex_conv resid", resid, r_sb, r_sn, B, N, cout)
+    if head_out is not None and (not head_out.is_contiguous() or head_out.numel() < B * N):
+        raise ValueError(f"hex_conv head_out: needs a contiguous (B={B}, N={N}) tensor")
     a = _lib.ConvArgs(
         x=x.data_ptr(), x_sb=x_sb, x_sn=x_sn, idx=idx.data_ptr(), taps=taps,
         idx_stride=idx_stride, mask=mask8.data_ptr(), w=wpack.data_ptr(), bias=bias.data_ptr(),
@@ -162,6 +180,36 @@ def launch_conv(
     )
     s = _lib.stream_handle() if stream is None else stream
     _lib.check(_lib.load().shrimp_hex_conv(ctypes_ref(a), s), "hex_conv")
+
+
+def conv_block_supported(taps, N, cin_pad, cout):
+    """True when shrimp_conv_block has a fused kernel for this ConvBlock shape."""
+    return bool(_lib.load().shrimp_conv_block_supported(taps, N, cin_pad, cout))
+
+
+def launch_conv_block(
+    *, x, x_sb, x_sn, idx, idx_stride, mask8, B, N, C, w1, b1, ln1_w, ln1_b, eps1,
+    w2, b2, ln2_w, ln2_b, eps2, gamma, out, o_sb, o_sn, stream=None,
+):
+    """ConvBlock.forward (reference model.py:395-422) as one launch; y1 stays on chip.
+
+    `out` may alias `x`. Raises when conv_block_supported() is false for the shape.
+    """
+    _check_rows("conv_block x", x, x_sb, x_sn, B, N, C)
+    _check_rows("conv_block out", out, o_sb, o_sn, B, N, C)
+    c1 = _lib.ConvArgs(
+        x=x.data_ptr(), x_sb=x_sb, x_sn=x_sn, idx=idx.data_ptr(), taps=7, idx_stride=idx_stride,
+        mask=mask8.data_ptr(), w=w1.data_ptr(), bias=b1.data_ptr(), ln_w=ln1_w.data_ptr(),
+        ln_b=ln1_b.data_ptr(), eps=float(eps1), relu=1, B=B, N=N, cin_pad=C, cout=C,
+    )
+    c2 = _lib.ConvArgs(
+        w=w2.data_ptr(), bias=b2.data_ptr(), ln_w=ln2_w.data_ptr(), ln_b=ln2_b.data_ptr(),
+        eps=float(eps2), relu=0, resid=x.data_ptr(), r_sb=x_sb, r_sn=x_sn,
+        gamma=gamma.data_ptr(), out=out.data_ptr(), o_sb=o_sb, o_sn=o_sn, B=B, N=N,
+        cin_pad=C, cout=C,
+    )
+    s = _lib.stream_handle() if stream is None else stream
+    _lib.check(_lib.load().shrimp_conv_block(ctypes_ref(c1), ctypes_ref(c2), s), "conv_block")
 
 
 def launch_linear(

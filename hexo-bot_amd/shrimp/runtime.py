@@ -35,10 +35,12 @@ from .constants import NUM_TOKENS, VALUE_BINS
 from .geometry import CELL_LUT_M
 from .ops import (
     attn_bias_table,
+    conv_block_supported,
     launch_attn,
     launch_attn_mlp,
     launch_attn_qkv,
     launch_conv,
+    launch_conv_block,
     launch_linear,
     pack_attn_mlp,
     pack_attn_qkv,
@@ -82,6 +84,9 @@ class HipForward:
         # LN1 + q/k/v kernel with LN1 folded into its weights where it
         # applies; off runs the linear kernel's QKV mode.
         self.use_fused_qkv = True
+        # ConvBlock as one launch (conv1's output kept in LDS) where a fused
+        # kernel exists; off runs the two convolutions.
+        self.use_fused_block = True
 
     def invalidate(self) -> None:
         self._packed = None
@@ -245,6 +250,14 @@ class HipForward:
             if kind == "C":
                 k = P.convs[ci]
                 ci += 1
+                if self.use_fused_block and conv_block_supported(7, N, C, C):
+                    launch_conv_block(
+                        x=cells, x_sb=S * C, x_sn=C, idx=idx, idx_stride=7, mask8=mask8, B=B,
+                        N=N, C=C, w1=k.w1, b1=k.b1, ln1_w=k.ln1w, ln1_b=k.ln1b, eps1=k.eps1,
+                        w2=k.w2, b2=k.b2, ln2_w=k.ln2w, ln2_b=k.ln2b, eps2=k.eps2,
+                        gamma=k.gamma, out=cells, o_sb=S * C, o_sn=C, stream=st,
+                    )
+                    continue
                 launch_conv(
                     x=cells, x_sb=S * C, x_sn=C, wpack=k.w1, bias=k.b1, cin_pad=C, cout=C,
                     ln_w=k.ln1w, ln_b=k.ln1b, eps=k.eps1, relu=True,

@@ -116,6 +116,23 @@ typedef struct {
 int shrimp_hex_conv(const shrimp_conv_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
+ * ConvBlock.forward (model.py:395-422) in one launch:
+ *   y1  = relu(LN1(conv1(x))) * m ;   out = relu(x + gamma * LN2(conv2(y1)) * m)
+ * the same result as shrimp_hex_conv(c1) followed by shrimp_hex_conv(c2) with
+ * c2.x = c1's output, but y1 never leaves the workgroup's LDS.
+ * c1: x, idx, taps, idx_stride, mask, w, bias, ln_w, ln_b, eps, relu = 1,
+ *     B, N, cin_pad, cout (out / resid / head unused);
+ * c2: w, bias, ln_w, ln_b, eps, relu = 0, resid = c1.x (same strides),
+ *     gamma, out, o_sb, o_sn (x, idx, mask, B, N are taken from c1).
+ * out may alias x. shrimp_conv_block_supported reports whether a fused
+ * kernel exists for the shape (taps 7, 128 -> 128 channels, N <= 512, and
+ * the automatic conv variant selected); otherwise shrimp_conv_block returns
+ * SHRIMP_EINVAL and the caller runs the two convolutions.
+ * ---------------------------------------------------------------------- */
+int shrimp_conv_block_supported(int taps, int N, int cin_pad, int cout);
+int shrimp_conv_block(const shrimp_conv_args* c1, const shrimp_conv_args* c2, void* stream);
+
+/* ------------------------------------------------------------------------
  * Dense row GEMM with fused prologue / epilogue (the nn.Linear calls of
  * RelPosAttention / AttnBlock, model.py:448-514, and the value heads,
  * model.py:990-1002):

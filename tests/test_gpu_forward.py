@@ -110,11 +110,19 @@ def test_fused_and_unfused_mlp_paths_agree(cfg4_batch):
     net = _net(128, 8, "CCACCACCACCA", seed=5)
     fused = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
     rt = net.hip_runtime()
-    rt.use_fused_mlp = rt.use_fused_qkv = False
+    # the one-launch ConvBlock repeats the two-launch arithmetic exactly
+    rt.use_fused_block = False
+    try:
+        two = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+    finally:
+        rt.use_fused_block = True
+    for key in ("policy", "value", "moves_left"):
+        assert torch.equal(fused[key], two[key]), key
+    rt.use_fused_mlp = rt.use_fused_qkv = rt.use_fused_block = False
     try:
         plain = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
     finally:
-        rt.use_fused_mlp = rt.use_fused_qkv = True
+        rt.use_fused_mlp = rt.use_fused_qkv = rt.use_fused_block = True
     for key in ("policy", "value", "moves_left"):
         err = (fused[key] - plain[key]).abs().max().item()
         print(f"fused vs unfused {key}: {err:.3e}", flush=True)

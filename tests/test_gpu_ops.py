@@ -143,6 +143,106 @@ def test_conv_residual_and_head_epilogues(conv_case, conv_variant):
     assert (head.cpu()[~mask] == 0).all()
 
 
+def _block_case(conv_case, n):
+    """conv_case cut (n < 256) or zero-padded (n > 256) to n cells per position;
+    neighbours outside [0, n) become the sentinel n."""
+
+    b = conv_case["batch"]
+    x = torch.from_numpy(conv_case["x"])
+    gidx = _gidx(b)
+    mask = b["mask"]
+    B, N0 = mask.shape
+    if n <= N0:
+        x, gidx, mask = x[:, :n], gidx[:, :n].clone(), mask[:, :n]
+        gidx[(gidx < 0) | (gidx >= n)] = n
+    else:
+        x = torch.cat([x, torch.zeros(B, n - N0, 128)], 1)
+        gidx = torch.where(gidx >= N0, torch.full_like(gidx, n), gidx)
+        pad = torch.full((B, n - N0, 7), n, dtype=gidx.dtype)
+        pad[..., 0] = torch.arange(N0, n)
+        gidx = torch.cat([gidx, pad], 1)
+        mask = torch.cat([mask, torch.zeros(B, n - N0, dtype=mask.dtype)], 1)
+    return x * mask[..., None], gidx.contiguous(), mask.contiguous()
+
+
+@pytest.mark.parametrize("n", [256, 64, 200, 300, 512])
+def test_conv_block_fused(conv_case, n):
+    """ConvBlock in one launch (y1 kept in LDS) against the two-launch path
+    (bit-identical: same MFMA order, same epilogue arithmetic, y1 rounded to
+    bf16 either way) and against the oracle's ConvBlock (model.py:419-421)."""
+
+    from shrimp import ops
+
+    torch.manual_seed(n)
+    x, gidx, mask = _block_case(conv_case, n)
+    B, N = mask.shape
+    w1 = torch.from_numpy(conv_case["w"])
+    w2 = torch.randn(7, 128, 128) / math.sqrt(7 * 128)
+    b1 = torch.from_numpy(conv_case["bias"])
+    b2 = torch.randn(128) * 0.02
+    l1w, l2w = torch.rand(128) + 0.5, torch.rand(128) + 0.5
+    l1b, l2b = torch.randn(128) * 0.1, torch.randn(128) * 0.1
+    g = torch.rand(128) * 0.5 + 0.5
+    assert ops.conv_block_supported(7, N, 128, 128)
+    d = {k: v.to(DEV) for k, v in dict(b1=b1, b2=b2, l1w=l1w, l2w=l2w, l1b=l1b, l2b=l2b, g=g).items()}
+    idx = gidx.to(DEV, torch.int32).contiguous()
+    m8 = mask.to(DEV, torch.uint8)
+    wp1, wp2 = ops.pack_conv_weight(w1.to(DEV)), ops.pack_conv_weight(w2.to(DEV))
+    xd = x.to(DEV, torch.bfloat16).contiguous()
+    print(f"conv_block n={N} B={B}", flush=True)
+
+    fused = xd.clone()  # in place, as the forward runs it
+    ops.launch_conv_block(
+        x=fused, x_sb=N * 128, x_sn=128, idx=idx, idx_stride=7, mask8=m8, B=B, N=N, C=128,
+        w1=wp1, b1=d["b1"], ln1_w=d["l1w"], ln1_b=d["l1b"], eps1=1e-5, w2=wp2, b2=d["b2"],
+        ln2_w=d["l2w"], ln2_b=d["l2b"], eps2=1e-5, gamma=d["g"], out=fused, o_sb=N * 128, o_sn=128,
+    )
+    y1 = torch.empty_like(xd)
+    common = dict(idx=idx, taps=7, idx_stride=7, mask8=m8, B=B, N=N, cin_pad=128, cout=128)
+    ops.launch_conv(x=xd, x_sb=N * 128, x_sn=128, wpack=wp1, bias=d["b1"], ln_w=d["l1w"],
+                    ln_b=d["l1b"], relu=True, out=y1, o_sb=N * 128, o_sn=128, **common)
+    two = xd.clone()
+    ops.launch_conv(x=y1, x_sb=N * 128, x_sn=128, wpack=wp2, bias=d["b2"], ln_w=d["l2w"],
+                    ln_b=d["l2b"], resid=two, r_sb=N * 128, r_sn=128, gamma=d["g"], out=two,
+                    o_sb=N * 128, o_sn=128, **common)
+    torch.cuda.synchronize()
+    diff = (fused.float() - two.float()).abs().max().item()
+    print(f"fused vs two launches: max diff {diff:.3e}", flush=True)
+    assert torch.equal(fused, two)
+
+    if N <= 256:
+        bx = bf(x)
+        y = ofwd.hex_conv_ln(bx, gidx, mask, bf(w1), b1.double(), l1w.double(), l1b.double(), 1e-5, True)
+        y = ofwd.hex_conv_ln(bf(y), gidx, mask, bf(w2), b2.double(), l2w.double(), l2b.double(), 1e-5, False)
+        want = torch.relu(bx + g.double() * y)
+        close(fused, want, what=f"conv block n={N}")
+    assert (fused.cpu()[~mask] == 0).all()
+
+
+def test_conv_block_rejects_other_shapes(conv_case):
+    from shrimp import _lib, ops
+
+    lib = _lib.load()
+    assert not ops.conv_block_supported(7, 576, 128, 128)
+    assert not ops.conv_block_supported(7, 256, 64, 64)
+    assert not ops.conv_block_supported(31, 256, 128, 128)
+    prev = lib.shrimp_conv_variant(1)
+    try:
+        assert not ops.conv_block_supported(7, 256, 128, 128)
+    finally:
+        lib.shrimp_conv_variant(prev)
+    x = torch.zeros(1, 576, 128, dtype=torch.bfloat16, device=DEV)
+    z = torch.zeros(128, device=DEV)
+    wp = torch.zeros(7 * 128 * 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="conv_block"):
+        ops.launch_conv_block(
+            x=x, x_sb=576 * 128, x_sn=128, idx=torch.zeros(1, 576, 7, dtype=torch.int32, device=DEV),
+            idx_stride=7, mask8=torch.zeros(1, 576, dtype=torch.uint8, device=DEV), B=1, N=576,
+            C=128, w1=wp, b1=z, ln1_w=z, ln1_b=z, eps1=1e-5, w2=wp, b2=z, ln2_w=z, ln2_b=z,
+            eps2=1e-5, gamma=z, out=x, o_sb=576 * 128, o_sn=128,
+        )
+
+
 @pytest.mark.parametrize("c", [32, 128])
 def test_hex_conv_multi_tile_positions(c, conv_variant):
     """Spec-variant positions (Npad = ceil64(max N) > 256: several row tiles

@@ -6,6 +6,7 @@ import random
 
 import numpy as np
 import pytest
+import torch
 
 from shrimp import constants as C
 from shrimp import features, geometry, support
@@ -108,3 +109,21 @@ def test_synthetic_l256_generator():
     assert np.array_equal(batch["feats"].numpy(), again["feats"].numpy())
     spec = synthetic.position_batch("cfg4_spec", 4)
     assert spec["feats"].shape[1] % 64 == 0 and spec["feats"].shape[1] > 256
+
+
+def test_row_launches_refuse_mismatched_strides():
+    """Row kernels address rows by the strides they are given; the launch
+    wrappers refuse a tensor whose layout disagrees (a compact clone of a
+    strided view, a short buffer) before anything reaches the device."""
+
+    from shrimp import ops
+
+    seq = torch.empty(4, 264, 128, dtype=torch.bfloat16)
+    cells = seq[:, 8:]
+    ops._check_rows("ok", cells, 264 * 128, 128, 4, 256, 128)
+    with pytest.raises(ValueError, match="strides"):
+        ops._check_rows("clone", cells.clone(), 264 * 128, 128, 4, 256, 128)
+    with pytest.raises(ValueError, match="strides"):
+        ops._check_rows("short", torch.empty(3, 256, 128), 256 * 128, 128, 4, 256, 128)
+    with pytest.raises(ValueError, match="strides"):
+        ops._check_rows("narrow", torch.empty(4, 256, 64), 256 * 64, 64, 4, 256, 128)
