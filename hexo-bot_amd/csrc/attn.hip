@@ -486,8 +486,9 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   const int lg = lane >> 4;
   const int nkb = LP / 16;
 
-  for (int qb = wave; qb * 16 < L; qb += 4) {
-    AttnQuery qi;
+  // One query block over key blocks [k0, k1): online-softmax state in m, l, o.
+  auto run_block = [&](int qb, int k0, int k1, AttnQuery& qi, float (&m)[HG], float (&l)[HG],
+                       f32x4 (&o)[HG][KD]) {
     qi.query = qb * 16 + lr;
     qi.qv = qi.query < L;
     qi.qtok = qi.query < nt;
@@ -511,8 +512,6 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
         const int64_t e = pos_base + (int64_t)(h0 + h) * a.qkv_sh + qi.query * DP + kd * 16 + lg * 4;
         qf[h][kd] = buf_load8(qrs, qi.qv ? (uint32_t)(e * 2) : SHRIMP_OOB_OFFSET);
       }
-    float m[HG], l[HG];
-    f32x4 o[HG][KD];
 #pragma unroll
     for (int h = 0; h < HG; ++h) {
       m[h] = SHRIMP_NEG_BIG;
@@ -537,14 +536,14 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     case 6: SHRIMP_CHUNK_FL(NB, 6); break;            \
     default: SHRIMP_CHUNK_FL(NB, 7); break;           \
   }
-    int kb = 0;
+    int kb = k0;
     if (!PAIR && linear_ok) {
-      // LINEAR everywhere, in runs of four key blocks from block 0; each
-      // chunk's exceptions (token queries, token keys in block 0, dead keys)
-      // pick a compile-time variant.
+      // LINEAR everywhere, in runs of four key blocks; each chunk's
+      // exceptions (token queries, token keys in block 0, dead keys) pick a
+      // compile-time variant.
       const int qtokb = qb * 16 < nt ? FL_QTOK : 0;
-      while (kb < nkb) {
-        const int run = min(4, nkb - kb);
+      while (kb < k1) {
+        const int run = min(4, k1 - kb);
         const int nb = run == 4 ? 4 : (run >= 2 ? 2 : 1);
         int dead = 0;
         for (int i = 0; i < nb; ++i) dead |= s.blk_dead[kb + i];
@@ -559,29 +558,25 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
         kb += nb;
       }
     }
-    while (!(!PAIR && linear_ok) && kb < nkb) {
+    while (!(!PAIR && linear_ok) && kb < k1) {
       if (qgen || s.blk_gen[kb]) {
         SHRIMP_CHUNK(1, PATH_GENERAL);
         kb += 1;
         continue;
       }
       int run = 1;  // consecutive fast blocks starting at kb (up to 4)
-      while (run < 4 && kb + run < nkb && !s.blk_gen[kb + run]) ++run;
-      if (PAIR) {
-        if (run == 4) SHRIMP_CHUNK(4, PATH_CLAMP);
-        else if (run >= 2) SHRIMP_CHUNK(2, PATH_CLAMP);
-        else SHRIMP_CHUNK(1, PATH_CLAMP);
-      } else {
-        if (run == 4) SHRIMP_CHUNK(4, PATH_CLAMP);
-        else if (run >= 2) SHRIMP_CHUNK(2, PATH_CLAMP);
-        else SHRIMP_CHUNK(1, PATH_CLAMP);
-      }
+      while (run < 4 && kb + run < k1 && !s.blk_gen[kb + run]) ++run;
+      if (run == 4) SHRIMP_CHUNK(4, PATH_CLAMP);
+      else if (run >= 2) SHRIMP_CHUNK(2, PATH_CLAMP);
+      else SHRIMP_CHUNK(1, PATH_CLAMP);
       kb += run == 4 ? 4 : (run >= 2 ? 2 : 1);
     }
 #undef SHRIMP_CHUNK
 #undef SHRIMP_CHUNK_FL
 #undef SHRIMP_CHUNK_FLS
+  };
 
+  auto store_block = [&](const AttnQuery& qi, const float (&l)[HG], const f32x4 (&o)[HG][KD]) {
 #pragma unroll
     for (int h = 0; h < HG; ++h) {
       // the row sum sits in lane group 0; broadcast it to the query's lanes
@@ -600,6 +595,78 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
           *reinterpret_cast<u32x2*>(orow + e) = pk;
         }
       }
+    }
+  };
+
+  // Whole query blocks round-robin over the 4 waves. When one block is left
+  // over (nqb % 4 == 1: 17 blocks at S = 264), it is split by key range into
+  // 4 parts, one per wave, instead of running whole on one wave; after a
+  // barrier the partial softmax states go through LDS (over K and V, which
+  // are no longer read) and wave 0 merges them.
+  const int nqb = (L + 15) / 16;
+  constexpr int PF = HG * (2 + 4 * KD);  // floats of one lane's partial state
+  const bool split =
+      (nqb & 3) == 1 && 3 * 64 * PF * 4 <= 2 * HG * SP * DP * 2;  // partials fit over K, V
+  const int nmain = split ? nqb - 1 : nqb;
+  AttnQuery qi;
+  float m[HG], l[HG];
+  f32x4 o[HG][KD];
+  for (int qb = wave;; qb += 4) {
+    const bool tail = qb >= nmain;
+    if (tail && !split) break;
+    const int k0 = tail ? (wave * nkb) / 4 : 0;
+    const int k1 = tail ? ((wave + 1) * nkb) / 4 : nkb;
+    run_block(tail ? nmain : qb, k0, k1, qi, m, l, o);
+    if (tail) break;
+    store_block(qi, l, o);
+  }
+  if (split) {
+    __syncthreads();  // K and V are no longer read: their LDS holds the partials
+    float* part_lds = reinterpret_cast<float*>(smem) + ((wave - 1) * 64 + lane) * PF;
+    if (wave > 0) {
+#pragma unroll
+      for (int h = 0; h < HG; ++h) {
+        part_lds[h * (2 + 4 * KD)] = m[h];
+        part_lds[h * (2 + 4 * KD) + 1] = l[h];
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) part_lds[h * (2 + 4 * KD) + 2 + kd * 4 + j] = o[h][kd][j];
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int h = 0; h < HG; ++h) {
+        float mp[3], lp[3];
+        f32x4 op[3][KD];
+        float mm = m[h];
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+          const float* src =
+              reinterpret_cast<const float*>(smem) + (p * 64 + lane) * PF + h * (2 + 4 * KD);
+          mp[p] = src[0];
+          lp[p] = src[1];
+#pragma unroll
+          for (int kd = 0; kd < KD; ++kd)
+            op[p][kd] = f32x4{src[2 + kd * 4], src[3 + kd * 4], src[4 + kd * 4], src[5 + kd * 4]};
+          mm = fmaxf(mm, mp[p]);
+        }
+        // parts that saw only masked keys keep m = NEG_BIG and l = 0: factor 0
+        const float f0 = __builtin_amdgcn_exp2f(m[h] - mm);
+        float lsum = l[h] * f0;
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd) o[h][kd] = o[h][kd] * f0;
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+          const float f = __builtin_amdgcn_exp2f(mp[p] - mm);
+          lsum += lp[p] * f;
+#pragma unroll
+          for (int kd = 0; kd < KD; ++kd) o[h][kd] = o[h][kd] + op[p][kd] * f;
+        }
+        l[h] = lsum;
+      }
+      store_block(qi, l, o);
     }
   }
 
@@ -643,7 +710,7 @@ static int dispatch_attn(const shrimp_attn_args* a, float qk_scale, uint32_t qkv
   if (a->dpad == DPV) {                                                                    \
     const size_t s2 = attn_smem_bytes(DPV, 2, a->S, tab_rows, PAIR);                       \
     const size_t s1 = attn_smem_bytes(DPV, 1, a->S, tab_rows, PAIR);                       \
-    if (a->H % 2 == 0 && s2 <= kAttnSmemCap)                                               \
+    if (a->H % 2 == 0 && s2 <= kAttnSmemCap && g_attn_variant == 0)                       \
       return launch_attn<DPV, 2, PAIR>(a, qk_scale, qkv_bytes, npos, s2, st);             \
     if (s1 <= kAttnSmemCap) return launch_attn<DPV, 1, PAIR>(a, qk_scale, qkv_bytes, npos, s1, st); \
     return set_error(SHRIMP_EINVAL, "attn: sequence %d too long for LDS staging", a->S);   \

@@ -18,6 +18,7 @@ int set_error(int code, const char* fmt, ...) {
 }
 
 int g_conv_variant = 0;
+int g_attn_variant = 0;
 
 int max_lds_per_block() {
   static std::atomic<int> cache[64];
@@ -42,6 +43,12 @@ extern "C" int shrimp_abi_version(void) { return SHRIMP_ABI_VERSION; }
 extern "C" int shrimp_conv_variant(int variant) {
   const int prev = shrimp::g_conv_variant;
   if (variant >= 0 && variant <= 3) shrimp::g_conv_variant = variant;
+  return prev;
+}
+
+extern "C" int shrimp_attn_variant(int variant) {
+  const int prev = shrimp::g_attn_variant;
+  if (variant >= 0 && variant <= 1) shrimp::g_attn_variant = variant;
   return prev;
 }
 

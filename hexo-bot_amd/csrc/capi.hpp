@@ -31,6 +31,9 @@ int max_lds_per_block();
 // global gather), 1 = always the global-gather kernel, 2 = LDS-staged
 // (no big tiles), 3 = as 0.
 extern int g_conv_variant;
+// Attention: 0 = automatic (two heads per workgroup when they fit), 1 = one
+// head per workgroup.
+extern int g_attn_variant;
 
 }  // namespace shrimp
 

@@ -99,6 +99,7 @@ SIGNATURES: dict = {
     "shrimp_last_error": (ctypes.c_char_p, []),
     "shrimp_abi_version": (ctypes.c_int, []),
     "shrimp_conv_variant": (ctypes.c_int, [ctypes.c_int]),
+    "shrimp_attn_variant": (ctypes.c_int, [ctypes.c_int]),
     "shrimp_max_lds_per_block": (ctypes.c_int, []),
     "shrimp_conv_wpack_bytes": (ctypes.c_size_t, [ctypes.c_int] * 3),
     "shrimp_pack_conv_weight": (ctypes.c_int, [_vp, _vp] + [ctypes.c_int] * 4 + [_vp]),

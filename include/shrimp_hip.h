@@ -49,9 +49,13 @@ int shrimp_abi_version(void);
  * 7-tap conv), 1 = always gather rows from global memory, 2 = LDS-staged
  * rows with small tiles, 3 = same as 0; other values only query. Returns
  * the previous setting. Process-wide.
+ * shrimp_attn_variant: 0 = automatic (two heads per attention workgroup when
+ * their K/V fit the LDS budget), 1 = one head per workgroup; other values
+ * only query. Returns the previous setting. Process-wide.
  * shrimp_max_lds_per_block: LDS bytes one workgroup may allocate on the
  * current device (the staged conv needs (N + 1) * cin_pad * 2). */
 int shrimp_conv_variant(int variant);
+int shrimp_attn_variant(int variant);
 int shrimp_max_lds_per_block(void);
 
 /* ------------------------------------------------------------------------
