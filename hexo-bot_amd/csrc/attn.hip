@@ -285,13 +285,44 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(a.v, qkv_bytes);
   const int64_t pos_base = (int64_t)b * a.qkv_sb;
 
+  // ---- global loads of the setup that nothing else depends on, issued first -----
+  // coordinates and liveness of keys tid and tid + 256 (the rare keys beyond
+  // 512 are loaded where they are used)
+  int kq[2] = {0, 0}, kr[2] = {0, 0};
+  bool km[2] = {false, false};
+  if (!PAIR) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = tid + 256 * i;
+      if (key >= nt && key < L) {
+        const int64_t cell = (int64_t)b * NC + (key - nt);
+        kq[i] = a.coords[cell * 2];
+        kr[i] = a.coords[cell * 2 + 1];
+        km[i] = a.mask[cell] != 0;
+      }
+    }
+  }
+  // the (XW*XW, HG) offset table of this head pair: XW*XW <= 12 * 256 dwords
+  constexpr int UX = 12;
+  static_assert(XW * XW <= 256 * UX, "offset table staging assumes one pass");
+  unsigned xv[UX];
+  const bool xstage = !PAIR && HG == 2 && a.xtab != nullptr;
+  if (xstage) {
+    const unsigned short* xg = static_cast<const unsigned short*>(a.xtab);
+#pragma unroll
+    for (int u = 0; u < UX; ++u) {
+      const int x = tid + u * 256;
+      xv[u] = x < XW * XW ? *reinterpret_cast<const unsigned*>(xg + (int64_t)x * a.H + h0) : 0u;
+    }
+  }
+
   // ---- stage K and V in MFMA fragment order -----------------------------------
   // K fragment (h, kd, kb): lane (lr, lg) holds K[kb*16 + lr][kd*16 + 4lg .. +3];
   // V fragment (h, kd, kb): lane (lr, lg) holds V[kb*16 + 4lg .. +3][kd*16 + lr].
   // A wave's fragment read is then one contiguous 512-byte LDS block.
   // Global loads are issued U at a time per thread before their LDS stores.
   constexpr int CH = DP / 8;
-  constexpr int U = 4;
+  constexpr int U = 5;
   {
     const int total = HG * LP * CH;
     for (int base = tid; base < total; base += 256 * U) {
@@ -328,6 +359,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     const int total = HG * (LP / 2) * CH;
     for (int base = tid; base < total; base += 256 * U) {
       u32x4 v0[U], v1[U];
+      bool d0[U], d1[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int i = base + u * 256;
@@ -336,12 +368,14 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
         const int key = 2 * (rem / CH);
         const int ch = rem - (key / 2) * CH;
         const int64_t e0 = pos_base + (int64_t)(h0 + h) * a.qkv_sh + key * DP + ch * 8;
-        // dead keys (past the bound, or masked cells) stage zero V rows
-        const bool l0 = i < total && key < L && (PAIR || key < nt || a.mask[(int64_t)b * NC + key - nt]);
-        const bool l1 = i < total && key + 1 < L &&
-                        (PAIR || key + 1 < nt || a.mask[(int64_t)b * NC + key + 1 - nt]);
+        // dead keys (past the bound, or masked cells) stage zero V rows: the
+        // mask is loaded beside the rows and applied when they are stored
+        const bool l0 = i < total && key < L;
+        const bool l1 = i < total && key + 1 < L;
         v0[u] = buf_load16(vrs, l0 ? (uint32_t)(e0 * 2) : SHRIMP_OOB_OFFSET);
         v1[u] = buf_load16(vrs, l1 ? (uint32_t)((e0 + DP) * 2) : SHRIMP_OOB_OFFSET);
+        d0[u] = !PAIR && l0 && key >= nt && !a.mask[(int64_t)b * NC + key - nt];
+        d1[u] = !PAIR && l1 && key + 1 >= nt && !a.mask[(int64_t)b * NC + key + 1 - nt];
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -351,6 +385,8 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
         const int rem = i - h * (LP / 2) * CH;
         const int key = 2 * (rem / CH);
         const int ch = rem - (key / 2) * CH;
+        if (d0[u]) v0[u] = u32x4{0u, 0u, 0u, 0u};
+        if (d1[u]) v1[u] = u32x4{0u, 0u, 0u, 0u};
         // keys (key, key+1) are j, j+1 of lane group (key % 16) / 4
         unsigned short* f = s.Vt + ((h * KD + (ch >> 1)) * NKB + key / 16) * 256 +
                             ((key & 15) >> 2) * 64 + (key & 3);
@@ -366,15 +402,23 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   // ---- key classes, coordinates, span of the live cells ----------------------------
   int qmin = 1 << 30, qmax = -(1 << 30), rmin = 1 << 30, rmax = -(1 << 30);
   if (!PAIR) {
-    for (int key = tid; key < LP; key += 256) {
+    for (int key = tid, i = 0; key < LP; key += 256, ++i) {
       int q = 0, r = 0, cls = KEY_DEAD;
       if (key < nt) {
         cls = KEY_TOKEN;
       } else if (key < L) {
-        const int64_t cell = (int64_t)b * NC + (key - nt);
-        q = a.coords[cell * 2];
-        r = a.coords[cell * 2 + 1];
-        cls = a.mask[cell] ? KEY_CELL : KEY_DEAD;
+        bool live;
+        if (i < 2) {
+          q = i == 0 ? kq[0] : kq[1];
+          r = i == 0 ? kr[0] : kr[1];
+          live = i == 0 ? km[0] : km[1];
+        } else {
+          const int64_t cell = (int64_t)b * NC + (key - nt);
+          q = a.coords[cell * 2];
+          r = a.coords[cell * 2 + 1];
+          live = a.mask[cell] != 0;
+        }
+        cls = live ? KEY_CELL : KEY_DEAD;
         if (cls == KEY_CELL) {
           qmin = min(qmin, q);
           qmax = max(qmax, q);
@@ -400,19 +444,10 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   } else if (a.xtab != nullptr) {
     const unsigned short* xg = static_cast<const unsigned short*>(a.xtab);
     if (HG == 2) {
-      constexpr int UX = 12;
-      for (int base = tid; base < XW * XW; base += 256 * UX) {
-        unsigned v[UX];
 #pragma unroll
-        for (int u = 0; u < UX; ++u) {
-          const int x = base + u * 256;
-          v[u] = x < XW * XW ? *reinterpret_cast<const unsigned*>(xg + (int64_t)x * a.H + h0) : 0u;
-        }
-#pragma unroll
-        for (int u = 0; u < UX; ++u) {
-          const int x = base + u * 256;
-          if (x < XW * XW) reinterpret_cast<unsigned*>(s.xtab)[x] = v[u];
-        }
+      for (int u = 0; u < UX; ++u) {
+        const int x = tid + u * 256;
+        if (x < XW * XW) reinterpret_cast<unsigned*>(s.xtab)[x] = xv[u];
       }
     } else {
       for (int i = tid; i < XW * XW * HG; i += 256) {
@@ -442,18 +477,27 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   __syncthreads();
   // Per-block flags, from the staged key classes: key blocks with a token, a
   // dead key or keys past the bound; query blocks with a token or dead query.
-  for (int blk = tid; blk < LP / 16; blk += 256) {
-    int kg = 0, qg = 0, kd = 0;
-    for (int j = 0; j < 16; ++j) {
-      const int key = blk * 16 + j;
-      const bool special = PAIR ? false : s.kcls[key] != KEY_CELL;
-      if (key >= L) kg = kd = 1;
-      else if (special || key < nt) kg = qg = 1;
-      if (!PAIR && key < L && s.kcls[key] == KEY_DEAD) kd = 1;
+  // One key per thread; a 16-key block is 16 lanes of one wave, so its flags
+  // are 16-bit fields of wave ballots.
+  for (int key0 = 0; key0 < LP; key0 += 256) {
+    const int key = key0 + tid;
+    bool kg = false, qg = false, kd = false;
+    if (key < LP) {
+      const int cls = PAIR ? KEY_CELL : s.kcls[key];
+      if (key >= L) kg = kd = true;
+      else if (cls != KEY_CELL || key < nt) kg = qg = true;
+      if (key < L && cls == KEY_DEAD) kd = true;
     }
-    s.blk_gen[blk] = kg;
-    q_gen[blk] = qg;
-    s.blk_dead[blk] = kd;
+    const uint64_t bk = __builtin_amdgcn_ballot_w64(kg);
+    const uint64_t bq = __builtin_amdgcn_ballot_w64(qg);
+    const uint64_t bd = __builtin_amdgcn_ballot_w64(kd);
+    if ((tid & 15) == 0 && key < LP) {
+      const int sh = tid & 48;
+      const int blk = key >> 4;
+      s.blk_gen[blk] = ((bk >> sh) & 0xFFFFu) != 0;
+      q_gen[blk] = ((bq >> sh) & 0xFFFFu) != 0;
+      s.blk_dead[blk] = ((bd >> sh) & 0xFFFFu) != 0;
+    }
   }
   if (!PAIR) {
     int q0 = span_red[0], q1 = span_red[1], r0 = span_red[2], r1 = span_red[3];
