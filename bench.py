@@ -166,6 +166,38 @@ def kernel_timings(net, inputs, reps=50):
     }
 
 
+def evaluator_timing(net, reps: int = 5) -> dict:
+    """Secondary figure: the ABI-1 evaluator end to end on the same 512 cfg4
+    positions as a wire payload (parse, upload of the CSR arrays, device pack,
+    forward, decode, reply bytes back on the host). Wall clock per payload;
+    host-device copies included, so it is reported beside `value`, not as it."""
+
+    import numpy as np
+    import torch
+
+    from shrimp import synthetic
+    from shrimp.inference import ShrimpEvaluator, plan_groups
+
+    payload, _ = synthetic.serve_payload("cfg4", B)
+    ev = ShrimpEvaluator(net, "cuda")
+    ev.evaluate_payload(payload)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ev.evaluate_payload(payload)
+    el = (time.perf_counter() - t0) / reps
+    offs = np.asarray(payload["node_row_offsets"], dtype=np.int64)
+    nbytes = sum(len(payload[k]) for k in ("node_feats", "node_qr", "nbr", "legal_counts"))
+    return {
+        "path": "ShrimpEvaluator.evaluate_payload (payload bytes -> reply bytes)",
+        "positions_per_s": round(B / el, 1),
+        "ms_per_payload": round(el * 1e3, 4),
+        "groups": len(plan_groups(offs[1:] - offs[:-1])),
+        "payload_bytes": nbytes,
+        "reps": reps,
+    }
+
+
 def cpu_baseline(batch, seconds: float):
     """Oracle fp32 eager forward (the reference CPU path, restated) on a
     bounded sample of the same workload; positions/s on the host cores."""
@@ -307,6 +339,7 @@ def main() -> int:
         },
         "block0_row_kernels": kt["linears"],
         "forward_tflops_padded": round(1.425e9 * B / (ms * 1e-3) / 1e12, 2),
+        "evaluator": evaluator_timing(net),
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(batch, args.cpu_seconds)

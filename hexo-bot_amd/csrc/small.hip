@@ -81,6 +81,58 @@ __global__ __launch_bounds__(256) void prep_kernel(const void* nbr, int nbr_dt, 
   }
 }
 
+// Serve pack + index preparation from the ABI-1 payload arrays, one workgroup
+// per row: row row0 + b occupies cells [off, off + n) of the CSR arrays, its
+// live cells are the first n of the N padded ones. Same outputs and rules as
+// prep_kernel on the host-packed batch (the 0xFFFF sentinel and indices >= N
+// become N; padding rows are self-only, masked, zero).
+__global__ __launch_bounds__(256) void prep_csr_kernel(const uint16_t* __restrict__ feats, int nfeat,
+                                                       const int16_t* __restrict__ qr,
+                                                       const uint16_t* __restrict__ nbr,
+                                                       const int64_t* __restrict__ offsets, int row0,
+                                                       int N, int n_tokens, int32_t* idx,
+                                                       uint8_t* mask8, int32_t* coords32,
+                                                       int32_t* seq_lens, uint8_t* seq_mask,
+                                                       uint16_t* xin) {
+  const int b = blockIdx.x;
+  const int64_t o = offsets[row0 + b];
+  const int64_t cnt = offsets[row0 + b + 1] - o;
+  const int n = cnt < 0 ? 0 : (cnt > N ? N : (int)cnt);
+  const int64_t base = (int64_t)b * N;
+  if (seq_mask)
+    for (int t = threadIdx.x; t < n_tokens; t += blockDim.x)
+      seq_mask[(int64_t)b * (n_tokens + N) + t] = 1;
+  for (int i = threadIdx.x; i < N; i += blockDim.x) {
+    const int64_t r = base + i;
+    const bool live = i < n;
+    const int64_t c = o + i;
+    if (mask8) mask8[r] = live ? 1 : 0;
+    if (seq_mask) seq_mask[(int64_t)b * (n_tokens + N) + n_tokens + i] = live ? 1 : 0;
+    if (idx) {
+      idx[r * 7] = i;
+#pragma unroll
+      for (int k = 0; k < 6; ++k) {
+        const unsigned j = live ? nbr[c * 6 + k] : 0xFFFFu;
+        idx[r * 7 + 1 + k] = (int)j < N ? (int32_t)j : N;
+      }
+    }
+    if (coords32) {
+      coords32[r * 2] = live ? qr[c * 2] : 0;
+      coords32[r * 2 + 1] = live ? qr[c * 2 + 1] : 0;
+    }
+    if (xin) {
+#pragma unroll 4
+      for (int f = 0; f < 32; f += 2) {
+        const float v0 = live && f < nfeat ? (float)__builtin_bit_cast(_Float16, feats[c * nfeat + f]) : 0.f;
+        const float v1 =
+            live && f + 1 < nfeat ? (float)__builtin_bit_cast(_Float16, feats[c * nfeat + f + 1]) : 0.f;
+        reinterpret_cast<unsigned*>(xin + r * 32)[f / 2] = pack_bf16x2(v0, v1);
+      }
+    }
+  }
+  if (seq_lens && threadIdx.x == 0) seq_lens[b] = n_tokens + n;
+}
+
 __global__ void fill_tokens_kernel(const float* __restrict__ tokens, int n_tokens, int C,
                                    uint16_t* __restrict__ seq, int64_t seq_sb) {
   const int b = blockIdx.x;
@@ -450,6 +502,24 @@ extern "C" int shrimp_prep_inputs(const void* nbr, int nbr_dt, const void* mask,
                      coords, coords_dt, feats, feats_dt, nfeat, N, n_tokens, idx, mask8, coords32,
                      seq_lens, seq_mask, static_cast<uint16_t*>(xin));
   return check_launch("prep_inputs");
+}
+
+extern "C" int shrimp_prep_csr(const void* node_feats, int nfeat, const int16_t* node_qr,
+                               const uint16_t* nbr, const int64_t* row_offsets, int row0, int B,
+                               int N, int n_tokens, int32_t* idx, uint8_t* mask8, int32_t* coords32,
+                               int32_t* seq_lens, uint8_t* seq_mask, void* xin, void* stream) {
+  SHRIMP_REQUIRE(B >= 0 && N > 0 && row0 >= 0 && n_tokens >= 0, "prep_csr: bad sizes");
+  if (B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(row_offsets, "prep_csr: null row offsets");
+  SHRIMP_REQUIRE(!idx || nbr, "prep_csr: idx needs nbr");
+  SHRIMP_REQUIRE(!coords32 || node_qr, "prep_csr: coords need node_qr");
+  SHRIMP_REQUIRE(!xin || (node_feats && nfeat > 0 && nfeat <= 32), "prep_csr: feats (nfeat %d)",
+                 nfeat);
+  hipLaunchKernelGGL(prep_csr_kernel, dim3(B), dim3(256), 0, as_stream(stream),
+                     static_cast<const uint16_t*>(node_feats), nfeat, node_qr, nbr, row_offsets,
+                     row0, N, n_tokens, idx, mask8, coords32, seq_lens, seq_mask,
+                     static_cast<uint16_t*>(xin));
+  return check_launch("prep_csr");
 }
 
 extern "C" int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void* seq,

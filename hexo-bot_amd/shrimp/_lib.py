@@ -125,6 +125,11 @@ SIGNATURES: dict = {
         [_vp, ctypes.c_int, _vp, _vp, ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int,
          ctypes.c_int, ctypes.c_int, ctypes.c_int] + [_vp] * 7,
     ),
+    "shrimp_prep_csr": (
+        ctypes.c_int,
+        [_vp, ctypes.c_int, _vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        + [_vp] * 7,
+    ),
     "shrimp_fill_tokens": (
         ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _i64, ctypes.c_int, _vp]
     ),

@@ -15,9 +15,13 @@ Reply: ``values_bytes`` f32 x B in [-1, 1]; ``priors_bytes`` f32 x sum(L),
 the softmax over each row's legal prefix, rows in order; optional
 ``moves_left_bytes`` f32 x B and ``priors_logits_bytes`` f32 x sum(L).
 
-Per group the forward and the decode (``shrimp_decode``: binned value,
-moves-left, legal-prefix softmax and the flat gather in one kernel) run on
-the current stream; ``result`` performs the only device-to-host copy.
+The payload's CSR arrays go to the device once (pinned host copies, one
+non-blocking upload each); per group the pack into the padded forward inputs
+(``shrimp_prep_csr``, one kernel: sentinel remap, masks, coordinates,
+sequence lengths, stem features), the forward and the decode
+(``shrimp_decode``: binned value, moves-left, legal-prefix softmax and the
+flat gather in one kernel) run on the current stream; ``result`` performs the
+only device-to-host copy.
 """
 
 from __future__ import annotations
@@ -36,6 +40,14 @@ NBR_SENTINEL = 0xFFFF
 PAIR_CEILING = float(os.environ.get("SHRIMP_PAIR_CEILING", 0) or 3.8e7)
 QUANT_NODES = 64
 WASTE_FRACTION = float(os.environ.get("SHRIMP_WASTE_FRACTION", 0) or 0.18)
+
+
+def _upload(arr: np.ndarray, dtype: torch.dtype, dev: torch.device) -> torch.Tensor:
+    """Host array -> device tensor through a pinned staging copy (non-blocking)."""
+
+    host = torch.empty(arr.shape, dtype=dtype, pin_memory=True)
+    host.numpy()[...] = arr
+    return host.to(dev, non_blocking=True)
 
 
 def _ceil_quant(n: int) -> int:
@@ -122,30 +134,20 @@ class ShrimpEvaluator:
         ml = torch.empty(b, dtype=torch.float32, device=dev) if request_ml else None
         priors = torch.empty(int(flat_off[-1]), dtype=torch.float32, device=dev)
         logits = torch.empty_like(priors) if request_logits else None
-        d_legal = torch.from_numpy(legal.copy()).to(dev, non_blocking=True)
-        d_off = torch.from_numpy(flat_off[:-1].copy()).to(dev, non_blocking=True)
+        d_legal = _upload(legal, torch.int32, dev)
+        d_off = _upload(flat_off[:-1], torch.int64, dev)
+        # the CSR payload itself; u16 neighbour ids travel as their int16 bits
+        d_feats = _upload(feats, torch.float16, dev)
+        d_qr = _upload(qr, torch.int16, dev)
+        d_nbr = _upload(nbr.view(np.int16), torch.int16, dev)
+        d_rows = _upload(offsets, torch.int64, dev)
         lib = _lib.load()
         stream = _lib.stream_handle(dev)
+        rt = self.model.hip_runtime()
         for start, end, pad_to in plan_groups(sizes):
             g = end - start
-            p_feats = np.zeros((g, pad_to, NUM_FEATURES), dtype=np.float16)
-            p_nbr = np.full((g, pad_to, 6), NBR_SENTINEL, dtype=np.uint16)
-            p_mask = np.zeros((g, pad_to), dtype=np.bool_)
-            p_coords = np.zeros((g, pad_to, 2), dtype=np.int32)
-            for k in range(g):
-                o = int(offsets[start + k])
-                n = int(sizes[start + k])
-                p_feats[k, :n] = feats[o:o + n]
-                p_nbr[k, :n] = nbr[o:o + n]
-                p_mask[k, :n] = True
-                p_coords[k, :n] = qr[o:o + n]
-            d_feats = torch.from_numpy(p_feats).pin_memory().to(dev, non_blocking=True)
-            d_nbr = torch.from_numpy(p_nbr).pin_memory().to(dev, non_blocking=True)
-            d_mask = torch.from_numpy(p_mask).pin_memory().to(dev, non_blocking=True)
-            d_coords = torch.from_numpy(p_coords).pin_memory().to(dev, non_blocking=True)
-            out = self.model.forward_policy_value(
-                d_feats, d_nbr, d_mask, d_coords, request_moves_left=request_ml
-            )
+            out = rt.forward_csr(d_feats, d_qr, d_nbr, d_rows, start, g, pad_to,
+                                 request_moves_left=request_ml)
             pol = out["policy"]
             _lib.check(
                 lib.shrimp_decode(

@@ -187,14 +187,57 @@ class HipForward:
         )
         return P
 
+    @staticmethod
+    def _prep_buffers(B: int, N: int, dev) -> SimpleNamespace:
+        i32, u8 = torch.int32, torch.uint8
+        S = N + NUM_TOKENS
+        return SimpleNamespace(
+            idx=torch.empty((B, N, 7), dtype=i32, device=dev),
+            mask8=torch.empty((B, N), dtype=u8, device=dev),
+            coords32=torch.empty((B, N, 2), dtype=i32, device=dev),
+            seq_lens=torch.empty((B,), dtype=i32, device=dev),
+            seq_mask=torch.empty((B, S), dtype=u8, device=dev),
+            xin=torch.empty((B, N, 32), dtype=torch.bfloat16, device=dev),
+        )
+
+    @torch.no_grad()
+    def forward_csr(self, node_feats, node_qr, nbr, row_offsets, row0: int, B: int, N: int, *,
+                    request_moves_left: bool = False) -> dict:
+        """Forward over rows row0 .. row0 + B - 1 of ABI-1 payload arrays already on
+        the device (node_feats (T, 15) f16, node_qr (T, 2) i16, nbr (T, 6) u16,
+        row_offsets (rows + 1) int64), padded to N cells on the device
+        (inference.py:865-892 / serve_pack.rs:155-216 in one kernel)."""
+
+        require_device(node_feats, "HipForward.forward_csr")
+        dev = node_feats.device
+        for t, dt in ((node_feats, torch.float16), (node_qr, torch.int16), (nbr, torch.int16),
+                      (row_offsets, torch.int64)):
+            if t.dtype not in (dt, torch.uint16) or not t.is_contiguous() or t.device != dev:
+                raise TypeError(f"forward_csr: {t.dtype} {tuple(t.shape)} is not a contiguous {dt} "
+                                f"tensor on {dev}")
+        if node_feats.dim() != 2 or node_feats.shape[1] > 32:
+            raise ValueError("forward_csr: node_feats must be (T, F) with F <= 32")
+        if row0 < 0 or row0 + B + 1 > row_offsets.shape[0]:
+            raise ValueError("forward_csr: rows outside row_offsets")
+        lib = _lib.load()
+        st = _lib.stream_handle(dev)
+        pb = self._prep_buffers(B, N, dev)
+        _lib.check(
+            lib.shrimp_prep_csr(
+                node_feats.data_ptr(), node_feats.shape[1], node_qr.data_ptr(), nbr.data_ptr(),
+                row_offsets.data_ptr(), row0, B, N, NUM_TOKENS, pb.idx.data_ptr(),
+                pb.mask8.data_ptr(), pb.coords32.data_ptr(), pb.seq_lens.data_ptr(),
+                pb.seq_mask.data_ptr(), pb.xin.data_ptr(), st,
+            ),
+            "prep_csr",
+        )
+        return self._trunk(pb, B, N, dev, request_moves_left)
+
     @torch.no_grad()
     def forward(self, feats, nbr, mask, coords, *, request_moves_left: bool = False) -> dict:
         require_device(feats, "ShrimpNet.forward_policy_value")
         dev = feats.device
         B, N, F = feats.shape
-        P = self.weights(dev)
-        C, H, d, dpad = P.C, P.H, P.d, P.dpad
-        S = N + NUM_TOKENS
         if nbr.dtype not in _NBR_DT or feats.dtype not in _FEAT_DT or coords.dtype not in _COORD_DT:
             raise TypeError(
                 f"unsupported dtypes feats={feats.dtype} nbr={nbr.dtype} coords={coords.dtype}"
@@ -210,22 +253,29 @@ class HipForward:
             mask_c = mask_c.to(torch.bool)
         coords_c = coords.contiguous()
 
-        i32, u8, bf = torch.int32, torch.uint8, torch.bfloat16
-        idx = torch.empty((B, N, 7), dtype=i32, device=dev)
-        mask8 = torch.empty((B, N), dtype=u8, device=dev)
-        coords32 = torch.empty((B, N, 2), dtype=i32, device=dev)
-        seq_lens = torch.empty((B,), dtype=i32, device=dev)
-        seq_mask = torch.empty((B, S), dtype=u8, device=dev)
-        xin = torch.empty((B, N, 32), dtype=bf, device=dev)
+        pb = self._prep_buffers(B, N, dev)
         _lib.check(
             lib.shrimp_prep_inputs(
                 nbr_c.data_ptr(), _NBR_DT[nbr_c.dtype], mask_c.data_ptr(), coords_c.data_ptr(),
                 _COORD_DT[coords_c.dtype], feats_c.data_ptr(), _FEAT_DT[feats_c.dtype], F, B, N,
-                NUM_TOKENS, idx.data_ptr(), mask8.data_ptr(), coords32.data_ptr(),
-                seq_lens.data_ptr(), seq_mask.data_ptr(), xin.data_ptr(), st,
+                NUM_TOKENS, pb.idx.data_ptr(), pb.mask8.data_ptr(), pb.coords32.data_ptr(),
+                pb.seq_lens.data_ptr(), pb.seq_mask.data_ptr(), pb.xin.data_ptr(), st,
             ),
             "prep_inputs",
         )
+        return self._trunk(pb, B, N, dev, request_moves_left)
+
+    def _trunk(self, pb: SimpleNamespace, B: int, N: int, dev, request_moves_left: bool) -> dict:
+        """Everything after the input preparation: stem, blocks, tail, heads."""
+
+        P = self.weights(dev)
+        C, H, d, dpad = P.C, P.H, P.d, P.dpad
+        S = N + NUM_TOKENS
+        lib = _lib.load()
+        st = _lib.stream_handle(dev)
+        bf = torch.bfloat16
+        idx, mask8, coords32 = pb.idx, pb.mask8, pb.coords32
+        seq_lens, seq_mask, xin = pb.seq_lens, pb.seq_mask, pb.xin
         seq = torch.empty((B, S, C), dtype=bf, device=dev)
         _lib.check(
             lib.shrimp_fill_tokens(P.tokens.data_ptr(), NUM_TOKENS, C, seq.data_ptr(), S * C, B, st),

@@ -138,6 +138,39 @@ def position_batch(name: str, count: int, seed: int | None = None) -> dict:
     return batch
 
 
+def serve_payload(name: str, count: int, seed: int | None = None, *,
+                  request_moves_left: bool = False, request_logits: bool = False) -> tuple:
+    """ABI-1 evaluator payload of ``count`` positions of config ``name``, built
+    as the Rust bridge builds it (``crates/shrimp/src/payload.rs:108-160``):
+    rows sorted by support size, descending (ties in request order), f16
+    features, i16 coordinates, u16 row-local neighbour ids with 0xFFFF for
+    absent. Returns (payload, order): order[k] is the request index of row k."""
+
+    rows = positions(name, count, seed)
+    order = sorted(range(count), key=lambda i: (-rows[i][1].num_nodes, i))
+    feats, qr, nbr, offs, legal = [], [], [], [0], []
+    for i in order:
+        _, sup, f = rows[i]
+        feats.append(np.asarray(f, dtype=np.float16))
+        qr.append(np.asarray(sup.coords, dtype=np.int16))
+        nb = np.asarray(sup.nbr, dtype=np.int64)
+        nbr.append(np.where(nb < 0, 0xFFFF, nb).astype(np.uint16))
+        offs.append(offs[-1] + sup.num_nodes)
+        legal.append(sup.legal_count)
+    payload = {
+        "abi": 1,
+        "shape": (count, offs[-1]),
+        "node_feats": np.concatenate(feats).tobytes(),
+        "node_qr": np.concatenate(qr).tobytes(),
+        "node_row_offsets": offs,
+        "nbr": np.concatenate(nbr).tobytes(),
+        "legal_counts": np.asarray(legal, dtype=np.int32).tobytes(),
+        "request_moves_left": request_moves_left,
+        "request_logits": request_logits,
+    }
+    return payload, order
+
+
 # ---- operator-level inputs (configs 1-3) -------------------------------------------
 
 

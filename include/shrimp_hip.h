@@ -323,6 +323,20 @@ int shrimp_prep_inputs(const void* nbr, int nbr_dt, const void* mask, const void
                        int n_tokens, int32_t* idx, uint8_t* mask8, int32_t* coords32,
                        int32_t* seq_lens, uint8_t* seq_mask, void* xin, void* stream);
 
+/* Serve pack + index preparation from the ABI-1 payload, on the device
+ * (inference.py:865-892 _pack_group / serve_pack.rs:155-216 pack_group, then
+ * the preparation above): rows row0 .. row0 + B - 1 of the CSR payload arrays
+ *   node_feats (T, nfeat) f16, node_qr (T, 2) i16, nbr (T, 6) u16 (0xFFFF =
+ *   absent; row-local indices), row_offsets (rows + 1) int64
+ * padded to N cells, written as shrimp_prep_inputs writes them (idx, mask8,
+ * coords32, seq_lens, seq_mask, xin; any output may be NULL). A row's live
+ * cells are its first n = row_offsets[r + 1] - row_offsets[r] (clamped to N);
+ * seq_lens = n_tokens + n. */
+int shrimp_prep_csr(const void* node_feats, int nfeat, const int16_t* node_qr, const uint16_t* nbr,
+                    const int64_t* row_offsets, int row0, int B, int N, int n_tokens, int32_t* idx,
+                    uint8_t* mask8, int32_t* coords32, int32_t* seq_lens, uint8_t* seq_mask,
+                    void* xin, void* stream);
+
 /* seq[b, t, :] = tokens[t, :] (bf16) for t < n_tokens; seq rows are C apart,
  * positions seq_sb apart. */
 int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void* seq, int64_t seq_sb, int B,

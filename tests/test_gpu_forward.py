@@ -180,3 +180,96 @@ def test_full_size_cfg4_properties():
     part = _run(net, b["feats"][sub], b["nbr"][sub], b["mask"][sub], b["coords"][sub])
     assert torch.equal(out["policy"][sub], part["policy"])
     assert torch.equal(out["value"][sub], part["value"])
+
+
+def _host_pack(payload, start, end, pad):
+    """Host pack of payload rows start..end-1 (inference.py:865-892 restated)."""
+
+    from shrimp.constants import NUM_FEATURES
+
+    b, total = (int(x) for x in payload["shape"])
+    offs = np.asarray(payload["node_row_offsets"], dtype=np.int64)
+    feats = np.frombuffer(payload["node_feats"], np.float16).reshape(total, NUM_FEATURES)
+    qr = np.frombuffer(payload["node_qr"], np.int16).reshape(total, 2)
+    nbr = np.frombuffer(payload["nbr"], np.uint16).reshape(total, 6)
+    g = end - start
+    pf = np.zeros((g, pad, NUM_FEATURES), np.float16)
+    pn = np.full((g, pad, 6), 0xFFFF, np.uint16)
+    pm = np.zeros((g, pad), bool)
+    pc = np.zeros((g, pad, 2), np.int32)
+    for k in range(g):
+        o, n = int(offs[start + k]), int(offs[start + k + 1] - offs[start + k])
+        pf[k, :n], pn[k, :n], pm[k, :n], pc[k, :n] = feats[o:o + n], nbr[o:o + n], True, qr[o:o + n]
+    return pf, pn, pm, pc
+
+
+def test_prep_csr_matches_host_pack():
+    """The device pack from the CSR payload (one kernel) writes exactly what
+    the host pack followed by the padded-batch preparation writes."""
+
+    from shrimp import _lib, synthetic
+    from shrimp.inference import plan_groups
+
+    payload, _ = synthetic.serve_payload("cfg4_spec", 12)
+    b, total = (int(x) for x in payload["shape"])
+    offs = np.asarray(payload["node_row_offsets"], dtype=np.int64)
+    feats = torch.from_numpy(np.frombuffer(payload["node_feats"], np.float16).copy()).view(total, 15)
+    qr = torch.from_numpy(np.frombuffer(payload["node_qr"], np.int16).copy()).view(total, 2)
+    nbr = torch.from_numpy(np.frombuffer(payload["nbr"], np.int16).copy()).view(total, 6)
+    d = [t.to(DEV) for t in (feats, qr, nbr, torch.from_numpy(offs))]
+    lib = _lib.load()
+    st = _lib.stream_handle()
+    groups = plan_groups(offs[1:] - offs[:-1])
+    assert len(groups) >= 2
+    for start, end, pad in groups:
+        g = end - start
+        print(f"prep_csr group rows {start}..{end} pad {pad}", flush=True)
+        outs = []
+        for mode in ("csr", "host"):
+            o = [torch.full((g, pad, 7), -5, dtype=torch.int32, device=DEV),
+                 torch.full((g, pad), 7, dtype=torch.uint8, device=DEV),
+                 torch.full((g, pad, 2), -5, dtype=torch.int32, device=DEV),
+                 torch.full((g,), -5, dtype=torch.int32, device=DEV),
+                 torch.full((g, pad + 8), 7, dtype=torch.uint8, device=DEV),
+                 torch.full((g, pad, 32), 3.0, dtype=torch.bfloat16, device=DEV)]
+            ptrs = [t.data_ptr() for t in o]
+            if mode == "csr":
+                rc = lib.shrimp_prep_csr(d[0].data_ptr(), 15, d[1].data_ptr(), d[2].data_ptr(),
+                                         d[3].data_ptr(), start, g, pad, 8, *ptrs, st)
+            else:
+                pf, pn, pm, pc = (torch.from_numpy(x).to(DEV) for x in _host_pack(payload, start, end, pad))
+                rc = lib.shrimp_prep_inputs(pn.view(torch.int16).data_ptr(), _lib.DT_U16, pm.data_ptr(),
+                                            pc.data_ptr(), _lib.DT_I32, pf.data_ptr(), _lib.DT_F16, 15,
+                                            g, pad, 8, *ptrs, st)
+            _lib.check(rc, mode)
+            torch.cuda.synchronize()
+            outs.append(o)
+        for a, c in zip(*outs):
+            assert torch.equal(a, c)
+
+
+def test_evaluator_multi_group_matches_oracle():
+    """Spec-variant payload (supports of 280-544 nodes): several groups with
+    different pad widths, packed on the device, against the CPU oracle's
+    evaluator on the same payload."""
+
+    from oracle import decode as odec
+    from shrimp import synthetic
+    from shrimp.inference import ShrimpEvaluator, plan_groups
+
+    payload, _ = synthetic.serve_payload("cfg4_spec", 10, request_moves_left=True, request_logits=True)
+    offs = np.asarray(payload["node_row_offsets"], dtype=np.int64)
+    assert len(plan_groups(offs[1:] - offs[:-1])) >= 2
+    sd = weights.make_state_dict(32, 4, "CCA", seed=3, mode="parity")
+    net = _net(32, 4, "CCA", seed=3)
+    got = ShrimpEvaluator(net, DEV).evaluate_payload(payload)
+    want = odec.evaluate(payload, sd, "CCA", 4)
+    for key, tol in (("values_bytes", TOL), ("priors_bytes", 5e-3), ("moves_left_bytes", 209 * TOL),
+                     ("priors_logits_bytes", TOL)):
+        a = np.frombuffer(got[key], np.float32)
+        b = np.frombuffer(want[key], np.float32)
+        assert a.shape == b.shape, key
+        err = np.abs(a - b).max()
+        print(f"evaluator multi-group {key}: max abs err {err:.3e}", flush=True)
+        assert err <= tol, key
+

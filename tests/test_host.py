@@ -127,3 +127,18 @@ def test_row_launches_refuse_mismatched_strides():
         ops._check_rows("short", torch.empty(3, 256, 128), 256 * 128, 128, 4, 256, 128)
     with pytest.raises(ValueError, match="strides"):
         ops._check_rows("narrow", torch.empty(4, 256, 64), 256 * 64, 64, 4, 256, 128)
+
+
+def test_serve_payload_matches_the_oracle_builder():
+    """The package's ABI-1 payload builder (the Rust bridge's layout) gives the
+    same bytes and row order as the oracle's builder on the same rows."""
+
+    from oracle import decode as odec
+    from shrimp import synthetic
+
+    payload, order = synthetic.serve_payload("cfg0", 6)
+    rows = synthetic.positions("cfg0", 6)
+    want, worder = odec.build_payload([(s, f) for _, s, f in rows])
+    assert order == worder
+    for key in ("abi", "shape", "node_feats", "node_qr", "node_row_offsets", "nbr", "legal_counts"):
+        assert payload[key] == want[key], key
