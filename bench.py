@@ -166,7 +166,7 @@ def kernel_timings(net, inputs, reps=50):
     }
 
 
-def evaluator_timing(net, reps: int = 5) -> dict:
+def evaluator_timing(net, count: int = B, graphs: bool = False, reps: int = 5) -> dict:
     """Secondary figure: the ABI-1 evaluator end to end on the same 512 cfg4
     positions as a wire payload (parse, upload of the CSR arrays, device pack,
     forward, decode, reply bytes back on the host). Wall clock per payload;
@@ -178,8 +178,8 @@ def evaluator_timing(net, reps: int = 5) -> dict:
     from shrimp import synthetic
     from shrimp.inference import ShrimpEvaluator, plan_groups
 
-    payload, _ = synthetic.serve_payload("cfg4", B)
-    ev = ShrimpEvaluator(net, "cuda")
+    payload, _ = synthetic.serve_payload("cfg4", count)
+    ev = ShrimpEvaluator(net, "cuda", graphs=graphs)
     ev.evaluate_payload(payload)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -190,7 +190,9 @@ def evaluator_timing(net, reps: int = 5) -> dict:
     nbytes = sum(len(payload[k]) for k in ("node_feats", "node_qr", "nbr", "legal_counts"))
     return {
         "path": "ShrimpEvaluator.evaluate_payload (payload bytes -> reply bytes)",
-        "positions_per_s": round(B / el, 1),
+        "graphs": graphs,
+        "positions": count,
+        "positions_per_s": round(count / el, 1),
         "ms_per_payload": round(el * 1e3, 4),
         "groups": len(plan_groups(offs[1:] - offs[:-1])),
         "payload_bytes": nbytes,
@@ -340,6 +342,8 @@ def main() -> int:
         "block0_row_kernels": kt["linears"],
         "forward_tflops_padded": round(1.425e9 * B / (ms * 1e-3) / 1e12, 2),
         "evaluator": evaluator_timing(net),
+        "evaluator_graphs": evaluator_timing(net, graphs=True),
+        "evaluator_small": [evaluator_timing(net, 32, g, reps=20) for g in (False, True)],
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(batch, args.cpu_seconds)

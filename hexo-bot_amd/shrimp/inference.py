@@ -80,7 +80,13 @@ def plan_groups(sizes) -> list:
 
 
 class ShrimpEvaluator:
-    def __init__(self, model: ShrimpNet, device="cuda"):
+    """graphs: replay each group's forward from a captured HIP graph keyed by
+    (batch bucket, Npad, moves-left) instead of launching its kernels one by
+    one; None follows SHRIMP_CUDA_GRAPHS=1 as the reference does
+    (inference.py:463-467). Groups above the largest bucket run eagerly."""
+
+    def __init__(self, model: ShrimpNet, device="cuda", graphs: bool | None = None):
+        self.graphs = os.environ.get("SHRIMP_CUDA_GRAPHS") == "1" if graphs is None else bool(graphs)
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise RuntimeError(
@@ -146,8 +152,11 @@ class ShrimpEvaluator:
         rt = self.model.hip_runtime()
         for start, end, pad_to in plan_groups(sizes):
             g = end - start
-            out = rt.forward_csr(d_feats, d_qr, d_nbr, d_rows, start, g, pad_to,
-                                 request_moves_left=request_ml)
+            csr = (d_feats, d_qr, d_nbr, d_rows)
+            out = rt.graph_forward_csr(*csr, start, g, pad_to, request_moves_left=request_ml) \
+                if self.graphs else None
+            if out is None:
+                out = rt.forward_csr(*csr, start, g, pad_to, request_moves_left=request_ml)
             pol = out["policy"]
             _lib.check(
                 lib.shrimp_decode(

@@ -87,6 +87,12 @@ class HipForward:
         # ConvBlock as one launch (conv1's output kept in LDS) where a fused
         # kernel exists; off runs the two convolutions.
         self.use_fused_block = True
+        # Captured forwards (graph_forward_csr), keyed by (batch bucket, Npad,
+        # moves-left, device); dropped when a parameter changes.
+        self._graphs: dict = {}
+        self._graph_params = None
+        self._graph_pool = None
+        self._empty_rows: dict = {}
 
     def invalidate(self) -> None:
         self._packed = None
@@ -232,6 +238,95 @@ class HipForward:
             "prep_csr",
         )
         return self._trunk(pb, B, N, dev, request_moves_left)
+
+    # ---- graph-captured serve forward (the reference's _GraphCache,
+    # inference.py:226-352): one captured trunk per (batch bucket, Npad,
+    # moves-left); the device pack runs eagerly into the capture's static
+    # input buffers, pad rows of the bucket carry the pad convention.
+    GRAPH_MAX_B = 260
+
+    @staticmethod
+    def graph_bucket(b: int):
+        """Batch size of the captured forward serving b rows (multiples of 4)."""
+
+        bb = max(4, -(-b // 4) * 4)
+        return bb if bb <= HipForward.GRAPH_MAX_B else None
+
+    def _prep_csr_rows(self, pb, lo: int, hi: int, N: int, csr, row0: int, st) -> None:
+        """shrimp_prep_csr of rows row0.. into batch rows [lo, hi) of pb."""
+
+        node_feats, node_qr, nbr, row_offsets = csr
+        lib = _lib.load()
+        _lib.check(
+            lib.shrimp_prep_csr(
+                node_feats.data_ptr(), node_feats.shape[1], node_qr.data_ptr(), nbr.data_ptr(),
+                row_offsets.data_ptr(), row0, hi - lo, N, NUM_TOKENS, pb.idx[lo:].data_ptr(),
+                pb.mask8[lo:].data_ptr(), pb.coords32[lo:].data_ptr(), pb.seq_lens[lo:].data_ptr(),
+                pb.seq_mask[lo:].data_ptr(), pb.xin[lo:].data_ptr(), st,
+            ),
+            "prep_csr",
+        )
+
+    def _empty_csr(self, dev):
+        """CSR arrays of rows with no cells: packing them writes pad rows."""
+
+        e = self._empty_rows.get(dev)
+        if e is None:
+            e = (torch.zeros((1, 15), dtype=torch.float16, device=dev),
+                 torch.zeros((1, 2), dtype=torch.int16, device=dev),
+                 torch.zeros((1, 6), dtype=torch.int16, device=dev),
+                 torch.zeros((self.GRAPH_MAX_B + 1,), dtype=torch.int64, device=dev))
+            self._empty_rows[dev] = e
+        return e
+
+    @torch.no_grad()
+    def graph_forward_csr(self, node_feats, node_qr, nbr, row_offsets, row0: int, B: int, N: int,
+                          *, request_moves_left: bool = False):
+        """forward_csr through a captured HIP graph; None when B is above the
+        largest bucket (the caller runs forward_csr). The returned tensors are
+        views of the capture's static outputs: valid until the next call with
+        the same bucket, so a caller consumes them (or clones) before that."""
+
+        bb = self.graph_bucket(B)
+        if bb is None:
+            return None
+        dev = node_feats.device
+        key_p = self._param_key(dev)
+        if key_p != self._graph_params:
+            self._graphs.clear()
+            self._graph_params = key_p
+        key = (bb, N, bool(request_moves_left), dev)
+        ent = self._graphs.get(key)
+        st = _lib.stream_handle(dev)
+        if ent is None:
+            self.weights(dev)  # pack outside the capture
+            pb = self._prep_buffers(bb, N, dev)
+            self._prep_csr_rows(pb, 0, bb, N, self._empty_csr(dev), 0, st)
+            keep, self.keep_buffers = self.keep_buffers, False
+            try:
+                cur = torch.cuda.current_stream(dev)
+                side = torch.cuda.Stream(dev)
+                side.wait_stream(cur)
+                with torch.cuda.stream(side):
+                    for _ in range(2):
+                        self._trunk(pb, bb, N, dev, request_moves_left)
+                cur.wait_stream(side)
+                if self._graph_pool is None:
+                    self._graph_pool = torch.cuda.graph_pool_handle()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, pool=self._graph_pool):
+                    out = self._trunk(pb, bb, N, dev, request_moves_left)
+            finally:
+                self.keep_buffers = keep
+            ent = SimpleNamespace(graph=graph, pb=pb, out=out, filled=0)
+            self._graphs[key] = ent
+            st = _lib.stream_handle(dev)
+        self._prep_csr_rows(ent.pb, 0, B, N, (node_feats, node_qr, nbr, row_offsets), row0, st)
+        if ent.filled > B:  # rows a larger group left behind go back to pad rows
+            self._prep_csr_rows(ent.pb, B, ent.filled, N, self._empty_csr(dev), 0, st)
+        ent.filled = B
+        ent.graph.replay()
+        return {k: v[:B] for k, v in ent.out.items()}
 
     @torch.no_grad()
     def forward(self, feats, nbr, mask, coords, *, request_moves_left: bool = False) -> dict:
