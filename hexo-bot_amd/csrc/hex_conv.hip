@@ -445,10 +445,10 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
 // one piece of 16 different rows hit distinct banks. One DMA instruction
 // fills 16 rows of one chunk; rows >= N (the zero row N for absent neighbours
 // and the padding up to NR = ceil((N+1)/16)*16) read past the buffer and land
-// as zeros. The K loop runs chunk-major (kc, then the 7 taps); chunk kc+1 is
-// requested while chunk kc's MFMAs run, always after the step's weight
-// prefetch (vmcnt retires in issue order, so a weight wait never waits for
-// an HBM row load), and a barrier publishes it at the chunk boundary.
+// as zeros. All four chunks are requested before the K loop: staging them
+// during the MFMA phases instead costs more than it hides, because vmcnt
+// retires in issue order and every weight load issued after a row DMA waits
+// for it. The K loop runs chunk-major (kc, then the 7 taps).
 constexpr int BIG_MAX_N = 512;
 constexpr int BIG_PARAMS = 5 * 128;  // floats: [bias | ln_w | ln_b | gamma or head_w | zeros]
 
@@ -458,7 +458,7 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Per-wave state of a big-tile workgroup (position b, rows 128 wave .. + 127).
 struct BigTile {
-  int lane, wave, nw, lg, N, NR, groups, mine, b;
+  int lane, wave, nw, lg, N, NR, groups, b;
   __amdgpu_buffer_rsrc_t xr;
   uint32_t xbase, xsn2;
   int rb[8], rn[8];
@@ -476,7 +476,7 @@ SHRIMP_DEV void big_dma(unsigned char* xs, const BigTile& t, int kc, int g) {
                                            off, 0, 0, 0);
 }
 
-// Requests chunk 0 by DMA and turns the neighbour indices of this wave's rows
+// Requests all four chunks by DMA and turns the neighbour indices of this wave's rows
 // into swizzled 16-bit LDS row addresses j * 64 | ((j >> 2) & 3) << 4.
 SHRIMP_DEV void big_setup(BigTile& t, const shrimp_conv_args& a, unsigned char* xs,
                           uint32_t x_bytes) {
@@ -488,12 +488,12 @@ SHRIMP_DEV void big_setup(BigTile& t, const shrimp_conv_args& a, unsigned char* 
   t.N = a.N;
   t.NR = big_rows_padded(a.N);
   t.groups = t.NR / 16;
-  t.mine = (t.groups - t.wave + t.nw - 1) / t.nw;
   t.b = blockIdx.x;
   t.xr = make_rsrc(a.x, x_bytes);
   t.xbase = (uint32_t)((int64_t)t.b * a.x_sb * 2);
   t.xsn2 = (uint32_t)(a.x_sn * 2);
-  for (int g = t.wave; g < t.groups; g += t.nw) big_dma(xs, t, 0, g);
+  for (int kc = 0; kc < 4; ++kc)
+    for (int g = t.wave; g < t.groups; g += t.nw) big_dma(xs, t, kc, g);
   const int row0 = t.wave * (MB * 16);
   const int* idxb = a.idx + (int64_t)t.b * t.N * a.idx_stride;
 #pragma unroll
@@ -540,9 +540,8 @@ SHRIMP_DEV void big_wload(__amdgpu_buffer_rsrc_t wr, int s, int lane, u32x4 (&w)
 
 // One 7-tap, 128 -> 128 conv over the rows in LDS: acc += sum_t W_t^T X[idx_t]^T.
 // On entry wf holds k-step 0 of `wr`; with NEXT, on exit it holds k-step 0 of
-// `wnext`. With STAGE, chunks 1..3 are still to be requested: chunk kc+1 is
-// spread over the 7 tap steps of chunk kc and a barrier publishes it.
-template <bool STAGE, bool NEXT>
+// `wnext`.
+template <bool NEXT>
 SHRIMP_DEV void big_pass(f32x4 (&acc)[8][8], u32x4 (&wf)[8], const BigTile& t,
                          unsigned char* xs, __amdgpu_buffer_rsrc_t wr,
                          __amdgpu_buffer_rsrc_t wnext) {
@@ -577,11 +576,6 @@ SHRIMP_DEV void big_pass(f32x4 (&acc)[8][8], u32x4 (&wf)[8], const BigTile& t,
       } else if (NEXT) {
         big_wload(wnext, 0, t.lane, wf);
       }
-      if (STAGE && more) {
-        // this wave's DMA groups i in [i0, i1) of chunk kc + 1
-        const int i0 = (tp * t.mine) / T, i1 = ((tp + 1) * t.mine) / T;
-        for (int i = i0; i < i1; ++i) big_dma(xs, t, kc + 1, t.wave + i * t.nw);
-      }
       // Keep the next step's loads ahead of this step's MFMAs (the scheduler
       // would otherwise sink them next to their uses).
       __builtin_amdgcn_sched_barrier(0);
@@ -590,10 +584,6 @@ SHRIMP_DEV void big_pass(f32x4 (&acc)[8][8], u32x4 (&wf)[8], const BigTile& t,
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = mfma16x16x32(wc[nb], xc[mb], acc[nb][mb]);
       __builtin_amdgcn_sched_barrier(0);
-    }
-    if (STAGE && more) {
-      __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA of chunk kc + 1 has landed
-      __syncthreads();
     }
   }
 }
@@ -616,7 +606,7 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
     for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  big_pass<true, false>(acc, wf, t, xs, wr, wr);
+  big_pass<false>(acc, wf, t, xs, wr, wr);
   conv_epilogue<128, 8, EPI, PS_LDS>(a, acc, t.rb, t.rn, t.rv, t.lg, lp);
 }
 
@@ -649,7 +639,7 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
     for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  big_pass<true, true>(acc, wf, t, xs, wr1, wr2);
+  big_pass<true>(acc, wf, t, xs, wr1, wr2);
   __syncthreads();  // every wave is done reading x from LDS
   {
     const uint32_t nr64 = (uint32_t)t.NR * 64;
@@ -682,7 +672,7 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
     for (int m2 = 0; m2 < 4; ++m2) asm volatile("" : "+v"(t.sw2[tp][m2]));
   asm volatile("" : "+v"(t.lane));
   t.lg = t.lane >> 4;
-  big_pass<false, false>(acc, wf, t, xs, wr2, wr2);
+  big_pass<false>(acc, wf, t, xs, wr2, wr2);
   conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(c2, acc, t.rb, t.rn, t.rv, t.lg, lp2);
 }
 
@@ -914,7 +904,9 @@ extern "C" int shrimp_conv_block(const shrimp_conv_args* c1, const shrimp_conv_a
   a2.N = c1->N;
   const int waves = (c1->N + 127) / 128;
   const size_t lds = (size_t)big_rows_padded(c1->N) * 256 + 2 * BIG_PARAMS * sizeof(float);
+  const uint32_t xb = (uint32_t)(x_extent * 2);
+  const uint32_t wb = (uint32_t)shrimp_conv_wpack_bytes(7, 128, 128);
   hipLaunchKernelGGL(hex_block_kernel, dim3(c1->B), dim3(64 * waves), lds, as_stream(stream), *c1,
-                     a2, (uint32_t)(x_extent * 2), (uint32_t)shrimp_conv_wpack_bytes(7, 128, 128));
+                     a2, xb, wb);
   return check_launch("conv_block");
 }

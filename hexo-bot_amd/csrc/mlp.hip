@@ -86,10 +86,23 @@ SHRIMP_DEV void load_x(const shrimp_mlp_args& a, __amdgpu_buffer_rsrc_t xr, int 
   for (int ks = 0; ks < MC / 32; ++ks) xf[ks] = buf_load16(xr, xo + ks * 64);
 }
 
-// One block of 16 rows (lane: row lane % 16, channel group lane / 16).
+// Residual rows (bf16, this lane's 4-channel groups) of the row `row`; rows at
+// or past `rows` read as zeros.
+SHRIMP_DEV void load_s(const shrimp_mlp_args& a, __amdgpu_buffer_rsrc_t sr, int row, int lg,
+                       u32x2 (&sf)[MC / 16]) {
+  const uint32_t so =
+      row < a.rows ? (uint32_t)((int64_t)row * a.s_sr * 2) + (uint32_t)(lg * 8) : SHRIMP_OOB_OFFSET;
+#pragma unroll
+  for (int nb = 0; nb < MC / 16; ++nb) sf[nb] = buf_load8(sr, so + nb * 32);
+}
+
+// One block of 16 rows (lane: row lane % 16, channel group lane / 16). sin
+// holds the block's residual rows on entry; once they are consumed the next
+// block's (row next_row) are requested into the same registers, so their
+// latency hides behind this block's MLP.
 SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, const float* bias,
                           __amdgpu_buffer_rsrc_t sr, const u32x4 (&xf)[MC / 32], int row,
-                          int lane) {
+                          int lane, u32x2 (&sin)[MC / 16], int next_row) {
   constexpr int KS1 = MC / 32, NB1 = MC / 16, NBH = MH / 16, KT = MH / 32, NB2 = MC / 16;
   const int lg = lane >> 4;
   const bool store = row < a.rows && a.mask[row] != 0;
@@ -97,17 +110,10 @@ SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, con
   const float* b1 = bias + MC;
   const float* b2 = bias + MC + MH;
 
-  // accumulators start at the biases; residual rows (bf16) requested alongside
+  // accumulators start at the biases
   f32x4 acc[NB1];
 #pragma unroll
   for (int nb = 0; nb < NB1; ++nb) acc[nb] = *reinterpret_cast<const f32x4*>(bo + nb * 16 + lg * 4);
-  u32x2 sin[NB1];
-  {
-    const uint32_t so =
-        row < a.rows ? (uint32_t)((int64_t)row * a.s_sr * 2) + (uint32_t)(lg * 8) : SHRIMP_OOB_OFFSET;
-#pragma unroll
-    for (int nb = 0; nb < NB1; ++nb) sin[nb] = buf_load8(sr, so + nb * 32);
-  }
 
   // ---- out_proj ----------------------------------------------------------
   // (scheduling barriers keep the weight-fragment reads next to their MFMAs;
@@ -135,6 +141,7 @@ SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, con
     sp[nb].x = pack_bf16x2(v[nb][0], v[nb][1]);
     sp[nb].y = pack_bf16x2(v[nb][2], v[nb][3]);
   }
+  load_s(a, sr, next_row, lg, sin);
   float s = 0.f;
 #pragma unroll
   for (int nb = 0; nb < NB1; ++nb)
@@ -255,14 +262,18 @@ __global__ __launch_bounds__(MWAVES * 64, 1) void attn_mlp_kernel(const shrimp_m
   const int end = (int)((gw + 1) * nblk / tw);
   const int lr = lane & 15, lg = lane >> 4;
   u32x4 cur[MC / 32], nxt[MC / 32];
-  if (begin < end) load_x(a, xr, begin * 16 + lr, lg, nxt);
+  u32x2 sres[MC / 16];
+  if (begin < end) {
+    load_x(a, xr, begin * 16 + lr, lg, nxt);
+    load_s(a, sr, begin * 16 + lr, lg, sres);
+  }
   for (int blk = begin; blk < end; ++blk) {
 #pragma unroll
     for (int ks = 0; ks < MC / 32; ++ks) cur[ks] = nxt[ks];
     // rows past this wave's range read as zeros (offset past the resource)
     const int nrow = blk + 1 < end ? (blk + 1) * 16 + lr : a.rows;
     load_x(a, xr, nrow, lg, nxt);
-    mlp_block(a, wl, bias, sr, cur, blk * 16 + lr, lane);
+    mlp_block(a, wl, bias, sr, cur, blk * 16 + lr, lane, sres, nrow);
   }
 }
 
