@@ -42,7 +42,7 @@ extern "C" int shrimp_abi_version(void) { return SHRIMP_ABI_VERSION; }
 
 extern "C" int shrimp_conv_variant(int variant) {
   const int prev = shrimp::g_conv_variant;
-  if (variant >= 0 && variant <= 4) shrimp::g_conv_variant = variant;
+  if (variant >= 0 && variant <= 3) shrimp::g_conv_variant = variant;
   return prev;
 }
 

@@ -38,7 +38,7 @@ enum : int { EPI_LN = 1, EPI_RELU = 2, EPI_RESID = 4, EPI_HEAD = 8 };
 // The residual rows are requested RD blocks ahead of their use.
 // `store(mb, nb, u32x2)` receives 4 packed bf16 channels 16 nb + 4 lg .. + 3
 // of row block mb, for rows that exist.
-enum : int { PS_GLOBAL = 0, PS_REGS = 1, PS_LDS = 2 };
+enum : int { PS_GLOBAL = 0, PS_REGS = 1, PS_LDS = 2, PS_LDSREG = 3 };
 
 template <int COUT, int MB, int EPI, int PSRC, typename Store>
 SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16][MB],
@@ -48,7 +48,9 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
   constexpr bool LN = (EPI & EPI_LN) != 0, RESID = (EPI & EPI_RESID) != 0;
   constexpr bool HEAD = (EPI & EPI_HEAD) != 0, RELU = (EPI & EPI_RELU) != 0;
   constexpr bool PRE = PSRC == PS_REGS;
-  constexpr bool LNMASK = LN && PSRC == PS_LDS;  // masking folded into the LayerNorm
+  constexpr bool FROM_LDS = PSRC == PS_LDS || PSRC == PS_LDSREG;
+  constexpr bool HREG = PSRC == PS_LDSREG;  // bias / ln_w read from LDS once, kept in registers
+  constexpr bool LNMASK = LN && FROM_LDS;   // masking folded into the LayerNorm
   constexpr int PN = PRE ? NB : 1;
   constexpr int RD = MB < 3 ? MB : 3;  // residual prefetch depth (row blocks)
   const int N = a.N;
@@ -68,12 +70,26 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
   }
   // ri: index into the register copy (0 when that array is a placeholder)
   auto pick = [&](int slot, const float* g, const f32x4* r, int nb, int ri) -> f32x4 {
-    if constexpr (PSRC == PS_LDS) return prm(lp + slot * COUT, nb);
+    if constexpr (FROM_LDS) return prm(lp + slot * COUT, nb);
     else if constexpr (PRE) return r[ri];
     else return prm(g, nb);
   };
-  auto P_b = [&](int nb) { return pick(0, a.bias, pb, nb, nb); };
-  auto P_w = [&](int nb) { return pick(1, a.ln_w, pw, nb, LN && PRE ? nb : 0); };
+  f32x4 hb_[HREG ? NB : 1], hw_[HREG ? NB : 1];
+  if constexpr (HREG) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      hb_[nb] = prm(lp, nb);
+      hw_[nb] = prm(lp + COUT, nb);
+    }
+  }
+  auto P_b = [&](int nb) {
+    if constexpr (HREG) return hb_[nb];
+    else return pick(0, a.bias, pb, nb, nb);
+  };
+  auto P_w = [&](int nb) {
+    if constexpr (HREG) return hw_[nb];
+    else return pick(1, a.ln_w, pw, nb, LN && PRE ? nb : 0);
+  };
   auto P_l = [&](int nb) { return pick(2, a.ln_b, pl, nb, LN && PRE ? nb : 0); };
   auto P_g = [&](int nb) { return pick(3, a.gamma, pg, nb, RESID && PRE ? nb : 0); };
   auto P_h = [&](int nb) { return pick(3, a.head_w, ph, nb, HEAD && PRE ? nb : 0); };
@@ -539,12 +555,9 @@ SHRIMP_DEV void big_wload(__amdgpu_buffer_rsrc_t wr, int s, int lane, u32x4 (&w)
 }
 
 // One 7-tap, 128 -> 128 conv over the rows in LDS: acc += sum_t W_t^T X[idx_t]^T.
-// On entry wf holds k-step 0 of `wr`; with NEXT, on exit it holds k-step 0 of
-// `wnext`.
-template <bool NEXT>
+// On entry wf holds k-step 0 of `wr`.
 SHRIMP_DEV void big_pass(f32x4 (&acc)[8][8], u32x4 (&wf)[8], const BigTile& t,
-                         unsigned char* xs, __amdgpu_buffer_rsrc_t wr,
-                         __amdgpu_buffer_rsrc_t wnext) {
+                         unsigned char* xs, __amdgpu_buffer_rsrc_t wr) {
   constexpr int KC = 4, T = 7, MB = 8, NB = 8;
   auto xload = [&](int tp, int kc, u32x4 (&x)[MB]) {
     const uint32_t kbase = (uint32_t)(kc * t.NR * 64);
@@ -573,8 +586,6 @@ SHRIMP_DEV void big_pass(f32x4 (&acc)[8][8], u32x4 (&wf)[8], const BigTile& t,
         big_wload(wr, (tp + 1) * KC + kc, t.lane, wf);
       } else if (more) {
         big_wload(wr, kc + 1, t.lane, wf);
-      } else if (NEXT) {
-        big_wload(wnext, 0, t.lane, wf);
       }
       // Keep the next step's loads ahead of this step's MFMAs (the scheduler
       // would otherwise sink them next to their uses).
@@ -606,7 +617,7 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
     for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  big_pass<false>(acc, wf, t, xs, wr, wr);
+  big_pass(acc, wf, t, xs, wr);
   conv_epilogue<128, 8, EPI, PS_LDS>(a, acc, t.rb, t.rn, t.rv, t.lg, lp);
 }
 
@@ -639,7 +650,9 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
     for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  big_pass<true>(acc, wf, t, xs, wr1, wr2);
+  // conv2's first weights are loaded after conv1's epilogue, whose bias and
+  // ln_w then fit in registers
+  big_pass(acc, wf, t, xs, wr1);
   __syncthreads();  // every wave is done reading x from LDS
   {
     const uint32_t nr64 = (uint32_t)t.NR * 64;
@@ -651,7 +664,7 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
       swz[mb] = (uint32_t)((t.rn[mb] >> 2) & 3);
     }
     const int lg = t.lg;
-    conv_epilogue<128, 8, EPI_LN | EPI_RELU, PS_LDS>(
+    conv_epilogue<128, 8, EPI_LN | EPI_RELU, PS_LDSREG>(
         c1, acc, t.rb, t.rn, t.rv, t.lg, lp1, [&](int mb, int nb, u32x2 pk) {
           const uint32_t piece = (uint32_t)((nb & 1) * 2 + (lg >> 1));
           const uint32_t addr = (uint32_t)(nb >> 1) * nr64 + row[mb] + ((piece ^ swz[mb]) << 4) + lo;
@@ -663,6 +676,7 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   __syncthreads();  // y1 is complete
+  big_wload(wr2, 0, t.lane, wf);
   // Hide the per-lane addresses from the optimizer: otherwise it keeps conv1's
   // LDS row and weight offsets alive (spilled) for reuse by conv2 instead of
   // recomputing them.
@@ -672,7 +686,7 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
     for (int m2 = 0; m2 < 4; ++m2) asm volatile("" : "+v"(t.sw2[tp][m2]));
   asm volatile("" : "+v"(t.lane));
   t.lg = t.lane >> 4;
-  big_pass<false>(acc, wf, t, xs, wr2, wr2);
+  big_pass(acc, wf, t, xs, wr2);
   conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(c2, acc, t.rb, t.rn, t.rv, t.lg, lp2);
 }
 
