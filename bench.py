@@ -89,21 +89,27 @@ def kernel_timings(net, inputs, reps=50):
         )
 
     a = P.attn[0]
+    seq = L["seq"]
+    # the forward keeps no q/k/v tensor when attention projects its own
     qkv = L["qkv"]
+    if qkv is None:
+        qkv = torch.empty((3, b, H, s, P.dpad), dtype=torch.bfloat16, device=seq.device)
+    bias_kw = dict(
+        seq_lens=L["seq_lens"], o=L["att"], o_sb=s * C, o_sh=P.d, o_sr=C, B=b, S=s, H=H,
+        d=P.d, dpad=P.dpad, coords=L["coords32"], mask8=L["mask8"], btab=a.btab_xtab[0],
+        xtab=a.btab_xtab[1], lut_m=CELL_LUT_M, n_tokens=8, stream=L["stream"],
+    )
 
     def attn():
-        ops.launch_attn(
-            q=qkv[0], k=qkv[1], v=qkv[2], qkv_sb=H * s * P.dpad, qkv_sh=s * P.dpad,
-            seq_lens=L["seq_lens"], o=L["att"], o_sb=s * C, o_sh=P.d, o_sr=C, B=b, S=s, H=H,
-            d=P.d, dpad=P.dpad, coords=L["coords32"], mask8=L["mask8"], btab=a.btab_xtab[0],
-            xtab=a.btab_xtab[1],
-            lut_m=CELL_LUT_M, n_tokens=8, stream=L["stream"],
-        )
+        ops.launch_attn(q=qkv[0], k=qkv[1], v=qkv[2], qkv_sb=H * s * P.dpad,
+                        qkv_sh=s * P.dpad, **bias_kw)
+
+    def attn_fused():
+        ops.launch_attn_fused(x=seq, x_sb=s * C, x_sr=C, packed=a.qkv, eps=a.eps1, **bias_kw)
 
     from shrimp import _lib
 
     rows = b * s
-    seq = L["seq"]
 
     def lin(mode, x, x_sr, w, bias, n_in, n_out, out, o_sr, **kw):
         return lambda: ops.launch_linear(
@@ -139,10 +145,17 @@ def kernel_timings(net, inputs, reps=50):
         })
     conv()
     block()
+    qkv_fn()
     attn()
     conv_ms = _events_time(conv, reps, stream)
     block_ms = _events_time(block, reps, stream)
     attn_ms = _events_time(attn, reps, stream)
+    # the one-launch LN1 + q/k/v + attention kernel, timed whichever path the
+    # forward takes
+    fused_ms = None
+    if P.fused_qkv and ops.attn_fused_supported(C, H, s, P.dpad):
+        attn_fused()
+        fused_ms = _events_time(attn_fused, reps, stream)
     extra = {}
     for name, (fn, flops, nbytes) in linears.items():
         fn()
@@ -160,8 +173,12 @@ def kernel_timings(net, inputs, reps=50):
         "conv_flops_valid": 2.0 * 7 * C * C * valid_rows,
         "conv_bytes": b * n * C * 2 * 2 + b * n * 7 * 4 + 7 * C * C * 2,
         "attn_ms": attn_ms,
+        "attn_fused_ms": fused_ms,
+        "forward_attn_fused": bool(L["attn_fused"]),
         "attn_flops": float(4 * P.d * H * (seq_lens ** 2).sum().item()),
         "attn_bytes": float(4 * 2 * P.d * H * seq_lens.sum().item()),
+        "proj_flops": rows * C * 3 * C * 2.0,
+        "proj_bytes": rows * C * 2 * 2.0,
         "linears": extra,
     }
 
@@ -288,7 +305,11 @@ def main() -> int:
 
     block_tflops = kt["block_flops"] / (kt["block_ms"] * 1e-3) / 1e12
     conv_tflops = kt["conv_flops"] / (kt["conv_ms"] * 1e-3) / 1e12
-    attn_tflops = kt["attn_flops"] / (kt["attn_ms"] * 1e-3) / 1e12
+    fused = kt["forward_attn_fused"]
+    a_ms = kt["attn_fused_ms"] if fused else kt["attn_ms"]
+    a_flops = kt["attn_flops"] + (kt["proj_flops"] if fused else 0.0)
+    a_bytes = kt["proj_bytes"] if fused else kt["attn_bytes"]
+    attn_tflops = a_flops / (a_ms * 1e-3) / 1e12
     traffic = None
     tfile = ROOT / "profiles" / "block_traffic.json"
     if tfile.exists():
@@ -332,12 +353,16 @@ def main() -> int:
             "mfma_frac": round(conv_tflops / PEAK_BF16_TFLOPS, 4),
         },
         "attention": {
-            "kernel": "attn_kernel<16,2,coords> (block 0)",
+            "kernel": ("attn_kernel<16,2,coords,proj> (block 0: LN1 + q/k/v projection + "
+                       "attention)") if fused else "attn_kernel<16,2,coords> (block 0)",
             "bound": "valu (d=16: one exp + ~6 VALU per score vs 64 MFMA flops)",
-            "launch_ms": round(kt["attn_ms"], 5),
+            "launch_ms": round(a_ms, 5),
             "tflops": round(attn_tflops, 2),
             "mfma_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
-            "hbm_gbs_algorithmic": round(kt["attn_bytes"] / (kt["attn_ms"] * 1e-3) / 1e9, 1),
+            "hbm_gbs_algorithmic": round(a_bytes / (a_ms * 1e-3) / 1e9, 1),
+            "two_launch_ms": {"qkv": kt["linears"]["qkv"]["ms"],
+                              "attn": round(kt["attn_ms"], 5)},
+            "one_launch_ms": None if kt["attn_fused_ms"] is None else round(kt["attn_fused_ms"], 5),
         },
         "block0_row_kernels": kt["linears"],
         "forward_tflops_padded": round(1.425e9 * B / (ms * 1e-3) / 1e12, 2),

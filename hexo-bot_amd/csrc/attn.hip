@@ -248,14 +248,47 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
   }
 }
 
-template <int DP, int HG, bool PAIR>
+// PROJ (1 or 2): q, k and v are not read from memory but projected in the
+// kernel from the block input rows p.x with the packed LN1 / q/k/v weights of
+// shrimp_pack_attn_qkv (LayerNorm folded into the products, see the
+// projection pass below):
+//   keys / values: every wave projects its own 16-row blocks (wave + 4 j)
+//     into the K and V fragments in LDS. K comes out of the weights-as-A
+//     product already in K-fragment order; V, with the operands swapped
+//     (rows as A, weights as B), in the transposed V-fragment order;
+//   queries: the same pass leaves each of the wave's query blocks (the
+//     blocks it walks later) in registers, at most PROJ_NQ per wave; waves
+//     1-3 also project the last query block when it is split over the waves.
+// PROJ = 2 regroups the grid so that the four head-pair workgroups of a
+// position run on one XCD (workgroups are dealt to the 8 XCDs round-robin):
+// the position's rows are then read from HBM into one L2, not four.
+constexpr int PROJ_NQ = 5;
+constexpr int PROJ_MAX_S = 4 * PROJ_NQ * 16;
+
+// The query registers are chosen by a run-time slot with selects over the
+// whole set; hiding each operand from the optimiser keeps it from folding
+// the selects into an indexed (scratch memory) array.
+SHRIMP_DEV u32x2 opaque2(u32x2 v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+template <int DP, int HG, bool PAIR, int PROJ>
 __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, float qk_scale,
-                                                   uint32_t qkv_bytes, int npos) {
+                                                   uint32_t qkv_bytes, int npos,
+                                                   const shrimp_attn_proj_args p, uint32_t x_bytes) {
+  static_assert(!PROJ || (DP == 16 && HG == 2 && !PAIR), "projection covers d = 16, two heads, coords");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ int span_red[16];
   constexpr int KD = DP / 16;
-  const int b = blockIdx.y;
-  const int h0 = blockIdx.x * HG;
+  int b = blockIdx.y;
+  int h0 = blockIdx.x * HG;
+  if (PROJ == 2) {
+    const int i = blockIdx.x + gridDim.x * blockIdx.y;
+    const int r = i & 31;
+    b = (i >> 5) * 8 + (r & 7);
+    h0 = (r >> 3) * HG;
+  }
   const int S = a.S;
   const int SP = (S + 15) & ~15;
   int L = a.seq_lens[b];
@@ -280,10 +313,44 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   s.xtab = reinterpret_cast<_Float16*>(tail);
 
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int lr = lane & 15;
+  const int lg = lane >> 4;
+  const int nkb = LP / 16;
   const __amdgpu_buffer_rsrc_t qrs = make_rsrc(a.q, qkv_bytes);
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.k, qkv_bytes);
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(a.v, qkv_bytes);
   const int64_t pos_base = (int64_t)b * a.qkv_sb;
+
+  // Whole query blocks round-robin over the 4 waves. When one block is left
+  // over (nqb % 4 == 1: 17 blocks at S = 264), it is split by key range into
+  // 4 parts, one per wave, instead of running whole on one wave; after a
+  // barrier the partial softmax states go through LDS (over K and V, which
+  // are no longer read) and wave 0 merges them.
+  const int nqb = (L + 15) / 16;
+  constexpr int PF = HG * (2 + 4 * KD);  // floats of one lane's partial state
+  const bool split =
+      (nqb & 3) == 1 && 3 * 64 * PF * 4 <= 2 * HG * SP * DP * 2;  // partials fit over K, V
+  const int nmain = split ? nqb - 1 : nqb;
+
+  // PROJ: row blocks this wave projects (nkb == nqb): its own blocks
+  // wave + 4 j for j < nreg, then the split block's queries (waves 1-3).
+  const int nreg = wave < nkb ? (nkb - wave + 3) / 4 : 0;
+  const int nitems = PROJ ? nreg + (split && wave > 0 ? 1 : 0) : 0;
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.x, x_bytes);
+  // rows of one 16-row block: lane (lr, lg) loads channels 32 ks + 8 lg .. +7
+  // of row blk * 16 + lr; rows past the bound read as zeros
+  auto load_x = [&](int j, u32x4 (&xf)[4]) {
+    const int row = (j < nreg ? wave + 4 * j : nmain) * 16 + lr;
+    const uint32_t off = row < L ? (uint32_t)(((int64_t)b * p.x_sb + (int64_t)row * p.x_sr) * 2) +
+                                       (uint32_t)(lg * 16)
+                                 : SHRIMP_OOB_OFFSET;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) xf[ks] = buf_load16(xrs, off + ks * 64);
+  };
+  u32x4 xnext[4];
+  if (PROJ && nitems > 0) load_x(0, xnext);
 
   // ---- global loads of the setup that nothing else depends on, issued first -----
   // coordinates and liveness of keys tid and tid + 256 (the rare keys beyond
@@ -323,6 +390,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   // Global loads are issued U at a time per thread before their LDS stores.
   constexpr int CH = DP / 8;
   constexpr int U = 5;
+  if constexpr (!PROJ) {
   {
     const int total = HG * LP * CH;
     for (int base = tid; base < total; base += 256 * U) {
@@ -399,14 +467,15 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
       }
     }
   }
+  }
   // ---- key classes, coordinates, span of the live cells ----------------------------
   int qmin = 1 << 30, qmax = -(1 << 30), rmin = 1 << 30, rmax = -(1 << 30);
   if (!PAIR) {
     for (int key = tid, i = 0; key < LP; key += 256, ++i) {
-      int q = 0, r = 0, cls = KEY_DEAD;
-      if (key < nt) {
+      int q = 0, r = 0, cls = KEY_DEAD;  // keys past the bound (tokens too) are dead
+      if (key < nt && key < L) {
         cls = KEY_TOKEN;
-      } else if (key < L) {
+      } else if (key >= nt && key < L) {
         bool live;
         if (i < 2) {
           q = i == 0 ? kq[0] : kq[1];
@@ -522,17 +591,111 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
       s.kkey[key] = (kk.x * XW + kk.y + XD * XW + XD) * 2 * HG;
     }
   }
+  // ---- PROJ: LayerNorm + q/k/v projection of this wave's row blocks ------------------
+  // The raw bf16 rows are the MFMA operand; LayerNorm is applied to the
+  // products: LN(x) W'^T + b' = rstd (x W'^T) + (b' - mean rstd cs), cs the
+  // column sums of the bf16 weights. Row statistics come from packed bf16 dot
+  // products (sum, sum of squares; variance = E[x^2] - mean^2 in fp32).
+  // Key classes are in LDS: dead keys (masked cells, keys past the bound) get
+  // zero V rows; rows past the bound zero K and Q, as the staged path reads
+  // them from the zero-padded tensor.
+  u32x2 qst[PROJ_NQ][HG];
+  if constexpr (PROJ) {
+#pragma unroll
+    for (int sl = 0; sl < PROJ_NQ; ++sl)
+#pragma unroll
+      for (int h = 0; h < HG; ++h) qst[sl][h] = u32x2{0u, 0u};
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(p.packed, QKV_W_BYTES);
+    const float* pbias = reinterpret_cast<const float*>(static_cast<const unsigned char*>(p.packed) + QKV_B_OFF);
+    const float* pcs = reinterpret_cast<const float*>(static_cast<const unsigned char*>(p.packed) + QKV_CS_OFF);
+    auto wfrag = [&](int ks, int nb) {
+      return buf_load16(wrs, (uint32_t)(((ks * QKV_NB + nb) * 64 + lane) * 16));
+    };
+    const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3F803F80u);
+    for (int j = 0; j < nitems; ++j) {
+      u32x4 xf[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) xf[ks] = xnext[ks];
+      if (j + 1 < nitems) load_x(j + 1, xnext);
+      const bool kv = j < nreg;  // wave-uniform
+      const int kb = kv ? wave + 4 * j : nmain;
+      const bool rowv = kb * 16 + lr < L;
+      // statistics of row lr (32 channels per lane, 4 lane groups)
+      float sx = 0.f, sq = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          // element copied out first: __builtin_bit_cast of a vector element
+          // (xf[ks][w] directly) reads element 0 whatever the index
+          const unsigned u = xf[ks][w];
+          const bf16x2 v = __builtin_bit_cast(bf16x2, u);
+          sx = __builtin_amdgcn_fdot2_f32_bf16(v, ones, sx, false);
+          sq = __builtin_amdgcn_fdot2_f32_bf16(v, v, sq, false);
+        }
+      const float mean = sum_groups_swap(sx) * (1.0f / QKV_C);
+      const float var = fmaxf(sum_groups_swap(sq) * (1.0f / QKV_C) - mean * mean, 0.f);
+      const float rstd = rsqrtf(var + p.eps);
+      const float nmr = -mean * rstd;
+      // the V fragment holds rows 4 lg + i: their statistics from lanes 4 lg + i
+      float vr[4], vn[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        vr[i] = __shfl(rstd, lg * 4 + i, 64);
+        vn[i] = __shfl(nmr, lg * 4 + i, 64);
+      }
+      // outputs n0 + 4 lg .. +3 of row lr (Q, K fragment order)
+      auto proj_rows = [&](int n0, f32x4 acc) -> u32x2 {
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(pbias + n0 + lg * 4);
+        const f32x4 cc = *reinterpret_cast<const f32x4*>(pcs + n0 + lg * 4);
+        float y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] = fmaf(acc[i], rstd, fmaf(nmr, cc[i], bb[i]));
+        return rowv ? u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])} : u32x2{0u, 0u};
+      };
+#pragma unroll
+      for (int h = 0; h < HG; ++h) {
+        const int hh = h0 + h;
+        // queries: outputs 16 hh + 4 lg .. +3 of row lr
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) acc = mfma16x16x32(wfrag(ks, hh), xf[ks], acc);
+        const u32x2 qv = proj_rows(hh * 16, acc);
+#pragma unroll
+        for (int sl = 0; sl < PROJ_NQ; ++sl) qst[sl][h] = sl == j ? qv : opaque2(qst[sl][h]);
+        if (kv) {
+          // keys: outputs QKV_C + 16 hh + 4 lg .. +3 of row lr = K-fragment order
+          acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) acc = mfma16x16x32(wfrag(ks, 8 + hh), xf[ks], acc);
+          *reinterpret_cast<u32x2*>(s.Ks + (h * NKB + kb) * 256 + (lg * 16 + lr) * 4) =
+              proj_rows(QKV_C + hh * 16, acc);
+          // values: rows 4 lg .. +3 of output 2 QKV_C + 16 hh + lr = V-fragment order
+          const int nv = 2 * QKV_C + hh * 16 + lr;
+          const float bv = pbias[nv], cv = pcs[nv];
+          acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) acc = mfma16x16x32(xf[ks], wfrag(ks, 16 + hh), acc);
+          const int4 cls = *reinterpret_cast<const int4*>(s.kcls + kb * 16 + lg * 4);
+          const int cl[4] = {cls.x, cls.y, cls.z, cls.w};
+          float y[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            y[i] = cl[i] != KEY_DEAD ? fmaf(acc[i], vr[i], fmaf(vn[i], cv, bv)) : 0.f;
+          *reinterpret_cast<u32x2*>(s.Vt + (h * NKB + kb) * 256 + (lg * 16 + lr) * 4) =
+              u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+        }
+      }
+    }
+  }
   __syncthreads();
 
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int lr = lane & 15;
-  const int lg = lane >> 4;
-  const int nkb = LP / 16;
-
   // One query block over key blocks [k0, k1): online-softmax state in m, l, o.
-  auto run_block = [&](int qb, int k0, int k1, AttnQuery& qi, float (&m)[HG], float (&l)[HG],
-                       f32x4 (&o)[HG][KD]) {
+  // PROJ: the block's queries are slot `slot` of the registers filled above
+  // (slot j of a wave = its block wave + 4 j; the split block's slot follows
+  // the wave's own blocks).
+  auto run_block = [&](int qb, int slot, int k0, int k1, AttnQuery& qi, float (&m)[HG],
+                       float (&l)[HG], f32x4 (&o)[HG][KD]) {
     qi.query = qb * 16 + lr;
     qi.qv = qi.query < L;
     qi.qtok = qi.query < nt;
@@ -549,13 +712,22 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     // token or dead queries in this block: general path (wave-uniform)
     const bool qgen = q_gen[qb] != 0;
     u32x2 qf[HG][KD];
+    if constexpr (PROJ) {
 #pragma unroll
-    for (int h = 0; h < HG; ++h)
+      for (int h = 0; h < HG; ++h) {
+        qf[h][0] = opaque2(qst[0][h]);
 #pragma unroll
-      for (int kd = 0; kd < KD; ++kd) {
-        const int64_t e = pos_base + (int64_t)(h0 + h) * a.qkv_sh + qi.query * DP + kd * 16 + lg * 4;
-        qf[h][kd] = buf_load8(qrs, qi.qv ? (uint32_t)(e * 2) : SHRIMP_OOB_OFFSET);
+        for (int sl = 1; sl < PROJ_NQ; ++sl) qf[h][0] = slot == sl ? opaque2(qst[sl][h]) : qf[h][0];
       }
+    } else {
+#pragma unroll
+      for (int h = 0; h < HG; ++h)
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd) {
+          const int64_t e = pos_base + (int64_t)(h0 + h) * a.qkv_sh + qi.query * DP + kd * 16 + lg * 4;
+          qf[h][kd] = buf_load8(qrs, qi.qv ? (uint32_t)(e * 2) : SHRIMP_OOB_OFFSET);
+        }
+    }
 #pragma unroll
     for (int h = 0; h < HG; ++h) {
       m[h] = SHRIMP_NEG_BIG;
@@ -642,25 +814,16 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     }
   };
 
-  // Whole query blocks round-robin over the 4 waves. When one block is left
-  // over (nqb % 4 == 1: 17 blocks at S = 264), it is split by key range into
-  // 4 parts, one per wave, instead of running whole on one wave; after a
-  // barrier the partial softmax states go through LDS (over K and V, which
-  // are no longer read) and wave 0 merges them.
-  const int nqb = (L + 15) / 16;
-  constexpr int PF = HG * (2 + 4 * KD);  // floats of one lane's partial state
-  const bool split =
-      (nqb & 3) == 1 && 3 * 64 * PF * 4 <= 2 * HG * SP * DP * 2;  // partials fit over K, V
-  const int nmain = split ? nqb - 1 : nqb;
+  // (query blocks round-robin over the waves, the split last block: see nmain)
   AttnQuery qi;
   float m[HG], l[HG];
   f32x4 o[HG][KD];
-  for (int qb = wave;; qb += 4) {
+  for (int qb = wave, slot = 0;; qb += 4, ++slot) {
     const bool tail = qb >= nmain;
     if (tail && !split) break;
     const int k0 = tail ? (wave * nkb) / 4 : 0;
     const int k1 = tail ? ((wave + 1) * nkb) / 4 : nkb;
-    run_block(tail ? nmain : qb, k0, k1, qi, m, l, o);
+    run_block(tail ? nmain : qb, slot, k0, k1, qi, m, l, o);
     if (tail) break;
     store_block(qi, l, o);
   }
@@ -739,8 +902,9 @@ template <int DP, int HG, bool PAIR>
 static int launch_attn(const shrimp_attn_args* a, float qk_scale, uint32_t qkv_bytes, int npos,
                        size_t smem, hipStream_t st) {
   dim3 grid(a->H / HG, a->B);
-  hipLaunchKernelGGL((attn_kernel<DP, HG, PAIR>), grid, dim3(256), smem, st, *a, qk_scale,
-                     qkv_bytes, npos);
+  const shrimp_attn_proj_args none{};
+  hipLaunchKernelGGL((attn_kernel<DP, HG, PAIR, 0>), grid, dim3(256), smem, st, *a, qk_scale,
+                     qkv_bytes, npos, none, 0u);
   return check_launch("attn");
 }
 
@@ -843,4 +1007,45 @@ extern "C" int shrimp_attn(const shrimp_attn_args* a, void* stream) {
   SHRIMP_REQUIRE(a->n_tokens == a->S || (a->coords && a->mask), "attn: coords mode needs coords and mask");
   const int w = 2 * a->lut_m + 1;
   return dispatch_attn<false>(a, qk_scale, (uint32_t)(extent * 2), w * w + 3, w * w, st);
+}
+
+extern "C" int shrimp_attn_fused_supported(int C, int H, int S, int dpad) {
+  return C == QKV_C && H == 8 && dpad == 16 && S > 0 && S <= PROJ_MAX_S &&
+         attn_smem_bytes(16, 2, S, 0, false) <= kAttnSmemCap;
+}
+
+extern "C" int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_proj_args* p,
+                                 void* stream) {
+  SHRIMP_REQUIRE(a != nullptr && p != nullptr, "attn_fused: null args");
+  SHRIMP_REQUIRE(a->B >= 0 && a->S > 0 && a->H > 0, "attn_fused: bad shape");
+  if (a->B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(shrimp_attn_fused_supported(a->H * a->d, a->H, a->S, a->dpad),
+                 "attn_fused: covers C = %d, H = 8, dpad = 16, S <= %d (got C = %d, H = %d, "
+                 "dpad = %d, S = %d)", QKV_C, PROJ_MAX_S, a->H * a->d, a->H, a->dpad, a->S);
+  SHRIMP_REQUIRE(a->pair == nullptr, "attn_fused: coords mode only");
+  SHRIMP_REQUIRE(a->o && a->seq_lens && p->x && p->packed, "attn_fused: null pointer");
+  SHRIMP_REQUIRE(a->o_sb % 4 == 0 && a->o_sh % 4 == 0 && a->o_sr % 4 == 0,
+                 "attn_fused: output strides must be multiples of 4");
+  SHRIMP_REQUIRE(a->n_tokens >= 0 && a->n_tokens <= a->S, "attn_fused: bad n_tokens");
+  SHRIMP_REQUIRE(a->btab && a->lut_m >= 0 && a->lut_m <= 64, "attn_fused: needs btab");
+  SHRIMP_REQUIRE(a->n_tokens == a->S || (a->coords && a->mask),
+                 "attn_fused: needs coords and mask");
+  SHRIMP_REQUIRE(p->x_sr >= QKV_C && p->x_sr % 8 == 0 && p->x_sb % 8 == 0 &&
+                     p->x_sb >= (int64_t)(a->S - 1) * p->x_sr + QKV_C,
+                 "attn_fused: x strides (row %lld, position %lld)", (long long)p->x_sr,
+                 (long long)p->x_sb);
+  const int64_t xe = ((int64_t)(a->B - 1) * p->x_sb + (int64_t)(a->S - 1) * p->x_sr + QKV_C) * 2;
+  SHRIMP_REQUIRE(xe < (int64_t)0x7FFF0000, "attn_fused: input rows too large");
+  const int w = 2 * a->lut_m + 1;
+  const size_t smem = attn_smem_bytes(16, 2, a->S, w * w + 3, false);
+  const float qk_scale = SHRIMP_LOG2E / sqrtf((float)a->d);
+  dim3 grid(a->H / 2, a->B);
+  // the XCD grouping needs whole groups of 8 positions (grid.x = 4 head pairs)
+  if (a->B % 8 == 0)
+    hipLaunchKernelGGL((attn_kernel<16, 2, false, 2>), grid, dim3(256), smem, as_stream(stream),
+                       *a, qk_scale, 0u, w * w, *p, (uint32_t)xe);
+  else
+    hipLaunchKernelGGL((attn_kernel<16, 2, false, 1>), grid, dim3(256), smem, as_stream(stream),
+                       *a, qk_scale, 0u, w * w, *p, (uint32_t)xe);
+  return check_launch("attn_fused");
 }

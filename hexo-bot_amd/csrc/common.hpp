@@ -116,6 +116,53 @@ SHRIMP_DEV float max_groups_swap(float x) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// ---- LayerNorm of 16 rows of 128 channels, MFMA operand layout ------------------
+//
+// Lane (lr, lg) holds channels 32 ks + 8 lg + e (ks < 4, e < 8) of row lr in
+// xf[ks] (bf16); hf receives the normalised row without affine, bf16, in the
+// same layout (the B operand of a 16x16x32 MFMA against output-major weight
+// fragments, or its A operand against input-major ones). Statistics are fp32:
+// mean first, then the centred sum of squares. An all-zero row gives zeros.
+SHRIMP_DEV void ln_row128(const u32x4 (&xf)[4], float eps, u32x4 (&hf)[4]) {
+  float s = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) s += bf16_lo(xf[ks][w]) + bf16_hi(xf[ks][w]);
+  const float mean = sum_groups_swap(s) * (1.0f / 128);
+  float q = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float u0 = bf16_lo(xf[ks][w]) - mean, u1 = bf16_hi(xf[ks][w]) - mean;
+      q = fmaf(u0, u0, fmaf(u1, u1, q));
+    }
+  const float rstd = rsqrtf(sum_groups_swap(q) * (1.0f / 128) + eps);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      hf[ks][w] = pack_bf16x2((bf16_lo(xf[ks][w]) - mean) * rstd, (bf16_hi(xf[ks][w]) - mean) * rstd);
+}
+
+// ---- packed LN1 + q/k/v weights of the attention block (C = 128) -----------------
+//
+// shrimp_pack_attn_qkv output: bf16 MFMA fragments of W' = Wqkv diag(ln1_w)
+// (rows: q 0-127, k 128-255, v 256-383), fragment (ks, nb) holding outputs
+// 16 nb .. +15 over input channels 32 ks .. +31, lane (lr, lg) at byte
+// ((ks * 24 + nb) * 64 + lane) * 16 with output 16 nb + lr and inputs
+// 32 ks + 8 lg .. +7; then the 384 folded fp32 biases b' = bqkv + Wqkv ln1_b;
+// then the 384 fp32 column sums cs[n] = sum_k W'[n][k] of the bf16 weights
+// (LN(x) W'^T = rstd (x W'^T - mean cs) lets a kernel feed raw rows to MFMA).
+constexpr int QKV_C = 128;
+constexpr int QKV_N = 3 * QKV_C;
+constexpr int QKV_NB = QKV_N / 16;
+constexpr uint32_t QKV_W_BYTES = QKV_C * QKV_N * 2;
+constexpr uint32_t QKV_B_OFF = QKV_W_BYTES;
+constexpr uint32_t QKV_CS_OFF = QKV_B_OFF + QKV_N * 4;  // fp32 sum over k of the bf16 W'[n][k]
+constexpr uint32_t QKV_PACK_BYTES = QKV_CS_OFF + QKV_N * 4;
+
 SHRIMP_DEV float wave_sum(float v) {
   for (int m = 32; m >= 1; m >>= 1) v += xor_shfl(v, m);
   return v;

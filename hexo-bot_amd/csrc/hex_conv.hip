@@ -23,7 +23,16 @@
 
 namespace shrimp {
 
-enum : int { EPI_LN = 1, EPI_RELU = 2, EPI_RESID = 4, EPI_HEAD = 8 };
+// EPI_BACC: the accumulators started from the bias (no bias add here).
+enum : int { EPI_LN = 1, EPI_RELU = 2, EPI_RESID = 4, EPI_HEAD = 8, EPI_BACC = 16 };
+
+// ReLU of two packed bf16: as 16-bit integers, every value with the sign bit
+// set is below 0, so a packed integer max against 0 is the float max.
+SHRIMP_DEV unsigned relu_bf16x2(unsigned w) {
+  typedef __attribute__((ext_vector_type(2))) short s16x2;
+  const s16x2 v = __builtin_bit_cast(s16x2, w);
+  return __builtin_bit_cast(unsigned, __builtin_elementwise_max(v, s16x2{0, 0}));
+}
 
 // Bias / LayerNorm / ReLU / mask / residual / head epilogue on the fp32
 // accumulators of MB row blocks. rb, rn: position and cell index of this
@@ -47,6 +56,7 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
   constexpr int NB = COUT / 16;
   constexpr bool LN = (EPI & EPI_LN) != 0, RESID = (EPI & EPI_RESID) != 0;
   constexpr bool HEAD = (EPI & EPI_HEAD) != 0, RELU = (EPI & EPI_RELU) != 0;
+  constexpr bool BACC = (EPI & EPI_BACC) != 0;
   constexpr bool PRE = PSRC == PS_REGS;
   constexpr bool FROM_LDS = PSRC == PS_LDS || PSRC == PS_LDSREG;
   constexpr bool HREG = PSRC == PS_LDSREG;  // bias / ln_w read from LDS once, kept in registers
@@ -118,9 +128,14 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
     float v[NB][4];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      const f32x4 bb = P_b(nb);
+      if constexpr (BACC) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[nb][j] = acc[nb][mb][j] + bb[j];
+        for (int j = 0; j < 4; ++j) v[nb][j] = acc[nb][mb][j];
+      } else {
+        const f32x4 bb = P_b(nb);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[nb][j] = acc[nb][mb][j] + bb[j];
+      }
     }
     if constexpr (LN) {
       float s = 0.f;
@@ -184,17 +199,20 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
         if constexpr (RESID) {
           const u32x2 rw = rbuf[mb % RD][nb];
           const f32x4 g = P_g(nb);
-          o[0] = fmaxf(fmaf(g[0], o[0], bf16_lo(rw.x)), 0.f);
-          o[1] = fmaxf(fmaf(g[1], o[1], bf16_hi(rw.x)), 0.f);
-          o[2] = fmaxf(fmaf(g[2], o[2], bf16_lo(rw.y)), 0.f);
-          o[3] = fmaxf(fmaf(g[3], o[3], bf16_hi(rw.y)), 0.f);
-        } else if constexpr (LNMASK && RELU) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) o[j] = fmaxf(o[j], 0.f);
+          o[0] = fmaf(g[0], o[0], bf16_lo(rw.x));
+          o[1] = fmaf(g[1], o[1], bf16_hi(rw.x));
+          o[2] = fmaf(g[2], o[2], bf16_lo(rw.y));
+          o[3] = fmaf(g[3], o[3], bf16_hi(rw.y));
         }
         u32x2 pk;
         pk.x = pack_bf16x2(o[0], o[1]);
         pk.y = pack_bf16x2(o[2], o[3]);
+        // the residual block's ReLU, and ReLU after a masking LayerNorm, on the
+        // rounded values (the same result as before rounding)
+        if constexpr (RESID || (LNMASK && RELU)) {
+          pk.x = relu_bf16x2(pk.x);
+          pk.y = relu_bf16x2(pk.y);
+        }
         store(mb, nb, pk);
       }
     }
@@ -217,6 +235,37 @@ struct GlobalRowStore {
   }
   SHRIMP_DEV void operator()(int mb, int nb, u32x2 pk) const {
     *reinterpret_cast<u32x2*>(p[mb] + nb * 16) = pk;
+  }
+};
+
+// Store functor for 128-channel rows with 16-byte stores: the output blocks
+// come in pairs (nb even, then nb + 1); one lane-group swap (v_permlane16_swap)
+// gives each lane 8 adjacent channels, lane group g of the pair's 32 channels
+// taking 8 g' .. 8 g' + 7 with g' = 2 (g & 1) + (g >> 1), so the four lane
+// groups of a row cover its 64 bytes. Needs o_sb, o_sn multiples of 8 and a
+// 16-byte aligned output; rows of a lane group exist or not together.
+template <int MB>
+struct GlobalRowStore16 {
+  unsigned short* p[MB];
+  u32x2 pend;
+  SHRIMP_DEV GlobalRowStore16(const shrimp_conv_args& a, const int (&rb)[MB], const int (&rn)[MB],
+                              int lg) {
+    const int sub = (lg & 1) * 16 + (lg >> 1) * 8;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      p[mb] = static_cast<unsigned short*>(a.out) + (int64_t)rb[mb] * a.o_sb +
+              (int64_t)rn[mb] * a.o_sn + sub;
+  }
+  SHRIMP_DEV void operator()(int mb, int nb, u32x2 pk) {
+    if ((nb & 1) == 0) {
+      pend = pk;
+      return;
+    }
+    // even rows of a 16-lane pair keep their block-nb channels and receive the
+    // partner's; odd rows receive the partner's block-(nb+1) channels
+    const auto sx = __builtin_amdgcn_permlane16_swap(pend.x, pk.x, false, false);
+    const auto sy = __builtin_amdgcn_permlane16_swap(pend.y, pk.y, false, false);
+    *reinterpret_cast<u32x4*>(p[mb] + (nb >> 1) * 32) = u32x4{sx[0], sy[0], sx[1], sy[1]};
   }
 };
 
@@ -554,6 +603,16 @@ SHRIMP_DEV void big_wload(__amdgpu_buffer_rsrc_t wr, int s, int lane, u32x4 (&w)
   for (int nb = 0; nb < 8; ++nb) w[nb] = buf_load16(wr, (uint32_t)(((s * 8 + nb) * 64 + lane) * 16));
 }
 
+// Accumulators start from the conv bias (lane: channels 16 nb + 4 lg .. + 3).
+SHRIMP_DEV void big_acc_init(f32x4 (&acc)[8][8], const float* bias, int lg) {
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) {
+    const f32x4 bb = *reinterpret_cast<const f32x4*>(bias + nb * 16 + lg * 4);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = bb;
+  }
+}
+
 // One 7-tap, 128 -> 128 conv over the rows in LDS: acc += sum_t W_t^T X[idx_t]^T.
 // On entry wf holds k-step 0 of `wr`.
 SHRIMP_DEV void big_pass(f32x4 (&acc)[8][8], u32x4 (&wf)[8], const BigTile& t,
@@ -610,15 +669,28 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
   big_wload(wr, 0, t.lane, wf);
   float* lp = reinterpret_cast<float*>(xs + 4 * t.NR * 64);
   big_params(lp, a.bias, a.ln_w, a.ln_b, (EPI & EPI_HEAD) ? a.head_w : a.gamma);
+  // the accumulators start from the bias, except for the residual epilogue,
+  // which adds it at the end like the fused ConvBlock's second conv (the two
+  // give bit-identical blocks)
+  constexpr int BA = (EPI & EPI_RESID) ? 0 : EPI_BACC;
   f32x4 acc[8][8];
+  if constexpr (BA != 0) {
+    big_acc_init(acc, a.bias, t.lg);
+  } else {
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb)
+    for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   big_pass(acc, wf, t, xs, wr);
-  conv_epilogue<128, 8, EPI, PS_LDS>(a, acc, t.rb, t.rn, t.rv, t.lg, lp);
+  if constexpr ((EPI & EPI_HEAD) != 0) {
+    conv_epilogue<128, 8, EPI | BA, PS_LDS>(a, acc, t.rb, t.rn, t.rv, t.lg, lp);
+  } else {
+    conv_epilogue<128, 8, EPI | BA, PS_LDS>(a, acc, t.rb, t.rn, t.rv, t.lg, lp,
+                                            GlobalRowStore16<8>(a, t.rb, t.rn, t.lg));
+  }
 }
 
 // ConvBlock in one launch (ConvBlock.forward, model.py:395-422):
@@ -627,8 +699,9 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
 // conv1 stages x and runs as the big-tile conv; after a barrier its epilogue
 // writes y1 (bf16, masked rows zero) into the same LDS layout, and conv2
 // gathers from there, so y1 never reaches HBM. The zero row N stays zero.
-// `c2.resid` is x and `c2.out` may alias it: a lane reads the residual
-// elements it later overwrites, and a position only touches its own rows.
+// `c2.resid` is x and `c2.out` may alias it: a wave's residual reads of a row
+// block complete before that block's stores (the stored values depend on
+// them), and a wave only touches its own rows.
 __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_args c1,
                                                            const shrimp_conv_args c2,
                                                            uint32_t x_bytes, uint32_t w_bytes) {
@@ -644,10 +717,7 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
   big_params(lp1, c1.bias, c1.ln_w, c1.ln_b, nullptr);
   big_params(lp2, c2.bias, c2.ln_w, c2.ln_b, c2.gamma);
   f32x4 acc[8][8];
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-    for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  big_acc_init(acc, c1.bias, t.lg);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   // conv2's first weights are loaded after conv1's epilogue, whose bias and
@@ -664,13 +734,15 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
       swz[mb] = (uint32_t)((t.rn[mb] >> 2) & 3);
     }
     const int lg = t.lg;
-    conv_epilogue<128, 8, EPI_LN | EPI_RELU, PS_LDSREG>(
+    conv_epilogue<128, 8, EPI_LN | EPI_RELU | EPI_BACC, PS_LDSREG>(
         c1, acc, t.rb, t.rn, t.rv, t.lg, lp1, [&](int mb, int nb, u32x2 pk) {
           const uint32_t piece = (uint32_t)((nb & 1) * 2 + (lg >> 1));
           const uint32_t addr = (uint32_t)(nb >> 1) * nr64 + row[mb] + ((piece ^ swz[mb]) << 4) + lo;
           *reinterpret_cast<u32x2*>(xs + addr) = pk;
         });
   }
+  // conv2 starts from zeros and adds its bias in the epilogue: starting from
+  // the bias here makes the register allocator spill
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
@@ -687,7 +759,8 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
   asm volatile("" : "+v"(t.lane));
   t.lg = t.lane >> 4;
   big_pass(acc, wf, t, xs, wr2);
-  conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(c2, acc, t.rb, t.rn, t.rv, t.lg, lp2);
+  conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(c2, acc, t.rb, t.rn, t.rv, t.lg, lp2,
+                                                    GlobalRowStore16<8>(c2, t.rb, t.rn, t.lg));
 }
 
 // ---- weight packing ------------------------------------------------------------
@@ -723,7 +796,9 @@ __global__ void pack_weight_kernel(const float* __restrict__ src, unsigned short
 template <int COUT, int MB, int EPI>
 static int launch_conv(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, size_t lds,
                        hipStream_t st) {
-  if (COUT == 128 && lds && a->cin_pad == 128 && a->taps == 7 && a->N <= BIG_MAX_N &&
+  const bool out16 = (EPI & EPI_HEAD) != 0 ||
+                     (a->o_sn % 8 == 0 && a->o_sb % 8 == 0 && ((uintptr_t)a->out & 15) == 0);
+  if (COUT == 128 && lds && a->cin_pad == 128 && a->taps == 7 && a->N <= BIG_MAX_N && out16 &&
       (g_conv_variant == 0 || g_conv_variant == 3)) {
     const int waves = (a->N + 127) / 128;
     const size_t big_lds = (size_t)big_rows_padded(a->N) * 256 + BIG_PARAMS * sizeof(float);
@@ -902,7 +977,9 @@ extern "C" int shrimp_conv_block(const shrimp_conv_args* c1, const shrimp_conv_a
   SHRIMP_REQUIRE((reinterpret_cast<uintptr_t>(c1->x) & 15) == 0 && c1->x_sn >= 128 &&
                      c1->x_sn % 8 == 0 && c1->x_sb % 8 == 0,
                  "conv_block: x rows must be 16-byte aligned");
-  SHRIMP_REQUIRE(c2->o_sn % 4 == 0 && c2->o_sb % 4 == 0, "conv_block: output strides %% 4");
+  SHRIMP_REQUIRE(c2->o_sn % 8 == 0 && c2->o_sb % 8 == 0 &&
+                     (reinterpret_cast<uintptr_t>(c2->out) & 15) == 0,
+                 "conv_block: output rows must be 16-byte aligned (strides %% 8)");
   const int64_t x_extent =
       (int64_t)(c1->B - 1) * c1->x_sb + (int64_t)(c1->N - 1) * c1->x_sn + c1->cin_pad;
   SHRIMP_REQUIRE(x_extent * 2 < (int64_t)0x7FFF0000, "conv_block: activation buffer too large");

@@ -28,12 +28,12 @@ __global__ void scale_rows_cols_kernel(const float* __restrict__ src, const floa
 
 namespace {
 
-constexpr int QC = 128;                         // channels
-constexpr int QN = 3 * QC;                      // outputs
+constexpr int QC = QKV_C;                       // channels
+constexpr int QN = QKV_N;                       // outputs
 constexpr int QWAVES = 12;                      // waves per workgroup (3 per SIMD)
-constexpr uint32_t QW_LDS = QC * QN * 2;        // 98304 bytes of fragments
-constexpr uint32_t QB_OFF = QW_LDS;             // folded bias (fp32) after the fragments
-constexpr uint32_t QPACK_BYTES = QB_OFF + QN * 4;
+constexpr uint32_t QW_LDS = QKV_W_BYTES;        // 98304 bytes of fragments
+constexpr uint32_t QB_OFF = QKV_B_OFF;          // folded bias (fp32) after the fragments
+constexpr uint32_t QPACK_BYTES = QKV_PACK_BYTES;
 
 SHRIMP_DEV void load_rows16(const shrimp_qkv_args& a, __amdgpu_buffer_rsrc_t xr, int row, int lg,
                             u32x4 (&xf)[QC / 32]) {
@@ -89,28 +89,8 @@ __global__ __launch_bounds__(QWAVES * 64, 1) void attn_qkv_kernel(const shrimp_q
 
     // LayerNorm over the 128 channels of this lane's row: 32 in this lane
     // (k = 32 ks + 8 lg + e), the rest in the 3 other lane groups.
-    float s = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) s += bf16_lo(cur[ks][w]) + bf16_hi(cur[ks][w]);
-    const float mean = sum_groups_swap(s) * (1.0f / QC);
-    float q = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float u0 = bf16_lo(cur[ks][w]) - mean, u1 = bf16_hi(cur[ks][w]) - mean;
-        q = fmaf(u0, u0, fmaf(u1, u1, q));
-      }
-    const float rstd = rsqrtf(sum_groups_swap(q) * (1.0f / QC) + a.eps);
     u32x4 hf[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int w = 0; w < 4; ++w)
-        hf[ks][w] = pack_bf16x2((bf16_lo(cur[ks][w]) - mean) * rstd,
-                                (bf16_hi(cur[ks][w]) - mean) * rstd);
+    ln_row128(cur, a.eps, hf);
 
     // destination of this lane's row in the head-major layout
     const bool rv = row < a.rows;
@@ -153,6 +133,20 @@ __global__ void qkv_bias_kernel(const float* __restrict__ w, const float* __rest
   out[n] = s;
 }
 
+// cs[n] = sum_k W'[n][k] over the packed bf16 fragments (output n = 16 nb + lr
+// sits in lane lr + 16 lg of fragment (ks, nb), inputs 32 ks + 8 lg .. +7).
+__global__ void qkv_colsum_kernel(const unsigned short* __restrict__ frag, float* __restrict__ cs) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= QN) return;
+  const int nb = n / 16, lr = n % 16;
+  float s = 0.f;
+  for (int ks = 0; ks < QC / 32; ++ks)
+    for (int lg = 0; lg < 4; ++lg)
+      for (int e = 0; e < 8; ++e)
+        s += bf16_bits_to_f32(frag[(((ks * (QN / 16) + nb) * 64) + lg * 16 + lr) * 8 + e]);
+  cs[n] = s;
+}
+
 }  // namespace shrimp
 
 using namespace shrimp;
@@ -177,6 +171,8 @@ extern "C" int shrimp_pack_attn_qkv(const float* qkv_w, const float* qkv_b, cons
                      (int64_t)1, (int64_t)QC, 0);
   hipLaunchKernelGGL(qkv_bias_kernel, dim3((QN + 255) / 256), dim3(256), 0, st, qkv_w, qkv_b,
                      ln_b, reinterpret_cast<float*>(pk + QB_OFF));
+  hipLaunchKernelGGL(qkv_colsum_kernel, dim3((QN + 255) / 256), dim3(256), 0, st,
+                     reinterpret_cast<const unsigned short*>(pk), reinterpret_cast<float*>(pk + QKV_CS_OFF));
   return check_launch("pack_attn_qkv");
 }
 

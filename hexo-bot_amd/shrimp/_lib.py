@@ -60,6 +60,12 @@ class AttnArgs(ctypes.Structure):
     ]
 
 
+class AttnProjArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", _vp), ("x_sb", _i64), ("x_sr", _i64), ("packed", _vp), ("eps", _f32),
+    ]
+
+
 class TailArgs(ctypes.Structure):
     _fields_ = [
         ("seq", _vp), ("s_sb", _i64), ("mask", _vp), ("ln_w", _vp), ("ln_b", _vp),
@@ -116,6 +122,8 @@ SIGNATURES: dict = {
     "shrimp_attn_mlp_pack_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
     "shrimp_pack_attn_mlp": (ctypes.c_int, [ctypes.POINTER(MlpWeights), _vp, _vp, _vp]),
     "shrimp_attn": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _vp]),
+    "shrimp_attn_fused": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.POINTER(AttnProjArgs), _vp]),
+    "shrimp_attn_fused_supported": (ctypes.c_int, [ctypes.c_int] * 4),
     "shrimp_attn_bias_table": (
         ctypes.c_int,
         [_vp, ctypes.c_int, ctypes.c_int, _vp] + [ctypes.c_int] * 4 + [_vp, _vp, _vp],

@@ -265,6 +265,34 @@ def launch_attn(
     _lib.check(_lib.load().shrimp_attn(ctypes_ref(a), s), "attn")
 
 
+def attn_fused_supported(C: int, H: int, S: int, dpad: int) -> bool:
+    """Shapes the one-launch LN1 -> q/k/v -> attention kernel covers."""
+
+    return bool(_lib.load().shrimp_attn_fused_supported(C, H, S, dpad))
+
+
+def launch_attn_fused(
+    *, x, x_sb, x_sr, packed, eps, seq_lens, o, o_sb, o_sh, o_sr, B, S, H, d, dpad,
+    coords=None, mask8=None, btab=None, xtab=None, lut_m=CELL_LUT_M, n_tokens=NUM_TOKENS,
+    stream=None,
+):
+    """AttnBlock LN1 -> q/k/v -> RelPosAttention in one launch (model.py:497-503, 448-492);
+    ``packed`` is the output of ``pack_attn_qkv``, ``x`` the block input rows."""
+
+    _check_rows("attn_fused x", x, x_sb, x_sr, B, S, H * d)
+    a = _lib.AttnArgs(
+        q=None, k=None, v=None, qkv_sb=0, qkv_sh=0, seq_lens=seq_lens.data_ptr(), pair=None,
+        p_sb=0, p_sq=0, table2=None, table_rows=0, coords=_lib.ptr(coords),
+        mask=_lib.ptr(mask8), btab=_lib.ptr(btab), xtab=_lib.ptr(xtab), lut_m=lut_m,
+        n_tokens=n_tokens, o=o.data_ptr(), o_sb=o_sb, o_sh=o_sh, o_sr=o_sr,
+        B=B, S=S, H=H, d=d, dpad=dpad,
+    )
+    pj = _lib.AttnProjArgs(x=x.data_ptr(), x_sb=x_sb, x_sr=x_sr, packed=packed.data_ptr(),
+                           eps=float(eps))
+    s = _lib.stream_handle() if stream is None else stream
+    _lib.check(_lib.load().shrimp_attn_fused(ctypes_ref(a), ctypes_ref(pj), s), "attn_fused")
+
+
 def ctypes_ref(struct):
     import ctypes
 

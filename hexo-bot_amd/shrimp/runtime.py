@@ -36,7 +36,9 @@ from .geometry import CELL_LUT_M
 from .ops import (
     attn_bias_table,
     conv_block_supported,
+    attn_fused_supported,
     launch_attn,
+    launch_attn_fused,
     launch_attn_mlp,
     launch_attn_qkv,
     launch_conv,
@@ -84,6 +86,11 @@ class HipForward:
         # LN1 + q/k/v kernel with LN1 folded into its weights where it
         # applies; off runs the linear kernel's QKV mode.
         self.use_fused_qkv = True
+        # LN1 + q/k/v projection inside the attention kernel (no q/k/v
+        # tensor, 3 x B x S x C bf16 less memory) where it applies; off (the
+        # default: about 1% faster at B=512) runs the q/k/v kernel, then
+        # attention.
+        self.use_fused_attn = False
         # ConvBlock as one launch (conv1's output kept in LDS) where a fused
         # kernel exists; off runs the two convolutions.
         self.use_fused_block = True
@@ -378,7 +385,11 @@ class HipForward:
         )
         cells = seq[:, NUM_TOKENS:]
         y1 = torch.empty((B, N, C), dtype=bf, device=dev)
-        qkv = (torch.zeros if d != dpad else torch.empty)((3, B, H, S, dpad), dtype=bf, device=dev)
+        attn_fused = (P.fused_qkv and self.use_fused_qkv and self.use_fused_attn
+                      and attn_fused_supported(C, H, S, dpad))
+        qkv = None
+        if not attn_fused:
+            qkv = (torch.zeros if d != dpad else torch.empty)((3, B, H, S, dpad), dtype=bf, device=dev)
         att = torch.empty((B, S, C), dtype=bf, device=dev)
         fused = P.fused_mlp and self.use_fused_mlp
         hid = None if fused else torch.empty((B, S, 2 * C), dtype=bf, device=dev)
@@ -417,7 +428,16 @@ class HipForward:
             else:
                 a = P.attn[ai]
                 ai += 1
-                if P.fused_qkv and self.use_fused_qkv:
+                bias_args = dict(
+                    seq_lens=seq_lens, o=att, o_sb=S * C, o_sh=d, o_sr=C, B=B, S=S, H=H, d=d,
+                    dpad=dpad, coords=coords32, mask8=mask8, btab=a.btab_xtab[0],
+                    xtab=a.btab_xtab[1] if self.use_linear_bias else None, lut_m=CELL_LUT_M,
+                    n_tokens=NUM_TOKENS, stream=st,
+                )
+                if attn_fused:
+                    launch_attn_fused(x=seq, x_sb=S * C, x_sr=C, packed=a.qkv, eps=a.eps1,
+                                      **bias_args)
+                elif P.fused_qkv and self.use_fused_qkv:
                     launch_attn_qkv(x=seq, x_sr=C, qkv=qkv, packed=a.qkv, eps=a.eps1, rows=rows,
                                     B=B, S=S, H=H, C=C, dpad=dpad, stream=st)
                 else:
@@ -426,13 +446,9 @@ class HipForward:
                         n_out=3 * C, mode=_lib.LIN_QKV, out=qkv, ln_w=a.ln1w, ln_b=a.ln1b,
                         eps=a.eps1, B=B, S=S, H=H, dpad=dpad, stream=st,
                     )
-                launch_attn(
-                    q=qkv[0], k=qkv[1], v=qkv[2], qkv_sb=H * S * dpad, qkv_sh=S * dpad,
-                    seq_lens=seq_lens, o=att, o_sb=S * C, o_sh=d, o_sr=C, B=B, S=S, H=H, d=d,
-                    dpad=dpad, coords=coords32, mask8=mask8, btab=a.btab_xtab[0],
-                    xtab=a.btab_xtab[1] if self.use_linear_bias else None, lut_m=CELL_LUT_M,
-                    n_tokens=NUM_TOKENS, stream=st,
-                )
+                if not attn_fused:
+                    launch_attn(q=qkv[0], k=qkv[1], v=qkv[2], qkv_sb=H * S * dpad,
+                                qkv_sh=S * dpad, **bias_args)
                 if fused:
                     launch_attn_mlp(
                         x=att, x_sr=C, seq=seq, s_sr=C, mask=seq_mask, packed=a.mlp,
@@ -484,6 +500,6 @@ class HipForward:
             self.last = dict(
                 P=P, B=B, N=N, S=S, idx=idx, mask8=mask8, coords32=coords32, seq_lens=seq_lens,
                 seq_mask=seq_mask, seq=seq, y1=y1, qkv=qkv, att=att, hid=hid, seqf=seqf,
-                stream=st,
+                stream=st, attn_fused=attn_fused,
             )
         return out

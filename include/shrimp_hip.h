@@ -128,7 +128,8 @@ int shrimp_hex_conv(const shrimp_conv_args* a, void* stream);
  *     B, N, cin_pad, cout (out / resid / head unused);
  * c2: w, bias, ln_w, ln_b, eps, relu = 0, resid = c1.x (same strides),
  *     gamma, out, o_sb, o_sn (x, idx, mask, B, N are taken from c1).
- * out may alias x. shrimp_conv_block_supported reports whether a fused
+ * out may alias x; out must be 16-byte aligned with o_sb, o_sn multiples of 8
+ * (rows leave as 16-byte stores). shrimp_conv_block_supported reports whether a fused
  * kernel exists for the shape (taps 7, 128 -> 128 channels, N <= 512, and
  * the automatic conv variant selected); otherwise shrimp_conv_block returns
  * SHRIMP_EINVAL and the caller runs the two convolutions.
@@ -182,7 +183,8 @@ int shrimp_linear(const shrimp_linear_args* a, void* stream);
  *   n = LN1(x[r]) ;  [q | k | v] = n @ Wqkv^T + bqkv   -> qkv (3, B, H, S, dpad)
  * with rows r = (b, s). The padding lanes d..dpad of qkv are not written.
  * shrimp_pack_attn_qkv folds LN1's affine into the weights (W diag(ln_w),
- * b + W ln_b) and writes MFMA fragments and the folded bias to `packed`
+ * b + W ln_b) and writes MFMA fragments, the folded bias and the column sums
+ * of the bf16 weights (used by shrimp_attn_fused) to `packed`
  * (shrimp_attn_qkv_pack_bytes(C) bytes; 0 = unsupported C). qkv_w is the
  * (3C, C) concatenation of q_proj / k_proj / v_proj weights (fp32), qkv_b
  * their biases; `scratch` holds 3C * C floats during packing.
@@ -296,6 +298,28 @@ typedef struct {
 } shrimp_attn_args;
 
 int shrimp_attn(const shrimp_attn_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * AttnBlock LN1 -> q/k/v projection -> attention in one launch
+ * (model.py:497-503 then RelPosAttention, model.py:448-492): the result of
+ * shrimp_attn_qkv followed by shrimp_attn up to rounding (LayerNorm is folded
+ * into the projection, so the normalised rows are not rounded to bf16),
+ * without the (3, B, H, S, dpad) q/k/v tensor. Each workgroup projects its
+ * heads' keys and values into LDS and its queries into registers from the
+ * position's rows and the packed weights of shrimp_pack_attn_qkv.
+ * Covers C = 128, H = 8 (d = dpad = 16), coords mode, S <= 320; a->q, a->k,
+ * a->v and a->qkv_* are not read. shrimp_attn_fused_supported(C, H, S,
+ * dpad) is 1 for those shapes (other shapes take the two launches).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* x;        /* (B, S, C) bf16 block input (before LN1) */
+  int64_t x_sb, x_sr;   /* elements between positions / rows */
+  const void* packed;   /* shrimp_pack_attn_qkv output */
+  float eps;            /* LN1 epsilon */
+} shrimp_attn_proj_args;
+
+int shrimp_attn_fused_supported(int C, int H, int S, int dpad);
+int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_proj_args* p, void* stream);
 
 #define SHRIMP_ATTN_XD 26
 

@@ -38,6 +38,9 @@ int main(void) {
   F(shrimp_attn_args, o_sh); F(shrimp_attn_args, o_sr); F(shrimp_attn_args, B);
   F(shrimp_attn_args, S); F(shrimp_attn_args, H); F(shrimp_attn_args, d);
   F(shrimp_attn_args, dpad);
+  Z(shrimp_attn_proj_args);
+  F(shrimp_attn_proj_args, x); F(shrimp_attn_proj_args, x_sb); F(shrimp_attn_proj_args, x_sr);
+  F(shrimp_attn_proj_args, packed); F(shrimp_attn_proj_args, eps);
   Z(shrimp_tail_args);
   F(shrimp_tail_args, seq); F(shrimp_tail_args, s_sb); F(shrimp_tail_args, mask);
   F(shrimp_tail_args, ln_w); F(shrimp_tail_args, ln_b); F(shrimp_tail_args, eps);

@@ -129,6 +129,32 @@ def test_fused_and_unfused_mlp_paths_agree(cfg4_batch):
         assert err <= 1e-2, key
 
 
+def test_fused_attention_option_matches_oracle(cfg4_batch):
+    """The one-launch LN1 + q/k/v + attention option (no q/k/v tensor): the
+    forward stays within tolerance of the oracle and of the default two-launch
+    path (LayerNorm is folded into the projection there, so the bits differ)."""
+
+    b = cfg4_batch
+    layout = "CCACCACCACCA"
+    net = _net(128, 8, layout, seed=5)
+    base = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+    rt = net.hip_runtime()
+    rt.use_fused_attn = True
+    try:
+        fused = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+    finally:
+        rt.use_fused_attn = False
+    want = ofwd.forward_policy_value(
+        weights.make_state_dict(128, 8, layout, seed=5), layout, 8, b["feats"], b["nbr"],
+        b["mask"], b["coords"], request_moves_left=True, dtype=torch.float32,
+    )
+    _check(fused, want, b["mask"], "cfg4 B=32 fused attention")
+    for key in ("policy", "value", "moves_left"):
+        err = (fused[key] - base[key]).abs().max().item()
+        print(f"fused vs two-launch attention {key}: {err:.3e}", flush=True)
+        assert err <= 1e-2, key
+
+
 def test_rows_are_independent_of_batch(cfg4_batch):
     """padded == single-row (tests/test_shrimp_model.py:139-164): a row's
     outputs do not depend on the rest of the batch (bit-exact here)."""

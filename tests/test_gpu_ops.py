@@ -540,6 +540,92 @@ def test_attn_offset_table_cfg2():
     close(out, want, atol=1e-2, what="cfg2 attention")
 
 
+def _attn_block_ref(x, w, b, lnw, lnb, coords, mask, lens, table, H, eps=1e-5):
+    """float64 LN1 -> q/k/v -> biased, key-masked attention with the packer's
+    folded weights (bf16 W diag(ln_w), fp32 b + W ln_b) and the reference's
+    pair rows (tables.pair_rows): (B, H, S, d); rows past the bound are 0."""
+
+    B, S, c = x.shape
+    d = c // H
+    n = torch.nn.functional.layer_norm(x.double(), (c,), None, None, eps)
+    y = n @ bf(w * lnw[None, :]).T + (b.double() + w.double() @ lnb.double())
+    q, k, v = y.reshape(B, S, 3, H, d).permute(2, 0, 3, 1, 4)
+    pair = torch.from_numpy(tables.pair_rows(coords.numpy(), mask.numpy()))
+    bias = table.double()[pair].permute(0, 3, 1, 2)  # (B, H, S, S)
+    keys = torch.arange(S)
+    live = torch.cat([torch.ones(B, 8, dtype=torch.bool), mask.bool()], dim=1)
+    live &= keys[None, :] < lens[:, None].long()
+    bias = torch.where(live[:, None, None, :], bias, torch.full_like(bias, float("-inf")))
+    s = (q @ k.transpose(-2, -1)) / math.sqrt(d) + bias
+    out = torch.softmax(s, dim=-1) @ v
+    rows = keys[None, :] < lens[:, None].long()
+    return torch.where(rows[:, None, :, None], out, torch.zeros_like(out))
+
+
+@pytest.mark.parametrize("S,lens,wide", [
+    # 17 query blocks (the last one split over the waves), ragged bounds, a
+    # bound inside the tokens, tokens only, an empty position
+    (264, [264, 251, 8 + 16 * 16 + 1, 40, 5, 8, 0], False),
+    # coordinates wider than the unclamped table: clamped-LUT path
+    (264, [264, 200, 137], True),
+    (40, [40, 33, 17], False),
+    # the longest sequence the kernel covers (20 blocks, 5 per wave)
+    (320, [320, 300, 8 + 16 * 16 + 1], False),
+])
+def test_attn_fused_matches_reference(S, lens, wide):
+    """LN1 -> q/k/v -> attention in one launch against a float64 restatement
+    (tolerance 2e-2 + 2e-2 |want|: q/k/v, P and V are bf16, the offset table
+    fp16), and against the q/k/v kernel followed by the attention kernel (which
+    rounds the normalised rows to bf16 before the projection: within 3e-2).
+    Rows past each position's bound are exactly zero."""
+
+    from shrimp import ops
+    from shrimp.constants import BIAS_ROWS
+    from shrimp.geometry import CELL_LUT_M, cell_bias_lut
+
+    torch.manual_seed(11)
+    c, H, d, nt = 128, 8, 16, 8
+    B, N = len(lens), S - 8
+    x = (torch.randn(B, S, c) * 1.5 + 0.3).to(torch.bfloat16)
+    w, b = torch.randn(3 * c, c) * 0.08, torch.randn(3 * c) * 0.1
+    lnw, lnb = torch.rand(c) + 0.5, torch.randn(c) * 0.1
+    packed = ops.pack_attn_qkv(w.to(DEV), b.to(DEV), lnw.to(DEV), lnb.to(DEV))
+    span = 40 if wide else 6
+    coords = torch.randint(-span, span + 1, (B, N, 2), dtype=torch.int32)
+    mask = torch.rand(B, N) > 0.2
+    seq_lens = torch.tensor(lens, dtype=torch.int32)
+    table = torch.randn(BIAS_ROWS, H) * 0.5
+    lut = torch.from_numpy(cell_bias_lut()).to(DEV)
+    btab, xtab = ops.attn_bias_table(table.to(DEV), lut, CELL_LUT_M)
+    assert ops.attn_fused_supported(c, H, S, 16)
+    xd = x.to(DEV)
+    outs = []
+    for fused in (True, False):
+        o = torch.full((B, S, c), 7.0, dtype=torch.bfloat16, device=DEV)
+        kw = dict(seq_lens=seq_lens.to(DEV), o=o, o_sb=S * c, o_sh=d, o_sr=c, B=B, S=S, H=H,
+                  d=d, dpad=16, coords=coords.to(DEV), mask8=mask.to(DEV, torch.uint8),
+                  btab=btab, xtab=xtab, lut_m=CELL_LUT_M, n_tokens=nt)
+        if fused:
+            ops.launch_attn_fused(x=xd, x_sb=S * c, x_sr=c, packed=packed, eps=1e-5, **kw)
+        else:
+            qkv = torch.empty((3, B, H, S, 16), dtype=torch.bfloat16, device=DEV)
+            ops.launch_attn_qkv(x=xd, x_sr=c, qkv=qkv, packed=packed, eps=1e-5, rows=B * S, B=B,
+                                S=S, H=H, C=c, dpad=16)
+            ops.launch_attn(q=qkv[0], k=qkv[1], v=qkv[2], qkv_sb=H * S * 16, qkv_sh=S * 16, **kw)
+        outs.append(o.cpu())
+    got, two = outs
+    for i, L in enumerate(lens):
+        assert (got[i, L:] == 0).all(), f"position {i}: rows past the bound"
+    want = _attn_block_ref(x, w, b, lnw, lnb, coords, mask, seq_lens, table, H)
+    g4 = got.double().reshape(B, S, H, d).permute(0, 2, 1, 3)
+    print(f"attn fused S={S} wide={wide}: max |got - f64| = {(g4 - want).abs().max().item():.3e}",
+          flush=True)
+    close(g4, want, atol=2e-2, rtol=2e-2, what=f"attn fused S={S} wide={wide}")
+    diff = (got.double() - two.double()).abs().max().item()
+    print(f"attn fused S={S} wide={wide}: max |fused - two launches| = {diff:.3e}", flush=True)
+    assert diff <= 3e-2
+
+
 def test_decode_kernel(golden):
     from shrimp import _lib
 

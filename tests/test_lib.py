@@ -51,6 +51,7 @@ def test_struct_layouts_match_c(tmp_path):
         "shrimp_conv_args": _lib.ConvArgs,
         "shrimp_linear_args": _lib.LinearArgs,
         "shrimp_attn_args": _lib.AttnArgs,
+        "shrimp_attn_proj_args": _lib.AttnProjArgs,
         "shrimp_tail_args": _lib.TailArgs,
         "shrimp_qkv_args": _lib.QkvArgs,
         "shrimp_mlp_weights": _lib.MlpWeights,
@@ -84,6 +85,21 @@ def test_bad_arguments_fail_with_message(lib):
     assert lib.shrimp_attn(ctypes.byref(aa), None) == -1
     assert b"head dim" in lib.shrimp_last_error()
     assert lib.shrimp_build_ray_index(1, 1, 1, 5000, 1, None) == -1
+    # one-launch LN1 + q/k/v + attention: C = 128, H = 8, dpad = 16, S <= 320 only
+    assert lib.shrimp_attn_fused_supported(128, 8, 264, 16) == 1
+    assert lib.shrimp_attn_fused_supported(128, 8, 320, 16) == 1
+    assert lib.shrimp_attn_fused_supported(128, 8, 321, 16) == 0
+    assert lib.shrimp_attn_fused_supported(128, 4, 264, 32) == 0
+    assert lib.shrimp_attn_fused_supported(64, 8, 264, 16) == 0
+    pj = _lib.AttnProjArgs(x=1, x_sb=264 * 128, x_sr=128, packed=1, eps=1e-5)
+    fa = _lib.AttnArgs(B=1, S=400, H=8, d=16, dpad=16, o=1, seq_lens=1, btab=1, coords=1,
+                       mask=1, o_sb=400 * 128, o_sh=16, o_sr=128, n_tokens=8)
+    assert lib.shrimp_attn_fused(ctypes.byref(fa), ctypes.byref(pj), None) == -1
+    assert b"S <= 320" in lib.shrimp_last_error()
+    fa.S = 264
+    pj.x_sr = 100
+    assert lib.shrimp_attn_fused(ctypes.byref(fa), ctypes.byref(pj), None) == -1
+    assert b"x strides" in lib.shrimp_last_error()
 
 
 def test_missing_library_raises(tmp_path):
