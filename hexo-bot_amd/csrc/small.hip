@@ -7,68 +7,116 @@
 
 namespace shrimp {
 
-__device__ __forceinline__ int64_t load_index(const void* p, int dt, int64_t i) {
-  switch (dt) {
-    case SHRIMP_DT_I64: return static_cast<const int64_t*>(p)[i];
-    case SHRIMP_DT_I32: return static_cast<const int32_t*>(p)[i];
-    case SHRIMP_DT_U16: {
-      const unsigned v = static_cast<const uint16_t*>(p)[i];
-      return v == 0xFFFFu ? -1 : (int64_t)v;
-    }
-    default: return -1;
+// Typed loads for the flat preparation loops (the element type is chosen once,
+// outside the loop, so the loop body has no branch and keeps loads in flight).
+template <int DT>
+SHRIMP_DEV int64_t load_index_t(const void* __restrict__ p, int64_t i) {
+  if constexpr (DT == SHRIMP_DT_I64) return static_cast<const int64_t*>(p)[i];
+  else if constexpr (DT == SHRIMP_DT_I32) return static_cast<const int32_t*>(p)[i];
+  else {
+    const unsigned v = static_cast<const uint16_t*>(p)[i];
+    return v == 0xFFFFu ? -1 : (int64_t)v;
   }
+}
+template <int DT>
+SHRIMP_DEV float load_feat_t(const void* __restrict__ p, int64_t i) {
+  if constexpr (DT == SHRIMP_DT_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (DT == SHRIMP_DT_F16) return (float)static_cast<const _Float16*>(p)[i];
+  else return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
 }
 
-__device__ __forceinline__ float load_feat(const void* p, int dt, int64_t i) {
-  switch (dt) {
-    case SHRIMP_DT_F32: return static_cast<const float*>(p)[i];
-    case SHRIMP_DT_F16: return (float)static_cast<const _Float16*>(p)[i];
-    case SHRIMP_DT_BF16: return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
-    default: return 0.f;
+// idx rows of one position: tap 0 = the cell itself, taps 1..6 its neighbours
+// (outside [0, N) -> N).
+// Each loop runs over the elements i0, i0 + step, ... of one position.
+template <int DT>
+SHRIMP_DEV void prep_idx(const void* __restrict__ nbr, int64_t base, int N, int32_t* __restrict__ ib,
+                         int i0, int step) {
+#pragma unroll 4
+  for (int i = i0; i < N * 7; i += step) {
+    const int n = i / 7, k = i - n * 7;
+    int32_t v = n;
+    if (k > 0) {
+      const int64_t j = load_index_t<DT>(nbr, (base + n) * 6 + k - 1);
+      v = (j >= 0 && j < N) ? (int32_t)j : N;
+    }
+    ib[i] = v;
   }
 }
+// 16 dwords (32 bf16 channels) per cell, zero past nfeat.
+template <int DT>
+SHRIMP_DEV void prep_feats(const void* __restrict__ feats, int nfeat, int64_t base, int N,
+                           unsigned* __restrict__ xb, int i0, int step) {
+#pragma unroll 4
+  for (int i = i0; i < N * 16; i += step) {
+    const int f = (i & 15) * 2;
+    const int64_t r = base + (i >> 4);
+    const float v0 = f < nfeat ? load_feat_t<DT>(feats, r * nfeat + f) : 0.f;
+    const float v1 = f + 1 < nfeat ? load_feat_t<DT>(feats, r * nfeat + f + 1) : 0.f;
+    xb[i] = pack_bf16x2(v0, v1);
+  }
+}
+template <int DT>
+SHRIMP_DEV void prep_coords(const void* __restrict__ coords, int64_t base, int N,
+                            int32_t* __restrict__ c32, int i0, int step) {
+#pragma unroll 4
+  for (int i = i0; i < N * 2; i += step)
+    c32[base * 2 + i] = (int32_t)load_index_t<DT>(coords, base * 2 + i);
+}
+
+// A position's flat loops are spread over PREP_PARTS workgroups (blockIdx.y),
+// so each thread has one or two rounds of loads in flight; the first
+// workgroup of a position also writes its token rows and seq_lens.
+constexpr int PREP_PARTS = 4;
 
 // ---- input preparation (model.py:861-863, 884-892; batching.py:264-276) --------
-__global__ __launch_bounds__(256) void prep_kernel(const void* nbr, int nbr_dt, const void* mask,
-                                                   const void* coords, int coords_dt,
-                                                   const void* feats, int feats_dt, int nfeat,
-                                                   int N, int n_tokens, int32_t* idx,
-                                                   uint8_t* mask8, int32_t* coords32,
-                                                   int32_t* seq_lens, uint8_t* seq_mask,
-                                                   uint16_t* xin) {
+// One workgroup per position; each output array is written by a flat loop over
+// its elements, so consecutive lanes touch consecutive addresses.
+// The pointers are __restrict__ and the loops unrolled, so each thread keeps
+// several loads in flight instead of one load / wait / store per element.
+__global__ __launch_bounds__(256) void prep_kernel(const void* __restrict__ nbr, int nbr_dt,
+                                                   const void* __restrict__ mask,
+                                                   const void* __restrict__ coords, int coords_dt,
+                                                   const void* __restrict__ feats, int feats_dt,
+                                                   int nfeat, int N, int n_tokens,
+                                                   int32_t* __restrict__ idx,
+                                                   uint8_t* __restrict__ mask8,
+                                                   int32_t* __restrict__ coords32,
+                                                   int32_t* __restrict__ seq_lens,
+                                                   uint8_t* __restrict__ seq_mask,
+                                                   uint16_t* __restrict__ xin) {
   const int b = blockIdx.x;
   const int64_t base = (int64_t)b * N;
+  const int i0 = blockIdx.y * blockDim.x + threadIdx.x;
+  const int step = PREP_PARTS * blockDim.x;
+  if (idx) {
+    int32_t* ib = idx + base * 7;
+    if (nbr_dt == SHRIMP_DT_I64) prep_idx<SHRIMP_DT_I64>(nbr, base, N, ib, i0, step);
+    else if (nbr_dt == SHRIMP_DT_I32) prep_idx<SHRIMP_DT_I32>(nbr, base, N, ib, i0, step);
+    else prep_idx<SHRIMP_DT_U16>(nbr, base, N, ib, i0, step);
+  }
+  if (xin) {
+    unsigned* xb = reinterpret_cast<unsigned*>(xin + base * 32);
+    if (feats_dt == SHRIMP_DT_F32) prep_feats<SHRIMP_DT_F32>(feats, nfeat, base, N, xb, i0, step);
+    else if (feats_dt == SHRIMP_DT_F16) prep_feats<SHRIMP_DT_F16>(feats, nfeat, base, N, xb, i0, step);
+    else prep_feats<SHRIMP_DT_BF16>(feats, nfeat, base, N, xb, i0, step);
+  }
+  if (coords32) {
+    if (coords_dt == SHRIMP_DT_I64) prep_coords<SHRIMP_DT_I64>(coords, base, N, coords32, i0, step);
+    else prep_coords<SHRIMP_DT_I32>(coords, base, N, coords32, i0, step);
+  }
+  for (int n = i0; n < N; n += step) {
+    const int64_t r = base + n;
+    const bool live = static_cast<const uint8_t*>(mask)[r] != 0;
+    if (mask8) mask8[r] = live ? 1 : 0;
+    if (seq_mask) seq_mask[(int64_t)b * (n_tokens + N) + n_tokens + n] = live ? 1 : 0;
+  }
+  if (blockIdx.y != 0) return;  // uniform
   if (seq_mask)
     for (int t = threadIdx.x; t < n_tokens; t += blockDim.x)
       seq_mask[(int64_t)b * (n_tokens + N) + t] = 1;
   int last = 0;  // 1 + index of the last live cell
-  for (int n = threadIdx.x; n < N; n += blockDim.x) {
-    const int64_t r = base + n;
-    const bool live = static_cast<const uint8_t*>(mask)[r] != 0;
-    if (live) last = n + 1;
-    if (mask8) mask8[r] = live ? 1 : 0;
-    if (seq_mask) seq_mask[(int64_t)b * (n_tokens + N) + n_tokens + n] = live ? 1 : 0;
-    if (idx) {
-      idx[r * 7] = n;
-#pragma unroll
-      for (int k = 0; k < 6; ++k) {
-        const int64_t j = load_index(nbr, nbr_dt, r * 6 + k);
-        idx[r * 7 + 1 + k] = (j >= 0 && j < N) ? (int32_t)j : N;
-      }
-    }
-    if (coords32) {
-      coords32[r * 2] = (int32_t)load_index(coords, coords_dt, r * 2);
-      coords32[r * 2 + 1] = (int32_t)load_index(coords, coords_dt, r * 2 + 1);
-    }
-    if (xin) {
-#pragma unroll 4
-      for (int f = 0; f < 32; f += 2) {
-        const float v0 = f < nfeat ? load_feat(feats, feats_dt, r * nfeat + f) : 0.f;
-        const float v1 = f + 1 < nfeat ? load_feat(feats, feats_dt, r * nfeat + f + 1) : 0.f;
-        reinterpret_cast<unsigned*>(xin + r * 32)[f / 2] = pack_bf16x2(v0, v1);
-      }
-    }
-  }
+  for (int n = threadIdx.x; n < N; n += blockDim.x)
+    if (static_cast<const uint8_t*>(mask)[base + n] != 0) last = n + 1;
   if (seq_lens) {
     __shared__ int red[256];
     red[threadIdx.x] = last;
@@ -90,47 +138,59 @@ __global__ __launch_bounds__(256) void prep_csr_kernel(const uint16_t* __restric
                                                        const int16_t* __restrict__ qr,
                                                        const uint16_t* __restrict__ nbr,
                                                        const int64_t* __restrict__ offsets, int row0,
-                                                       int N, int n_tokens, int32_t* idx,
-                                                       uint8_t* mask8, int32_t* coords32,
-                                                       int32_t* seq_lens, uint8_t* seq_mask,
-                                                       uint16_t* xin) {
+                                                       int N, int n_tokens, int32_t* __restrict__ idx,
+                                                       uint8_t* __restrict__ mask8,
+                                                       int32_t* __restrict__ coords32,
+                                                       int32_t* __restrict__ seq_lens,
+                                                       uint8_t* __restrict__ seq_mask,
+                                                       uint16_t* __restrict__ xin) {
   const int b = blockIdx.x;
   const int64_t o = offsets[row0 + b];
   const int64_t cnt = offsets[row0 + b + 1] - o;
   const int n = cnt < 0 ? 0 : (cnt > N ? N : (int)cnt);
   const int64_t base = (int64_t)b * N;
-  if (seq_mask)
+  const int i0 = blockIdx.y * blockDim.x + threadIdx.x;
+  const int step = PREP_PARTS * blockDim.x;
+  if (seq_mask && blockIdx.y == 0)
     for (int t = threadIdx.x; t < n_tokens; t += blockDim.x)
       seq_mask[(int64_t)b * (n_tokens + N) + t] = 1;
-  for (int i = threadIdx.x; i < N; i += blockDim.x) {
-    const int64_t r = base + i;
-    const bool live = i < n;
-    const int64_t c = o + i;
-    if (mask8) mask8[r] = live ? 1 : 0;
-    if (seq_mask) seq_mask[(int64_t)b * (n_tokens + N) + n_tokens + i] = live ? 1 : 0;
-    if (idx) {
-      idx[r * 7] = i;
-#pragma unroll
-      for (int k = 0; k < 6; ++k) {
-        const unsigned j = live ? nbr[c * 6 + k] : 0xFFFFu;
-        idx[r * 7 + 1 + k] = (int)j < N ? (int32_t)j : N;
-      }
-    }
-    if (coords32) {
-      coords32[r * 2] = live ? qr[c * 2] : 0;
-      coords32[r * 2 + 1] = live ? qr[c * 2 + 1] : 0;
-    }
-    if (xin) {
+  // flat loops over each output array (consecutive lanes, consecutive addresses)
+  if (idx) {
+    int32_t* ib = idx + base * 7;
 #pragma unroll 4
-      for (int f = 0; f < 32; f += 2) {
-        const float v0 = live && f < nfeat ? (float)__builtin_bit_cast(_Float16, feats[c * nfeat + f]) : 0.f;
-        const float v1 =
-            live && f + 1 < nfeat ? (float)__builtin_bit_cast(_Float16, feats[c * nfeat + f + 1]) : 0.f;
-        reinterpret_cast<unsigned*>(xin + r * 32)[f / 2] = pack_bf16x2(v0, v1);
+    for (int i = i0; i < N * 7; i += step) {
+      const int r = i / 7, k = i - r * 7;
+      int32_t v = r;
+      if (k > 0) {
+        const unsigned j = r < n ? nbr[(o + r) * 6 + k - 1] : 0xFFFFu;
+        v = (int)j < N ? (int32_t)j : N;
       }
+      ib[i] = v;
     }
   }
-  if (seq_lens && threadIdx.x == 0) seq_lens[b] = n_tokens + n;
+  if (xin) {
+    unsigned* xb = reinterpret_cast<unsigned*>(xin + base * 32);
+#pragma unroll 4
+    for (int i = i0; i < N * 16; i += step) {
+      const int r = i >> 4, f = (i & 15) * 2;
+      const bool live = r < n;
+      const int64_t c = o + r;
+      const float v0 = live && f < nfeat ? (float)__builtin_bit_cast(_Float16, feats[c * nfeat + f]) : 0.f;
+      const float v1 =
+          live && f + 1 < nfeat ? (float)__builtin_bit_cast(_Float16, feats[c * nfeat + f + 1]) : 0.f;
+      xb[i] = pack_bf16x2(v0, v1);
+    }
+  }
+  if (coords32)
+    for (int i = i0; i < N * 2; i += step)
+      coords32[base * 2 + i] = (i >> 1) < n ? qr[o * 2 + i] : 0;
+  for (int i = i0; i < N; i += step) {
+    const int64_t r = base + i;
+    const bool live = i < n;
+    if (mask8) mask8[r] = live ? 1 : 0;
+    if (seq_mask) seq_mask[(int64_t)b * (n_tokens + N) + n_tokens + i] = live ? 1 : 0;
+  }
+  if (seq_lens && blockIdx.y == 0 && threadIdx.x == 0) seq_lens[b] = n_tokens + n;
 }
 
 __global__ void fill_tokens_kernel(const float* __restrict__ tokens, int n_tokens, int C,
@@ -245,11 +305,12 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a)
 
 // Pass 2: one head (value or moves-left, blockIdx.y) for kHeadPos positions
 // per workgroup: hid = relu(in @ Wr + br) (in = [T | T' | pooled], 3C),
-// out = hid @ Wh + bh. Weights are transposed (k-major) so consecutive lanes
-// read consecutive outputs; the K range is split over the idle threads and
-// reduced through LDS.
+// out = hid @ Wh + bh. Weights are transposed (k-major) so consecutive lanes read consecutive
+// outputs; the K range is split over the kHeadThreads / C (then / bins)
+// thread slices and reduced through LDS.
 constexpr int kHeadPos = 4;
-__global__ __launch_bounds__(256) void value_head_kernel(const shrimp_tail_args a) {
+constexpr int kHeadThreads = 1024;
+__global__ __launch_bounds__(kHeadThreads) void value_head_kernel(const shrimp_tail_args a) {
   extern __shared__ float hs[];
   const int C = a.C, bins = a.bins, K1 = 3 * C;
   const int head = blockIdx.y;
@@ -262,8 +323,8 @@ __global__ __launch_bounds__(256) void value_head_kernel(const shrimp_tail_args 
   const int b0 = blockIdx.x * kHeadPos;
   const int np = min(kHeadPos, a.B - b0);
   const int t = threadIdx.x;
-  const int ks1 = 256 / C;         // K slices, layer 1
-  const int ks2 = 256 / bins;      // K slices, layer 2
+  const int ks1 = kHeadThreads / C;     // K slices, layer 1
+  const int ks2 = kHeadThreads / bins;  // K slices, layer 2
   float* in = hs;                              // [kHeadPos][K1]
   float* red = in + kHeadPos * K1;             // [ks1][kHeadPos][C]
   float* hid = red + ks1 * kHeadPos * C;       // [kHeadPos][C]
@@ -498,7 +559,7 @@ extern "C" int shrimp_prep_inputs(const void* nbr, int nbr_dt, const void* mask,
                           (feats_dt == SHRIMP_DT_F32 || feats_dt == SHRIMP_DT_F16 ||
                            feats_dt == SHRIMP_DT_BF16)),
                  "prep_inputs: feats dtype / width");
-  hipLaunchKernelGGL(prep_kernel, dim3(B), dim3(256), 0, as_stream(stream), nbr, nbr_dt, mask,
+  hipLaunchKernelGGL(prep_kernel, dim3(B, PREP_PARTS), dim3(256), 0, as_stream(stream), nbr, nbr_dt, mask,
                      coords, coords_dt, feats, feats_dt, nfeat, N, n_tokens, idx, mask8, coords32,
                      seq_lens, seq_mask, static_cast<uint16_t*>(xin));
   return check_launch("prep_inputs");
@@ -515,7 +576,7 @@ extern "C" int shrimp_prep_csr(const void* node_feats, int nfeat, const int16_t*
   SHRIMP_REQUIRE(!coords32 || node_qr, "prep_csr: coords need node_qr");
   SHRIMP_REQUIRE(!xin || (node_feats && nfeat > 0 && nfeat <= 32), "prep_csr: feats (nfeat %d)",
                  nfeat);
-  hipLaunchKernelGGL(prep_csr_kernel, dim3(B), dim3(256), 0, as_stream(stream),
+  hipLaunchKernelGGL(prep_csr_kernel, dim3(B, PREP_PARTS), dim3(256), 0, as_stream(stream),
                      static_cast<const uint16_t*>(node_feats), nfeat, node_qr, nbr, row_offsets,
                      row0, N, n_tokens, idx, mask8, coords32, seq_lens, seq_mask,
                      static_cast<uint16_t*>(xin));
@@ -556,11 +617,11 @@ extern "C" int shrimp_trunk_tail(const shrimp_tail_args* a, void* stream) {
   else hipLaunchKernelGGL(final_ln_kernel<32>, dim3(a->B), dim3(256), lsm, st, *a);
   if (int rc = check_launch("trunk_tail/ln")) return rc;
   if (!a->value && !a->moves_left) return SHRIMP_OK;
-  const int ks1 = 256 / a->C, ks2 = 256 / a->bins;
+  const int ks1 = kHeadThreads / a->C, ks2 = kHeadThreads / a->bins;
   const size_t smem = ((size_t)kHeadPos * 3 * a->C + (size_t)ks1 * kHeadPos * a->C +
                        (size_t)kHeadPos * a->C + (size_t)ks2 * kHeadPos * a->bins) * sizeof(float);
-  hipLaunchKernelGGL(value_head_kernel, dim3((a->B + kHeadPos - 1) / kHeadPos, 2), dim3(256),
-                     smem, st, *a);
+  hipLaunchKernelGGL(value_head_kernel, dim3((a->B + kHeadPos - 1) / kHeadPos, 2),
+                     dim3(kHeadThreads), smem, st, *a);
   return check_launch("trunk_tail/heads");
 }
 
