@@ -217,6 +217,58 @@ def evaluator_timing(net, count: int = B, graphs: bool = False, reps: int = 5) -
     }
 
 
+def featurize_timing(rows, reps: int = 20) -> dict:
+    """The featurizer row: the 512 cfg4 decision states (placement records)
+    -> padded forward inputs on the device (``shrimp_featurize``), timed with
+    HIP events around the launch (records already resident); the host builder
+    (``build_position`` + ``collate_rows``, one thread) on the same states for
+    comparison. The device output is checked against the host batch."""
+
+    import ctypes
+
+    import torch
+
+    from shrimp import _lib
+    from shrimp.batching import collate_rows
+    from shrimp.featurize import featurize, pack_records
+    from shrimp.features import build_position
+    from shrimp.synthetic import CONFIGS
+
+    facts = [f for f, _, _ in rows]
+    rad = CONFIGS["cfg4"].radius  # the support radius the positions were drawn for
+    dev = torch.device("cuda")
+    out = featurize(facts, radius=rad, npad=NPAD, device=dev)
+    t0 = time.perf_counter()
+    host = collate_rows([build_position(f, radius=rad) for f in facts], pad_to=NPAD)
+    host_s = time.perf_counter() - t0
+    exact = bool(torch.equal(out["feats"].cpu(), host["feats"]) and
+                 torch.equal(out["nbr"].cpu().long(), host["nbr"]))
+    pk = {k: torch.from_numpy(v).to(dev) for k, v in pack_records(facts).items()}
+    lib = _lib.load()
+    st = _lib.stream_handle(dev)
+    b = len(facts)
+    args = [pk["qr"].data_ptr(), pk["owner"].data_ptr(), pk["index"].data_ptr(),
+            pk["offsets"].data_ptr(), pk["player"].data_ptr(), pk["phase"].data_ptr(), b, rad, NPAD,
+            out["feats"].data_ptr(), out["nbr"].data_ptr(),
+            torch.empty((b, NPAD), dtype=torch.uint8, device=dev).data_ptr(),
+            out["coords"].data_ptr(), out["counts"].data_ptr(), out["status"].data_ptr(), st]
+    run = lambda: _lib.check(lib.shrimp_featurize(*args), "featurize")
+    run()
+    ms = _events_time(run, reps, torch.cuda.current_stream(dev))
+    stones = int(pk["offsets"][-1].item())
+    return {
+        "kernel": "featurize_kernel (records -> support, node order, nbr, 15 planes, padded)",
+        "positions": b,
+        "launch_ms": round(ms, 5),
+        "positions_per_s": round(b / (ms * 1e-3), 1),
+        "input_bytes": stones * 12 + (b + 1) * 8 + 2 * b,
+        "output_bytes": b * NPAD * (15 * 4 + 6 * 4 + 1 + 2 * 4),
+        "host_builder_positions_per_s": round(b / host_s, 1),
+        "host_builder_threads": 1,
+        "matches_host_builder": exact,
+    }
+
+
 def cpu_baseline(batch, seconds: float):
     """Oracle fp32 eager forward (the reference CPU path, restated) on a
     bounded sample of the same workload; positions/s on the host cores."""
@@ -366,6 +418,7 @@ def main() -> int:
         },
         "block0_row_kernels": kt["linears"],
         "forward_tflops_padded": round(1.425e9 * B / (ms * 1e-3) / 1e12, 2),
+        "featurize": featurize_timing(batch["rows"]),
         "evaluator": evaluator_timing(net),
         "evaluator_graphs": evaluator_timing(net, graphs=True),
         "evaluator_small": [evaluator_timing(net, 32, g, reps=20) for g in (False, True)],

@@ -122,6 +122,8 @@ SIGNATURES: dict = {
     "shrimp_attn_mlp_pack_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
     "shrimp_pack_attn_mlp": (ctypes.c_int, [ctypes.POINTER(MlpWeights), _vp, _vp, _vp]),
     "shrimp_attn": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _vp]),
+    "shrimp_featurize": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "shrimp_attn_fused": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.POINTER(AttnProjArgs), _vp]),
     "shrimp_attn_fused_supported": (ctypes.c_int, [ctypes.c_int] * 4),
     "shrimp_attn_bias_table": (

@@ -367,6 +367,33 @@ int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void* seq, int6
                        void* stream);
 
 /* ------------------------------------------------------------------------
+ * Featurizer on the device (support.py:84-205 build_support, features.py:80-240
+ * build_features with the window scan and the opponent's last turn; the
+ * production featurizer is Rust, support.rs:52 / features.rs:19).
+ * Position b owns the placement records [rec_offsets[b], rec_offsets[b+1]),
+ * in placement order: cell rec_qr[i] = (q, r), owner rec_owner[i] (0 / 1),
+ * placement index rec_index[i] (NULL: the record's ordinal). player and
+ * phase (0 opening, 1 first stone, 2 second stone) may be NULL: they are then
+ * derived from the record count as for a decision state (player 0 opens,
+ * then two stones per turn), and in phase 2 the last record is the turn's
+ * first stone. Support radius R (1..24): legal = empty cells within R of a
+ * stone, halo = distance R + 1; hot / win-now cells from the single-colour
+ * length-6 window scan. Outputs, Npad rows per position (collate layout,
+ * batching.py:45-80):
+ *   feats (B, Npad, 15) f32, nbr (B, Npad, 6) int32 row-local (absent and
+ *   padding rows = Npad), mask (B, Npad) u8, coords (B, Npad, 2) int32;
+ *   counts (B, 4) int32 = nodes, legal, stones, halo;
+ *   status (B) int32: 0 ok, 2 the support does not fit the 64 x 64 cell
+ *   window of one workgroup (outputs zero), 3 more nodes than Npad (rows past
+ *   Npad dropped).
+ * feats == NULL computes counts and status only (to choose Npad).
+ * ---------------------------------------------------------------------- */
+int shrimp_featurize(const int32_t* rec_qr, const uint8_t* rec_owner, const int32_t* rec_index,
+                     const int64_t* rec_offsets, const uint8_t* player, const uint8_t* phase,
+                     int B, int radius, int Npad, float* feats, int32_t* nbr, uint8_t* mask,
+                     int32_t* coords, int32_t* counts, int32_t* status, void* stream);
+
+/* ------------------------------------------------------------------------
  * Trunk tail + value head (model.py:927-935, 990-1002):
  *   seq_f = LayerNorm(seq) (all S rows, fp32 stats), cell rows * mask -> out_seq (bf16)
  *   pooled = masked mean of the normalized cells (count clamped to 1)

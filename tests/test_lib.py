@@ -85,6 +85,16 @@ def test_bad_arguments_fail_with_message(lib):
     assert lib.shrimp_attn(ctypes.byref(aa), None) == -1
     assert b"head dim" in lib.shrimp_last_error()
     assert lib.shrimp_build_ray_index(1, 1, 1, 5000, 1, None) == -1
+    # featurizer: radius range and required outputs are checked before any launch
+    one = (ctypes.c_int64 * 2)(0, 0)
+    cnt = (ctypes.c_int32 * 4)()
+    stt = (ctypes.c_int32 * 1)()
+    assert lib.shrimp_featurize(None, None, None, one, None, None, 1, 0, 64, None, None, None,
+                                None, cnt, stt, None) == -1
+    assert b"radius" in lib.shrimp_last_error()
+    assert lib.shrimp_featurize(None, None, None, one, None, None, 1, 8, 64, cnt, None, None,
+                                None, cnt, stt, None) == -1
+    assert b"outputs" in lib.shrimp_last_error()
     # one-launch LN1 + q/k/v + attention: C = 128, H = 8, dpad = 16, S <= 320 only
     assert lib.shrimp_attn_fused_supported(128, 8, 264, 16) == 1
     assert lib.shrimp_attn_fused_supported(128, 8, 320, 16) == 1
