@@ -99,6 +99,32 @@ class MlpArgs(ctypes.Structure):
     ]
 
 
+class RayAttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp), ("k", _vp), ("v", _vp),
+        ("q_sb", _i64), ("q_sh", _i64), ("q_sn", _i64),
+        ("k_sb", _i64), ("k_sh", _i64), ("k_sn", _i64),
+        ("v_sb", _i64), ("v_sh", _i64), ("v_sn", _i64),
+        ("idx", _vp), ("idx_sb", _i64), ("idx_sn", _i64),
+        ("slot_bias", _vp), ("raylen", _vp), ("rl_sb", _i64), ("rl_sn", _i64),
+        ("seq_lens", _vp), ("out", _vp), ("o_sb", _i64), ("o_sh", _i64), ("o_sn", _i64),
+        ("B", _i32), ("H", _i32), ("N", _i32), ("D", _i32), ("blockers", _i32),
+    ]
+
+
+class RaytapArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", _vp), ("x_sb", _i64), ("x_sn", _i64),
+        ("gather_idx", _vp), ("g_sb", _i64), ("g_sn", _i64),
+        ("mask", _vp), ("packed_w", _vp), ("bias", _vp), ("ln_w", _vp), ("ln_b", _vp),
+        ("ray_idx", _vp), ("r_sb", _i64), ("r_sn", _i64),
+        ("reach", _vp), ("re_sb", _i64), ("re_sn", _i64),
+        ("alpha", _vp), ("eps", _f32), ("relu", _i32), ("corb", _i32),
+        ("out", _vp), ("o_sb", _i64), ("o_sn", _i64),
+        ("B", _i32), ("N", _i32), ("C", _i32), ("Cout", _i32),
+    ]
+
+
 # Exported symbols and their ctypes signatures; tests check every one of them
 # against the header and the built library.
 SIGNATURES: dict = {
@@ -153,6 +179,11 @@ SIGNATURES: dict = {
         ctypes.c_int, [_vp, _vp, _vp] + [ctypes.c_int] * 8 + [_vp, _vp]
     ),
     "shrimp_build_ray_index": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+    "shrimp_ray_attn": (ctypes.c_int, [ctypes.POINTER(RayAttnArgs), _vp]),
+    "shrimp_ray_attn_variant": (ctypes.c_int, [ctypes.c_int]),
+    "shrimp_raytap_wpack_bytes": (ctypes.c_size_t, [ctypes.c_int] * 2),
+    "shrimp_pack_raytap_weight": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+    "shrimp_conv_ln_raytap": (ctypes.c_int, [ctypes.POINTER(RaytapArgs), _vp]),
 }
 
 _LIB = None

@@ -450,6 +450,102 @@ int shrimp_build_pair_u8(const int32_t* coords, const uint8_t* mask, const uint8
 int shrimp_build_ray_index(const int32_t* coords, const uint8_t* mask, int B, int N,
                            int32_t* idx, void* stream);
 
+/* ------------------------------------------------------------------------
+ * hexfield_eq::ray_attn (hexfield_eq/_triton_ray.py:681-715; kernel :378-501):
+ * gathered ray attention over the 32-slot index above.
+ *   q, k, v, out: (B, H, N, D) fp16, D in {16, 32, 64, 128}, element strides
+ *     *_sb / *_sh / *_sn (multiples of 8, bases 16-byte aligned; the head
+ *     dimension is contiguous). The (B, N, H, D).transpose(1, 2) views the
+ *     reference passes satisfy this.
+ *   idx (B, N, 32) int32, strides idx_sb / idx_sn, slot stride 1; an entry
+ *     outside [0, N) is an absent key.
+ *   slot_bias (32, H) fp16 (the reference rounds its fp32 slot bias to fp16).
+ *   raylen (B, N, 12) u8, strides rl_sb / rl_sn; read only when blockers != 0
+ *     (may be NULL otherwise).
+ *   seq_lens (B,) int32: rows >= seq_lens[b] are written as zeros.
+ * Head h rides win axis h / 2 and side h % 2: slot s of row i is live when
+ * idx[i, s] is present and s == 0, or s = 1 + (h/2)*10 + dir*5 + (k-1) with
+ * k <= raylen[i, (h%2)*6 + (h/2)*2 + dir] (k <= 5 without blockers); heads
+ * h >= 6 see only slot 0.
+ *   out = sum_s softmax(q . k_s / sqrt(D) + slot_bias[s, h]) v_s (fp32 math,
+ *   fp16 store); a row without a live slot is zero.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t q_sb, q_sh, q_sn;
+  int64_t k_sb, k_sh, k_sn;
+  int64_t v_sb, v_sh, v_sn;
+  const int32_t* idx;
+  int64_t idx_sb, idx_sn;
+  const uint16_t* slot_bias;
+  const uint8_t* raylen;
+  int64_t rl_sb, rl_sn;
+  const int32_t* seq_lens;
+  uint16_t* out;
+  int64_t o_sb, o_sh, o_sn;
+  int B, H, N, D;
+  int blockers;
+} shrimp_ray_attn_args;
+
+int shrimp_ray_attn(const shrimp_ray_attn_args* a, void* stream);
+/* Kernel selection for tests and measurement: 0 = automatic (the head pair's
+ * K/V rows staged in LDS when 8 * N * D <= 64 KiB, else gathered from global
+ * memory), 1 = always global. Returns the previous setting. */
+int shrimp_ray_attn_variant(int v);
+
+/* ------------------------------------------------------------------------
+ * hexfield_eq::hex_conv_ln_raytap, K1 (hexfield_eq/_triton_conv.py:501-555;
+ * kernel :391-499): ray-tap conv + LayerNorm (+ReLU) + row mask.
+ *   x (B, N, C) fp16, strides x_sb / x_sn (multiples of 8, 16-byte aligned).
+ *   gather_idx (B, N, >= 1) int32, strides g_sb / g_sn: tap 0 (the centre row)
+ *     is the only tap read; an entry outside [0, N) reads a zero row.
+ *   ray_idx (B, N, 32) int32 and reach (B, N, 2, 6) u8 ([side][tap - 1]),
+ *     strides r_sb / r_sn and re_sb / re_sn.
+ *   alpha (5, C) fp16; corb the orbit width (C % corb == 0, corb % 8 == 0):
+ *     channel c is on side (c % corb) >= corb / 2.
+ *   tap t = 1..6, channel c: sum_{k=1..5} alpha[k-1, c] * x[ray_idx[i,
+ *     slot(t, k)], c] over the k <= reach[i, side(c), t-1] with a present
+ *     index (fp32 sum, stored as fp16), slot(t, k) = 1 + axis*10 + dir*5 +
+ *     (k-1) for the tap's (axis, dir).
+ *   conv = [x[centre] | tap 1 .. tap 6] . W + bias, W (7C, Cout) fp16 packed by
+ *     shrimp_pack_raytap_weight, fp32 accumulation; y = LayerNorm(conv) over
+ *     Cout with ln_w / ln_b (fp32, eps); ReLU if relu; rows with mask 0 -> 0;
+ *     out (B, N, Cout) fp16, strides o_sb / o_sn (multiples of 4).
+ *   mask (B, N) u8, row stride N.
+ * C and Cout in {64, 96, 128}; N <= 512.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const uint16_t* x;
+  int64_t x_sb, x_sn;
+  const int32_t* gather_idx;
+  int64_t g_sb, g_sn;
+  const uint8_t* mask;
+  const void* packed_w;
+  const float* bias;
+  const float* ln_w;
+  const float* ln_b;
+  const int32_t* ray_idx;
+  int64_t r_sb, r_sn;
+  const uint8_t* reach;
+  int64_t re_sb, re_sn;
+  const uint16_t* alpha;
+  float eps;
+  int relu;
+  int corb;
+  uint16_t* out;
+  int64_t o_sb, o_sn;
+  int B, N, C, Cout;
+} shrimp_raytap_args;
+
+/* Bytes of the packed K1 weight for (C, Cout); 0 if unsupported. */
+size_t shrimp_raytap_wpack_bytes(int C, int Cout);
+/* w (7, C, Cout) fp16 row-major (= the reference's weight.reshape(7C, Cout))
+ * -> packed fp16 MFMA fragments. */
+int shrimp_pack_raytap_weight(const uint16_t* w, int C, int Cout, void* packed, void* stream);
+int shrimp_conv_ln_raytap(const shrimp_raytap_args* a, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

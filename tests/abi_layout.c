@@ -66,5 +66,27 @@ int main(void) {
   F(shrimp_mlp_args, s_sr); F(shrimp_mlp_args, mask); F(shrimp_mlp_args, packed);
   F(shrimp_mlp_args, eps); F(shrimp_mlp_args, rows); F(shrimp_mlp_args, C);
   F(shrimp_mlp_args, hidden);
+  Z(shrimp_ray_attn_args);
+  F(shrimp_ray_attn_args, q); F(shrimp_ray_attn_args, k); F(shrimp_ray_attn_args, v);
+  F(shrimp_ray_attn_args, q_sb); F(shrimp_ray_attn_args, q_sh); F(shrimp_ray_attn_args, q_sn);
+  F(shrimp_ray_attn_args, k_sb); F(shrimp_ray_attn_args, k_sh); F(shrimp_ray_attn_args, k_sn);
+  F(shrimp_ray_attn_args, v_sb); F(shrimp_ray_attn_args, v_sh); F(shrimp_ray_attn_args, v_sn);
+  F(shrimp_ray_attn_args, idx); F(shrimp_ray_attn_args, idx_sb); F(shrimp_ray_attn_args, idx_sn);
+  F(shrimp_ray_attn_args, slot_bias); F(shrimp_ray_attn_args, raylen);
+  F(shrimp_ray_attn_args, rl_sb); F(shrimp_ray_attn_args, rl_sn); F(shrimp_ray_attn_args, seq_lens);
+  F(shrimp_ray_attn_args, out); F(shrimp_ray_attn_args, o_sb); F(shrimp_ray_attn_args, o_sh);
+  F(shrimp_ray_attn_args, o_sn); F(shrimp_ray_attn_args, B); F(shrimp_ray_attn_args, H);
+  F(shrimp_ray_attn_args, N); F(shrimp_ray_attn_args, D); F(shrimp_ray_attn_args, blockers);
+  Z(shrimp_raytap_args);
+  F(shrimp_raytap_args, x); F(shrimp_raytap_args, x_sb); F(shrimp_raytap_args, x_sn);
+  F(shrimp_raytap_args, gather_idx); F(shrimp_raytap_args, g_sb); F(shrimp_raytap_args, g_sn);
+  F(shrimp_raytap_args, mask); F(shrimp_raytap_args, packed_w); F(shrimp_raytap_args, bias);
+  F(shrimp_raytap_args, ln_w); F(shrimp_raytap_args, ln_b); F(shrimp_raytap_args, ray_idx);
+  F(shrimp_raytap_args, r_sb); F(shrimp_raytap_args, r_sn); F(shrimp_raytap_args, reach);
+  F(shrimp_raytap_args, re_sb); F(shrimp_raytap_args, re_sn); F(shrimp_raytap_args, alpha);
+  F(shrimp_raytap_args, eps); F(shrimp_raytap_args, relu); F(shrimp_raytap_args, corb);
+  F(shrimp_raytap_args, out); F(shrimp_raytap_args, o_sb); F(shrimp_raytap_args, o_sn);
+  F(shrimp_raytap_args, B); F(shrimp_raytap_args, N); F(shrimp_raytap_args, C);
+  F(shrimp_raytap_args, Cout);
   return 0;
 }

@@ -56,6 +56,8 @@ def test_struct_layouts_match_c(tmp_path):
         "shrimp_qkv_args": _lib.QkvArgs,
         "shrimp_mlp_weights": _lib.MlpWeights,
         "shrimp_mlp_args": _lib.MlpArgs,
+        "shrimp_ray_attn_args": _lib.RayAttnArgs,
+        "shrimp_raytap_args": _lib.RaytapArgs,
     }
     seen = 0
     for line in filter(None, lines):
@@ -110,6 +112,37 @@ def test_bad_arguments_fail_with_message(lib):
     pj.x_sr = 100
     assert lib.shrimp_attn_fused(ctypes.byref(fa), ctypes.byref(pj), None) == -1
     assert b"x strides" in lib.shrimp_last_error()
+    # hexfield ray attention: head dim, strides, blockers without raylen
+    ra = _lib.RayAttnArgs(B=1, H=6, N=64, D=24, q=16, k=16, v=16, out=16, idx=16, slot_bias=16,
+                          seq_lens=16, idx_sb=64 * 32, idx_sn=32, blockers=0)
+    assert lib.shrimp_ray_attn(ctypes.byref(ra), None) == -1
+    assert b"head dim" in lib.shrimp_last_error()
+    ra.D = 16
+    ra.q_sn = 12
+    assert lib.shrimp_ray_attn(ctypes.byref(ra), None) == -1
+    assert b"multiples of 8" in lib.shrimp_last_error()
+    ra.q_sn = 96
+    ra.blockers = 1
+    assert lib.shrimp_ray_attn(ctypes.byref(ra), None) == -1
+    assert b"raylen" in lib.shrimp_last_error()
+    ra.B = 0
+    assert lib.shrimp_ray_attn(ctypes.byref(ra), None) == 0  # nothing to do
+    prev = lib.shrimp_ray_attn_variant(1)
+    assert lib.shrimp_ray_attn_variant(-1) == 1
+    lib.shrimp_ray_attn_variant(prev)
+    # hexfield K1: channel sets, N bound, orbit width
+    assert lib.shrimp_raytap_wpack_bytes(96, 96) == 7 * 96 * 96 * 2
+    assert lib.shrimp_raytap_wpack_bytes(100, 128) == 0
+    assert lib.shrimp_pack_raytap_weight(16, 80, 128, 16, None) == -1
+    rt = _lib.RaytapArgs(B=1, N=600, C=128, Cout=128, corb=8)
+    assert lib.shrimp_conv_ln_raytap(ctypes.byref(rt), None) == -1
+    assert b"N=600" in lib.shrimp_last_error()
+    rt = _lib.RaytapArgs(B=1, N=64, C=128, Cout=128, corb=12, x=16, gather_idx=16, mask=16,
+                         packed_w=16, bias=16, ln_w=16, ln_b=16, ray_idx=16, reach=16, alpha=16,
+                         out=16, x_sb=64 * 128, x_sn=128, o_sb=64 * 128, o_sn=128, r_sn=32,
+                         re_sn=12, g_sn=7)
+    assert lib.shrimp_conv_ln_raytap(ctypes.byref(rt), None) == -1
+    assert b"corb=12" in lib.shrimp_last_error()
 
 
 def test_missing_library_raises(tmp_path):
