@@ -269,6 +269,137 @@ def featurize_timing(rows, reps: int = 20) -> dict:
     }
 
 
+def hexfield_timing(reps: int = 50, cpu_sample: int = 16) -> dict:
+    """The hexfield ray kernels at the config-3 shape (B = 1024 cfg3 cell sets,
+    Npad = 256, 32-slot ray index from shrimp_build_ray_index, random raylen
+    0..5): ray attention with 6 heads of 16 (C = 96) and K1 (ray-tap conv +
+    LayerNorm + ReLU) at C = Cout = 128 (orbit width 128) and C = Cout = 96
+    (orbit width 8). HIP events on the launch stream around back-to-back
+    launches; algorithmic bytes count each row of q/k/v/x/idx once (live rows
+    only where the kernel skips the rest) and every output row. The CPU
+    column is the fp32 oracle on ``cpu_sample`` positions, one thread."""
+
+    import numpy as np
+    import torch
+
+    from hexfield_eq import build_ray_gather_index, build_tap_reach, ops as hops
+    from oracle import hexfield as ohf
+    from shrimp import synthetic
+
+    dev = torch.device("cuda")
+    stream = torch.cuda.current_stream(dev)
+    bt = synthetic.position_batch("cfg3", 1024)
+    mask = bt["mask"].to(dev)
+    coords = bt["coords"].to(dev)
+    b, n = mask.shape
+    gen = torch.Generator().manual_seed(5)
+    idx = build_ray_gather_index(coords, mask)
+    raylen = torch.randint(0, 6, (b, n, 12), generator=gen, dtype=torch.uint8).to(dev)
+    cell = torch.arange(1, n + 1, device=dev, dtype=torch.int32)
+    seq = (cell * mask.to(torch.int32)).amax(dim=1).to(torch.int32)
+    live_rows = int(seq.sum().item())
+    out = {}
+
+    # ray attention
+    h, d = 6, 16
+    q, k, v = [torch.randn(b, n, h, d, generator=gen).half().to(dev).transpose(1, 2)
+               for _ in range(3)]
+    sb = (0.5 * torch.randn(32, h, generator=gen)).half().to(dev)
+    o = torch.empty((b, h, n, d), dtype=torch.float16, device=dev)
+    run = lambda: hops.launch_ray_attn(q, k, v, idx, sb, raylen, seq, True, o)
+    run()
+    ms = _events_time(run, reps, stream)
+    prev = hops.ray_attn_variant(1)
+    run()
+    ms_glob = _events_time(run, reps, stream)
+    hops.ray_attn_variant(prev)
+    # live (row, head, slot) triples, for the flop count
+    ii = idx.long()
+    present = (ii >= 0) & (ii < n)
+    rows_live = torch.arange(n, device=dev)[None, :] < seq[:, None].long()
+    slots = torch.arange(32, device=dev)
+    kk = (slots - 1) % 5 + 1
+    live_pairs = 0
+    for hh in range(h):
+        ax, side = hh // 2, hh % 2
+        geo = (slots >= 1 + 10 * ax) & (slots <= 10 + 10 * ax)
+        dirn = ((slots - 1) % 10) // 5
+        rl = raylen.long()[:, :, side * 6 + ax * 2 + dirn.clamp(0, 1)]
+        ok = present & ((slots == 0) | (geo & (kk <= rl)))
+        live_pairs += int((ok & rows_live[:, :, None]).sum().item())
+    flops = live_pairs * 4 * d
+    nbytes = 3 * live_rows * h * d * 2 + b * n * h * d * 2 + live_rows * (32 * 4 + 12) + b * 4
+    sel = slice(0, cpu_sample)
+    qc, kc, vc = q[sel].cpu().float(), k[sel].cpu().float(), v[sel].cpu().float()
+    t0 = time.perf_counter()
+    ohf.ray_attn(qc, kc, vc, idx[sel].cpu(), sb.cpu(), raylen[sel].cpu(), seq[sel].cpu(), True,
+                 dtype=torch.float32)
+    cpu_s = time.perf_counter() - t0
+    out["ray_attn"] = {
+        "kernel": "ray_attn_kernel<16, staged> (K/V of a head pair in LDS)",
+        "workload": f"B={b} Npad={n} H={h} D={d} blockers, cfg3 cell sets",
+        "launch_ms": round(ms, 5),
+        "launch_ms_global_gather": round(ms_glob, 5),
+        "algorithmic_bytes": nbytes,
+        "bound": "hbm",
+        "achieved_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "peak_gbs": PEAK_HBM_GBS,
+        "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "live_slot_pairs": live_pairs,
+        "flops": flops,
+        "positions_per_s": round(b / (ms * 1e-3), 1),
+        "cpu_oracle_positions_per_s": round(cpu_sample / cpu_s, 1),
+        "cpu_sample": f"{cpu_sample} positions, fp32 gathered oracle, 1 process",
+    }
+
+    # K1 ray-tap conv + LN
+    reach = build_tap_reach(raylen)
+    nbr = bt["nbr"].to(dev).to(torch.int32)
+    gidx = torch.cat([torch.arange(n, device=dev, dtype=torch.int32).view(1, n, 1).expand(b, n, 1),
+                      nbr], dim=2).contiguous()
+    m8 = mask.to(torch.uint8).contiguous()
+    re12 = reach.reshape(b, n, 12).contiguous()
+    for c, corb in ((128, 128), (96, 8)):
+        x = torch.randn(b, n, c, generator=gen).half().to(dev)
+        w = (torch.randn(7, c, c, generator=gen) / np.sqrt(7 * c)).half().to(dev)
+        bias = (0.02 * torch.randn(c, generator=gen)).to(dev)
+        lnw = (torch.rand(c, generator=gen) + 0.5).to(dev)
+        lnb = (0.1 * torch.randn(c, generator=gen)).to(dev)
+        alpha = torch.stack([0.8 ** kk_ * (1 + 0.1 * torch.randn(c, generator=gen))
+                             for kk_ in range(5)]).half().to(dev)
+        packed = hops.pack_raytap_weight(w)
+        y = torch.empty((b, n, c), dtype=torch.float16, device=dev)
+        run = lambda: hops.launch_conv_ln_raytap(x, gidx, m8, packed, bias, lnw, lnb, idx, re12,
+                                                 alpha, 1e-5, True, corb, y)
+        run()
+        ms = _events_time(run, reps, stream)
+        kflops = b * n * 7 * c * c * 2
+        kbytes = b * n * (c * 2 + 32 * 4 + 12 + 7 * 4 + 1 + c * 2) + 7 * c * c * 2
+        tfl = kflops / (ms * 1e-3) / 1e12
+        xs, ws = x[sel].cpu().float(), w.cpu().float()
+        t0 = time.perf_counter()
+        ohf.conv_ln_raytap(xs, gidx[sel].cpu(), mask[sel].cpu(), ws, bias.cpu(), lnw.cpu(),
+                           lnb.cpu(), idx[sel].cpu(), reach[sel].cpu(), alpha.cpu().float(), 1e-5,
+                           True, corb, dtype=torch.float32)
+        cpu_s = time.perf_counter() - t0
+        out[f"conv_ln_raytap_c{c}"] = {
+            "kernel": f"conv_ln_raytap_kernel<{c}, {c}> (orbit width {corb})",
+            "workload": f"B={b} Npad={n} C=Cout={c}, 7 taps from 31 ray rows, LN + ReLU",
+            "launch_ms": round(ms, 5),
+            "bound": "mfma",
+            "achieved_tflops": round(tfl, 2),
+            "peak_tflops": PEAK_BF16_TFLOPS,
+            "frac": round(tfl / PEAK_BF16_TFLOPS, 4),
+            "flops": kflops,
+            "algorithmic_bytes": kbytes,
+            "hbm_gbs_algorithmic": round(kbytes / (ms * 1e-3) / 1e9, 1),
+            "positions_per_s": round(b / (ms * 1e-3), 1),
+            "cpu_oracle_positions_per_s": round(cpu_sample / cpu_s, 1),
+            "cpu_sample": f"{cpu_sample} positions, fp32 oracle, 1 process",
+        }
+    return out
+
+
 def cpu_baseline(batch, seconds: float):
     """Oracle fp32 eager forward (the reference CPU path, restated) on a
     bounded sample of the same workload; positions/s on the host cores."""
@@ -419,6 +550,7 @@ def main() -> int:
         "block0_row_kernels": kt["linears"],
         "forward_tflops_padded": round(1.425e9 * B / (ms * 1e-3) / 1e12, 2),
         "featurize": featurize_timing(batch["rows"]),
+        "hexfield": hexfield_timing(),
         "evaluator": evaluator_timing(net),
         "evaluator_graphs": evaluator_timing(net, graphs=True),
         "evaluator_small": [evaluator_timing(net, 32, g, reps=20) for g in (False, True)],

@@ -330,93 +330,125 @@ __global__ __launch_bounds__(64 * RT_MAX_WAVES) void conv_ln_raytap_kernel(
     const int j = rv[mb] ? a.gather_idx[(int64_t)b * a.g_sb + (int64_t)rn[mb] * a.g_sn] : N;
     crow[mb] = (unsigned)j < (unsigned)N ? (uint32_t)j : (uint32_t)N;
   }
-  // Side of the lane's two 4-channel halves in chunk kc, (c % corb) >= corb / 2,
-  // as the shift that selects the opp row from a packed (own | opp << 16) pair.
-  int hshift[KC][2];
+  // Side of the lane's two 4-channel halves of chunk kc, (c % corb) >= corb / 2:
+  // bit 2 kc + h set for the opp side.
+  uint32_t sidebits = 0;
 #pragma unroll
   for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int c = kc * 32 + lg * 8 + h * 4;
-      hshift[kc][h] = (c % a.corb) >= (a.corb >> 1) ? 16 : 0;
+      if ((c % a.corb) >= (a.corb >> 1)) sidebits |= 1u << (2 * kc + h);
     }
+
+  // Ray rows and reach of one direction tap for row wave * 64 + lane, loaded
+  // one tap ahead so the global latency hides behind the previous tap.
+  const int trow = wave * 64 + lane;
+  int pj[RAY_STEPS];
+  uint32_t preach = 0;
+  auto tap_fetch = [&](int t) {
+#pragma unroll
+    for (int k = 0; k < RAY_STEPS; ++k) pj[k] = N;
+    preach = 0;
+    if (trow < N) {
+      const int32_t* ir = rib + (int64_t)trow * a.r_sn + RT_SLOT_BASE[t];
+#pragma unroll
+      for (int k = 0; k < RAY_STEPS; ++k) pj[k] = ir[k];
+      const uint8_t* re = reb + (int64_t)trow * a.re_sn;
+      preach = (uint32_t)re[t] | ((uint32_t)re[6 + t] << 8);
+    }
+  };
+  tap_fetch(0);
 
   __syncthreads();
 
-  // Tap 0.
+  // Tap 0: two weight buffers (nothing else is live here); the last chunk
+  // requests the first step of tap 1.
+  u32x4 w[NB];
   {
-    u32x4 w[NB];
+    u32x4 wa[NB], wb[NB];
+    wload(0, wa);
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
-      wload(kc, w);
+      u32x4 (&wc)[NB] = (kc & 1) ? wb : wa;
+      u32x4 (&wn)[NB] = (kc & 1) ? wa : wb;
+      wload(kc + 1, wn);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         const u32x4 xf = *reinterpret_cast<const u32x4*>(xs + crow[mb] * RS + (kc * 32 + lg * 8) * 2);
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc[nb][mb] = mfma_f16(w[nb], xf, acc[nb][mb]);
+        for (int nb = 0; nb < NB; ++nb) acc[nb][mb] = mfma_f16(wc[nb], xf, acc[nb][mb]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    u32x4 (&wl)[NB] = (KC & 1) ? wb : wa;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) w[nb] = wl[nb];
   }
 
-  // Taps 1..6. Per tap, lane l of each wave first writes, for row wave * 64 + l,
-  // the visible row of every step and side into the wave's slice of `vt`
-  // (5 dwords, own | opp << 16, N = the zero row; 8 dwords per row), then every
-  // chunk of the tap reads it back for its rows.
+  // Taps 1..6. Per tap, lane l of each wave writes, for row wave * 64 + l, the
+  // visible row of every step and side into the wave's slice of `vt` (5 dwords,
+  // own | opp << 16, N = the zero row; 8 dwords per row); every chunk of the tap
+  // reads it back for its rows. The slice belongs to one wave and a wave's LDS
+  // accesses complete in issue order, so no workgroup barrier is needed.
   uint32_t* vt = reinterpret_cast<uint32_t*>(al + RAY_STEPS * CIN * 2) + wave * 64 * 8;
   for (int t = 0; t < 6; ++t) {
     {
-      const int row = wave * 64 + lane;
+      const int r0 = (int)(preach & 0xFF), r1 = (int)(preach >> 8);
       uint32_t vr[RAY_STEPS];
-      int r0 = 0, r1 = 0;
-      int js[RAY_STEPS];
-#pragma unroll
-      for (int k = 0; k < RAY_STEPS; ++k) js[k] = N;
-      if (row < N) {
-        const int32_t* ir = rib + (int64_t)row * a.r_sn + RT_SLOT_BASE[t];
-#pragma unroll
-        for (int k = 0; k < RAY_STEPS; ++k) js[k] = ir[k];
-        const uint8_t* re = reb + (int64_t)row * a.re_sn;
-        r0 = re[t];
-        r1 = re[6 + t];
-      }
 #pragma unroll
       for (int k = 0; k < RAY_STEPS; ++k) {
-        const bool pres = (unsigned)js[k] < (unsigned)N;
-        const uint32_t own = pres && k + 1 <= r0 ? (uint32_t)js[k] : (uint32_t)N;
-        const uint32_t opp = pres && k + 1 <= r1 ? (uint32_t)js[k] : (uint32_t)N;
+        const bool pres = (unsigned)pj[k] < (unsigned)N;
+        const uint32_t own = pres && k + 1 <= r0 ? (uint32_t)pj[k] : (uint32_t)N;
+        const uint32_t opp = pres && k + 1 <= r1 ? (uint32_t)pj[k] : (uint32_t)N;
         vr[k] = own | (opp << 16);
       }
       *reinterpret_cast<u32x4*>(vt + lane * 8) = u32x4{vr[0], vr[1], vr[2], vr[3]};
       vt[lane * 8 + 4] = vr[4];
     }
-    __syncthreads();
+    if (t + 1 < 6) tap_fetch(t + 1);
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+    // Table entries of the next row block, read one block ahead (they do not
+    // depend on the chunk, so the block after the last is block 0 again).
+    auto vt_read = [&](int mb, uint32_t (&v)[RAY_STEPS]) {
+      const uint32_t* vp = vt + (mb * 16 + lr) * 8;
+      const u32x4 v4 = *reinterpret_cast<const u32x4*>(vp);
+      v[0] = v4[0];
+      v[1] = v4[1];
+      v[2] = v4[2];
+      v[3] = v4[3];
+      v[4] = vp[4];
+    };
+    uint32_t vnext[RAY_STEPS];
+    vt_read(0, vnext);
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
-      u32x4 w[NB];
-      wload((1 + t) * KC + kc, w);
       // alpha of the lane's 8 channels, steps 1..5
       u32x4 av[RAY_STEPS];
 #pragma unroll
       for (int k = 0; k < RAY_STEPS; ++k)
         av[k] = *reinterpret_cast<const u32x4*>(al + (k * CIN + kc * 32 + lg * 8) * 2);
-      const int sh0 = hshift[kc][0], sh1 = hshift[kc][1];
+      const int sh0 = ((sidebits >> (2 * kc)) & 1u) * 16, sh1 = ((sidebits >> (2 * kc + 1)) & 1u) * 16;
       const uint32_t cb = (uint32_t)(kc * 32 + lg * 8) * 2;
+      const int next = (1 + t) * KC + kc + 1;  // weight step after this one
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const uint32_t* vp = vt + (mb * 16 + lr) * 8;
-        const u32x4 v4 = *reinterpret_cast<const u32x4*>(vp);
-        const uint32_t vrow[RAY_STEPS] = {v4[0], v4[1], v4[2], v4[3], vp[4]};
+        u32x2 xr[RAY_STEPS][2];
+#pragma unroll
+        for (int k = 0; k < RAY_STEPS; ++k) {
+          const uint32_t j0 = (vnext[k] >> sh0) & 0xFFFFu;
+          const uint32_t j1 = (vnext[k] >> sh1) & 0xFFFFu;
+          xr[k][0] = *reinterpret_cast<const u32x2*>(xs + j0 * RS + cb);
+          xr[k][1] = *reinterpret_cast<const u32x2*>(xs + j1 * RS + cb + 8);
+        }
+        vt_read(mb + 1 < MB ? mb + 1 : 0, vnext);
         float sum[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) sum[e] = 0.f;
 #pragma unroll
         for (int k = 0; k < RAY_STEPS; ++k) {
-          const uint32_t j0 = (vrow[k] >> sh0) & 0xFFFFu;
-          const uint32_t j1 = (vrow[k] >> sh1) & 0xFFFFu;
-          const u32x2 x0 = *reinterpret_cast<const u32x2*>(xs + j0 * RS + cb);
-          const u32x2 x1 = *reinterpret_cast<const u32x2*>(xs + j1 * RS + cb + 8);
-          const unsigned xw[4] = {x0[0], x0[1], x1[0], x1[1]};
+          const unsigned xw[4] = {xr[k][0][0], xr[k][0][1], xr[k][1][0], xr[k][1][1]};
 #pragma unroll
           for (int w2 = 0; w2 < 4; ++w2) {
             const unsigned au = av[k][w2];
@@ -430,6 +462,9 @@ __global__ __launch_bounds__(64 * RT_MAX_WAVES) void conv_ln_raytap_kernel(
         for (int w2 = 0; w2 < 4; ++w2) bf[w2] = pack_f16x2(sum[2 * w2], sum[2 * w2 + 1]);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) acc[nb][mb] = mfma_f16(w[nb], bf, acc[nb][mb]);
+        // The last block's products hold the step's weights; the next step's
+        // fragments load into the same registers right behind them.
+        if (mb == MB - 1 && next < 7 * KC) wload(next, w);
         // Keep the next row block's loads behind this block's products (hoisting all
         // four blocks' loads overflows the register budget).
         __builtin_amdgcn_sched_barrier(0);
