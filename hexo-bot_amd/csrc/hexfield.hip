@@ -242,6 +242,14 @@ constexpr int RT_MAX_WAVES = RT_MAX_N / (16 * RT_MB);
 __constant__ int RT_SLOT_BASE[6] = {1, 11, 26, 6, 16, 21};
 
 __host__ __device__ constexpr int rt_row_stride(int cin) { return cin * 2 + 16; }
+__host__ __device__ constexpr int rt_out_stride(int cout) { return cout * 2 + 16; }
+// Bytes of the row region: the x rows (N + 1 of them) during the taps, the
+// output rows (64 per wave) in the epilogue.
+__host__ __device__ inline uint32_t rt_rows_bytes(int N, int cin, int cout, int waves) {
+  const uint32_t xr = (uint32_t)(N + 1) * rt_row_stride(cin);
+  const uint32_t orr = (uint32_t)waves * 64 * rt_out_stride(cout);
+  return xr > orr ? xr : orr;
+}
 
 template <int CIN, int COUT>
 constexpr uint32_t rt_wpack_bytes() {
@@ -281,8 +289,8 @@ __global__ __launch_bounds__(64 * RT_MAX_WAVES) void conv_ln_raytap_kernel(
   const int b = (int)blockIdx.x;
   const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
-  unsigned char* xs = lds;                                  // (N + 1) rows of RS bytes
-  unsigned char* al = lds + (size_t)(N + 1) * RS;           // alpha (5, CIN) fp16
+  unsigned char* xs = lds;  // (N + 1) rows of RS bytes, later the output rows
+  unsigned char* al = lds + rt_rows_bytes(N, CIN, COUT, (int)(blockDim.x >> 6));  // alpha (5, CIN) fp16
 
   // Stage the position's rows, the zero row N and alpha.
   {
@@ -497,6 +505,12 @@ __global__ __launch_bounds__(64 * RT_MAX_WAVES) void conv_ln_raytap_kernel(
     rstd[mb] = rsqrtf(sum_groups_swap(q) * (1.0f / COUT) + a.eps);
     live[mb] = rv[mb] && mk[rn[mb]] != 0;
   }
+  // The output rows go through LDS (each wave's 64 rows in its own slice over
+  // the x rows, which every wave has finished reading) and leave as whole
+  // 16-byte row pieces: 8-byte stores per lane would write 32-byte segments.
+  __syncthreads();
+  constexpr int OS = rt_out_stride(COUT);
+  unsigned char* ob = xs + (size_t)wave * 64 * OS;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int c0 = nb * 16 + lg * 4;
@@ -511,9 +525,22 @@ __global__ __launch_bounds__(64 * RT_MAX_WAVES) void conv_ln_raytap_kernel(
         if (a.relu) v = fmaxf(v, 0.f);
         y[j] = live[mb] ? v : 0.f;
       }
-      if (rv[mb])
-        *reinterpret_cast<u32x2*>(a.out + (int64_t)b * a.o_sb + (int64_t)rn[mb] * a.o_sn + c0) =
-            u32x2{pack_f16x2(y[0], y[1]), pack_f16x2(y[2], y[3])};
+      *reinterpret_cast<u32x2*>(ob + (mb * 16 + lr) * OS + c0 * 2) =
+          u32x2{pack_f16x2(y[0], y[1]), pack_f16x2(y[2], y[3])};
+    }
+  }
+  // The slice belongs to this wave and its LDS accesses complete in issue order.
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+  constexpr int CPR = COUT / 8;  // 16-byte pieces per output row
+  const int ch = lane & 15;
+#pragma unroll
+  for (int it = 0; it < 16; ++it) {
+    const int r = it * 4 + (lane >> 4);
+    const int row = wave * 64 + r;
+    if (ch < CPR && row < N) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ob + r * OS + ch * 16);
+      *reinterpret_cast<u32x4*>(a.out + (int64_t)b * a.o_sb + (int64_t)row * a.o_sn + ch * 8) = v;
     }
   }
 }
@@ -616,17 +643,16 @@ extern "C" int shrimp_conv_ln_raytap(const shrimp_raytap_args* a, void* stream) 
                  "conv_ln_raytap: corb=%d must divide C=%d and be a multiple of 8", a->corb, a->C);
   SHRIMP_REQUIRE(aligned16(a->x) && a->x_sb % 8 == 0 && a->x_sn % 8 == 0 && a->x_sn >= a->C,
                  "conv_ln_raytap: x must be 16-byte aligned with strides multiples of 8");
-  SHRIMP_REQUIRE((reinterpret_cast<uintptr_t>(a->out) & 7) == 0 && a->o_sb % 4 == 0 &&
-                     a->o_sn % 4 == 0 && a->o_sn >= a->Cout,
-                 "conv_ln_raytap: out must be 8-byte aligned with strides multiples of 4");
+  SHRIMP_REQUIRE(aligned16(a->out) && a->o_sb % 8 == 0 && a->o_sn % 8 == 0 && a->o_sn >= a->Cout,
+                 "conv_ln_raytap: out must be 16-byte aligned with strides multiples of 8");
   SHRIMP_REQUIRE(aligned16(a->alpha) && aligned16(a->bias) && aligned16(a->ln_w) &&
                      aligned16(a->ln_b) && aligned16(a->packed_w),
                  "conv_ln_raytap: alpha / bias / ln params / weights must be 16-byte aligned");
   SHRIMP_REQUIRE(a->r_sn >= RAY_SLOT_COUNT && a->re_sn >= 12 && a->g_sn >= 1,
                  "conv_ln_raytap: ray_idx rows need 32 slots, reach rows 12 bytes");
   const int waves = (a->N + 16 * RT_MB - 1) / (16 * RT_MB);
-  const size_t lds = (size_t)(a->N + 1) * rt_row_stride(a->C) + (size_t)RAY_STEPS * a->C * 2 +
-                     (size_t)waves * 64 * 8 * 4;
+  const size_t lds = (size_t)rt_rows_bytes(a->N, a->C, a->Cout, waves) +
+                     (size_t)RAY_STEPS * a->C * 2 + (size_t)waves * 64 * 8 * 4;
   SHRIMP_REQUIRE(lds <= (size_t)max_lds_per_block(), "conv_ln_raytap: needs %zu bytes of LDS", lds);
   hipStream_t s = as_stream(stream);
   switch (a->C) {

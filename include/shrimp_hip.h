@@ -512,7 +512,7 @@ int shrimp_ray_attn_variant(int v);
  *   conv = [x[centre] | tap 1 .. tap 6] . W + bias, W (7C, Cout) fp16 packed by
  *     shrimp_pack_raytap_weight, fp32 accumulation; y = LayerNorm(conv) over
  *     Cout with ln_w / ln_b (fp32, eps); ReLU if relu; rows with mask 0 -> 0;
- *     out (B, N, Cout) fp16, strides o_sb / o_sn (multiples of 4).
+ *     out (B, N, Cout) fp16, 16-byte aligned, strides o_sb / o_sn (multiples of 8).
  *   mask (B, N) u8, row stride N.
  * C and Cout in {64, 96, 128}; N <= 512.
  * ---------------------------------------------------------------------- */
