@@ -34,6 +34,7 @@ constexpr int RAY_SLOT_COUNT = 32;
 constexpr int RAY_STEPS = 5;
 constexpr int RA_THREADS = 256;
 constexpr uint32_t RA_STAGE_MAX_LDS = 64 * 1024;
+constexpr uint32_t RA_BIAS_LDS = 96;  // the head pair's 22 fp32 slot biases, padded
 constexpr float LOG2E_F = 1.4426950408889634f;
 
 int g_ray_variant = 0;
@@ -99,13 +100,16 @@ SHRIMP_DEV void fma_row16(float (&acc)[16], float p, const Row16& v) {
 }
 
 // Workgroup: (position b, head pair p), 256 threads, D / 16 lanes per query row
-// (each owning 16 of its D channels). LDS (STAGE): [K | V][head of pair][row][D].
+// (each owning 16 of its D channels). LDS: the pair's 22 slot biases (fp32),
+// then (STAGE) [K | V][head of pair][row][D] fp16. Head rows are addressed
+// from per-head base pointers with 32-bit byte offsets (the host checks that
+// a position's rows of one head span less than 2 GiB).
 template <int D, bool STAGE>
 __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_attn_args a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   constexpr int LPR = D / 16;
   constexpr int RPP = RA_THREADS / LPR;
-  const int npairs = (a.H + 1) >> 1;
+    const int npairs = (a.H + 1) >> 1;
   int b, p;
   if ((a.B & 7) == 0) {
     // Consecutive workgroups go to the eight XCDs in turn: keep the head pairs
@@ -123,45 +127,72 @@ __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_a
   const int live_rows = min(max(a.seq_lens[b], 0), N);
   const int nst = STAGE ? live_rows : 0;
   const int part = (int)threadIdx.x % LPR;
+  const bool axis = p < 3;
 
-  const unsigned char* gsrc[2] = {reinterpret_cast<const unsigned char*>(a.k),
-                                  reinterpret_cast<const unsigned char*>(a.v)};
-  const int64_t gsb[2] = {a.k_sb, a.v_sb}, gsh[2] = {a.k_sh, a.v_sh}, gsn[2] = {a.k_sn, a.v_sn};
+  // Per-head base pointers (the second head of an odd pair aliases the first
+  // and is never used) and byte row strides.
+  const unsigned char* qb[2];
+  const unsigned char* kb[2];
+  const unsigned char* vb[2];
+  unsigned char* ob[2];
+#pragma unroll
+  for (int hl = 0; hl < 2; ++hl) {
+    const int64_t hh = 2 * p + min(hl, nh - 1);
+    qb[hl] = reinterpret_cast<const unsigned char*>(a.q + (int64_t)b * a.q_sb + hh * a.q_sh);
+    kb[hl] = reinterpret_cast<const unsigned char*>(a.k + (int64_t)b * a.k_sb + hh * a.k_sh);
+    vb[hl] = reinterpret_cast<const unsigned char*>(a.v + (int64_t)b * a.v_sb + hh * a.v_sh);
+    ob[hl] = reinterpret_cast<unsigned char*>(a.out + (int64_t)b * a.o_sb + hh * a.o_sh);
+  }
+  const uint32_t qsn = (uint32_t)a.q_sn * 2, ksn = (uint32_t)a.k_sn * 2;
+  const uint32_t vsn = (uint32_t)a.v_sn * 2, osn = (uint32_t)a.o_sn * 2;
 
+  // slot biases of the pair: [hl][i], i = 0 self, 1 + t the axis slots
+  float* sbias = reinterpret_cast<float*>(lds);
+  if (threadIdx.x < 22) {
+    const int hl = (int)threadIdx.x / 11, i = (int)threadIdx.x % 11;
+    const int slot = i == 0 ? 0 : 1 + 10 * (axis ? p : 0) + (i - 1);
+    const int hh = 2 * p + min(hl, nh - 1);
+    sbias[threadIdx.x] = (float)__builtin_bit_cast(_Float16, a.slot_bias[slot * a.H + hh]);
+  }
+  unsigned char* rows = lds + RA_BIAS_LDS;
   if constexpr (STAGE) {
     constexpr int CPR = D / 8;  // 16-byte chunks per row and head
-    const int per_row = nh * CPR;
-    const int total = 2 * nst * per_row;
-    for (int c = (int)threadIdx.x; c < total; c += RA_THREADS) {
-      const int tsr = c / (nst * per_row);
-      const int rem = c - tsr * nst * per_row;
-      const int j = rem / per_row;
-      const int hl = (rem % per_row) / CPR;
-      const int ch = rem % CPR;
-      const int64_t off = (int64_t)b * gsb[tsr] + (int64_t)(2 * p + hl) * gsh[tsr] +
-                          (int64_t)j * gsn[tsr] + ch * 8;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(gsrc[tsr] + off * 2);
-      *reinterpret_cast<u32x4*>(lds + (((size_t)(tsr * 2 + hl) * N + j) * D + ch * 8) * 2) = v;
-    }
-    __syncthreads();
+    const int per = nst * CPR;
+#pragma unroll
+    for (int tsr = 0; tsr < 2; ++tsr)
+      for (int hl = 0; hl < nh; ++hl) {
+        const unsigned char* src = tsr ? vb[hl] : kb[hl];
+        const uint32_t sn = tsr ? vsn : ksn;
+        unsigned char* dst = rows + (size_t)(tsr * 2 + hl) * N * D * 2;
+        for (int c = (int)threadIdx.x; c < per; c += RA_THREADS) {
+          const int j = c / CPR, ch = c % CPR;
+          *reinterpret_cast<u32x4*>(dst + (uint32_t)(j * D + ch * 8) * 2) =
+              *reinterpret_cast<const u32x4*>(src + (uint32_t)j * sn + ch * 16);
+        }
+      }
   }
+  __syncthreads();
 
-  // Key row fetch: the lane's 16 channels of row j of head (2p + hl).
+  // Key row fetch: the lane's 16 channels of row j of head (2p + hl). Rows
+  // not staged in LDS are buffer loads from the head pair's base (a distinct
+  // load kind, so the two paths never merge into one generic-pointer load).
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kb[0], 0x7FFFFFFFu);
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vb[0], 0x7FFFFFFFu);
+  const uint32_t khs = (uint32_t)(kb[1] - kb[0]), vhs = (uint32_t)(vb[1] - vb[0]);
   auto fetch = [&](int tsr, int hl, int j) -> Row16 {
     if (STAGE && j < nst)
-      return load_row16(lds + (((size_t)(tsr * 2 + hl) * N + j) * D + part * 16) * 2);
-    const int64_t off = (int64_t)b * gsb[tsr] + (int64_t)(2 * p + hl) * gsh[tsr] +
-                        (int64_t)j * gsn[tsr] + part * 16;
-    return load_row16(gsrc[tsr] + off * 2);
+      return load_row16(rows + (((size_t)(tsr * 2 + hl) * N + j) * D + part * 16) * 2);
+    const uint32_t off = (uint32_t)hl * (tsr ? vhs : khs) + (uint32_t)j * (tsr ? vsn : ksn) + part * 32;
+    Row16 r;
+    r.p0 = buf_load16(tsr ? vrs : krs, off);
+    r.p1 = buf_load16(tsr ? vrs : krs, off + 16);
+    return r;
   };
 
-  const bool axis = p < 3;
   for (int r = (int)threadIdx.x / LPR; r < N; r += RPP) {
     if (r >= live_rows) {
       for (int hl = 0; hl < nh; ++hl) {
-        const int64_t off = (int64_t)b * a.o_sb + (int64_t)(2 * p + hl) * a.o_sh + (int64_t)r * a.o_sn +
-                            part * 16;
-        u32x4* dst = reinterpret_cast<u32x4*>(a.out + off);
+        u32x4* dst = reinterpret_cast<u32x4*>(ob[hl] + (uint32_t)r * osn + part * 32);
         dst[0] = u32x4{0u, 0u, 0u, 0u};
         dst[1] = u32x4{0u, 0u, 0u, 0u};
       }
@@ -172,34 +203,34 @@ __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_a
     js[0] = ir[0];
 #pragma unroll
     for (int t = 0; t < 10; ++t) js[1 + t] = axis ? ir[1 + 10 * p + t] : -1;
+    uint32_t rl4 = 0x05050505u;  // reach (own dir 0, own dir 1, opp dir 0, opp dir 1)
+    if (a.blockers && axis) {
+      const uint8_t* rl = a.raylen + (int64_t)b * a.rl_sb + (int64_t)r * a.rl_sn + 2 * p;
+      rl4 = (uint32_t)rl[0] | ((uint32_t)rl[1] << 8) | ((uint32_t)rl[6] << 16) | ((uint32_t)rl[7] << 24);
+    }
+
     for (int hl = 0; hl < nh; ++hl) {
-      const int hh = 2 * p + hl;
-      int reach0 = RAY_STEPS, reach1 = RAY_STEPS;
-      if (a.blockers && axis) {
-        const uint8_t* rl = a.raylen + (int64_t)b * a.rl_sb + (int64_t)r * a.rl_sn + hl * 6 + 2 * p;
-        reach0 = rl[0];
-        reach1 = rl[1];
-      }
-      bool lv[11];
-      lv[0] = (unsigned)js[0] < (unsigned)N;
+      const int reach0 = (int)((rl4 >> (16 * hl)) & 0xFF);
+      const int reach1 = (int)((rl4 >> (16 * hl + 8)) & 0xFF);
+      // live slots as a per-lane bit mask (lane masks per slot would pin 22
+      // scalar registers across the slot loops)
+      uint32_t live = (unsigned)js[0] < (unsigned)N ? 1u : 0u;
 #pragma unroll
       for (int t = 0; t < 10; ++t)
-        lv[1 + t] = (unsigned)js[1 + t] < (unsigned)N && (t % 5 + 1) <= (t < 5 ? reach0 : reach1);
+        live |= ((unsigned)js[1 + t] < (unsigned)N && (t % 5 + 1) <= (t < 5 ? reach0 : reach1) ? 1u : 0u)
+                << (1 + t);
 
-      const int64_t qoff = (int64_t)b * a.q_sb + (int64_t)hh * a.q_sh + (int64_t)r * a.q_sn + part * 16;
-      const Row16 q = load_row16(reinterpret_cast<const unsigned char*>(a.q + qoff));
+      const Row16 q = load_row16(qb[hl] + (uint32_t)r * qsn + part * 32);
       float s[11];
       float m = -INFINITY;
 #pragma unroll
       for (int i = 0; i < 11; ++i) {
         s[i] = -INFINITY;
-        if (lv[i]) {
+        if (live & (1u << i)) {
           float d = dot16(q, fetch(0, hl, js[i]));
 #pragma unroll
           for (int x = 1; x < LPR; x <<= 1) d += __shfl_xor(d, x, 64);
-          const int slot = i == 0 ? 0 : 1 + 10 * p + (i - 1);
-          const unsigned short bb = a.slot_bias[slot * a.H + hh];
-          s[i] = d * inv_sqrt_d<D>() + (float)__builtin_bit_cast(_Float16, bb);
+          s[i] = d * inv_sqrt_d<D>() + sbias[hl * 11 + i];
           m = fmaxf(m, s[i]);
         }
       }
@@ -209,7 +240,7 @@ __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_a
       float l = 0.f;
 #pragma unroll
       for (int i = 0; i < 11; ++i) {
-        if (lv[i]) {
+        if (live & (1u << i)) {
           const float pr = __builtin_amdgcn_exp2f((s[i] - m) * LOG2E_F);
           l += pr;
           fma_row16(acc, pr, fetch(1, hl, js[i]));
@@ -222,8 +253,7 @@ __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_a
         o0[w] = pack_f16x2(acc[2 * w] * inv, acc[2 * w + 1] * inv);
         o1[w] = pack_f16x2(acc[8 + 2 * w] * inv, acc[8 + 2 * w + 1] * inv);
       }
-      const int64_t off = (int64_t)b * a.o_sb + (int64_t)hh * a.o_sh + (int64_t)r * a.o_sn + part * 16;
-      u32x4* dst = reinterpret_cast<u32x4*>(a.out + off);
+      u32x4* dst = reinterpret_cast<u32x4*>(ob[hl] + (uint32_t)r * osn + part * 32);
       dst[0] = o0;
       dst[1] = o1;
     }
@@ -552,10 +582,10 @@ int launch_ray_attn(const shrimp_ray_attn_args& a, bool stage, hipStream_t st) {
   const int npairs = (a.H + 1) / 2;
   const dim3 grid((unsigned)((int64_t)a.B * npairs));
   if (stage) {
-    const uint32_t lds = 8u * (uint32_t)a.N * D;
+    const uint32_t lds = RA_BIAS_LDS + 8u * (uint32_t)a.N * D;
     hipLaunchKernelGGL((ray_attn_kernel<D, true>), grid, dim3(RA_THREADS), lds, st, a);
   } else {
-    hipLaunchKernelGGL((ray_attn_kernel<D, false>), grid, dim3(RA_THREADS), 0, st, a);
+    hipLaunchKernelGGL((ray_attn_kernel<D, false>), grid, dim3(RA_THREADS), RA_BIAS_LDS, st, a);
   }
   return check_launch("ray_attn");
 }
@@ -603,6 +633,12 @@ extern "C" int shrimp_ray_attn(const shrimp_ray_attn_args* a, void* stream) {
   SHRIMP_REQUIRE(a->idx_sn >= RAY_SLOT_COUNT && a->idx_sb >= (int64_t)a->N * a->idx_sn - a->idx_sn + RAY_SLOT_COUNT,
                  "ray_attn: idx rows must hold 32 slots");
   SHRIMP_REQUIRE(!a->blockers || a->rl_sn >= 12, "ray_attn: raylen rows must hold 12 slots");
+  const int64_t rsn[4] = {a->q_sn, a->k_sn, a->v_sn, a->o_sn};
+  const int64_t rsh[4] = {a->q_sh, a->k_sh, a->v_sh, a->o_sh};
+  for (int i = 0; i < 4; ++i)
+    SHRIMP_REQUIRE(rsn[i] >= a->D && ((int64_t)a->N * rsn[i] + (rsh[i] < 0 ? -rsh[i] : rsh[i])) * 2 <
+                                         (1LL << 31),
+                   "ray_attn: a head pair's rows of a position must span less than 2 GiB");
   SHRIMP_REQUIRE((int64_t)a->B * ((a->H + 1) / 2) < (1LL << 31), "ray_attn: grid too large");
   const bool stage = g_ray_variant == 0 && 8u * (uint64_t)a->N * a->D <= RA_STAGE_MAX_LDS;
   hipStream_t s = as_stream(stream);
