@@ -16,12 +16,15 @@ the softmax over each row's legal prefix, rows in order; optional
 ``moves_left_bytes`` f32 x B and ``priors_logits_bytes`` f32 x sum(L).
 
 The payload's CSR arrays go to the device once (pinned host copies, one
-non-blocking upload each); per group the pack into the padded forward inputs
-(``shrimp_prep_csr``, one kernel: sentinel remap, masks, coordinates,
-sequence lengths, stem features), the forward and the decode
-(``shrimp_decode``: binned value, moves-left, legal-prefix softmax and the
-flat gather in one kernel) run on the current stream; ``result`` performs the
-only device-to-host copy.
+non-blocking upload each, on the evaluator's copy stream); per group the pack
+into the padded forward inputs (``shrimp_prep_csr``, one kernel: sentinel
+remap, masks, coordinates, sequence lengths, stem features), the forward and
+the decode (``shrimp_decode``: binned value, moves-left, legal-prefix softmax
+and the flat gather in one kernel) run on the current stream once the upload
+is done. ``result`` waits for that payload's work only and copies its outputs
+back on the copy stream, so a caller that submits the next payload before
+collecting this one (as the reference's ``submit_payload`` / ``result``
+pair allows) overlaps the next upload and host parse with this forward.
 """
 
 from __future__ import annotations
@@ -94,6 +97,17 @@ class ShrimpEvaluator:
                 f"(got {self.device})"
             )
         self.model = model.to(self.device).eval()
+        # Uploads and reply copies of payloads submitted while another is in
+        # flight run here, beside the compute (default priority, like every
+        # stream of this build); a lone payload stays on the caller's stream,
+        # which saves the cross-stream waits.
+        self._copy_stream = None
+        self._inflight = 0
+
+    def _copies(self) -> torch.cuda.Stream:
+        if self._copy_stream is None:
+            self._copy_stream = torch.cuda.Stream(self.device)
+        return self._copy_stream
 
     def __call__(self, payload: dict) -> dict:
         return self.evaluate_payload(payload)
@@ -140,13 +154,20 @@ class ShrimpEvaluator:
         ml = torch.empty(b, dtype=torch.float32, device=dev) if request_ml else None
         priors = torch.empty(int(flat_off[-1]), dtype=torch.float32, device=dev)
         logits = torch.empty_like(priors) if request_logits else None
-        d_legal = _upload(legal, torch.int32, dev)
-        d_off = _upload(flat_off[:-1], torch.int64, dev)
-        # the CSR payload itself; u16 neighbour ids travel as their int16 bits
-        d_feats = _upload(feats, torch.float16, dev)
-        d_qr = _upload(qr, torch.int16, dev)
-        d_nbr = _upload(nbr.view(np.int16), torch.int16, dev)
-        d_rows = _upload(offsets, torch.int64, dev)
+        compute = torch.cuda.current_stream(dev)
+        copies = self._copies() if self._inflight > 0 else compute
+        with torch.cuda.stream(copies):
+            d_legal = _upload(legal, torch.int32, dev)
+            d_off = _upload(flat_off[:-1], torch.int64, dev)
+            # the CSR payload itself; u16 neighbour ids travel as their int16 bits
+            d_feats = _upload(feats, torch.float16, dev)
+            d_qr = _upload(qr, torch.int16, dev)
+            d_nbr = _upload(nbr.view(np.int16), torch.int16, dev)
+            d_rows = _upload(offsets, torch.int64, dev)
+        if copies is not compute:
+            compute.wait_stream(copies)
+            for t in (d_legal, d_off, d_feats, d_qr, d_nbr, d_rows):
+                t.record_stream(compute)
         lib = _lib.load()
         stream = _lib.stream_handle(dev)
         rt = self.model.hip_runtime()
@@ -170,19 +191,42 @@ class ShrimpEvaluator:
                 ),
                 "decode",
             )
+        done = torch.cuda.Event()
+        done.record(compute)
+        self._inflight += 1
         return {
             "b": b, "request_ml": request_ml, "request_logits": request_logits,
             "values_gpu": values, "ml_gpu": ml, "priors_gpu": priors, "logits_gpu": logits,
+            "done": done,
         }
 
     @torch.no_grad()
     def result(self, handle: dict) -> dict:
-        reply = {
-            "values_bytes": handle["values_gpu"].cpu().numpy().astype(np.float32, copy=False).tobytes(),
-            "priors_bytes": handle["priors_gpu"].cpu().numpy().astype(np.float32, copy=False).tobytes(),
-        }
+        """Waits for this payload's work (not for payloads submitted after it)
+        and returns its reply bytes."""
+
+        names = [("values_bytes", "values_gpu")]
+        names.append(("priors_bytes", "priors_gpu"))
         if handle["request_ml"]:
-            reply["moves_left_bytes"] = handle["ml_gpu"].cpu().numpy().tobytes()
+            names.append(("moves_left_bytes", "ml_gpu"))
         if handle["request_logits"]:
-            reply["priors_logits_bytes"] = handle["logits_gpu"].cpu().numpy().tobytes()
-        return reply
+            names.append(("priors_logits_bytes", "logits_gpu"))
+        self._inflight = max(0, self._inflight - 1)
+        if self._inflight == 0:
+            # nothing was submitted after this payload: copy on its own stream
+            return {key: handle[src].cpu().numpy().astype(np.float32, copy=False).tobytes()
+                    for key, src in names}
+        copies = self._copies()
+        host = {}
+        with torch.cuda.stream(copies):
+            copies.wait_event(handle["done"])
+            for key, src in names:
+                t = handle[src]
+                h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+                h.copy_(t, non_blocking=True)
+                t.record_stream(copies)
+                host[key] = h
+            fetched = torch.cuda.Event()
+            fetched.record(copies)
+        fetched.synchronize()
+        return {key: host[key].numpy().astype(np.float32, copy=False).tobytes() for key, _ in names}

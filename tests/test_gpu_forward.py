@@ -328,3 +328,26 @@ def test_graph_replays_match_eager():
     rt = net.hip_runtime()
     assert len(rt._graphs) >= 1
 
+
+
+@pytest.mark.parametrize("graphs", [False, True], ids=["eager", "graphs"])
+def test_evaluator_pipelined_submissions_match(graphs):
+    """Three payloads submitted before any is collected (uploads on the copy
+    stream overlap the forwards), collected out of order: each reply is
+    byte-identical to evaluating that payload alone."""
+
+    from shrimp import synthetic
+    from shrimp.inference import ShrimpEvaluator
+
+    net = _net(128, 8, "CCACCACCACCA", seed=9)
+    ev = ShrimpEvaluator(net, DEV, graphs=graphs)
+    pays = [synthetic.serve_payload("cfg4", n, seed=s, request_moves_left=(s % 2 == 0))[0]
+            for n, s in ((40, 11), (7, 12), (64, 13))]
+    want = [ev.evaluate_payload(p) for p in pays]
+    handles = [ev.submit_payload(p) for p in pays]
+    for i in (1, 0, 2):
+        print(f"pipelined result {i} graphs={graphs}", flush=True)
+        got = ev.result(handles[i])
+        assert set(got) == set(want[i])
+        for key in want[i]:
+            assert got[key] == want[i][key], (i, key)
