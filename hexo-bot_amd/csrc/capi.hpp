@@ -25,11 +25,14 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // Largest dynamic LDS allocation one workgroup may request on the current
 // device (queried once per device).
 int max_lds_per_block();
+// Compute units of the current device (queried once per device).
+int cu_count();
 
-// Conv kernel selection: 0 = automatic (big-tile LDS kernel for the
-// 128-channel 7-tap shape, else LDS-staged when the position fits, else
-// global gather), 1 = always the global-gather kernel, 2 = LDS-staged
-// (no big tiles), 3 = as 0.
+// Conv kernel selection: 0 = automatic (small batches: one 64-row tile per
+// workgroup; else big-tile LDS kernel for the 128-channel 7-tap shape, else
+// LDS-staged when the position fits, else global gather), 1 = always the
+// global-gather kernel, 2 = LDS-staged (no big tiles), 3 = as 0 without the
+// small-batch row split.
 extern int g_conv_variant;
 // Attention: 0 = automatic (two heads per workgroup when they fit), 1 = one
 // head per workgroup.

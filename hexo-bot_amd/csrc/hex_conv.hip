@@ -363,7 +363,9 @@ __global__ __launch_bounds__(256, 2) void hex_conv_kernel(const shrimp_conv_args
   conv_epilogue<COUT, MB, EPI, PS_GLOBAL>(a, acc, rb, rn, rv, lg);
 }
 
-// LDS-staged variant: one workgroup per position. The position's N rows
+// LDS-staged variant: workgroups (position, row split); split y of Y takes the
+// row tiles y, y + Y, ... (Y = 1 for batches that fill the GPU; small batches
+// spread a position's tiles over several workgroups, each staging all rows). The position's N rows
 // (cin_pad = CIN channels) are copied once into LDS, plus one zero row at
 // index N that stands for every absent neighbour, and all taps gather from
 // there, so HBM sees each row once (the global variant re-fetches a row per
@@ -371,7 +373,11 @@ __global__ __launch_bounds__(256, 2) void hex_conv_kernel(const shrimp_conv_args
 // Row j occupies bytes [j*2*CIN, (j+1)*2*CIN); its 16-byte chunk c is stored
 // at chunk slot c ^ (j % (CIN/8)), so the 16 lanes of an MFMA lane group,
 // reading the same chunk of 16 different rows, mostly hit distinct banks.
-template <int COUT, int MB, int EPI, int CIN>
+// BIGORDER (7 taps): the big-tile kernel's arithmetic, so a small batch split
+// over workgroups gives the same bits as the large batch: accumulators start
+// from the bias (except for the residual epilogue) and the K loop runs channel
+// chunk outer, tap inner.
+template <int COUT, int MB, int EPI, int CIN, bool BIGORDER = false>
 __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_args a,
                                                               uint32_t w_bytes) {
   constexpr int NB = COUT / 16;
@@ -421,7 +427,7 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
   const int taps = a.taps;
   const int nsteps = taps * KC;
 
-  for (int tile0 = 0; tile0 < N; tile0 += TILE) {
+  for (int tile0 = (int)blockIdx.y * TILE; tile0 < N; tile0 += (int)gridDim.y * TILE) {
     const int row_base = tile0 + wave * MB * 16;
     if (row_base >= N) break;
     int rb[MB], rn[MB];
@@ -445,6 +451,58 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
     };
 
     f32x4 acc[NB][MB];
+    if constexpr (BIGORDER) {
+      constexpr bool BA = (EPI & EPI_RESID) == 0;
+      constexpr int T = 7;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const f32x4 bb = BA ? *reinterpret_cast<const f32x4*>(a.bias + nb * 16 + lg * 4)
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = bb;
+      }
+      uint32_t sa[T][MB];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        int j[MB];
+        tap_rows(t, j);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) sa[t][mb] = row_addr(j[mb]);
+      }
+      // Weight fragments run two steps ahead through a ring of three (a small
+      // tile has few products per step to cover the L2 latency), row fragments
+      // one step ahead.
+      constexpr int NS = T * KC;
+      u32x4 wq[3][NB], xq[2][MB];
+      auto load_w = [&](int s, u32x4 (&w)[NB]) {
+        const int kc = s / T, t = s % T;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          w[nb] = buf_load16(wr, (uint32_t)((((t * KC + kc) * NB + nb) * 64 + lane) * 16));
+      };
+      auto load_x = [&](int s, u32x4 (&x)[MB]) {
+        const int kc = s / T, t = s % T;
+        const uint32_t cs = (uint32_t)(kc * 4 + lg) << 4;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) x[mb] = *reinterpret_cast<const u32x4*>(xs + (sa[t][mb] ^ cs));
+      };
+      load_w(0, wq[0]);
+      load_w(1, wq[1]);
+      load_x(0, xq[0]);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        if (s + 2 < NS) load_w(s + 2, wq[(s + 2) % 3]);
+        if (s + 1 < NS) load_x(s + 1, xq[(s + 1) % 2]);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+            acc[nb][mb] = mfma16x16x32(wq[s % 3][nb], xq[s % 2][mb], acc[nb][mb]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      conv_epilogue<COUT, MB, BA ? (EPI | EPI_BACC) : EPI, PS_GLOBAL>(a, acc, rb, rn, rv, lg);
+      continue;
+    }
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -798,11 +856,28 @@ static int launch_conv(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, size
                        hipStream_t st) {
   const bool out16 = (EPI & EPI_HEAD) != 0 ||
                      (a->o_sn % 8 == 0 && a->o_sb % 8 == 0 && ((uintptr_t)a->out & 15) == 0);
-  if (COUT == 128 && lds && a->cin_pad == 128 && a->taps == 7 && a->N <= BIG_MAX_N && out16 &&
-      (g_conv_variant == 0 || g_conv_variant == 3)) {
+  const size_t big_lds = (size_t)big_rows_padded(a->N) * 256 + BIG_PARAMS * sizeof(float);
+  const bool big = COUT == 128 && lds && a->cin_pad == 128 && a->taps == 7 && a->N <= BIG_MAX_N &&
+                   out16 && (g_conv_variant == 0 || g_conv_variant == 3) &&
+                   big_lds <= (size_t)max_lds_per_block();
+  // Small batches (at most half as many positions as compute units): one row
+  // tile of 64 rows per workgroup, (B, N / 64) workgroups, instead of one
+  // workgroup per position; where the big-tile kernel would run, with its
+  // arithmetic (same bits).
+  if (COUT == 128 && lds && (a->cin_pad == 32 || a->cin_pad == 128) &&
+      (int64_t)a->B * 2 <= cu_count() && g_conv_variant == 0) {
+    const dim3 grid((unsigned)a->B, (unsigned)((a->N + 63) / 64));
+    if (big)
+      hipLaunchKernelGGL((hex_conv_lds_kernel<128, 1, EPI, 128, true>), grid, dim3(256), lds, st, *a, wb);
+    else if (a->cin_pad == 32)
+      hipLaunchKernelGGL((hex_conv_lds_kernel<128, 1, EPI, 32>), grid, dim3(256), lds, st, *a, wb);
+    else
+      hipLaunchKernelGGL((hex_conv_lds_kernel<128, 1, EPI, 128>), grid, dim3(256), lds, st, *a, wb);
+    return check_launch("hex_conv");
+  }
+  if (big) {
     const int waves = (a->N + 127) / 128;
-    const size_t big_lds = (size_t)big_rows_padded(a->N) * 256 + BIG_PARAMS * sizeof(float);
-    if (big_lds <= (size_t)max_lds_per_block()) {
+    {
       hipLaunchKernelGGL((hex_conv_big_kernel<EPI>), dim3(a->B), dim3(64 * waves), big_lds, st, *a,
                          xb, wb);
       return check_launch("hex_conv");

@@ -94,12 +94,23 @@ class HipForward:
         # ConvBlock as one launch (conv1's output kept in LDS) where a fused
         # kernel exists; off runs the two convolutions.
         self.use_fused_block = True
+        self._cu_cache: dict = {}
         # Captured forwards (graph_forward_csr), keyed by (batch bucket, Npad,
         # moves-left, device); dropped when a parameter changes.
         self._graphs: dict = {}
         self._graph_params = None
         self._graph_pool = None
         self._empty_rows: dict = {}
+
+    def _cus(self, dev) -> int:
+        """Compute units of the device. Batches of at most half that many
+        positions run ConvBlocks as two row-split convolutions (same bits as the
+        fused block): the fused block gives each position one workgroup and
+        would leave most units idle."""
+
+        if dev.index not in self._cu_cache:
+            self._cu_cache[dev.index] = torch.cuda.get_device_properties(dev).multi_processor_count
+        return self._cu_cache[dev.index]
 
     def invalidate(self) -> None:
         self._packed = None
@@ -406,7 +417,7 @@ class HipForward:
             if kind == "C":
                 k = P.convs[ci]
                 ci += 1
-                if self.use_fused_block and conv_block_supported(7, N, C, C):
+                if self.use_fused_block and 2 * B > self._cus(dev) and conv_block_supported(7, N, C, C):
                     launch_conv_block(
                         x=cells, x_sb=S * C, x_sn=C, idx=idx, idx_stride=7, mask8=mask8, B=B,
                         N=N, C=C, w1=k.w1, b1=k.b1, ln1_w=k.ln1w, ln1_b=k.ln1b, eps1=k.eps1,

@@ -46,9 +46,13 @@ int shrimp_abi_version(void);
 /* Tuning / test switches (no counterpart in the reference).
  * shrimp_conv_variant: 0 = automatic conv kernel choice (a position's rows
  * staged in LDS when they fit, 128x128 tiles per wave for the 128-channel
- * 7-tap conv), 1 = always gather rows from global memory, 2 = LDS-staged
- * rows with small tiles, 3 = same as 0; other values only query. Returns
- * the previous setting. Process-wide.
+ * 7-tap conv, and for batches of at most half the compute-unit count one
+ * 64-row tile per workgroup so a position's rows spread over several; that
+ * split repeats the big-tile kernel's arithmetic where the big-tile kernel
+ * would serve a large batch, so results do not depend on the batch), 1 = always
+ * gather rows from global memory, 2 = LDS-staged rows with small tiles,
+ * 3 = as 0 without the small-batch row split; other values only query.
+ * Returns the previous setting. Process-wide.
  * shrimp_attn_variant: 0 = automatic (two heads per attention workgroup when
  * their K/V fit the LDS budget), 1 = one head per workgroup; other values
  * only query. Returns the previous setting. Process-wide.

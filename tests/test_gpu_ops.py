@@ -33,11 +33,13 @@ def close(got, want, atol=2e-2, rtol=1e-2, what=""):
     assert worst <= atol, f"{what}: max excess error {worst}"
 
 
-@pytest.fixture(params=[0, 1, 2], ids=["auto", "global", "staged"])
+@pytest.fixture(params=[0, 1, 2, 3], ids=["auto", "global", "staged", "big"])
 def conv_variant(request):
-    """Runs a conv test with the automatic kernel choice (big-tile staged
-    kernel for 128 -> 128 channels, 7 taps), with the global-gather kernel
-    forced and with the small-tile LDS-staged kernel forced."""
+    """Runs a conv test with the automatic kernel choice (at these small
+    batches: one 64-row tile per workgroup), with the global-gather kernel
+    forced, with the small-tile LDS-staged kernel forced, and with the
+    automatic choice minus the small-batch split (big-tile staged kernel for
+    128 -> 128 channels, 7 taps)."""
 
     from shrimp import _lib
 
@@ -199,13 +201,21 @@ def test_conv_block_fused(conv_case, n):
     )
     y1 = torch.empty_like(xd)
     common = dict(idx=idx, taps=7, idx_stride=7, mask8=m8, B=B, N=N, cin_pad=128, cout=128)
-    ops.launch_conv(x=xd, x_sb=N * 128, x_sn=128, wpack=wp1, bias=d["b1"], ln_w=d["l1w"],
-                    ln_b=d["l1b"], relu=True, out=y1, o_sb=N * 128, o_sn=128, **common)
-    two = xd.clone()
-    ops.launch_conv(x=y1, x_sb=N * 128, x_sn=128, wpack=wp2, bias=d["b2"], ln_w=d["l2w"],
-                    ln_b=d["l2b"], resid=two, r_sb=N * 128, r_sn=128, gamma=d["g"], out=two,
-                    o_sb=N * 128, o_sn=128, **common)
-    torch.cuda.synchronize()
+    # the big-tile convs (this small batch would otherwise take the row split,
+    # whose products run in another order)
+    from shrimp import _lib
+
+    prev = _lib.load().shrimp_conv_variant(3)
+    try:
+        ops.launch_conv(x=xd, x_sb=N * 128, x_sn=128, wpack=wp1, bias=d["b1"], ln_w=d["l1w"],
+                        ln_b=d["l1b"], relu=True, out=y1, o_sb=N * 128, o_sn=128, **common)
+        two = xd.clone()
+        ops.launch_conv(x=y1, x_sb=N * 128, x_sn=128, wpack=wp2, bias=d["b2"], ln_w=d["l2w"],
+                        ln_b=d["l2b"], resid=two, r_sb=N * 128, r_sn=128, gamma=d["g"], out=two,
+                        o_sb=N * 128, o_sn=128, **common)
+        torch.cuda.synchronize()
+    finally:
+        _lib.load().shrimp_conv_variant(prev)
     diff = (fused.float() - two.float()).abs().max().item()
     print(f"fused vs two launches: max diff {diff:.3e}", flush=True)
     assert torch.equal(fused, two)
