@@ -815,19 +815,25 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   };
 
   // (query blocks round-robin over the waves, the split last block: see nmain)
+  // Small batches spread a position's query blocks over gridDim.z workgroups:
+  // workgroup g takes the rounds g, g + Z, ... of the round-robin (each block on
+  // the wave and with the key order it has with Z = 1, so the bits do not
+  // change) and the last one the split block.
+  const int qz = PROJ ? 0 : (int)blockIdx.z, nz = PROJ ? 1 : (int)gridDim.z;
+  const bool tail_here = split && qz == nz - 1;
   AttnQuery qi;
   float m[HG], l[HG];
   f32x4 o[HG][KD];
-  for (int qb = wave, slot = 0;; qb += 4, ++slot) {
+  for (int qb = wave + 4 * qz, slot = 0;; qb += 4 * nz, ++slot) {
     const bool tail = qb >= nmain;
-    if (tail && !split) break;
+    if (tail && !tail_here) break;
     const int k0 = tail ? (wave * nkb) / 4 : 0;
     const int k1 = tail ? ((wave + 1) * nkb) / 4 : nkb;
     run_block(tail ? nmain : qb, slot, k0, k1, qi, m, l, o);
     if (tail) break;
     store_block(qi, l, o);
   }
-  if (split) {
+  if (tail_here) {
     __syncthreads();  // K and V are no longer read: their LDS holds the partials
     float* part_lds = reinterpret_cast<float*>(smem) + ((wave - 1) * 64 + lane) * PF;
     if (wave > 0) {
@@ -879,7 +885,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
 
   // Query rows past the live bound store zeros.
   const int dq4 = a.d / 4;
-  for (int i = tid; i < (S - L) * HG * dq4; i += 256) {
+  for (int i = qz == 0 ? tid : (S - L) * HG * dq4; i < (S - L) * HG * dq4; i += 256) {
     const int row = L + i / (HG * dq4);
     const int rem = i - (row - L) * HG * dq4;
     const int h = rem / dq4;
@@ -901,7 +907,14 @@ static size_t attn_smem_bytes(int DP, int HG, int S, int npos, bool pair) {
 template <int DP, int HG, bool PAIR>
 static int launch_attn(const shrimp_attn_args* a, float qk_scale, uint32_t qkv_bytes, int npos,
                        size_t smem, hipStream_t st) {
-  dim3 grid(a->H / HG, a->B);
+  // query splits (small batches): up to 4, doubling while the workgroups stay
+  // within two per compute unit and each split keeps at least two rounds of
+  // four query blocks
+  const int groups = a->H / HG * a->B;
+  const int rounds = ((a->S + 15) / 16) / 4;
+  int z = 1;
+  while (z < 4 && groups * z * 2 <= 2 * cu_count() && rounds >= 2 * z) z *= 2;
+  dim3 grid(a->H / HG, a->B, z);
   const shrimp_attn_proj_args none{};
   hipLaunchKernelGGL((attn_kernel<DP, HG, PAIR, 0>), grid, dim3(256), smem, st, *a, qk_scale,
                      qkv_bytes, npos, none, 0u);
