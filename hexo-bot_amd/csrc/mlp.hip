@@ -367,7 +367,9 @@ extern "C" int shrimp_attn_mlp(const shrimp_mlp_args* a, void* stream) {
       cus <= 0)
     return set_error(SHRIMP_ELAUNCH, "attn_mlp: cannot query the compute unit count");
   const int64_t nblk = (a->rows + 15) / 16;
-  const int grid = (int)std::min<int64_t>(cus, (nblk + MWAVES - 1) / MWAVES);
+  // at least one workgroup per 4 row blocks (up to one per compute unit): small
+  // row counts spread over more units, each staging the weights once
+  const int grid = (int)std::min<int64_t>(cus, std::max<int64_t>((nblk + MWAVES - 1) / MWAVES, (nblk + 3) / 4));
   hipLaunchKernelGGL(attn_mlp_kernel, dim3(grid), dim3(MWAVES * 64), W_LDS, as_stream(stream), *a,
                      (uint32_t)xe, (uint32_t)se);
   return check_launch("attn_mlp");

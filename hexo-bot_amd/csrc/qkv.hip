@@ -201,7 +201,9 @@ extern "C" int shrimp_attn_qkv(const shrimp_qkv_args* a, void* stream) {
   int dshift = 0;
   while ((1 << dshift) < d) ++dshift;
   const int64_t nblk = (a->rows + 15) / 16;
-  const int grid = (int)std::min<int64_t>(cus, (nblk + QWAVES - 1) / QWAVES);
+  // at least one workgroup per 4 row blocks (up to one per compute unit): small
+  // row counts spread over more units, each staging the weights once
+  const int grid = (int)std::min<int64_t>(cus, std::max<int64_t>((nblk + QWAVES - 1) / QWAVES, (nblk + 3) / 4));
   hipLaunchKernelGGL(attn_qkv_kernel, dim3(grid), dim3(QWAVES * 64), QW_LDS, as_stream(stream), *a,
                      (uint32_t)xe, dshift);
   return check_launch("attn_qkv");
