@@ -52,7 +52,9 @@ struct AttnLds {
   unsigned short* Ks;  // [HG][KD][SP/16] K fragments (256 bf16 each)
   unsigned short* Vt;  // [HG][KD][SP/16] V fragments (256 bf16 each)
   int2* kqr;           // [SP] key coordinates
-  int* kkey;           // [SP] byte offset code (q*XW + r + XD*XW + XD) * 2 HG
+  int* kkey;           // [SP] LDS byte address of the key's table row for query
+                       // offset code 0: xtab + (q*XW + r + XD*XW + XD) * 2 HG
+  const unsigned char* base;  // start of the dynamic LDS (kkey is relative to it)
   int* kcls;           // [SP] KEY_CELL / KEY_TOKEN / KEY_DEAD
   int* blk_gen;        // [SP / 16] 1 if the block holds a token or dead key
   int* blk_dead;       // [SP / 16] 1 if the block holds a dead key (or keys past the bound)
@@ -130,7 +132,7 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
 #pragma unroll
         for (int h = 0; h < HG; ++h) bias[kb][j][h] = s.tab[p * HG + h];
       } else if (PATH == PATH_LINEAR) {
-        const char* xp = reinterpret_cast<const char*>(s.xtab) + (s.kkey[key] - qi.qkey);
+        const char* xp = reinterpret_cast<const char*>(s.base) + (s.kkey[key] - qi.qkey);
         if (HG == 2) {
           const unsigned w = *reinterpret_cast<const unsigned*>(xp);
           bias[kb][j][0] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xFFFFu));
@@ -273,13 +275,17 @@ SHRIMP_DEV u32x2 opaque2(u32x2 v) {
   return v;
 }
 
-template <int DP, int HG, bool PAIR, int PROJ>
-__global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, float qk_scale,
+template <int DP, int HG, bool PAIR, int PROJ, int NW>
+__global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const shrimp_attn_args a, float qk_scale,
                                                    uint32_t qkv_bytes, int npos,
                                                    const shrimp_attn_proj_args p, uint32_t x_bytes) {
-  static_assert(!PROJ || (DP == 16 && HG == 2 && !PAIR), "projection covers d = 16, two heads, coords");
+  static_assert(!PROJ || (DP == 16 && HG == 2 && !PAIR && NW == 4),
+                "projection covers d = 16, two heads, coords, four waves");
+  static_assert(NW == 4 || NW == 8, "four or eight waves per workgroup");
+  static_assert(HG == 1 || HG == 2, "one or two heads per workgroup");
+  constexpr int NT = 64 * NW;  // threads per workgroup
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  __shared__ int span_red[16];
+  __shared__ int span_red[4 * NW];
   constexpr int KD = DP / 16;
   int b = blockIdx.y;
   int h0 = blockIdx.x * HG;
@@ -311,6 +317,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   float* tail = s.tokb + 3 * HG;
   s.tab = tail;
   s.xtab = reinterpret_cast<_Float16*>(tail);
+  s.base = smem;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -323,15 +330,15 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(a.v, qkv_bytes);
   const int64_t pos_base = (int64_t)b * a.qkv_sb;
 
-  // Whole query blocks round-robin over the 4 waves. When one block is left
-  // over (nqb % 4 == 1: 17 blocks at S = 264), it is split by key range into
-  // 4 parts, one per wave, instead of running whole on one wave; after a
+  // Whole query blocks round-robin over the NW waves. When one block is left
+  // over (nqb % NW == 1: 17 blocks at S = 264), it is split by key range into
+  // NW parts, one per wave, instead of running whole on one wave; after a
   // barrier the partial softmax states go through LDS (over K and V, which
   // are no longer read) and wave 0 merges them.
   const int nqb = (L + 15) / 16;
   constexpr int PF = HG * (2 + 4 * KD);  // floats of one lane's partial state
   const bool split =
-      (nqb & 3) == 1 && 3 * 64 * PF * 4 <= 2 * HG * SP * DP * 2;  // partials fit over K, V
+      nqb % NW == 1 && (NW - 1) * 64 * PF * 4 <= 2 * HG * SP * DP * 2;  // partials fit over K, V
   const int nmain = split ? nqb - 1 : nqb;
 
   // PROJ: row blocks this wave projects (nkb == nqb): its own blocks
@@ -353,14 +360,15 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   if (PROJ && nitems > 0) load_x(0, xnext);
 
   // ---- global loads of the setup that nothing else depends on, issued first -----
-  // coordinates and liveness of keys tid and tid + 256 (the rare keys beyond
-  // 512 are loaded where they are used)
+  // coordinates and liveness of keys tid (and tid + 256 with four waves; the
+  // rare keys beyond 512 are loaded where they are used)
+  constexpr int KQN = 512 / NT;
   int kq[2] = {0, 0}, kr[2] = {0, 0};
   bool km[2] = {false, false};
   if (!PAIR) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int key = tid + 256 * i;
+    for (int i = 0; i < KQN; ++i) {
+      const int key = tid + NT * i;
       if (key >= nt && key < L) {
         const int64_t cell = (int64_t)b * NC + (key - nt);
         kq[i] = a.coords[cell * 2];
@@ -369,16 +377,15 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
       }
     }
   }
-  // the (XW*XW, HG) offset table of this head pair: XW*XW <= 12 * 256 dwords
-  constexpr int UX = 12;
-  static_assert(XW * XW <= 256 * UX, "offset table staging assumes one pass");
+  // the (XW*XW, HG) offset table of this head pair: XW*XW dwords, one pass
+  constexpr int UX = (XW * XW + NT - 1) / NT;
   unsigned xv[UX];
   const bool xstage = !PAIR && HG == 2 && a.xtab != nullptr;
   if (xstage) {
     const unsigned short* xg = static_cast<const unsigned short*>(a.xtab);
 #pragma unroll
     for (int u = 0; u < UX; ++u) {
-      const int x = tid + u * 256;
+      const int x = tid + u * NT;
       xv[u] = x < XW * XW ? *reinterpret_cast<const unsigned*>(xg + (int64_t)x * a.H + h0) : 0u;
     }
   }
@@ -393,12 +400,12 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   if constexpr (!PROJ) {
   {
     const int total = HG * LP * CH;
-    for (int base = tid; base < total; base += 256 * U) {
+    for (int base = tid; base < total; base += NT * U) {
       u32x4 v[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int i = base + u * 256;
-        const int h = i / (LP * CH);
+        const int i = base + u * NT;
+        const int h = HG == 2 && i >= LP * CH ? 1 : 0;  // HG <= 2: no division
         const int rem = i - h * LP * CH;
         const int key = rem / CH;
         const int ch = rem - key * CH;
@@ -409,9 +416,9 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int i = base + u * 256;
+        const int i = base + u * NT;
         if (i >= total) break;
-        const int h = i / (LP * CH);
+        const int h = HG == 2 && i >= LP * CH ? 1 : 0;  // HG <= 2: no division
         const int rem = i - h * LP * CH;
         const int key = rem / CH;
         const int ch = rem - key * CH;
@@ -425,13 +432,13 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   }
   {
     const int total = HG * (LP / 2) * CH;
-    for (int base = tid; base < total; base += 256 * U) {
+    for (int base = tid; base < total; base += NT * U) {
       u32x4 v0[U], v1[U];
       bool d0[U], d1[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int i = base + u * 256;
-        const int h = i / ((LP / 2) * CH);
+        const int i = base + u * NT;
+        const int h = HG == 2 && i >= (LP / 2) * CH ? 1 : 0;
         const int rem = i - h * (LP / 2) * CH;
         const int key = 2 * (rem / CH);
         const int ch = rem - (key / 2) * CH;
@@ -447,9 +454,9 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int i = base + u * 256;
+        const int i = base + u * NT;
         if (i >= total) break;
-        const int h = i / ((LP / 2) * CH);
+        const int h = HG == 2 && i >= (LP / 2) * CH ? 1 : 0;
         const int rem = i - h * (LP / 2) * CH;
         const int key = 2 * (rem / CH);
         const int ch = rem - (key / 2) * CH;
@@ -471,13 +478,13 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   // ---- key classes, coordinates, span of the live cells ----------------------------
   int qmin = 1 << 30, qmax = -(1 << 30), rmin = 1 << 30, rmax = -(1 << 30);
   if (!PAIR) {
-    for (int key = tid, i = 0; key < LP; key += 256, ++i) {
+    for (int key = tid, i = 0; key < LP; key += NT, ++i) {
       int q = 0, r = 0, cls = KEY_DEAD;  // keys past the bound (tokens too) are dead
       if (key < nt && key < L) {
         cls = KEY_TOKEN;
       } else if (key >= nt && key < L) {
         bool live;
-        if (i < 2) {
+        if (i < KQN) {
           q = i == 0 ? kq[0] : kq[1];
           r = i == 0 ? kr[0] : kr[1];
           live = i == 0 ? km[0] : km[1];
@@ -505,7 +512,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     s.tokb[tid] = a.btab[(W2 + tid / HG) * a.H + h0 + tid % HG];
   }
   if (PAIR) {
-    for (int i = tid; i < npos * HG; i += 256) {
+    for (int i = tid; i < npos * HG; i += NT) {
       const int pos = i / HG;
       const int h = i - pos * HG;
       s.tab[i] = a.table2[pos * a.H + h0 + h] * SHRIMP_LOG2E;
@@ -515,11 +522,11 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     if (HG == 2) {
 #pragma unroll
       for (int u = 0; u < UX; ++u) {
-        const int x = tid + u * 256;
+        const int x = tid + u * NT;
         if (x < XW * XW) reinterpret_cast<unsigned*>(s.xtab)[x] = xv[u];
       }
     } else {
-      for (int i = tid; i < XW * XW * HG; i += 256) {
+      for (int i = tid; i < XW * XW * HG; i += NT) {
         const int x = i / HG;
         reinterpret_cast<unsigned short*>(s.xtab)[i] = xg[(int64_t)x * a.H + h0 + (i - x * HG)];
       }
@@ -548,7 +555,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   // dead key or keys past the bound; query blocks with a token or dead query.
   // One key per thread; a 16-key block is 16 lanes of one wave, so its flags
   // are 16-bit fields of wave ballots.
-  for (int key0 = 0; key0 < LP; key0 += 256) {
+  for (int key0 = 0; key0 < LP; key0 += NT) {
     const int key = key0 + tid;
     bool kg = false, qg = false, kd = false;
     if (key < LP) {
@@ -570,7 +577,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   }
   if (!PAIR) {
     int q0 = span_red[0], q1 = span_red[1], r0 = span_red[2], r1 = span_red[3];
-    for (int w = 1; w < 4; ++w) {
+    for (int w = 1; w < NW; ++w) {
       q0 = min(q0, span_red[w * 4 + 0]);
       q1 = max(q1, span_red[w * 4 + 1]);
       r0 = min(r0, span_red[w * 4 + 2]);
@@ -586,9 +593,10 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     // (dq, dr) -> ((dq + XD) * XW + (dr + XD)) * 2 HG = kkey - qkey. Token and
     // dead keys take the code of the live cell (q0, r0), so every LINEAR read
     // stays inside the table; their biases are selected afterwards.
-    for (int key = tid; key < LP; key += 256) {
+    const int xoff = (int)(reinterpret_cast<const unsigned char*>(s.xtab) - smem);
+    for (int key = tid; key < LP; key += NT) {
       const int2 kk = s.kcls[key] == KEY_CELL ? s.kqr[key] : make_int2(q0, r0);
-      s.kkey[key] = (kk.x * XW + kk.y + XD * XW + XD) * 2 * HG;
+      s.kkey[key] = xoff + (kk.x * XW + kk.y + XD * XW + XD) * 2 * HG;
     }
   }
   // ---- PROJ: LayerNorm + q/k/v projection of this wave's row blocks ------------------
@@ -824,11 +832,11 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
   AttnQuery qi;
   float m[HG], l[HG];
   f32x4 o[HG][KD];
-  for (int qb = wave + 4 * qz, slot = 0;; qb += 4 * nz, ++slot) {
+  for (int qb = wave + NW * qz, slot = 0;; qb += NW * nz, ++slot) {
     const bool tail = qb >= nmain;
     if (tail && !tail_here) break;
-    const int k0 = tail ? (wave * nkb) / 4 : 0;
-    const int k1 = tail ? ((wave + 1) * nkb) / 4 : nkb;
+    const int k0 = tail ? (wave * nkb) / NW : 0;
+    const int k1 = tail ? ((wave + 1) * nkb) / NW : nkb;
     run_block(tail ? nmain : qb, slot, k0, k1, qi, m, l, o);
     if (tail) break;
     store_block(qi, l, o);
@@ -851,31 +859,24 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
     if (wave == 0) {
 #pragma unroll
       for (int h = 0; h < HG; ++h) {
-        float mp[3], lp[3];
-        f32x4 op[3][KD];
+        const float* part = reinterpret_cast<const float*>(smem) + lane * PF + h * (2 + 4 * KD);
         float mm = m[h];
 #pragma unroll
-        for (int p = 0; p < 3; ++p) {
-          const float* src =
-              reinterpret_cast<const float*>(smem) + (p * 64 + lane) * PF + h * (2 + 4 * KD);
-          mp[p] = src[0];
-          lp[p] = src[1];
-#pragma unroll
-          for (int kd = 0; kd < KD; ++kd)
-            op[p][kd] = f32x4{src[2 + kd * 4], src[3 + kd * 4], src[4 + kd * 4], src[5 + kd * 4]};
-          mm = fmaxf(mm, mp[p]);
-        }
+        for (int p = 0; p < NW - 1; ++p) mm = fmaxf(mm, part[p * 64 * PF]);
         // parts that saw only masked keys keep m = NEG_BIG and l = 0: factor 0
         const float f0 = __builtin_amdgcn_exp2f(m[h] - mm);
         float lsum = l[h] * f0;
 #pragma unroll
         for (int kd = 0; kd < KD; ++kd) o[h][kd] = o[h][kd] * f0;
 #pragma unroll
-        for (int p = 0; p < 3; ++p) {
-          const float f = __builtin_amdgcn_exp2f(mp[p] - mm);
-          lsum += lp[p] * f;
+        for (int p = 0; p < NW - 1; ++p) {
+          const float* src = part + p * 64 * PF;
+          const float f = __builtin_amdgcn_exp2f(src[0] - mm);
+          lsum += src[1] * f;
 #pragma unroll
-          for (int kd = 0; kd < KD; ++kd) o[h][kd] = o[h][kd] + op[p][kd] * f;
+          for (int kd = 0; kd < KD; ++kd)
+            o[h][kd] = o[h][kd] +
+                       f32x4{src[2 + kd * 4], src[3 + kd * 4], src[4 + kd * 4], src[5 + kd * 4]} * f;
         }
         l[h] = lsum;
       }
@@ -885,7 +886,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const shrimp_attn_args a, flo
 
   // Query rows past the live bound store zeros.
   const int dq4 = a.d / 4;
-  for (int i = qz == 0 ? tid : (S - L) * HG * dq4; i < (S - L) * HG * dq4; i += 256) {
+  for (int i = qz == 0 ? tid : (S - L) * HG * dq4; i < (S - L) * HG * dq4; i += NT) {
     const int row = L + i / (HG * dq4);
     const int rem = i - (row - L) * HG * dq4;
     const int h = rem / dq4;
@@ -904,20 +905,20 @@ static size_t attn_smem_bytes(int DP, int HG, int S, int npos, bool pair) {
   return bytes;
 }
 
-template <int DP, int HG, bool PAIR>
+template <int DP, int HG, bool PAIR, int NW>
 static int launch_attn(const shrimp_attn_args* a, float qk_scale, uint32_t qkv_bytes, int npos,
                        size_t smem, hipStream_t st) {
   // query splits (small batches): up to 4, doubling while the workgroups stay
   // within two per compute unit and each split keeps at least two rounds of
-  // four query blocks
+  // NW query blocks
   const int groups = a->H / HG * a->B;
-  const int rounds = ((a->S + 15) / 16) / 4;
+  const int rounds = ((a->S + 15) / 16) / NW;
   int z = 1;
   while (z < 4 && groups * z * 2 <= 2 * cu_count() && rounds >= 2 * z) z *= 2;
   dim3 grid(a->H / HG, a->B, z);
   const shrimp_attn_proj_args none{};
-  hipLaunchKernelGGL((attn_kernel<DP, HG, PAIR, 0>), grid, dim3(256), smem, st, *a, qk_scale,
-                     qkv_bytes, npos, none, 0u);
+  hipLaunchKernelGGL((attn_kernel<DP, HG, PAIR, 0, NW>), grid, dim3(64 * NW), smem, st, *a,
+                     qk_scale, qkv_bytes, npos, none, 0u);
   return check_launch("attn");
 }
 
@@ -931,9 +932,12 @@ static int dispatch_attn(const shrimp_attn_args* a, float qk_scale, uint32_t qkv
   if (a->dpad == DPV) {                                                                    \
     const size_t s2 = attn_smem_bytes(DPV, 2, a->S, tab_rows, PAIR);                       \
     const size_t s1 = attn_smem_bytes(DPV, 1, a->S, tab_rows, PAIR);                       \
-    if (a->H % 2 == 0 && s2 <= kAttnSmemCap && g_attn_variant == 0)                       \
-      return launch_attn<DPV, 2, PAIR>(a, qk_scale, qkv_bytes, npos, s2, st);             \
-    if (s1 <= kAttnSmemCap) return launch_attn<DPV, 1, PAIR>(a, qk_scale, qkv_bytes, npos, s1, st); \
+    if (a->H % 2 == 0 && s2 <= kAttnSmemCap && g_attn_variant != 1)                       \
+      return DPV == 16 && g_attn_variant == 0                                              \
+                 ? launch_attn<DPV, 2, PAIR, DPV == 16 ? 8 : 4>(a, qk_scale, qkv_bytes, npos, s2, st) \
+                 : launch_attn<DPV, 2, PAIR, 4>(a, qk_scale, qkv_bytes, npos, s2, st);     \
+    if (s1 <= kAttnSmemCap)                                                                \
+      return launch_attn<DPV, 1, PAIR, 4>(a, qk_scale, qkv_bytes, npos, s1, st);          \
     return set_error(SHRIMP_EINVAL, "attn: sequence %d too long for LDS staging", a->S);   \
   }
   SHRIMP_ATTN_DP(16)
@@ -1055,10 +1059,10 @@ extern "C" int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_pr
   dim3 grid(a->H / 2, a->B);
   // the XCD grouping needs whole groups of 8 positions (grid.x = 4 head pairs)
   if (a->B % 8 == 0)
-    hipLaunchKernelGGL((attn_kernel<16, 2, false, 2>), grid, dim3(256), smem, as_stream(stream),
+    hipLaunchKernelGGL((attn_kernel<16, 2, false, 2, 4>), grid, dim3(256), smem, as_stream(stream),
                        *a, qk_scale, 0u, w * w, *p, (uint32_t)xe);
   else
-    hipLaunchKernelGGL((attn_kernel<16, 2, false, 1>), grid, dim3(256), smem, as_stream(stream),
+    hipLaunchKernelGGL((attn_kernel<16, 2, false, 1, 4>), grid, dim3(256), smem, as_stream(stream),
                        *a, qk_scale, 0u, w * w, *p, (uint32_t)xe);
   return check_launch("attn_fused");
 }

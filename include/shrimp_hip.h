@@ -54,8 +54,9 @@ int shrimp_abi_version(void);
  * 3 = as 0 without the small-batch row split; other values only query.
  * Returns the previous setting. Process-wide.
  * shrimp_attn_variant: 0 = automatic (two heads per attention workgroup when
- * their K/V fit the LDS budget), 1 = one head per workgroup; other values
- * only query. Returns the previous setting. Process-wide.
+ * their K/V fit the LDS budget, on eight waves at padded head dim 16, else
+ * four), 1 = one head per workgroup, 2 = two heads on four waves; other
+ * values only query. Returns the previous setting. Process-wide.
  * shrimp_max_lds_per_block: LDS bytes one workgroup may allocate on the
  * current device (the staged conv needs (N + 1) * cin_pad * 2). */
 int shrimp_conv_variant(int variant);

@@ -51,6 +51,22 @@ def conv_variant(request):
         lib.shrimp_conv_variant(prev)
 
 
+@pytest.fixture(params=[0, 1, 2], ids=["auto", "one_head", "four_waves"])
+def attn_variant(request):
+    """Runs an attention test with the automatic kernel choice (two heads per
+    workgroup; eight waves at head dim 16), with one head per workgroup, and
+    with two heads on four waves."""
+
+    from shrimp import _lib
+
+    lib = _lib.load()
+    prev = lib.shrimp_attn_variant(request.param)
+    try:
+        yield request.param
+    finally:
+        lib.shrimp_attn_variant(prev)
+
+
 @pytest.fixture(scope="module")
 def conv_case():
     from shrimp import synthetic
@@ -510,24 +526,27 @@ def test_attn_mlp_pack_rejects_other_shapes():
                              z(64, 128), z(64), z(64)) is None
 
 
+# query-block counts 5, 4, 2 and 9, 9, 3: a leftover block split over four
+# waves (5), over four and over eight waves (9), and none
+@pytest.mark.parametrize("S,lens", [(70, [70, 61, 23]), (140, [140, 129, 33])])
 @pytest.mark.parametrize("d", [16, 32, 64])
-def test_attn_pair_op(d):
+def test_attn_pair_op(d, S, lens, attn_variant):
     torch.manual_seed(2)
-    B, H, S = 3, 4, 70
+    B, H = 3, 4
     q, k, v = (torch.randn(B, H, S, d) for _ in range(3))
     rows = 238
     table2 = torch.randn(rows, H) * 0.5
     table2[rows - 1] = -3.0e4
     pair = torch.randint(0, rows - 1, (B, S, S), dtype=torch.uint8)
     pair[1, :, 50:60] = rows - 1  # pad keys inside the bound
-    lens = torch.tensor([70, 61, 23], dtype=torch.int32)
+    lens = torch.tensor(lens, dtype=torch.int32)
     got = torch.ops.shrimp.attn_pair(q.to(DEV), k.to(DEV), v.to(DEV), pair.to(DEV),
                                      table2.to(DEV), lens.to(DEV))
     want = ofwd.attn_pair(bf(q), bf(k), bf(v), pair, table2.double(), lens)
     close(got, want, atol=1e-2, what=f"attn d={d}")
 
 
-def test_attn_offset_table_cfg2():
+def test_attn_offset_table_cfg2(attn_variant):
     from shrimp import ops, synthetic
 
     case = synthetic.attention_inputs(4, heads=8, d=16)
@@ -582,7 +601,7 @@ def _attn_block_ref(x, w, b, lnw, lnb, coords, mask, lens, table, H, eps=1e-5):
     # the longest sequence the kernel covers (20 blocks, 5 per wave)
     (320, [320, 300, 8 + 16 * 16 + 1], False),
 ])
-def test_attn_fused_matches_reference(S, lens, wide):
+def test_attn_fused_matches_reference(S, lens, wide, attn_variant):
     """LN1 -> q/k/v -> attention in one launch against a float64 restatement
     (tolerance 2e-2 + 2e-2 |want|: q/k/v, P and V are bf16, the offset table
     fp16), and against the q/k/v kernel followed by the attention kernel (which
