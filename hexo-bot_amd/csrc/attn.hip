@@ -92,6 +92,10 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
   const int NKB = SP / 16;
   const int M = a.lut_m;
   const int W = 2 * M + 1;
+  // this lane's K and V fragment slots of the chunk's first key block: the
+  // blocks of one head follow at 512-byte steps (immediate LDS offsets)
+  const unsigned short* kbase = s.Ks + kb0 * 256 + (lg * 16 + lr) * 4;
+  const unsigned short* vbase = s.Vt + kb0 * 256 + (lg * 16 + lr) * 4;
   f32x4 sc4[HG][NBK];
 #pragma unroll
   for (int kb = 0; kb < NBK; ++kb)
@@ -100,8 +104,7 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
       f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd) {
-        const u32x2 kf = *reinterpret_cast<const u32x2*>(
-            s.Ks + ((h * KD + kd) * NKB + kb0 + kb) * 256 + (lg * 16 + lr) * 4);
+        const u32x2 kf = *reinterpret_cast<const u32x2*>(kbase + (h * KD + kd) * NKB * 256 + kb * 256);
         acc = mfma16x16x16(kf, qf[h][kd], acc);
       }
       sc4[h][kb] = acc;
@@ -220,8 +223,7 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
       lacc = mfma16x16x16(ones, pf[0], lacc);
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd) {
-        const u32x2 vf = *reinterpret_cast<const u32x2*>(
-            s.Vt + ((h * KD + kd) * NKB + kb0) * 256 + (lg * 16 + lr) * 4);
+        const u32x2 vf = *reinterpret_cast<const u32x2*>(vbase + (h * KD + kd) * NKB * 256);
         acc[kd] = mfma16x16x16(vf, pf[0], acc[kd]);
       }
     } else {
@@ -237,7 +239,7 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
         lacc = mfma16x16x32(ones, pp, lacc);
 #pragma unroll
         for (int kd = 0; kd < KD; ++kd) {
-          const unsigned short* vf = s.Vt + ((h * KD + kd) * NKB + kb0 + kp) * 256 + (lg * 16 + lr) * 4;
+          const unsigned short* vf = vbase + (h * KD + kd) * NKB * 256 + kp * 256;
           const u32x2 v0 = *reinterpret_cast<const u32x2*>(vf);
           const u32x2 v1 = *reinterpret_cast<const u32x2*>(vf + 256);
           acc[kd] = mfma16x16x32(u32x4{v0.x, v0.y, v1.x, v1.y}, pp, acc[kd]);
