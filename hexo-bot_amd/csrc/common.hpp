@@ -107,22 +107,13 @@ SHRIMP_DEV float sum_groups_swap(float x) {
   const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
-// The lane swaps' results feed v_max_f32 directly: fmaxf would first
-// canonicalise both operands (two more VALU instructions per step). The
-// values are finite scores, so IEEE NaN quieting has nothing to do.
-SHRIMP_DEV float vmax_raw(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-
 SHRIMP_DEV float max_groups_swap(float x) {
   const unsigned u = __float_as_uint(x);
   const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  const float y = vmax_raw(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const unsigned v = __float_as_uint(y);
   const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return vmax_raw(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 // ---- LayerNorm of 16 rows of 128 channels, MFMA operand layout ------------------
