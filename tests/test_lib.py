@@ -145,6 +145,26 @@ def test_bad_arguments_fail_with_message(lib):
     assert b"corb=12" in lib.shrimp_last_error()
 
 
+def test_variant_switches(lib):
+    """Process-wide kernel switches: valid values are set and return the
+    previous one, others only query (attention: 0 auto, 1 one head, 2 two heads
+    on four waves)."""
+    prev = lib.shrimp_attn_variant(2)
+    try:
+        assert lib.shrimp_attn_variant(3) == 2  # out of range: query only
+        assert lib.shrimp_attn_variant(-1) == 2
+        assert lib.shrimp_attn_variant(1) == 2
+        assert lib.shrimp_attn_variant(-1) == 1
+    finally:
+        lib.shrimp_attn_variant(prev)
+    prev = lib.shrimp_conv_variant(3)
+    try:
+        assert lib.shrimp_conv_variant(4) == 3
+        assert lib.shrimp_conv_variant(-1) == 3
+    finally:
+        lib.shrimp_conv_variant(prev)
+
+
 def test_missing_library_raises(tmp_path):
     with pytest.raises(_lib.HipLibraryMissing):
         _lib.load(tmp_path / "nope.so")
