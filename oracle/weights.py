@@ -13,6 +13,11 @@ LayerNorm 1 / 0; tokens N(0, 0.02); bias tables 0; LayerScale 1e-4.
 spirit of tests/test_shrimp_model.py:45-57: LayerNorm weights U(0.5, 1.5) and
 biases N(0, 0.1), Linear biases N(0, 0.02), out_proj / fc2 N(0, 0.05),
 bias tables N(0, 0.5), LayerScale U(0.5, 1.0).
+``mode="heads"``: as "parity", with the serve heads' Linear weights N(0,
+1 / fan_in) for the value / moves-left reduction and head and N(0, 1 / (4
+fan_in)) for the policy head, so value logits are O(1) and policy logits
+O(0.5): an absolute logit gate then sees an error in the trunk (with std
+0.02 heads the logits are O(0.05) and a 2e-2 gate cannot).
 """
 
 from __future__ import annotations
@@ -27,6 +32,8 @@ NUM_TOKENS = 8
 VALUE_BINS = 65
 BIAS_ROWS = 237
 STV_HORIZONS = (2, 6, 16)
+# Linear layers of the serve heads (model.py:990-1020): O(1) weights in "heads" mode.
+SERVE_HEADS = ("policy_head", "value_reduction", "value_head", "ml_reduction", "moves_left_head")
 
 
 def param_shapes(channels: int, heads: int, layout: str) -> dict:
@@ -92,7 +99,7 @@ def param_shapes(channels: int, heads: int, layout: str) -> dict:
 
 def make_state_dict(channels: int, heads: int, layout: str, seed: int = 0,
                     mode: str = "parity") -> dict:
-    if mode not in ("parity", "fresh"):
+    if mode not in ("parity", "fresh", "heads"):
         raise ValueError(mode)
     out = {}
     for key, (shape, kind) in param_shapes(channels, heads, layout).items():
@@ -104,20 +111,22 @@ def make_state_dict(channels: int, heads: int, layout: str, seed: int = 0,
             bound = 1.0 / np.sqrt(7 * cin)
             v = rng.uniform(-bound, bound, size=shape)
         elif kind == "lin_w":
-            std = 0.05 if (mode == "parity" and (".out_proj." in key or ".fc2." in key)) else 0.02
+            std = 0.05 if (mode != "fresh" and (".out_proj." in key or ".fc2." in key)) else 0.02
+            if mode == "heads" and key.split(".")[0] in SERVE_HEADS:
+                std = (0.5 if key.startswith("policy_head.") else 1.0) / np.sqrt(shape[1])
             v = rng.normal(0.0, std, size=shape)
         elif kind == "lin_b":
-            v = rng.normal(0.0, 0.02, size=shape) if mode == "parity" else np.zeros(shape)
+            v = rng.normal(0.0, 0.02, size=shape) if mode != "fresh" else np.zeros(shape)
         elif kind == "ln_w":
-            v = rng.uniform(0.5, 1.5, size=shape) if mode == "parity" else np.ones(shape)
+            v = rng.uniform(0.5, 1.5, size=shape) if mode != "fresh" else np.ones(shape)
         elif kind == "ln_b":
-            v = rng.normal(0.0, 0.1, size=shape) if mode == "parity" else np.zeros(shape)
+            v = rng.normal(0.0, 0.1, size=shape) if mode != "fresh" else np.zeros(shape)
         elif kind == "gamma":
-            v = rng.uniform(0.5, 1.0, size=shape) if mode == "parity" else np.full(shape, 1e-4)
+            v = rng.uniform(0.5, 1.0, size=shape) if mode != "fresh" else np.full(shape, 1e-4)
         elif kind == "tokens":
             v = rng.normal(0.0, 0.02, size=shape)
         elif kind == "table":
-            v = rng.normal(0.0, np.sqrt(0.5), size=shape) if mode == "parity" else np.zeros(shape)
+            v = rng.normal(0.0, np.sqrt(0.5), size=shape) if mode != "fresh" else np.zeros(shape)
         else:  # pragma: no cover
             raise AssertionError(kind)
         out[key] = torch.from_numpy(np.asarray(v, dtype=np.float32))

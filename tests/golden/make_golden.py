@@ -137,7 +137,7 @@ def save_forward(path, c, h, layout, seed_pos, count, kmax, wseed, with_fresh):
     batch = collate_rows(rows, pad_to=256)
     args = (batch["feats"], batch["nbr"], batch["mask"], batch["coords"])
     out = {}
-    for mode, ws in (("parity", wseed), ("fresh", wseed + 1)):
+    for mode, ws in (("parity", wseed), ("fresh", wseed + 1), ("heads", wseed + 2)):
         if mode == "fresh" and not with_fresh:
             continue
         net = net_with(W.make_state_dict(c, h, layout, seed=ws, mode=mode), c, h, layout)

@@ -290,7 +290,8 @@ def test_hex_conv_multi_tile_positions(c, conv_variant):
 
 
 def test_conv_variants_agree_at_full_shape():
-    """At config 1's real shape (B=512, Npad=256): the global-gather and the
+    """At config 1's row shape (Npad=256, C=128) with B=512 positions (config
+    1 itself, B=1024, is test_cfg1_conv_bias_relu): the global-gather and the
     staged kernels issue the same MFMA sequence on the same operands
     (bit-identical outputs); the big-tile kernel sums the same products in
     another order (channel chunk before tap), so it agrees to fp32 rounding:
@@ -682,3 +683,153 @@ def test_decode_kernel(golden):
     want = torch.cat([torch.softmax(pol[i, : legal[i]].double(), 0) for i in range(B)])
     assert torch.allclose(pri.cpu().double(), want, atol=1e-6)
     assert torch.equal(lg.cpu(), torch.cat([pol[i, : legal[i]] for i in range(B)]))
+
+
+# ---- configs 1-3 at their own shapes ---------------------------------------------------
+
+
+def _sample_rows(B):
+    return [0, 1, B // 2, B - 1]
+
+
+@pytest.fixture(scope="module")
+def cfg1_full():
+    from shrimp import synthetic
+
+    return synthetic.conv_inputs(1024, channels=128)
+
+
+@pytest.mark.parametrize("B", [4, 1024])
+def test_cfg1_conv_bias_relu(cfg1_full, B, conv_variant):
+    """Config 1's op: 7-tap gather-GEMM with the fused bias + ReLU + mask
+    epilogue (no LayerNorm), at B=4 and at config 1's own B=1024: finite, pad
+    rows exactly zero, sampled positions against the oracle, and (B=1024) the
+    sampled positions equal to a sub-batch run of the same kernel choice."""
+
+    from shrimp import ops
+
+    b = cfg1_full["batch"]
+    x = torch.from_numpy(cfg1_full["x"][:B])
+    w = torch.from_numpy(cfg1_full["w"])
+    bias = torch.from_numpy(cfg1_full["bias"])
+    gidx = _gidx(b)[:B].contiguous()
+    mask = b["mask"][:B].contiguous()
+    N = mask.shape[1]
+    wp = ops.pack_conv_weight(w.to(DEV))
+    bd = bias.to(DEV)
+
+    def run(rows):
+        xd = x[rows].to(DEV, torch.bfloat16).contiguous()
+        out = torch.full((len(rows), N, 128), 3.0, dtype=torch.bfloat16, device=DEV)
+        ops.launch_conv(x=xd, x_sb=N * 128, x_sn=128, idx=gidx[rows].to(DEV, torch.int32).contiguous(),
+                        taps=7, idx_stride=7, mask8=mask[rows].to(DEV, torch.uint8).contiguous(),
+                        wpack=wp, bias=bd, B=len(rows), N=N, cin_pad=128, cout=128, relu=True,
+                        out=out, o_sb=N * 128, o_sn=128)
+        return out.cpu()
+
+    print(f"cfg1 conv bias+relu B={B}", flush=True)
+    full = run(list(range(B)))
+    assert torch.isfinite(full.float()).all()
+    assert (full[~mask] == 0).all()
+    assert (full.float() >= 0).all()
+    rows = _sample_rows(B)
+    want = torch.relu(ofwd.hex_conv(bf(x[rows]), gidx[rows], mask[rows], bf(w), bias.double()))
+    close(full[rows], want, what=f"cfg1 B={B}")
+    if B > 4:
+        assert torch.equal(full[rows], run(rows))
+
+
+@pytest.fixture(scope="module")
+def cfg2_full():
+    from shrimp import synthetic
+
+    return synthetic.attention_inputs(1024, heads=8, d=16)
+
+
+def test_cfg2_attention_full_shape(cfg2_full, attn_variant):
+    """Config 2's op at its own shape (B=1024, H=8, L=256, d=16, lengths
+    U[64, 256], 33x33 per-head offset table): finite, rows past each length
+    exactly zero, sampled positions against the oracle (attn_offset_table,
+    pinned against the reference's pair rows), and equal to a sub-batch run."""
+
+    from shrimp import ops
+
+    c = cfg2_full
+    q, k, v = (torch.from_numpy(c[n]) for n in ("q", "k", "v"))
+    B, H, S, d = q.shape
+    table = torch.from_numpy(c["table"])
+    btab = (torch.cat([table, torch.zeros(3, H)]) * (1.0 / math.log(2.0))).to(DEV).contiguous()
+    coords, mask, lens = (torch.from_numpy(c[n]) for n in ("coords", "mask", "lens"))
+
+    def run(rows):
+        n = len(rows)
+        qd, kd, vd = (t[rows].to(DEV, torch.bfloat16).contiguous() for t in (q, k, v))
+        out = torch.full((n, H, S, d), 5.0, dtype=torch.bfloat16, device=DEV)
+        ops.launch_attn(
+            q=qd, k=kd, v=vd, qkv_sb=H * S * d, qkv_sh=S * d, seq_lens=lens[rows].to(DEV), o=out,
+            o_sb=H * S * d, o_sh=S * d, o_sr=d, B=n, S=S, H=H, d=d, dpad=16,
+            coords=coords[rows].to(DEV, torch.int32).contiguous(),
+            mask8=mask[rows].to(DEV, torch.uint8).contiguous(), btab=btab, lut_m=16, n_tokens=0,
+        )
+        return out.cpu()
+
+    print(f"cfg2 attention B={B}", flush=True)
+    full = run(list(range(B)))
+    assert torch.isfinite(full.float()).all()
+    for i in range(B):
+        assert (full[i, :, int(lens[i]):] == 0).all(), i
+    rows = _sample_rows(B)
+    want = ofwd.attn_offset_table(bf(q[rows]), bf(k[rows]), bf(v[rows]), coords[rows], mask[rows],
+                                  table.double(), 16)
+    close(full[rows], want, atol=1e-2, what="cfg2 B=1024")
+    assert torch.equal(full[rows], run(rows))
+
+
+@pytest.fixture(scope="module")
+def cfg3_full():
+    from shrimp import synthetic
+
+    return synthetic.raytap_inputs(1024, channels=128)
+
+
+def test_cfg3_raytap_full_shape(cfg3_full):
+    """Config 3's op at its own shape (B=1024, L=256, C=128, 31 independent
+    taps over the 32-slot ray index built on the device): finite, pad rows
+    exactly zero, sampled positions against the oracle's 31-tap conv, and
+    equal to a sub-batch run."""
+
+    from shrimp import _lib, ops
+
+    c = cfg3_full
+    b = c["batch"]
+    B, N = b["mask"].shape
+    x, w, bias = (torch.from_numpy(c[k]) for k in ("x", "w", "bias"))
+    coords = b["coords"].to(torch.int32)
+    mask = b["mask"]
+    lib = _lib.load()
+    wp = ops.pack_conv_weight(w.to(DEV))
+    bd = bias.to(DEV)
+
+    def run(rows):
+        n = len(rows)
+        c32 = coords[rows].to(DEV).contiguous()
+        m8 = mask[rows].to(DEV, torch.uint8).contiguous()
+        idx = torch.empty(n, N, 32, dtype=torch.int32, device=DEV)
+        _lib.check(lib.shrimp_build_ray_index(c32.data_ptr(), m8.data_ptr(), n, N, idx.data_ptr(),
+                                              _lib.stream_handle()), "ray")
+        out = torch.full((n, N, 128), 3.0, dtype=torch.bfloat16, device=DEV)
+        ops.launch_conv(x=x[rows].to(DEV, torch.bfloat16).contiguous(), x_sb=N * 128, x_sn=128,
+                        idx=idx, taps=31, idx_stride=32, mask8=m8, wpack=wp, bias=bd, B=n, N=N,
+                        cin_pad=128, cout=128, out=out, o_sb=N * 128, o_sn=128)
+        return out.cpu(), idx.cpu()
+
+    print(f"cfg3 raytap B={B}", flush=True)
+    full, idx = run(list(range(B)))
+    assert torch.isfinite(full.float()).all()
+    assert (full[~mask] == 0).all()
+    rows = _sample_rows(B)
+    ridx = torch.from_numpy(tables.ray_index(coords[rows].numpy(), mask[rows].numpy()))
+    assert torch.equal(idx[rows], ridx)
+    want = ofwd.raytap_conv(bf(x[rows]), ridx, mask[rows], bf(w), bias.double())
+    close(full[rows], want, what="cfg3 B=1024")
+    assert torch.equal(full[rows], run(rows)[0])

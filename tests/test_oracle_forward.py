@@ -11,6 +11,8 @@ import torch.nn.functional as F
 
 from oracle import decode, forward, tables, weights
 
+from gates import LOGIT_TOL, TRUNK_MEAN
+
 
 def _fwd(g, mode, **kw):
     c, h = (int(x) for x in g["arch"])
@@ -23,7 +25,8 @@ def _fwd(g, mode, **kw):
 
 
 @pytest.mark.parametrize("name,mode", [("forward_cfg0", "parity"), ("forward_cfg0", "fresh"),
-                                       ("forward_cfg4", "parity")])
+                                       ("forward_cfg0", "heads"), ("forward_cfg4", "parity"),
+                                       ("forward_cfg4", "heads")])
 def test_forward_matches_reference_golden(golden, name, mode):
     g = golden(name)
     out = _fwd(g, mode)
@@ -36,6 +39,58 @@ def test_forward_matches_reference_golden(golden, name, mode):
     # pad logits are exactly zero
     mask = torch.from_numpy(g["mask"])
     assert (out["policy"][~mask] == 0).all()
+
+
+def _mutations(sd):
+    """Composition mistakes a forward could make with correct kernels: a block
+    reading a zeroed, another block's or a head-permuted bias table, and a
+    skipped attention sub-block."""
+
+    out = {}
+    s = dict(sd)
+    s["bias_tables.0"] = torch.zeros_like(s["bias_tables.0"])
+    out["zeroed table 0"] = s
+    s = dict(sd)
+    s["bias_tables.0"] = s["bias_tables.0"].flip(1)
+    out["heads of table 0 reversed"] = s
+    s = dict(sd)
+    s["bias_tables.3"] = s["bias_tables.3"].roll(1, 1)
+    out["heads of table 3 rotated"] = s
+    s = dict(sd)
+    s["bias_tables.0"], s["bias_tables.1"] = s["bias_tables.1"], s["bias_tables.0"]
+    out["tables 0 and 1 swapped"] = s
+    s = dict(sd)
+    s["attn_blocks.0.ls_attn.gamma"] = torch.zeros_like(s["attn_blocks.0.ls_attn.gamma"])
+    out["attention sub-block 0 skipped"] = s
+    return out
+
+
+@pytest.mark.parametrize("mode", ["parity", "heads"])
+def test_trunk_gates_see_composition_mistakes(golden, mode):
+    """The GPU forward tests gate the trunk output's tokens at TRUNK_MEAN (mean
+    absolute error) and, with O(1) heads, the value logits at LOGIT_TOL. Each
+    composition mistake moves the fp32 reference by at least twice a gate, so
+    a forward that made it fails the GPU test even with exact kernels."""
+
+    g = golden("forward_cfg4")
+    c, h = (int(x) for x in g["arch"])
+    layout = str(g["layout"])
+    sd = weights.make_state_dict(c, h, layout, seed=int(g[f"{mode}_seed"]), mode=mode)
+    args = (g["feats"], g["nbr"], g["mask"], g["coords"])
+
+    def run(d):
+        return forward.forward_policy_value(d, layout, h, *args, request_moves_left=True,
+                                            return_trunk=True, dtype=torch.float32)
+
+    base = run(sd)
+    for name, bad in _mutations(sd).items():
+        o = run(bad)
+        tok = (o["tokens"] - base["tokens"]).abs().mean().item()
+        val = (o["value"] - base["value"]).abs().max().item()
+        print(f"{mode} {name}: tokens mean {tok:.4f}, value max {val:.4f}")
+        assert tok >= 2 * TRUNK_MEAN, name
+        if mode == "heads":
+            assert val >= 2 * LOGIT_TOL, name
 
 
 def test_forward_fp32_close_to_fp64(golden):
@@ -118,6 +173,54 @@ def test_attention_equals_sdpa():
     bias = torch.randn(2, 3, 20, 20, dtype=torch.float64)
     want = F.scaled_dot_product_attention(q, k, v, attn_mask=bias)
     assert torch.allclose(forward.attention(q, k, v, bias), want, atol=1e-12)
+
+
+def _pair_case(golden, b, compact):
+    """Live cells of golden position b (all of them, or those with |q|, |r| <= 8
+    so every offset lies within +-16), their coordinates, and the reference's
+    pair rows between them (pair.npz, written by _build_pair_u8)."""
+
+    g = golden("pair")
+    coords, mask, pair = g["coords"][b], g["mask"][b], g["pair_u8"][b]
+    sel = np.flatnonzero(mask)
+    if compact:
+        sel = sel[(np.abs(coords[sel]) <= 8).all(1)]
+    return coords[sel], pair[np.ix_(8 + sel, 8 + sel)]
+
+
+@pytest.mark.parametrize("m", [17, 16])
+@pytest.mark.parametrize("b", [0, 3])
+def test_attn_offset_table_matches_reference_pair_rows(golden, m, b):
+    """attn_offset_table (config 2's attention) against the reference's own
+    pair rows: with the per-offset table T[(dq + m)(2m + 1) + dr + m] =
+    table[lut(dq, dr)] it must equal attn_pair with table[pair[i, j]], where
+    pair comes from the reference's _build_pair_u8 (key - query offsets, the
+    35x35 LUT clamped at 17). m = 17 covers whole boards (offsets up to 26:
+    the clamp); m = 16, config 2's table, covers compact cell sets. A swap of
+    dq and dr, or query - key instead of key - query, fails (checked below by
+    transposing or negating the coordinates)."""
+
+    coords, pair = _pair_case(golden, b, compact=(m == 16))
+    n = coords.shape[0]
+    hd, d = 3, 4
+    rng = np.random.default_rng(10 * b + m)
+    table = torch.from_numpy(rng.normal(0, 0.8, size=(tables.BIAS_ROWS, hd)))
+    lut35 = tables.cell_lut()  # (35 * 35,) rows, offsets clamped to +-17
+    w = 2 * m + 1
+    off = np.arange(-m, m + 1)
+    dq, dr = np.meshgrid(off, off, indexing="ij")
+    t = table[torch.from_numpy(lut35[(dq.ravel() + 17) * 35 + dr.ravel() + 17].astype(np.int64))]
+    assert t.shape == (w * w, hd)
+    q, k, v = (torch.from_numpy(rng.standard_normal((1, hd, n, d))) for _ in range(3))
+    live = torch.ones(1, n, dtype=torch.bool)
+    got = forward.attn_offset_table(q, k, v, torch.from_numpy(coords)[None], live, t, m)
+    tab2 = torch.cat([table, torch.full((1, hd), -3.0e4, dtype=table.dtype)])
+    want = forward.attn_pair(q, k, v, torch.from_numpy(pair.astype(np.int64))[None], tab2,
+                             torch.tensor([n]))
+    assert torch.allclose(got, want, atol=1e-12)
+    for wrong in (coords[:, ::-1].copy(), -coords):
+        bad = forward.attn_offset_table(q, k, v, torch.from_numpy(wrong)[None], live, t, m)
+        assert (bad - want).abs().max().item() > 1e-2
 
 
 def test_attn_pair_masks_keys_and_rows():
