@@ -5,6 +5,8 @@
 #include "capi.hpp"
 #include "common.hpp"
 
+#include <mutex>
+
 namespace shrimp {
 
 // Typed loads for the flat preparation loops (the element type is chosen once,
@@ -592,10 +594,10 @@ extern "C" int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void
   return check_launch("fill_tokens");
 }
 
-extern "C" int shrimp_trunk_tail(const shrimp_tail_args* a, void* stream) {
-  SHRIMP_REQUIRE(a != nullptr, "trunk_tail: null args");
-  if (a->B == 0) return SHRIMP_OK;
-  SHRIMP_REQUIRE(a->seq && a->mask && a->ln_w && a->ln_b && a->out_seq && a->workspace,
+// Checks the tail arguments (all but the workspace) and launches the two
+// passes with the head inputs in `ws` ((B, 6C) fp32, device memory).
+static int launch_trunk_tail(const shrimp_tail_args* a, float* ws, hipStream_t st) {
+  SHRIMP_REQUIRE(a->seq && a->mask && a->ln_w && a->ln_b && a->out_seq,
                  "trunk_tail: null pointer");
   SHRIMP_REQUIRE(a->C > 0 && a->C <= 256 && a->C % 2 == 0, "trunk_tail: C %d outside (0, 256]",
                  a->C);
@@ -607,22 +609,73 @@ extern "C" int shrimp_trunk_tail(const shrimp_tail_args* a, void* stream) {
   SHRIMP_REQUIRE(a->C % 8 == 0 && a->C <= 256 && a->s_sb % 8 == 0,
                  "trunk_tail: C %d must be a multiple of 8 (<= 256), position stride of 8", a->C);
   SHRIMP_REQUIRE(a->bins > 0 && a->bins <= 256, "trunk_tail: bins %d", a->bins);
-  hipStream_t st = as_stream(stream);
-  const int tpr = a->C / 8;
+  shrimp_tail_args k = *a;
+  k.workspace = ws;
+  const int tpr = k.C / 8;
   const size_t lsm = (size_t)(256 / ((tpr <= 4) ? 4 : (tpr <= 8) ? 8 : (tpr <= 16) ? 16 : 32)) *
-                     (a->C + 1) * sizeof(float);
-  if (tpr <= 4) hipLaunchKernelGGL(final_ln_kernel<4>, dim3(a->B), dim3(256), lsm, st, *a);
-  else if (tpr <= 8) hipLaunchKernelGGL(final_ln_kernel<8>, dim3(a->B), dim3(256), lsm, st, *a);
-  else if (tpr <= 16) hipLaunchKernelGGL(final_ln_kernel<16>, dim3(a->B), dim3(256), lsm, st, *a);
-  else hipLaunchKernelGGL(final_ln_kernel<32>, dim3(a->B), dim3(256), lsm, st, *a);
+                     (k.C + 1) * sizeof(float);
+  if (tpr <= 4) hipLaunchKernelGGL(final_ln_kernel<4>, dim3(k.B), dim3(256), lsm, st, k);
+  else if (tpr <= 8) hipLaunchKernelGGL(final_ln_kernel<8>, dim3(k.B), dim3(256), lsm, st, k);
+  else if (tpr <= 16) hipLaunchKernelGGL(final_ln_kernel<16>, dim3(k.B), dim3(256), lsm, st, k);
+  else hipLaunchKernelGGL(final_ln_kernel<32>, dim3(k.B), dim3(256), lsm, st, k);
   if (int rc = check_launch("trunk_tail/ln")) return rc;
-  if (!a->value && !a->moves_left) return SHRIMP_OK;
-  const int ks1 = kHeadThreads / a->C, ks2 = kHeadThreads / a->bins;
-  const size_t smem = ((size_t)kHeadPos * 3 * a->C + (size_t)ks1 * kHeadPos * a->C +
-                       (size_t)kHeadPos * a->C + (size_t)ks2 * kHeadPos * a->bins) * sizeof(float);
-  hipLaunchKernelGGL(value_head_kernel, dim3((a->B + kHeadPos - 1) / kHeadPos, 2),
-                     dim3(kHeadThreads), smem, st, *a);
+  if (!k.value && !k.moves_left) return SHRIMP_OK;
+  const int ks1 = kHeadThreads / k.C, ks2 = kHeadThreads / k.bins;
+  const size_t smem = ((size_t)kHeadPos * 3 * k.C + (size_t)ks1 * kHeadPos * k.C +
+                       (size_t)kHeadPos * k.C + (size_t)ks2 * kHeadPos * k.bins) * sizeof(float);
+  hipLaunchKernelGGL(value_head_kernel, dim3((k.B + kHeadPos - 1) / kHeadPos, 2),
+                     dim3(kHeadThreads), smem, st, k);
   return check_launch("trunk_tail/heads");
+}
+
+// ---- the allocation-free tail ---------------------------------------------------
+// The head inputs of shrimp_trunk_tail_noalloc live in this fixed array, one
+// copy per device, held until the process ends. Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the symbol):
+// the device address comes from hipGetSymbolAddress, once per device with that
+// device current, and is kept in scratch_dev.
+static __device__ __align__(256) float scratch[SHRIMP_TAIL_SCRATCH_FLOATS];
+
+constexpr int kMaxDevices = 64;
+static std::mutex scratch_mu;
+static float* scratch_dev[kMaxDevices];
+
+static int scratch_of_current_device(float** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(SHRIMP_ELAUNCH, "trunk_tail_noalloc: no current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(SHRIMP_ELAUNCH, "trunk_tail_noalloc: hipGetSymbolAddress: %s",
+                       hipGetErrorString(e));
+    scratch_dev[dev] = static_cast<float*>(p);
+  }
+  *out = scratch_dev[dev];
+  return SHRIMP_OK;
+}
+
+extern "C" int shrimp_trunk_tail(const shrimp_tail_args* a, void* stream) {
+  SHRIMP_REQUIRE(a != nullptr, "trunk_tail: null args");
+  if (a->B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(a->workspace, "trunk_tail: null workspace");
+  return launch_trunk_tail(a, a->workspace, as_stream(stream));
+}
+
+extern "C" int shrimp_trunk_tail_noalloc(const shrimp_tail_args* a, void* stream) {
+  SHRIMP_REQUIRE(a != nullptr, "trunk_tail_noalloc: null args");
+  if (a->B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(a->B > 0 && a->C > 0, "trunk_tail_noalloc: bad shape (B %d, C %d)", a->B, a->C);
+  const int64_t need = (int64_t)a->B * 6 * a->C;
+  SHRIMP_REQUIRE(need <= (int64_t)SHRIMP_TAIL_SCRATCH_FLOATS,
+                 "trunk_tail_noalloc: B * 6 * C = %lld floats exceeds the fixed scratch of %d "
+                 "floats (use shrimp_trunk_tail with a workspace)",
+                 (long long)need, (int)SHRIMP_TAIL_SCRATCH_FLOATS);
+  float* ws = nullptr;
+  if (int rc = scratch_of_current_device(&ws)) return rc;
+  return launch_trunk_tail(a, ws, as_stream(stream));
 }
 
 extern "C" int shrimp_decode(const float* value_logits, const float* ml_logits,

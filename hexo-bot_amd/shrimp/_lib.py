@@ -170,6 +170,7 @@ SIGNATURES: dict = {
         ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _i64, ctypes.c_int, _vp]
     ),
     "shrimp_trunk_tail": (ctypes.c_int, [ctypes.POINTER(TailArgs), _vp]),
+    "shrimp_trunk_tail_noalloc": (ctypes.c_int, [ctypes.POINTER(TailArgs), _vp]),
     "shrimp_decode": (
         ctypes.c_int,
         [_vp, _vp, _vp, _i64, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_float]

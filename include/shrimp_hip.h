@@ -428,6 +428,18 @@ typedef struct {
 
 int shrimp_trunk_tail(const shrimp_tail_args* a, void* stream);
 
+/* shrimp_trunk_tail without a workspace: no counterpart in the reference. It
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serve loops, harnesses that forbid hipMalloc). The head
+ * inputs live in a fixed device array of SHRIMP_TAIL_SCRATCH_FLOATS floats
+ * (8 MiB) that the library holds on each device it runs on until the process
+ * ends; a->workspace is ignored. Requires B * 6 * C <= SHRIMP_TAIL_SCRATCH_FLOATS
+ * (else SHRIMP_EINVAL, nothing launched). Calls on one device share that
+ * array: calls that overlap in time on one device (other streams, other host
+ * threads) race and must be serialised by the caller. Allocates nothing. */
+#define SHRIMP_TAIL_SCRATCH_FLOATS (2 * 1024 * 1024)
+int shrimp_trunk_tail_noalloc(const shrimp_tail_args* a, void* stream);
+
 /* ------------------------------------------------------------------------
  * Serve decode (inference.py:998-1042, losses.py:40-60):
  *   value[b] = clamp(sum softmax(value_logits[b]) * linspace(-1,1,bins), -1, 1)
