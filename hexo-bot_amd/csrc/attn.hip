@@ -924,12 +924,17 @@ static int launch_attn(const shrimp_attn_args* a, float qk_scale, uint32_t qkv_b
   return check_launch("attn");
 }
 
-// LDS budget per workgroup kept at 64 KiB so several groups share a CU.
+// LDS budget per workgroup kept at 64 KiB so several groups share a CU;
+// sequences too long for it take one head per workgroup with up to the
+// device's per-workgroup LDS, and longer ones the chunked kernel of f32.hip
+// (keys streamed through LDS, one query row per thread).
 static const size_t kAttnSmemCap = 64 * 1024;
+int attn_rows_bf16(const shrimp_attn_args* a, hipStream_t st);
 
 template <bool PAIR>
 static int dispatch_attn(const shrimp_attn_args* a, float qk_scale, uint32_t qkv_bytes, int npos,
                          int tab_rows, hipStream_t st) {
+  if (g_attn_variant == 3) return attn_rows_bf16(a, st);
 #define SHRIMP_ATTN_DP(DPV)                                                                \
   if (a->dpad == DPV) {                                                                    \
     const size_t s2 = attn_smem_bytes(DPV, 2, a->S, tab_rows, PAIR);                       \
@@ -938,9 +943,9 @@ static int dispatch_attn(const shrimp_attn_args* a, float qk_scale, uint32_t qkv
       return DPV == 16 && g_attn_variant == 0                                              \
                  ? launch_attn<DPV, 2, PAIR, DPV == 16 ? 8 : 4>(a, qk_scale, qkv_bytes, npos, s2, st) \
                  : launch_attn<DPV, 2, PAIR, 4>(a, qk_scale, qkv_bytes, npos, s2, st);     \
-    if (s1 <= kAttnSmemCap)                                                                \
+    if (s1 <= kAttnSmemCap || s1 <= (size_t)max_lds_per_block())                          \
       return launch_attn<DPV, 1, PAIR, 4>(a, qk_scale, qkv_bytes, npos, s1, st);          \
-    return set_error(SHRIMP_EINVAL, "attn: sequence %d too long for LDS staging", a->S);   \
+    return attn_rows_bf16(a, st);                                                          \
   }
   SHRIMP_ATTN_DP(16)
   SHRIMP_ATTN_DP(32)

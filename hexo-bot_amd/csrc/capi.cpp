@@ -61,7 +61,7 @@ extern "C" int shrimp_conv_variant(int variant) {
 
 extern "C" int shrimp_attn_variant(int variant) {
   const int prev = shrimp::g_attn_variant;
-  if (variant >= 0 && variant <= 2) shrimp::g_attn_variant = variant;
+  if (variant >= 0 && variant <= 3) shrimp::g_attn_variant = variant;
   return prev;
 }
 

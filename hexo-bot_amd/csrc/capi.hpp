@@ -35,7 +35,9 @@ int cu_count();
 // small-batch row split.
 extern int g_conv_variant;
 // Attention: 0 = automatic (two heads per workgroup when they fit), 1 = one
-// head per workgroup.
+// head per workgroup, 2 = two heads on four waves, 3 = the chunked kernel
+// (keys streamed through LDS; otherwise used only for sequences that do not
+// fit one workgroup's LDS).
 extern int g_attn_variant;
 
 }  // namespace shrimp

@@ -208,7 +208,8 @@ __global__ void fill_tokens_kernel(const float* __restrict__ tokens, int n_token
 // [T4 | T5 | pooled] go to the workspace (B, 6C) fp32.
 // A row is handled by TPR = C / 8 lanes (16 bytes each), 256 / TPR rows per
 // pass, four passes in flight; row statistics reduce over the TPR lanes.
-template <int TPR>
+// F32: seq and out_seq hold fp32 rows instead of bf16 (the fp32 serve mode).
+template <int TPR, bool F32>
 __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a) {
   constexpr int RPP = 256 / TPR;  // rows per pass
   constexpr int U = 4;            // passes in flight
@@ -222,6 +223,8 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a)
   const bool cv = c0 < C;
   const uint16_t* seq = static_cast<const uint16_t*>(a.seq) + (int64_t)b * a.s_sb;
   uint16_t* outs = static_cast<uint16_t*>(a.out_seq) + (int64_t)b * a.s_sb;
+  const float* seq32 = static_cast<const float*>(a.seq) + (int64_t)b * a.s_sb;
+  float* outs32 = static_cast<float*>(a.out_seq) + (int64_t)b * a.s_sb;
   float* vin = a.workspace + (int64_t)b * 6 * C;
   float w[8], bb[8], pool[8];
 #pragma unroll
@@ -233,12 +236,19 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a)
   int cnt = 0;
   const float invc = 1.0f / (float)C;
   for (int r0 = 0; r0 < S; r0 += U * RPP) {
-    u32x4 raw[U];
+    u32x4 raw[U], raw2[F32 ? U : 1];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int row = r0 + u * RPP + rs;
-      raw[u] = (row < S && cv) ? *reinterpret_cast<const u32x4*>(seq + (int64_t)row * C + c0)
-                               : u32x4{0u, 0u, 0u, 0u};
+      const bool ok = row < S && cv;
+      if constexpr (F32) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(seq32 + (int64_t)row * C + c0);
+        raw[u] = ok ? p[0] : u32x4{0u, 0u, 0u, 0u};
+        raw2[u] = ok ? p[1] : u32x4{0u, 0u, 0u, 0u};
+      } else {
+        raw[u] = ok ? *reinterpret_cast<const u32x4*>(seq + (int64_t)row * C + c0)
+                    : u32x4{0u, 0u, 0u, 0u};
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -247,10 +257,16 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a)
       float s = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        x[2 * e] = bf16_lo(raw[u][e]);
-        x[2 * e + 1] = bf16_hi(raw[u][e]);
-        s += x[2 * e] + x[2 * e + 1];
+        if constexpr (F32) {
+          x[e] = __uint_as_float(raw[u][e]);
+          x[4 + e] = __uint_as_float(raw2[u][e]);
+        } else {
+          x[2 * e] = bf16_lo(raw[u][e]);
+          x[2 * e + 1] = bf16_hi(raw[u][e]);
+        }
       }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += x[e];
 #pragma unroll
       for (int m = 1; m < TPR; m <<= 1) s += __shfl_xor(s, m, 64);
       const float mean = s * invc;
@@ -269,9 +285,15 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a)
       float y[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) y[e] = live ? fmaf(x[e] * rstd, w[e], bb[e]) : 0.f;
-      *reinterpret_cast<u32x4*>(outs + (int64_t)row * C + c0) =
-          u32x4{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]),
-                pack_bf16x2(y[6], y[7])};
+      if constexpr (F32) {
+        f32x4* p = reinterpret_cast<f32x4*>(outs32 + (int64_t)row * C + c0);
+        p[0] = f32x4{y[0], y[1], y[2], y[3]};
+        p[1] = f32x4{y[4], y[5], y[6], y[7]};
+      } else {
+        *reinterpret_cast<u32x4*>(outs + (int64_t)row * C + c0) =
+            u32x4{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]),
+                  pack_bf16x2(y[6], y[7])};
+      }
       if (cell) {
         if (live && sub == 0) ++cnt;
 #pragma unroll
@@ -596,7 +618,8 @@ extern "C" int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void
 
 // Checks the tail arguments (all but the workspace) and launches the two
 // passes with the head inputs in `ws` ((B, 6C) fp32, device memory).
-static int launch_trunk_tail(const shrimp_tail_args* a, float* ws, hipStream_t st) {
+static int launch_trunk_tail(const shrimp_tail_args* a, float* ws, hipStream_t st,
+                             bool f32 = false) {
   SHRIMP_REQUIRE(a->seq && a->mask && a->ln_w && a->ln_b && a->out_seq,
                  "trunk_tail: null pointer");
   SHRIMP_REQUIRE(a->C > 0 && a->C <= 256 && a->C % 2 == 0, "trunk_tail: C %d outside (0, 256]",
@@ -614,10 +637,16 @@ static int launch_trunk_tail(const shrimp_tail_args* a, float* ws, hipStream_t s
   const int tpr = k.C / 8;
   const size_t lsm = (size_t)(256 / ((tpr <= 4) ? 4 : (tpr <= 8) ? 8 : (tpr <= 16) ? 16 : 32)) *
                      (k.C + 1) * sizeof(float);
-  if (tpr <= 4) hipLaunchKernelGGL(final_ln_kernel<4>, dim3(k.B), dim3(256), lsm, st, k);
-  else if (tpr <= 8) hipLaunchKernelGGL(final_ln_kernel<8>, dim3(k.B), dim3(256), lsm, st, k);
-  else if (tpr <= 16) hipLaunchKernelGGL(final_ln_kernel<16>, dim3(k.B), dim3(256), lsm, st, k);
-  else hipLaunchKernelGGL(final_ln_kernel<32>, dim3(k.B), dim3(256), lsm, st, k);
+#define SHRIMP_FLN(T)                                                                      \
+  do {                                                                                       \
+    if (f32) hipLaunchKernelGGL((final_ln_kernel<T, true>), dim3(k.B), dim3(256), lsm, st, k); \
+    else hipLaunchKernelGGL((final_ln_kernel<T, false>), dim3(k.B), dim3(256), lsm, st, k);    \
+  } while (0)
+  if (tpr <= 4) SHRIMP_FLN(4);
+  else if (tpr <= 8) SHRIMP_FLN(8);
+  else if (tpr <= 16) SHRIMP_FLN(16);
+  else SHRIMP_FLN(32);
+#undef SHRIMP_FLN
   if (int rc = check_launch("trunk_tail/ln")) return rc;
   if (!k.value && !k.moves_left) return SHRIMP_OK;
   const int ks1 = kHeadThreads / k.C, ks2 = kHeadThreads / k.bins;
@@ -662,6 +691,13 @@ extern "C" int shrimp_trunk_tail(const shrimp_tail_args* a, void* stream) {
   if (a->B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(a->workspace, "trunk_tail: null workspace");
   return launch_trunk_tail(a, a->workspace, as_stream(stream));
+}
+
+extern "C" int shrimp_trunk_tail_f32(const shrimp_tail_args* a, void* stream) {
+  SHRIMP_REQUIRE(a != nullptr, "trunk_tail_f32: null args");
+  if (a->B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(a->workspace, "trunk_tail_f32: null workspace");
+  return launch_trunk_tail(a, a->workspace, as_stream(stream), true);
 }
 
 extern "C" int shrimp_trunk_tail_noalloc(const shrimp_tail_args* a, void* stream) {

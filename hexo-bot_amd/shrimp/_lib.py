@@ -185,6 +185,20 @@ SIGNATURES: dict = {
     "shrimp_raytap_wpack_bytes": (ctypes.c_size_t, [ctypes.c_int] * 2),
     "shrimp_pack_raytap_weight": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
     "shrimp_conv_ln_raytap": (ctypes.c_int, [ctypes.POINTER(RaytapArgs), _vp]),
+    "shrimp_conv_wpack_bytes_f32": (ctypes.c_size_t, [ctypes.c_int] * 3),
+    "shrimp_pack_conv_weight_f32": (ctypes.c_int, [_vp, _vp] + [ctypes.c_int] * 4 + [_vp]),
+    "shrimp_pack_linear_weight_f32": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp]),
+    "shrimp_hex_conv_f32": (ctypes.c_int, [ctypes.POINTER(ConvArgs), _vp]),
+    "shrimp_linear_f32": (ctypes.c_int, [ctypes.POINTER(LinearArgs), _vp]),
+    "shrimp_attn_f32": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _vp]),
+    "shrimp_trunk_tail_f32": (ctypes.c_int, [ctypes.POINTER(TailArgs), _vp]),
+    "shrimp_prep_feats_f32": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             ctypes.c_int, _vp, _vp]),
+    "shrimp_prep_csr_feats_f32": (ctypes.c_int, [_vp, ctypes.c_int, _vp] + [ctypes.c_int] * 3
+                                  + [_vp, _vp]),
+    "shrimp_fill_tokens_f32": (
+        ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _i64, ctypes.c_int, _vp]
+    ),
 }
 
 _LIB = None

@@ -22,10 +22,18 @@ Kernel sequence (reference lines in model.py):
     hex_conv  (policy)   conv + ReLU + Linear(C,1) + mask                      :1011-1020
 Weights are packed once into MFMA fragment order (bf16) and re-packed when
 any parameter changes (tracked through tensor version counters).
+
+precision "fp32" (the reference's serve with autocast off,
+inference.py:50-68) runs the same sequence on the fp32 kernels: fp32
+activations end to end (seq, y1, qkv, att, hid, seqf all fp32), fp32 MFMA
+products, the attention on the chunked fp32 kernel, the bias tables rounded
+to fp16 as the reference's no-grad bias is (model.py:737-760).
 """
 
 from __future__ import annotations
 
+import ctypes
+import os
 from types import SimpleNamespace
 
 import torch
@@ -68,6 +76,16 @@ def head_dim_pad(d: int) -> int:
     return max(16, -(-d // 16) * 16)
 
 
+def default_precision() -> str:
+    """"bf16" unless SHRIMP_SERVE_AUTOCAST=0 (the reference's switch for an
+    fp32 serve on CUDA devices, inference.py:50-68), then "fp32"."""
+
+    return "fp32" if os.environ.get("SHRIMP_SERVE_AUTOCAST", "1") == "0" else "bf16"
+
+
+PRECISIONS = ("bf16", "fp32")
+
+
 class HipForward:
     def __init__(self, net) -> None:
         self.net = net
@@ -101,6 +119,8 @@ class HipForward:
         self._graph_params = None
         self._graph_pool = None
         self._empty_rows: dict = {}
+        # "bf16" (bf16 activations, fp32 accumulation) or "fp32"
+        self.precision = default_precision()
 
     def _cus(self, dev) -> int:
         """Compute units of the device. Batches of at most half that many
@@ -117,15 +137,22 @@ class HipForward:
         self._key = None
 
     def _param_key(self, device) -> tuple:
-        return (str(device),) + tuple(
+        return (str(device), self.precision) + tuple(
             (p.data_ptr(), p._version) for p in self.net.parameters()
         )
+
+    @property
+    def fp32(self) -> bool:
+        if self.precision not in PRECISIONS:
+            raise ValueError(f"HipForward.precision must be one of {PRECISIONS}, "
+                             f"not {self.precision!r}")
+        return self.precision == "fp32"
 
     def weights(self, device: torch.device) -> SimpleNamespace:
         key = self._param_key(device)
         if self._packed is not None and key == self._key:
             return self._packed
-        self._packed = self._pack(device)
+        self._packed = self._pack32(device) if self.fp32 else self._pack(device)
         self._key = key
         return self._packed
 
@@ -211,17 +238,106 @@ class HipForward:
         )
         return P
 
-    @staticmethod
-    def _prep_buffers(B: int, N: int, dev) -> SimpleNamespace:
+    @torch.no_grad()
+    def _pack32(self, device: torch.device) -> SimpleNamespace:
+        """fp32 weights in the fp32 kernels' fragment order."""
+
+        net = self.net
+        lib = _lib.load()
+        st = _lib.stream_handle(device)
+
+        def f32(t):
+            return t.detach().to(device=device, dtype=torch.float32).contiguous()
+
+        def conv_w(conv, cin_pad=None):
+            w = f32(conv.weight)
+            t, cin, cout = w.shape
+            cp = -(-cin // 16) * 16 if cin_pad is None else cin_pad
+            out = torch.empty(t * cp * cout, dtype=torch.float32, device=device)
+            _lib.check(lib.shrimp_pack_conv_weight_f32(w.data_ptr(), out.data_ptr(), t, cin, cp,
+                                                       cout, st), "pack_conv_weight_f32")
+            torch.cuda.current_stream(device).synchronize()  # w dies with this frame
+            return out
+
+        def lin_w(weight):
+            w = f32(weight)
+            n_out, n_in = w.shape
+            out = torch.empty(n_in * n_out, dtype=torch.float32, device=device)
+            _lib.check(lib.shrimp_pack_linear_weight_f32(w.data_ptr(), out.data_ptr(), n_in, n_out,
+                                                         st), "pack_linear_weight_f32")
+            torch.cuda.current_stream(device).synchronize()
+            return out
+
+        c = net.channels
+        P = SimpleNamespace()
+        P.C, P.H = c, net.heads
+        P.d = c // P.H
+        if P.d % 4:
+            raise ValueError(f"fp32 serve: head dim {P.d} must be a multiple of 4")
+        P.layout = net.trunk_layout
+        P.stem = SimpleNamespace(
+            w=conv_w(net.stem, 16), b=f32(net.stem.bias), lnw=f32(net.stem_ln.weight),
+            lnb=f32(net.stem_ln.bias), eps=net.stem_ln.eps,
+        )
+        P.convs = [
+            SimpleNamespace(
+                w1=conv_w(blk.conv1), b1=f32(blk.conv1.bias), ln1w=f32(blk.ln1.weight),
+                ln1b=f32(blk.ln1.bias), eps1=blk.ln1.eps,
+                w2=conv_w(blk.conv2), b2=f32(blk.conv2.bias), ln2w=f32(blk.ln2.weight),
+                ln2b=f32(blk.ln2.bias), eps2=blk.ln2.eps, gamma=f32(blk.ls.gamma),
+            )
+            for blk in net.conv_blocks
+        ]
+        lut = net._cell_bias_lut_u8.to(device)
+        P.attn = []
+        for i, blk in enumerate(net.attn_blocks):
+            at = blk.attn
+            qkv_w = torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight], 0)
+            qkv_b = torch.cat([at.q_proj.bias, at.k_proj.bias, at.v_proj.bias], 0)
+            # the reference's no-grad bias rounds the block's table to fp16
+            table = net.bias_tables[i].detach().to(device).half().float()
+            P.attn.append(
+                SimpleNamespace(
+                    ln1w=f32(blk.ln1.weight), ln1b=f32(blk.ln1.bias), eps1=blk.ln1.eps,
+                    qkv_w=lin_w(qkv_w), qkv_b=f32(qkv_b),
+                    out_w=lin_w(at.out_proj.weight), out_b=f32(at.out_proj.bias),
+                    ln2w=f32(blk.ln2.weight), ln2b=f32(blk.ln2.bias), eps2=blk.ln2.eps,
+                    fc1_w=lin_w(blk.fc1.weight), fc1_b=f32(blk.fc1.bias),
+                    fc2_w=lin_w(blk.fc2.weight), fc2_b=f32(blk.fc2.bias),
+                    g_attn=f32(blk.ls_attn.gamma), g_mlp=f32(blk.ls_mlp.gamma),
+                    btab=attn_bias_table(table, lut, CELL_LUT_M)[0],
+                )
+            )
+        P.tokens = f32(net.tokens)
+        P.lnf = SimpleNamespace(w=f32(net.ln_final.weight), b=f32(net.ln_final.bias),
+                                eps=net.ln_final.eps)
+        P.value = SimpleNamespace(
+            rw=f32(net.value_reduction.weight.t()), rb=f32(net.value_reduction.bias),
+            hw=f32(net.value_head.weight.t()), hb=f32(net.value_head.bias),
+        )
+        P.ml = SimpleNamespace(
+            rw=f32(net.ml_reduction.weight.t()), rb=f32(net.ml_reduction.bias),
+            hw=f32(net.moves_left_head.weight.t()), hb=f32(net.moves_left_head.bias),
+        )
+        P.policy = SimpleNamespace(
+            w=conv_w(net.policy_conv), b=f32(net.policy_conv.bias),
+            hw=f32(net.policy_head.weight.reshape(-1)), hb=f32(net.policy_head.bias.reshape(-1)),
+        )
+        return P
+
+    def _prep_buffers(self, B: int, N: int, dev) -> SimpleNamespace:
         i32, u8 = torch.int32, torch.uint8
         S = N + NUM_TOKENS
+        f32 = self.fp32
         return SimpleNamespace(
             idx=torch.empty((B, N, 7), dtype=i32, device=dev),
             mask8=torch.empty((B, N), dtype=u8, device=dev),
             coords32=torch.empty((B, N, 2), dtype=i32, device=dev),
             seq_lens=torch.empty((B,), dtype=i32, device=dev),
             seq_mask=torch.empty((B, S), dtype=u8, device=dev),
-            xin=torch.empty((B, N, 32), dtype=torch.bfloat16, device=dev),
+            # stem input: bf16 (B, N, 32), or fp32 (B, N, 16) in the fp32 mode
+            xin=None if f32 else torch.empty((B, N, 32), dtype=torch.bfloat16, device=dev),
+            xin32=torch.empty((B, N, 16), dtype=torch.float32, device=dev) if f32 else None,
         )
 
     @torch.no_grad()
@@ -246,15 +362,7 @@ class HipForward:
         lib = _lib.load()
         st = _lib.stream_handle(dev)
         pb = self._prep_buffers(B, N, dev)
-        _lib.check(
-            lib.shrimp_prep_csr(
-                node_feats.data_ptr(), node_feats.shape[1], node_qr.data_ptr(), nbr.data_ptr(),
-                row_offsets.data_ptr(), row0, B, N, NUM_TOKENS, pb.idx.data_ptr(),
-                pb.mask8.data_ptr(), pb.coords32.data_ptr(), pb.seq_lens.data_ptr(),
-                pb.seq_mask.data_ptr(), pb.xin.data_ptr(), st,
-            ),
-            "prep_csr",
-        )
+        self._prep_csr_rows(pb, 0, B, N, (node_feats, node_qr, nbr, row_offsets), row0, st)
         return self._trunk(pb, B, N, dev, request_moves_left)
 
     # ---- graph-captured serve forward (the reference's _GraphCache,
@@ -280,10 +388,19 @@ class HipForward:
                 node_feats.data_ptr(), node_feats.shape[1], node_qr.data_ptr(), nbr.data_ptr(),
                 row_offsets.data_ptr(), row0, hi - lo, N, NUM_TOKENS, pb.idx[lo:].data_ptr(),
                 pb.mask8[lo:].data_ptr(), pb.coords32[lo:].data_ptr(), pb.seq_lens[lo:].data_ptr(),
-                pb.seq_mask[lo:].data_ptr(), pb.xin[lo:].data_ptr(), st,
+                pb.seq_mask[lo:].data_ptr(), None if pb.xin is None else pb.xin[lo:].data_ptr(),
+                st,
             ),
             "prep_csr",
         )
+        if pb.xin32 is not None:
+            _lib.check(
+                lib.shrimp_prep_csr_feats_f32(
+                    node_feats.data_ptr(), node_feats.shape[1], row_offsets.data_ptr(), row0,
+                    hi - lo, N, pb.xin32[lo:].data_ptr(), st,
+                ),
+                "prep_csr_feats_f32",
+            )
 
     def _empty_csr(self, dev):
         """CSR arrays of rows with no cells: packing them writes pad rows."""
@@ -372,15 +489,23 @@ class HipForward:
                 nbr_c.data_ptr(), _NBR_DT[nbr_c.dtype], mask_c.data_ptr(), coords_c.data_ptr(),
                 _COORD_DT[coords_c.dtype], feats_c.data_ptr(), _FEAT_DT[feats_c.dtype], F, B, N,
                 NUM_TOKENS, pb.idx.data_ptr(), pb.mask8.data_ptr(), pb.coords32.data_ptr(),
-                pb.seq_lens.data_ptr(), pb.seq_mask.data_ptr(), pb.xin.data_ptr(), st,
+                pb.seq_lens.data_ptr(), pb.seq_mask.data_ptr(), _lib.ptr(pb.xin), st,
             ),
             "prep_inputs",
         )
+        if pb.xin32 is not None:
+            _lib.check(
+                lib.shrimp_prep_feats_f32(feats_c.data_ptr(), _FEAT_DT[feats_c.dtype], F, B, N,
+                                          pb.xin32.data_ptr(), st),
+                "prep_feats_f32",
+            )
         return self._trunk(pb, B, N, dev, request_moves_left)
 
     def _trunk(self, pb: SimpleNamespace, B: int, N: int, dev, request_moves_left: bool) -> dict:
         """Everything after the input preparation: stem, blocks, tail, heads."""
 
+        if self.fp32:
+            return self._trunk32(pb, B, N, dev, request_moves_left)
         P = self.weights(dev)
         C, H, d, dpad = P.C, P.H, P.d, P.dpad
         S = N + NUM_TOKENS
@@ -495,8 +620,6 @@ class HipForward:
             mh_b=P.ml.hb.data_ptr(), moves_left=_lib.ptr(ml), workspace=tail_ws.data_ptr(),
             B=B, S=S, n_tokens=NUM_TOKENS, C=C, bins=VALUE_BINS,
         )
-        import ctypes
-
         _lib.check(lib.shrimp_trunk_tail(ctypes.byref(tail), st), "trunk_tail")
         policy = torch.empty((B, N), dtype=torch.float32, device=dev)
         launch_conv(
@@ -512,5 +635,111 @@ class HipForward:
                 P=P, B=B, N=N, S=S, idx=idx, mask8=mask8, coords32=coords32, seq_lens=seq_lens,
                 seq_mask=seq_mask, seq=seq, y1=y1, qkv=qkv, att=att, hid=hid, seqf=seqf,
                 stream=st, attn_fused=attn_fused,
+            )
+        return out
+
+    def _trunk32(self, pb: SimpleNamespace, B: int, N: int, dev, request_moves_left: bool) -> dict:
+        """The fp32 serve mode's trunk: the launch sequence of _trunk on the fp32
+        kernels (model.py:395-514, 905-1020), fp32 activations throughout."""
+
+        P = self.weights(dev)
+        C, H, d = P.C, P.H, P.d
+        S = N + NUM_TOKENS
+        lib = _lib.load()
+        st = _lib.stream_handle(dev)
+        f = torch.float32
+        idx, mask8, coords32 = pb.idx, pb.mask8, pb.coords32
+        seq_lens, seq_mask = pb.seq_lens, pb.seq_mask
+        seq = torch.empty((B, S, C), dtype=f, device=dev)
+        _lib.check(lib.shrimp_fill_tokens_f32(P.tokens.data_ptr(), NUM_TOKENS, C, seq.data_ptr(),
+                                              S * C, B, st), "fill_tokens_f32")
+        cells = seq[:, NUM_TOKENS:]
+        y1 = torch.empty((B, N, C), dtype=f, device=dev)
+        qkv = torch.empty((3, B, H, S, d), dtype=f, device=dev)
+        att = torch.empty((B, S, C), dtype=f, device=dev)
+        hid = torch.empty((B, S, 2 * C), dtype=f, device=dev)
+        rows = B * S
+
+        def conv(x, x_sb, x_sn, w, b, cin_pad, **kw):
+            a = _lib.ConvArgs(
+                x=x.data_ptr(), x_sb=x_sb, x_sn=x_sn, idx=idx.data_ptr(), taps=7, idx_stride=7,
+                mask=mask8.data_ptr(), w=w.data_ptr(), bias=b.data_ptr(),
+                ln_w=_lib.ptr(kw.get("ln_w")), ln_b=_lib.ptr(kw.get("ln_b")),
+                eps=float(kw.get("eps", 1e-5)), relu=int(bool(kw.get("relu", False))),
+                resid=_lib.ptr(kw.get("resid")), r_sb=S * C, r_sn=C,
+                gamma=_lib.ptr(kw.get("gamma")), head_w=_lib.ptr(kw.get("head_w")),
+                head_b=_lib.ptr(kw.get("head_b")), head_out=_lib.ptr(kw.get("head_out")),
+                out=_lib.ptr(kw.get("out")), o_sb=kw.get("o_sb", 0), o_sn=kw.get("o_sn", 0),
+                B=B, N=N, cin_pad=cin_pad, cout=C,
+            )
+            _lib.check(lib.shrimp_hex_conv_f32(ctypes.byref(a), st), "hex_conv_f32")
+
+        def linear(x, x_sr, w, b, n_in, n_out, mode, out, o_sr=0, **kw):
+            a = _lib.LinearArgs(
+                x=x.data_ptr(), x_sr=x_sr, w=w.data_ptr(), bias=b.data_ptr(),
+                ln_w=_lib.ptr(kw.get("ln_w")), ln_b=_lib.ptr(kw.get("ln_b")),
+                eps=float(kw.get("eps", 1e-5)), mode=mode, resid=_lib.ptr(kw.get("resid")),
+                r_sr=kw.get("r_sr", 0), gamma=_lib.ptr(kw.get("gamma")),
+                mask=_lib.ptr(kw.get("mask")), out=out.data_ptr(), o_sr=o_sr, rows=rows,
+                in_features=n_in, out_features=n_out, B=B, S=S, H=H, dpad=d,
+            )
+            _lib.check(lib.shrimp_linear_f32(ctypes.byref(a), st), "linear_f32")
+
+        conv(pb.xin32, N * 16, 16, P.stem.w, P.stem.b, 16, ln_w=P.stem.lnw, ln_b=P.stem.lnb,
+             eps=P.stem.eps, relu=True, out=cells, o_sb=S * C, o_sn=C)
+        ci = ai = 0
+        for kind in P.layout:
+            if kind == "C":
+                k = P.convs[ci]
+                ci += 1
+                conv(cells, S * C, C, k.w1, k.b1, C, ln_w=k.ln1w, ln_b=k.ln1b, eps=k.eps1,
+                     relu=True, out=y1, o_sb=N * C, o_sn=C)
+                conv(y1, N * C, C, k.w2, k.b2, C, ln_w=k.ln2w, ln_b=k.ln2b, eps=k.eps2,
+                     resid=cells, gamma=k.gamma, out=cells, o_sb=S * C, o_sn=C)
+                continue
+            a = P.attn[ai]
+            ai += 1
+            linear(seq, C, a.qkv_w, a.qkv_b, C, 3 * C, _lib.LIN_QKV, qkv, ln_w=a.ln1w,
+                   ln_b=a.ln1b, eps=a.eps1)
+            at = _lib.AttnArgs(
+                q=qkv[0].data_ptr(), k=qkv[1].data_ptr(), v=qkv[2].data_ptr(), qkv_sb=H * S * d,
+                qkv_sh=S * d, seq_lens=seq_lens.data_ptr(), pair=None, p_sb=0, p_sq=0,
+                table2=None, table_rows=0, coords=coords32.data_ptr(), mask=mask8.data_ptr(),
+                btab=a.btab.data_ptr(), xtab=None, lut_m=CELL_LUT_M, n_tokens=NUM_TOKENS,
+                o=att.data_ptr(), o_sb=S * C, o_sh=d, o_sr=C, B=B, S=S, H=H, d=d, dpad=d,
+            )
+            _lib.check(lib.shrimp_attn_f32(ctypes.byref(at), st), "attn_f32")
+            linear(att, C, a.out_w, a.out_b, C, C, _lib.LIN_RESID, seq, o_sr=C, resid=seq, r_sr=C,
+                   gamma=a.g_attn, mask=seq_mask)
+            linear(seq, C, a.fc1_w, a.fc1_b, C, 2 * C, _lib.LIN_GELU, hid, o_sr=2 * C,
+                   ln_w=a.ln2w, ln_b=a.ln2b, eps=a.eps2)
+            linear(hid, 2 * C, a.fc2_w, a.fc2_b, 2 * C, C, _lib.LIN_RESID, seq, o_sr=C, resid=seq,
+                   r_sr=C, gamma=a.g_mlp, mask=seq_mask)
+
+        seqf = torch.empty((B, S, C), dtype=f, device=dev)
+        value = torch.empty((B, VALUE_BINS), dtype=f, device=dev)
+        ml = torch.empty((B, VALUE_BINS), dtype=f, device=dev) if request_moves_left else None
+        tail_ws = torch.empty((B, 6 * C), dtype=f, device=dev)
+        tail = _lib.TailArgs(
+            seq=seq.data_ptr(), s_sb=S * C, mask=mask8.data_ptr(), ln_w=P.lnf.w.data_ptr(),
+            ln_b=P.lnf.b.data_ptr(), eps=float(P.lnf.eps), out_seq=seqf.data_ptr(),
+            vr_w=P.value.rw.data_ptr(), vr_b=P.value.rb.data_ptr(), vh_w=P.value.hw.data_ptr(),
+            vh_b=P.value.hb.data_ptr(), value=value.data_ptr(),
+            mr_w=P.ml.rw.data_ptr(), mr_b=P.ml.rb.data_ptr(), mh_w=P.ml.hw.data_ptr(),
+            mh_b=P.ml.hb.data_ptr(), moves_left=_lib.ptr(ml), workspace=tail_ws.data_ptr(),
+            B=B, S=S, n_tokens=NUM_TOKENS, C=C, bins=VALUE_BINS,
+        )
+        _lib.check(lib.shrimp_trunk_tail_f32(ctypes.byref(tail), st), "trunk_tail_f32")
+        policy = torch.empty((B, N), dtype=f, device=dev)
+        conv(seqf[:, NUM_TOKENS:], S * C, C, P.policy.w, P.policy.b, C, relu=True,
+             head_w=P.policy.hw, head_b=P.policy.hb, head_out=policy)
+        out = {"policy": policy, "value": value}
+        if request_moves_left:
+            out["moves_left"] = ml
+        if self.keep_buffers:
+            self.last = dict(
+                P=P, B=B, N=N, S=S, idx=idx, mask8=mask8, coords32=coords32, seq_lens=seq_lens,
+                seq_mask=seq_mask, seq=seq, y1=y1, qkv=qkv, att=att, hid=hid, seqf=seqf,
+                stream=st, attn_fused=False,
             )
         return out

@@ -54,9 +54,12 @@ int shrimp_abi_version(void);
  * 3 = as 0 without the small-batch row split; other values only query.
  * Returns the previous setting. Process-wide.
  * shrimp_attn_variant: 0 = automatic (two heads per attention workgroup when
- * their K/V fit the LDS budget, on eight waves at padded head dim 16, else
- * four), 1 = one head per workgroup, 2 = two heads on four waves; other
- * values only query. Returns the previous setting. Process-wide.
+ * their K/V fit the 64 KiB budget, on eight waves at padded head dim 16, else
+ * four; one head per workgroup with up to the device's per-workgroup LDS for
+ * longer sequences; beyond that the chunked kernel of shrimp_attn_f32 on bf16
+ * operands), 1 = one head per workgroup, 2 = two heads on four waves, 3 = the
+ * chunked kernel; other values only query. Returns the previous setting.
+ * Process-wide.
  * shrimp_max_lds_per_block: LDS bytes one workgroup may allocate on the
  * current device (the staged conv needs (N + 1) * cin_pad * 2). */
 int shrimp_conv_variant(int variant);
@@ -562,6 +565,49 @@ size_t shrimp_raytap_wpack_bytes(int C, int Cout);
  * -> packed fp16 MFMA fragments. */
 int shrimp_pack_raytap_weight(const uint16_t* w, int C, int Cout, void* packed, void* stream);
 int shrimp_conv_ln_raytap(const shrimp_raytap_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * fp32 serve mode: the forward with fp32 activations end to end, as the
+ * reference serves with autocast off (SHRIMP_SERVE_AUTOCAST=0,
+ * packages/shrimp/python/shrimp/inference.py:50-68; model.py:346-514 run in
+ * fp32). Same argument structs and semantics as the bf16 entry points above,
+ * with these differences:
+ *   - activations (x, resid, out, seq, out_seq, q, k, v, o) are fp32;
+ *   - weights are packed by the *_f32 packers: 16-byte fp32 fragments, for
+ *     k-chunk kc (16 rows of K) and output block nb (16 outputs), lane l
+ *     holding W[16 kc + 4 (l / 16) + j][16 nb + l % 16], j < 4; conv weights
+ *     with K = taps * cin_pad (cin_pad a multiple of 16), linear weights with
+ *     K = in_features;
+ *   - shrimp_hex_conv_f32: cin_pad and cout multiples of 16; LayerNorm and
+ *     head epilogues need cout in {32, 64, 96, 128, 192, 256};
+ *   - shrimp_linear_f32: in / out features multiples of 16; QKV mode writes
+ *     (3, B, H, S, dpad) fp32 with dpad >= d, dpad % 4 == 0;
+ *   - shrimp_attn_f32: q, k, v (B, H, S, dpad) fp32, d <= 64, any S; pair or
+ *     coords bias as shrimp_attn (btab and table2 fp32; xtab unused); one
+ *     query row per thread with keys streamed through LDS;
+ *   - shrimp_trunk_tail_f32: seq and out_seq fp32;
+ *   - shrimp_prep_feats_f32 / shrimp_prep_csr_feats_f32: the stem input
+ *     xin (B, N, 16) fp32 (features zero-padded to 16 channels) from padded
+ *     feats of feats_dt (nfeat <= 16) or from the ABI-1 CSR f16 node_feats
+ *     (rows as in shrimp_prep_csr); the other preparation outputs come from
+ *     shrimp_prep_inputs / shrimp_prep_csr with xin = NULL;
+ *   - shrimp_fill_tokens_f32: token rows of an fp32 seq.
+ * ---------------------------------------------------------------------- */
+size_t shrimp_conv_wpack_bytes_f32(int taps, int cin_pad, int cout);
+int shrimp_pack_conv_weight_f32(const float* w, float* packed, int taps, int cin, int cin_pad,
+                                int cout, void* stream);
+int shrimp_pack_linear_weight_f32(const float* w, float* packed, int in_features,
+                                  int out_features, void* stream);
+int shrimp_hex_conv_f32(const shrimp_conv_args* a, void* stream);
+int shrimp_linear_f32(const shrimp_linear_args* a, void* stream);
+int shrimp_attn_f32(const shrimp_attn_args* a, void* stream);
+int shrimp_trunk_tail_f32(const shrimp_tail_args* a, void* stream);
+int shrimp_prep_feats_f32(const void* feats, int feats_dt, int nfeat, int B, int N, float* xin,
+                          void* stream);
+int shrimp_prep_csr_feats_f32(const void* node_feats, int nfeat, const int64_t* row_offsets,
+                              int row0, int B, int N, float* xin, void* stream);
+int shrimp_fill_tokens_f32(const float* tokens, int n_tokens, int C, float* seq, int64_t seq_sb,
+                           int B, void* stream);
 
 #ifdef __cplusplus
 }

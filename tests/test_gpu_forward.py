@@ -118,6 +118,48 @@ def test_forward_cfg4_matches_oracle(cfg4_batch):
     _check_trunk(out, want, b["mask"], "cfg4 B=32")
 
 
+def _wide_batch(npad):
+    """Three positions padded to npad: L256 positions for 256, spec-variant
+    positions (supports of 280-512 cells) for 512."""
+
+    from shrimp import synthetic
+    from shrimp.batching import collate_rows
+
+    if npad == 256:
+        return synthetic.position_batch("cfg4", 3, seed=31)
+    rows = [r for r in synthetic.positions("cfg4_spec", 12, seed=32) if r[1].num_nodes <= npad][:3]
+    assert len(rows) == 3 and max(r[1].num_nodes for r in rows) > 256
+    return collate_rows([(s, f) for _, s, f in rows], pad_to=npad)
+
+
+@pytest.mark.parametrize("c,h,npad", [(96, 4, 256), (96, 4, 512), (192, 3, 256), (192, 3, 512),
+                                      (192, 3, 576)])
+def test_forward_other_widths_match_oracle(c, h, npad):
+    """The reference's default width (C=96, H=4: head dim 24, padded to 32)
+    and its main config's (C=192, H=3: head dim 64) at Npad 256, 512 and 576
+    (S = 584 at head dim 64 exceeds one workgroup's LDS: the chunked
+    attention kernel) against the oracle; these widths take the generic
+    linear kernels and two-launch ConvBlocks."""
+
+    b = _wide_batch(min(npad, 512))
+    if npad == 576:
+        from shrimp.batching import collate_rows
+        from shrimp import synthetic
+
+        rows = [r for r in synthetic.positions("cfg4_spec", 12, seed=32) if r[1].num_nodes <= 512][:3]
+        b = collate_rows([(s, f) for _, s, f in rows], pad_to=576)
+    layout = "CCA"
+    net = _net(c, h, layout, seed=c + h, mode="heads")
+    out = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"], trunk=True)
+    want = ofwd.forward_policy_value(
+        weights.make_state_dict(c, h, layout, seed=c + h, mode="heads"), layout, h, b["feats"],
+        b["nbr"], b["mask"], b["coords"], request_moves_left=True, dtype=torch.float32,
+        return_trunk=True,
+    )
+    _check(out, want, b["mask"], f"C={c} H={h} Npad={npad}")
+    _check_trunk(out, want, b["mask"], f"C={c} H={h} Npad={npad}")
+
+
 def test_forward_feature_and_index_dtypes(cfg4_batch):
     """f16 features + int32 nbr/coords (the evaluator wire types) give the
     same result as f32 + int64 up to the f16 rounding of the features."""

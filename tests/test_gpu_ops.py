@@ -51,11 +51,12 @@ def conv_variant(request):
         lib.shrimp_conv_variant(prev)
 
 
-@pytest.fixture(params=[0, 1, 2], ids=["auto", "one_head", "four_waves"])
+@pytest.fixture(params=[0, 1, 2, 3], ids=["auto", "one_head", "four_waves", "chunked"])
 def attn_variant(request):
     """Runs an attention test with the automatic kernel choice (two heads per
-    workgroup; eight waves at head dim 16), with one head per workgroup, and
-    with two heads on four waves."""
+    workgroup; eight waves at head dim 16), with one head per workgroup, with
+    two heads on four waves, and with the chunked kernel (keys streamed
+    through LDS, the path of sequences too long for one workgroup's LDS)."""
 
     from shrimp import _lib
 

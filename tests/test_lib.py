@@ -148,11 +148,14 @@ def test_bad_arguments_fail_with_message(lib):
 def test_variant_switches(lib):
     """Process-wide kernel switches: valid values are set and return the
     previous one, others only query (attention: 0 auto, 1 one head, 2 two heads
-    on four waves)."""
+    on four waves, 3 the chunked kernel)."""
     prev = lib.shrimp_attn_variant(2)
     try:
-        assert lib.shrimp_attn_variant(3) == 2  # out of range: query only
+        assert lib.shrimp_attn_variant(4) == 2  # out of range: query only
         assert lib.shrimp_attn_variant(-1) == 2
+        assert lib.shrimp_attn_variant(3) == 2
+        assert lib.shrimp_attn_variant(-1) == 3
+        assert lib.shrimp_attn_variant(2) == 3
         assert lib.shrimp_attn_variant(1) == 2
         assert lib.shrimp_attn_variant(-1) == 1
     finally:
