@@ -9,9 +9,12 @@ positions (shrimp.synthetic "cfg4": 10-80 stones, support radius 4, L256
 capped). Inputs are device-resident before timing. One step = one forward.
 
 Prints one JSON line with the metric, the per-kernel roofline of the
-dominant kernel (the trunk hex conv, timed live with HIP events on the
-launch stream), the attention kernel's figures, and the CPU baseline (the
-oracle's fp32 eager forward on a bounded sample, rank 0 only).
+dominant kernel (the fused ConvBlock, timed live with HIP events on the
+launch stream, re-launched alone and inside the forward), the attention
+kernel's figures, per-kernel times inside real forwards, configs 1-3 as
+standalone ops at B=1024 with their rooflines, the fp32 serve mode's
+forward, and the CPU baseline (the oracle's fp32 eager forward on a bounded
+sample, rank 0 only).
 """
 
 from __future__ import annotations
@@ -415,18 +418,44 @@ def hexfield_timing(reps: int = 50, cpu_sample: int = 16) -> dict:
     return out
 
 
-def cpu_baseline(batch, seconds: float):
+def _host_cpu() -> dict:
+    """CPU model and the cores this process may use (lscpu / sched affinity)."""
+
+    model = None
+    try:
+        import subprocess
+
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for ln in out.splitlines():
+            if ln.startswith("Model name:"):
+                model = ln.split(":", 1)[1].strip()
+    except Exception:  # lscpu missing: model stays unknown
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"model": model, "cores_visible": os.cpu_count(), "cores_usable": usable}
+
+
+def cpu_baseline(batch, seconds: float, sample: int = 64):
     """Oracle fp32 eager forward (the reference CPU path, restated) on a
-    bounded sample of the same workload; positions/s on the host cores."""
+    bounded sample of the same workload (the first `sample` of the 512 cfg4
+    positions, one forward per batch of `sample`); positions/s on the host
+    cores this process may use, capped by OMP_NUM_THREADS where the host sets
+    it (the GPU box allots 16 threads per GPU)."""
 
     import torch
 
     from oracle import forward as ofwd
     from oracle import weights
 
-    threads = int(os.environ.get("SHRIMP_CPU_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    host = _host_cpu()
+    threads = host["cores_usable"]
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    threads = int(os.environ.get("SHRIMP_CPU_THREADS", "0")) or max(1, threads)
     torch.set_num_threads(threads)
-    sample = 8
     sd = weights.make_state_dict(C, H, LAYOUT, seed=0, mode="fresh")
     args = [batch[k][:sample] for k in ("feats", "nbr", "mask", "coords")]
     ofwd.forward_policy_value(sd, LAYOUT, H, *args, dtype=torch.float32)
@@ -443,7 +472,199 @@ def cpu_baseline(batch, seconds: float):
         "unit": "positions/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{runs} forwards x {sample} cfg4 positions (fp32 eager oracle, {el:.1f} s)",
+        "sample": f"{runs} forwards x {sample} cfg4 positions (fp32 eager oracle, {el:.1f} s, "
+                  f"torch threads {threads})",
+        "cpu_model": host["model"],
+        "cores_visible": host["cores_visible"],
+        "cores_usable": host["cores_usable"],
+    }
+
+
+def forward_timeline(net, inputs, reps: int = 10) -> dict:
+    """Per-kernel times inside real forwards: HIP events recorded on the
+    launch stream after every launch of `reps` eager forwards; average per
+    launch and total per forward for each kernel kind."""
+
+    import torch
+
+    rt = net.hip_runtime()
+    rt.timeline = []
+    try:
+        for _ in range(reps):
+            net.forward_policy_value(*inputs)
+        torch.cuda.synchronize()
+        marks = rt.timeline
+    finally:
+        rt.timeline = None
+    per: dict = {}
+    for (_, e0), (name, e1) in zip(marks, marks[1:]):
+        if name == "start":
+            continue
+        per.setdefault(name, []).append(e0.elapsed_time(e1))
+    return {name: {"launches_per_forward": len(v) // reps,
+                   "avg_ms": round(sum(v) / len(v), 5),
+                   "ms_per_forward": round(sum(v) / reps, 5)} for name, v in per.items()}
+
+
+def ops_timing(reps: int = 30) -> dict:
+    """Configs 1-3 as standalone ops at their own shapes (B = 1024, Npad = 256),
+    HIP events around back-to-back launches on the launch stream:
+
+    cfg1  7-tap gather-GEMM 128 -> 128 with the fused bias + ReLU + mask
+          epilogue; work 2*7*C*C per row over all B*N rows (60.13 GFLOP),
+          bytes (Cin + Cout)*2 + 7*4 per row + weights (141.8 MB);
+    cfg2  rel-biased masked attention, H = 8, d = 16, lengths U[64, 256], the
+          33x33 per-head offset table, no tokens; work 4*d*H*sum n_b^2, bytes
+          8*d*H*sum n_b (Q, K, V in, O out) + coordinates + table;
+    cfg3  31 independent tap weights over the 32-slot ray index (built on
+          the device), 128 -> 128; work 2*31*C*C per row (266.3 GFLOP), bytes
+          2*C*2 + 32*4 per row + weights."""
+
+    import math
+
+    import torch
+
+    from oracle import tables
+    from shrimp import _lib, ops, synthetic
+
+    dev = torch.device("cuda")
+    stream = torch.cuda.current_stream(dev)
+    lib = _lib.load()
+    res = {}
+
+    # cfg1
+    case = synthetic.conv_inputs(1024, channels=128)
+    b = case["batch"]
+    bb, n = b["mask"].shape
+    x = torch.from_numpy(case["x"]).to(dev, torch.bfloat16).contiguous()
+    wp = ops.pack_conv_weight(torch.from_numpy(case["w"]).to(dev))
+    bias = torch.from_numpy(case["bias"]).to(dev)
+    idx = torch.from_numpy(tables.gather_index(b["nbr"].numpy())).to(dev, torch.int32).contiguous()
+    m8 = b["mask"].to(dev, torch.uint8).contiguous()
+    out = torch.empty((bb, n, 128), dtype=torch.bfloat16, device=dev)
+    run = lambda: ops.launch_conv(x=x, x_sb=n * 128, x_sn=128, idx=idx, taps=7, idx_stride=7,
+                                  mask8=m8, wpack=wp, bias=bias, B=bb, N=n, cin_pad=128, cout=128,
+                                  relu=True, out=out, o_sb=n * 128, o_sn=128)
+    run()
+    ms = _events_time(run, reps, stream)
+    rows = bb * n
+    valid = int(b["mask"].sum().item())
+    flops = 2.0 * 7 * 128 * 128 * rows
+    nbytes = rows * (256 * 2 + 7 * 4) + 7 * 128 * 128 * 2 + 4 * 128
+    tfl = flops / (ms * 1e-3) / 1e12
+    res["cfg1"] = {
+        "op": "hex_conv bias+ReLU (7 taps, 128 -> 128)", "workload": f"B={bb} Npad={n}",
+        "launch_ms": round(ms, 5), "flops": flops, "flops_valid_rows": 2.0 * 7 * 128 * 128 * valid,
+        "algorithmic_bytes": nbytes, "bound": "mfma", "achieved_tflops": round(tfl, 2),
+        "peak_tflops": PEAK_BF16_TFLOPS, "frac": round(tfl / PEAK_BF16_TFLOPS, 4),
+        "hbm_gbs_algorithmic": round(nbytes / (ms * 1e-3) / 1e9, 1),
+    }
+    del x, out
+
+    # cfg2
+    c2 = synthetic.attention_inputs(1024, heads=8, d=16)
+    q, k, v = (torch.from_numpy(c2[nm]).to(dev, torch.bfloat16).contiguous() for nm in "qkv")
+    B2, H2, S2, d2 = q.shape
+    table = torch.from_numpy(c2["table"])
+    btab = (torch.cat([table, torch.zeros(3, H2)]) * (1.0 / math.log(2.0))).to(dev).contiguous()
+    xtab = cfg2_xtab(btab, 16)
+    coords = torch.from_numpy(c2["coords"]).to(dev, torch.int32).contiguous()
+    mask2 = torch.from_numpy(c2["mask"]).to(dev, torch.uint8).contiguous()
+    lens = torch.from_numpy(c2["lens"]).to(dev)
+    o = torch.empty((B2, H2, S2, d2), dtype=torch.bfloat16, device=dev)
+    run = lambda: ops.launch_attn(q=q, k=k, v=v, qkv_sb=H2 * S2 * d2, qkv_sh=S2 * d2, seq_lens=lens,
+                                  o=o, o_sb=H2 * S2 * d2, o_sh=S2 * d2, o_sr=d2, B=B2, S=S2, H=H2,
+                                  d=d2, dpad=16, coords=coords, mask8=mask2, btab=btab, xtab=xtab,
+                                  lut_m=16, n_tokens=0)
+    run()
+    ms = _events_time(run, reps, stream)
+    nb = c2["lens"].astype("float64")
+    flops = float(4 * d2 * H2 * (nb ** 2).sum())
+    nbytes = float(8 * d2 * H2 * nb.sum() + nb.sum() * (2 * 4 + 1) + btab.numel() * 4)
+    tfl = flops / (ms * 1e-3) / 1e12
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    res["cfg2"] = {
+        "op": "attention, coords bias (33x33 table), key mask", "workload":
+            f"B={B2} H={H2} L={S2} d={d2} lengths U[64,256] (sum {int(nb.sum())})",
+        "launch_ms": round(ms, 5), "flops": flops, "algorithmic_bytes": nbytes, "bound": "hbm",
+        "achieved_gbs": round(gbs, 1), "peak_gbs": PEAK_HBM_GBS, "frac": round(gbs / PEAK_HBM_GBS, 4),
+        "tflops": round(tfl, 2), "mfma_frac": round(tfl / PEAK_BF16_TFLOPS, 4),
+    }
+    del q, k, v, o
+
+    # cfg3
+    c3 = synthetic.raytap_inputs(1024, channels=128)
+    b3 = c3["batch"]
+    B3, n3 = b3["mask"].shape
+    x3 = torch.from_numpy(c3["x"]).to(dev, torch.bfloat16).contiguous()
+    wp3 = ops.pack_conv_weight(torch.from_numpy(c3["w"]).to(dev))
+    bias3 = torch.from_numpy(c3["bias"]).to(dev)
+    c32 = b3["coords"].to(dev, torch.int32).contiguous()
+    m83 = b3["mask"].to(dev, torch.uint8).contiguous()
+    ridx = torch.empty((B3, n3, 32), dtype=torch.int32, device=dev)
+    _lib.check(lib.shrimp_build_ray_index(c32.data_ptr(), m83.data_ptr(), B3, n3, ridx.data_ptr(),
+                                          _lib.stream_handle(dev)), "ray index")
+    out3 = torch.empty((B3, n3, 128), dtype=torch.bfloat16, device=dev)
+    run = lambda: ops.launch_conv(x=x3, x_sb=n3 * 128, x_sn=128, idx=ridx, taps=31, idx_stride=32,
+                                  mask8=m83, wpack=wp3, bias=bias3, B=B3, N=n3, cin_pad=128,
+                                  cout=128, out=out3, o_sb=n3 * 128, o_sn=128)
+    run()
+    ms = _events_time(run, reps, stream)
+    rows = B3 * n3
+    flops = 2.0 * 31 * 128 * 128 * rows
+    nbytes = rows * (2 * 128 * 2 + 32 * 4) + 31 * 128 * 128 * 2
+    tfl = flops / (ms * 1e-3) / 1e12
+    res["cfg3"] = {
+        "op": "31-tap ray conv (independent tap weights, 128 -> 128)", "workload": f"B={B3} Npad={n3}",
+        "launch_ms": round(ms, 5), "flops": flops, "algorithmic_bytes": nbytes, "bound": "mfma",
+        "achieved_tflops": round(tfl, 2), "peak_tflops": PEAK_BF16_TFLOPS,
+        "frac": round(tfl / PEAK_BF16_TFLOPS, 4),
+        "hbm_gbs_algorithmic": round(nbytes / (ms * 1e-3) / 1e9, 1),
+    }
+    return res
+
+
+def cfg2_xtab(btab, m: int):
+    """The attention kernel's unclamped offset table for a (2m+1)^2 per-offset
+    table: xtab[(dq + XD)(2 XD + 1) + dr + XD, h] = fp16(btab[clamped (dq, dr), h])
+    over |dq|, |dr| <= XD (what shrimp_attn_bias_table writes for the model's
+    LUT), so compact cell sets take the kernel's linear-offset path."""
+
+    import torch
+
+    from shrimp.ops import ATTN_XD
+
+    r = torch.arange(-ATTN_XD, ATTN_XD + 1, device=btab.device)
+    dq, dr = torch.meshgrid(r, r, indexing="ij")
+    pos = (dq.clamp(-m, m) + m) * (2 * m + 1) + dr.clamp(-m, m) + m
+    return btab[pos.reshape(-1)].half().contiguous()
+
+
+def fp32_timing(net, inputs, steps: int = 10) -> dict:
+    """Secondary figure: the config 4 forward in the fp32 serve mode (fp32
+    activations, fp32 MFMA), same inputs and weights."""
+
+    import torch
+
+    rt = net.hip_runtime()
+    prev = rt.precision
+    rt.precision = "fp32"
+    try:
+        net.forward_policy_value(*inputs)
+        torch.cuda.synchronize()
+        ms = _events_time(lambda: net.forward_policy_value(*inputs), steps,
+                          torch.cuda.current_stream())
+        tl = forward_timeline(net, inputs, reps=3)
+    finally:
+        rt.precision = prev
+    return {
+        "workload": "shrimp_forward_policy_value_cfg4 (fp32 serve mode)",
+        "dtype": "fp32",
+        "positions_per_s": round(B / (ms * 1e-3), 1),
+        "ms_per_step": round(ms, 4),
+        "tflops_padded": round(1.425e9 * B / (ms * 1e-3) / 1e12, 2),
+        "peak_fp32_mfma_tflops": 157.3,
+        "in_forward": tl,
     }
 
 
@@ -500,6 +721,7 @@ def main() -> int:
     torch.cuda.synchronize(dev)
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     kt = kernel_timings(net, inputs)
+    timeline = forward_timeline(net, inputs)
 
     block_tflops = kt["block_flops"] / (kt["block_ms"] * 1e-3) / 1e12
     conv_tflops = kt["conv_flops"] / (kt["conv_ms"] * 1e-3) / 1e12
@@ -543,6 +765,10 @@ def main() -> int:
             "algorithmic_bytes": kt["block_bytes"],
             "launch_ms": round(kt["block_ms"], 5),
             "flops_per_launch": kt["block_flops"],
+            "in_forward_launch_ms": timeline.get("conv_block", {}).get("avg_ms"),
+            "in_forward_frac": (round(kt["block_flops"] / (timeline["conv_block"]["avg_ms"] * 1e-3)
+                                      / 1e12 / PEAK_BF16_TFLOPS, 4)
+                                if "conv_block" in timeline else None),
         },
         "single_conv": {
             "kernel": "hex_conv_big_kernel<LN|RELU> (ConvBlock 0 conv1 alone)",
@@ -563,6 +789,9 @@ def main() -> int:
             "one_launch_ms": None if kt["attn_fused_ms"] is None else round(kt["attn_fused_ms"], 5),
         },
         "block0_row_kernels": kt["linears"],
+        "in_forward": timeline,
+        "ops": ops_timing(),
+        "fp32": fp32_timing(net, inputs),
         "forward_tflops_padded": round(1.425e9 * B / (ms * 1e-3) / 1e12, 2),
         "featurize": featurize_timing(batch["rows"]),
         "hexfield": hexfield_timing(),

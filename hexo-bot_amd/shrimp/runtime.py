@@ -121,6 +121,16 @@ class HipForward:
         self._empty_rows: dict = {}
         # "bf16" (bf16 activations, fp32 accumulation) or "fp32"
         self.precision = default_precision()
+        # When a list, eager forwards append (name, event) after each launch
+        # (HIP events on the launch stream) so a caller can read per-kernel
+        # times inside a real forward; None (the default) records nothing.
+        self.timeline = None
+
+    def _mark(self, name: str) -> None:
+        if self.timeline is not None:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            self.timeline.append((name, ev))
 
     def _cus(self, dev) -> int:
         """Compute units of the device. Batches of at most half that many
@@ -438,6 +448,7 @@ class HipForward:
             pb = self._prep_buffers(bb, N, dev)
             self._prep_csr_rows(pb, 0, bb, N, self._empty_csr(dev), 0, st)
             keep, self.keep_buffers = self.keep_buffers, False
+            tl, self.timeline = self.timeline, None
             try:
                 cur = torch.cuda.current_stream(dev)
                 side = torch.cuda.Stream(dev)
@@ -453,6 +464,7 @@ class HipForward:
                     out = self._trunk(pb, bb, N, dev, request_moves_left)
             finally:
                 self.keep_buffers = keep
+                self.timeline = tl
             ent = SimpleNamespace(graph=graph, pb=pb, out=out, filled=0)
             self._graphs[key] = ent
             st = _lib.stream_handle(dev)
@@ -531,11 +543,13 @@ class HipForward:
         hid = None if fused else torch.empty((B, S, 2 * C), dtype=bf, device=dev)
 
         conv_common = dict(idx=idx, taps=7, idx_stride=7, mask8=mask8, B=B, N=N, stream=st)
+        self._mark("start")
         launch_conv(
             x=xin, x_sb=N * 32, x_sn=32, wpack=P.stem.w, bias=P.stem.b, cin_pad=32, cout=C,
             ln_w=P.stem.lnw, ln_b=P.stem.lnb, eps=P.stem.eps, relu=True,
             out=cells, o_sb=S * C, o_sn=C, **conv_common,
         )
+        self._mark("stem")
         ci = ai = 0
         rows = B * S
         for kind in P.layout:
@@ -549,18 +563,21 @@ class HipForward:
                         w2=k.w2, b2=k.b2, ln2_w=k.ln2w, ln2_b=k.ln2b, eps2=k.eps2,
                         gamma=k.gamma, out=cells, o_sb=S * C, o_sn=C, stream=st,
                     )
+                    self._mark("conv_block")
                     continue
                 launch_conv(
                     x=cells, x_sb=S * C, x_sn=C, wpack=k.w1, bias=k.b1, cin_pad=C, cout=C,
                     ln_w=k.ln1w, ln_b=k.ln1b, eps=k.eps1, relu=True,
                     out=y1, o_sb=N * C, o_sn=C, **conv_common,
                 )
+                self._mark("conv1")
                 launch_conv(
                     x=y1, x_sb=N * C, x_sn=C, wpack=k.w2, bias=k.b2, cin_pad=C, cout=C,
                     ln_w=k.ln2w, ln_b=k.ln2b, eps=k.eps2, relu=False,
                     resid=cells, r_sb=S * C, r_sn=C, gamma=k.gamma,
                     out=cells, o_sb=S * C, o_sn=C, **conv_common,
                 )
+                self._mark("conv2")
             else:
                 a = P.attn[ai]
                 ai += 1
@@ -573,23 +590,28 @@ class HipForward:
                 if attn_fused:
                     launch_attn_fused(x=seq, x_sb=S * C, x_sr=C, packed=a.qkv, eps=a.eps1,
                                       **bias_args)
+                    self._mark("attn_fused")
                 elif P.fused_qkv and self.use_fused_qkv:
                     launch_attn_qkv(x=seq, x_sr=C, qkv=qkv, packed=a.qkv, eps=a.eps1, rows=rows,
                                     B=B, S=S, H=H, C=C, dpad=dpad, stream=st)
+                    self._mark("qkv")
                 else:
                     launch_linear(
                         x=seq, x_sr=C, wpack=a.qkv_w, bias=a.qkv_b, rows=rows, n_in=C,
                         n_out=3 * C, mode=_lib.LIN_QKV, out=qkv, ln_w=a.ln1w, ln_b=a.ln1b,
                         eps=a.eps1, B=B, S=S, H=H, dpad=dpad, stream=st,
                     )
+                    self._mark("qkv")
                 if not attn_fused:
                     launch_attn(q=qkv[0], k=qkv[1], v=qkv[2], qkv_sb=H * S * dpad,
                                 qkv_sh=S * dpad, **bias_args)
+                    self._mark("attn")
                 if fused:
                     launch_attn_mlp(
                         x=att, x_sr=C, seq=seq, s_sr=C, mask=seq_mask, packed=a.mlp,
                         eps=a.eps2, rows=rows, C=C, hidden=2 * C, stream=st,
                     )
+                    self._mark("mlp")
                     continue
                 launch_linear(
                     x=att, x_sr=C, wpack=a.out_w, bias=a.out_b, rows=rows, n_in=C, n_out=C,
@@ -606,6 +628,7 @@ class HipForward:
                     n_out=C, mode=_lib.LIN_RESID, out=seq, o_sr=C, resid=seq, r_sr=C,
                     gamma=a.g_mlp, mask=seq_mask, stream=st,
                 )
+                self._mark("mlp")
 
         seqf = torch.empty((B, S, C), dtype=bf, device=dev)
         value = torch.empty((B, VALUE_BINS), dtype=torch.float32, device=dev)
@@ -621,12 +644,14 @@ class HipForward:
             B=B, S=S, n_tokens=NUM_TOKENS, C=C, bins=VALUE_BINS,
         )
         _lib.check(lib.shrimp_trunk_tail(ctypes.byref(tail), st), "trunk_tail")
+        self._mark("tail")
         policy = torch.empty((B, N), dtype=torch.float32, device=dev)
         launch_conv(
             x=seqf[:, NUM_TOKENS:], x_sb=S * C, x_sn=C, wpack=P.policy.w, bias=P.policy.b,
             cin_pad=C, cout=C, relu=True, head_w=P.policy.hw, head_b=P.policy.hb,
             head_out=policy, **conv_common,
         )
+        self._mark("policy")
         out = {"policy": policy, "value": value}
         if request_moves_left:
             out["moves_left"] = ml
@@ -685,8 +710,10 @@ class HipForward:
             )
             _lib.check(lib.shrimp_linear_f32(ctypes.byref(a), st), "linear_f32")
 
+        self._mark("start")
         conv(pb.xin32, N * 16, 16, P.stem.w, P.stem.b, 16, ln_w=P.stem.lnw, ln_b=P.stem.lnb,
              eps=P.stem.eps, relu=True, out=cells, o_sb=S * C, o_sn=C)
+        self._mark("stem")
         ci = ai = 0
         for kind in P.layout:
             if kind == "C":
@@ -694,13 +721,16 @@ class HipForward:
                 ci += 1
                 conv(cells, S * C, C, k.w1, k.b1, C, ln_w=k.ln1w, ln_b=k.ln1b, eps=k.eps1,
                      relu=True, out=y1, o_sb=N * C, o_sn=C)
+                self._mark("conv1")
                 conv(y1, N * C, C, k.w2, k.b2, C, ln_w=k.ln2w, ln_b=k.ln2b, eps=k.eps2,
                      resid=cells, gamma=k.gamma, out=cells, o_sb=S * C, o_sn=C)
+                self._mark("conv2")
                 continue
             a = P.attn[ai]
             ai += 1
             linear(seq, C, a.qkv_w, a.qkv_b, C, 3 * C, _lib.LIN_QKV, qkv, ln_w=a.ln1w,
                    ln_b=a.ln1b, eps=a.eps1)
+            self._mark("qkv")
             at = _lib.AttnArgs(
                 q=qkv[0].data_ptr(), k=qkv[1].data_ptr(), v=qkv[2].data_ptr(), qkv_sb=H * S * d,
                 qkv_sh=S * d, seq_lens=seq_lens.data_ptr(), pair=None, p_sb=0, p_sq=0,
@@ -709,12 +739,14 @@ class HipForward:
                 o=att.data_ptr(), o_sb=S * C, o_sh=d, o_sr=C, B=B, S=S, H=H, d=d, dpad=d,
             )
             _lib.check(lib.shrimp_attn_f32(ctypes.byref(at), st), "attn_f32")
+            self._mark("attn")
             linear(att, C, a.out_w, a.out_b, C, C, _lib.LIN_RESID, seq, o_sr=C, resid=seq, r_sr=C,
                    gamma=a.g_attn, mask=seq_mask)
             linear(seq, C, a.fc1_w, a.fc1_b, C, 2 * C, _lib.LIN_GELU, hid, o_sr=2 * C,
                    ln_w=a.ln2w, ln_b=a.ln2b, eps=a.eps2)
             linear(hid, 2 * C, a.fc2_w, a.fc2_b, 2 * C, C, _lib.LIN_RESID, seq, o_sr=C, resid=seq,
                    r_sr=C, gamma=a.g_mlp, mask=seq_mask)
+            self._mark("mlp")
 
         seqf = torch.empty((B, S, C), dtype=f, device=dev)
         value = torch.empty((B, VALUE_BINS), dtype=f, device=dev)
@@ -730,9 +762,11 @@ class HipForward:
             B=B, S=S, n_tokens=NUM_TOKENS, C=C, bins=VALUE_BINS,
         )
         _lib.check(lib.shrimp_trunk_tail_f32(ctypes.byref(tail), st), "trunk_tail_f32")
+        self._mark("tail")
         policy = torch.empty((B, N), dtype=f, device=dev)
         conv(seqf[:, NUM_TOKENS:], S * C, C, P.policy.w, P.policy.b, C, relu=True,
              head_w=P.policy.hw, head_b=P.policy.hb, head_out=policy)
+        self._mark("policy")
         out = {"policy": policy, "value": value}
         if request_moves_left:
             out["moves_left"] = ml

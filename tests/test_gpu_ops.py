@@ -548,11 +548,17 @@ def test_attn_pair_op(d, S, lens, attn_variant):
     close(got, want, atol=1e-2, what=f"attn d={d}")
 
 
-def test_attn_offset_table_cfg2(attn_variant):
+@pytest.mark.parametrize("qk_gain", [1.0, 12.0])
+def test_attn_offset_table_cfg2(attn_variant, qk_gain):
+    """Config 2's attention at B=4 against the oracle; qk_gain 12 gives
+    softmax rows dominated by one key (scores spread over ~100 in log2
+    units)."""
+
     from shrimp import ops, synthetic
 
     case = synthetic.attention_inputs(4, heads=8, d=16)
     q, k, v = (torch.from_numpy(case[n]) for n in ("q", "k", "v"))
+    q, k = q * qk_gain, k * qk_gain
     B, H, S, d = q.shape
     table = torch.from_numpy(case["table"])  # (33*33, H)
     btab = torch.cat([table, torch.zeros(3, H)]) * (1.0 / math.log(2.0))
@@ -747,12 +753,16 @@ def cfg2_full():
     return synthetic.attention_inputs(1024, heads=8, d=16)
 
 
-def test_cfg2_attention_full_shape(cfg2_full, attn_variant):
+@pytest.mark.parametrize("linear", [False, True], ids=["clamped", "linear"])
+def test_cfg2_attention_full_shape(cfg2_full, attn_variant, linear):
     """Config 2's op at its own shape (B=1024, H=8, L=256, d=16, lengths
     U[64, 256], 33x33 per-head offset table): finite, rows past each length
     exactly zero, sampled positions against the oracle (attn_offset_table,
-    pinned against the reference's pair rows), and equal to a sub-batch run."""
+    pinned against the reference's pair rows), and equal to a sub-batch run.
+    Clamped: the clamped-LUT path; linear: with the unclamped fp16 offset
+    table (bench.cfg2_xtab) the compact positions take the linear path."""
 
+    from bench import cfg2_xtab
     from shrimp import ops
 
     c = cfg2_full
@@ -760,6 +770,7 @@ def test_cfg2_attention_full_shape(cfg2_full, attn_variant):
     B, H, S, d = q.shape
     table = torch.from_numpy(c["table"])
     btab = (torch.cat([table, torch.zeros(3, H)]) * (1.0 / math.log(2.0))).to(DEV).contiguous()
+    xtab = cfg2_xtab(btab, 16) if linear else None
     coords, mask, lens = (torch.from_numpy(c[n]) for n in ("coords", "mask", "lens"))
 
     def run(rows):
@@ -770,11 +781,12 @@ def test_cfg2_attention_full_shape(cfg2_full, attn_variant):
             q=qd, k=kd, v=vd, qkv_sb=H * S * d, qkv_sh=S * d, seq_lens=lens[rows].to(DEV), o=out,
             o_sb=H * S * d, o_sh=S * d, o_sr=d, B=n, S=S, H=H, d=d, dpad=16,
             coords=coords[rows].to(DEV, torch.int32).contiguous(),
-            mask8=mask[rows].to(DEV, torch.uint8).contiguous(), btab=btab, lut_m=16, n_tokens=0,
+            mask8=mask[rows].to(DEV, torch.uint8).contiguous(), btab=btab, xtab=xtab, lut_m=16,
+            n_tokens=0,
         )
         return out.cpu()
 
-    print(f"cfg2 attention B={B}", flush=True)
+    print(f"cfg2 attention B={B} linear={linear}", flush=True)
     full = run(list(range(B)))
     assert torch.isfinite(full.float()).all()
     for i in range(B):
