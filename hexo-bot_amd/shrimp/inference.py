@@ -130,6 +130,14 @@ class ShrimpEvaluator:
         legal = np.frombuffer(payload["legal_counts"], dtype=np.int32)
         if legal.shape[0] != b:
             raise ValueError("legal_counts byte count mismatch")
+        sizes = offsets[1:] - offsets[:-1]
+        if b and (sizes < 0).any():
+            raise ValueError("node_row_offsets must be non-decreasing")
+        if b > 1 and (sizes[1:] > sizes[:-1]).any():
+            # plan_groups pads each group to its first (largest) row
+            raise ValueError("rows must arrive sorted by support size, descending")
+        if b and ((legal < 0) | (legal > sizes)).any():
+            raise ValueError("legal_counts must lie in [0, row size]")
         feats = np.frombuffer(payload["node_feats"], dtype=np.float16)
         if feats.shape[0] != total * NUM_FEATURES:
             raise ValueError("node_feats byte count mismatch")

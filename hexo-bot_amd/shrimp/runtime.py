@@ -121,6 +121,9 @@ class HipForward:
         self._empty_rows: dict = {}
         # "bf16" (bf16 activations, fp32 accumulation) or "fp32"
         self.precision = default_precision()
+        # Largest batch of one forward launch sequence (None: the buffer limit
+        # below); forward() splits larger batches into independent slices.
+        self.max_batch = None
         # When a list, eager forwards append (name, event) after each launch
         # (HIP events on the launch stream) so a caller can read per-kernel
         # times inside a real forward; None (the default) records nothing.
@@ -369,6 +372,12 @@ class HipForward:
             raise ValueError("forward_csr: node_feats must be (T, F) with F <= 32")
         if row0 < 0 or row0 + B + 1 > row_offsets.shape[0]:
             raise ValueError("forward_csr: rows outside row_offsets")
+        lim = self.batch_limit(N)
+        if B > lim:
+            parts = [self.forward_csr(node_feats, node_qr, nbr, row_offsets, row0 + i,
+                                      min(lim, B - i), N, request_moves_left=request_moves_left)
+                     for i in range(0, B, lim)]
+            return {k: torch.cat([p[k] for p in parts]) for k in parts[0]}
         lib = _lib.load()
         st = _lib.stream_handle(dev)
         pb = self._prep_buffers(B, N, dev)
@@ -429,8 +438,9 @@ class HipForward:
                           *, request_moves_left: bool = False):
         """forward_csr through a captured HIP graph; None when B is above the
         largest bucket (the caller runs forward_csr). The returned tensors are
-        views of the capture's static outputs: valid until the next call with
-        the same bucket, so a caller consumes them (or clones) before that."""
+        views of the capture's static outputs, and all captures share one
+        memory pool: they are valid until the next graph replay of any bucket,
+        so a caller consumes them (or clones) before that."""
 
         bb = self.graph_bucket(B)
         if bb is None:
@@ -475,11 +485,35 @@ class HipForward:
         ent.graph.replay()
         return {k: v[:B] for k, v in ent.out.items()}
 
+    # Kernels address activation rows through buffer resources with 32-bit
+    # byte offsets: every activation buffer of one launch stays below this.
+    BUFFER_LIMIT = 0x7FFF0000
+
+    def batch_limit(self, N: int) -> int:
+        """Positions one forward can take at Npad = N: the widest per-position
+        activation buffer (the MLP hidden (S, 2C) or q/k/v (H, S, dpad)) times
+        the batch stays under BUFFER_LIMIT bytes; max_batch caps it further."""
+
+        net = self.net
+        c, h = net.channels, net.heads
+        width = max(2 * c, h * head_dim_pad(c // h))
+        elem = 4 if self.fp32 else 2
+        lim = max(1, (self.BUFFER_LIMIT - 1) // ((N + NUM_TOKENS) * width * elem))
+        return lim if self.max_batch is None else max(1, min(lim, int(self.max_batch)))
+
     @torch.no_grad()
     def forward(self, feats, nbr, mask, coords, *, request_moves_left: bool = False) -> dict:
         require_device(feats, "ShrimpNet.forward_policy_value")
         dev = feats.device
         B, N, F = feats.shape
+        lim = self.batch_limit(N)
+        if B > lim:
+            # rows are independent (per-position LayerNorm, masks, attention):
+            # slices of at most `lim` positions give the same rows
+            parts = [self.forward(feats[i:i + lim], nbr[i:i + lim], mask[i:i + lim],
+                                  coords[i:i + lim], request_moves_left=request_moves_left)
+                     for i in range(0, B, lim)]
+            return {k: torch.cat([p[k] for p in parts]) for k in parts[0]}
         if nbr.dtype not in _NBR_DT or feats.dtype not in _FEAT_DT or coords.dtype not in _COORD_DT:
             raise TypeError(
                 f"unsupported dtypes feats={feats.dtype} nbr={nbr.dtype} coords={coords.dtype}"

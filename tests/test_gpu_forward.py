@@ -257,6 +257,27 @@ def test_rows_are_independent_of_batch(cfg4_batch):
         assert torch.equal(full[key][sub], part[key]), key
 
 
+def test_batches_above_the_limit_split_bit_exact(cfg4_batch):
+    """A batch above the runtime's per-launch limit runs as slices: the
+    outputs equal the unsplit forward's bit for bit (rows are independent)."""
+
+    b = cfg4_batch
+    net = _net(128, 8, "CCACCACCACCA", seed=5)
+    rt = net.hip_runtime()
+    args = [torch.as_tensor(b[k][:12]).to(DEV) for k in ("feats", "nbr", "mask", "coords")]
+    full = rt.forward(*args, request_moves_left=True)
+    full = {k: v.clone() for k, v in full.items()}
+    rt.max_batch = 5
+    try:
+        assert rt.batch_limit(args[0].shape[1]) == 5
+        split = rt.forward(*args, request_moves_left=True)
+    finally:
+        rt.max_batch = None
+    for key in ("policy", "value", "moves_left"):
+        assert split[key].shape == full[key].shape, key
+        assert torch.equal(split[key], full[key]), key
+
+
 @pytest.mark.parametrize("graphs", [False, True], ids=["eager", "graphs"])
 def test_evaluator_matches_reference_reply(golden, graphs):
     """The reference evaluator's reply (ShrimpEvaluator(net, "cpu"), written

@@ -142,3 +142,75 @@ def test_serve_payload_matches_the_oracle_builder():
     assert order == worder
     for key in ("abi", "shape", "node_feats", "node_qr", "node_row_offsets", "nbr", "legal_counts"):
         assert payload[key] == want[key], key
+
+
+def test_batch_limit_keeps_buffers_under_32_bit_offsets():
+    """One forward launch sequence takes at most as many positions as keep its
+    widest activation buffer (MLP hidden (S, 2C), q/k/v (H, S, dpad)) below the
+    32-bit buffer-offset limit; max_batch lowers it further."""
+
+    from shrimp.model import ShrimpNet
+    from shrimp.runtime import HipForward
+
+    rt = HipForward(ShrimpNet(channels=128, attention_heads=8, trunk_layout="CCACCACCACCA"))
+    rt.precision = "bf16"
+    lim = rt.batch_limit(256)
+    assert lim == (HipForward.BUFFER_LIMIT - 1) // (264 * 256 * 2)
+    assert lim * 264 * 256 * 2 < 2 ** 31
+    rt.precision = "fp32"
+    assert rt.batch_limit(256) == (HipForward.BUFFER_LIMIT - 1) // (264 * 256 * 4)
+    rt.max_batch = 7
+    assert rt.batch_limit(256) == 7
+    assert rt.batch_limit(10 ** 7) == 1
+
+
+def _payload(sizes, legal):
+    total = int(sum(sizes))
+    return {
+        "abi": 1, "shape": (len(sizes), total),
+        "node_feats": np.zeros((total, C.NUM_FEATURES), np.float16).tobytes(),
+        "node_qr": np.zeros((total, 2), np.int16).tobytes(),
+        "node_row_offsets": np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64),
+        "nbr": np.full((total, 6), 0xFFFF, np.uint16).tobytes(),
+        "legal_counts": np.asarray(legal, np.int32).tobytes(),
+    }
+
+
+def test_evaluator_payload_validation():
+    """The serve side refuses payloads whose rows break the wire contract
+    before anything is uploaded (inference.py:509-531 checks shape and byte
+    counts; rows sorted by size and legal counts within the row are what
+    plan_groups and the decode rely on)."""
+
+    from shrimp.inference import ShrimpEvaluator
+
+    parse = ShrimpEvaluator._parse
+    b, total, *_ = parse(_payload([70, 64, 10], [5, 64, 0]))
+    assert (b, total) == (3, 144)
+    assert parse(_payload([], []))[0] == 0
+    with pytest.raises(ValueError, match="sorted by support size"):
+        parse(_payload([10, 70], [1, 1]))
+    with pytest.raises(ValueError, match="legal_counts must lie"):
+        parse(_payload([70, 64], [71, 1]))
+    with pytest.raises(ValueError, match="legal_counts must lie"):
+        parse(_payload([70, 64], [1, -1]))
+    bad = _payload([70, 64], [1, 1])
+    bad["abi"] = 2
+    with pytest.raises(ValueError, match="ABI"):
+        parse(bad)
+    bad = _payload([70, 64], [1, 1])
+    bad["node_row_offsets"] = np.array([0, 50, 134], np.int64)
+    with pytest.raises(ValueError, match="sorted"):
+        parse(bad)
+    bad = _payload([70, 64], [1, 1])
+    bad["node_row_offsets"] = np.array([0, 140, 134], np.int64)
+    with pytest.raises(ValueError, match="non-decreasing"):
+        parse(bad)
+    bad = _payload([70, 64], [1, 1])
+    bad["legal_counts"] = bad["legal_counts"][:4]
+    with pytest.raises(ValueError, match="legal_counts byte count"):
+        parse(bad)
+    bad = _payload([70, 64], [1, 1])
+    bad["nbr"] = bad["nbr"][:-12]
+    with pytest.raises(ValueError, match="nbr byte count"):
+        parse(bad)
