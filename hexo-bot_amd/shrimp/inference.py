@@ -31,6 +31,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import time
 
 import numpy as np
 import torch
@@ -82,6 +83,63 @@ def plan_groups(sizes) -> list:
     return groups
 
 
+class GpuBusyTrace:
+    """Device-busy instrument of the serve loop (SHRIMP_PERF_TRACE=1), with the
+    report of the reference's PerfTrace (inference.py:113-199).
+
+    submit_payload records a timing event on the compute stream before its
+    first pack and one after its last decode; result reads the pair once the
+    payload's work has finished (it waits for that anyway), so tracing adds two
+    event records per payload and no synchronisation. Busy fraction = summed
+    device time of the payloads / wall time from the first submit to the last
+    result."""
+
+    def __init__(self) -> None:
+        self.flush_ms: list = []
+        self.flush_states: list = []
+        self._t_first = None
+        self._t_last = None
+
+    def begin(self, stream) -> tuple:
+        if self._t_first is None:
+            self._t_first = time.perf_counter()
+        start = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        return start, torch.cuda.Event(enable_timing=True)
+
+    def finish(self, events, n_states: int) -> None:
+        """After the payload's outputs are on the host (both events done)."""
+
+        self._t_last = time.perf_counter()
+        start, end = events
+        self.flush_ms.append(float(start.elapsed_time(end)))
+        self.flush_states.append(int(n_states))
+
+    def report(self) -> dict:
+        ms, st = self.flush_ms, self.flush_states
+        wall = 0.0
+        if self._t_first is not None and self._t_last is not None:
+            wall = max(0.0, (self._t_last - self._t_first) * 1e3)
+        busy_ms = float(sum(ms))
+        busy = busy_ms / wall if wall > 0 else 0.0
+        n, states = len(ms), int(sum(st))
+        rep = {
+            "gpu_busy_fraction": round(busy, 4),
+            "gpu_idle_fraction": round(1.0 - busy, 4) if wall > 0 else None,
+            "device_busy_ms": round(busy_ms, 2),
+            "wall_window_ms": round(wall, 2),
+            "measured_flushes": n,
+            "measured_states": states,
+            "mean_batch": round(states / n, 1) if n else 0.0,
+            "mean_forward_ms": round(busy_ms / n, 3) if n else 0.0,
+            "mean_ms_per_state": round(busy_ms / states, 4) if states else 0.0,
+        }
+        if n >= 2:
+            rep["median_forward_ms"] = round(float(np.median(ms)), 3)
+            rep["median_batch"] = round(float(np.median(st)), 1)
+        return rep
+
+
 class ShrimpEvaluator:
     """graphs: replay each group's forward from a captured HIP graph keyed by
     (batch bucket, Npad, moves-left) instead of launching its kernels one by
@@ -103,6 +161,7 @@ class ShrimpEvaluator:
         # which saves the cross-stream waits.
         self._copy_stream = None
         self._inflight = 0
+        self._perf = GpuBusyTrace() if os.environ.get("SHRIMP_PERF_TRACE") == "1" else None
 
     def _copies(self) -> torch.cuda.Stream:
         if self._copy_stream is None:
@@ -116,8 +175,10 @@ class ShrimpEvaluator:
     def evaluate_payload(self, payload: dict) -> dict:
         return self.result(self.submit_payload(payload))
 
-    def perf_trace_report(self):
-        return None
+    def perf_trace_report(self) -> dict | None:
+        """GpuBusyTrace report; None unless SHRIMP_PERF_TRACE=1 (inference.py:505-507)."""
+
+        return self._perf.report() if self._perf is not None else None
 
     @staticmethod
     def _parse(payload: dict):
@@ -179,6 +240,7 @@ class ShrimpEvaluator:
         lib = _lib.load()
         stream = _lib.stream_handle(dev)
         rt = self.model.hip_runtime()
+        perf = self._perf.begin(compute) if self._perf is not None else None
         for start, end, pad_to in plan_groups(sizes):
             g = end - start
             csr = (d_feats, d_qr, d_nbr, d_rows)
@@ -199,13 +261,15 @@ class ShrimpEvaluator:
                 ),
                 "decode",
             )
+        if perf is not None:
+            perf[1].record(compute)
         done = torch.cuda.Event()
         done.record(compute)
         self._inflight += 1
         return {
             "b": b, "request_ml": request_ml, "request_logits": request_logits,
             "values_gpu": values, "ml_gpu": ml, "priors_gpu": priors, "logits_gpu": logits,
-            "done": done,
+            "done": done, "perf": perf,
         }
 
     @torch.no_grad()
@@ -222,8 +286,10 @@ class ShrimpEvaluator:
         self._inflight = max(0, self._inflight - 1)
         if self._inflight == 0:
             # nothing was submitted after this payload: copy on its own stream
-            return {key: handle[src].cpu().numpy().astype(np.float32, copy=False).tobytes()
-                    for key, src in names}
+            reply = {key: handle[src].cpu().numpy().astype(np.float32, copy=False).tobytes()
+                     for key, src in names}
+            self._trace(handle)
+            return reply
         copies = self._copies()
         host = {}
         with torch.cuda.stream(copies):
@@ -237,4 +303,10 @@ class ShrimpEvaluator:
             fetched = torch.cuda.Event()
             fetched.record(copies)
         fetched.synchronize()
+        self._trace(handle)
         return {key: host[key].numpy().astype(np.float32, copy=False).tobytes() for key, _ in names}
+
+    def _trace(self, handle: dict) -> None:
+        if self._perf is not None and handle.get("perf") is not None:
+            handle["perf"][1].synchronize()
+            self._perf.finish(handle["perf"], handle["b"])

@@ -474,3 +474,29 @@ def test_evaluator_pipelined_submissions_match(graphs):
         assert set(got) == set(want[i])
         for key in want[i]:
             assert got[key] == want[i][key], (i, key)
+
+
+def test_evaluator_busy_trace_counts_every_payload():
+    """With the busy trace on (SHRIMP_PERF_TRACE=1 sets it), every collected
+    payload adds its device time and rows to the report; tracing leaves the
+    reply bytes unchanged."""
+
+    from shrimp import synthetic
+    from shrimp.inference import GpuBusyTrace, ShrimpEvaluator
+
+    net = _net(128, 8, "CCACCACCACCA", seed=9)
+    ev = ShrimpEvaluator(net, DEV)
+    assert ev.perf_trace_report() is None
+    pays = [synthetic.serve_payload("cfg4", n, seed=s)[0] for n, s in ((40, 21), (9, 22), (64, 23))]
+    want = [ev.evaluate_payload(p) for p in pays]
+    ev._perf = GpuBusyTrace()
+    got = [ev.evaluate_payload(pays[0])]
+    handles = [ev.submit_payload(p) for p in pays[1:]]
+    got += [ev.result(h) for h in handles]
+    assert got == want
+    rep = ev.perf_trace_report()
+    print("busy trace:", rep, flush=True)
+    assert rep["measured_flushes"] == 3 and rep["measured_states"] == 113
+    assert rep["device_busy_ms"] > 0 and rep["wall_window_ms"] > 0
+    assert 0 < rep["gpu_busy_fraction"] <= 1.5
+    assert rep["mean_batch"] == round(113 / 3, 1) and rep["median_batch"] == 40.0

@@ -214,3 +214,31 @@ def test_evaluator_payload_validation():
     bad["nbr"] = bad["nbr"][:-12]
     with pytest.raises(ValueError, match="nbr byte count"):
         parse(bad)
+
+
+def test_busy_trace_report_arithmetic():
+    """GpuBusyTrace's report (the keys of the reference's PerfTrace report,
+    inference.py:171-199) from known per-payload device times."""
+
+    from shrimp.inference import GpuBusyTrace
+
+    class _Ev:
+        def __init__(self, ms):
+            self.ms = ms
+
+        def elapsed_time(self, other):
+            return other.ms - self.ms
+
+    tr = GpuBusyTrace()
+    assert tr.report()["gpu_idle_fraction"] is None
+    tr._t_first = 100.0
+    for n, (a, b) in ((10, (0.0, 2.0)), (30, (5.0, 9.0)), (20, (9.0, 15.0))):
+        tr.finish((_Ev(a), _Ev(b)), n)
+    tr._t_last = 100.024
+    rep = tr.report()
+    assert rep["device_busy_ms"] == 12.0 and rep["wall_window_ms"] == 24.0
+    assert rep["gpu_busy_fraction"] == 0.5 and rep["gpu_idle_fraction"] == 0.5
+    assert rep["measured_flushes"] == 3 and rep["measured_states"] == 60
+    assert rep["mean_batch"] == 20.0 and rep["median_batch"] == 20.0
+    assert rep["mean_forward_ms"] == 4.0 and rep["median_forward_ms"] == 4.0
+    assert rep["mean_ms_per_state"] == 0.2
