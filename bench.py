@@ -103,7 +103,14 @@ def kernel_timings(net, inputs, reps=50):
         xtab=a.btab_xtab[1], lut_m=CELL_LUT_M, n_tokens=8, stream=L["stream"],
     )
 
+    staged = bool(L.get("staged"))
+
     def attn():
+        if staged:
+            kw = {k: v for k, v in bias_kw.items() if k not in ("coords", "mask8")}
+            ops.launch_attn_staged(q=qkv[0], qkv_sb=H * s * P.dpad, qkv_sh=s * P.dpad,
+                                   kvf=L["kvf"], meta=L["meta"], **kw)
+            return
         ops.launch_attn(q=qkv[0], k=qkv[1], v=qkv[2], qkv_sb=H * s * P.dpad,
                         qkv_sh=s * P.dpad, **bias_kw)
 
@@ -122,7 +129,9 @@ def kernel_timings(net, inputs, reps=50):
     # Timing re-launches write into the forward's scratch buffers only (never
     # back into seq): residual modes target a copy.
     seq_copy = seq.clone()
-    qkv_fn = (lambda: ops.launch_attn_qkv(
+    qkv_fn = (lambda: ops.launch_attn_qkv_kvf(
+        x=seq, x_sr=C, q=qkv, kvf=L["kvf"], packed=a.qkv, eps=a.eps1, rows=rows, B=b, S=s, H=H,
+        C=C, dpad=P.dpad, stream=L["stream"])) if staged else (lambda: ops.launch_attn_qkv(
         x=seq, x_sr=C, qkv=qkv[0], packed=a.qkv, eps=a.eps1, rows=rows, B=b, S=s, H=H, C=C,
         dpad=P.dpad, stream=L["stream"])) if P.fused_qkv else lin(
             _lib.LIN_QKV, seq, C, a.qkv_w, a.qkv_b, C, 3 * C, qkv[0], 0, ln_w=a.ln1w,
@@ -176,6 +185,7 @@ def kernel_timings(net, inputs, reps=50):
         "conv_flops_valid": 2.0 * 7 * C * C * valid_rows,
         "conv_bytes": b * n * C * 2 * 2 + b * n * 7 * 4 + 7 * C * C * 2,
         "attn_ms": attn_ms,
+        "attn_staged": staged,
         "attn_fused_ms": fused_ms,
         "forward_attn_fused": bool(L["attn_fused"]),
         "attn_flops": float(4 * P.d * H * (seq_lens ** 2).sum().item()),

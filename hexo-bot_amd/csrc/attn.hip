@@ -47,6 +47,29 @@ constexpr int XW = 2 * XD + 1;
 
 SHRIMP_DEV int clampi(int x, int m) { return min(max(x, -m), m); }
 
+// LDS byte addresses as plain integers: table reads at a computed address
+// then need no base pointer added per read.
+typedef __attribute__((address_space(3))) const unsigned char lds_cu8;
+typedef __attribute__((address_space(3))) void lds_dst_t;
+SHRIMP_DEV int lds_addr(const void* p) { return (int)(uintptr_t)(lds_cu8*)p; }
+SHRIMP_DEV unsigned lds_u32(int addr) {
+  return *(__attribute__((address_space(3))) const unsigned*)(uintptr_t)(unsigned)addr;
+}
+SHRIMP_DEV float lds_f16(int addr) {
+  return (float)*(__attribute__((address_space(3))) const _Float16*)(uintptr_t)(unsigned)addr;
+}
+
+// Key table of one position (shrimp_attn_keys), int32 words laid out as the
+// attention kernel's LDS region that starts at kqr:
+//   [kqr: 2 SP][kkey: SP][kcls: SP][blk_gen: NKB][q_gen: NKB][blk_dead: NKB][hdr: 8]
+// padded to 16 bytes. kkey holds the relative LINEAR code (q XW + r) 2 HG of
+// the key (token and dead keys: of the live cell (q0, r0)) for two heads per
+// workgroup; hdr holds the span test and (q0, r0).
+enum : int { HDR_SPAN_OK = 0, HDR_SAFE_Q = 1, HDR_SAFE_R = 2 };
+__host__ __device__ inline int attn_meta_ints(int SP) {
+  return (4 * SP + 3 * (SP / 16) + 8 + 3) & ~3;
+}
+
 template <int HG>
 struct AttnLds {
   unsigned short* Ks;  // [HG][KD][SP/16] K fragments (256 bf16 each)
@@ -54,7 +77,6 @@ struct AttnLds {
   int2* kqr;           // [SP] key coordinates
   int* kkey;           // [SP] LDS byte address of the key's table row for query
                        // offset code 0: xtab + (q*XW + r + XD*XW + XD) * 2 HG
-  const unsigned char* base;  // start of the dynamic LDS (kkey is relative to it)
   int* kcls;           // [SP] KEY_CELL / KEY_TOKEN / KEY_DEAD
   int* blk_gen;        // [SP / 16] 1 if the block holds a token or dead key
   int* blk_dead;       // [SP / 16] 1 if the block holds a dead key (or keys past the bound)
@@ -77,10 +99,10 @@ struct AttnQuery {
 //   FL_QTOK  the query block holds token queries: their biases toward cell
 //            keys are selected per lane;
 //   FL_KTOK  the chunk's first key block holds the token keys;
-//   FL_DEAD  the chunk holds dead keys: their V rows are staged as zeros and
-//            the row-sum MFMA weighs keys by liveness, so they drop out of
-//            both the output and the normaliser (their scores only enter the
-//            running maximum, which any finite value keeps exact).
+//   FL_DEAD  the chunk holds dead keys (masked cells, keys past the bound):
+//            they are left out of the maximum and get p = 0, so they drop out
+//            of the output and the normaliser whatever their K and V rows hold
+//            (finite values).
 enum : int { FL_QTOK = 1, FL_KTOK = 2, FL_DEAD = 4 };
 
 template <int DP, int HG, bool PAIR, int NBK, int PATH, int FL = 0>
@@ -135,19 +157,20 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
 #pragma unroll
         for (int h = 0; h < HG; ++h) bias[kb][j][h] = s.tab[p * HG + h];
       } else if (PATH == PATH_LINEAR) {
-        const char* xp = reinterpret_cast<const char*>(s.base) + (s.kkey[key] - qi.qkey);
+        const int xa = s.kkey[key] - qi.qkey;
         if (HG == 2) {
-          const unsigned w = *reinterpret_cast<const unsigned*>(xp);
+          const unsigned w = lds_u32(xa);
           bias[kb][j][0] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xFFFFu));
           bias[kb][j][HG - 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> 16));
         } else {
 #pragma unroll
-          for (int h = 0; h < HG; ++h) bias[kb][j][h] = (float)reinterpret_cast<const _Float16*>(xp)[h];
+          for (int h = 0; h < HG; ++h) bias[kb][j][h] = lds_f16(xa + 2 * h);
         }
         if (FL & FL_QTOK) {
 #pragma unroll
           for (int h = 0; h < HG; ++h) bias[kb][j][h] = qi.qtok ? ckb[h] : bias[kb][j][h];
         }
+        if (FL & FL_DEAD) live[kb][j] = s.kcls[key] != KEY_DEAD;
         if ((FL & FL_KTOK) && kb == 0) {
           const bool ktok = key < a.n_tokens;
 #pragma unroll
@@ -173,14 +196,7 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
   // Constant A fragment: row 0 of "V^T" is all ones, so P^T times it gives the
   // per-query sum of P in accumulator row 0 (lane group 0, element 0).
   const unsigned one2 = lr == 0 ? 0x3F803F80u : 0u;
-  // FL_DEAD: row 0 of the ones fragment carries 1 for live keys only.
-  // live2(key): bf16 pair (1 or 0 for keys key, key + 1) in row 0's lanes.
-  auto live2 = [&](int key) -> unsigned {
-    if (lr != 0) return 0u;
-    const unsigned lo = s.kcls[key] != KEY_DEAD ? 0x3F80u : 0u;
-    const unsigned hi = s.kcls[key + 1] != KEY_DEAD ? 0x3F80u : 0u;
-    return lo | (hi << 16);
-  };
+  constexpr bool MASKED = PATH == PATH_GENERAL || (PATH == PATH_LINEAR && (FL & FL_DEAD));
 #pragma unroll
   for (int h = 0; h < HG; ++h) {
     float sc[NBK][4];
@@ -190,7 +206,7 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float v = fmaf(sc4[h][kb][j], qk_scale, bias[kb][j][h]);
-        if (PATH == PATH_GENERAL) v = live[kb][j] ? v : SHRIMP_NEG_BIG;
+        if (MASKED) v = live[kb][j] ? v : SHRIMP_NEG_BIG;
         sc[kb][j] = v;
         mx = fmaxf(mx, v);
       }
@@ -205,7 +221,7 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         p[j] = __builtin_amdgcn_exp2f(sc[kb][j] - mnew);
-        if (PATH == PATH_GENERAL) p[j] = live[kb][j] ? p[j] : 0.f;
+        if (MASKED) p[j] = live[kb][j] ? p[j] : 0.f;
       }
       pf[kb].x = pack_bf16x2(p[0], p[1]);
       pf[kb].y = pack_bf16x2(p[2], p[3]);
@@ -215,12 +231,7 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
 #pragma unroll
     for (int kd = 0; kd < KD; ++kd) acc[kd] = o[h][kd] * alpha;
     if (NBK == 1) {
-      u32x2 ones = u32x2{one2, one2};
-      if (FL & FL_DEAD) {
-        const int k0 = kb0 * 16 + lg * 4;
-        ones = u32x2{live2(k0), live2(k0 + 2)};
-      }
-      lacc = mfma16x16x16(ones, pf[0], lacc);
+      lacc = mfma16x16x16(u32x2{one2, one2}, pf[0], lacc);
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd) {
         const u32x2 vf = *reinterpret_cast<const u32x2*>(vbase + (h * KD + kd) * NKB * 256);
@@ -231,12 +242,7 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
       for (int kp = 0; kp < NBK; kp += 2) {
         // k slots 0-3 of lane group g: keys 4g..4g+3 of block kp; 4-7: of kp+1.
         const u32x4 pp = u32x4{pf[kp].x, pf[kp].y, pf[kp + 1].x, pf[kp + 1].y};
-        u32x4 ones = u32x4{one2, one2, one2, one2};
-        if (FL & FL_DEAD) {
-          const int k0 = (kb0 + kp) * 16 + lg * 4;
-          ones = u32x4{live2(k0), live2(k0 + 2), live2(k0 + 16), live2(k0 + 18)};
-        }
-        lacc = mfma16x16x32(ones, pp, lacc);
+        lacc = mfma16x16x32(u32x4{one2, one2, one2, one2}, pp, lacc);
 #pragma unroll
         for (int kd = 0; kd < KD; ++kd) {
           const unsigned short* vf = vbase + (h * KD + kd) * NKB * 256 + kp * 256;
@@ -250,6 +256,126 @@ SHRIMP_DEV void attn_chunk(const shrimp_attn_args& a, const AttnLds<HG>& s, cons
 #pragma unroll
     for (int kd = 0; kd < KD; ++kd) o[h][kd] = acc[kd];
   }
+}
+
+// LINEAR chunk with a fixed softmax offset. After a query block's first
+// chunk (attn_chunk, which sets the running maximum m) the offset stays at
+// that m: the QK^T accumulators start from cinit = -m / qk_scale, so
+// fma(s, qk_scale, bias) is already score - m, and p = exp2 of it needs no
+// maximum, no rescale of o and l and no lane exchange. Any fixed offset gives
+// the same softmax; it only has to keep the row sums in range, so the chunk
+// checks them (l < 2^64 covers overflow to inf and NaN) and returns false with
+// o and l untouched when one leaves it; the caller then runs attn_chunk,
+// which moves the offset. Exceptions as in attn_chunk (FL_KTOK cannot occur:
+// key block 0 is always a first chunk); dead keys get p = 0, so the row-sum
+// operand stays all ones.
+template <int DP, int HG, int NBK, int FL>
+SHRIMP_DEV bool attn_chunk_lazy(const AttnLds<HG>& s, const AttnQuery& qi, int kb0, int SP, int lr,
+                                int lg, float qk_scale, const u32x2 (&qf)[HG][DP / 16],
+                                const float (&cinit)[HG], float (&l)[HG],
+                                f32x4 (&o)[HG][DP / 16]) {
+  static_assert((FL & FL_KTOK) == 0, "token keys only in first chunks");
+  constexpr int KD = DP / 16;
+  const int NKB = SP / 16;
+  const unsigned short* kbase = s.Ks + kb0 * 256 + (lg * 16 + lr) * 4;
+  const unsigned short* vbase = s.Vt + kb0 * 256 + (lg * 16 + lr) * 4;
+  f32x4 sc4[HG][NBK];
+#pragma unroll
+  for (int kb = 0; kb < NBK; ++kb)
+#pragma unroll
+    for (int h = 0; h < HG; ++h) {
+      f32x4 acc = f32x4{cinit[h], cinit[h], cinit[h], cinit[h]};
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) {
+        const u32x2 kf = *reinterpret_cast<const u32x2*>(kbase + (h * KD + kd) * NKB * 256 + kb * 256);
+        acc = mfma16x16x16(kf, qf[h][kd], acc);
+      }
+      sc4[h][kb] = acc;
+    }
+  float ckb[HG];
+  if (FL & FL_QTOK) {
+#pragma unroll
+    for (int h = 0; h < HG; ++h) ckb[h] = s.tokb[HG + h];
+  }
+  u32x2 pf[HG][NBK];
+#pragma unroll
+  for (int kb = 0; kb < NBK; ++kb) {
+    const int key0 = (kb0 + kb) * 16 + lg * 4;
+    int4 cls = int4{KEY_CELL, KEY_CELL, KEY_CELL, KEY_CELL};
+    if (FL & FL_DEAD) cls = *reinterpret_cast<const int4*>(s.kcls + key0);
+    const int4 kk = *reinterpret_cast<const int4*>(s.kkey + key0);
+    const int kkv[4] = {kk.x, kk.y, kk.z, kk.w};
+    const int clv[4] = {cls.x, cls.y, cls.z, cls.w};
+    float p[HG][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int xa = kkv[j] - qi.qkey;
+      float bias[HG];
+      if (HG == 2) {
+        const unsigned w = lds_u32(xa);
+        bias[0] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xFFFFu));
+        bias[HG - 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> 16));
+      } else {
+#pragma unroll
+        for (int h = 0; h < HG; ++h) bias[h] = lds_f16(xa + 2 * h);
+      }
+#pragma unroll
+      for (int h = 0; h < HG; ++h) {
+        if (FL & FL_QTOK) bias[h] = qi.qtok ? ckb[h] : bias[h];
+        p[h][j] = __builtin_amdgcn_exp2f(fmaf(sc4[h][kb][j], qk_scale, bias[h]));
+        if (FL & FL_DEAD) p[h][j] = clv[j] != KEY_DEAD ? p[h][j] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < HG; ++h) {
+      pf[h][kb].x = pack_bf16x2(p[h][0], p[h][1]);
+      pf[h][kb].y = pack_bf16x2(p[h][2], p[h][3]);
+    }
+  }
+  // row sums first (lane group 0, element 0; other lanes hold zeros): a
+  // chunk that takes one out of range returns before touching o
+  const unsigned one2 = lr == 0 ? 0x3F803F80u : 0u;
+  float ln[HG];
+  bool bad = false;
+#pragma unroll
+  for (int h = 0; h < HG; ++h) {
+    f32x4 lacc = f32x4{l[h], 0.f, 0.f, 0.f};
+    if (NBK == 1) {
+      lacc = mfma16x16x16(u32x2{one2, one2}, pf[h][0], lacc);
+    } else {
+#pragma unroll
+      for (int kp = 0; kp < NBK; kp += 2)
+        lacc = mfma16x16x32(u32x4{one2, one2, one2, one2},
+                            u32x4{pf[h][kp].x, pf[h][kp].y, pf[h][kp + 1].x, pf[h][kp + 1].y}, lacc);
+    }
+    ln[h] = lacc[0];
+    bad |= !(ln[h] < 0x1p64f);
+  }
+  if (__builtin_amdgcn_ballot_w64(bad) != 0) return false;
+#pragma unroll
+  for (int h = 0; h < HG; ++h) {
+    l[h] = ln[h];
+    if (NBK == 1) {
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) {
+        const u32x2 vf = *reinterpret_cast<const u32x2*>(vbase + (h * KD + kd) * NKB * 256);
+        o[h][kd] = mfma16x16x16(vf, pf[h][0], o[h][kd]);
+      }
+    } else {
+#pragma unroll
+      for (int kp = 0; kp < NBK; kp += 2) {
+        const u32x4 pp = u32x4{pf[h][kp].x, pf[h][kp].y, pf[h][kp + 1].x, pf[h][kp + 1].y};
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd) {
+          const unsigned short* vf = vbase + (h * KD + kd) * NKB * 256 + kp * 256;
+          const u32x2 v0 = *reinterpret_cast<const u32x2*>(vf);
+          const u32x2 v1 = *reinterpret_cast<const u32x2*>(vf + 256);
+          o[h][kd] = mfma16x16x32(u32x4{v0.x, v0.y, v1.x, v1.y}, pp, o[h][kd]);
+        }
+      }
+    }
+  }
+  return true;
 }
 
 // PROJ (1 or 2): q, k and v are not read from memory but projected in the
@@ -281,13 +407,17 @@ template <int DP, int HG, bool PAIR, int PROJ, int NW>
 __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const shrimp_attn_args a, float qk_scale,
                                                    uint32_t qkv_bytes, int npos,
                                                    const shrimp_attn_proj_args p, uint32_t x_bytes) {
-  static_assert(!PROJ || (DP == 16 && HG == 2 && !PAIR && NW == 4),
+  // PROJ 1, 2: q/k/v projected in the kernel; 3: staged (K and V fragments
+  // and the key table by DMA from shrimp_attn_qkv_kvf / shrimp_attn_keys)
+  constexpr bool PJ = PROJ == 1 || PROJ == 2;
+  constexpr bool STG = PROJ == 3;
+  static_assert(!PJ || (DP == 16 && HG == 2 && !PAIR && NW == 4),
                 "projection covers d = 16, two heads, coords, four waves");
+  static_assert(!STG || (DP == 16 && HG == 2 && !PAIR), "staged path covers d = 16, two heads, coords");
   static_assert(NW == 4 || NW == 8, "four or eight waves per workgroup");
   static_assert(HG == 1 || HG == 2, "one or two heads per workgroup");
   constexpr int NT = 64 * NW;  // threads per workgroup
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  __shared__ int span_red[4 * NW];
   constexpr int KD = DP / 16;
   int b = blockIdx.y;
   int h0 = blockIdx.x * HG;
@@ -315,11 +445,12 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
   s.blk_gen = s.kcls + SP;
   int* q_gen = s.blk_gen + NKB;
   s.blk_dead = q_gen + NKB;
-  s.tokb = reinterpret_cast<float*>(s.blk_dead + NKB);
-  float* tail = s.tokb + 3 * HG;
+  const int* hdr = s.blk_dead + NKB;
+  s.tokb = reinterpret_cast<float*>(reinterpret_cast<int*>(s.kqr) + attn_meta_ints(SP));
+  int* span_red = reinterpret_cast<int*>(s.tokb + 3 * HG);  // [NW][4]
+  float* tail = reinterpret_cast<float*>(span_red + 4 * NW);
   s.tab = tail;
   s.xtab = reinterpret_cast<_Float16*>(tail);
-  s.base = smem;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -346,7 +477,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
   // PROJ: row blocks this wave projects (nkb == nqb): its own blocks
   // wave + 4 j for j < nreg, then the split block's queries (waves 1-3).
   const int nreg = wave < nkb ? (nkb - wave + 3) / 4 : 0;
-  const int nitems = PROJ ? nreg + (split && wave > 0 ? 1 : 0) : 0;
+  const int nitems = PJ ? nreg + (split && wave > 0 ? 1 : 0) : 0;
   const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.x, x_bytes);
   // rows of one 16-row block: lane (lr, lg) loads channels 32 ks + 8 lg .. +7
   // of row blk * 16 + lr; rows past the bound read as zeros
@@ -359,8 +490,66 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
     for (int ks = 0; ks < 4; ++ks) xf[ks] = buf_load16(xrs, off + ks * 64);
   };
   u32x4 xnext[4];
-  if (PROJ && nitems > 0) load_x(0, xnext);
+  if (PJ && nitems > 0) load_x(0, xnext);
 
+  bool linear_ok = false;
+  int safe_q = 0, safe_r = 0;
+  int kdelta = 0;  // subtracted from a query's LINEAR code: kkey - qkey is the table address
+  if constexpr (STG) {
+    // K and V fragments of the two heads (shrimp_attn_qkv_kvf: per (position,
+    // head) SP/16 K fragments, then SP/16 V fragments, 512 bytes each), the
+    // position's key table (a.v, shrimp_attn_keys) and the head pair's
+    // offset table arrive by buffer-to-LDS DMA (no registers, no LDS store
+    // instructions). Fragment pieces of keys >= S read past the buffer and
+    // land as zeros.
+    const int H = a.H;
+    const __amdgpu_buffer_rsrc_t kvr = make_rsrc(a.k, (uint32_t)((int64_t)a.B * H * SP * 64));
+    const int mbytes = attn_meta_ints(SP) * 4;
+    const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.v, (uint32_t)((int64_t)a.B * mbytes));
+    // fragments f = (tensor, h, kb) in LDS order, two per 1 KiB DMA
+    const int nfr = 2 * HG * NKB;
+    const int half = lane >> 5, sub = lane & 31;
+    for (int i = wave; 2 * i < nfr; i += NW) {
+      const int f = 2 * i + half;
+      const int tensor = f >= HG * NKB ? 1 : 0;
+      const int r = f - tensor * HG * NKB;
+      const int h = r >= NKB ? 1 : 0;
+      const int kb = r - h * NKB;
+      // first key of this lane's 16 bytes: K slots (lg, lr), (lg, lr + 1) with
+      // lr = 2 (sub % 8) hold keys lr, lr + 1; V slots hold keys 4 lg .. + 3
+      const int key = kb * 16 + (tensor ? 4 * (sub >> 3) : 2 * (sub & 7));
+      const uint32_t off =
+          key < S ? (uint32_t)((((int64_t)b * H + h0 + h) * 2 + tensor) * SP * 32 + kb * 512 + sub * 16)
+                  : SHRIMP_OOB_OFFSET;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(kvr, (lds_dst_t*)(smem + i * 1024), 16, off, 0, 0, 0);
+    }
+    unsigned char* mdst = reinterpret_cast<unsigned char*>(s.kqr);
+    for (int i = wave; i * 1024 < mbytes; i += NW) {
+      const int o = i * 1024 + lane * 16;
+      if (o < mbytes)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(mr, (lds_dst_t*)(mdst + i * 1024), 16,
+                                                 (uint32_t)((int64_t)b * mbytes + o), 0, 0, 0);
+    }
+    // (XW*XW, H) fp16 table: the head pair's dword of each offset
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xtab, (uint32_t)(XW * XW * H * 2));
+    unsigned char* xdst = reinterpret_cast<unsigned char*>(s.xtab);
+    for (int i = wave; i * 64 < XW * XW; i += NW) {
+      const int x = i * 64 + lane;
+      if (x < XW * XW)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_dst_t*)(xdst + i * 256), 4,
+                                                 (uint32_t)((x * H + h0) * 2), 0, 0, 0);
+    }
+    if (tid < 3 * HG) {
+      const int W2 = (2 * a.lut_m + 1) * (2 * a.lut_m + 1);
+      s.tokb[tid] = a.btab[(W2 + tid / HG) * H + h0 + tid % HG];
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    linear_ok = hdr[HDR_SPAN_OK] != 0;
+    safe_q = hdr[HDR_SAFE_Q];
+    safe_r = hdr[HDR_SAFE_R];
+    kdelta = lds_addr(s.xtab) + (XD * XW + XD) * 2 * HG;
+  } else {
   // ---- global loads of the setup that nothing else depends on, issued first -----
   // coordinates and liveness of keys tid (and tid + 256 with four waves; the
   // rare keys beyond 512 are loaded where they are used)
@@ -399,7 +588,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
   // Global loads are issued U at a time per thread before their LDS stores.
   constexpr int CH = DP / 8;
   constexpr int U = 5;
-  if constexpr (!PROJ) {
+  if constexpr (PROJ == 0) {
   {
     const int total = HG * LP * CH;
     for (int base = tid; base < total; base += NT * U) {
@@ -535,8 +724,6 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
     }
   }
   // Coordinate span of the live cells (block-wide min / max).
-  bool linear_ok = false;
-  int safe_q = 0, safe_r = 0;
   if (!PAIR) {
     for (int m = 32; m >= 1; m >>= 1) {
       qmin = min(qmin, __shfl_xor(qmin, m, 64));
@@ -595,12 +782,13 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
     // (dq, dr) -> ((dq + XD) * XW + (dr + XD)) * 2 HG = kkey - qkey. Token and
     // dead keys take the code of the live cell (q0, r0), so every LINEAR read
     // stays inside the table; their biases are selected afterwards.
-    const int xoff = (int)(reinterpret_cast<const unsigned char*>(s.xtab) - smem);
+    const int xoff = lds_addr(s.xtab);
     for (int key = tid; key < LP; key += NT) {
       const int2 kk = s.kcls[key] == KEY_CELL ? s.kqr[key] : make_int2(q0, r0);
       s.kkey[key] = xoff + (kk.x * XW + kk.y + XD * XW + XD) * 2 * HG;
     }
   }
+  }  // staged / in-kernel setup
   // ---- PROJ: LayerNorm + q/k/v projection of this wave's row blocks ------------------
   // The raw bf16 rows are the MFMA operand; LayerNorm is applied to the
   // products: LN(x) W'^T + b' = rstd (x W'^T) + (b' - mean rstd cs), cs the
@@ -610,7 +798,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
   // zero V rows; rows past the bound zero K and Q, as the staged path reads
   // them from the zero-padded tensor.
   u32x2 qst[PROJ_NQ][HG];
-  if constexpr (PROJ) {
+  if constexpr (PJ) {
 #pragma unroll
     for (int sl = 0; sl < PROJ_NQ; ++sl)
 #pragma unroll
@@ -717,12 +905,12 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
       const bool qcell = qi.qv && !qi.qtok;
       qi.qq = qcell ? qc.x : safe_q;
       qi.qr = qcell ? qc.y : safe_r;
-      qi.qkey = (qi.qq * XW + qi.qr) * 2 * HG;
+      qi.qkey = (qi.qq * XW + qi.qr) * 2 * HG - kdelta;
     }
     // token or dead queries in this block: general path (wave-uniform)
     const bool qgen = q_gen[qb] != 0;
     u32x2 qf[HG][KD];
-    if constexpr (PROJ) {
+    if constexpr (PJ) {
 #pragma unroll
       for (int h = 0; h < HG; ++h) {
         qf[h][0] = opaque2(qst[0][h]);
@@ -762,28 +950,57 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
     case 6: SHRIMP_CHUNK_FL(NB, 6); break;            \
     default: SHRIMP_CHUNK_FL(NB, 7); break;           \
   }
+#define SHRIMP_LAZY(NB, F) \
+  attn_chunk_lazy<DP, HG, NB, F>(s, qi, kb, SP, lr, lg, qk_scale, qf, cinit, l, o)
+#define SHRIMP_LAZY_FLS(NB)                                 \
+  switch (fl) {                                             \
+    case 0: ok = SHRIMP_LAZY(NB, 0); break;                 \
+    case FL_QTOK: ok = SHRIMP_LAZY(NB, FL_QTOK); break;     \
+    case FL_DEAD: ok = SHRIMP_LAZY(NB, FL_DEAD); break;     \
+    default: ok = SHRIMP_LAZY(NB, FL_QTOK | FL_DEAD); break; \
+  }
     int kb = k0;
     if (!PAIR && linear_ok) {
       // LINEAR everywhere, in runs of four key blocks; each chunk's
       // exceptions (token queries, token keys in block 0, dead keys) pick a
-      // compile-time variant.
+      // compile-time variant. The first chunk sets the softmax offset, the
+      // others keep it (attn_chunk_lazy) unless their row sums leave range.
       const int qtokb = qb * 16 < nt ? FL_QTOK : 0;
+      bool first = true;
+      float cinit[HG];
       while (kb < k1) {
         const int run = min(4, k1 - kb);
         const int nb = run == 4 ? 4 : (run >= 2 ? 2 : 1);
         int dead = 0;
         for (int i = 0; i < nb; ++i) dead |= s.blk_dead[kb + i];
         const int fl = qtokb | (kb == 0 && nt > 0 ? FL_KTOK : 0) | (dead ? FL_DEAD : 0);
-        if (nb == 4) {
-          SHRIMP_CHUNK_FLS(4)
-        } else if (nb == 2) {
-          SHRIMP_CHUNK_FLS(2)
-        } else {
-          SHRIMP_CHUNK_FLS(1)
+        bool ok = false;
+        if (!first) {
+          if (nb == 4) {
+            SHRIMP_LAZY_FLS(4)
+          } else if (nb == 2) {
+            SHRIMP_LAZY_FLS(2)
+          } else {
+            SHRIMP_LAZY_FLS(1)
+          }
+        }
+        if (!ok) {
+          if (nb == 4) {
+            SHRIMP_CHUNK_FLS(4)
+          } else if (nb == 2) {
+            SHRIMP_CHUNK_FLS(2)
+          } else {
+            SHRIMP_CHUNK_FLS(1)
+          }
+          first = false;
+#pragma unroll
+          for (int h = 0; h < HG; ++h) cinit[h] = -m[h] * (1.0f / qk_scale);
         }
         kb += nb;
       }
     }
+#undef SHRIMP_LAZY
+#undef SHRIMP_LAZY_FLS
     while (!(!PAIR && linear_ok) && kb < k1) {
       if (qgen || s.blk_gen[kb]) {
         SHRIMP_CHUNK(1, PATH_GENERAL);
@@ -829,7 +1046,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
   // workgroup g takes the rounds g, g + Z, ... of the round-robin (each block on
   // the wave and with the key order it has with Z = 1, so the bits do not
   // change) and the last one the split block.
-  const int qz = PROJ ? 0 : (int)blockIdx.z, nz = PROJ ? 1 : (int)gridDim.z;
+  const int qz = PJ ? 0 : (int)blockIdx.z, nz = PJ ? 1 : (int)gridDim.z;
   const bool tail_here = split && qz == nz - 1;
   AttnQuery qi;
   float m[HG], l[HG];
@@ -902,7 +1119,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
 // LDS bytes of one workgroup; npos = pair-table rows (pair mode only).
 static size_t attn_smem_bytes(int DP, int HG, int S, int npos, bool pair) {
   const size_t SP = (size_t)((S + 15) & ~15);
-  size_t bytes = 2 * HG * SP * DP * 2 + SP * (8 + 4 + 4) + (SP / 16) * 12 + 3 * HG * 4;
+  size_t bytes = 2 * HG * SP * DP * 2 + (size_t)attn_meta_ints((int)SP) * 4 + 3 * HG * 4 + 4 * 8 * 4;
   bytes += pair ? (size_t)npos * HG * 4 : (size_t)XW * XW * HG * 2;
   return bytes;
 }
@@ -982,6 +1199,97 @@ __global__ void attn_xtab_kernel(const float* __restrict__ btab, int H, int M,
   const int W = 2 * M + 1;
   const int pos = (clampi(dq, M) + M) * W + (clampi(dr, M) + M);
   xtab[i] = __builtin_bit_cast(unsigned short, (_Float16)btab[pos * H + h]);
+}
+
+// Key table of every position for the staged attention (layout at
+// attn_meta_ints): the classes, coordinates, LINEAR codes, per-block flags
+// and span of the in-kernel setup, once per forward instead of once per
+// (position, head pair, attention block). One workgroup per position.
+__global__ __launch_bounds__(256) void attn_keys_kernel(const int32_t* __restrict__ coords,
+                                                        const uint8_t* __restrict__ mask,
+                                                        const int32_t* __restrict__ seq_lens, int S,
+                                                        int nt, int* __restrict__ meta) {
+  extern __shared__ int ks[];  // [3][SP]: class, q, r
+  __shared__ int red[4][4];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int SP = (S + 15) & ~15, NKB = SP / 16, NC = S - nt;
+  int L = seq_lens[b];
+  L = L < 0 ? 0 : (L > S ? S : L);
+  const int mi = attn_meta_ints(SP);
+  int* m = meta + (int64_t)b * mi;
+  int* kkey = m + 2 * SP;
+  int* kcls = m + 3 * SP;
+  int* bgen = m + 4 * SP;
+  int* qgen = bgen + NKB;
+  int* bdead = qgen + NKB;
+  int* hdr = bdead + NKB;
+  int qmin = 1 << 30, qmax = -(1 << 30), rmin = 1 << 30, rmax = -(1 << 30);
+  for (int key = tid; key < SP; key += 256) {
+    int q = 0, r = 0, cls = KEY_DEAD;  // keys past the bound (tokens too) are dead
+    if (key < nt && key < L) {
+      cls = KEY_TOKEN;
+    } else if (key >= nt && key < L) {
+      const int64_t cell = (int64_t)b * NC + (key - nt);
+      q = coords[cell * 2];
+      r = coords[cell * 2 + 1];
+      cls = mask[cell] != 0 ? KEY_CELL : KEY_DEAD;
+      if (cls == KEY_CELL) {
+        qmin = min(qmin, q);
+        qmax = max(qmax, q);
+        rmin = min(rmin, r);
+        rmax = max(rmax, r);
+      }
+    }
+    m[2 * key] = q;
+    m[2 * key + 1] = r;
+    kcls[key] = cls;
+    ks[key] = cls;
+    ks[SP + key] = q;
+    ks[2 * SP + key] = r;
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    qmin = min(qmin, __shfl_xor(qmin, o, 64));
+    qmax = max(qmax, __shfl_xor(qmax, o, 64));
+    rmin = min(rmin, __shfl_xor(rmin, o, 64));
+    rmax = max(rmax, __shfl_xor(rmax, o, 64));
+  }
+  if ((tid & 63) == 0) {
+    red[tid >> 6][0] = qmin;
+    red[tid >> 6][1] = qmax;
+    red[tid >> 6][2] = rmin;
+    red[tid >> 6][3] = rmax;
+  }
+  __syncthreads();
+  int q0 = red[0][0], q1 = red[0][1], r0 = red[0][2], r1 = red[0][3];
+  for (int w = 1; w < 4; ++w) {
+    q0 = min(q0, red[w][0]);
+    q1 = max(q1, red[w][1]);
+    r0 = min(r0, red[w][2]);
+    r1 = max(r1, red[w][3]);
+  }
+  // LINEAR needs a live cell (its code stands in for token and dead keys)
+  const bool span_ok = nt <= 16 && q0 <= q1 && (q1 - q0) <= XD && (r1 - r0) <= XD;
+  // key blocks with a token, a dead key or keys past the bound; query blocks
+  // with a token or dead query; key blocks with a dead key or keys past the bound
+  for (int blk = tid; blk < NKB; blk += 256) {
+    int kg = 0, qg = 0, kd = 0;
+    for (int j = 0; j < 16; ++j) {
+      const int key = blk * 16 + j;
+      const int cls = ks[key];
+      if (key >= L) kg = kd = 1;
+      else if (cls != KEY_CELL || key < nt) kg = qg = 1;
+      if (key < L && cls == KEY_DEAD) kd = 1;
+    }
+    bgen[blk] = kg;
+    qgen[blk] = qg;
+    bdead[blk] = kd;
+  }
+  for (int key = tid; key < SP; key += 256) {
+    const bool cell = ks[key] == KEY_CELL;
+    kkey[key] = span_ok ? ((cell ? ks[SP + key] : q0) * XW + (cell ? ks[2 * SP + key] : r0)) * 4 : 0;
+  }
+  for (int i = tid; i < mi - (4 * SP + 3 * NKB); i += 256)
+    hdr[i] = i == HDR_SPAN_OK ? (int)span_ok : (i == HDR_SAFE_Q ? q0 : (i == HDR_SAFE_R ? r0 : 0));
 }
 
 }  // namespace shrimp
@@ -1072,4 +1380,70 @@ extern "C" int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_pr
     hipLaunchKernelGGL((attn_kernel<16, 2, false, 1, 4>), grid, dim3(256), smem, as_stream(stream),
                        *a, qk_scale, 0u, w * w, *p, (uint32_t)xe);
   return check_launch("attn_fused");
+}
+
+extern "C" size_t shrimp_attn_keys_bytes(int S) {
+  return S > 0 ? (size_t)attn_meta_ints((S + 15) & ~15) * 4 : 0;
+}
+
+extern "C" int shrimp_attn_keys(const int32_t* coords, const uint8_t* mask, const int32_t* seq_lens,
+                                int B, int S, int n_tokens, int32_t* meta, void* stream) {
+  SHRIMP_REQUIRE(B >= 0 && S > 0 && n_tokens >= 0 && n_tokens <= S, "attn_keys: bad shape");
+  if (B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(seq_lens && meta && (n_tokens == S || (coords && mask)), "attn_keys: null pointer");
+  const int SP = (S + 15) & ~15;
+  SHRIMP_REQUIRE(SP <= 4096, "attn_keys: S = %d too large", S);
+  hipLaunchKernelGGL(attn_keys_kernel, dim3(B), dim3(256), (size_t)3 * SP * 4, as_stream(stream),
+                     coords, mask, seq_lens, S, n_tokens, meta);
+  return check_launch("attn_keys");
+}
+
+extern "C" int shrimp_attn_staged_supported(int H, int S, int dpad) {
+  const int SP = (S + 15) & ~15;
+  return dpad == 16 && H > 0 && H % 2 == 0 && S > 0 && S % 4 == 0 && SP <= 1024 &&
+         attn_smem_bytes(16, 2, S, 0, false) <= kAttnSmemCap;
+}
+
+extern "C" int shrimp_attn_staged(const shrimp_attn_args* a, const void* kvf, const int32_t* meta,
+                                  void* stream) {
+  SHRIMP_REQUIRE(a != nullptr, "attn_staged: null args");
+  SHRIMP_REQUIRE(a->B >= 0 && a->S > 0 && a->H > 0, "attn_staged: bad shape");
+  if (a->B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(shrimp_attn_staged_supported(a->H, a->S, a->dpad),
+                 "attn_staged: covers dpad = 16, even H, S %% 4 == 0 (got H = %d, S = %d, dpad = %d)",
+                 a->H, a->S, a->dpad);
+  SHRIMP_REQUIRE(a->pair == nullptr, "attn_staged: coords mode only");
+  SHRIMP_REQUIRE(a->q && kvf && meta && a->o && a->seq_lens && a->btab && a->xtab,
+                 "attn_staged: null pointer");
+  SHRIMP_REQUIRE(a->d > 0 && a->d % 4 == 0 && a->d <= 16, "attn_staged: head dim %d", a->d);
+  SHRIMP_REQUIRE(a->o_sb % 4 == 0 && a->o_sh % 4 == 0 && a->o_sr % 4 == 0,
+                 "attn_staged: output strides must be multiples of 4");
+  SHRIMP_REQUIRE(a->n_tokens >= 0 && a->n_tokens <= a->S, "attn_staged: bad n_tokens");
+  SHRIMP_REQUIRE(a->lut_m >= 0 && a->lut_m <= 64, "attn_staged: lut_m");
+  const int SP = (a->S + 15) & ~15;
+  const int64_t kvb = (int64_t)a->B * a->H * SP * 64;
+  const int64_t mb = (int64_t)a->B * shrimp_attn_keys_bytes(a->S);
+  const int64_t qe = ((int64_t)(a->B - 1) * a->qkv_sb + (int64_t)(a->H - 1) * a->qkv_sh +
+                      (int64_t)a->S * a->dpad) * 2;
+  SHRIMP_REQUIRE(kvb < (int64_t)0x7FFF0000 && mb < (int64_t)0x7FFF0000 && qe < (int64_t)0x7FFF0000,
+                 "attn_staged: buffers too large");
+  shrimp_attn_args s = *a;
+  s.k = kvf;
+  s.v = meta;
+  const float qk_scale = SHRIMP_LOG2E / sqrtf((float)a->d);
+  const size_t smem = attn_smem_bytes(16, 2, a->S, 0, false);
+  const int groups = a->H / 2 * a->B;
+  const int NW = g_attn_variant == 2 ? 4 : 8;
+  const int rounds = ((a->S + 15) / 16) / NW;
+  int z = 1;
+  while (z < 4 && groups * z * 2 <= 2 * cu_count() && rounds >= 2 * z) z *= 2;
+  dim3 grid(a->H / 2, a->B, z);
+  const shrimp_attn_proj_args none{};
+  if (NW == 4)
+    hipLaunchKernelGGL((attn_kernel<16, 2, false, 3, 4>), grid, dim3(256), smem, as_stream(stream), s,
+                       qk_scale, (uint32_t)qe, 0, none, 0u);
+  else
+    hipLaunchKernelGGL((attn_kernel<16, 2, false, 3, 8>), grid, dim3(512), smem, as_stream(stream), s,
+                       qk_scale, (uint32_t)qe, 0, none, 0u);
+  return check_launch("attn_staged");
 }

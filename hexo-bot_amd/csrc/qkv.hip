@@ -45,8 +45,18 @@ SHRIMP_DEV void load_rows16(const shrimp_qkv_args& a, __amdgpu_buffer_rsrc_t xr,
 
 }  // namespace
 
+// KVF (d = dpad = 16): q keeps the (B, H, S, 16) layout of a.qkv (its first
+// plane); k and v go to `kvf` in the staged attention's fragment order, per
+// (position, head) SP/16 K fragments then SP/16 V fragments of 512 bytes:
+//   K fragment kb, lane (lr, lg): K[16 kb + lr][4 lg .. +3]
+//   V fragment kb, lane (lr, lg): V[16 kb + 4 lg .. +3][lr]   (V^T)
+// K comes out of the usual product in that order; V from the product with
+// the operands swapped (rows as A, weights as B), which leaves each lane four
+// consecutive rows of one output channel. Slots of keys >= S are not written.
+template <bool KVF>
 __global__ __launch_bounds__(QWAVES * 64, 1) void attn_qkv_kernel(const shrimp_qkv_args a,
-                                                                  uint32_t x_bytes, int dshift) {
+                                                                  uint32_t x_bytes, int dshift,
+                                                                  unsigned short* kvf, int SP) {
   extern __shared__ __attribute__((aligned(16))) unsigned char wl[];
   constexpr int KS = QC / 32, NB = QN / 16;
   const int lane = threadIdx.x & 63;
@@ -105,13 +115,40 @@ __global__ __launch_bounds__(QWAVES * 64, 1) void attn_qkv_kernel(const shrimp_q
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
         w[ks] = *reinterpret_cast<const u32x4*>(wl + (uint32_t)(((ks * NB + nb) * 64 + lane) * 16));
+      const int which = nb / (QC / 16);
+      if (KVF && which == 2) {
+        // rows 16 blk + 4 lg .. + 3 of output channel 16 (nb - 16) + lr = head nb - 16, dim lr
+        const float bv = bias[nb * 16 + lr];
+        f32x4 acc = f32x4{bv, bv, bv, bv};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) acc = mfma16x16x32(hf[ks], w[ks], acc);
+        const int r0 = blk * 16 + lg * 4;
+        if (r0 < a.rows) {
+          const int b0 = r0 / a.S;
+          const int s0 = r0 - b0 * a.S;
+          const int head = nb - 2 * (QC / 16);
+          unsigned short* dst = kvf + (((int64_t)b0 * a.H + head) * 2 + 1) * SP * 16 +
+                                (s0 >> 4) * 256 + (((s0 & 15) >> 2) * 16 + lr) * 4;
+          *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        continue;
+      }
       f32x4 acc = *reinterpret_cast<const f32x4*>(bias + nb * 16 + lg * 4);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) acc = mfma16x16x32(w[ks], hf[ks], acc);
-      const int which = nb / (QC / 16);
       const int within = (nb % (QC / 16)) * 16 + lg * 4;
       const int head = within >> dshift;
       const int dd = within & (d - 1);
+      if (KVF && which == 1) {
+        if (rv) {
+          unsigned short* dst = kvf + (((int64_t)bq * a.H + head) * 2) * SP * 16 + (sq >> 4) * 256 +
+                                (lg * 16 + (sq & 15)) * 4;
+          *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        continue;
+      }
       if (rv) {
         u32x2 pk;
         pk.x = pack_bf16x2(acc[0], acc[1]);
@@ -204,7 +241,36 @@ extern "C" int shrimp_attn_qkv(const shrimp_qkv_args* a, void* stream) {
   // at least one workgroup per 4 row blocks (up to one per compute unit): small
   // row counts spread over more units, each staging the weights once
   const int grid = (int)std::min<int64_t>(cus, std::max<int64_t>((nblk + QWAVES - 1) / QWAVES, (nblk + 3) / 4));
-  hipLaunchKernelGGL(attn_qkv_kernel, dim3(grid), dim3(QWAVES * 64), QW_LDS, as_stream(stream), *a,
-                     (uint32_t)xe, dshift);
+  hipLaunchKernelGGL(attn_qkv_kernel<false>, dim3(grid), dim3(QWAVES * 64), QW_LDS, as_stream(stream),
+                     *a, (uint32_t)xe, dshift, (unsigned short*)nullptr, 0);
   return check_launch("attn_qkv");
+}
+
+extern "C" int shrimp_attn_qkv_kvf(const shrimp_qkv_args* a, void* kvf, void* stream) {
+  SHRIMP_REQUIRE(a != nullptr, "attn_qkv_kvf: null args");
+  SHRIMP_REQUIRE(a->rows >= 0, "attn_qkv_kvf: negative rows");
+  if (a->rows == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(a->C == QC && a->H == QC / 16 && a->dpad == 16,
+                 "attn_qkv_kvf: covers C = %d, H = %d, dpad = 16 (got C = %d, H = %d, dpad = %d)", QC,
+                 QC / 16, a->C, a->H, a->dpad);
+  SHRIMP_REQUIRE(a->x && a->qkv && a->packed && kvf, "attn_qkv_kvf: null pointer");
+  SHRIMP_REQUIRE(a->B > 0 && a->S > 0 && a->S % 4 == 0 && (int64_t)a->B * a->S == a->rows,
+                 "attn_qkv_kvf: rows must be B * S with S %% 4 == 0");
+  SHRIMP_REQUIRE(a->x_sr >= QC && a->x_sr % 8 == 0, "attn_qkv_kvf: x row stride");
+  const int SP = (a->S + 15) & ~15;
+  const int64_t xe = ((int64_t)(a->rows - 1) * a->x_sr + QC) * 2;
+  SHRIMP_REQUIRE(xe < (int64_t)0x7FFF0000 && (int64_t)a->B * a->H * SP * 64 < (int64_t)0x7FFF0000,
+                 "attn_qkv_kvf: buffers too large");
+  SHRIMP_REQUIRE((size_t)max_lds_per_block() >= QW_LDS, "attn_qkv_kvf: needs %u bytes of LDS",
+                 (unsigned)QW_LDS);
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return set_error(SHRIMP_ELAUNCH, "attn_qkv_kvf: cannot query the compute unit count");
+  const int64_t nblk = (a->rows + 15) / 16;
+  const int grid = (int)std::min<int64_t>(cus, std::max<int64_t>((nblk + QWAVES - 1) / QWAVES, (nblk + 3) / 4));
+  hipLaunchKernelGGL(attn_qkv_kernel<true>, dim3(grid), dim3(QWAVES * 64), QW_LDS, as_stream(stream),
+                     *a, (uint32_t)xe, 4, static_cast<unsigned short*>(kvf), SP);
+  return check_launch("attn_qkv_kvf");
 }

@@ -142,6 +142,11 @@ SIGNATURES: dict = {
     "shrimp_conv_block": (ctypes.c_int, [ctypes.POINTER(ConvArgs), ctypes.POINTER(ConvArgs), _vp]),
     "shrimp_linear": (ctypes.c_int, [ctypes.POINTER(LinearArgs), _vp]),
     "shrimp_attn_qkv": (ctypes.c_int, [ctypes.POINTER(QkvArgs), _vp]),
+    "shrimp_attn_qkv_kvf": (ctypes.c_int, [ctypes.POINTER(QkvArgs), _vp, _vp]),
+    "shrimp_attn_keys_bytes": (ctypes.c_size_t, [ctypes.c_int]),
+    "shrimp_attn_keys": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+    "shrimp_attn_staged_supported": (ctypes.c_int, [ctypes.c_int] * 3),
+    "shrimp_attn_staged": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _vp, _vp, _vp]),
     "shrimp_attn_qkv_pack_bytes": (ctypes.c_size_t, [ctypes.c_int]),
     "shrimp_pack_attn_qkv": (ctypes.c_int, [_vp] * 6 + [ctypes.c_int, _vp]),
     "shrimp_attn_mlp": (ctypes.c_int, [ctypes.POINTER(MlpArgs), _vp]),

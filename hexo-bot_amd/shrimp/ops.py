@@ -265,6 +265,54 @@ def launch_attn(
     _lib.check(_lib.load().shrimp_attn(ctypes_ref(a), s), "attn")
 
 
+def launch_attn_qkv_kvf(*, x, x_sr, q, kvf, packed, eps, rows, B, S, H, C, dpad, stream=None):
+    """LN1 + q/k/v projection: q into the (B, H, S, dpad) layout of ``q``, k and v
+    into the staged attention's fragment layout ``kvf`` (B, H, 2, SP, 16)."""
+
+    a = _lib.QkvArgs(x=x.data_ptr(), x_sr=x_sr, qkv=q.data_ptr(), packed=packed.data_ptr(),
+                     eps=float(eps), rows=rows, B=B, S=S, H=H, C=C, dpad=dpad)
+    s = _lib.stream_handle() if stream is None else stream
+    _lib.check(_lib.load().shrimp_attn_qkv_kvf(ctypes_ref(a), kvf.data_ptr(), s), "attn_qkv_kvf")
+
+
+def attn_keys_ints(S: int) -> int:
+    """int32 words of one position's key table (shrimp_attn_keys)."""
+
+    return int(_lib.load().shrimp_attn_keys_bytes(S)) // 4
+
+
+def launch_attn_keys(*, coords, mask8, seq_lens, B, S, n_tokens, meta, stream=None):
+    """Key table of every position for the staged attention (once per forward)."""
+
+    s = _lib.stream_handle() if stream is None else stream
+    _lib.check(_lib.load().shrimp_attn_keys(
+        _lib.ptr(coords), _lib.ptr(mask8), seq_lens.data_ptr(), B, S, n_tokens, meta.data_ptr(), s),
+        "attn_keys")
+
+
+def attn_staged_supported(H: int, S: int, dpad: int) -> bool:
+    return bool(_lib.load().shrimp_attn_staged_supported(H, S, dpad))
+
+
+def launch_attn_staged(
+    *, q, qkv_sb, qkv_sh, kvf, meta, seq_lens, o, o_sb, o_sh, o_sr, B, S, H, d, dpad, btab, xtab,
+    lut_m=CELL_LUT_M, n_tokens=NUM_TOKENS, stream=None,
+):
+    """Attention over K / V fragments from launch_attn_qkv_kvf and the key table
+    from launch_attn_keys (coords mode, LINEAR table required)."""
+
+    a = _lib.AttnArgs(
+        q=q.data_ptr(), k=None, v=None, qkv_sb=qkv_sb, qkv_sh=qkv_sh,
+        seq_lens=seq_lens.data_ptr(), pair=None, p_sb=0, p_sq=0, table2=None, table_rows=0,
+        coords=None, mask=None, btab=btab.data_ptr(), xtab=xtab.data_ptr(), lut_m=lut_m,
+        n_tokens=n_tokens, o=o.data_ptr(), o_sb=o_sb, o_sh=o_sh, o_sr=o_sr,
+        B=B, S=S, H=H, d=d, dpad=dpad,
+    )
+    s = _lib.stream_handle() if stream is None else stream
+    _lib.check(_lib.load().shrimp_attn_staged(ctypes_ref(a), kvf.data_ptr(), meta.data_ptr(), s),
+               "attn_staged")
+
+
 def attn_fused_supported(C: int, H: int, S: int, dpad: int) -> bool:
     """Shapes the one-launch LN1 -> q/k/v -> attention kernel covers."""
 

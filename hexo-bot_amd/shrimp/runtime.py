@@ -43,12 +43,17 @@ from .constants import NUM_TOKENS, VALUE_BINS
 from .geometry import CELL_LUT_M
 from .ops import (
     attn_bias_table,
+    attn_keys_ints,
+    attn_staged_supported,
     conv_block_supported,
     attn_fused_supported,
     launch_attn,
     launch_attn_fused,
+    launch_attn_keys,
     launch_attn_mlp,
     launch_attn_qkv,
+    launch_attn_qkv_kvf,
+    launch_attn_staged,
     launch_conv,
     launch_conv_block,
     launch_linear,
@@ -109,6 +114,12 @@ class HipForward:
         # default: about 1% faster at B=512) runs the q/k/v kernel, then
         # attention.
         self.use_fused_attn = False
+        # Staged attention where it applies (C = 128, H = 8, the LINEAR
+        # table): the q/k/v kernel writes K and V in the attention kernel's
+        # fragment order and a once-per-forward key table replaces the
+        # per-workgroup key setup, so the attention kernel stages by DMA;
+        # off runs the (3, B, H, S, dpad) layout and the in-kernel setup.
+        self.use_staged_attn = True
         # ConvBlock as one launch (conv1's output kept in LDS) where a fused
         # kernel exists; off runs the two convolutions.
         self.use_fused_block = True
@@ -491,14 +502,18 @@ class HipForward:
 
     def batch_limit(self, N: int) -> int:
         """Positions one forward can take at Npad = N: the widest per-position
-        activation buffer (the MLP hidden (S, 2C) or q/k/v (H, S, dpad)) times
-        the batch stays under BUFFER_LIMIT bytes; max_batch caps it further."""
+        activation buffer (the MLP hidden (S, 2C), q/k/v (H, S, dpad) or the K / V
+        fragments (H, 2, SP, 16)) times the batch stays under BUFFER_LIMIT
+        bytes; max_batch caps it further."""
 
         net = self.net
         c, h = net.channels, net.heads
         width = max(2 * c, h * head_dim_pad(c // h))
         elem = 4 if self.fp32 else 2
-        lim = max(1, (self.BUFFER_LIMIT - 1) // ((N + NUM_TOKENS) * width * elem))
+        # the staged attention's K / V fragments: (H, 2, SP, 16) bf16 per position
+        sp = (N + NUM_TOKENS + 15) // 16 * 16
+        per = max((N + NUM_TOKENS) * width * elem, h * sp * 64)
+        lim = max(1, (self.BUFFER_LIMIT - 1) // per)
         return lim if self.max_batch is None else max(1, min(lim, int(self.max_batch)))
 
     @torch.no_grad()
@@ -569,8 +584,15 @@ class HipForward:
         y1 = torch.empty((B, N, C), dtype=bf, device=dev)
         attn_fused = (P.fused_qkv and self.use_fused_qkv and self.use_fused_attn
                       and attn_fused_supported(C, H, S, dpad))
-        qkv = None
-        if not attn_fused:
+        staged = (not attn_fused and P.fused_qkv and self.use_fused_qkv and self.use_staged_attn
+                  and self.use_linear_bias and d == dpad and attn_staged_supported(H, S, dpad))
+        qkv = kvf = meta = None
+        if staged:
+            sp = (S + 15) // 16 * 16
+            qkv = torch.empty((1, B, H, S, dpad), dtype=bf, device=dev)
+            kvf = torch.empty((B, H, 2, sp, 16), dtype=bf, device=dev)
+            meta = torch.empty((B, attn_keys_ints(S)), dtype=torch.int32, device=dev)
+        elif not attn_fused:
             qkv = (torch.zeros if d != dpad else torch.empty)((3, B, H, S, dpad), dtype=bf, device=dev)
         att = torch.empty((B, S, C), dtype=bf, device=dev)
         fused = P.fused_mlp and self.use_fused_mlp
@@ -578,6 +600,10 @@ class HipForward:
 
         conv_common = dict(idx=idx, taps=7, idx_stride=7, mask8=mask8, B=B, N=N, stream=st)
         self._mark("start")
+        if staged:
+            launch_attn_keys(coords=coords32, mask8=mask8, seq_lens=seq_lens, B=B, S=S,
+                             n_tokens=NUM_TOKENS, meta=meta, stream=st)
+            self._mark("attn_keys")
         launch_conv(
             x=xin, x_sb=N * 32, x_sn=32, wpack=P.stem.w, bias=P.stem.b, cin_pad=32, cout=C,
             ln_w=P.stem.lnw, ln_b=P.stem.lnb, eps=P.stem.eps, relu=True,
@@ -625,6 +651,17 @@ class HipForward:
                     launch_attn_fused(x=seq, x_sb=S * C, x_sr=C, packed=a.qkv, eps=a.eps1,
                                       **bias_args)
                     self._mark("attn_fused")
+                elif staged:
+                    launch_attn_qkv_kvf(x=seq, x_sr=C, q=qkv, kvf=kvf, packed=a.qkv, eps=a.eps1,
+                                        rows=rows, B=B, S=S, H=H, C=C, dpad=dpad, stream=st)
+                    self._mark("qkv")
+                    launch_attn_staged(
+                        q=qkv, qkv_sb=H * S * dpad, qkv_sh=S * dpad, kvf=kvf, meta=meta,
+                        seq_lens=seq_lens, o=att, o_sb=S * C, o_sh=d, o_sr=C, B=B, S=S, H=H, d=d,
+                        dpad=dpad, btab=a.btab_xtab[0], xtab=a.btab_xtab[1], lut_m=CELL_LUT_M,
+                        n_tokens=NUM_TOKENS, stream=st,
+                    )
+                    self._mark("attn")
                 elif P.fused_qkv and self.use_fused_qkv:
                     launch_attn_qkv(x=seq, x_sr=C, qkv=qkv, packed=a.qkv, eps=a.eps1, rows=rows,
                                     B=B, S=S, H=H, C=C, dpad=dpad, stream=st)
@@ -636,7 +673,7 @@ class HipForward:
                         eps=a.eps1, B=B, S=S, H=H, dpad=dpad, stream=st,
                     )
                     self._mark("qkv")
-                if not attn_fused:
+                if not attn_fused and not staged:
                     launch_attn(q=qkv[0], k=qkv[1], v=qkv[2], qkv_sb=H * S * dpad,
                                 qkv_sh=S * dpad, **bias_args)
                     self._mark("attn")
@@ -693,7 +730,7 @@ class HipForward:
             self.last = dict(
                 P=P, B=B, N=N, S=S, idx=idx, mask8=mask8, coords32=coords32, seq_lens=seq_lens,
                 seq_mask=seq_mask, seq=seq, y1=y1, qkv=qkv, att=att, hid=hid, seqf=seqf,
-                stream=st, attn_fused=attn_fused,
+                stream=st, attn_fused=attn_fused, staged=staged, kvf=kvf, meta=meta,
             )
         return out
 

@@ -329,6 +329,34 @@ typedef struct {
 int shrimp_attn_fused_supported(int C, int H, int S, int dpad);
 int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_proj_args* p, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Staged attention: the same operator as shrimp_attn in coords mode
+ * (RelPosAttention, model.py:448-492; the serve kernel _triton_attn.py:59-130)
+ * with its inputs in layouts the kernel copies into LDS by DMA.
+ *   shrimp_attn_keys: once per forward, the key table of every position
+ *     (classes, coordinates, LINEAR offset codes, per-16-key-block flags, the
+ *     span test), shrimp_attn_keys_bytes(S) bytes per position, from the
+ *     coords / mask / seq_lens that shrimp_attn reads (the per-block setup of
+ *     model.py:718-760 done once for all heads and attention blocks).
+ *   shrimp_attn_qkv_kvf: shrimp_attn_qkv (C = 128, H = 8, dpad = 16,
+ *     S % 4 == 0) with q in the first plane of a->qkv ((B, H, S, 16)) and k,
+ *     v in kvf as (B, H, 2, SP, 16) bf16 MFMA fragments, SP = S rounded up to
+ *     16 (slots of keys >= S are not written and not read).
+ *   shrimp_attn_staged: a->q, a->qkv_sb / qkv_sh the q layout above, kvf and
+ *     meta from the two calls above, btab and xtab required, pair NULL;
+ *     a->k, a->v, a->coords and a->mask are not read. Results equal
+ *     shrimp_attn's up to the bf16 rounding of P (the softmax offsets may
+ *     differ). shrimp_attn_staged_supported(H, S, dpad): dpad = 16, even H,
+ *     S % 4 == 0 and the LDS budget.
+ * ---------------------------------------------------------------------- */
+size_t shrimp_attn_keys_bytes(int S);
+int shrimp_attn_keys(const int32_t* coords, const uint8_t* mask, const int32_t* seq_lens, int B,
+                     int S, int n_tokens, int32_t* meta, void* stream);
+int shrimp_attn_qkv_kvf(const shrimp_qkv_args* a, void* kvf, void* stream);
+int shrimp_attn_staged_supported(int H, int S, int dpad);
+int shrimp_attn_staged(const shrimp_attn_args* a, const void* kvf, const int32_t* meta,
+                       void* stream);
+
 #define SHRIMP_ATTN_XD 26
 
 /* btab[pos, h] = log2(e) * table[lut[pos], h] for pos < (2M+1)^2 and the 3

@@ -500,3 +500,104 @@ def test_evaluator_busy_trace_counts_every_payload():
     assert rep["device_busy_ms"] > 0 and rep["wall_window_ms"] > 0
     assert 0 < rep["gpu_busy_fraction"] <= 1.5
     assert rep["mean_batch"] == round(113 / 3, 1) and rep["median_batch"] == 40.0
+
+
+def test_staged_attention_matches_the_row_layout_path(cfg4_batch):
+    """The staged attention (K and V in fragment order from the q/k/v kernel,
+    the key table once per forward, DMA staging) against the (3, B, H, S,
+    dpad) layout with the in-kernel key setup: both compute the same products
+    in the same order and drop dead keys the same way, so the forward is
+    bit-identical."""
+
+    b = cfg4_batch
+    net = _net(128, 8, "CCACCACCACCA", seed=5, mode="heads")
+    rt = net.hip_runtime()
+    rt.use_staged_attn = False
+    try:
+        base = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"], trunk=True)
+    finally:
+        rt.use_staged_attn = True
+    rt.keep_buffers = True
+    try:
+        net.forward_policy_value(*[torch.as_tensor(b[k]).to(DEV) for k in ("feats", "nbr", "mask", "coords")])
+        assert rt.last["staged"], "the staged path did not run"
+    finally:
+        rt.keep_buffers = False
+        rt.last = None
+    staged = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"], trunk=True)
+    for key in ("policy", "value", "moves_left", "tokens", "cells"):
+        err = (staged[key] - base[key]).abs().max().item()
+        print(f"staged vs row-layout attention {key}: {err:.3e}", flush=True)
+        assert err == 0.0, key
+
+
+def _keys_table(coords, mask, seq_lens, S, nt, xw=53, xd=26):
+    """numpy restatement of shrimp_attn_keys' table (layout in attn.hip)."""
+
+    B = coords.shape[0]
+    sp = (S + 15) // 16 * 16
+    nkb = sp // 16
+    ints = (4 * sp + 3 * nkb + 8 + 3) & ~3
+    out = np.zeros((B, ints), np.int64)
+    for p in range(B):
+        L = int(min(max(seq_lens[p], 0), S))
+        cls = np.full(sp, 2)
+        q = np.zeros(sp, np.int64)
+        r = np.zeros(sp, np.int64)
+        for key in range(sp):
+            if key < nt and key < L:
+                cls[key] = 1
+            elif nt <= key < L:
+                q[key], r[key] = coords[p, key - nt]
+                cls[key] = 0 if mask[p, key - nt] else 2
+        live = cls == 0
+        span_ok = nt <= 16 and live.any()
+        q0 = r0 = 0
+        if live.any():
+            q0, r0 = q[live].min(), r[live].min()
+            span_ok = span_ok and q[live].max() - q0 <= xd and r[live].max() - r0 <= xd
+        else:
+            q0 = r0 = 1 << 30
+        m = out[p]
+        m[0:2 * sp:2], m[1:2 * sp:2] = q, r
+        if span_ok:
+            m[2 * sp:3 * sp] = (np.where(live, q, q0) * xw + np.where(live, r, r0)) * 4
+        m[3 * sp:4 * sp] = cls
+        for blk in range(nkb):
+            keys = np.arange(blk * 16, blk * 16 + 16)
+            past = keys >= L
+            special = (~past) & ((cls[keys] != 0) | (keys < nt))
+            m[4 * sp + blk] = int(past.any() or special.any())
+            m[4 * sp + nkb + blk] = int(special.any())
+            m[4 * sp + 2 * nkb + blk] = int(past.any() or ((~past) & (cls[keys] == 2)).any())
+        h = 4 * sp + 3 * nkb
+        m[h], m[h + 1], m[h + 2] = int(span_ok), q0, r0
+    return out.astype(np.int32)
+
+
+def test_attn_keys_table_matches_restatement():
+    """shrimp_attn_keys against a numpy restatement on positions with tokens,
+    masked cells inside the bound, a short bound, a wide (non-LINEAR) span and
+    an empty position."""
+
+    from shrimp import ops
+
+    rng = np.random.default_rng(4)
+    B, N, nt = 5, 40, 8
+    S = N + nt
+    coords = rng.integers(-6, 7, size=(B, N, 2)).astype(np.int32)
+    mask = np.ones((B, N), np.uint8)
+    mask[1, 5] = 0
+    mask[1, 17] = 0
+    coords[3, 2] = (40, -3)  # span > 26
+    mask[4] = 0
+    seq_lens = np.array([S, S, 30, S, 0], np.int32)
+    meta = torch.empty((B, ops.attn_keys_ints(S)), dtype=torch.int32, device=DEV)
+    ops.launch_attn_keys(coords=torch.as_tensor(coords).to(DEV), mask8=torch.as_tensor(mask).to(DEV),
+                         seq_lens=torch.as_tensor(seq_lens).to(DEV), B=B, S=S, n_tokens=nt, meta=meta)
+    got = meta.cpu().numpy()
+    want = _keys_table(coords, mask, seq_lens, S, nt)
+    assert got.shape == want.shape
+    for p in range(B):
+        bad = np.nonzero(got[p] != want[p])[0]
+        assert bad.size == 0, (p, bad[:8], got[p][bad[:8]], want[p][bad[:8]])

@@ -155,8 +155,8 @@ def test_batch_limit_keeps_buffers_under_32_bit_offsets():
     rt = HipForward(ShrimpNet(channels=128, attention_heads=8, trunk_layout="CCACCACCACCA"))
     rt.precision = "bf16"
     lim = rt.batch_limit(256)
-    assert lim == (HipForward.BUFFER_LIMIT - 1) // (264 * 256 * 2)
-    assert lim * 264 * 256 * 2 < 2 ** 31
+    assert lim == (HipForward.BUFFER_LIMIT - 1) // (8 * 272 * 64)
+    assert lim * 8 * 272 * 64 < 2 ** 31 and lim * 264 * 256 * 2 < 2 ** 31
     rt.precision = "fp32"
     assert rt.batch_limit(256) == (HipForward.BUFFER_LIMIT - 1) // (264 * 256 * 4)
     rt.max_batch = 7
