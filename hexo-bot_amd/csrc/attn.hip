@@ -1432,18 +1432,16 @@ extern "C" int shrimp_attn_staged(const shrimp_attn_args* a, const void* kvf, co
   s.v = meta;
   const float qk_scale = SHRIMP_LOG2E / sqrtf((float)a->d);
   const size_t smem = attn_smem_bytes(16, 2, a->S, 0, false);
+  // four waves per workgroup (three workgroups per compute unit): measured
+  // faster than eight here
   const int groups = a->H / 2 * a->B;
-  const int NW = g_attn_variant == 2 ? 4 : 8;
+  constexpr int NW = 4;
   const int rounds = ((a->S + 15) / 16) / NW;
   int z = 1;
   while (z < 4 && groups * z * 2 <= 2 * cu_count() && rounds >= 2 * z) z *= 2;
   dim3 grid(a->H / 2, a->B, z);
   const shrimp_attn_proj_args none{};
-  if (NW == 4)
-    hipLaunchKernelGGL((attn_kernel<16, 2, false, 3, 4>), grid, dim3(256), smem, as_stream(stream), s,
-                       qk_scale, (uint32_t)qe, 0, none, 0u);
-  else
-    hipLaunchKernelGGL((attn_kernel<16, 2, false, 3, 8>), grid, dim3(512), smem, as_stream(stream), s,
-                       qk_scale, (uint32_t)qe, 0, none, 0u);
+  hipLaunchKernelGGL((attn_kernel<16, 2, false, 3, NW>), grid, dim3(64 * NW), smem, as_stream(stream),
+                     s, qk_scale, (uint32_t)qe, 0, none, 0u);
   return check_launch("attn_staged");
 }

@@ -505,17 +505,24 @@ def test_evaluator_busy_trace_counts_every_payload():
 def test_staged_attention_matches_the_row_layout_path(cfg4_batch):
     """The staged attention (K and V in fragment order from the q/k/v kernel,
     the key table once per forward, DMA staging) against the (3, B, H, S,
-    dpad) layout with the in-kernel key setup: both compute the same products
-    in the same order and drop dead keys the same way, so the forward is
-    bit-identical."""
+    dpad) layout with the in-kernel key setup at the same wave count: both
+    compute the same products in the same order and drop dead keys the same
+    way, so the forward is bit-identical."""
+
+    from shrimp import _lib
 
     b = cfg4_batch
     net = _net(128, 8, "CCACCACCACCA", seed=5, mode="heads")
     rt = net.hip_runtime()
     rt.use_staged_attn = False
+    # the staged kernel runs four waves per workgroup: the row-layout kernel's
+    # four-wave variant splits the last query block the same way
+    lib = _lib.load()
+    prev = lib.shrimp_attn_variant(2)
     try:
         base = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"], trunk=True)
     finally:
+        lib.shrimp_attn_variant(prev)
         rt.use_staged_attn = True
     rt.keep_buffers = True
     try:
