@@ -788,8 +788,10 @@ def main() -> int:
         },
         "attention": {
             "kernel": ("attn_kernel<16,2,coords,proj> (block 0: LN1 + q/k/v projection + "
-                       "attention)") if fused else "attn_kernel<16,2,coords> (block 0)",
-            "bound": "valu (d=16: one exp + ~6 VALU per score vs 64 MFMA flops)",
+                       "attention)") if fused else (
+                           "attn_kernel<16,2,coords,staged> (block 0: K/V fragments and the key "
+                           "table by DMA)" if kt["attn_staged"] else "attn_kernel<16,2,coords> (block 0)"),
+            "bound": "valu (d=16: one exp + ~4 VALU per score vs 64 MFMA flops)",
             "launch_ms": round(a_ms, 5),
             "tflops": round(attn_tflops, 2),
             "mfma_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
