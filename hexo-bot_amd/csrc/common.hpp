@@ -56,7 +56,11 @@ SHRIMP_DEV unsigned pack_bf16x2(float lo, float hi) {
   bf16x2 v;
   v.x = (__bf16)lo;
   v.y = (__bf16)hi;
-  return __builtin_bit_cast(unsigned, v);
+  unsigned r = __builtin_bit_cast(unsigned, v);
+  // opaque to the vectorisers: merged into wider vectors, the conversions are
+  // split into one v_cvt_pk_bf16_f32 per value plus a v_perm_b32 per pair
+  asm("" : "+v"(r));
+  return r;
 }
 
 SHRIMP_DEV unsigned short f32_to_bf16_bits(float f) {
