@@ -76,6 +76,31 @@ SHRIMP_DEV u32x4 lds_frag(const unsigned char* wl, uint32_t base, int ks, int nb
   return *reinterpret_cast<const u32x4*>(wl + base + (uint32_t)(((ks * nbt + nb) * 64 + lane) * 16));
 }
 
+// The folded biases [bo' | b1' | b2'] are 32 blocks of 16 channels. A wave keeps
+// them in 8 registers, register r holding at lane (lr, lg) channel lr of block
+// 4 r + lg, and starts an accumulator at bias block t with one fp32 MFMA
+// against a one-hot B operand (lane (lr, lg): 1 when lg = t % 4): D[i][j] =
+// bias[16 t + i] exactly. The loop body then issues no bias loads, which would
+// otherwise wait behind the next block's HBM requests (memory loads retire in
+// order).
+struct MlpBias {
+  float reg[8];
+  float onehot[4];
+};
+
+SHRIMP_DEV void load_bias(const float* bias, int lane, MlpBias& mb) {
+  const int lr = lane & 15, lg = lane >> 4;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) mb.reg[r] = bias[(4 * r + lg) * 16 + lr];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) mb.onehot[t] = lg == t ? 1.0f : 0.0f;
+}
+
+SHRIMP_DEV f32x4 bias_acc(const MlpBias& mb, int t) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(mb.reg[t >> 2], mb.onehot[t & 3],
+                                               f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+}
+
 // Attention-output fragments (out_proj input) of one 16-row block; rows at
 // or past `rows` read as zeros.
 SHRIMP_DEV void load_x(const shrimp_mlp_args& a, __amdgpu_buffer_rsrc_t xr, int row, int lg,
@@ -100,20 +125,17 @@ SHRIMP_DEV void load_s(const shrimp_mlp_args& a, __amdgpu_buffer_rsrc_t sr, int 
 // holds the block's residual rows on entry; once they are consumed the next
 // block's (row next_row) are requested into the same registers, so their
 // latency hides behind this block's MLP.
-SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, const float* bias,
+SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, const MlpBias& bias,
                           __amdgpu_buffer_rsrc_t sr, const u32x4 (&xf)[MC / 32], int row,
-                          int lane, u32x2 (&sin)[MC / 16], int next_row) {
+                          int lane, u32x2 (&sin)[MC / 16], int next_row, bool store) {
   constexpr int KS1 = MC / 32, NB1 = MC / 16, NBH = MH / 16, KT = MH / 32, NB2 = MC / 16;
+  constexpr int TB1 = NB1, TB2 = NB1 + NBH;  // first bias block of b1', b2'
   const int lg = lane >> 4;
-  const bool store = row < a.rows && a.mask[row] != 0;
-  const float* bo = bias;
-  const float* b1 = bias + MC;
-  const float* b2 = bias + MC + MH;
 
   // accumulators start at the biases
   f32x4 acc[NB1];
 #pragma unroll
-  for (int nb = 0; nb < NB1; ++nb) acc[nb] = *reinterpret_cast<const f32x4*>(bo + nb * 16 + lg * 4);
+  for (int nb = 0; nb < NB1; ++nb) acc[nb] = bias_acc(bias, nb);
 
   // ---- out_proj ----------------------------------------------------------
   // (scheduling barriers keep the weight-fragment reads next to their MFMAs;
@@ -171,10 +193,7 @@ SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, con
   // ---- fc1 -> GELU -> fc2, one 32-wide hidden slice at a time ---------------
   f32x4 acc2[NB2];
 #pragma unroll
-  for (int nb = 0; nb < NB2; ++nb) acc2[nb] = *reinterpret_cast<const f32x4*>(b2 + nb * 16 + lg * 4);
-  f32x4 bh[2];
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh) bh[hh] = *reinterpret_cast<const f32x4*>(b1 + hh * 16 + lg * 4);
+  for (int nb = 0; nb < NB2; ++nb) acc2[nb] = bias_acc(bias, TB2 + nb);
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt) {
     f32x4 ah[2];
@@ -183,17 +202,12 @@ SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, con
       u32x4 w[KS1];
 #pragma unroll
       for (int ks = 0; ks < KS1; ++ks) w[ks] = lds_frag(wl, W1_OFF, ks, 2 * kt + hh, NBH, lane);
-      ah[hh] = bh[hh];
+      ah[hh] = bias_acc(bias, TB1 + 2 * kt + hh);
 #pragma unroll
       for (int ks = 0; ks < KS1; ++ks) ah[hh] = mfma16x16x32(w[ks], hf[ks], ah[hh]);
     }
-    // next slice's fc1 biases; fc2 fragments in two halves, the first half's
-    // LDS reads overlapping the GELU
-    if (kt + 1 < KT) {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-        bh[hh] = *reinterpret_cast<const f32x4*>(b1 + (2 * kt + 2 + hh) * 16 + lg * 4);
-    }
+    // fc2 fragments in two halves, the first half's LDS reads overlapping the
+    // GELU
     u32x4 w2[NB2 / 2];
 #pragma unroll
     for (int nb = 0; nb < NB2 / 2; ++nb) w2[nb] = lds_frag(wl, W2_OFF, kt, nb, NB2, lane);
@@ -250,9 +264,13 @@ __global__ __launch_bounds__(MWAVES * 64, 1) void attn_mlp_kernel(const shrimp_m
   }
   __syncthreads();
 
-  const float* bias = reinterpret_cast<const float*>(static_cast<const unsigned char*>(a.packed) + BO_OFF);
+  MlpBias bias;
+  load_bias(reinterpret_cast<const float*>(static_cast<const unsigned char*>(a.packed) + BO_OFF),
+            lane, bias);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes);
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.seq, s_bytes);
+  // row mask bytes: rows at or past `rows` read as 0 (not stored)
+  const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.mask, (uint32_t)a.rows);
   // Contiguous, balanced range of 16-row blocks per wave; the next block's
   // attention rows are requested before the current block's math.
   const int64_t nblk = (a.rows + 15) / 16;
@@ -261,19 +279,29 @@ __global__ __launch_bounds__(MWAVES * 64, 1) void attn_mlp_kernel(const shrimp_m
   const int begin = (int)(gw * nblk / tw);
   const int end = (int)((gw + 1) * nblk / tw);
   const int lr = lane & 15, lg = lane >> 4;
+  auto load_m = [&](int row) {
+    const uint32_t off = row < a.rows ? (uint32_t)row : SHRIMP_OOB_OFFSET;
+    return (unsigned)__builtin_amdgcn_raw_buffer_load_b8(mr, off, 0, 0);
+  };
   u32x4 cur[MC / 32], nxt[MC / 32];
   u32x2 sres[MC / 16];
+  unsigned mcur = 0, mnxt = 0;
   if (begin < end) {
+    mnxt = load_m(begin * 16 + lr);
     load_x(a, xr, begin * 16 + lr, lg, nxt);
     load_s(a, sr, begin * 16 + lr, lg, sres);
   }
   for (int blk = begin; blk < end; ++blk) {
 #pragma unroll
     for (int ks = 0; ks < MC / 32; ++ks) cur[ks] = nxt[ks];
+    mcur = mnxt;
     // rows past this wave's range read as zeros (offset past the resource)
     const int nrow = blk + 1 < end ? (blk + 1) * 16 + lr : a.rows;
+    // the next block's mask byte ahead of its rows: a wait for it never waits
+    // for them
+    mnxt = load_m(nrow);
     load_x(a, xr, nrow, lg, nxt);
-    mlp_block(a, wl, bias, sr, cur, blk * 16 + lr, lane, sres, nrow);
+    mlp_block(a, wl, bias, sr, cur, blk * 16 + lr, lane, sres, nrow, mcur != 0);
   }
 }
 
