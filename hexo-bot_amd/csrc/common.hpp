@@ -167,6 +167,39 @@ constexpr uint32_t QKV_B_OFF = QKV_W_BYTES;
 constexpr uint32_t QKV_CS_OFF = QKV_B_OFF + QKV_N * 4;  // fp32 sum over k of the bf16 W'[n][k]
 constexpr uint32_t QKV_PACK_BYTES = QKV_CS_OFF + QKV_N * 4;
 
+// ---- per-channel biases held in registers -------------------------------------
+//
+// NT blocks of 16 channels kept in NT / 4 registers: register r holds at lane
+// (lr, lg) channel lr of block 4 r + lg. An accumulator starts at bias block t
+// with one fp32 MFMA against a one-hot operand (lane (lr, lg): 1 when
+// lg = t % 4), exactly: the products are bias * 1 and bias * 0. This keeps
+// bias loads out of loops whose global loads would otherwise make each bias
+// wait for every earlier load and store (memory operations retire in order).
+template <int NT>
+struct BiasRegs {
+  static_assert(NT % 4 == 0, "bias blocks come in fours");
+  float reg[NT / 4];
+  float onehot[4];
+
+  SHRIMP_DEV void load(const float* bias, int lane) {
+    const int lr = lane & 15, lg = lane >> 4;
+#pragma unroll
+    for (int r = 0; r < NT / 4; ++r) reg[r] = bias[(4 * r + lg) * 16 + lr];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) onehot[t] = lg == t ? 1.0f : 0.0f;
+  }
+  // 16x16 fragment with rows = channels: lane (lr, lg) gets bias[16 t + 4 lg + j]
+  SHRIMP_DEV f32x4 rows(int t) const {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(reg[t >> 2], onehot[t & 3],
+                                                 f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+  }
+  // 16x16 fragment with columns = channels: lane (lr, lg) gets bias[16 t + lr]
+  SHRIMP_DEV f32x4 cols(int t) const {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(onehot[t & 3], reg[t >> 2],
+                                                 f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+  }
+};
+
 SHRIMP_DEV float wave_sum(float v) {
   for (int m = 32; m >= 1; m >>= 1) v += xor_shfl(v, m);
   return v;

@@ -76,30 +76,9 @@ SHRIMP_DEV u32x4 lds_frag(const unsigned char* wl, uint32_t base, int ks, int nb
   return *reinterpret_cast<const u32x4*>(wl + base + (uint32_t)(((ks * nbt + nb) * 64 + lane) * 16));
 }
 
-// The folded biases [bo' | b1' | b2'] are 32 blocks of 16 channels. A wave keeps
-// them in 8 registers, register r holding at lane (lr, lg) channel lr of block
-// 4 r + lg, and starts an accumulator at bias block t with one fp32 MFMA
-// against a one-hot B operand (lane (lr, lg): 1 when lg = t % 4): D[i][j] =
-// bias[16 t + i] exactly. The loop body then issues no bias loads, which would
-// otherwise wait behind the next block's HBM requests (memory loads retire in
-// order).
-struct MlpBias {
-  float reg[8];
-  float onehot[4];
-};
-
-SHRIMP_DEV void load_bias(const float* bias, int lane, MlpBias& mb) {
-  const int lr = lane & 15, lg = lane >> 4;
-#pragma unroll
-  for (int r = 0; r < 8; ++r) mb.reg[r] = bias[(4 * r + lg) * 16 + lr];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) mb.onehot[t] = lg == t ? 1.0f : 0.0f;
-}
-
-SHRIMP_DEV f32x4 bias_acc(const MlpBias& mb, int t) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(mb.reg[t >> 2], mb.onehot[t & 3],
-                                               f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-}
+// The folded biases [bo' | b1' | b2'] are 32 blocks of 16 channels, kept in
+// registers (BiasRegs): the loop body issues no bias loads.
+typedef BiasRegs<(MC + MH + MC) / 16> MlpBias;
 
 // Attention-output fragments (out_proj input) of one 16-row block; rows at
 // or past `rows` read as zeros.
@@ -135,7 +114,7 @@ SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, con
   // accumulators start at the biases
   f32x4 acc[NB1];
 #pragma unroll
-  for (int nb = 0; nb < NB1; ++nb) acc[nb] = bias_acc(bias, nb);
+  for (int nb = 0; nb < NB1; ++nb) acc[nb] = bias.rows(nb);
 
   // ---- out_proj ----------------------------------------------------------
   // (scheduling barriers keep the weight-fragment reads next to their MFMAs;
@@ -193,7 +172,7 @@ SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, con
   // ---- fc1 -> GELU -> fc2, one 32-wide hidden slice at a time ---------------
   f32x4 acc2[NB2];
 #pragma unroll
-  for (int nb = 0; nb < NB2; ++nb) acc2[nb] = bias_acc(bias, TB2 + nb);
+  for (int nb = 0; nb < NB2; ++nb) acc2[nb] = bias.rows(TB2 + nb);
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt) {
     f32x4 ah[2];
@@ -202,7 +181,7 @@ SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, con
       u32x4 w[KS1];
 #pragma unroll
       for (int ks = 0; ks < KS1; ++ks) w[ks] = lds_frag(wl, W1_OFF, ks, 2 * kt + hh, NBH, lane);
-      ah[hh] = bias_acc(bias, TB1 + 2 * kt + hh);
+      ah[hh] = bias.rows(TB1 + 2 * kt + hh);
 #pragma unroll
       for (int ks = 0; ks < KS1; ++ks) ah[hh] = mfma16x16x32(w[ks], hf[ks], ah[hh]);
     }
@@ -265,8 +244,8 @@ __global__ __launch_bounds__(MWAVES * 64, 1) void attn_mlp_kernel(const shrimp_m
   __syncthreads();
 
   MlpBias bias;
-  load_bias(reinterpret_cast<const float*>(static_cast<const unsigned char*>(a.packed) + BO_OFF),
-            lane, bias);
+  bias.load(reinterpret_cast<const float*>(static_cast<const unsigned char*>(a.packed) + BO_OFF),
+            lane);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes);
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.seq, s_bytes);
   // row mask bytes: rows at or past `rows` read as 0 (not stored)

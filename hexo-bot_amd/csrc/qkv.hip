@@ -53,10 +53,16 @@ SHRIMP_DEV void load_rows16(const shrimp_qkv_args& a, __amdgpu_buffer_rsrc_t xr,
 // K comes out of the usual product in that order; V from the product with
 // the operands swapped (rows as A, weights as B), which leaves each lane four
 // consecutive rows of one output channel. Slots of keys >= S are not written.
+// Every store goes through a buffer resource, rows that do not exist at an
+// offset past it (dropped): with no store under a branch, the wait for the
+// next block's rows counts exactly the stores issued after them and never
+// waits for those stores.
 template <bool KVF>
 __global__ __launch_bounds__(QWAVES * 64, 1) void attn_qkv_kernel(const shrimp_qkv_args a,
                                                                   uint32_t x_bytes, int dshift,
-                                                                  unsigned short* kvf, int SP) {
+                                                                  unsigned short* kvf, int SP,
+                                                                  uint32_t q_bytes,
+                                                                  uint32_t kvf_bytes) {
   extern __shared__ __attribute__((aligned(16))) unsigned char wl[];
   constexpr int KS = QC / 32, NB = QN / 16;
   const int lane = threadIdx.x & 63;
@@ -78,8 +84,12 @@ __global__ __launch_bounds__(QWAVES * 64, 1) void attn_qkv_kernel(const shrimp_q
   }
   __syncthreads();
 
-  const float* bias = reinterpret_cast<const float*>(static_cast<const unsigned char*>(a.packed) + QB_OFF);
+  // the folded biases in registers: the block loop issues no bias loads
+  BiasRegs<QN / 16> bias;
+  bias.load(reinterpret_cast<const float*>(static_cast<const unsigned char*>(a.packed) + QB_OFF), lane);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes);
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.qkv, q_bytes);
+  const __amdgpu_buffer_rsrc_t kr = make_rsrc(kvf, kvf_bytes);
   const int d = QC / a.H;
   const int64_t plane = (int64_t)a.B * a.H * a.S * a.dpad;  // one of q / k / v
   const int64_t hstride = (int64_t)a.S * a.dpad;
@@ -106,8 +116,7 @@ __global__ __launch_bounds__(QWAVES * 64, 1) void attn_qkv_kernel(const shrimp_q
     const bool rv = row < a.rows;
     const int bq = rv ? row / a.S : 0;
     const int sq = rv ? row - bq * a.S : 0;
-    unsigned short* rowbase = static_cast<unsigned short*>(a.qkv) +
-                              ((int64_t)bq * a.H * a.S + sq) * a.dpad;
+    const int64_t rowbase = ((int64_t)bq * a.H * a.S + sq) * a.dpad;  // elements
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -118,43 +127,41 @@ __global__ __launch_bounds__(QWAVES * 64, 1) void attn_qkv_kernel(const shrimp_q
       const int which = nb / (QC / 16);
       if (KVF && which == 2) {
         // rows 16 blk + 4 lg .. + 3 of output channel 16 (nb - 16) + lr = head nb - 16, dim lr
-        const float bv = bias[nb * 16 + lr];
-        f32x4 acc = f32x4{bv, bv, bv, bv};
+        f32x4 acc = bias.cols(nb);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) acc = mfma16x16x32(hf[ks], w[ks], acc);
         const int r0 = blk * 16 + lg * 4;
-        if (r0 < a.rows) {
-          const int b0 = r0 / a.S;
-          const int s0 = r0 - b0 * a.S;
-          const int head = nb - 2 * (QC / 16);
-          unsigned short* dst = kvf + (((int64_t)b0 * a.H + head) * 2 + 1) * SP * 16 +
-                                (s0 >> 4) * 256 + (((s0 & 15) >> 2) * 16 + lr) * 4;
-          *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
-        }
+        const int b0 = r0 < a.rows ? r0 / a.S : 0;
+        const int s0 = r0 - b0 * a.S;
+        const int head = nb - 2 * (QC / 16);
+        const uint32_t off =
+            r0 < a.rows ? (uint32_t)(((((int64_t)b0 * a.H + head) * 2 + 1) * SP * 16 + (s0 >> 4) * 256 +
+                                      (((s0 & 15) >> 2) * 16 + lr) * 4) * 2)
+                        : SHRIMP_OOB_OFFSET;
+        __builtin_amdgcn_raw_buffer_store_b64(
+            u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])}, kr, off, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         continue;
       }
-      f32x4 acc = *reinterpret_cast<const f32x4*>(bias + nb * 16 + lg * 4);
+      f32x4 acc = bias.rows(nb);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) acc = mfma16x16x32(w[ks], hf[ks], acc);
       const int within = (nb % (QC / 16)) * 16 + lg * 4;
       const int head = within >> dshift;
       const int dd = within & (d - 1);
+      const u32x2 pk{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
       if (KVF && which == 1) {
-        if (rv) {
-          unsigned short* dst = kvf + (((int64_t)bq * a.H + head) * 2) * SP * 16 + (sq >> 4) * 256 +
-                                (lg * 16 + (sq & 15)) * 4;
-          *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
-        }
+        const uint32_t off =
+            rv ? (uint32_t)(((((int64_t)bq * a.H + head) * 2) * SP * 16 + (sq >> 4) * 256 +
+                             (lg * 16 + (sq & 15)) * 4) * 2)
+               : SHRIMP_OOB_OFFSET;
+        __builtin_amdgcn_raw_buffer_store_b64(pk, kr, off, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         continue;
       }
-      if (rv) {
-        u32x2 pk;
-        pk.x = pack_bf16x2(acc[0], acc[1]);
-        pk.y = pack_bf16x2(acc[2], acc[3]);
-        *reinterpret_cast<u32x2*>(rowbase + which * plane + head * hstride + dd) = pk;
-      }
+      const uint32_t off =
+          rv ? (uint32_t)((rowbase + which * plane + head * hstride + dd) * 2) : SHRIMP_OOB_OFFSET;
+      __builtin_amdgcn_raw_buffer_store_b64(pk, qr, off, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -228,6 +235,8 @@ extern "C" int shrimp_attn_qkv(const shrimp_qkv_args* a, void* stream) {
   SHRIMP_REQUIRE(a->x_sr >= QC && a->x_sr % 8 == 0, "attn_qkv: x row stride");
   const int64_t xe = ((int64_t)(a->rows - 1) * a->x_sr + QC) * 2;
   SHRIMP_REQUIRE(xe < (int64_t)0x7FFF0000, "attn_qkv: activation buffer too large");
+  const int64_t qe = (int64_t)3 * a->B * a->H * a->S * a->dpad * 2;  // q, k and v planes
+  SHRIMP_REQUIRE(qe < (int64_t)0x7FFF0000, "attn_qkv: q/k/v buffer too large");
   SHRIMP_REQUIRE((size_t)max_lds_per_block() >= QW_LDS, "attn_qkv: needs %u bytes of LDS",
                  (unsigned)QW_LDS);
   int dev = 0, cus = 0;
@@ -242,7 +251,7 @@ extern "C" int shrimp_attn_qkv(const shrimp_qkv_args* a, void* stream) {
   // row counts spread over more units, each staging the weights once
   const int grid = (int)std::min<int64_t>(cus, std::max<int64_t>((nblk + QWAVES - 1) / QWAVES, (nblk + 3) / 4));
   hipLaunchKernelGGL(attn_qkv_kernel<false>, dim3(grid), dim3(QWAVES * 64), QW_LDS, as_stream(stream),
-                     *a, (uint32_t)xe, dshift, (unsigned short*)nullptr, 0);
+                     *a, (uint32_t)xe, dshift, (unsigned short*)nullptr, 0, (uint32_t)qe, 0u);
   return check_launch("attn_qkv");
 }
 
@@ -259,7 +268,9 @@ extern "C" int shrimp_attn_qkv_kvf(const shrimp_qkv_args* a, void* kvf, void* st
   SHRIMP_REQUIRE(a->x_sr >= QC && a->x_sr % 8 == 0, "attn_qkv_kvf: x row stride");
   const int SP = (a->S + 15) & ~15;
   const int64_t xe = ((int64_t)(a->rows - 1) * a->x_sr + QC) * 2;
-  SHRIMP_REQUIRE(xe < (int64_t)0x7FFF0000 && (int64_t)a->B * a->H * SP * 64 < (int64_t)0x7FFF0000,
+  const int64_t qe = (int64_t)a->B * a->H * a->S * 16 * 2;  // the q plane
+  const int64_t ke = (int64_t)a->B * a->H * SP * 64;       // K and V fragments
+  SHRIMP_REQUIRE(xe < (int64_t)0x7FFF0000 && qe < (int64_t)0x7FFF0000 && ke < (int64_t)0x7FFF0000,
                  "attn_qkv_kvf: buffers too large");
   SHRIMP_REQUIRE((size_t)max_lds_per_block() >= QW_LDS, "attn_qkv_kvf: needs %u bytes of LDS",
                  (unsigned)QW_LDS);
@@ -271,6 +282,7 @@ extern "C" int shrimp_attn_qkv_kvf(const shrimp_qkv_args* a, void* kvf, void* st
   const int64_t nblk = (a->rows + 15) / 16;
   const int grid = (int)std::min<int64_t>(cus, std::max<int64_t>((nblk + QWAVES - 1) / QWAVES, (nblk + 3) / 4));
   hipLaunchKernelGGL(attn_qkv_kernel<true>, dim3(grid), dim3(QWAVES * 64), QW_LDS, as_stream(stream),
-                     *a, (uint32_t)xe, 4, static_cast<unsigned short*>(kvf), SP);
+                     *a, (uint32_t)xe, 4, static_cast<unsigned short*>(kvf), SP, (uint32_t)qe,
+                     (uint32_t)ke);
   return check_launch("attn_qkv_kvf");
 }
