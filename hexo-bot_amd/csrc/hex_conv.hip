@@ -18,6 +18,8 @@
 //               lane groups with two cross-lane steps.
 // Next k-step fragments are loaded before the current step's MFMAs issue, so
 // the gather latency overlaps the matrix work of the previous step.
+#include <type_traits>
+
 #include "capi.hpp"
 #include "common.hpp"
 
@@ -49,6 +51,18 @@ SHRIMP_DEV unsigned relu_bf16x2(unsigned w) {
 // of row block mb, for rows that exist.
 enum : int { PS_GLOBAL = 0, PS_REGS = 1, PS_LDS = 2, PS_LDSREG = 3 };
 
+// Store functors with a `kBuffered` member write through a buffer resource and
+// take every row, absent ones at an offset past the resource (dropped); with
+// them the epilogue also reads the residual rows through the functor's
+// `rres` resource, absent rows reading zeros. No load or store then sits under
+// a per-row branch, so waiting for a prefetched residual row counts exactly
+// the requests issued after it (memory operations retire in order; a branch
+// makes the compiler assume the fewest and wait for every earlier store).
+template <class T, class = void>
+struct is_buffered_store : std::false_type {};
+template <class T>
+struct is_buffered_store<T, std::void_t<decltype(T::kBuffered)>> : std::true_type {};
+
 template <int COUT, int MB, int EPI, int PSRC, typename Store>
 SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16][MB],
                               const int (&rb)[MB], const int (&rn)[MB], const bool (&rv)[MB],
@@ -58,6 +72,7 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
   constexpr bool HEAD = (EPI & EPI_HEAD) != 0, RELU = (EPI & EPI_RELU) != 0;
   constexpr bool BACC = (EPI & EPI_BACC) != 0;
   constexpr bool PRE = PSRC == PS_REGS;
+  constexpr bool BUF = is_buffered_store<std::remove_cv_t<std::remove_reference_t<Store>>>::value;
   constexpr bool FROM_LDS = PSRC == PS_LDS || PSRC == PS_LDSREG;
   constexpr bool HREG = PSRC == PS_LDSREG;  // bias / ln_w read from LDS once, kept in registers
   constexpr bool LNMASK = LN && FROM_LDS;   // masking folded into the LayerNorm
@@ -109,7 +124,13 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
   const float hb = HEAD ? a.head_b[0] : 0.f;
 
   auto resid_row = [&](int mb, u32x2 (&r)[NB]) {
-    if constexpr (RESID) {
+    if constexpr (RESID && BUF) {
+      const uint32_t ro =
+          rv[mb] ? (uint32_t)(((int64_t)rb[mb] * a.r_sb + (int64_t)rn[mb] * a.r_sn + lg * 4) * 2)
+                 : SHRIMP_OOB_OFFSET;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) r[nb] = buf_load8(store.rres, ro + nb * 32);
+    } else if constexpr (RESID) {
       const unsigned short* rp = static_cast<const unsigned short*>(a.resid) +
                                  (int64_t)rb[mb] * a.r_sb + (int64_t)rn[mb] * a.r_sn + lg * 4;
 #pragma unroll
@@ -186,7 +207,7 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
     }
     // ReLU and the row mask in one clamp: med3(v, 0, +inf) = relu(v), med3(v, 0, 0) = 0.
     const float cap = live[mb] ? __builtin_inff() : 0.f;
-    if (rv[mb]) {
+    if (BUF || rv[mb]) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         float o[4];
@@ -266,6 +287,35 @@ struct GlobalRowStore16 {
     const auto sx = __builtin_amdgcn_permlane16_swap(pend.x, pk.x, false, false);
     const auto sy = __builtin_amdgcn_permlane16_swap(pend.y, pk.y, false, false);
     *reinterpret_cast<u32x4*>(p[mb] + (nb >> 1) * 32) = u32x4{sx[0], sy[0], sx[1], sy[1]};
+  }
+};
+
+// GlobalRowStore16 through buffer resources (see is_buffered_store): `out`
+// spans o_bytes, the residual rows `rres` r_bytes.
+template <int MB>
+struct BufRowStore16 {
+  static constexpr bool kBuffered = true;
+  __amdgpu_buffer_rsrc_t orr, rres;
+  uint32_t off[MB];
+  u32x2 pend;
+  SHRIMP_DEV BufRowStore16(const shrimp_conv_args& a, const int (&rb)[MB], const int (&rn)[MB],
+                           const bool (&rv)[MB], int lg, uint32_t o_bytes, uint32_t r_bytes)
+      : orr(make_rsrc(a.out, o_bytes)), rres(make_rsrc(a.resid, r_bytes)) {
+    const int sub = (lg & 1) * 16 + (lg >> 1) * 8;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      off[mb] = rv[mb] ? (uint32_t)(((int64_t)rb[mb] * a.o_sb + (int64_t)rn[mb] * a.o_sn + sub) * 2)
+                       : SHRIMP_OOB_OFFSET;
+  }
+  SHRIMP_DEV void operator()(int mb, int nb, u32x2 pk) {
+    if ((nb & 1) == 0) {
+      pend = pk;
+      return;
+    }
+    const auto sx = __builtin_amdgcn_permlane16_swap(pend.x, pk.x, false, false);
+    const auto sy = __builtin_amdgcn_permlane16_swap(pend.y, pk.y, false, false);
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{sx[0], sy[0], sx[1], sy[1]}, orr,
+                                           off[mb] + (uint32_t)((nb >> 1) * 64), 0, 0);
   }
 };
 
@@ -762,7 +812,8 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
 // them), and a wave only touches its own rows.
 __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_args c1,
                                                            const shrimp_conv_args c2,
-                                                           uint32_t x_bytes, uint32_t w_bytes) {
+                                                           uint32_t x_bytes, uint32_t w_bytes,
+                                                           uint32_t o_bytes) {
   extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
   BigTile t;
   big_setup(t, c1, xs, x_bytes);
@@ -817,8 +868,9 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
   asm volatile("" : "+v"(t.lane));
   t.lg = t.lane >> 4;
   big_pass(acc, wf, t, xs, wr2);
-  conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(c2, acc, t.rb, t.rn, t.rv, t.lg, lp2,
-                                                    GlobalRowStore16<8>(c2, t.rb, t.rn, t.lg));
+  conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(
+      c2, acc, t.rb, t.rn, t.rv, t.lg, lp2,
+      BufRowStore16<8>(c2, t.rb, t.rn, t.rv, t.lg, o_bytes, x_bytes));
 }
 
 // ---- weight packing ------------------------------------------------------------
@@ -1068,11 +1120,14 @@ extern "C" int shrimp_conv_block(const shrimp_conv_args* c1, const shrimp_conv_a
   a2.mask = c1->mask;
   a2.B = c1->B;
   a2.N = c1->N;
+  const int64_t o_extent =
+      (int64_t)(c1->B - 1) * c2->o_sb + (int64_t)(c1->N - 1) * c2->o_sn + 128;
+  SHRIMP_REQUIRE(o_extent * 2 < (int64_t)0x7FFF0000, "conv_block: output buffer too large");
   const int waves = (c1->N + 127) / 128;
   const size_t lds = (size_t)big_rows_padded(c1->N) * 256 + 2 * BIG_PARAMS * sizeof(float);
   const uint32_t xb = (uint32_t)(x_extent * 2);
   const uint32_t wb = (uint32_t)shrimp_conv_wpack_bytes(7, 128, 128);
   hipLaunchKernelGGL(hex_block_kernel, dim3(c1->B), dim3(64 * waves), lds, as_stream(stream), *c1,
-                     a2, xb, wb);
+                     a2, xb, wb, (uint32_t)(o_extent * 2));
   return check_launch("conv_block");
 }
