@@ -406,7 +406,8 @@ SHRIMP_DEV u32x2 opaque2(u32x2 v) {
 template <int DP, int HG, bool PAIR, int PROJ, int NW>
 __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const shrimp_attn_args a, float qk_scale,
                                                    uint32_t qkv_bytes, int npos,
-                                                   const shrimp_attn_proj_args p, uint32_t x_bytes) {
+                                                   const shrimp_attn_proj_args p, uint32_t x_bytes,
+                                                   uint32_t o_bytes) {
   // PROJ 1, 2: q/k/v projected in the kernel; 3: staged (K and V fragments
   // and the key table by DMA from shrimp_attn_qkv_kvf / shrimp_attn_keys)
   constexpr bool PJ = PROJ == 1 || PROJ == 2;
@@ -454,13 +455,14 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = wave_id();
   const int lr = lane & 15;
   const int lg = lane >> 4;
   const int nkb = LP / 16;
   const __amdgpu_buffer_rsrc_t qrs = make_rsrc(a.q, qkv_bytes);
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.k, qkv_bytes);
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(a.v, qkv_bytes);
+  const __amdgpu_buffer_rsrc_t ors = make_rsrc(a.o, o_bytes);
   const int64_t pos_base = (int64_t)b * a.qkv_sb;
 
   // Whole query blocks round-robin over the NW waves. When one block is left
@@ -893,7 +895,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
   // (slot j of a wave = its block wave + 4 j; the split block's slot follows
   // the wave's own blocks).
   auto run_block = [&](int qb, int slot, int k0, int k1, AttnQuery& qi, float (&m)[HG],
-                       float (&l)[HG], f32x4 (&o)[HG][KD]) {
+                       float (&l)[HG], f32x4 (&o)[HG][KD], const u32x2 (&qin)[HG][KD]) {
     qi.query = qb * 16 + lr;
     qi.qv = qi.query < L;
     qi.qtok = qi.query < nt;
@@ -921,10 +923,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
 #pragma unroll
       for (int h = 0; h < HG; ++h)
 #pragma unroll
-        for (int kd = 0; kd < KD; ++kd) {
-          const int64_t e = pos_base + (int64_t)(h0 + h) * a.qkv_sh + qi.query * DP + kd * 16 + lg * 4;
-          qf[h][kd] = buf_load8(qrs, qi.qv ? (uint32_t)(e * 2) : SHRIMP_OOB_OFFSET);
-        }
+        for (int kd = 0; kd < KD; ++kd) qf[h][kd] = qin[h][kd];
     }
 #pragma unroll
     for (int h = 0; h < HG; ++h) {
@@ -1019,26 +1018,42 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
 #undef SHRIMP_CHUNK_FLS
   };
 
-  auto store_block = [&](const AttnQuery& qi, const float (&l)[HG], const f32x4 (&o)[HG][KD]) {
+  // Output rows through a buffer resource, absent ones (query past the live
+  // bound, channel past d, every row when !on) at an offset past it: no store
+  // sits under a branch, so the wait for the next block's prefetched queries
+  // counts exactly the stores issued after them (memory operations retire in
+  // order).
+  auto store_block = [&](const AttnQuery& qi, const float (&l)[HG], const f32x4 (&o)[HG][KD], bool on) {
 #pragma unroll
     for (int h = 0; h < HG; ++h) {
       // the row sum sits in lane group 0; broadcast it to the query's lanes
       const float lt = __shfl(l[h], lr, 64);
       const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-      if (!qi.qv) continue;
-      unsigned short* orow = static_cast<unsigned short*>(a.o) + (int64_t)b * a.o_sb +
-                             (int64_t)(h0 + h) * a.o_sh + (int64_t)qi.query * a.o_sr;
+      const int64_t orow = (int64_t)b * a.o_sb + (int64_t)(h0 + h) * a.o_sh + (int64_t)qi.query * a.o_sr;
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd) {
         const int e = kd * 16 + lg * 4;
-        if (e < a.d) {
-          u32x2 pk;
-          pk.x = pack_bf16x2(o[h][kd][0] * inv, o[h][kd][1] * inv);
-          pk.y = pack_bf16x2(o[h][kd][2] * inv, o[h][kd][3] * inv);
-          *reinterpret_cast<u32x2*>(orow + e) = pk;
-        }
+        u32x2 pk;
+        pk.x = pack_bf16x2(o[h][kd][0] * inv, o[h][kd][1] * inv);
+        pk.y = pack_bf16x2(o[h][kd][2] * inv, o[h][kd][3] * inv);
+        const uint32_t off = on && qi.qv && e < a.d ? (uint32_t)((orow + e) * 2) : SHRIMP_OOB_OFFSET;
+        __builtin_amdgcn_raw_buffer_store_b64(pk, ors, off, 0, 0);
       }
     }
+  };
+
+  // Query fragments of block qb (rows past the live bound, and every row when
+  // !on, read zeros); each block's are requested one block ahead, with no
+  // branch around the request.
+  auto load_q = [&](int qb, bool on, u32x2 (&qf)[HG][KD]) {
+    const int query = qb * 16 + lr;
+#pragma unroll
+    for (int h = 0; h < HG; ++h)
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) {
+        const int64_t e = pos_base + (int64_t)(h0 + h) * a.qkv_sh + query * DP + kd * 16 + lg * 4;
+        qf[h][kd] = buf_load8(qrs, on && query < L ? (uint32_t)(e * 2) : SHRIMP_OOB_OFFSET);
+      }
   };
 
   // (query blocks round-robin over the waves, the split last block: see nmain)
@@ -1051,14 +1066,36 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
   AttnQuery qi;
   float m[HG], l[HG];
   f32x4 o[HG][KD];
-  for (int qb = wave + NW * qz, slot = 0;; qb += NW * nz, ++slot) {
-    const bool tail = qb >= nmain;
-    if (tail && !tail_here) break;
+  u32x2 qnext[HG][KD];
+  // This wave's whole blocks are qb0, qb0 + NW nz, ... below nmain (nr of
+  // them), then, where tail_here, its key range of the split block (round
+  // nr). Every round issues the same requests and stores, none under a
+  // branch.
+  const int qb0 = wave + NW * qz;
+  const int nr = qb0 < nmain ? (nmain - 1 - qb0) / (NW * nz) + 1 : 0;
+  const int rounds = nr + (tail_here ? 1 : 0);
+  if constexpr (!PJ) load_q(nr > 0 ? qb0 : nmain, rounds > 0, qnext);
+  // as many dropped stores (distinct offsets past the resource, so none is
+  // merged away) as a round issues after its prefetch: the loop is then
+  // entered with the same requests in flight as from its last round, and the
+  // wait for the prefetched queries counts the stores
+#pragma unroll
+  for (int i = 0; i < HG * KD; ++i)
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{0u, 0u}, ors, SHRIMP_OOB_OFFSET - i * 256u, 0, 0);
+  for (int r = 0; r < rounds; ++r) {
+    const bool tail = r == nr;
+    const int qb = tail ? nmain : qb0 + r * NW * nz;
+    u32x2 qcur[HG][KD];
+#pragma unroll
+    for (int h = 0; h < HG; ++h)
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) qcur[h][kd] = qnext[h][kd];
+    if constexpr (!PJ) load_q(r + 1 < nr ? qb + NW * nz : nmain, r + 1 < rounds, qnext);
     const int k0 = tail ? (wave * nkb) / NW : 0;
     const int k1 = tail ? ((wave + 1) * nkb) / NW : nkb;
-    run_block(tail ? nmain : qb, slot, k0, k1, qi, m, l, o);
-    if (tail) break;
-    store_block(qi, l, o);
+    run_block(qb, r, k0, k1, qi, m, l, o, qcur);
+    // the split block's partial state is merged below, not stored
+    store_block(qi, l, o, !tail);
   }
   if (tail_here) {
     __syncthreads();  // K and V are no longer read: their LDS holds the partials
@@ -1099,7 +1136,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
         }
         l[h] = lsum;
       }
-      store_block(qi, l, o);
+      store_block(qi, l, o, true);
     }
   }
 
@@ -1115,6 +1152,15 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const sh
     *reinterpret_cast<u32x2*>(orow + e) = u32x2{0u, 0u};
   }
 }
+
+// Bytes spanned by the output rows (a.o); callers have checked them against
+// the 32-bit buffer-offset limit (attn_out_fits).
+static int64_t attn_out_extent(const shrimp_attn_args* a) {
+  return ((int64_t)(a->B - 1) * a->o_sb + (int64_t)(a->H - 1) * a->o_sh + (int64_t)(a->S - 1) * a->o_sr +
+          a->d) * 2;
+}
+static bool attn_out_fits(const shrimp_attn_args* a) { return attn_out_extent(a) < (int64_t)0x7FFF0000; }
+static uint32_t attn_out_bytes(const shrimp_attn_args* a) { return (uint32_t)attn_out_extent(a); }
 
 // LDS bytes of one workgroup; npos = pair-table rows (pair mode only).
 static size_t attn_smem_bytes(int DP, int HG, int S, int npos, bool pair) {
@@ -1137,7 +1183,7 @@ static int launch_attn(const shrimp_attn_args* a, float qk_scale, uint32_t qkv_b
   dim3 grid(a->H / HG, a->B, z);
   const shrimp_attn_proj_args none{};
   hipLaunchKernelGGL((attn_kernel<DP, HG, PAIR, 0, NW>), grid, dim3(64 * NW), smem, st, *a,
-                     qk_scale, qkv_bytes, npos, none, 0u);
+                     qk_scale, qkv_bytes, npos, none, 0u, attn_out_bytes(a));
   return check_launch("attn");
 }
 
@@ -1324,6 +1370,7 @@ extern "C" int shrimp_attn(const shrimp_attn_args* a, void* stream) {
                  a->d, a->dpad);
   SHRIMP_REQUIRE(a->o_sb % 4 == 0 && a->o_sh % 4 == 0 && a->o_sr % 4 == 0,
                  "attn: output strides must be multiples of 4");
+  SHRIMP_REQUIRE(attn_out_fits(a), "attn: output buffer too large");
   SHRIMP_REQUIRE(a->n_tokens >= 0 && a->n_tokens <= a->S, "attn: bad n_tokens");
   const int64_t extent =
       (int64_t)(a->B - 1) * a->qkv_sb + (int64_t)(a->H - 1) * a->qkv_sh + (int64_t)a->S * a->dpad;
@@ -1358,6 +1405,7 @@ extern "C" int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_pr
   SHRIMP_REQUIRE(a->o && a->seq_lens && p->x && p->packed, "attn_fused: null pointer");
   SHRIMP_REQUIRE(a->o_sb % 4 == 0 && a->o_sh % 4 == 0 && a->o_sr % 4 == 0,
                  "attn_fused: output strides must be multiples of 4");
+  SHRIMP_REQUIRE(attn_out_fits(a), "attn: output buffer too large");
   SHRIMP_REQUIRE(a->n_tokens >= 0 && a->n_tokens <= a->S, "attn_fused: bad n_tokens");
   SHRIMP_REQUIRE(a->btab && a->lut_m >= 0 && a->lut_m <= 64, "attn_fused: needs btab");
   SHRIMP_REQUIRE(a->n_tokens == a->S || (a->coords && a->mask),
@@ -1375,10 +1423,10 @@ extern "C" int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_pr
   // the XCD grouping needs whole groups of 8 positions (grid.x = 4 head pairs)
   if (a->B % 8 == 0)
     hipLaunchKernelGGL((attn_kernel<16, 2, false, 2, 4>), grid, dim3(256), smem, as_stream(stream),
-                       *a, qk_scale, 0u, w * w, *p, (uint32_t)xe);
+                       *a, qk_scale, 0u, w * w, *p, (uint32_t)xe, attn_out_bytes(a));
   else
     hipLaunchKernelGGL((attn_kernel<16, 2, false, 1, 4>), grid, dim3(256), smem, as_stream(stream),
-                       *a, qk_scale, 0u, w * w, *p, (uint32_t)xe);
+                       *a, qk_scale, 0u, w * w, *p, (uint32_t)xe, attn_out_bytes(a));
   return check_launch("attn_fused");
 }
 
@@ -1418,6 +1466,7 @@ extern "C" int shrimp_attn_staged(const shrimp_attn_args* a, const void* kvf, co
   SHRIMP_REQUIRE(a->d > 0 && a->d % 4 == 0 && a->d <= 16, "attn_staged: head dim %d", a->d);
   SHRIMP_REQUIRE(a->o_sb % 4 == 0 && a->o_sh % 4 == 0 && a->o_sr % 4 == 0,
                  "attn_staged: output strides must be multiples of 4");
+  SHRIMP_REQUIRE(attn_out_fits(a), "attn: output buffer too large");
   SHRIMP_REQUIRE(a->n_tokens >= 0 && a->n_tokens <= a->S, "attn_staged: bad n_tokens");
   SHRIMP_REQUIRE(a->lut_m >= 0 && a->lut_m <= 64, "attn_staged: lut_m");
   const int SP = (a->S + 15) & ~15;
@@ -1442,6 +1491,6 @@ extern "C" int shrimp_attn_staged(const shrimp_attn_args* a, const void* kvf, co
   dim3 grid(a->H / 2, a->B, z);
   const shrimp_attn_proj_args none{};
   hipLaunchKernelGGL((attn_kernel<16, 2, false, 3, NW>), grid, dim3(64 * NW), smem, as_stream(stream),
-                     s, qk_scale, (uint32_t)qe, 0, none, 0u);
+                     s, qk_scale, (uint32_t)qe, 0, none, 0u, attn_out_bytes(a));
   return check_launch("attn_staged");
 }

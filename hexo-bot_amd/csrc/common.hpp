@@ -86,6 +86,12 @@ SHRIMP_DEV f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c) {
 
 // ---- cross-lane -----------------------------------------------------------------
 
+// Index of this wave in its workgroup, as a wave-uniform (scalar) value: the
+// compiler cannot prove threadIdx.x / 64 uniform, and loops bounded by a value
+// it takes as divergent are built as masked loops whose memory requests it
+// can no longer count precisely.
+SHRIMP_DEV int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 SHRIMP_DEV float xor_shfl(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
 // Sum over the 4 lane groups (l/16 = 0..3) sharing the same l % 16.

@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
   constexpr bool CRES = (F & G_CRES) != 0, LRES = (F & G_LRES) != 0;
   constexpr bool GELU = (F & G_GELU) != 0, QKV = (F & G_QKV) != 0, HEAD = (F & G_HEAD) != 0;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int lr = lane & 15;
   const int lg = lane >> 4;
   const int64_t R = (int64_t)g.B * g.N;

@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void hex_conv_kernel(const shrimp_conv_args
                                                           uint32_t x_bytes, uint32_t w_bytes) {
   constexpr int NB = COUT / 16;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int lr = lane & 15;
   const int lg = lane >> 4;
   const int N = a.N;
@@ -439,7 +439,7 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
   extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int lr = lane & 15;
   const int lg = lane >> 4;
   const int N = a.N;
@@ -655,7 +655,7 @@ SHRIMP_DEV void big_setup(BigTile& t, const shrimp_conv_args& a, unsigned char* 
                           uint32_t x_bytes) {
   constexpr int T = 7, MB = 8;
   t.lane = threadIdx.x & 63;
-  t.wave = threadIdx.x >> 6;
+  t.wave = wave_id();
   t.nw = blockDim.x >> 6;
   t.lg = t.lane >> 4;
   t.N = a.N;

@@ -317,7 +317,7 @@ __global__ __launch_bounds__(64 * RT_MAX_WAVES) void conv_ln_raytap_kernel(
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int N = a.N;
   const int b = (int)blockIdx.x;
-  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  const int lane = (int)threadIdx.x & 63, wave = wave_id();
   const int lr = lane & 15, lg = lane >> 4;
   unsigned char* xs = lds;  // (N + 1) rows of RS bytes, later the output rows
   unsigned char* al = lds + rt_rows_bytes(N, CIN, COUT, (int)(blockDim.x >> 6));  // alpha (5, CIN) fp16

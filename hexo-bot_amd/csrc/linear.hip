@@ -18,7 +18,7 @@ __global__ __launch_bounds__(256, 2) void linear_kernel(const shrimp_linear_args
                                                         uint32_t x_bytes, uint32_t w_bytes) {
   constexpr int KS = K / 32;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int lr = lane & 15;
   const int lg = lane >> 4;
   const int row_base = (blockIdx.x * 4 + wave) * (MB * 16);

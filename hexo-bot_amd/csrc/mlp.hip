@@ -225,7 +225,7 @@ __global__ __launch_bounds__(MWAVES * 64, 1) void attn_mlp_kernel(const shrimp_m
                                                                   uint32_t s_bytes) {
   extern __shared__ __attribute__((aligned(16))) unsigned char wl[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
 
   // The packed fragments of all three matrices into LDS (16-byte chunks).
   {

@@ -66,7 +66,7 @@ __global__ __launch_bounds__(QWAVES * 64, 1) void attn_qkv_kernel(const shrimp_q
   extern __shared__ __attribute__((aligned(16))) unsigned char wl[];
   constexpr int KS = QC / 32, NB = QN / 16;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int lr = lane & 15, lg = lane >> 4;
 
   {
@@ -101,6 +101,13 @@ __global__ __launch_bounds__(QWAVES * 64, 1) void attn_qkv_kernel(const shrimp_q
   const int end = (int)((gw + 1) * nblk / tw);
   u32x4 cur[KS], nxt[KS];
   if (begin < end) load_rows16(a, xr, begin * 16 + lr, lg, nxt);
+  // as many dropped stores (distinct offsets past the resource, so none is
+  // merged away) as a block issues after its prefetch: the loop is then
+  // entered with the same requests in flight as from its last block, and the
+  // wait for the prefetched rows counts the stores instead of waiting for them
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{0u, 0u}, qr, SHRIMP_OOB_OFFSET - i * 256u, 0, 0);
   for (int blk = begin; blk < end; ++blk) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) cur[ks] = nxt[ks];

@@ -408,7 +408,7 @@ __global__ __launch_bounds__(kHeadThreads) void value_head_kernel(const shrimp_t
 
 // ---- serve decode (inference.py:998-1042, losses.py:40-60) ---------------------
 __device__ float block_reduce(float v, bool is_max, float* red) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   for (int m = 32; m >= 1; m >>= 1) {
     const float o = __shfl_xor(v, m, 64);
     v = is_max ? fmaxf(v, o) : v + o;
