@@ -206,13 +206,19 @@ __global__ void fill_tokens_kernel(const float* __restrict__ tokens, int n_token
 // Pass 1, one workgroup per position: final LayerNorm of every row (cells
 // masked), written to out_seq; the value-head inputs [T0 | T1 | pooled] and
 // [T4 | T5 | pooled] go to the workspace (B, 6C) fp32.
-// A row is handled by TPR = C / 8 lanes (16 bytes each), 256 / TPR rows per
-// pass, four passes in flight; row statistics reduce over the TPR lanes.
+// A row is handled by TPR = C / 8 lanes (8 channels each), 256 / TPR rows per
+// pass, U passes per chunk, a chunk's rows and mask bytes requested at once
+// (at C = 128 a position of up to 272 rows is one chunk). Rows go in and out
+// through buffer resources (rows past S or channels past C at an offset past
+// them), with no request or store under a branch. Row statistics reduce over
+// the TPR lanes.
 // F32: seq and out_seq hold fp32 rows instead of bf16 (the fp32 serve mode).
 template <int TPR, bool F32>
-__global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a) {
+__global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a, uint32_t seq_bytes,
+                                                       uint32_t mask_bytes, uint32_t ws_bytes) {
   constexpr int RPP = 256 / TPR;  // rows per pass
-  constexpr int U = 4;            // passes in flight
+  constexpr int U = F32 ? 4 : 17;  // passes per chunk (bf16, C = 128: a position of up to 272 rows)
+  constexpr int EB = F32 ? 4 : 2;  // bytes per element
   extern __shared__ float fl[];   // [RPP][C] pooled partial sums, then [RPP] counts
   const int b = blockIdx.x;
   const int C = a.C, S = a.S, nt = a.n_tokens, N = S - nt;
@@ -221,11 +227,12 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a)
   const int rs = t / TPR;          // row slot
   const int c0 = sub * 8;
   const bool cv = c0 < C;
-  const uint16_t* seq = static_cast<const uint16_t*>(a.seq) + (int64_t)b * a.s_sb;
-  uint16_t* outs = static_cast<uint16_t*>(a.out_seq) + (int64_t)b * a.s_sb;
-  const float* seq32 = static_cast<const float*>(a.seq) + (int64_t)b * a.s_sb;
-  float* outs32 = static_cast<float*>(a.out_seq) + (int64_t)b * a.s_sb;
-  float* vin = a.workspace + (int64_t)b * 6 * C;
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.seq, seq_bytes);
+  const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.out_seq, seq_bytes);
+  const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.mask, mask_bytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.workspace, ws_bytes);
+  const uint32_t pos_off = (uint32_t)((int64_t)b * a.s_sb * EB);
+  const uint32_t vin_off = (uint32_t)((int64_t)b * 6 * C * 4);
   float w[8], bb[8], pool[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -235,24 +242,31 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a)
   }
   int cnt = 0;
   const float invc = 1.0f / (float)C;
-  for (int r0 = 0; r0 < S; r0 += U * RPP) {
-    u32x4 raw[U], raw2[F32 ? U : 1];
+  const int nchunk = (S + U * RPP - 1) / (U * RPP);
+  // byte offset of this lane's 8 channels of row `row`, or past the buffer
+  auto row_off = [&](int row) {
+    return row < S && cv ? pos_off + (uint32_t)((row * C + c0) * EB) : SHRIMP_OOB_OFFSET;
+  };
+  constexpr int U2 = F32 ? U : 1;  // second 16 bytes of an fp32 row chunk
+  auto load = [&](int chunk, u32x4 (&raw)[U], u32x4 (&raw2)[U2], unsigned (&mk)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int row = r0 + u * RPP + rs;
-      const bool ok = row < S && cv;
-      if constexpr (F32) {
-        const u32x4* p = reinterpret_cast<const u32x4*>(seq32 + (int64_t)row * C + c0);
-        raw[u] = ok ? p[0] : u32x4{0u, 0u, 0u, 0u};
-        raw2[u] = ok ? p[1] : u32x4{0u, 0u, 0u, 0u};
-      } else {
-        raw[u] = ok ? *reinterpret_cast<const u32x4*>(seq + (int64_t)row * C + c0)
-                    : u32x4{0u, 0u, 0u, 0u};
-      }
+      const int row = chunk * U * RPP + u * RPP + rs;
+      const uint32_t off = chunk < nchunk ? row_off(row) : SHRIMP_OOB_OFFSET;
+      raw[u] = buf_load16(sr, off);
+      if constexpr (F32) raw2[u] = buf_load16(sr, off + 16);
+      const bool cell = row >= nt && row < S && chunk < nchunk;
+      mk[u] = (unsigned)__builtin_amdgcn_raw_buffer_load_b8(
+          mr, cell ? (uint32_t)((int64_t)b * N + (row - nt)) : SHRIMP_OOB_OFFSET, 0, 0);
     }
+  };
+  for (int ch = 0; ch < nchunk; ++ch) {
+    u32x4 raw[U], raw2[U2];
+    unsigned mk[U];
+    load(ch, raw, raw2, mk);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int row = r0 + u * RPP + rs;
+      const int row = ch * U * RPP + u * RPP + rs;
       float x[8];
       float s = 0.f;
 #pragma unroll
@@ -279,35 +293,43 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a)
 #pragma unroll
       for (int m = 1; m < TPR; m <<= 1) q += __shfl_xor(q, m, 64);
       const float rstd = rsqrtf(q * invc + a.eps);
-      if (row >= S || !cv) continue;
+      const bool rv = row < S && cv;
       const bool cell = row >= nt;
-      const bool live = !cell || a.mask[(int64_t)b * N + (row - nt)] != 0;
+      const bool live = !cell || mk[u] != 0;
       float y[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) y[e] = live ? fmaf(x[e] * rstd, w[e], bb[e]) : 0.f;
+      const uint32_t off = row_off(row);
       if constexpr (F32) {
-        f32x4* p = reinterpret_cast<f32x4*>(outs32 + (int64_t)row * C + c0);
-        p[0] = f32x4{y[0], y[1], y[2], y[3]};
-        p[1] = f32x4{y[4], y[5], y[6], y[7]};
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]), __float_as_uint(y[3])},
+            orr, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{__float_as_uint(y[4]), __float_as_uint(y[5]), __float_as_uint(y[6]), __float_as_uint(y[7])},
+            orr, off + 16, 0, 0);
       } else {
-        *reinterpret_cast<u32x4*>(outs + (int64_t)row * C + c0) =
+        __builtin_amdgcn_raw_buffer_store_b128(
             u32x4{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]),
-                  pack_bf16x2(y[6], y[7])};
+                  pack_bf16x2(y[6], y[7])},
+            orr, off, 0, 0);
       }
-      if (cell) {
-        if (live && sub == 0) ++cnt;
+      // pooled cells (dead ones add zeros); token rows 0, 1 feed the value
+      // head, rows 4, 5 the moves-left head
+      const bool pooled = rv && cell;
+      if (pooled && live && sub == 0) ++cnt;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pool[e] += y[e];
-      } else {
-        // token rows 0, 1 feed the value head, rows 4, 5 the moves-left head
-        const int slot = row == 0 ? 0 : row == 1 ? 1 : row == 4 ? 3 : row == 5 ? 4 : -1;
-        if (slot >= 0) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) vin[slot * C + c0 + e] = y[e];
-        }
-      }
+      for (int e = 0; e < 8; ++e) pool[e] += pooled ? y[e] : 0.f;
+      const int slot = row == 0 ? 0 : row == 1 ? 1 : row == 4 ? 3 : row == 5 ? 4 : -1;
+      const uint32_t voff = rv && slot >= 0 ? vin_off + (uint32_t)((slot * C + c0) * 4) : SHRIMP_OOB_OFFSET;
+      __builtin_amdgcn_raw_buffer_store_b128(
+          u32x4{__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]), __float_as_uint(y[3])},
+          wr, voff, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(
+          u32x4{__float_as_uint(y[4]), __float_as_uint(y[5]), __float_as_uint(y[6]), __float_as_uint(y[7])},
+          wr, voff + 16, 0, 0);
     }
   }
+  float* vin = a.workspace + (int64_t)b * 6 * C;
   float* red = fl;                 // [RPP][C]
   float* cred = fl + RPP * C;      // [RPP]
   if (cv) {
@@ -634,13 +656,22 @@ static int launch_trunk_tail(const shrimp_tail_args* a, float* ws, hipStream_t s
   SHRIMP_REQUIRE(a->bins > 0 && a->bins <= 256, "trunk_tail: bins %d", a->bins);
   shrimp_tail_args k = *a;
   k.workspace = ws;
+  const int64_t seq_bytes = ((int64_t)(k.B - 1) * k.s_sb + (int64_t)k.S * k.C) * (f32 ? 4 : 2);
+  const int64_t mask_bytes = (int64_t)k.B * (k.S - k.n_tokens);
+  const int64_t ws_bytes = (int64_t)k.B * 6 * k.C * 4;
+  SHRIMP_REQUIRE(seq_bytes < (int64_t)0x7FFF0000 && ws_bytes < (int64_t)0x7FFF0000,
+                 "trunk_tail: buffers too large for 32-bit offsets");
   const int tpr = k.C / 8;
   const size_t lsm = (size_t)(256 / ((tpr <= 4) ? 4 : (tpr <= 8) ? 8 : (tpr <= 16) ? 16 : 32)) *
                      (k.C + 1) * sizeof(float);
 #define SHRIMP_FLN(T)                                                                      \
   do {                                                                                       \
-    if (f32) hipLaunchKernelGGL((final_ln_kernel<T, true>), dim3(k.B), dim3(256), lsm, st, k); \
-    else hipLaunchKernelGGL((final_ln_kernel<T, false>), dim3(k.B), dim3(256), lsm, st, k);    \
+    if (f32)                                                                                 \
+      hipLaunchKernelGGL((final_ln_kernel<T, true>), dim3(k.B), dim3(256), lsm, st, k,         \
+                         (uint32_t)seq_bytes, (uint32_t)mask_bytes, (uint32_t)ws_bytes);       \
+    else                                                                                     \
+      hipLaunchKernelGGL((final_ln_kernel<T, false>), dim3(k.B), dim3(256), lsm, st, k,        \
+                         (uint32_t)seq_bytes, (uint32_t)mask_bytes, (uint32_t)ws_bytes);       \
   } while (0)
   if (tpr <= 4) SHRIMP_FLN(4);
   else if (tpr <= 8) SHRIMP_FLN(8);
