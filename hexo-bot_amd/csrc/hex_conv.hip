@@ -413,6 +413,34 @@ __global__ __launch_bounds__(256, 2) void hex_conv_kernel(const shrimp_conv_args
   conv_epilogue<COUT, MB, EPI, PS_GLOBAL>(a, acc, rb, rn, rv, lg);
 }
 
+// Per-channel parameters of an LDS-parameter epilogue (PS_LDS): [bias | ln_w |
+// ln_b | gamma or head_w | zeros], COUT floats each, absent ones zero.
+template <int COUT>
+SHRIMP_DEV void stage_params(float* lp, const shrimp_conv_args& a, bool head) {
+  const float* extra = head ? a.head_w : a.gamma;
+  for (int i = threadIdx.x; i < 5 * COUT; i += blockDim.x) {
+    const int slot = i / COUT, c = i - slot * COUT;
+    const float* sp = slot == 0 ? a.bias : slot == 1 ? a.ln_w : slot == 2 ? a.ln_b : slot == 3 ? extra : nullptr;
+    lp[i] = sp ? sp[c] : 0.f;
+  }
+}
+
+// Epilogue of the LDS-staged conv: parameters from LDS; B16: 16-byte stores
+// (and residual reads) through buffer resources over o_bytes / r_bytes.
+template <int COUT, int MB, int EPI, bool B16>
+SHRIMP_DEV void lds_conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16][MB],
+                                  const int (&rb)[MB], const int (&rn)[MB], const bool (&rv)[MB],
+                                  int lg, const float* lp, uint32_t o_bytes, uint32_t r_bytes) {
+  if constexpr ((EPI & EPI_HEAD) != 0) {
+    conv_epilogue<COUT, MB, EPI, PS_LDS>(a, acc, rb, rn, rv, lg, lp, [](int, int, u32x2) {});
+  } else if constexpr (B16) {
+    conv_epilogue<COUT, MB, EPI, PS_LDS>(a, acc, rb, rn, rv, lg, lp,
+                                         BufRowStore16<MB>(a, rb, rn, rv, lg, o_bytes, r_bytes));
+  } else {
+    conv_epilogue<COUT, MB, EPI, PS_LDS>(a, acc, rb, rn, rv, lg, lp, GlobalRowStore<MB>(a, rb, rn, lg));
+  }
+}
+
 // LDS-staged variant: workgroups (position, row split); split y of Y takes the
 // row tiles y, y + Y, ... (Y = 1 for batches that fill the GPU; small batches
 // spread a position's tiles over several workgroups, each staging all rows). The position's N rows
@@ -427,9 +455,12 @@ __global__ __launch_bounds__(256, 2) void hex_conv_kernel(const shrimp_conv_args
 // over workgroups gives the same bits as the large batch: accumulators start
 // from the bias (except for the residual epilogue) and the K loop runs channel
 // chunk outer, tap inner.
-template <int COUT, int MB, int EPI, int CIN, bool BIGORDER = false>
+// The per-channel parameters follow the rows in LDS (stage_params); B16: see
+// lds_conv_epilogue.
+template <int COUT, int MB, int EPI, int CIN, bool BIGORDER = false, bool B16 = false>
 __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_args a,
-                                                              uint32_t w_bytes) {
+                                                              uint32_t w_bytes, uint32_t o_bytes,
+                                                              uint32_t r_bytes) {
   constexpr int NB = COUT / 16;
   constexpr int ROWB = CIN * 2;
   constexpr int CPR = CIN / 8;
@@ -470,6 +501,8 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
       }
     }
   }
+  float* lp = reinterpret_cast<float*>(xs + (((N + 1) * ROWB + 15) & ~15));
+  stage_params<COUT>(lp, a, (EPI & EPI_HEAD) != 0);
   __syncthreads();
 
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, w_bytes);
@@ -550,7 +583,8 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
             acc[nb][mb] = mfma16x16x32(wq[s % 3][nb], xq[s % 2][mb], acc[nb][mb]);
         __builtin_amdgcn_sched_barrier(0);
       }
-      conv_epilogue<COUT, MB, BA ? (EPI | EPI_BACC) : EPI, PS_GLOBAL>(a, acc, rb, rn, rv, lg);
+      lds_conv_epilogue<COUT, MB, BA ? (EPI | EPI_BACC) : EPI, B16>(a, acc, rb, rn, rv, lg, lp,
+                                                                   o_bytes, r_bytes);
       continue;
     }
 #pragma unroll
@@ -600,7 +634,7 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = mfma16x16x32(wc[nb], xc[mb], acc[nb][mb]);
     }
-    conv_epilogue<COUT, MB, EPI, PS_GLOBAL>(a, acc, rb, rn, rv, lg);
+    lds_conv_epilogue<COUT, MB, EPI, B16>(a, acc, rb, rn, rv, lg, lp, o_bytes, r_bytes);
   }
 }
 
@@ -912,20 +946,39 @@ static int launch_conv(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, size
   const bool big = COUT == 128 && lds && a->cin_pad == 128 && a->taps == 7 && a->N <= BIG_MAX_N &&
                    out16 && (g_conv_variant == 0 || g_conv_variant == 3) &&
                    big_lds <= (size_t)max_lds_per_block();
+  // The LDS kernels keep the rows plus the per-channel parameters in LDS;
+  // their 16-byte buffered stores (COUT = 128) need 16-byte aligned rows and
+  // extents within the 32-bit buffer offsets.
+  const size_t lds_p = lds ? ((lds + 15) & ~(size_t)15) + (size_t)5 * COUT * sizeof(float) : 0;
+  const bool lds_ok = lds && lds_p <= (size_t)max_lds_per_block();
+  const bool head = (EPI & EPI_HEAD) != 0;
+  const int64_t o_ext = head ? 0 : ((int64_t)(a->B - 1) * a->o_sb + (int64_t)(a->N - 1) * a->o_sn + COUT) * 2;
+  const int64_t r_ext =
+      (EPI & EPI_RESID) ? ((int64_t)(a->B - 1) * a->r_sb + (int64_t)(a->N - 1) * a->r_sn + COUT) * 2 : 0;
+  const bool b16 = COUT == 128 && !head && out16 && o_ext < (int64_t)0x7FFF0000 &&
+                   r_ext < (int64_t)0x7FFF0000 &&
+                   (!(EPI & EPI_RESID) || (a->r_sn % 4 == 0 && a->r_sb % 4 == 0));
+  const uint32_t ob = (uint32_t)o_ext, rbb = (uint32_t)r_ext;
+#define SHRIMP_LDS_LAUNCH(GRID, MBV, CINV, BIGO)                                                     \
+  do {                                                                                             \
+    if (b16)                                                                                       \
+      hipLaunchKernelGGL((hex_conv_lds_kernel<COUT, MBV, EPI, CINV, BIGO, COUT == 128>), GRID,     \
+                         dim3(256), lds_p, st, *a, wb, ob, rbb);                                   \
+    else                                                                                           \
+      hipLaunchKernelGGL((hex_conv_lds_kernel<COUT, MBV, EPI, CINV, BIGO, false>), GRID, dim3(256), \
+                         lds_p, st, *a, wb, ob, rbb);                                              \
+    return check_launch("hex_conv");                                                               \
+  } while (0)
   // Small batches (at most half as many positions as compute units): one row
   // tile of 64 rows per workgroup, (B, N / 64) workgroups, instead of one
   // workgroup per position; where the big-tile kernel would run, with its
   // arithmetic (same bits).
-  if (COUT == 128 && lds && (a->cin_pad == 32 || a->cin_pad == 128) &&
+  if (COUT == 128 && lds_ok && (a->cin_pad == 32 || a->cin_pad == 128) &&
       (int64_t)a->B * 2 <= cu_count() && g_conv_variant == 0) {
     const dim3 grid((unsigned)a->B, (unsigned)((a->N + 63) / 64));
-    if (big)
-      hipLaunchKernelGGL((hex_conv_lds_kernel<128, 1, EPI, 128, true>), grid, dim3(256), lds, st, *a, wb);
-    else if (a->cin_pad == 32)
-      hipLaunchKernelGGL((hex_conv_lds_kernel<128, 1, EPI, 32>), grid, dim3(256), lds, st, *a, wb);
-    else
-      hipLaunchKernelGGL((hex_conv_lds_kernel<128, 1, EPI, 128>), grid, dim3(256), lds, st, *a, wb);
-    return check_launch("hex_conv");
+    if (big) SHRIMP_LDS_LAUNCH(grid, 1, 128, true);
+    else if (a->cin_pad == 32) SHRIMP_LDS_LAUNCH(grid, 1, 32, false);
+    else SHRIMP_LDS_LAUNCH(grid, 1, 128, false);
   }
   if (big) {
     const int waves = (a->N + 127) / 128;
@@ -935,21 +988,16 @@ static int launch_conv(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, size
       return check_launch("hex_conv");
     }
   }
-  if (lds) {
+  if (lds_ok) {
     switch (a->cin_pad) {
-#define SHRIMP_CONV_LDS(CINV)                                                               \
-  case CINV:                                                                                \
-    hipLaunchKernelGGL((hex_conv_lds_kernel<COUT, MB, EPI, CINV>), dim3(a->B), dim3(256), lds, \
-                       st, *a, wb);                                                         \
-    return check_launch("hex_conv");
-      SHRIMP_CONV_LDS(32)
-      SHRIMP_CONV_LDS(64)
-      SHRIMP_CONV_LDS(128)
-#undef SHRIMP_CONV_LDS
+      case 32: SHRIMP_LDS_LAUNCH(dim3(a->B), MB, 32, false);
+      case 64: SHRIMP_LDS_LAUNCH(dim3(a->B), MB, 64, false);
+      case 128: SHRIMP_LDS_LAUNCH(dim3(a->B), MB, 128, false);
       default:
         break;
     }
   }
+#undef SHRIMP_LDS_LAUNCH
   const int rows = a->B * a->N;
   const int per_block = 4 * MB * 16;
   const int grid = (rows + per_block - 1) / per_block;
