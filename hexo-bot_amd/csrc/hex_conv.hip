@@ -835,6 +835,122 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
   }
 }
 
+// Epilogue store of a ConvBlock that another ConvBlock follows in the same
+// launch: every row goes to HBM (BufRowStore16: the next block's residual and
+// the trunk state), and the rows that exist also into the LDS row layout as
+// the next block's input (rows >= N are never written there: row N is the zero
+// row).
+struct BlockOutStore : BufRowStore16<8> {
+  unsigned char* xs;
+  uint32_t nr64;
+  const BigTile& t;
+  SHRIMP_DEV BlockOutStore(const shrimp_conv_args& a, const BigTile& tt, unsigned char* x, uint32_t o_bytes,
+                           uint32_t r_bytes)
+      : BufRowStore16<8>(a, tt.rb, tt.rn, tt.rv, tt.lg, o_bytes, r_bytes), xs(x),
+        nr64((uint32_t)tt.NR * 64), t(tt) {}
+  SHRIMP_DEV void operator()(int mb, int nb, u32x2 pk) {
+    if (t.rv[mb]) {
+      const uint32_t row = (uint32_t)t.rn[mb] * 64, swz = (uint32_t)((t.rn[mb] >> 2) & 3);
+      const uint32_t piece = (uint32_t)((nb & 1) * 2 + (t.lg >> 1));
+      *reinterpret_cast<u32x2*>(xs + (uint32_t)(nb >> 1) * nr64 + row + ((piece ^ swz) << 4) +
+                                (uint32_t)(t.lg & 1) * 8) = pk;
+    }
+    BufRowStore16<8>::operator()(mb, nb, pk);
+  }
+};
+
+// The two convs of one ConvBlock over the rows in LDS (ConvBlock.forward,
+// model.py:395-422):
+//   y1  = relu(LN1(conv1(x))) * m          -> written into LDS over x's rows
+//   out = relu(x + gamma * LN2(conv2(y1)) * m)
+// After a barrier conv1's epilogue writes y1 (bf16, masked rows zero) into the
+// x layout and conv2 gathers from there, so y1 never reaches HBM; the zero row
+// N stays zero. `c2.resid` is x and `c2.out` may alias it: a wave's residual
+// reads of a row block complete before that block's stores (the stored values
+// depend on them), and a wave only touches its own rows. NEXT: another block
+// follows, and the output rows also become its input rows in LDS.
+// first: x arrives by the DMA that big_setup issued (waited for here);
+// otherwise the previous block wrote it into LDS.
+template <bool NEXT>
+SHRIMP_DEV void block_convs(BigTile& t, unsigned char* xs, const shrimp_conv_args& c1,
+                            const shrimp_conv_args& a2, const float* lp1, const float* lp2,
+                            uint32_t w_bytes, uint32_t o_bytes, uint32_t r_bytes, bool first) {
+  if (!first) {
+    // as before conv2: the previous block's LDS row and weight offsets are
+    // recomputed, not kept alive (spilled) for reuse
+#pragma unroll
+    for (int tp = 0; tp < 7; ++tp)
+#pragma unroll
+      for (int m2 = 0; m2 < 4; ++m2) asm volatile("" : "+v"(t.sw2[tp][m2]));
+    asm volatile("" : "+v"(t.lane));
+    t.lg = t.lane >> 4;
+  }
+  const __amdgpu_buffer_rsrc_t wr1 = make_rsrc(c1.w, w_bytes);
+  const __amdgpu_buffer_rsrc_t wr2 = make_rsrc(a2.w, w_bytes);
+  u32x4 wf[8];
+  big_wload(wr1, 0, t.lane, wf);
+  f32x4 acc[8][8];
+  big_acc_init(acc, c1.bias, t.lg);
+  if (first) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  } else {
+    // the previous block's LDS writes are complete (its HBM stores need not be)
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+  }
+  // conv2's first weights are loaded after conv1's epilogue, whose bias and
+  // ln_w then fit in registers
+  big_pass(acc, wf, t, xs, wr1);
+  __syncthreads();  // every wave is done reading x from LDS
+  {
+    const uint32_t nr64 = (uint32_t)t.NR * 64;
+    const uint32_t lo = (uint32_t)(t.lg & 1) * 8;
+    uint32_t row[8], swz[8];
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      row[mb] = (uint32_t)t.rn[mb] * 64;
+      swz[mb] = (uint32_t)((t.rn[mb] >> 2) & 3);
+    }
+    const int lg = t.lg;
+    conv_epilogue<128, 8, EPI_LN | EPI_RELU | EPI_BACC, PS_LDSREG>(
+        c1, acc, t.rb, t.rn, t.rv, t.lg, lp1, [&](int mb, int nb, u32x2 pk) {
+          const uint32_t piece = (uint32_t)((nb & 1) * 2 + (lg >> 1));
+          const uint32_t addr = (uint32_t)(nb >> 1) * nr64 + row[mb] + ((piece ^ swz[mb]) << 4) + lo;
+          *reinterpret_cast<u32x2*>(xs + addr) = pk;
+        });
+  }
+  // conv2 starts from zeros and adds its bias in the epilogue: starting from
+  // the bias here makes the register allocator spill
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  __syncthreads();  // y1 is complete
+  big_wload(wr2, 0, t.lane, wf);
+  // Hide the per-lane addresses from the optimizer: otherwise it keeps conv1's
+  // LDS row and weight offsets alive (spilled) for reuse by conv2 instead of
+  // recomputing them.
+#pragma unroll
+  for (int tp = 0; tp < 7; ++tp)
+#pragma unroll
+    for (int m2 = 0; m2 < 4; ++m2) asm volatile("" : "+v"(t.sw2[tp][m2]));
+  asm volatile("" : "+v"(t.lane));
+  t.lg = t.lane >> 4;
+  big_pass(acc, wf, t, xs, wr2);
+  if constexpr (NEXT) {
+    // every wave is done reading y1 before the output rows replace it
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(a2, acc, t.rb, t.rn, t.rv, t.lg, lp2,
+                                                      BlockOutStore(a2, t, xs, o_bytes, r_bytes));
+  } else {
+    conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(
+        a2, acc, t.rb, t.rn, t.rv, t.lg, lp2,
+        BufRowStore16<8>(a2, t.rb, t.rn, t.rv, t.lg, o_bytes, r_bytes));
+  }
+}
+
 // ConvBlock in one launch (ConvBlock.forward, model.py:395-422):
 //   y1  = relu(LN1(conv1(x))) * m          -> written into LDS over x's rows
 //   out = relu(x + gamma * LN2(conv2(y1)) * m)
@@ -905,6 +1021,31 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
   conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(
       c2, acc, t.rb, t.rn, t.rv, t.lg, lp2,
       BufRowStore16<8>(c2, t.rb, t.rn, t.rv, t.lg, o_bytes, x_bytes));
+}
+
+// Two consecutive ConvBlocks (c1, c2 then c3, c4) in one launch: x staged
+// once by DMA (big_setup), the first block's output rows handed to the second
+// in LDS, so the second does not read them back from HBM for its convs (its
+// residual reads them: a wave reads rows it wrote itself). x_bytes spans c1.x
+// (the first residual), o_bytes c2.out (= c3.x, the second residual),
+// o2_bytes c4.out.
+__global__ __launch_bounds__(256, 1) void hex_block_pair_kernel(
+    const shrimp_conv_args c1, const shrimp_conv_args c2, const shrimp_conv_args c3,
+    const shrimp_conv_args c4, uint32_t x_bytes, uint32_t w_bytes, uint32_t o_bytes,
+    uint32_t o2_bytes) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
+  BigTile t;
+  big_setup(t, c1, xs, x_bytes);
+  float* lp1 = reinterpret_cast<float*>(xs + 4 * t.NR * 64);
+  float* lp2 = lp1 + BIG_PARAMS;
+  float* lp3 = lp2 + BIG_PARAMS;
+  float* lp4 = lp3 + BIG_PARAMS;
+  big_params(lp1, c1.bias, c1.ln_w, c1.ln_b, nullptr);
+  big_params(lp2, c2.bias, c2.ln_w, c2.ln_b, c2.gamma);
+  big_params(lp3, c3.bias, c3.ln_w, c3.ln_b, nullptr);
+  big_params(lp4, c4.bias, c4.ln_w, c4.ln_b, c4.gamma);
+  block_convs<true>(t, xs, c1, c2, lp1, lp2, w_bytes, o_bytes, x_bytes, true);
+  block_convs<false>(t, xs, c3, c4, lp3, lp4, w_bytes, o2_bytes, o_bytes, false);
 }
 
 // ---- weight packing ------------------------------------------------------------
@@ -1131,15 +1272,17 @@ extern "C" int shrimp_conv_block_supported(int taps, int N, int cin_pad, int cou
   return lds <= (size_t)max_lds_per_block() ? 1 : 0;
 }
 
-extern "C" int shrimp_conv_block(const shrimp_conv_args* c1, const shrimp_conv_args* c2,
-                                 void* stream) {
+// Checks of one ConvBlock's two conv argument sets (the contract of
+// shrimp_conv_block); fills conv2's launch arguments (x, index, mask and shape
+// of conv1) and the byte extents of x and of the output.
+static int check_block(const shrimp_conv_args* c1, const shrimp_conv_args* c2, shrimp_conv_args* a2_out,
+                       int64_t* x_bytes, int64_t* o_bytes) {
   SHRIMP_REQUIRE(c1 != nullptr && c2 != nullptr, "conv_block: null args");
   SHRIMP_REQUIRE(c1->B >= 0 && c1->N > 0, "conv_block: bad B/N (%d, %d)", c1->B, c1->N);
   SHRIMP_REQUIRE(shrimp_conv_block_supported(c1->taps, c1->N, c1->cin_pad, c1->cout) &&
                      c2->cin_pad == 128 && c2->cout == 128,
                  "conv_block: no fused kernel for taps %d, N %d, %d -> %d channels", c1->taps,
                  c1->N, c1->cin_pad, c1->cout);
-  if (c1->B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(c1->x && c1->idx && c1->mask && c1->w && c1->bias && c2->w && c2->bias,
                  "conv_block: null input pointer");
   SHRIMP_REQUIRE(c1->idx_stride >= 7, "conv_block: idx_stride %d < 7", c1->idx_stride);
@@ -1171,11 +1314,56 @@ extern "C" int shrimp_conv_block(const shrimp_conv_args* c1, const shrimp_conv_a
   const int64_t o_extent =
       (int64_t)(c1->B - 1) * c2->o_sb + (int64_t)(c1->N - 1) * c2->o_sn + 128;
   SHRIMP_REQUIRE(o_extent * 2 < (int64_t)0x7FFF0000, "conv_block: output buffer too large");
+  *a2_out = a2;
+  *x_bytes = x_extent * 2;
+  *o_bytes = o_extent * 2;
+  return SHRIMP_OK;
+}
+
+extern "C" int shrimp_conv_block(const shrimp_conv_args* c1, const shrimp_conv_args* c2,
+                                 void* stream) {
+  SHRIMP_REQUIRE(c1 != nullptr && c2 != nullptr, "conv_block: null args");
+  if (c1->B == 0) return SHRIMP_OK;
+  shrimp_conv_args a2;
+  int64_t xb = 0, ob = 0;
+  if (int rc = check_block(c1, c2, &a2, &xb, &ob)) return rc;
   const int waves = (c1->N + 127) / 128;
   const size_t lds = (size_t)big_rows_padded(c1->N) * 256 + 2 * BIG_PARAMS * sizeof(float);
-  const uint32_t xb = (uint32_t)(x_extent * 2);
   const uint32_t wb = (uint32_t)shrimp_conv_wpack_bytes(7, 128, 128);
   hipLaunchKernelGGL(hex_block_kernel, dim3(c1->B), dim3(64 * waves), lds, as_stream(stream), *c1,
-                     a2, xb, wb, (uint32_t)(o_extent * 2));
+                     a2, (uint32_t)xb, wb, (uint32_t)ob);
   return check_launch("conv_block");
+}
+
+static size_t block_pair_lds(int N) {
+  return (size_t)big_rows_padded(N) * 256 + 4 * BIG_PARAMS * sizeof(float);
+}
+
+extern "C" int shrimp_conv_block_pair_supported(int taps, int N, int cin_pad, int cout) {
+  return shrimp_conv_block_supported(taps, N, cin_pad, cout) &&
+         block_pair_lds(N) <= (size_t)max_lds_per_block();
+}
+
+extern "C" int shrimp_conv_block_pair(const shrimp_conv_args* c1, const shrimp_conv_args* c2,
+                                      const shrimp_conv_args* c3, const shrimp_conv_args* c4,
+                                      void* stream) {
+  SHRIMP_REQUIRE(c1 && c2 && c3 && c4, "conv_block_pair: null args");
+  if (c1->B == 0) return SHRIMP_OK;
+  shrimp_conv_args a2, a4;
+  int64_t xb = 0, ob = 0, xb3 = 0, ob4 = 0;
+  if (int rc = check_block(c1, c2, &a2, &xb, &ob)) return rc;
+  if (int rc = check_block(c3, c4, &a4, &xb3, &ob4)) return rc;
+  SHRIMP_REQUIRE(c3->x == c2->out && c3->x_sb == c2->o_sb && c3->x_sn == c2->o_sn,
+                 "conv_block_pair: the second block's input must be the first block's output");
+  SHRIMP_REQUIRE(c3->idx == c1->idx && c3->idx_stride == c1->idx_stride && c3->mask == c1->mask &&
+                     c3->B == c1->B && c3->N == c1->N,
+                 "conv_block_pair: both blocks must share the index, mask and shape");
+  SHRIMP_REQUIRE(shrimp_conv_block_pair_supported(7, c1->N, 128, 128),
+                 "conv_block_pair: %d rows do not fit the LDS of one workgroup", c1->N);
+  const int waves = (c1->N + 127) / 128;
+  const uint32_t wb = (uint32_t)shrimp_conv_wpack_bytes(7, 128, 128);
+  hipLaunchKernelGGL(hex_block_pair_kernel, dim3(c1->B), dim3(64 * waves), block_pair_lds(c1->N),
+                     as_stream(stream), *c1, a2, *c3, a4, (uint32_t)xb, wb, (uint32_t)ob,
+                     (uint32_t)ob4);
+  return check_launch("conv_block_pair");
 }

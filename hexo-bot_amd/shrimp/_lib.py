@@ -140,6 +140,8 @@ SIGNATURES: dict = {
     "shrimp_hex_conv": (ctypes.c_int, [ctypes.POINTER(ConvArgs), _vp]),
     "shrimp_conv_block_supported": (ctypes.c_int, [ctypes.c_int] * 4),
     "shrimp_conv_block": (ctypes.c_int, [ctypes.POINTER(ConvArgs), ctypes.POINTER(ConvArgs), _vp]),
+    "shrimp_conv_block_pair_supported": (ctypes.c_int, [ctypes.c_int] * 4),
+    "shrimp_conv_block_pair": (ctypes.c_int, [ctypes.POINTER(ConvArgs)] * 4 + [_vp]),
     "shrimp_linear": (ctypes.c_int, [ctypes.POINTER(LinearArgs), _vp]),
     "shrimp_attn_qkv": (ctypes.c_int, [ctypes.POINTER(QkvArgs), _vp]),
     "shrimp_attn_qkv_kvf": (ctypes.c_int, [ctypes.POINTER(QkvArgs), _vp, _vp]),

@@ -187,14 +187,9 @@ def conv_block_supported(taps, N, cin_pad, cout):
     return bool(_lib.load().shrimp_conv_block_supported(taps, N, cin_pad, cout))
 
 
-def launch_conv_block(
-    *, x, x_sb, x_sn, idx, idx_stride, mask8, B, N, C, w1, b1, ln1_w, ln1_b, eps1,
-    w2, b2, ln2_w, ln2_b, eps2, gamma, out, o_sb, o_sn, stream=None,
-):
-    """ConvBlock.forward (reference model.py:395-422) as one launch; y1 stays on chip.
-
-    `out` may alias `x`. Raises when conv_block_supported() is false for the shape.
-    """
+def _block_args(x, x_sb, x_sn, idx, idx_stride, mask8, B, N, C, w1, b1, ln1_w, ln1_b, eps1,
+                w2, b2, ln2_w, ln2_b, eps2, gamma, out, o_sb, o_sn):
+    """shrimp_conv_args of one ConvBlock's two convs (shrimp_conv_block's contract)."""
     _check_rows("conv_block x", x, x_sb, x_sn, B, N, C)
     _check_rows("conv_block out", out, o_sb, o_sn, B, N, C)
     c1 = _lib.ConvArgs(
@@ -208,8 +203,43 @@ def launch_conv_block(
         gamma=gamma.data_ptr(), out=out.data_ptr(), o_sb=o_sb, o_sn=o_sn, B=B, N=N,
         cin_pad=C, cout=C,
     )
+    return c1, c2
+
+
+def launch_conv_block(
+    *, x, x_sb, x_sn, idx, idx_stride, mask8, B, N, C, w1, b1, ln1_w, ln1_b, eps1,
+    w2, b2, ln2_w, ln2_b, eps2, gamma, out, o_sb, o_sn, stream=None,
+):
+    """ConvBlock.forward (reference model.py:395-422) as one launch; y1 stays on chip.
+
+    `out` may alias `x`. Raises when conv_block_supported() is false for the shape.
+    """
+    c1, c2 = _block_args(x, x_sb, x_sn, idx, idx_stride, mask8, B, N, C, w1, b1, ln1_w, ln1_b,
+                         eps1, w2, b2, ln2_w, ln2_b, eps2, gamma, out, o_sb, o_sn)
     s = _lib.stream_handle() if stream is None else stream
     _lib.check(_lib.load().shrimp_conv_block(ctypes_ref(c1), ctypes_ref(c2), s), "conv_block")
+
+
+def conv_block_pair_supported(taps, N, cin_pad, cout):
+    """True when shrimp_conv_block_pair can run two ConvBlocks of this shape in one launch."""
+    return bool(_lib.load().shrimp_conv_block_pair_supported(taps, N, cin_pad, cout))
+
+
+def launch_conv_block_pair(*, x, x_sb, x_sn, idx, idx_stride, mask8, B, N, C, blocks, out, o_sb,
+                           o_sn, stream=None):
+    """Two consecutive ConvBlocks (model.py:395-422) in one launch, in place on `out`
+    after the first: `blocks` holds two dicts of w1, b1, ln1_w, ln1_b, eps1, w2, b2,
+    ln2_w, ln2_b, eps2, gamma. The first block reads `x` and writes `out`; the second
+    reads and writes `out` (its rows handed over inside the workgroup)."""
+    if len(blocks) != 2:
+        raise ValueError("launch_conv_block_pair takes two blocks")
+    c1, c2 = _block_args(x, x_sb, x_sn, idx, idx_stride, mask8, B, N, C, out=out, o_sb=o_sb,
+                         o_sn=o_sn, **blocks[0])
+    c3, c4 = _block_args(out, o_sb, o_sn, idx, idx_stride, mask8, B, N, C, out=out, o_sb=o_sb,
+                         o_sn=o_sn, **blocks[1])
+    s = _lib.stream_handle() if stream is None else stream
+    _lib.check(_lib.load().shrimp_conv_block_pair(ctypes_ref(c1), ctypes_ref(c2), ctypes_ref(c3),
+                                                  ctypes_ref(c4), s), "conv_block_pair")
 
 
 def launch_linear(

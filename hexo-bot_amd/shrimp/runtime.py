@@ -16,6 +16,7 @@ Kernel sequence (reference lines in model.py):
     prep_inputs          gather_idx / mask / coords / seq_lens / padded feats  :861-892
     hex_conv  (stem)     conv + LN + ReLU + mask                               :865
     per 'C': hex_conv x2 conv1+LN+ReLU+mask -> y1; conv2+LN+mask, ReLU(x+g*y)  :395-422
+             (one conv_block launch per 'C', one conv_block_pair per 'CC')
     per 'A': attn_qkv (LN1, q/k/v) -> attn -> attn_mlp (out_proj, residual, LN2,
              fc1, GELU, fc2, residual; three linear launches when C != 128)   :448-514
     trunk_tail           final LN, pooled mean, value / moves-left heads       :927-935, 990-1002
@@ -45,6 +46,7 @@ from .ops import (
     attn_bias_table,
     attn_keys_ints,
     attn_staged_supported,
+    conv_block_pair_supported,
     conv_block_supported,
     attn_fused_supported,
     launch_attn,
@@ -56,6 +58,7 @@ from .ops import (
     launch_attn_staged,
     launch_conv,
     launch_conv_block,
+    launch_conv_block_pair,
     launch_linear,
     pack_attn_mlp,
     pack_attn_qkv,
@@ -106,6 +109,10 @@ class HipForward:
         # Fused out_proj + MLP kernel where it applies; off runs the three
         # linear kernels (used to check one against the other).
         self.use_fused_mlp = True
+        # Two consecutive ConvBlocks in one launch (the first one's output
+        # rows handed to the second inside the workgroup) where it applies;
+        # off runs one launch per block (bit-identical).
+        self.use_block_pair = True
         # LN1 + q/k/v kernel with LN1 folded into its weights where it
         # applies; off runs the linear kernel's QKV mode.
         self.use_fused_qkv = True
@@ -612,11 +619,30 @@ class HipForward:
         self._mark("stem")
         ci = ai = 0
         rows = B * S
-        for kind in P.layout:
+        fused_block = self.use_fused_block and 2 * B > self._cus(dev) and conv_block_supported(7, N, C, C)
+        pair_ok = fused_block and self.use_block_pair and conv_block_pair_supported(7, N, C, C)
+        skip = False
+        for li, kind in enumerate(P.layout):
+            if skip:
+                skip = False
+                continue
             if kind == "C":
                 k = P.convs[ci]
                 ci += 1
-                if self.use_fused_block and 2 * B > self._cus(dev) and conv_block_supported(7, N, C, C):
+                if pair_ok and P.layout[li + 1:li + 2] == "C":
+                    k2 = P.convs[ci]
+                    ci += 1
+                    skip = True
+                    blocks = [dict(w1=q.w1, b1=q.b1, ln1_w=q.ln1w, ln1_b=q.ln1b, eps1=q.eps1, w2=q.w2,
+                                   b2=q.b2, ln2_w=q.ln2w, ln2_b=q.ln2b, eps2=q.eps2, gamma=q.gamma)
+                              for q in (k, k2)]
+                    launch_conv_block_pair(
+                        x=cells, x_sb=S * C, x_sn=C, idx=idx, idx_stride=7, mask8=mask8, B=B, N=N,
+                        C=C, blocks=blocks, out=cells, o_sb=S * C, o_sn=C, stream=st,
+                    )
+                    self._mark("conv_block_pair")
+                    continue
+                if fused_block:
                     launch_conv_block(
                         x=cells, x_sb=S * C, x_sn=C, idx=idx, idx_stride=7, mask8=mask8, B=B,
                         N=N, C=C, w1=k.w1, b1=k.b1, ln1_w=k.ln1w, ln1_b=k.ln1b, eps1=k.eps1,

@@ -145,6 +145,18 @@ int shrimp_hex_conv(const shrimp_conv_args* a, void* stream);
 int shrimp_conv_block_supported(int taps, int N, int cin_pad, int cout);
 int shrimp_conv_block(const shrimp_conv_args* c1, const shrimp_conv_args* c2, void* stream);
 
+/* Two consecutive ConvBlocks in one launch (no counterpart in the reference,
+ * which runs ConvBlock.forward per block, model.py:395-422; the trunk layouts
+ * repeat "CC"): shrimp_conv_block(c1, c2) then shrimp_conv_block(c3, c4), with
+ * the same result, the first block's output rows handed to the second inside
+ * the workgroup instead of read back from HBM. (c1, c2) and (c3, c4) each meet
+ * shrimp_conv_block's contract; c3.x must be c2.out (same strides), and c3
+ * shares c1's idx, idx_stride, mask, B and N. shrimp_conv_block_pair_supported
+ * reports whether the pair fits one workgroup's LDS (else SHRIMP_EINVAL). */
+int shrimp_conv_block_pair_supported(int taps, int N, int cin_pad, int cout);
+int shrimp_conv_block_pair(const shrimp_conv_args* c1, const shrimp_conv_args* c2,
+                           const shrimp_conv_args* c3, const shrimp_conv_args* c4, void* stream);
+
 /* ------------------------------------------------------------------------
  * Dense row GEMM with fused prologue / epilogue (the nn.Linear calls of
  * RelPosAttention / AttnBlock, model.py:448-514, and the value heads,

@@ -246,6 +246,81 @@ def test_conv_block_fused(conv_case, n):
     assert (fused.cpu()[~mask] == 0).all()
 
 
+@pytest.mark.parametrize("n", [256, 64, 200, 300])
+def test_conv_block_pair_matches_two_blocks(conv_case, n):
+    """Two ConvBlocks in one launch (the first block's output rows handed to
+    the second in LDS) against two shrimp_conv_block launches: bit-identical,
+    including the masked rows and the rows past N (the zero row)."""
+
+    from shrimp import ops
+
+    torch.manual_seed(100 + n)
+    x, gidx, mask = _block_case(conv_case, n)
+    B, N = mask.shape
+    assert ops.conv_block_pair_supported(7, N, 128, 128)
+    blocks = []
+    for _ in range(2):
+        blocks.append(dict(
+            w1=ops.pack_conv_weight((torch.randn(7, 128, 128) / math.sqrt(7 * 128)).to(DEV)),
+            b1=(torch.randn(128) * 0.02).to(DEV), ln1_w=(torch.rand(128) + 0.5).to(DEV),
+            ln1_b=(torch.randn(128) * 0.1).to(DEV), eps1=1e-5,
+            w2=ops.pack_conv_weight((torch.randn(7, 128, 128) / math.sqrt(7 * 128)).to(DEV)),
+            b2=(torch.randn(128) * 0.02).to(DEV), ln2_w=(torch.rand(128) + 0.5).to(DEV),
+            ln2_b=(torch.randn(128) * 0.1).to(DEV), eps2=1e-5,
+            gamma=(torch.rand(128) * 0.5 + 0.5).to(DEV)))
+    idx = gidx.to(DEV, torch.int32).contiguous()
+    m8 = mask.to(DEV, torch.uint8)
+    xd = x.to(DEV, torch.bfloat16).contiguous()
+    print(f"conv_block_pair n={N} B={B}", flush=True)
+    common = dict(idx=idx, idx_stride=7, mask8=m8, B=B, N=N, C=128)
+    two = xd.clone()
+    for blk in blocks:
+        ops.launch_conv_block(x=two, x_sb=N * 128, x_sn=128, out=two, o_sb=N * 128, o_sn=128,
+                              **common, **blk)
+    pair = xd.clone()
+    ops.launch_conv_block_pair(x=pair, x_sb=N * 128, x_sn=128, blocks=blocks, out=pair,
+                               o_sb=N * 128, o_sn=128, **common)
+    # out of place: the first block reads x and writes out
+    oop = torch.zeros_like(xd)
+    ops.launch_conv_block_pair(x=xd, x_sb=N * 128, x_sn=128, blocks=blocks, out=oop,
+                               o_sb=N * 128, o_sn=128, **common)
+    torch.cuda.synchronize()
+    diff = (pair.float() - two.float()).abs().max().item()
+    print(f"pair vs two launches: max diff {diff:.3e}", flush=True)
+    assert torch.equal(pair, two)
+    assert torch.equal(oop, two)
+    assert (pair.cpu()[~mask] == 0).all()
+
+
+def test_conv_block_pair_rejects_mismatched_blocks(conv_case):
+    """The second block must read the first block's output with the same index,
+    mask and shape."""
+
+    from shrimp import _lib, ops
+
+    x, gidx, mask = _block_case(conv_case, 64)
+    B, N = mask.shape
+    idx = gidx.to(DEV, torch.int32).contiguous()
+    m8 = mask.to(DEV, torch.uint8)
+    xd = x.to(DEV, torch.bfloat16).contiguous()
+    other = torch.zeros_like(xd)
+    blk = dict(w1=ops.pack_conv_weight(torch.zeros(7, 128, 128, device=DEV)),
+               b1=torch.zeros(128, device=DEV), ln1_w=torch.ones(128, device=DEV),
+               ln1_b=torch.zeros(128, device=DEV), eps1=1e-5,
+               w2=ops.pack_conv_weight(torch.zeros(7, 128, 128, device=DEV)),
+               b2=torch.zeros(128, device=DEV), ln2_w=torch.ones(128, device=DEV),
+               ln2_b=torch.zeros(128, device=DEV), eps2=1e-5, gamma=torch.ones(128, device=DEV))
+    c1, c2 = ops._block_args(xd, N * 128, 128, idx, 7, m8, B, N, 128, out=xd, o_sb=N * 128,
+                             o_sn=128, **blk)
+    c3, c4 = ops._block_args(other, N * 128, 128, idx, 7, m8, B, N, 128, out=other,
+                             o_sb=N * 128, o_sn=128, **blk)
+    lib = _lib.load()
+    rc = lib.shrimp_conv_block_pair(ops.ctypes_ref(c1), ops.ctypes_ref(c2), ops.ctypes_ref(c3),
+                                    ops.ctypes_ref(c4), None)
+    assert rc != 0
+    assert b"first block's output" in lib.shrimp_last_error()
+
+
 def test_conv_block_rejects_other_shapes(conv_case):
     from shrimp import _lib, ops
 
