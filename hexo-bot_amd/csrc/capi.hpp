@@ -25,6 +25,10 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // Largest dynamic LDS allocation one workgroup may request on the current
 // device (queried once per device).
 int max_lds_per_block();
+
+// The value / moves-left heads of the trunk tail from the head inputs in
+// a->workspace ((B, 6C) fp32: [T0 | T1 | pooled | T4 | T5 | pooled]).
+int launch_value_heads(const shrimp_tail_args* a, hipStream_t st);
 // Compute units of the current device (queried once per device).
 int cu_count();
 

@@ -126,6 +126,25 @@ SHRIMP_DEV float max_groups_swap(float x) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// Sum over aligned groups of G lanes (G = 2, 4, 8, 16) with DPP lane moves on
+// the VALU instead of LDS-routed shuffles, the same bits as the butterfly
+// v += shfl_xor(v, m) for m = 1, 2, 4, 8: after the steps within a quad every
+// lane of the quad holds the same value, so the mirror moves (lane i <- 7 - i
+// in each half row, then i <- 15 - i in the row) bring the partner quad's or
+// half's value as the xor 4 and xor 8 partners would (addition commutes).
+template <int G>
+SHRIMP_DEV float group_sum_dpp(float v) {
+  static_assert(G == 2 || G == 4 || G == 8 || G == 16, "group of 2 to 16 lanes");
+#define SHRIMP_DPP_MOV(x, ctrl) \
+  __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), ctrl, 0xF, 0xF, false))
+  v += SHRIMP_DPP_MOV(v, 0xB1);                        // quad_perm [1, 0, 3, 2]: xor 1
+  if constexpr (G >= 4) v += SHRIMP_DPP_MOV(v, 0x4E);   // quad_perm [2, 3, 0, 1]: xor 2
+  if constexpr (G >= 8) v += SHRIMP_DPP_MOV(v, 0x141);  // row_half_mirror
+  if constexpr (G >= 16) v += SHRIMP_DPP_MOV(v, 0x140); // row_mirror
+#undef SHRIMP_DPP_MOV
+  return v;
+}
+
 // ---- LayerNorm of 16 rows of 128 channels, MFMA operand layout ------------------
 //
 // Lane (lr, lg) holds channels 32 ks + 8 lg + e (ks < 4, e < 8) of row lr in

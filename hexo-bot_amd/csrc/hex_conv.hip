@@ -1048,6 +1048,123 @@ __global__ __launch_bounds__(256, 1) void hex_block_pair_kernel(
   block_convs<false>(t, xs, c3, c4, lp3, lp4, w_bytes, o2_bytes, o_bytes, false);
 }
 
+// ---- trunk tail + policy head (model.py:927-935, 990-1020) ---------------------
+// The final LayerNorm of shrimp_trunk_tail's first pass (final_ln_kernel) with
+// the same arithmetic and summation order, over one position: its cell rows
+// in place in LDS (the big-tile conv's row layout, staged by big_setup), token
+// rows 0, 1, 4 and 5 from seq; the head inputs [T0 | T1 | pooled | T4 | T5 |
+// pooled] to the workspace. As in final_ln_kernel a row is 16 lanes of 8
+// channels, and row slot rs (= row % 16) pools its cells in row order; the 16
+// slot sums then add in slot order (red: [16][128] floats, cred: [16]).
+SHRIMP_DEV void tail_ln_lds(const BigTile& t, unsigned char* xs, const shrimp_tail_args& ta,
+                            float* red, float* cred) {
+  constexpr int C = 128;
+  const int S = ta.S, nt = ta.n_tokens, N = S - nt;
+  const int tid = threadIdx.x, ngrp = (int)(blockDim.x >> 4);
+  const int sub = tid & 15, c0 = sub * 8;
+  const uint32_t koff = (uint32_t)((sub >> 2) * t.NR * 64), piece = (uint32_t)(sub & 3);
+  const uint16_t* seq = static_cast<const uint16_t*>(ta.seq) + (int64_t)t.b * ta.s_sb;
+  const uint8_t* mask = ta.mask + (int64_t)t.b * N;
+  float* vin = ta.workspace + (int64_t)t.b * 6 * C;
+  float w[8], bb[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    w[e] = ta.ln_w[c0 + e];
+    bb[e] = ta.ln_b[c0 + e];
+  }
+  const float invc = 1.0f / (float)C;
+  for (int rs = tid >> 4; rs < 16; rs += ngrp) {
+    float pool[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pool[e] = 0.f;
+    int cnt = 0;
+    for (int r = rs; r < S; r += 16) {
+      const bool cell = r >= nt;
+      const int j = r - nt;
+      const uint32_t addr = koff + (uint32_t)j * 64 + ((piece ^ (uint32_t)((j >> 2) & 3)) << 4);
+      const u32x4 raw = cell ? *reinterpret_cast<const u32x4*>(xs + addr)
+                             : *reinterpret_cast<const u32x4*>(seq + (int64_t)r * C + c0);
+      float x[8];
+      float sm = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[2 * e] = bf16_lo(raw[e]);
+        x[2 * e + 1] = bf16_hi(raw[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm += x[e];
+      sm = group_sum_dpp<16>(sm);
+      const float mean = sm * invc;
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[e] = x[e] - mean;
+        q = fmaf(x[e], x[e], q);
+      }
+      q = group_sum_dpp<16>(q);
+      const float rstd = rsqrtf(q * invc + ta.eps);
+      const bool live = !cell || mask[j] != 0;
+      float y[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = live ? fmaf(x[e] * rstd, w[e], bb[e]) : 0.f;
+      if (cell) {
+        *reinterpret_cast<u32x4*>(xs + addr) =
+            u32x4{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]),
+                  pack_bf16x2(y[6], y[7])};
+        if (live && sub == 0) ++cnt;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pool[e] += y[e];
+      } else {
+        const int slot = r == 0 ? 0 : r == 1 ? 1 : r == 4 ? 3 : r == 5 ? 4 : -1;
+        if (slot >= 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vin[slot * C + c0 + e] = y[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[rs * C + c0 + e] = pool[e];
+    if (sub == 0) cred[rs] = (float)cnt;
+  }
+  __syncthreads();
+  float total = 0.f;
+  for (int i = 0; i < 16; ++i) total += cred[i];
+  const float inv = 1.0f / fmaxf(1.f, total);
+  for (int c = tid; c < C; c += (int)blockDim.x) {
+    float p = 0.f;
+    for (int i = 0; i < 16; ++i) p += red[i * C + c];
+    vin[2 * C + c] = p * inv;
+    vin[5 * C + c] = p * inv;
+  }
+}
+
+// shrimp_policy_tail's first launch: the big-tile policy conv (conv + bias +
+// ReLU + Linear(C, 1) head + mask, EPI_HEAD | EPI_RELU) whose staged rows are
+// the position's pre-LayerNorm cells; tail_ln_lds normalises them in LDS first.
+__global__ __launch_bounds__(256, 1) void policy_tail_kernel(const shrimp_conv_args a,
+                                                             const shrimp_tail_args ta,
+                                                             uint32_t x_bytes, uint32_t w_bytes) {
+  constexpr int EPI = EPI_HEAD | EPI_RELU;
+  extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
+  BigTile t;
+  big_setup(t, a, xs, x_bytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, w_bytes);
+  u32x4 wf[8];
+  big_wload(wr, 0, t.lane, wf);
+  float* lp = reinterpret_cast<float*>(xs + 4 * t.NR * 64);
+  float* red = lp + BIG_PARAMS;
+  float* cred = red + 16 * 128;
+  big_params(lp, a.bias, a.ln_w, a.ln_b, a.head_w);
+  f32x4 acc[8][8];
+  big_acc_init(acc, a.bias, t.lg);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  tail_ln_lds(t, xs, ta, red, cred);
+  __syncthreads();  // the normalised rows are complete
+  big_pass(acc, wf, t, xs, wr);
+  conv_epilogue<128, 8, EPI | EPI_BACC, PS_LDS>(a, acc, t.rb, t.rn, t.rv, t.lg, lp);
+}
+
 // ---- weight packing ------------------------------------------------------------
 // Fragment f = (ks * NB + nb) * 64 + lane holds 8 bf16, element e:
 //   W[k][n = 16*nb + lane%16] with
@@ -1366,4 +1483,47 @@ extern "C" int shrimp_conv_block_pair(const shrimp_conv_args* c1, const shrimp_c
                      as_stream(stream), *c1, a2, *c3, a4, (uint32_t)xb, wb, (uint32_t)ob,
                      (uint32_t)ob4);
   return check_launch("conv_block_pair");
+}
+
+static size_t policy_tail_lds(int N) {
+  return (size_t)big_rows_padded(N) * 256 + (BIG_PARAMS + 16 * 128 + 16) * sizeof(float);
+}
+
+extern "C" int shrimp_policy_tail_supported(int N, int C) {
+  return C == 128 && N > 0 && N <= BIG_MAX_N && (g_conv_variant == 0 || g_conv_variant == 3) &&
+         policy_tail_lds(N) <= (size_t)max_lds_per_block();
+}
+
+extern "C" int shrimp_policy_tail(const shrimp_conv_args* p, const shrimp_tail_args* ta,
+                                  void* stream) {
+  SHRIMP_REQUIRE(p != nullptr && ta != nullptr, "policy_tail: null args");
+  if (ta->B == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(ta->seq && ta->mask && ta->ln_w && ta->ln_b && ta->workspace,
+                 "policy_tail: null tail pointer");
+  SHRIMP_REQUIRE(ta->C == 128 && ta->n_tokens >= 6 && ta->S > ta->n_tokens && ta->s_sb % 8 == 0 &&
+                     (reinterpret_cast<uintptr_t>(ta->seq) & 15) == 0,
+                 "policy_tail: needs C = 128, >= 6 tokens, 16-byte aligned rows (C %d, tokens %d)",
+                 ta->C, ta->n_tokens);
+  SHRIMP_REQUIRE(!ta->value || (ta->vr_w && ta->vr_b && ta->vh_w && ta->vh_b),
+                 "policy_tail: value head");
+  SHRIMP_REQUIRE(!ta->moves_left || (ta->mr_w && ta->mr_b && ta->mh_w && ta->mh_b),
+                 "policy_tail: moves-left head");
+  SHRIMP_REQUIRE(ta->bins > 0 && ta->bins <= 256, "policy_tail: bins %d", ta->bins);
+  const int N = ta->S - ta->n_tokens;
+  SHRIMP_REQUIRE(shrimp_policy_tail_supported(N, ta->C), "policy_tail: no fused kernel for N %d", N);
+  SHRIMP_REQUIRE(p->B == ta->B && p->N == N && p->cin_pad == 128 && p->cout == 128 && p->taps == 7 &&
+                     p->idx_stride >= 7 && p->idx && p->w && p->bias && p->head_w && p->head_b &&
+                     p->head_out && p->relu && !p->ln_w && !p->resid,
+                 "policy_tail: policy must be the 7-tap 128-channel conv + ReLU + head over the cells");
+  SHRIMP_REQUIRE(p->x == static_cast<const uint16_t*>(ta->seq) + (int64_t)ta->n_tokens * 128 &&
+                     p->x_sb == ta->s_sb && p->x_sn == 128 && p->mask == ta->mask,
+                 "policy_tail: the policy conv must read the cell rows of tail.seq with its mask");
+  const int64_t x_extent = (int64_t)(p->B - 1) * p->x_sb + (int64_t)(N - 1) * p->x_sn + 128;
+  SHRIMP_REQUIRE(x_extent * 2 < (int64_t)0x7FFF0000, "policy_tail: activation buffer too large");
+  const int waves = (N + 127) / 128;
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(policy_tail_kernel, dim3(p->B), dim3(64 * waves), policy_tail_lds(N), st, *p,
+                     *ta, (uint32_t)(x_extent * 2), (uint32_t)shrimp_conv_wpack_bytes(7, 128, 128));
+  if (int rc = check_launch("policy_tail")) return rc;
+  return launch_value_heads(ta, st);
 }

@@ -203,6 +203,20 @@ __global__ void fill_tokens_kernel(const float* __restrict__ tokens, int n_token
 }
 
 // ---- trunk tail + value heads (model.py:927-935, 990-1002) --------------------
+// Sum over the TPR lanes of a row: DPP moves up to 16 lanes, then one shuffle
+// (the butterfly order of v += shfl_xor(v, m), m = 1, 2, 4, ...).
+template <int TPR>
+SHRIMP_DEV float row_group_sum(float v) {
+  if constexpr (TPR <= 16) {
+    return group_sum_dpp<TPR>(v);
+  } else {
+    v = group_sum_dpp<16>(v);
+#pragma unroll
+    for (int m = 16; m < TPR; m <<= 1) v += __shfl_xor(v, m, 64);
+    return v;
+  }
+}
+
 // Pass 1, one workgroup per position: final LayerNorm of every row (cells
 // masked), written to out_seq; the value-head inputs [T0 | T1 | pooled] and
 // [T4 | T5 | pooled] go to the workspace (B, 6C) fp32.
@@ -281,8 +295,7 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a,
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) s += x[e];
-#pragma unroll
-      for (int m = 1; m < TPR; m <<= 1) s += __shfl_xor(s, m, 64);
+      s = row_group_sum<TPR>(s);
       const float mean = s * invc;
       float q = 0.f;
 #pragma unroll
@@ -290,8 +303,7 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a,
         x[e] = cv ? x[e] - mean : 0.f;
         q = fmaf(x[e], x[e], q);
       }
-#pragma unroll
-      for (int m = 1; m < TPR; m <<= 1) q += __shfl_xor(q, m, 64);
+      q = row_group_sum<TPR>(q);
       const float rstd = rsqrtf(q * invc + a.eps);
       const bool rv = row < S && cv;
       const bool cell = row >= nt;
@@ -679,6 +691,13 @@ static int launch_trunk_tail(const shrimp_tail_args* a, float* ws, hipStream_t s
   else SHRIMP_FLN(32);
 #undef SHRIMP_FLN
   if (int rc = check_launch("trunk_tail/ln")) return rc;
+  return launch_value_heads(&k, st);
+}
+
+// Pass 2 of the tail: the value / moves-left heads from the head inputs in
+// a->workspace (pass 1 or the fused policy tail wrote them).
+int shrimp::launch_value_heads(const shrimp_tail_args* a, hipStream_t st) {
+  const shrimp_tail_args& k = *a;
   if (!k.value && !k.moves_left) return SHRIMP_OK;
   const int ks1 = kHeadThreads / k.C, ks2 = kHeadThreads / k.bins;
   const size_t smem = ((size_t)kHeadPos * 3 * k.C + (size_t)ks1 * kHeadPos * k.C +

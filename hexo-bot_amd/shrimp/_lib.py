@@ -177,6 +177,8 @@ SIGNATURES: dict = {
         ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _i64, ctypes.c_int, _vp]
     ),
     "shrimp_trunk_tail": (ctypes.c_int, [ctypes.POINTER(TailArgs), _vp]),
+    "shrimp_policy_tail_supported": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
+    "shrimp_policy_tail": (ctypes.c_int, [ctypes.POINTER(ConvArgs), ctypes.POINTER(TailArgs), _vp]),
     "shrimp_trunk_tail_noalloc": (ctypes.c_int, [ctypes.POINTER(TailArgs), _vp]),
     "shrimp_decode": (
         ctypes.c_int,

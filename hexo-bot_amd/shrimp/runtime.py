@@ -113,6 +113,11 @@ class HipForward:
         # rows handed to the second inside the workgroup) where it applies;
         # off runs one launch per block (bit-identical).
         self.use_block_pair = True
+        # Final LayerNorm, pooled head inputs and policy conv in one launch
+        # (the normalised cells never leave the workgroup) where it applies;
+        # off, and whenever keep_buffers asks for seqf, runs shrimp_trunk_tail
+        # and the policy conv (bit-identical outputs).
+        self.use_fused_tail = True
         # LN1 + q/k/v kernel with LN1 folded into its weights where it
         # applies; off runs the linear kernel's QKV mode.
         self.use_fused_qkv = True
@@ -740,15 +745,27 @@ class HipForward:
             mh_b=P.ml.hb.data_ptr(), moves_left=_lib.ptr(ml), workspace=tail_ws.data_ptr(),
             B=B, S=S, n_tokens=NUM_TOKENS, C=C, bins=VALUE_BINS,
         )
-        _lib.check(lib.shrimp_trunk_tail(ctypes.byref(tail), st), "trunk_tail")
-        self._mark("tail")
         policy = torch.empty((B, N), dtype=torch.float32, device=dev)
-        launch_conv(
-            x=seqf[:, NUM_TOKENS:], x_sb=S * C, x_sn=C, wpack=P.policy.w, bias=P.policy.b,
-            cin_pad=C, cout=C, relu=True, head_w=P.policy.hw, head_b=P.policy.hb,
-            head_out=policy, **conv_common,
-        )
-        self._mark("policy")
+        if (self.use_fused_tail and not self.keep_buffers and 2 * B > self._cus(dev)
+                and lib.shrimp_policy_tail_supported(N, C)):
+            pa = _lib.ConvArgs(
+                x=seq.data_ptr() + NUM_TOKENS * C * seq.element_size(), x_sb=S * C, x_sn=C,
+                idx=idx.data_ptr(), taps=7, idx_stride=7, mask=mask8.data_ptr(),
+                w=P.policy.w.data_ptr(), bias=P.policy.b.data_ptr(), relu=1,
+                head_w=P.policy.hw.data_ptr(), head_b=P.policy.hb.data_ptr(),
+                head_out=policy.data_ptr(), B=B, N=N, cin_pad=C, cout=C,
+            )
+            _lib.check(lib.shrimp_policy_tail(ctypes.byref(pa), ctypes.byref(tail), st), "policy_tail")
+            self._mark("policy_tail")
+        else:
+            _lib.check(lib.shrimp_trunk_tail(ctypes.byref(tail), st), "trunk_tail")
+            self._mark("tail")
+            launch_conv(
+                x=seqf[:, NUM_TOKENS:], x_sb=S * C, x_sn=C, wpack=P.policy.w, bias=P.policy.b,
+                cin_pad=C, cout=C, relu=True, head_w=P.policy.hw, head_b=P.policy.hb,
+                head_out=policy, **conv_common,
+            )
+            self._mark("policy")
         out = {"policy": policy, "value": value}
         if request_moves_left:
             out["moves_left"] = ml

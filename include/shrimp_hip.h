@@ -471,6 +471,21 @@ typedef struct {
 
 int shrimp_trunk_tail(const shrimp_tail_args* a, void* stream);
 
+/* Trunk tail and policy head in one pass over the cells (model.py:927-935,
+ * 990-1020; no single counterpart in the reference, which normalises, pools
+ * and runs the policy head as separate modules): shrimp_trunk_tail(tail)
+ * followed by shrimp_hex_conv(policy) on tail's normalised cell rows, with the
+ * same results, except that the normalised rows stay in the policy conv's
+ * workgroup: tail->out_seq is not written. tail: as for shrimp_trunk_tail,
+ * bf16 seq with C = 128 and 16-byte aligned rows. policy: the 7-tap
+ * 128 -> 128 conv + bias + ReLU + Linear(C, 1) head (w, bias, head_w, head_b,
+ * head_out, relu = 1, idx, idx_stride, B, N = S - n_tokens) reading the cell
+ * rows of tail->seq: x = seq + n_tokens * 128, x_sb = tail->s_sb, x_sn = 128,
+ * mask = tail->mask. shrimp_policy_tail_supported reports whether the fused
+ * kernel covers N cells of C channels (else SHRIMP_EINVAL). */
+int shrimp_policy_tail_supported(int N, int C);
+int shrimp_policy_tail(const shrimp_conv_args* policy, const shrimp_tail_args* tail, void* stream);
+
 /* shrimp_trunk_tail without a workspace: no counterpart in the reference. It
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serve loops, harnesses that forbid hipMalloc). The head

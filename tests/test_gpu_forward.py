@@ -216,6 +216,33 @@ def test_fused_and_unfused_mlp_paths_agree(cfg4_batch):
         assert err <= 1e-2, key
 
 
+def test_large_batch_launch_fusions_are_bit_identical():
+    """At batches that give every position its own workgroup (2 B > compute
+    units) the forward runs consecutive ConvBlocks as one pair launch and the
+    final LayerNorm, pooling and policy conv as one launch; both hand rows over
+    inside the workgroup instead of through HBM and must give the same bits as
+    the separate launches (one ConvBlock launch per block, shrimp_trunk_tail
+    and the policy conv)."""
+
+    from shrimp import synthetic
+
+    b = synthetic.position_batch("cfg4", 160, seed=78)
+    net = _net(128, 8, "CCACCACCACCA", seed=6)
+    rt = net.hip_runtime()
+    print("large batch fusions B=160", flush=True)
+    fused = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+    rt.use_block_pair = rt.use_fused_tail = False
+    try:
+        plain = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+    finally:
+        rt.use_block_pair = rt.use_fused_tail = True
+    for key in ("policy", "value", "moves_left"):
+        err = (fused[key] - plain[key]).abs().max().item()
+        print(f"fused launches vs separate {key}: {err:.3e}", flush=True)
+        assert torch.equal(fused[key], plain[key]), key
+    assert fused["value"].abs().max() > 0 and fused["policy"].abs().max() > 0
+
+
 def test_fused_attention_option_matches_oracle(cfg4_batch):
     """The one-launch LN1 + q/k/v + attention option (no q/k/v tensor): the
     forward stays within tolerance of the oracle and of the default two-launch
