@@ -1055,16 +1055,16 @@ __global__ __launch_bounds__(256, 1) void hex_block_pair_kernel(
 // rows 0, 1, 4 and 5 from seq; the head inputs [T0 | T1 | pooled | T4 | T5 |
 // pooled] to the workspace. As in final_ln_kernel a row is 16 lanes of 8
 // channels, and row slot rs (= row % 16) pools its cells in row order; the 16
-// slot sums then add in slot order (red: [16][128] floats, cred: [16]).
+// slot sums then add in slot order (red: [16][128] floats, cred: [16]). mk:
+// the position's cell mask bytes, staged in LDS.
 SHRIMP_DEV void tail_ln_lds(const BigTile& t, unsigned char* xs, const shrimp_tail_args& ta,
-                            float* red, float* cred) {
+                            float* red, float* cred, const uint8_t* mk) {
   constexpr int C = 128;
   const int S = ta.S, nt = ta.n_tokens, N = S - nt;
   const int tid = threadIdx.x, ngrp = (int)(blockDim.x >> 4);
   const int sub = tid & 15, c0 = sub * 8;
   const uint32_t koff = (uint32_t)((sub >> 2) * t.NR * 64), piece = (uint32_t)(sub & 3);
   const uint16_t* seq = static_cast<const uint16_t*>(ta.seq) + (int64_t)t.b * ta.s_sb;
-  const uint8_t* mask = ta.mask + (int64_t)t.b * N;
   float* vin = ta.workspace + (int64_t)t.b * 6 * C;
   float w[8], bb[8];
 #pragma unroll
@@ -1103,7 +1103,7 @@ SHRIMP_DEV void tail_ln_lds(const BigTile& t, unsigned char* xs, const shrimp_ta
       }
       q = group_sum_dpp<16>(q);
       const float rstd = rsqrtf(q * invc + ta.eps);
-      const bool live = !cell || mask[j] != 0;
+      const bool live = !cell || mk[j] != 0;
       float y[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) y[e] = live ? fmaf(x[e] * rstd, w[e], bb[e]) : 0.f;
@@ -1154,12 +1154,14 @@ __global__ __launch_bounds__(256, 1) void policy_tail_kernel(const shrimp_conv_a
   float* lp = reinterpret_cast<float*>(xs + 4 * t.NR * 64);
   float* red = lp + BIG_PARAMS;
   float* cred = red + 16 * 128;
+  uint8_t* mk = reinterpret_cast<uint8_t*>(cred + 16);
   big_params(lp, a.bias, a.ln_w, a.ln_b, a.head_w);
+  for (int j = threadIdx.x; j < t.N; j += blockDim.x) mk[j] = ta.mask[(int64_t)t.b * t.N + j];
   f32x4 acc[8][8];
   big_acc_init(acc, a.bias, t.lg);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  tail_ln_lds(t, xs, ta, red, cred);
+  tail_ln_lds(t, xs, ta, red, cred, mk);
   __syncthreads();  // the normalised rows are complete
   big_pass(acc, wf, t, xs, wr);
   conv_epilogue<128, 8, EPI | EPI_BACC, PS_LDS>(a, acc, t.rb, t.rn, t.rv, t.lg, lp);
@@ -1486,7 +1488,8 @@ extern "C" int shrimp_conv_block_pair(const shrimp_conv_args* c1, const shrimp_c
 }
 
 static size_t policy_tail_lds(int N) {
-  return (size_t)big_rows_padded(N) * 256 + (BIG_PARAMS + 16 * 128 + 16) * sizeof(float);
+  return (size_t)big_rows_padded(N) * 256 + (BIG_PARAMS + 16 * 128 + 16) * sizeof(float) +
+         (size_t)((N + 15) & ~15);
 }
 
 extern "C" int shrimp_policy_tail_supported(int N, int C) {
