@@ -873,8 +873,8 @@ struct BlockOutStore : BufRowStore16<8> {
 // otherwise the previous block wrote it into LDS.
 template <bool NEXT>
 SHRIMP_DEV void block_convs(BigTile& t, unsigned char* xs, const shrimp_conv_args& c1,
-                            const shrimp_conv_args& a2, const float* lp1, const float* lp2,
-                            uint32_t w_bytes, uint32_t o_bytes, uint32_t r_bytes, bool first) {
+                            const shrimp_conv_args& a2, int pslot, uint32_t w_bytes,
+                            uint32_t o_bytes, uint32_t r_bytes, bool first) {
   if (!first) {
     // as before conv2: the previous block's LDS row and weight offsets are
     // recomputed, not kept alive (spilled) for reuse
@@ -889,6 +889,9 @@ SHRIMP_DEV void block_convs(BigTile& t, unsigned char* xs, const shrimp_conv_arg
   const __amdgpu_buffer_rsrc_t wr2 = make_rsrc(a2.w, w_bytes);
   u32x4 wf[8];
   big_wload(wr1, 0, t.lane, wf);
+  // this block's parameter sets: slots pslot and pslot + 1 after the rows
+  const float* lp1 = reinterpret_cast<const float*>(xs + 4 * t.NR * 64) + pslot * BIG_PARAMS;
+  const float* lp2 = lp1 + BIG_PARAMS;
   f32x4 acc[8][8];
   big_acc_init(acc, c1.bias, t.lg);
   if (first) {
@@ -1023,16 +1026,32 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
       BufRowStore16<8>(c2, t.rb, t.rn, t.rv, t.lg, o_bytes, x_bytes));
 }
 
-// Two consecutive ConvBlocks (c1, c2 then c3, c4) in one launch: x staged
-// once by DMA (big_setup), the first block's output rows handed to the second
-// in LDS, so the second does not read them back from HBM for its convs (its
-// residual reads them: a wave reads rows it wrote itself). x_bytes spans c1.x
-// (the first residual), o_bytes c2.out (= c3.x, the second residual),
-// o2_bytes c4.out.
+// What the second ConvBlock of a pair needs beyond the first one's arguments:
+// its weights, epsilons and epilogue parameters (it reads and writes the
+// first block's output rows, with the first block's index, mask and shape).
+struct PairSecond {
+  const void* w3;
+  const float* b3;
+  const float* l3w;
+  const float* l3b;
+  float eps3;
+  const void* w4;
+  const float* b4;
+  const float* l4w;
+  const float* l4b;
+  const float* g4;
+  float eps4;
+};
+
+// Two consecutive ConvBlocks in one launch: x staged once by DMA
+// (big_setup), the first block's output rows handed to the second in LDS, so
+// the second does not read them back from HBM for its convs (its residual
+// reads them: a wave reads rows it wrote itself, and writes them again in
+// place). x_bytes spans c1.x (the first residual), o_bytes c2.out (the second
+// block's residual and output).
 __global__ __launch_bounds__(256, 1) void hex_block_pair_kernel(
-    const shrimp_conv_args c1, const shrimp_conv_args c2, const shrimp_conv_args c3,
-    const shrimp_conv_args c4, uint32_t x_bytes, uint32_t w_bytes, uint32_t o_bytes,
-    uint32_t o2_bytes) {
+    const shrimp_conv_args c1, const shrimp_conv_args c2, const PairSecond p2, uint32_t x_bytes,
+    uint32_t w_bytes, uint32_t o_bytes) {
   extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
   BigTile t;
   big_setup(t, c1, xs, x_bytes);
@@ -1042,10 +1061,20 @@ __global__ __launch_bounds__(256, 1) void hex_block_pair_kernel(
   float* lp4 = lp3 + BIG_PARAMS;
   big_params(lp1, c1.bias, c1.ln_w, c1.ln_b, nullptr);
   big_params(lp2, c2.bias, c2.ln_w, c2.ln_b, c2.gamma);
-  big_params(lp3, c3.bias, c3.ln_w, c3.ln_b, nullptr);
-  big_params(lp4, c4.bias, c4.ln_w, c4.ln_b, c4.gamma);
-  block_convs<true>(t, xs, c1, c2, lp1, lp2, w_bytes, o_bytes, x_bytes, true);
-  block_convs<false>(t, xs, c3, c4, lp3, lp4, w_bytes, o2_bytes, o_bytes, false);
+  big_params(lp3, p2.b3, p2.l3w, p2.l3b, nullptr);
+  big_params(lp4, p2.b4, p2.l4w, p2.l4b, p2.g4);
+  block_convs<true>(t, xs, c1, c2, 0, w_bytes, o_bytes, x_bytes, true);
+  shrimp_conv_args c3 = c1;
+  c3.w = p2.w3;
+  c3.bias = p2.b3;
+  c3.eps = p2.eps3;
+  shrimp_conv_args c4 = c2;
+  c4.w = p2.w4;
+  c4.eps = p2.eps4;
+  c4.resid = c2.out;
+  c4.r_sb = c2.o_sb;
+  c4.r_sn = c2.o_sn;
+  block_convs<false>(t, xs, c3, c4, 2, w_bytes, o_bytes, o_bytes, false);
 }
 
 // ---- trunk tail + policy head (model.py:927-935, 990-1020) ---------------------
@@ -1477,13 +1506,16 @@ extern "C" int shrimp_conv_block_pair(const shrimp_conv_args* c1, const shrimp_c
   SHRIMP_REQUIRE(c3->idx == c1->idx && c3->idx_stride == c1->idx_stride && c3->mask == c1->mask &&
                      c3->B == c1->B && c3->N == c1->N,
                  "conv_block_pair: both blocks must share the index, mask and shape");
+  SHRIMP_REQUIRE(c4->out == c2->out && c4->o_sb == c2->o_sb && c4->o_sn == c2->o_sn,
+                 "conv_block_pair: the second block must write in place over the first block's output");
   SHRIMP_REQUIRE(shrimp_conv_block_pair_supported(7, c1->N, 128, 128),
                  "conv_block_pair: %d rows do not fit the LDS of one workgroup", c1->N);
   const int waves = (c1->N + 127) / 128;
   const uint32_t wb = (uint32_t)shrimp_conv_wpack_bytes(7, 128, 128);
+  const PairSecond p2{c3->w, c3->bias, c3->ln_w, c3->ln_b, c3->eps,
+                      c4->w, c4->bias, c4->ln_w, c4->ln_b, c4->gamma, c4->eps};
   hipLaunchKernelGGL(hex_block_pair_kernel, dim3(c1->B), dim3(64 * waves), block_pair_lds(c1->N),
-                     as_stream(stream), *c1, a2, *c3, a4, (uint32_t)xb, wb, (uint32_t)ob,
-                     (uint32_t)ob4);
+                     as_stream(stream), *c1, a2, p2, (uint32_t)xb, wb, (uint32_t)ob);
   return check_launch("conv_block_pair");
 }
 
