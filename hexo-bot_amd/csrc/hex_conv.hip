@@ -683,11 +683,56 @@ SHRIMP_DEV void big_dma(unsigned char* xs, const BigTile& t, int kc, int g) {
                                            off, 0, 0, 0);
 }
 
+// Epilogue parameters of NS convs, [bias | ln_w | ln_b | extra | zeros] of
+// 128 floats each in LDS. They are requested into registers before the row
+// DMA (memory requests retire in order, so a wait for them issued after the
+// DMA would wait for the rows as well) and written to LDS once it is issued.
+// Slot s = tid + j * blockDim.x (j = 0, 1; stored when s < 128) carries
+// floats 4 (s & 31) .. + 3 of array s >> 5; a null array stores zeros.
+template <int NS>
+struct BigParams {
+  f32x4 v[NS][2];
+  SHRIMP_DEV void load(int set, const float* bias, const float* ln_w, const float* ln_b,
+                       const float* extra) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int sl = (int)(threadIdx.x + j * blockDim.x) & 127;
+      const int arr = sl >> 5;
+      const float* src = arr == 0 ? bias : (arr == 1 ? ln_w : (arr == 2 ? ln_b : extra));
+      const float* p = src ? src : bias;
+      const f32x4 x = *reinterpret_cast<const f32x4*>(p + 4 * (sl & 31));
+      v[set][j] = src ? x : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  SHRIMP_DEV void store(float* lp) const {
+#pragma unroll
+    for (int set = 0; set < NS; ++set) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int sl = (int)(threadIdx.x + j * blockDim.x);
+        if (sl < 128)
+          *reinterpret_cast<f32x4*>(lp + set * BIG_PARAMS + (sl >> 5) * 128 + 4 * (sl & 31)) = v[set][j];
+      }
+      if (threadIdx.x < 32)
+        *reinterpret_cast<f32x4*>(lp + set * BIG_PARAMS + 512 + 4 * threadIdx.x) =
+            f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+};
+
 // Requests all four chunks by DMA and turns the neighbour indices of this wave's rows
 // into swizzled 16-bit LDS row addresses j * 64 | ((j >> 2) & 3) << 4.
+// The indices are requested before the rows (three loads per row block, absent
+// rows reading zeros past the resource), and every wave issues the same nine
+// DMAs per chunk (a wave with fewer groups repeats its first one: the same
+// bytes to the same place), so the wait for the indices counts the DMAs
+// instead of waiting for them and the row addresses are computed while the
+// rows arrive. Needs idx_stride >= 7 and N <= BIG_MAX_N.
 SHRIMP_DEV void big_setup(BigTile& t, const shrimp_conv_args& a, unsigned char* xs,
                           uint32_t x_bytes) {
-  constexpr int T = 7, MB = 8;
+  // DMAs per chunk and wave: with ceil(N / 128) waves a wave owns at most
+  // ceil((8 nw + 1) / nw) = 9 of the ceil((N + 1) / 16) row groups
+  constexpr int T = 7, MB = 8, GPW = 9;
   t.lane = threadIdx.x & 63;
   t.wave = wave_id();
   t.nw = blockDim.x >> 6;
@@ -699,21 +744,32 @@ SHRIMP_DEV void big_setup(BigTile& t, const shrimp_conv_args& a, unsigned char* 
   t.xr = make_rsrc(a.x, x_bytes);
   t.xbase = (uint32_t)((int64_t)t.b * a.x_sb * 2);
   t.xsn2 = (uint32_t)(a.x_sn * 2);
-  for (int kc = 0; kc < 4; ++kc)
-    for (int g = t.wave; g < t.groups; g += t.nw) big_dma(xs, t, kc, g);
   const int row0 = t.wave * (MB * 16);
-  const int* idxb = a.idx + (int64_t)t.b * t.N * a.idx_stride;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     t.rb[mb] = t.b;
     t.rn[mb] = row0 + mb * 16 + (t.lane & 15);
     t.rv[mb] = t.rn[mb] < t.N;
   }
-  int jr[T][MB];
+  const __amdgpu_buffer_rsrc_t ir =
+      make_rsrc(a.idx + (int64_t)t.b * t.N * a.idx_stride, (uint32_t)(t.N * a.idx_stride * 4));
+  u32x4 i0[MB];
+  u32x2 i1[MB];
+  unsigned i2[MB];
 #pragma unroll
-  for (int tp = 0; tp < T; ++tp)
+  for (int mb = 0; mb < MB; ++mb) {
+    const uint32_t off = t.rv[mb] ? (uint32_t)(t.rn[mb] * a.idx_stride * 4) : SHRIMP_OOB_OFFSET;
+    i0[mb] = buf_load16(ir, off);
+    i1[mb] = buf_load8(ir, off + 16);
+    i2[mb] = buf_load4(ir, off + 24);
+  }
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) jr[tp][mb] = t.rv[mb] ? idxb[t.rn[mb] * a.idx_stride + tp] : t.N;
+  for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+    for (int i = 0; i < GPW; ++i) {
+      const int g = t.wave + i * t.nw;
+      big_dma(xs, t, kc, g < t.groups ? g : t.wave);
+    }
 #pragma unroll
   for (int tp = 0; tp < T; ++tp)
 #pragma unroll
@@ -721,22 +777,14 @@ SHRIMP_DEV void big_setup(BigTile& t, const shrimp_conv_args& a, unsigned char* 
       uint32_t pk = 0;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int j = jr[tp][2 * m2 + h];
+        const int mb = 2 * m2 + h;
+        const unsigned raw = tp < 4 ? i0[mb][tp] : (tp < 6 ? i1[mb][tp - 4] : i2[mb]);
+        const int j = t.rv[mb] ? (int)raw : t.N;
         const int jj = (j >= 0 && j < t.N) ? j : t.N;
         pk |= (uint32_t)(jj * 64 + (((jj >> 2) & 3) << 4)) << (16 * h);
       }
       t.sw2[tp][m2] = pk;
     }
-}
-
-// Epilogue parameters of one conv into LDS: [bias | ln_w | ln_b | extra | zeros].
-SHRIMP_DEV void big_params(float* lp, const float* bias, const float* ln_w, const float* ln_b,
-                           const float* extra) {
-  const float* src[4] = {bias, ln_w, ln_b, extra};
-  for (int i = threadIdx.x; i < BIG_PARAMS; i += blockDim.x) {
-    const float* sp = i < 4 * 128 ? src[i / 128] : nullptr;
-    lp[i] = sp ? sp[i % 128] : 0.f;
-  }
 }
 
 // Weight fragments of k-step s (8 output blocks).
@@ -804,13 +852,15 @@ template <int EPI>
 __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_args a,
                                                               uint32_t x_bytes, uint32_t w_bytes) {
   extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
+  BigParams<1> bp;
+  bp.load(0, a.bias, a.ln_w, a.ln_b, (EPI & EPI_HEAD) ? a.head_w : a.gamma);
   BigTile t;
   big_setup(t, a, xs, x_bytes);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, w_bytes);
   u32x4 wf[8];
   big_wload(wr, 0, t.lane, wf);
   float* lp = reinterpret_cast<float*>(xs + 4 * t.NR * 64);
-  big_params(lp, a.bias, a.ln_w, a.ln_b, (EPI & EPI_HEAD) ? a.head_w : a.gamma);
+  bp.store(lp);
   // the accumulators start from the bias, except for the residual epilogue,
   // which adds it at the end like the fused ConvBlock's second conv (the two
   // give bit-identical blocks)
@@ -968,6 +1018,9 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
                                                            uint32_t x_bytes, uint32_t w_bytes,
                                                            uint32_t o_bytes) {
   extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
+  BigParams<2> bp;
+  bp.load(0, c1.bias, c1.ln_w, c1.ln_b, nullptr);
+  bp.load(1, c2.bias, c2.ln_w, c2.ln_b, c2.gamma);
   BigTile t;
   big_setup(t, c1, xs, x_bytes);
   const __amdgpu_buffer_rsrc_t wr1 = make_rsrc(c1.w, w_bytes);
@@ -976,8 +1029,7 @@ __global__ __launch_bounds__(256, 1) void hex_block_kernel(const shrimp_conv_arg
   big_wload(wr1, 0, t.lane, wf);
   float* lp1 = reinterpret_cast<float*>(xs + 4 * t.NR * 64);
   float* lp2 = lp1 + BIG_PARAMS;
-  big_params(lp1, c1.bias, c1.ln_w, c1.ln_b, nullptr);
-  big_params(lp2, c2.bias, c2.ln_w, c2.ln_b, c2.gamma);
+  bp.store(lp1);
   f32x4 acc[8][8];
   big_acc_init(acc, c1.bias, t.lg);
   __builtin_amdgcn_s_waitcnt(0);
@@ -1053,16 +1105,14 @@ __global__ __launch_bounds__(256, 1) void hex_block_pair_kernel(
     const shrimp_conv_args c1, const shrimp_conv_args c2, const PairSecond p2, uint32_t x_bytes,
     uint32_t w_bytes, uint32_t o_bytes) {
   extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
+  BigParams<4> bp;
+  bp.load(0, c1.bias, c1.ln_w, c1.ln_b, nullptr);
+  bp.load(1, c2.bias, c2.ln_w, c2.ln_b, c2.gamma);
+  bp.load(2, p2.b3, p2.l3w, p2.l3b, nullptr);
+  bp.load(3, p2.b4, p2.l4w, p2.l4b, p2.g4);
   BigTile t;
   big_setup(t, c1, xs, x_bytes);
-  float* lp1 = reinterpret_cast<float*>(xs + 4 * t.NR * 64);
-  float* lp2 = lp1 + BIG_PARAMS;
-  float* lp3 = lp2 + BIG_PARAMS;
-  float* lp4 = lp3 + BIG_PARAMS;
-  big_params(lp1, c1.bias, c1.ln_w, c1.ln_b, nullptr);
-  big_params(lp2, c2.bias, c2.ln_w, c2.ln_b, c2.gamma);
-  big_params(lp3, p2.b3, p2.l3w, p2.l3b, nullptr);
-  big_params(lp4, p2.b4, p2.l4w, p2.l4b, p2.g4);
+  bp.store(reinterpret_cast<float*>(xs + 4 * t.NR * 64));
   block_convs<true>(t, xs, c1, c2, 0, w_bytes, o_bytes, x_bytes, true);
   shrimp_conv_args c3 = c1;
   c3.w = p2.w3;
@@ -1175,6 +1225,8 @@ __global__ __launch_bounds__(256, 1) void policy_tail_kernel(const shrimp_conv_a
                                                              uint32_t x_bytes, uint32_t w_bytes) {
   constexpr int EPI = EPI_HEAD | EPI_RELU;
   extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
+  BigParams<1> bp;
+  bp.load(0, a.bias, a.ln_w, a.ln_b, a.head_w);
   BigTile t;
   big_setup(t, a, xs, x_bytes);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, w_bytes);
@@ -1184,7 +1236,7 @@ __global__ __launch_bounds__(256, 1) void policy_tail_kernel(const shrimp_conv_a
   float* red = lp + BIG_PARAMS;
   float* cred = red + 16 * 128;
   uint8_t* mk = reinterpret_cast<uint8_t*>(cred + 16);
-  big_params(lp, a.bias, a.ln_w, a.ln_b, a.head_w);
+  bp.store(lp);
   for (int j = threadIdx.x; j < t.N; j += blockDim.x) mk[j] = ta.mask[(int64_t)t.b * t.N + j];
   f32x4 acc[8][8];
   big_acc_init(acc, a.bias, t.lg);
