@@ -1139,7 +1139,7 @@ __global__ __launch_bounds__(256, 1) void hex_block_pair_kernel(
 SHRIMP_DEV void tail_ln_lds(const BigTile& t, unsigned char* xs, const shrimp_tail_args& ta,
                             float* red, float* cred, const uint8_t* mk) {
   constexpr int C = 128;
-  const int S = ta.S, nt = ta.n_tokens, N = S - nt;
+  const int S = ta.S, nt = ta.n_tokens;
   const int tid = threadIdx.x, ngrp = (int)(blockDim.x >> 4);
   const int sub = tid & 15, c0 = sub * 8;
   const uint32_t koff = (uint32_t)((sub >> 2) * t.NR * 64), piece = (uint32_t)(sub & 3);
