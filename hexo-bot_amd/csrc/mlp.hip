@@ -19,8 +19,10 @@
 //
 // Layout: one persistent workgroup per CU keeps the packed fragments of the
 // three matrices in LDS (C = 128: 32 + 64 + 64 KiB = the whole 160 KiB); each
-// of its 12 waves streams blocks of 16 rows through the three products
-// without leaving registers: a product's output fragment (lane l: channels
+// of its 16 waves (four per SIMD, at most 128 VGPRs each: the rows are not
+// requested a block ahead, the other waves of the SIMD cover their latency)
+// streams blocks of 16 rows through the three products without leaving
+// registers: a product's output fragment (lane l: channels
 // 16 nb + 4 (l/16) + j of row l % 16) is directly the next product's input
 // fragment for K-step nb / 2, because W1' and W2' are packed with that
 // interleaved K order. The biases enter as the accumulators' initial values.
@@ -41,7 +43,7 @@ namespace {
 
 constexpr int MC = 128;           // channels
 constexpr int MH = 2 * MC;        // hidden width
-constexpr int MWAVES = 12;        // waves per workgroup (3 per SIMD)
+constexpr int MWAVES = 16;        // waves per workgroup (4 per SIMD)
 constexpr uint32_t WO_OFF = 0;                        // out_proj fragments
 constexpr uint32_t W1_OFF = MC * MC * 2;              // fc1 fragments
 constexpr uint32_t W2_OFF = W1_OFF + MC * MH * 2;     // fc2 fragments
@@ -100,16 +102,17 @@ SHRIMP_DEV void load_s(const shrimp_mlp_args& a, __amdgpu_buffer_rsrc_t sr, int 
   for (int nb = 0; nb < MC / 16; ++nb) sf[nb] = buf_load8(sr, so + nb * 32);
 }
 
-// One block of 16 rows (lane: row lane % 16, channel group lane / 16). sin
-// holds the block's residual rows on entry; once they are consumed the next
-// block's (row next_row) are requested into the same registers, so their
-// latency hides behind this block's MLP.
+// One block of 16 rows (lane: row lane % 16, channel group lane / 16); xf:
+// the block's attention-output fragments.
 SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, const MlpBias& bias,
                           __amdgpu_buffer_rsrc_t sr, const u32x4 (&xf)[MC / 32], int row,
-                          int lane, u32x2 (&sin)[MC / 16], int next_row, bool store) {
+                          int lane, bool store) {
   constexpr int KS1 = MC / 32, NB1 = MC / 16, NBH = MH / 16, KT = MH / 32, NB2 = MC / 16;
   constexpr int TB1 = NB1, TB2 = NB1 + NBH;  // first bias block of b1', b2'
   const int lg = lane >> 4;
+  // the block's residual rows, consumed after out_proj
+  u32x2 sin[MC / 16];
+  load_s(a, sr, row, lg, sin);
 
   // accumulators start at the biases
   f32x4 acc[NB1];
@@ -142,7 +145,6 @@ SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, con
     sp[nb].x = pack_bf16x2(v[nb][0], v[nb][1]);
     sp[nb].y = pack_bf16x2(v[nb][2], v[nb][3]);
   }
-  load_s(a, sr, next_row, lg, sin);
   float s = 0.f;
 #pragma unroll
   for (int nb = 0; nb < NB1; ++nb)
@@ -251,7 +253,7 @@ __global__ __launch_bounds__(MWAVES * 64, 1) void attn_mlp_kernel(const shrimp_m
   // row mask bytes: rows at or past `rows` read as 0 (not stored)
   const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.mask, (uint32_t)a.rows);
   // Contiguous, balanced range of 16-row blocks per wave; the next block's
-  // attention rows are requested before the current block's math.
+  // mask byte is requested before the current block's math.
   const int64_t nblk = (a.rows + 15) / 16;
   const int64_t tw = (int64_t)gridDim.x * MWAVES;
   const int64_t gw = (int64_t)blockIdx.x * MWAVES + wave;
@@ -262,25 +264,18 @@ __global__ __launch_bounds__(MWAVES * 64, 1) void attn_mlp_kernel(const shrimp_m
     const uint32_t off = row < a.rows ? (uint32_t)row : SHRIMP_OOB_OFFSET;
     return (unsigned)__builtin_amdgcn_raw_buffer_load_b8(mr, off, 0, 0);
   };
-  u32x4 cur[MC / 32], nxt[MC / 32];
-  u32x2 sres[MC / 16];
+  u32x4 cur[MC / 32];
   unsigned mcur = 0, mnxt = 0;
-  if (begin < end) {
-    mnxt = load_m(begin * 16 + lr);
-    load_x(a, xr, begin * 16 + lr, lg, nxt);
-    load_s(a, sr, begin * 16 + lr, lg, sres);
-  }
+  if (begin < end) mnxt = load_m(begin * 16 + lr);
   for (int blk = begin; blk < end; ++blk) {
-#pragma unroll
-    for (int ks = 0; ks < MC / 32; ++ks) cur[ks] = nxt[ks];
     mcur = mnxt;
-    // rows past this wave's range read as zeros (offset past the resource)
+    // past this wave's range: an offset past the resource (reads zero)
     const int nrow = blk + 1 < end ? (blk + 1) * 16 + lr : a.rows;
-    // the next block's mask byte ahead of its rows: a wait for it never waits
-    // for them
+    // the next block's mask byte ahead of this block's rows: a wait for it
+    // never waits for them
     mnxt = load_m(nrow);
-    load_x(a, xr, nrow, lg, nxt);
-    mlp_block(a, wl, bias, sr, cur, blk * 16 + lr, lane, sres, nrow, mcur != 0);
+    load_x(a, xr, blk * 16 + lr, lg, cur);
+    mlp_block(a, wl, bias, sr, cur, blk * 16 + lr, lane, mcur != 0);
   }
 }
 
