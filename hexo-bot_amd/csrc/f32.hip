@@ -461,6 +461,224 @@ __global__ __launch_bounds__(AR_THREADS) void attn_rows_kernel(const shrimp_attn
     if (e < d) store_act(o, e, acc[e] * inv);
 }
 
+// fp32 attention at head dim 16 on bf16 MFMA, coords mode (the fp32 serve
+// mode's attention; same semantics as attn_rows_kernel<float, 16, false>).
+// Every fp32 operand x of a product is split as x = hi + lo with hi = bf16(x)
+// and lo = bf16(x - hi), and a product of x and y takes the three MFMAs
+// hi·hi + hi·lo + lo·hi (the lo·lo term is below 2^-16 of the product), with
+// fp32 accumulation: relative error near 2^-16 against fp32 products, well
+// inside the fp32 mode's 1e-4. One workgroup per (position, head), four
+// waves; K and V are staged once in LDS as hi / lo fragments in MFMA order
+// (K fragment of key block kb: lane (lr, lg) holds K[16 kb + lr][4 lg .. + 3];
+// V^T fragment: lane (lr, lg) holds V[16 kb + 4 lg .. + 3][lr]); each wave
+// walks 16-query blocks over 16-key blocks with S^T = K Q^T (scale folded into
+// q), an fp32 online softmax in base 2, and O^T += V^T P^T. The bias comes
+// from an unclamped 53 x 53 copy of the head's LUT table when the position's
+// cells inside the key bound (masked ones too: a masked query row still gets
+// its attention, with its own coordinates) span at most 26 in q and r (one
+// LDS read at key code - query code), else from the clamped table.
+constexpr int A32_XD = 26, A32_XW = 2 * A32_XD + 1;
+
+__host__ __device__ inline size_t attn32_mfma_lds(int S) {
+  const size_t SP = (size_t)((S + 15) & ~15);
+  return SP * (4 * 32 + 4 * 4) + (size_t)(A32_XW * A32_XW + 3) * 4 + 16;
+}
+
+__global__ __launch_bounds__(256) void attn32_mfma_kernel(const shrimp_attn_args a, float qk_scale) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  enum { K_CELL = 0, K_TOKEN = 1, K_DEAD = 2 };
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int lr = lane & 15, lg = lane >> 4;
+  const int S = a.S, H = a.H, nt = a.n_tokens, NC = S - nt;
+  const int SP = (S + 15) & ~15, NKB = SP / 16;
+  int L = a.seq_lens[b];
+  L = L < 0 ? 0 : (L > S ? S : L);
+  const int M = a.lut_m, W = 2 * M + 1;
+
+  u32x2* khi = reinterpret_cast<u32x2*>(smem);
+  u32x2* klo = khi + NKB * 64;
+  u32x2* vhi = klo + NKB * 64;
+  u32x2* vlo = vhi + NKB * 64;
+  int* kq = reinterpret_cast<int*>(vlo + NKB * 64);
+  int* kr = kq + SP;
+  int* kcls = kr + SP;
+  int* kcode = kcls + SP;
+  float* tab = reinterpret_cast<float*>(kcode + SP);  // [XW*XW or W*W] + 3 token biases
+  int* red = reinterpret_cast<int*>(tab + A32_XW * A32_XW + 3);  // qmin, qmax, rmin, rmax
+
+  if (tid < 4) red[tid] = (tid & 1) ? -(1 << 30) : (1 << 30);
+  const float* q = static_cast<const float*>(a.q) + (int64_t)b * a.qkv_sb + (int64_t)h * a.qkv_sh;
+  const float* k = static_cast<const float*>(a.k) + (int64_t)b * a.qkv_sb + (int64_t)h * a.qkv_sh;
+  const float* v = static_cast<const float*>(a.v) + (int64_t)b * a.qkv_sb + (int64_t)h * a.qkv_sh;
+  __syncthreads();
+
+  // ---- keys: class, coordinates, span of the cells inside the bound ----------
+  int qmn = 1 << 30, qmx = -(1 << 30), rmn = 1 << 30, rmx = -(1 << 30);
+  for (int key = tid; key < SP; key += 256) {
+    int cls = K_DEAD, cq = 0, cr = 0;
+    if (key < L) {
+      if (key < nt) {
+        cls = K_TOKEN;
+      } else {
+        const int64_t cell = (int64_t)b * NC + (key - nt);
+        cls = a.mask[cell] ? K_CELL : K_DEAD;
+        cq = a.coords[cell * 2];
+        cr = a.coords[cell * 2 + 1];
+        qmn = min(qmn, cq);
+        qmx = max(qmx, cq);
+        rmn = min(rmn, cr);
+        rmx = max(rmx, cr);
+      }
+    }
+    kcls[key] = cls;
+    kq[key] = cq;
+    kr[key] = cr;
+  }
+  atomicMin(&red[0], qmn);
+  atomicMax(&red[1], qmx);
+  atomicMin(&red[2], rmn);
+  atomicMax(&red[3], rmx);
+
+  // ---- K and V as hi / lo bf16 fragments ---------------------------------------
+  // item (key, g): dims 4 g .. + 3 of one key; keys >= L stage zeros
+  for (int it = tid; it < SP * 4; it += 256) {
+    const int key = it >> 2, g = it & 3;
+    f32x4 kv = f32x4{0.f, 0.f, 0.f, 0.f}, vv = kv;
+    if (key < L) {
+      kv = *reinterpret_cast<const f32x4*>(k + (int64_t)key * a.dpad + 4 * g);
+      vv = *reinterpret_cast<const f32x4*>(v + (int64_t)key * a.dpad + 4 * g);
+    }
+    const int kb = key >> 4, kl = key & 15;
+    u32x2 hi, lo;
+    hi.x = pack_bf16x2(kv[0], kv[1]);
+    hi.y = pack_bf16x2(kv[2], kv[3]);
+    lo.x = pack_bf16x2(kv[0] - bf16_lo(hi.x), kv[1] - bf16_hi(hi.x));
+    lo.y = pack_bf16x2(kv[2] - bf16_lo(hi.y), kv[3] - bf16_hi(hi.y));
+    khi[kb * 64 + g * 16 + kl] = hi;
+    klo[kb * 64 + g * 16 + kl] = lo;
+    // V^T: element (dim 4 g + c, key) -> lane (4 g + c, (key & 15) >> 2), slot key & 3
+    unsigned short* vh16 = reinterpret_cast<unsigned short*>(vhi);
+    unsigned short* vl16 = reinterpret_cast<unsigned short*>(vlo);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int slot = ((kb * 64 + (kl >> 2) * 16 + 4 * g + c) << 2) + (key & 3);
+      const unsigned short hb = f32_to_bf16_bits(vv[c]);
+      vh16[slot] = hb;
+      vl16[slot] = f32_to_bf16_bits(vv[c] - bf16_bits_to_f32(hb));
+    }
+  }
+  __syncthreads();
+
+  // ---- the head's bias table --------------------------------------------------
+  const int q0 = red[0], r0 = red[2];
+  const bool linear = red[0] <= red[1] && red[1] - red[0] <= A32_XD && red[3] - red[2] <= A32_XD;
+  const int W2 = W * W;
+  if (linear) {
+    // T[dq + XD][dr + XD] = btab at the clamped offset (the same value)
+    for (int i = tid; i < A32_XW * A32_XW; i += 256) {
+      const int dq = i / A32_XW - A32_XD, dr = i % A32_XW - A32_XD;
+      const int pos = (min(max(dq, -M), M) + M) * W + (min(max(dr, -M), M) + M);
+      tab[i] = a.btab[(int64_t)pos * H + h];
+    }
+  } else {
+    for (int i = tid; i < W2; i += 256) tab[i] = a.btab[(int64_t)i * H + h];
+  }
+  if (tid < 3) tab[A32_XW * A32_XW + tid] = a.btab[(int64_t)(W2 + tid) * H + h];
+  // cells (masked ones too) at their own offsets; tokens and keys past the
+  // bound at (q0, r0), a valid index (their biases are selected per key)
+  for (int key = tid; key < SP; key += 256) {
+    const bool cell = key >= nt && key < L;
+    kcode[key] = ((cell ? kq[key] : q0) - q0) * A32_XW + ((cell ? kr[key] : r0) - r0);
+  }
+  __syncthreads();
+  const float t_ct = tab[A32_XW * A32_XW], t_tc = tab[A32_XW * A32_XW + 1],
+              t_tt = tab[A32_XW * A32_XW + 2];
+
+  // ---- query blocks -------------------------------------------------------------
+  const int nqb = (L + 15) / 16, nkb = (L + 15) / 16;
+  for (int qb = wave; qb < nqb; qb += 4) {
+    const int query = qb * 16 + lr;
+    const bool qv = query < L, qtok = query < nt;
+    const bool qcell = qv && !qtok;
+    const int qq = qcell ? kq[query] : q0, qr = qcell ? kr[query] : r0;
+    // table index of key j = kcode[j] - qoff
+    const int qoff = (qq - q0) * A32_XW + (qr - r0) - (A32_XD * A32_XW + A32_XD);
+    f32x4 qs = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (qv) qs = *reinterpret_cast<const f32x4*>(q + (int64_t)query * a.dpad + 4 * lg);
+    qs = qs * qk_scale;
+    u32x2 qh, ql;
+    qh.x = pack_bf16x2(qs[0], qs[1]);
+    qh.y = pack_bf16x2(qs[2], qs[3]);
+    ql.x = pack_bf16x2(qs[0] - bf16_lo(qh.x), qs[1] - bf16_hi(qh.x));
+    ql.y = pack_bf16x2(qs[2] - bf16_lo(qh.y), qs[3] - bf16_hi(qh.y));
+    float m = SHRIMP_NEG_BIG_F32, l = 0.f;
+    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < nkb; ++kb) {
+      const int fs = kb * 64 + lg * 16 + lr;
+      f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+      sc = mfma16x16x16(khi[fs], ql, sc);
+      sc = mfma16x16x16(klo[fs], qh, sc);
+      sc = mfma16x16x16(khi[fs], qh, sc);
+      // keys 16 kb + 4 lg + j of query lr
+      const int key0 = kb * 16 + lg * 4;
+      const int4 cl = *reinterpret_cast<const int4*>(kcls + key0);
+      const int clv[4] = {cl.x, cl.y, cl.z, cl.w};
+      float s[4];
+      float mx = SHRIMP_NEG_BIG_F32;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = key0 + j;
+        float bias;
+        if (linear) {
+          bias = tab[kcode[key] - qoff];
+        } else {
+          const int pos = (min(max(kq[key] - qq, -M), M) + M) * W + (min(max(kr[key] - qr, -M), M) + M);
+          bias = tab[pos];
+        }
+        bias = qtok ? t_tc : bias;
+        bias = clv[j] == K_TOKEN ? (qtok ? t_tt : t_ct) : bias;
+        s[j] = clv[j] == K_DEAD ? SHRIMP_NEG_BIG_F32 : sc[j] + bias;
+        mx = fmaxf(mx, s[j]);
+      }
+      mx = max_groups_swap(mx);
+      const float mnew = fmaxf(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+      m = mnew;
+      float p[4], ps = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        p[j] = s[j] > 0.5f * SHRIMP_NEG_BIG_F32 ? __builtin_amdgcn_exp2f(s[j] - mnew) : 0.f;
+        ps += p[j];
+      }
+      l = l * alpha + sum_groups_swap(ps);
+      u32x2 ph, pl;
+      ph.x = pack_bf16x2(p[0], p[1]);
+      ph.y = pack_bf16x2(p[2], p[3]);
+      pl.x = pack_bf16x2(p[0] - bf16_lo(ph.x), p[1] - bf16_hi(ph.x));
+      pl.y = pack_bf16x2(p[2] - bf16_lo(ph.y), p[3] - bf16_hi(ph.y));
+      o = o * alpha;
+      o = mfma16x16x16(vhi[fs], pl, o);
+      o = mfma16x16x16(vlo[fs], ph, o);
+      o = mfma16x16x16(vhi[fs], ph, o);
+    }
+    // lane (lr, lg): dims 4 lg .. + 3 of query lr
+    if (query < S) {
+      const float inv = (qv && l > 0.f) ? 1.0f / l : 0.f;
+      float* op = static_cast<float*>(a.o) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
+                  (int64_t)query * a.o_sr + 4 * lg;
+      *reinterpret_cast<f32x4*>(op) = o * inv;
+    }
+  }
+  // query rows past the live bound (whole blocks) store zeros
+  for (int i = nqb * 16 * 4 + tid; i < S * 4; i += 256) {
+    const int row = i >> 2, g = i & 3;
+    float* op = static_cast<float*>(a.o) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
+                (int64_t)row * a.o_sr + 4 * g;
+    *reinterpret_cast<f32x4*>(op) = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
 template <typename T, bool PAIR>
 static int launch_attn_rows(const shrimp_attn_args* a, int npos, hipStream_t st) {
   const float qk_scale = SHRIMP_LOG2E_F32 / sqrtf((float)a->d);
@@ -714,6 +932,18 @@ extern "C" int shrimp_attn_f32(const shrimp_attn_args* a, void* stream) {
   int npos = 0;
   if (int rc = check_attn_rows(a, 4, &npos)) return rc;
   hipStream_t st = as_stream(stream);
+  // head dim 16 in coords mode: the MFMA kernel (variant 3 keeps the chunked
+  // kernel, for comparison)
+  const auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const size_t lds = attn32_mfma_lds(a->S);
+  if (!a->pair && a->d == 16 && a->dpad == 16 && a->lut_m <= A32_XD && g_attn_variant != 3 &&
+      lds <= (size_t)max_lds_per_block() && al16(a->q) && al16(a->k) && al16(a->v) && al16(a->o) &&
+      a->qkv_sb % 4 == 0 && a->qkv_sh % 4 == 0 && a->o_sb % 4 == 0 && a->o_sh % 4 == 0 &&
+      a->o_sr % 4 == 0) {
+    hipLaunchKernelGGL(attn32_mfma_kernel, dim3(a->H, a->B), dim3(256), lds, st, *a,
+                       SHRIMP_LOG2E_F32 / sqrtf((float)a->d));
+    return check_launch("attn32_mfma");
+  }
   return a->pair ? launch_attn_rows<float, true>(a, npos, st)
                  : launch_attn_rows<float, false>(a, npos, st);
 }

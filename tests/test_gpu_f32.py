@@ -337,20 +337,23 @@ def test_f32_linear_modes(mode, c, h):
 
 @pytest.mark.parametrize("d", [8, 16, 24, 64])
 @pytest.mark.parametrize("S,lens", [(40, [40, 33, 9]), (270, [270, 200, 0])])
-def test_f32_attention_coords(d, S, lens):
+@pytest.mark.parametrize("radius", [20, 12])
+def test_f32_attention_coords(d, S, lens, radius):
     """Coords-mode attention with 8 summary tokens, dead cells and key bounds
     (including an empty position), against the float64 restatement with the
-    reference's pair rows."""
+    reference's pair rows. Coordinates within +-12 keep every position's live
+    span at most 26 (the head-dim-16 kernel's unclamped table), +-20 do not
+    (its clamped table)."""
 
     from shrimp import _lib, ops
     from shrimp.constants import BIAS_ROWS
     from shrimp.geometry import CELL_LUT_M, cell_bias_lut
 
-    torch.manual_seed(d + S)
+    torch.manual_seed(d + S + radius)
     B, H, nt = len(lens), 3, 8
     N = S - nt
     q, k, v = (torch.randn(B, H, S, d, dtype=torch.float64) for _ in range(3))
-    coords = torch.randint(-20, 21, (B, N, 2), dtype=torch.int32)
+    coords = torch.randint(-radius, radius + 1, (B, N, 2), dtype=torch.int32)
     mask = torch.rand(B, N) > 0.2
     table = torch.randn(BIAS_ROWS, H) * 0.5
     lut = torch.from_numpy(cell_bias_lut()).to(DEV)
@@ -376,6 +379,46 @@ def test_f32_attention_coords(d, S, lens):
     rows = torch.arange(S)[None, :] < seq_lens[:, None].long()
     want = torch.where(rows[:, None, :, None], want, torch.zeros_like(want))
     rel_close(out.cpu(), want, f"fp32 attention d={d} S={S}")
+
+
+@pytest.mark.parametrize("radius", [20, 12])
+def test_f32_attention_mfma_matches_chunked(radius):
+    """At head dim 16 (coords mode) shrimp_attn_f32 runs the MFMA kernel; the
+    chunked kernel (attention variant 3) on the same inputs agrees to the fp32
+    tolerance, at the forward's shape (S = 264, 8 heads)."""
+
+    from shrimp import _lib, ops
+    from shrimp.constants import BIAS_ROWS
+    from shrimp.geometry import CELL_LUT_M, cell_bias_lut
+
+    torch.manual_seed(radius)
+    B, H, S, d, nt = 6, 8, 264, 16, 8
+    N = S - nt
+    f = lambda t: t.to(DEV, torch.float32).contiguous()
+    q, k, v = (f(torch.randn(B, H, S, d)) for _ in range(3))
+    coords = torch.randint(-radius, radius + 1, (B, N, 2), dtype=torch.int32).to(DEV).contiguous()
+    mask = (torch.rand(B, N) > 0.1).to(DEV, torch.uint8)
+    table = torch.randn(BIAS_ROWS, H) * 0.5
+    lut = torch.from_numpy(cell_bias_lut()).to(DEV)
+    btab, _ = ops.attn_bias_table(table.to(DEV), lut, CELL_LUT_M)
+    sd = torch.tensor([264, 200, 137, 16, 9, 0], dtype=torch.int32, device=DEV)
+    lib = _lib.load()
+    outs = []
+    for variant in (0, 3):
+        out = torch.full((B, S, H * d), 7.0, device=DEV)
+        a = _lib.AttnArgs(q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), qkv_sb=H * S * d,
+                          qkv_sh=S * d, seq_lens=sd.data_ptr(), coords=coords.data_ptr(),
+                          mask=mask.data_ptr(), btab=btab.data_ptr(), lut_m=CELL_LUT_M,
+                          n_tokens=nt, o=out.data_ptr(), o_sb=S * H * d, o_sh=d, o_sr=H * d,
+                          B=B, S=S, H=H, d=d, dpad=d)
+        prev = lib.shrimp_attn_variant(variant)
+        try:
+            _lib.check(lib.shrimp_attn_f32(ctypes.byref(a), _lib.stream_handle()), "attn_f32")
+            torch.cuda.synchronize()
+        finally:
+            lib.shrimp_attn_variant(prev)
+        outs.append(out.cpu())
+    rel_close(outs[0], outs[1], f"fp32 attention MFMA vs chunked, coords +-{radius}")
 
 
 def test_f32_attention_pair_mode():
