@@ -481,7 +481,7 @@ constexpr int A32_XD = 26, A32_XW = 2 * A32_XD + 1;
 
 __host__ __device__ inline size_t attn32_mfma_lds(int S) {
   const size_t SP = (size_t)((S + 15) & ~15);
-  return SP * (4 * 32 + 4 * 4) + (size_t)(A32_XW * A32_XW + 3) * 4 + 16;
+  return SP * (4 * 32 + 4 * 4) + (size_t)(A32_XW * A32_XW + 3) * 4 + 16 + (SP / 16) * 4;
 }
 
 __global__ __launch_bounds__(256) void attn32_mfma_kernel(const shrimp_attn_args a, float qk_scale) {
@@ -506,6 +506,7 @@ __global__ __launch_bounds__(256) void attn32_mfma_kernel(const shrimp_attn_args
   int* kcode = kcls + SP;
   float* tab = reinterpret_cast<float*>(kcode + SP);  // [XW*XW or W*W] + 3 token biases
   int* red = reinterpret_cast<int*>(tab + A32_XW * A32_XW + 3);  // qmin, qmax, rmin, rmax
+  int* bspec = red + 4;  // [NKB]: key block holds a token or a dead key
 
   if (tid < 4) red[tid] = (tid & 1) ? -(1 << 30) : (1 << 30);
   const float* q = static_cast<const float*>(a.q) + (int64_t)b * a.qkv_sb + (int64_t)h * a.qkv_sh;
@@ -591,6 +592,11 @@ __global__ __launch_bounds__(256) void attn32_mfma_kernel(const shrimp_attn_args
     const bool cell = key >= nt && key < L;
     kcode[key] = ((cell ? kq[key] : q0) - q0) * A32_XW + ((cell ? kr[key] : r0) - r0);
   }
+  for (int kb = tid; kb < NKB; kb += 256) {
+    int sp = 0;
+    for (int j = 0; j < 16; ++j) sp |= kcls[kb * 16 + j] != K_CELL;
+    bspec[kb] = sp;
+  }
   __syncthreads();
   const float t_ct = tab[A32_XW * A32_XW], t_tc = tab[A32_XW * A32_XW + 1],
               t_tt = tab[A32_XW * A32_XW + 2];
@@ -600,6 +606,7 @@ __global__ __launch_bounds__(256) void attn32_mfma_kernel(const shrimp_attn_args
   for (int qb = wave; qb < nqb; qb += 4) {
     const int query = qb * 16 + lr;
     const bool qv = query < L, qtok = query < nt;
+    const bool qtokb = qb * 16 < nt;  // the block holds token queries (wave-uniform)
     const bool qcell = qv && !qtok;
     const int qq = qcell ? kq[query] : q0, qr = qcell ? kr[query] : r0;
     // table index of key j = kcode[j] - qoff
@@ -622,24 +629,35 @@ __global__ __launch_bounds__(256) void attn32_mfma_kernel(const shrimp_attn_args
       sc = mfma16x16x16(khi[fs], qh, sc);
       // keys 16 kb + 4 lg + j of query lr
       const int key0 = kb * 16 + lg * 4;
-      const int4 cl = *reinterpret_cast<const int4*>(kcls + key0);
-      const int clv[4] = {cl.x, cl.y, cl.z, cl.w};
       float s[4];
       float mx = SHRIMP_NEG_BIG_F32;
+      if (linear && !qtokb && !bspec[kb]) {
+        // cell queries, cell keys only (wave-uniform): one table read per key
+        const int4 kc = *reinterpret_cast<const int4*>(kcode + key0);
+        const int kcv[4] = {kc.x, kc.y, kc.z, kc.w};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = key0 + j;
-        float bias;
-        if (linear) {
-          bias = tab[kcode[key] - qoff];
-        } else {
-          const int pos = (min(max(kq[key] - qq, -M), M) + M) * W + (min(max(kr[key] - qr, -M), M) + M);
-          bias = tab[pos];
+        for (int j = 0; j < 4; ++j) {
+          s[j] = sc[j] + tab[kcv[j] - qoff];
+          mx = fmaxf(mx, s[j]);
         }
-        bias = qtok ? t_tc : bias;
-        bias = clv[j] == K_TOKEN ? (qtok ? t_tt : t_ct) : bias;
-        s[j] = clv[j] == K_DEAD ? SHRIMP_NEG_BIG_F32 : sc[j] + bias;
-        mx = fmaxf(mx, s[j]);
+      } else {
+        const int4 cl = *reinterpret_cast<const int4*>(kcls + key0);
+        const int clv[4] = {cl.x, cl.y, cl.z, cl.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = key0 + j;
+          float bias;
+          if (linear) {
+            bias = tab[kcode[key] - qoff];
+          } else {
+            const int pos = (min(max(kq[key] - qq, -M), M) + M) * W + (min(max(kr[key] - qr, -M), M) + M);
+            bias = tab[pos];
+          }
+          bias = qtok ? t_tc : bias;
+          bias = clv[j] == K_TOKEN ? (qtok ? t_tt : t_ct) : bias;
+          s[j] = clv[j] == K_DEAD ? SHRIMP_NEG_BIG_F32 : sc[j] + bias;
+          mx = fmaxf(mx, s[j]);
+        }
       }
       mx = max_groups_swap(mx);
       const float mnew = fmaxf(m, mx);
