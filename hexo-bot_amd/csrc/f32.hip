@@ -467,7 +467,7 @@ __global__ __launch_bounds__(AR_THREADS) void attn_rows_kernel(const shrimp_attn
 // and lo = bf16(x - hi), and a product of x and y takes the three MFMAs
 // hi·hi + hi·lo + lo·hi (the lo·lo term is below 2^-16 of the product), with
 // fp32 accumulation: relative error near 2^-16 against fp32 products, well
-// inside the fp32 mode's 1e-4. One workgroup per (position, head), four
+// inside the fp32 mode's 1e-4. One workgroup per (position, head), eight
 // waves; K and V are staged once in LDS as hi / lo fragments in MFMA order
 // (K fragment of key block kb: lane (lr, lg) holds K[16 kb + lr][4 lg .. + 3];
 // V^T fragment: lane (lr, lg) holds V[16 kb + 4 lg .. + 3][lr]); each wave
@@ -478,13 +478,15 @@ __global__ __launch_bounds__(AR_THREADS) void attn_rows_kernel(const shrimp_attn
 // its attention, with its own coordinates) span at most 26 in q and r (one
 // LDS read at key code - query code), else from the clamped table.
 constexpr int A32_XD = 26, A32_XW = 2 * A32_XD + 1;
+constexpr int A32_NW = 8;  // waves per workgroup
 
 __host__ __device__ inline size_t attn32_mfma_lds(int S) {
   const size_t SP = (size_t)((S + 15) & ~15);
   return SP * (4 * 32 + 4 * 4) + (size_t)(A32_XW * A32_XW + 3) * 4 + 16 + (SP / 16) * 4;
 }
 
-__global__ __launch_bounds__(256) void attn32_mfma_kernel(const shrimp_attn_args a, float qk_scale) {
+__global__ __launch_bounds__(A32_NW * 64) void attn32_mfma_kernel(const shrimp_attn_args a, float qk_scale) {
+  constexpr int NT = A32_NW * 64;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   enum { K_CELL = 0, K_TOKEN = 1, K_DEAD = 2 };
   const int h = blockIdx.x, b = blockIdx.y;
@@ -516,7 +518,7 @@ __global__ __launch_bounds__(256) void attn32_mfma_kernel(const shrimp_attn_args
 
   // ---- keys: class, coordinates, span of the cells inside the bound ----------
   int qmn = 1 << 30, qmx = -(1 << 30), rmn = 1 << 30, rmx = -(1 << 30);
-  for (int key = tid; key < SP; key += 256) {
+  for (int key = tid; key < SP; key += NT) {
     int cls = K_DEAD, cq = 0, cr = 0;
     if (key < L) {
       if (key < nt) {
@@ -543,7 +545,7 @@ __global__ __launch_bounds__(256) void attn32_mfma_kernel(const shrimp_attn_args
 
   // ---- K and V as hi / lo bf16 fragments ---------------------------------------
   // item (key, g): dims 4 g .. + 3 of one key; keys >= L stage zeros
-  for (int it = tid; it < SP * 4; it += 256) {
+  for (int it = tid; it < SP * 4; it += NT) {
     const int key = it >> 2, g = it & 3;
     f32x4 kv = f32x4{0.f, 0.f, 0.f, 0.f}, vv = kv;
     if (key < L) {
@@ -577,22 +579,22 @@ __global__ __launch_bounds__(256) void attn32_mfma_kernel(const shrimp_attn_args
   const int W2 = W * W;
   if (linear) {
     // T[dq + XD][dr + XD] = btab at the clamped offset (the same value)
-    for (int i = tid; i < A32_XW * A32_XW; i += 256) {
+    for (int i = tid; i < A32_XW * A32_XW; i += NT) {
       const int dq = i / A32_XW - A32_XD, dr = i % A32_XW - A32_XD;
       const int pos = (min(max(dq, -M), M) + M) * W + (min(max(dr, -M), M) + M);
       tab[i] = a.btab[(int64_t)pos * H + h];
     }
   } else {
-    for (int i = tid; i < W2; i += 256) tab[i] = a.btab[(int64_t)i * H + h];
+    for (int i = tid; i < W2; i += NT) tab[i] = a.btab[(int64_t)i * H + h];
   }
   if (tid < 3) tab[A32_XW * A32_XW + tid] = a.btab[(int64_t)(W2 + tid) * H + h];
   // cells (masked ones too) at their own offsets; tokens and keys past the
   // bound at (q0, r0), a valid index (their biases are selected per key)
-  for (int key = tid; key < SP; key += 256) {
+  for (int key = tid; key < SP; key += NT) {
     const bool cell = key >= nt && key < L;
     kcode[key] = ((cell ? kq[key] : q0) - q0) * A32_XW + ((cell ? kr[key] : r0) - r0);
   }
-  for (int kb = tid; kb < NKB; kb += 256) {
+  for (int kb = tid; kb < NKB; kb += NT) {
     int sp = 0;
     for (int j = 0; j < 16; ++j) sp |= kcls[kb * 16 + j] != K_CELL;
     bspec[kb] = sp;
@@ -603,7 +605,7 @@ __global__ __launch_bounds__(256) void attn32_mfma_kernel(const shrimp_attn_args
 
   // ---- query blocks -------------------------------------------------------------
   const int nqb = (L + 15) / 16, nkb = (L + 15) / 16;
-  for (int qb = wave; qb < nqb; qb += 4) {
+  for (int qb = wave; qb < nqb; qb += A32_NW) {
     const int query = qb * 16 + lr;
     const bool qv = query < L, qtok = query < nt;
     const bool qtokb = qb * 16 < nt;  // the block holds token queries (wave-uniform)
@@ -689,7 +691,7 @@ __global__ __launch_bounds__(256) void attn32_mfma_kernel(const shrimp_attn_args
     }
   }
   // query rows past the live bound (whole blocks) store zeros
-  for (int i = nqb * 16 * 4 + tid; i < S * 4; i += 256) {
+  for (int i = nqb * 16 * 4 + tid; i < S * 4; i += NT) {
     const int row = i >> 2, g = i & 3;
     float* op = static_cast<float*>(a.o) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
                 (int64_t)row * a.o_sr + 4 * g;
@@ -958,7 +960,7 @@ extern "C" int shrimp_attn_f32(const shrimp_attn_args* a, void* stream) {
       lds <= (size_t)max_lds_per_block() && al16(a->q) && al16(a->k) && al16(a->v) && al16(a->o) &&
       a->qkv_sb % 4 == 0 && a->qkv_sh % 4 == 0 && a->o_sb % 4 == 0 && a->o_sh % 4 == 0 &&
       a->o_sr % 4 == 0) {
-    hipLaunchKernelGGL(attn32_mfma_kernel, dim3(a->H, a->B), dim3(256), lds, st, *a,
+    hipLaunchKernelGGL(attn32_mfma_kernel, dim3(a->H, a->B), dim3(A32_NW * 64), lds, st, *a,
                        SHRIMP_LOG2E_F32 / sqrtf((float)a->d));
     return check_launch("attn32_mfma");
   }
