@@ -633,7 +633,8 @@ __global__ __launch_bounds__(A32_NW * 64) void attn32_mfma_kernel(const shrimp_a
       const int key0 = kb * 16 + lg * 4;
       float s[4];
       float mx = SHRIMP_NEG_BIG_F32;
-      if (linear && !qtokb && !bspec[kb]) {
+      const bool plain = linear && !qtokb && !bspec[kb];
+      if (plain) {
         // cell queries, cell keys only (wave-uniform): one table read per key
         const int4 kc = *reinterpret_cast<const int4*>(kcode + key0);
         const int kcv[4] = {kc.x, kc.y, kc.z, kc.w};
@@ -641,6 +642,31 @@ __global__ __launch_bounds__(A32_NW * 64) void attn32_mfma_kernel(const shrimp_a
         for (int j = 0; j < 4; ++j) {
           s[j] = sc[j] + tab[kcv[j] - qoff];
           mx = fmaxf(mx, s[j]);
+        }
+        // Once every query of the block has an offset m, the tile keeps it:
+        // p = exp2(s - m) needs no maximum, no rescale and no lane exchange
+        // (any fixed offset gives the same softmax; the row sums only have to
+        // stay finite and in range, else the tile takes the maximum path).
+        if (__builtin_amdgcn_ballot_w64(!(m > 0.5f * SHRIMP_NEG_BIG_F32)) == 0) {
+          float p[4], ps = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            p[j] = __builtin_amdgcn_exp2f(s[j] - m);
+            ps += p[j];
+          }
+          const float tot = sum_groups_swap(ps);
+          if (__builtin_amdgcn_ballot_w64(!(tot < 0x1p64f)) == 0) {
+            l += tot;
+            u32x2 ph, pl;
+            ph.x = pack_bf16x2(p[0], p[1]);
+            ph.y = pack_bf16x2(p[2], p[3]);
+            pl.x = pack_bf16x2(p[0] - bf16_lo(ph.x), p[1] - bf16_hi(ph.x));
+            pl.y = pack_bf16x2(p[2] - bf16_lo(ph.y), p[3] - bf16_hi(ph.y));
+            o = mfma16x16x16(vhi[fs], pl, o);
+            o = mfma16x16x16(vlo[fs], ph, o);
+            o = mfma16x16x16(vhi[fs], ph, o);
+            continue;
+          }
         }
       } else {
         const int4 cl = *reinterpret_cast<const int4*>(kcls + key0);
