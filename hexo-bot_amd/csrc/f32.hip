@@ -16,6 +16,8 @@
 //    input channels: lane group lg loads channels 4 lg .. +3 of its row as
 //    one 16-byte load, and MFMA step s (0..3) of the chunk takes channel
 //    4 lg + s as k slot lg. Weights are packed to match (16-byte fragments).
+//  * attn32_mfma_kernel: the fp32 attention at head dim 16 (coords mode) on
+//    bf16 MFMA with hi / lo operand splitting (see the kernel);
 //  * attn_rows_kernel: softmax(q k^T / sqrt(d) + bias) v with one query row
 //    per thread and keys streamed through LDS in chunks, so any sequence
 //    length fits (the fused bf16 kernel stages the whole sequence). fp32

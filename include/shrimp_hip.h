@@ -638,8 +638,13 @@ int shrimp_conv_ln_raytap(const shrimp_raytap_args* a, void* stream);
  *   - shrimp_linear_f32: in / out features multiples of 16; QKV mode writes
  *     (3, B, H, S, dpad) fp32 with dpad >= d, dpad % 4 == 0;
  *   - shrimp_attn_f32: q, k, v (B, H, S, dpad) fp32, d <= 64, any S; pair or
- *     coords bias as shrimp_attn (btab and table2 fp32; xtab unused); one
- *     query row per thread with keys streamed through LDS;
+ *     coords bias as shrimp_attn (btab and table2 fp32; xtab unused). At
+ *     d = dpad = 16 in coords mode (lut_m <= 26, 16-byte aligned q/k/v/o,
+ *     strides multiples of 4, the sequence within one workgroup's LDS) it runs
+ *     on bf16 MFMA with each fp32 operand split into hi and lo bf16 parts
+ *     (three products per tile, fp32 accumulation and softmax); otherwise,
+ *     and at attention variant 3, one query row per thread with keys streamed
+ *     through LDS;
  *   - shrimp_trunk_tail_f32: seq and out_seq fp32;
  *   - shrimp_prep_feats_f32 / shrimp_prep_csr_feats_f32: the stem input
  *     xin (B, N, 16) fp32 (features zero-padded to 16 channels) from padded
