@@ -79,7 +79,14 @@ struct Gemm32 {
 
 // One wave: MB x 16 rows by NB x 16 outputs (blockIdx.y selects the output
 // blocks); four waves per workgroup.
-template <int NB, int MB, int F>
+// X3 (kin a multiple of 32): the products on bf16 MFMA with each fp32 operand
+// split as x = hi + lo (hi = bf16(x), lo = bf16(x - hi)), a 16 x 16 x 32 tile
+// taken as hi·lo + lo·hi + hi·hi (the lo·lo term is below 2^-16 of the
+// product): relative error near 2^-16 per product against fp32 products, at
+// 16x the fp32 MFMA rate. The weights come packed as hi / lo fragments
+// (pack_w32x3_kernel); x is split as it is loaded, lane group lg taking
+// channels 8 lg .. + 7 of each 32-channel chunk.
+template <int NB, int MB, int F, bool X3>
 __global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
   constexpr bool GATHER = (F & G_GATHER) != 0, PLN = (F & G_PLN) != 0;
   constexpr bool LN = (F & G_LN) != 0, RELU = (F & G_RELU) != 0, MASK = (F & G_MASK) != 0;
@@ -148,8 +155,51 @@ __global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
       if (GATHER) j = rv[mb] ? g.idx[((int64_t)rb[mb] * g.N + rn[mb]) * g.idx_stride + t] : -1;
       const bool ok = rv[mb] && j >= 0 && j < g.N;
       xoff[mb] = ok ? (uint32_t)(((int64_t)rb[mb] * g.x_sb + (int64_t)j * g.x_sr) * 4) +
-                          (uint32_t)(lg * 16)
+                          (uint32_t)(lg * (X3 ? 32 : 16))
                     : SHRIMP_OOB_OFFSET;
+    }
+    if constexpr (X3) {
+      const u32x4* wq = reinterpret_cast<const u32x4*>(g.w);
+      const int KC2 = g.kin / 32;
+      for (int kc = 0; kc < KC2; ++kc) {
+        u32x4 xh[MB], xl[MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const f32x4 v0 = as_f32x4(buf_load16(xr, xoff[mb] + kc * 128));
+          const f32x4 v1 = as_f32x4(buf_load16(xr, xoff[mb] + kc * 128 + 16));
+          float x[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+          if constexpr (PLN) {
+            const int c = kc * 32 + lg * 8;
+            const f32x4 lw0 = *reinterpret_cast<const f32x4*>(g.ln_w + c);
+            const f32x4 lw1 = *reinterpret_cast<const f32x4*>(g.ln_w + c + 4);
+            const f32x4 lb0 = *reinterpret_cast<const f32x4*>(g.ln_b + c);
+            const f32x4 lb1 = *reinterpret_cast<const f32x4*>(g.ln_b + c + 4);
+            const float lw[8] = {lw0[0], lw0[1], lw0[2], lw0[3], lw1[0], lw1[1], lw1[2], lw1[3]};
+            const float lb[8] = {lb0[0], lb0[1], lb0[2], lb0[3], lb1[0], lb1[1], lb1[2], lb1[3]};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = fmaf((x[e] - pmean[mb]) * prstd[mb], lw[e], lb[e]);
+          }
+#pragma unroll
+          for (int w2 = 0; w2 < 4; ++w2) {
+            const unsigned hw = pack_bf16x2(x[2 * w2], x[2 * w2 + 1]);
+            xh[mb][w2] = hw;
+            xl[mb][w2] = pack_bf16x2(x[2 * w2] - bf16_lo(hw), x[2 * w2 + 1] - bf16_hi(hw));
+          }
+        }
+        const int64_t kb = ((int64_t)t * KC2 + kc) * NBT;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const u32x4 wh = wq[((kb + nb0 + nb) * 2) * 64 + lane];
+          const u32x4 wl = wq[((kb + nb0 + nb) * 2 + 1) * 64 + lane];
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) {
+            acc[nb][mb] = mfma16x16x32(wh, xl[mb], acc[nb][mb]);
+            acc[nb][mb] = mfma16x16x32(wl, xh[mb], acc[nb][mb]);
+            acc[nb][mb] = mfma16x16x32(wh, xh[mb], acc[nb][mb]);
+          }
+        }
+      }
+      continue;
     }
     for (int kc = 0; kc < KC; ++kc) {
       f32x4 bx[MB];
@@ -289,13 +339,59 @@ __global__ void pack_w32_kernel(const float* __restrict__ w, float* __restrict__
   packed[i] = c < kin_real ? w[(int64_t)t * st + (int64_t)c * sk + (int64_t)n * sn] : 0.f;
 }
 
+// The same weights for the X3 path (kin a multiple of 32), in the bytes of the
+// fp32 layout: per (32-row k-chunk kc, output block nb) a 1 KiB hi fragment
+// and a 1 KiB lo fragment, lane (lr, lg) holding W[32 kc + 8 lg + e][16 nb +
+// lr], e < 8, as bf16 (hi = bf16(w), lo = bf16(w - hi)).
+__global__ void pack_w32x3_kernel(const float* __restrict__ w, unsigned short* __restrict__ packed,
+                                  int taps, int kin_real, int kin, int cout, int64_t st, int64_t sk,
+                                  int64_t sn) {
+  const int64_t total = (int64_t)taps * kin * cout;  // weights; each one a hi and a lo element
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int e = (int)(i & 7);
+  const int lane = (int)((i >> 3) & 63);
+  const int64_t frag = i >> 9;  // (t, kc, nb)
+  const int NBT = cout / 16;
+  const int nb = (int)(frag % NBT);
+  const int64_t kcg = frag / NBT;
+  const int kcpt = kin / 32;
+  const int t = (int)(kcg / kcpt);
+  const int c = (int)(kcg - (int64_t)t * kcpt) * 32 + (lane >> 4) * 8 + e;
+  const int n = nb * 16 + (lane & 15);
+  const float v = c < kin_real ? w[(int64_t)t * st + (int64_t)c * sk + (int64_t)n * sn] : 0.f;
+  const unsigned short hi = f32_to_bf16_bits(v);
+  const unsigned short lo = f32_to_bf16_bits(v - bf16_bits_to_f32(hi));
+  packed[frag * 1024 + lane * 8 + e] = hi;
+  packed[frag * 1024 + 512 + lane * 8 + e] = lo;
+}
+
 template <int NB, int MB, int F>
 static int launch_gemm32(const Gemm32& g, hipStream_t st) {
   const int64_t R = (int64_t)g.B * g.N;
   const int64_t per = 4 * MB * 16;
   dim3 grid((unsigned)((R + per - 1) / per), (unsigned)(g.cout / 16 / NB));
-  hipLaunchKernelGGL((gemm32_kernel<NB, MB, F>), grid, dim3(256), 0, st, g);
+  if (g.kin % 32 == 0)
+    hipLaunchKernelGGL((gemm32_kernel<NB, MB, F, true>), grid, dim3(256), 0, st, g);
+  else
+    hipLaunchKernelGGL((gemm32_kernel<NB, MB, F, false>), grid, dim3(256), 0, st, g);
   return check_launch("gemm32");
+}
+
+// Packs into the layout the kernel reads for this kin: hi / lo bf16
+// fragments when kin is a multiple of 32, fp32 fragments otherwise.
+static int pack_w32(const float* w, float* packed, int taps, int kin_real, int kin, int cout,
+                    int64_t st, int64_t sk, int64_t sn, hipStream_t stream) {
+  const int64_t total = (int64_t)taps * kin * cout;
+  const dim3 grid((unsigned)((total + 255) / 256));
+  if (kin % 32 == 0)
+    hipLaunchKernelGGL(pack_w32x3_kernel, grid, dim3(256), 0, stream, w,
+                       reinterpret_cast<unsigned short*>(packed), taps, kin_real, kin, cout, st, sk,
+                       sn);
+  else
+    hipLaunchKernelGGL(pack_w32_kernel, grid, dim3(256), 0, stream, w, packed, taps, kin_real,
+                       kin, cout, st, sk, sn);
+  return SHRIMP_OK;
 }
 
 // Every output block in one wave (LayerNorm, head epilogues): NB = cout / 16.
@@ -827,10 +923,8 @@ extern "C" int shrimp_pack_conv_weight_f32(const float* w, float* packed, int ta
   SHRIMP_REQUIRE(taps > 0 && cin > 0 && cin <= cin_pad && cin_pad % 16 == 0,
                  "pack_conv_weight_f32: bad taps/cin (%d, %d, %d)", taps, cin, cin_pad);
   SHRIMP_REQUIRE(cout > 0 && cout % 16 == 0, "pack_conv_weight_f32: cout %d", cout);
-  const int64_t total = (int64_t)taps * cin_pad * cout;
-  hipLaunchKernelGGL(pack_w32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     as_stream(stream), w, packed, taps, cin, cin_pad, cout, (int64_t)cin * cout,
-                     (int64_t)cout, (int64_t)1);
+  pack_w32(w, packed, taps, cin, cin_pad, cout, (int64_t)cin * cout, (int64_t)cout, (int64_t)1,
+           as_stream(stream));
   return check_launch("pack_conv_weight_f32");
 }
 
@@ -841,10 +935,8 @@ extern "C" int shrimp_pack_linear_weight_f32(const float* w, float* packed, int 
                      out_features % 16 == 0,
                  "pack_linear_weight_f32: shape (%d -> %d) needs multiples of 16", in_features,
                  out_features);
-  const int64_t total = (int64_t)in_features * out_features;
-  hipLaunchKernelGGL(pack_w32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     as_stream(stream), w, packed, 1, in_features, in_features, out_features,
-                     (int64_t)0, (int64_t)1, (int64_t)in_features);
+  pack_w32(w, packed, 1, in_features, in_features, out_features, (int64_t)0, (int64_t)1,
+           (int64_t)in_features, as_stream(stream));
   return check_launch("pack_linear_weight_f32");
 }
 

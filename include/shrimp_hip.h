@@ -628,11 +628,17 @@ int shrimp_conv_ln_raytap(const shrimp_raytap_args* a, void* stream);
  * fp32). Same argument structs and semantics as the bf16 entry points above,
  * with these differences:
  *   - activations (x, resid, out, seq, out_seq, q, k, v, o) are fp32;
- *   - weights are packed by the *_f32 packers: 16-byte fp32 fragments, for
- *     k-chunk kc (16 rows of K) and output block nb (16 outputs), lane l
- *     holding W[16 kc + 4 (l / 16) + j][16 nb + l % 16], j < 4; conv weights
- *     with K = taps * cin_pad (cin_pad a multiple of 16), linear weights with
- *     K = in_features;
+ *   - weights are packed by the *_f32 packers into 4 bytes per weight, in
+ *     one of two layouts chosen by the per-tap input width kin (cin_pad for
+ *     conv weights, tap-major; in_features for linear weights). kin a
+ *     multiple of 32: per tap, k-chunk kc (32 rows) and output block nb (16
+ *     outputs) a 1 KiB hi fragment then a 1 KiB lo fragment, lane l holding
+ *     8 bf16 of W[32 kc + 8 (l / 16) + e][16 nb + l % 16] (hi = bf16(w), lo =
+ *     bf16(w - hi)); the GEMMs then run on bf16 MFMA with x split the same
+ *     way, three products per tile (hi·lo + lo·hi + hi·hi, fp32
+ *     accumulation). Otherwise (kin 16): per tap, kc (16 rows) and nb,
+ *     16-byte fp32 fragments, lane l holding W[16 kc + 4 (l / 16) + j][16 nb
+ *     + l % 16], j < 4, for fp32 MFMA;
  *   - shrimp_hex_conv_f32: cin_pad and cout multiples of 16; LayerNorm and
  *     head epilogues need cout in {32, 64, 96, 128, 192, 256};
  *   - shrimp_linear_f32: in / out features multiples of 16; QKV mode writes
