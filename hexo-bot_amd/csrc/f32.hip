@@ -162,6 +162,16 @@ __global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
       const u32x4* wq = reinterpret_cast<const u32x4*>(g.w);
       const int KC2 = g.kin / 32;
       for (int kc = 0; kc < KC2; ++kc) {
+        // All of this chunk's weight fragments are requested before x is
+        // split, so one L2 round trip covers the chunk.
+        const int64_t kb = ((int64_t)t * KC2 + kc) * NBT;
+        u32x4 wh[NB], wl[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          wh[nb] = wq[((kb + nb0 + nb) * 2) * 64 + lane];
+          wl[nb] = wq[((kb + nb0 + nb) * 2 + 1) * 64 + lane];
+        }
+        __builtin_amdgcn_sched_barrier(0);
         u32x4 xh[MB], xl[MB];
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
@@ -186,16 +196,13 @@ __global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
             xl[mb][w2] = pack_bf16x2(x[2 * w2] - bf16_lo(hw), x[2 * w2 + 1] - bf16_hi(hw));
           }
         }
-        const int64_t kb = ((int64_t)t * KC2 + kc) * NBT;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-          const u32x4 wh = wq[((kb + nb0 + nb) * 2) * 64 + lane];
-          const u32x4 wl = wq[((kb + nb0 + nb) * 2 + 1) * 64 + lane];
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb) {
-            acc[nb][mb] = mfma16x16x32(wh, xl[mb], acc[nb][mb]);
-            acc[nb][mb] = mfma16x16x32(wl, xh[mb], acc[nb][mb]);
-            acc[nb][mb] = mfma16x16x32(wh, xh[mb], acc[nb][mb]);
+            acc[nb][mb] = mfma16x16x32(wh[nb], xl[mb], acc[nb][mb]);
+            acc[nb][mb] = mfma16x16x32(wl[nb], xh[mb], acc[nb][mb]);
+            acc[nb][mb] = mfma16x16x32(wh[nb], xh[mb], acc[nb][mb]);
           }
         }
       }
