@@ -98,7 +98,9 @@ __global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
   const int lg = lane >> 4;
   const int64_t R = (int64_t)g.B * g.N;
   const int64_t row_base = ((int64_t)blockIdx.x * 4 + wave) * (MB * 16);
-  if (row_base >= R) return;
+  // X3 waves share weight fragments through LDS with a barrier per chunk, so
+  // a wave past the last row stays until the K loop ends.
+  if (!X3 && row_base >= R) return;
   const int nb0 = blockIdx.y * NB;
   const int NBT = g.cout / 16;
   const int KC = g.kin / 16;
@@ -146,6 +148,35 @@ __global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
     for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int T = GATHER ? g.taps : 1;
+  // X3: a chunk's NB hi / lo fragment pairs (NB x 2 KiB, contiguous in the
+  // packed weights) are loaded once per workgroup, 16 bytes per thread at a
+  // time, into one of two LDS buffers; the waves read their lane's fragments
+  // from there.
+  constexpr int SPT = X3 ? (NB * 128 + 255) / 256 : 1;  // staging loads per thread
+  __shared__ u32x4 wsh[X3 ? 2 : 1][X3 ? NB * 128 : 1];
+  u32x4 stg[SPT];
+  const int NC = X3 ? T * (g.kin / 32) : 0;
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(g.w, X3 ? (uint32_t)((int64_t)NC * NBT * 2048) : 0u);
+  auto stage_load = [&](int c) {
+    const uint32_t base = (uint32_t)(c * NBT + nb0) * 2048u;
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const int i = threadIdx.x + k * 256;
+      if (NB * 128 % 256 == 0 || i < NB * 128) stg[k] = buf_load16(wr, base + (uint32_t)i * 16u);
+    }
+  };
+  auto stage_store = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const int i = threadIdx.x + k * 256;
+      if (NB * 128 % 256 == 0 || i < NB * 128) wsh[buf][i] = stg[k];
+    }
+  };
+  if constexpr (X3) {
+    stage_load(0);
+    stage_store(0);
+    __syncthreads();
+  }
   const f32x4* wp = reinterpret_cast<const f32x4*>(g.w);
   for (int t = 0; t < T; ++t) {
     uint32_t xoff[MB];
@@ -159,31 +190,36 @@ __global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
                     : SHRIMP_OOB_OFFSET;
     }
     if constexpr (X3) {
-      const u32x4* wq = reinterpret_cast<const u32x4*>(g.w);
       const int KC2 = g.kin / 32;
       for (int kc = 0; kc < KC2; ++kc) {
-        // All of this chunk's weight fragments are requested before x is
-        // split, so one L2 round trip covers the chunk.
-        const int64_t kb = ((int64_t)t * KC2 + kc) * NBT;
+        const int c = t * KC2 + kc;
+        // This chunk's rows first, then the next chunk's fragments into the
+        // staging registers, so the wait for the rows leaves those in flight.
+        f32x4 xv[MB][2];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          xv[mb][0] = as_f32x4(buf_load16(xr, xoff[mb] + kc * 128));
+          xv[mb][1] = as_f32x4(buf_load16(xr, xoff[mb] + kc * 128 + 16));
+        }
+        stage_load(c + 1 < NC ? c + 1 : c);
+        __builtin_amdgcn_sched_barrier(0);
         u32x4 wh[NB], wl[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-          wh[nb] = wq[((kb + nb0 + nb) * 2) * 64 + lane];
-          wl[nb] = wq[((kb + nb0 + nb) * 2 + 1) * 64 + lane];
+          wh[nb] = wsh[c & 1][(nb * 2) * 64 + lane];
+          wl[nb] = wsh[c & 1][(nb * 2 + 1) * 64 + lane];
         }
-        __builtin_amdgcn_sched_barrier(0);
         u32x4 xh[MB], xl[MB];
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-          const f32x4 v0 = as_f32x4(buf_load16(xr, xoff[mb] + kc * 128));
-          const f32x4 v1 = as_f32x4(buf_load16(xr, xoff[mb] + kc * 128 + 16));
-          float x[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+          float x[8] = {xv[mb][0][0], xv[mb][0][1], xv[mb][0][2], xv[mb][0][3],
+                        xv[mb][1][0], xv[mb][1][1], xv[mb][1][2], xv[mb][1][3]};
           if constexpr (PLN) {
-            const int c = kc * 32 + lg * 8;
-            const f32x4 lw0 = *reinterpret_cast<const f32x4*>(g.ln_w + c);
-            const f32x4 lw1 = *reinterpret_cast<const f32x4*>(g.ln_w + c + 4);
-            const f32x4 lb0 = *reinterpret_cast<const f32x4*>(g.ln_b + c);
-            const f32x4 lb1 = *reinterpret_cast<const f32x4*>(g.ln_b + c + 4);
+            const int ch = kc * 32 + lg * 8;
+            const f32x4 lw0 = *reinterpret_cast<const f32x4*>(g.ln_w + ch);
+            const f32x4 lw1 = *reinterpret_cast<const f32x4*>(g.ln_w + ch + 4);
+            const f32x4 lb0 = *reinterpret_cast<const f32x4*>(g.ln_b + ch);
+            const f32x4 lb1 = *reinterpret_cast<const f32x4*>(g.ln_b + ch + 4);
             const float lw[8] = {lw0[0], lw0[1], lw0[2], lw0[3], lw1[0], lw1[1], lw1[2], lw1[3]};
             const float lb[8] = {lb0[0], lb0[1], lb0[2], lb0[3], lb1[0], lb1[1], lb1[2], lb1[3]};
 #pragma unroll
@@ -205,6 +241,10 @@ __global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
             acc[nb][mb] = mfma16x16x32(wh[nb], xh[mb], acc[nb][mb]);
           }
         }
+        // The other buffer was last read in chunk c - 1, before the previous
+        // barrier; the barrier below publishes it for chunk c + 1.
+        stage_store((c + 1) & 1);
+        __syncthreads();
       }
       continue;
     }
@@ -234,6 +274,7 @@ __global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
     }
   }
 
+  if (row_base >= R) return;
   // ---- epilogue: lane (lr, lg) holds outputs 16 (nb0 + nb) + 4 lg + j of row lr --------
   const float inv_cout = 1.0f / (float)g.cout;
   const float hb = HEAD ? g.head_b[0] : 0.f;
