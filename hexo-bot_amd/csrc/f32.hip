@@ -87,7 +87,7 @@ struct Gemm32 {
 // (pack_w32x3_kernel); x is split as it is loaded, lane group lg taking
 // channels 8 lg .. + 7 of each 32-channel chunk.
 template <int NB, int MB, int F, bool X3>
-__global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
+__global__ __launch_bounds__(256, 2) void gemm32_kernel(const Gemm32 g) {
   constexpr bool GATHER = (F & G_GATHER) != 0, PLN = (F & G_PLN) != 0;
   constexpr bool LN = (F & G_LN) != 0, RELU = (F & G_RELU) != 0, MASK = (F & G_MASK) != 0;
   constexpr bool CRES = (F & G_CRES) != 0, LRES = (F & G_LRES) != 0;
@@ -173,12 +173,113 @@ __global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
     }
   };
   if constexpr (X3) {
+    // Flat K loop over 32-channel chunks (tap t, chunk kc of KC2). Chunk c
+    // requests chunk c + 1's x rows, then its weight fragments into the
+    // staging registers; the wait for the staging before the LDS store at
+    // the end of chunk c covers both, so chunk c + 1 starts with its rows
+    // and fragments in place. A tap's gather indices are requested during
+    // the first chunk of the tap before (the last chunk reloads itself).
+    const int KC2 = g.kin / 32;
+    int jn[MB];
+    uint32_t xo[MB];
+    auto tap_idx = [&](int t) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        jn[mb] = rn[mb];
+        if (GATHER) jn[mb] = rv[mb] ? g.idx[((int64_t)rb[mb] * g.N + rn[mb]) * g.idx_stride + t] : -1;
+      }
+    };
+    auto tap_off = [&]() {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const bool ok = rv[mb] && jn[mb] >= 0 && jn[mb] < g.N;
+        xo[mb] = ok ? (uint32_t)(((int64_t)rb[mb] * g.x_sb + (int64_t)jn[mb] * g.x_sr) * 4) +
+                          (uint32_t)(lg * 32)
+                    : SHRIMP_OOB_OFFSET;
+      }
+    };
+    auto xload = [&](int kc, f32x4(&x)[MB][2]) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        x[mb][0] = as_f32x4(buf_load16(xr, xo[mb] + kc * 128));
+        x[mb][1] = as_f32x4(buf_load16(xr, xo[mb] + kc * 128 + 16));
+      }
+    };
+    int t = 0, kc = 0;  // the chunk being computed
+    auto step = [&](int c, const f32x4(&xv)[MB][2], f32x4(&xn)[MB][2]) {
+      const int kcc = kc, tc = t;
+      // The next tap's indices go out after this step's rows and fragments
+      // (so waiting for those never waits for them), except with one chunk
+      // per tap, where the next step already needs them.
+      if (KC2 == 1 && tc + 1 < T) tap_idx(tc + 1);
+      if (++kc == KC2) {
+        kc = 0;
+        if (++t < T) tap_off();
+        else { t = T - 1; kc = KC2 - 1; }  // past the end: reload the last chunk
+      }
+      xload(kc, xn);
+      stage_load(c + 1 < NC ? c + 1 : c);
+      if (KC2 > 1 && kcc == 0 && tc + 1 < T) tap_idx(tc + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      u32x4 wh[NB], wl[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        wh[nb] = wsh[c & 1][(nb * 2) * 64 + lane];
+        wl[nb] = wsh[c & 1][(nb * 2 + 1) * 64 + lane];
+      }
+      u32x4 xh[MB], xl[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        float x[8] = {xv[mb][0][0], xv[mb][0][1], xv[mb][0][2], xv[mb][0][3],
+                      xv[mb][1][0], xv[mb][1][1], xv[mb][1][2], xv[mb][1][3]};
+        if constexpr (PLN) {
+          const int ch = kcc * 32 + lg * 8;
+          const f32x4 lw0 = *reinterpret_cast<const f32x4*>(g.ln_w + ch);
+          const f32x4 lw1 = *reinterpret_cast<const f32x4*>(g.ln_w + ch + 4);
+          const f32x4 lb0 = *reinterpret_cast<const f32x4*>(g.ln_b + ch);
+          const f32x4 lb1 = *reinterpret_cast<const f32x4*>(g.ln_b + ch + 4);
+          const float lw[8] = {lw0[0], lw0[1], lw0[2], lw0[3], lw1[0], lw1[1], lw1[2], lw1[3]};
+          const float lb[8] = {lb0[0], lb0[1], lb0[2], lb0[3], lb1[0], lb1[1], lb1[2], lb1[3]};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = fmaf((x[e] - pmean[mb]) * prstd[mb], lw[e], lb[e]);
+        }
+#pragma unroll
+        for (int w2 = 0; w2 < 4; ++w2) {
+          const unsigned hw = pack_bf16x2(x[2 * w2], x[2 * w2 + 1]);
+          xh[mb][w2] = hw;
+          xl[mb][w2] = pack_bf16x2(x[2 * w2] - bf16_lo(hw), x[2 * w2 + 1] - bf16_hi(hw));
+        }
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          acc[nb][mb] = mfma16x16x32(wh[nb], xl[mb], acc[nb][mb]);
+          acc[nb][mb] = mfma16x16x32(wl[nb], xh[mb], acc[nb][mb]);
+          acc[nb][mb] = mfma16x16x32(wh[nb], xh[mb], acc[nb][mb]);
+        }
+      }
+      // The other buffer was last read in chunk c - 1, before the previous
+      // barrier; the barrier below publishes it for chunk c + 1.
+      stage_store((c + 1) & 1);
+      __syncthreads();
+    };
+    f32x4 xa[MB][2], xb[MB][2];
+    tap_idx(0);
+    tap_off();
+    xload(0, xa);
     stage_load(0);
     stage_store(0);
     __syncthreads();
+    int c = 0;
+    for (; c + 1 < NC; c += 2) {
+      step(c, xa, xb);
+      step(c + 1, xb, xa);
+    }
+    if (c < NC) step(c, xa, xb);
   }
   const f32x4* wp = reinterpret_cast<const f32x4*>(g.w);
-  for (int t = 0; t < T; ++t) {
+  for (int t = 0; t < (X3 ? 0 : T); ++t) {
     uint32_t xoff[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -186,67 +287,8 @@ __global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
       if (GATHER) j = rv[mb] ? g.idx[((int64_t)rb[mb] * g.N + rn[mb]) * g.idx_stride + t] : -1;
       const bool ok = rv[mb] && j >= 0 && j < g.N;
       xoff[mb] = ok ? (uint32_t)(((int64_t)rb[mb] * g.x_sb + (int64_t)j * g.x_sr) * 4) +
-                          (uint32_t)(lg * (X3 ? 32 : 16))
+                          (uint32_t)(lg * 16)
                     : SHRIMP_OOB_OFFSET;
-    }
-    if constexpr (X3) {
-      const int KC2 = g.kin / 32;
-      for (int kc = 0; kc < KC2; ++kc) {
-        const int c = t * KC2 + kc;
-        // This chunk's rows first, then the next chunk's fragments into the
-        // staging registers, so the wait for the rows leaves those in flight.
-        f32x4 xv[MB][2];
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          xv[mb][0] = as_f32x4(buf_load16(xr, xoff[mb] + kc * 128));
-          xv[mb][1] = as_f32x4(buf_load16(xr, xoff[mb] + kc * 128 + 16));
-        }
-        stage_load(c + 1 < NC ? c + 1 : c);
-        __builtin_amdgcn_sched_barrier(0);
-        u32x4 wh[NB], wl[NB];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          wh[nb] = wsh[c & 1][(nb * 2) * 64 + lane];
-          wl[nb] = wsh[c & 1][(nb * 2 + 1) * 64 + lane];
-        }
-        u32x4 xh[MB], xl[MB];
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          float x[8] = {xv[mb][0][0], xv[mb][0][1], xv[mb][0][2], xv[mb][0][3],
-                        xv[mb][1][0], xv[mb][1][1], xv[mb][1][2], xv[mb][1][3]};
-          if constexpr (PLN) {
-            const int ch = kc * 32 + lg * 8;
-            const f32x4 lw0 = *reinterpret_cast<const f32x4*>(g.ln_w + ch);
-            const f32x4 lw1 = *reinterpret_cast<const f32x4*>(g.ln_w + ch + 4);
-            const f32x4 lb0 = *reinterpret_cast<const f32x4*>(g.ln_b + ch);
-            const f32x4 lb1 = *reinterpret_cast<const f32x4*>(g.ln_b + ch + 4);
-            const float lw[8] = {lw0[0], lw0[1], lw0[2], lw0[3], lw1[0], lw1[1], lw1[2], lw1[3]};
-            const float lb[8] = {lb0[0], lb0[1], lb0[2], lb0[3], lb1[0], lb1[1], lb1[2], lb1[3]};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] = fmaf((x[e] - pmean[mb]) * prstd[mb], lw[e], lb[e]);
-          }
-#pragma unroll
-          for (int w2 = 0; w2 < 4; ++w2) {
-            const unsigned hw = pack_bf16x2(x[2 * w2], x[2 * w2 + 1]);
-            xh[mb][w2] = hw;
-            xl[mb][w2] = pack_bf16x2(x[2 * w2] - bf16_lo(hw), x[2 * w2 + 1] - bf16_hi(hw));
-          }
-        }
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb) {
-            acc[nb][mb] = mfma16x16x32(wh[nb], xl[mb], acc[nb][mb]);
-            acc[nb][mb] = mfma16x16x32(wl[nb], xh[mb], acc[nb][mb]);
-            acc[nb][mb] = mfma16x16x32(wh[nb], xh[mb], acc[nb][mb]);
-          }
-        }
-        // The other buffer was last read in chunk c - 1, before the previous
-        // barrier; the barrier below publishes it for chunk c + 1.
-        stage_store((c + 1) & 1);
-        __syncthreads();
-      }
-      continue;
     }
     for (int kc = 0; kc < KC; ++kc) {
       f32x4 bx[MB];
