@@ -4,18 +4,22 @@
 // packages/shrimp/python/shrimp/inference.py:50-68). These kernels run the
 // same forward as the bf16 kernels with fp32 activations end to end:
 //
-//  * gemm32_kernel: the gather-GEMM hex conv (HexNodeConv / hex_conv_ln,
-//    model.py:346-370, 395-422; _triton_conv.py:46-196) and the nn.Linear
-//    row GEMMs of the attention block (model.py:448-514) on
-//    v_mfma_f32_16x16x4_f32, with every epilogue of the bf16 kernels
-//    (bias, LayerNorm, ReLU, row mask, ConvBlock residual, LayerScale
-//    residual, GELU, q/k/v head split, policy head) and a LayerNorm
-//    prologue for the linear inputs.
+//  * gemm32x3_kernel / gemm32_kernel (one body, gemm32_body): the
+//    gather-GEMM hex conv (HexNodeConv / hex_conv_ln, model.py:346-370,
+//    395-422; _triton_conv.py:46-196) and the nn.Linear row GEMMs of the
+//    attention block (model.py:448-514), with every epilogue of the bf16
+//    kernels (bias, LayerNorm, ReLU, row mask, ConvBlock residual,
+//    LayerScale residual, GELU, q/k/v head split, policy head) and a
+//    LayerNorm prologue for the linear inputs. Input widths that are
+//    multiples of 32 run gemm32x3_kernel: bf16 MFMA on hi / lo split
+//    operands (see gemm32_body). The 16-channel stem runs gemm32_kernel on
+//    v_mfma_f32_16x16x4_f32.
 //    Orientation as in the bf16 kernels: out^T = W^T . X^T, so lane (lr, lg)
-//    of a 16x16 result holds outputs 4 lg .. +3 of row lr. A k-chunk is 16
-//    input channels: lane group lg loads channels 4 lg .. +3 of its row as
-//    one 16-byte load, and MFMA step s (0..3) of the chunk takes channel
-//    4 lg + s as k slot lg. Weights are packed to match (16-byte fragments).
+//    of a 16x16 result holds outputs 4 lg .. +3 of row lr. In the fp32
+//    kernel a k-chunk is 16 input channels: lane group lg loads channels
+//    4 lg .. +3 of its row as one 16-byte load, and MFMA step s (0..3) of
+//    the chunk takes channel 4 lg + s as k slot lg. Weights are packed to
+//    match (16-byte fragments).
 //  * attn32_mfma_kernel: the fp32 attention at head dim 16 (coords mode) on
 //    bf16 MFMA with hi / lo operand splitting (see the kernel);
 //  * attn_rows_kernel: softmax(q k^T / sqrt(d) + bias) v with one query row
@@ -87,7 +91,7 @@ struct Gemm32 {
 // (pack_w32x3_kernel); x is split as it is loaded, lane group lg taking
 // channels 8 lg .. + 7 of each 32-channel chunk.
 template <int NB, int MB, int F, bool X3>
-__global__ __launch_bounds__(256, 2) void gemm32_kernel(const Gemm32 g) {
+SHRIMP_DEV void gemm32_body(const Gemm32& g) {
   constexpr bool GATHER = (F & G_GATHER) != 0, PLN = (F & G_PLN) != 0;
   constexpr bool LN = (F & G_LN) != 0, RELU = (F & G_RELU) != 0, MASK = (F & G_MASK) != 0;
   constexpr bool CRES = (F & G_CRES) != 0, LRES = (F & G_LRES) != 0;
@@ -116,29 +120,47 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(const Gemm32 g) {
     rn[mb] = rv[mb] ? (int)(r - (int64_t)rb[mb] * g.N) : 0;
   }
 
-  // LayerNorm statistics of the input rows (two passes over the row)
+  // LayerNorm statistics of the input rows (two passes over the row; each
+  // pass requests four 16-channel chunks of every row block at a time, the
+  // sums still taken chunk by chunk in order)
   float pmean[MB], prstd[MB];
   if constexpr (PLN) {
+    uint32_t off[MB];
+    float s[MB], q[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      const uint32_t off = rv[mb] ? (uint32_t)(((int64_t)rb[mb] * g.x_sb + (int64_t)rn[mb] * g.x_sr) * 4) +
-                                        (uint32_t)(lg * 16)
-                                  : SHRIMP_OOB_OFFSET;
-      float s = 0.f;
-      for (int kc = 0; kc < KC; ++kc) {
-        const f32x4 v = as_f32x4(buf_load16(xr, off + kc * 64));
-        s += (v[0] + v[1]) + (v[2] + v[3]);
-      }
-      const float mean = sum_lane_groups(s) / (float)g.kin;
-      float q = 0.f;
-      for (int kc = 0; kc < KC; ++kc) {
-        const f32x4 v = as_f32x4(buf_load16(xr, off + kc * 64));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) q = fmaf(v[j] - mean, v[j] - mean, q);
-      }
-      pmean[mb] = mean;
-      prstd[mb] = rsqrtf(sum_lane_groups(q) / (float)g.kin + g.eps);
+      off[mb] = rv[mb] ? (uint32_t)(((int64_t)rb[mb] * g.x_sb + (int64_t)rn[mb] * g.x_sr) * 4) +
+                             (uint32_t)(lg * 16)
+                       : SHRIMP_OOB_OFFSET;
+      s[mb] = 0.f;
+      q[mb] = 0.f;
     }
+    auto pass = [&](auto&& use) {
+      int kc = 0;
+      for (; kc + 4 <= KC; kc += 4) {
+        f32x4 v[MB][4];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) v[mb][u] = as_f32x4(buf_load16(xr, off[mb] + (kc + u) * 64));
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) use(mb, v[mb][u]);
+      }
+      for (; kc < KC; ++kc)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) use(mb, as_f32x4(buf_load16(xr, off[mb] + kc * 64)));
+    };
+    pass([&](int mb, const f32x4& v) { s[mb] += (v[0] + v[1]) + (v[2] + v[3]); });
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) pmean[mb] = sum_lane_groups(s[mb]) / (float)g.kin;
+    pass([&](int mb, const f32x4& v) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) q[mb] = fmaf(v[j] - pmean[mb], v[j] - pmean[mb], q[mb]);
+    });
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) prstd[mb] = rsqrtf(sum_lane_groups(q[mb]) / (float)g.kin + g.eps);
   }
 
   f32x4 acc[NB][MB];
@@ -407,6 +429,17 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(const Gemm32 g) {
   }
 }
 
+// The split-operand kernels keep two waves per SIMD (at most 256 registers);
+// the fp32-fragment kernel (16-channel inputs) keeps the default bound.
+template <int NB, int MB, int F>
+__global__ __launch_bounds__(256, 2) void gemm32x3_kernel(const Gemm32 g) {
+  gemm32_body<NB, MB, F, true>(g);
+}
+template <int NB, int MB, int F>
+__global__ __launch_bounds__(256) void gemm32_kernel(const Gemm32 g) {
+  gemm32_body<NB, MB, F, false>(g);
+}
+
 // Packs W (K x cout, element (k, n) at w[k * sk + n * sn], k = t * kin + c
 // for c < kin_real and zero for kin_real <= c < kin) into 16-byte fragments:
 // fragment (kc, nb) lane (lr, lg) = W[16 kc + 4 lg + j][16 nb + lr], j < 4.
@@ -462,9 +495,9 @@ static int launch_gemm32(const Gemm32& g, hipStream_t st) {
   const int64_t per = 4 * MB * 16;
   dim3 grid((unsigned)((R + per - 1) / per), (unsigned)(g.cout / 16 / NB));
   if (g.kin % 32 == 0)
-    hipLaunchKernelGGL((gemm32_kernel<NB, MB, F, true>), grid, dim3(256), 0, st, g);
+    hipLaunchKernelGGL((gemm32x3_kernel<NB, MB, F>), grid, dim3(256), 0, st, g);
   else
-    hipLaunchKernelGGL((gemm32_kernel<NB, MB, F, false>), grid, dim3(256), 0, st, g);
+    hipLaunchKernelGGL((gemm32_kernel<NB, MB, F>), grid, dim3(256), 0, st, g);
   return check_launch("gemm32");
 }
 
