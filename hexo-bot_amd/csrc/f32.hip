@@ -842,42 +842,39 @@ __global__ __launch_bounds__(A32_NW * 64) void attn32_mfma_kernel(const shrimp_a
     qh.y = pack_bf16x2(qs[2], qs[3]);
     ql.x = pack_bf16x2(qs[0] - bf16_lo(qh.x), qs[1] - bf16_hi(qh.x));
     ql.y = pack_bf16x2(qs[2] - bf16_lo(qh.y), qs[3] - bf16_hi(qh.y));
-    float m = SHRIMP_NEG_BIG_F32, l = 0.f;
+    // m: the row's offset; lp: this lane's share of the row sum (its four
+    // keys of every block), summed over the lane groups once at the end
+    float m = SHRIMP_NEG_BIG_F32, lp = 0.f;
+    bool mset = false;  // every query of the block has its offset (wave-uniform)
     f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int kb = 0; kb < nkb; ++kb) {
       const int fs = kb * 64 + lg * 16 + lr;
-      f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
-      sc = mfma16x16x16(khi[fs], ql, sc);
-      sc = mfma16x16x16(klo[fs], qh, sc);
-      sc = mfma16x16x16(khi[fs], qh, sc);
       // keys 16 kb + 4 lg + j of query lr
       const int key0 = kb * 16 + lg * 4;
       float s[4];
       float mx = SHRIMP_NEG_BIG_F32;
       const bool plain = linear && !qtokb && !bspec[kb];
       if (plain) {
-        // cell queries, cell keys only (wave-uniform): one table read per key
+        // cell queries, cell keys only (wave-uniform): the accumulators
+        // start at the keys' biases, one table read per key
         const int4 kc = *reinterpret_cast<const int4*>(kcode + key0);
-        const int kcv[4] = {kc.x, kc.y, kc.z, kc.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          s[j] = sc[j] + tab[kcv[j] - qoff];
-          mx = fmaxf(mx, s[j]);
-        }
+        f32x4 sc = f32x4{tab[kc.x - qoff], tab[kc.y - qoff], tab[kc.z - qoff], tab[kc.w - qoff]};
+        sc = mfma16x16x16(khi[fs], ql, sc);
+        sc = mfma16x16x16(klo[fs], qh, sc);
+        sc = mfma16x16x16(khi[fs], qh, sc);
         // Once every query of the block has an offset m, the tile keeps it:
         // p = exp2(s - m) needs no maximum, no rescale and no lane exchange
-        // (any fixed offset gives the same softmax; the row sums only have to
+        // (any fixed offset gives the same softmax; the sums only have to
         // stay finite and in range, else the tile takes the maximum path).
-        if (__builtin_amdgcn_ballot_w64(!(m > 0.5f * SHRIMP_NEG_BIG_F32)) == 0) {
+        if (mset) {
           float p[4], ps = 0.f;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            p[j] = __builtin_amdgcn_exp2f(s[j] - m);
+            p[j] = __builtin_amdgcn_exp2f(sc[j] - m);
             ps += p[j];
           }
-          const float tot = sum_groups_swap(ps);
-          if (__builtin_amdgcn_ballot_w64(!(tot < 0x1p64f)) == 0) {
-            l += tot;
+          if (__builtin_amdgcn_ballot_w64(!(ps < 0x1p62f)) == 0) {
+            lp += ps;
             u32x2 ph, pl;
             ph.x = pack_bf16x2(p[0], p[1]);
             ph.y = pack_bf16x2(p[2], p[3]);
@@ -889,7 +886,16 @@ __global__ __launch_bounds__(A32_NW * 64) void attn32_mfma_kernel(const shrimp_a
             continue;
           }
         }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          s[j] = sc[j];
+          mx = fmaxf(mx, s[j]);
+        }
       } else {
+        f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+        sc = mfma16x16x16(khi[fs], ql, sc);
+        sc = mfma16x16x16(klo[fs], qh, sc);
+        sc = mfma16x16x16(khi[fs], qh, sc);
         const int4 cl = *reinterpret_cast<const int4*>(kcls + key0);
         const int clv[4] = {cl.x, cl.y, cl.z, cl.w};
 #pragma unroll
@@ -912,13 +918,14 @@ __global__ __launch_bounds__(A32_NW * 64) void attn32_mfma_kernel(const shrimp_a
       const float mnew = fmaxf(m, mx);
       const float alpha = __builtin_amdgcn_exp2f(m - mnew);
       m = mnew;
+      mset = __builtin_amdgcn_ballot_w64(!(m > 0.5f * SHRIMP_NEG_BIG_F32)) == 0;
       float p[4], ps = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         p[j] = s[j] > 0.5f * SHRIMP_NEG_BIG_F32 ? __builtin_amdgcn_exp2f(s[j] - mnew) : 0.f;
         ps += p[j];
       }
-      l = l * alpha + sum_groups_swap(ps);
+      lp = lp * alpha + ps;
       u32x2 ph, pl;
       ph.x = pack_bf16x2(p[0], p[1]);
       ph.y = pack_bf16x2(p[2], p[3]);
@@ -929,6 +936,7 @@ __global__ __launch_bounds__(A32_NW * 64) void attn32_mfma_kernel(const shrimp_a
       o = mfma16x16x16(vlo[fs], ph, o);
       o = mfma16x16x16(vhi[fs], ph, o);
     }
+    const float l = sum_groups_swap(lp);
     // lane (lr, lg): dims 4 lg .. + 3 of query lr
     if (query < S) {
       const float inv = (qv && l > 0.f) ? 1.0f / l : 0.f;
