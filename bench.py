@@ -669,7 +669,10 @@ def cfg2_xtab(btab, m: int):
 
 def fp32_timing(net, inputs, steps: int = 10) -> dict:
     """Secondary figure: the config 4 forward in the fp32 serve mode (fp32
-    activations, fp32 MFMA), same inputs and weights."""
+    activations; the GEMMs and attention as three bf16 MFMA products of hi / lo
+    split operands, the 16-channel stem on fp32 MFMA), same inputs and
+    weights. tflops_padded counts each product once (the fp32 forward's
+    padded FLOPs); the bf16 MFMA work is three times that."""
 
     import torch
 
@@ -690,7 +693,8 @@ def fp32_timing(net, inputs, steps: int = 10) -> dict:
         "positions_per_s": round(B / (ms * 1e-3), 1),
         "ms_per_step": round(ms, 4),
         "tflops_padded": round(1.425e9 * B / (ms * 1e-3) / 1e12, 2),
-        "peak_fp32_mfma_tflops": 157.3,
+        "mfma": "bf16, three products per fp32 product (hi·lo + lo·hi + hi·hi)",
+        "bf16_mfma_frac": round(3 * 1.425e9 * B / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "in_forward": tl,
     }
 
