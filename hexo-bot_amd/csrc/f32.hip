@@ -105,7 +105,9 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
   // X3 waves share weight fragments through LDS with a barrier per chunk, so
   // a wave past the last row stays until the K loop ends.
   if (!X3 && row_base >= R) return;
-  const int nb0 = blockIdx.y * NB;
+  // With a LayerNorm prologue the split kernel walks all output blocks itself
+  // (grid.y 1), so the rows come from HBM and their statistics are taken once.
+  constexpr bool YLOOP = X3 && PLN;
   const int NBT = g.cout / 16;
   const int KC = g.kin / 16;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.x, g.x_bytes);
@@ -163,6 +165,8 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
     for (int mb = 0; mb < MB; ++mb) prstd[mb] = rsqrtf(sum_lane_groups(q[mb]) / (float)g.kin + g.eps);
   }
 
+  for (int yb = 0; yb < (YLOOP ? NBT / NB : 1); ++yb) {
+  const int nb0 = (YLOOP ? yb : (int)blockIdx.y) * NB;
   f32x4 acc[NB][MB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
@@ -338,7 +342,10 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
     }
   }
 
-  if (row_base >= R) return;
+  if (row_base >= R) {
+    if constexpr (YLOOP) continue;  // the next output block's barriers need the wave
+    else return;
+  }
   // ---- epilogue: lane (lr, lg) holds outputs 16 (nb0 + nb) + 4 lg + j of row lr --------
   const float inv_cout = 1.0f / (float)g.cout;
   const float hb = HEAD ? g.head_b[0] : 0.f;
@@ -427,6 +434,7 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
       *reinterpret_cast<f32x4*>(dst) = f32x4{o[0], o[1], o[2], o[3]};
     }
   }
+  }  // output blocks
 }
 
 // The split-operand kernels keep two waves per SIMD (at most 256 registers);
@@ -493,7 +501,8 @@ template <int NB, int MB, int F>
 static int launch_gemm32(const Gemm32& g, hipStream_t st) {
   const int64_t R = (int64_t)g.B * g.N;
   const int64_t per = 4 * MB * 16;
-  dim3 grid((unsigned)((R + per - 1) / per), (unsigned)(g.cout / 16 / NB));
+  const bool yloop = (F & G_PLN) != 0 && g.kin % 32 == 0;  // gemm32_body's YLOOP
+  dim3 grid((unsigned)((R + per - 1) / per), yloop ? 1u : (unsigned)(g.cout / 16 / NB));
   if (g.kin % 32 == 0)
     hipLaunchKernelGGL((gemm32x3_kernel<NB, MB, F>), grid, dim3(256), 0, st, g);
   else
