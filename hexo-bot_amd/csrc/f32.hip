@@ -177,34 +177,40 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
   // X3: a chunk's NB hi / lo fragment pairs (NB x 2 KiB, contiguous in the
   // packed weights) are loaded once per workgroup, 16 bytes per thread at a
   // time, into one of two LDS buffers; the waves read their lane's fragments
-  // from there.
-  constexpr int SPT = X3 ? (NB * 128 + 255) / 256 : 1;  // staging loads per thread
-  __shared__ u32x4 wsh[X3 ? 2 : 1][X3 ? NB * 128 : 1];
+  // from there. A buffer (stage) holds SD consecutive chunks, so the waves
+  // meet at a barrier once per SD chunks.
+  constexpr int SD = NB <= 8 ? 2 : 1;  // chunks per stage (64 KiB of LDS at NB = 8)
+  constexpr int CW = NB * 128;         // 16-byte pieces per chunk
+  constexpr int SPT = X3 ? (SD * CW + 255) / 256 : 1;  // staging loads per thread
+  __shared__ u32x4 wsh[X3 ? 2 : 1][X3 ? SD * CW : 1];
   u32x4 stg[SPT];
   const int NC = X3 ? T * (g.kin / 32) : 0;
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(g.w, X3 ? (uint32_t)((int64_t)NC * NBT * 2048) : 0u);
-  auto stage_load = [&](int c) {
-    const uint32_t base = (uint32_t)(c * NBT + nb0) * 2048u;
+  auto stage_load = [&](int st) {  // chunks SD st .. + SD - 1, past the last one reloading it
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
       const int i = threadIdx.x + k * 256;
-      if (NB * 128 % 256 == 0 || i < NB * 128) stg[k] = buf_load16(wr, base + (uint32_t)i * 16u);
+      if ((SD * CW) % 256 == 0 || i < SD * CW) {
+        const int cc = min(st * SD + i / CW, NC - 1);
+        stg[k] = buf_load16(wr, (uint32_t)(cc * NBT + nb0) * 2048u + (uint32_t)(i % CW) * 16u);
+      }
     }
   };
   auto stage_store = [&](int buf) {
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
       const int i = threadIdx.x + k * 256;
-      if (NB * 128 % 256 == 0 || i < NB * 128) wsh[buf][i] = stg[k];
+      if ((SD * CW) % 256 == 0 || i < SD * CW) wsh[buf][i] = stg[k];
     }
   };
   if constexpr (X3) {
     // Flat K loop over 32-channel chunks (tap t, chunk kc of KC2). Chunk c
-    // requests chunk c + 1's x rows, then its weight fragments into the
-    // staging registers; the wait for the staging before the LDS store at
-    // the end of chunk c covers both, so chunk c + 1 starts with its rows
-    // and fragments in place. A tap's gather indices are requested during
-    // the first chunk of the tap before (the last chunk reloads itself).
+    // requests chunk c + 1's x rows; the first chunk of a stage also requests
+    // the next stage's weight fragments into the staging registers, which
+    // the stage's last chunk stores to the other LDS buffer before the
+    // barrier. So every chunk starts with its rows and fragments in place. A
+    // tap's gather indices are requested during the first chunk of the tap
+    // before (past the last chunk, loads reload the last one).
     const int KC2 = g.kin / 32;
     int jn[MB];
     uint32_t xo[MB];
@@ -232,7 +238,8 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
       }
     };
     int t = 0, kc = 0;  // the chunk being computed
-    auto step = [&](int c, const f32x4(&xv)[MB][2], f32x4(&xn)[MB][2]) {
+    // even: c is the first chunk of its pair (a compile-time constant per call)
+    auto step = [&](int c, bool even, const f32x4(&xv)[MB][2], f32x4(&xn)[MB][2]) {
       const int kcc = kc, tc = t;
       // The next tap's indices go out after this step's rows and fragments
       // (so waiting for those never waits for them), except with one chunk
@@ -244,14 +251,14 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
         else { t = T - 1; kc = KC2 - 1; }  // past the end: reload the last chunk
       }
       xload(kc, xn);
-      stage_load(c + 1 < NC ? c + 1 : c);
+      if (SD == 1 || even) stage_load(c / SD + 1);
       if (KC2 > 1 && kcc == 0 && tc + 1 < T) tap_idx(tc + 1);
       __builtin_amdgcn_sched_barrier(0);
       u32x4 wh[NB], wl[NB];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        wh[nb] = wsh[c & 1][(nb * 2) * 64 + lane];
-        wl[nb] = wsh[c & 1][(nb * 2 + 1) * 64 + lane];
+        wh[nb] = wsh[(c / SD) & 1][(c % SD) * CW + (nb * 2) * 64 + lane];
+        wl[nb] = wsh[(c / SD) & 1][(c % SD) * CW + (nb * 2 + 1) * 64 + lane];
       }
       u32x4 xh[MB], xl[MB];
 #pragma unroll
@@ -285,10 +292,12 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
           acc[nb][mb] = mfma16x16x32(wh[nb], xh[mb], acc[nb][mb]);
         }
       }
-      // The other buffer was last read in chunk c - 1, before the previous
-      // barrier; the barrier below publishes it for chunk c + 1.
-      stage_store((c + 1) & 1);
-      __syncthreads();
+      // The other buffer was last read in the previous stage, before the
+      // previous barrier; the barrier below publishes it for the next stage.
+      if (SD == 1 || !even) {
+        stage_store((c / SD + 1) & 1);
+        __syncthreads();
+      }
     };
     f32x4 xa[MB][2], xb[MB][2];
     tap_idx(0);
@@ -299,10 +308,10 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
     __syncthreads();
     int c = 0;
     for (; c + 1 < NC; c += 2) {
-      step(c, xa, xb);
-      step(c + 1, xb, xa);
+      step(c, true, xa, xb);
+      step(c + 1, false, xb, xa);
     }
-    if (c < NC) step(c, xa, xb);
+    if (c < NC) step(c, true, xa, xb);
   }
   const f32x4* wp = reinterpret_cast<const f32x4*>(g.w);
   for (int t = 0; t < (X3 ? 0 : T); ++t) {
