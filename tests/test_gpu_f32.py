@@ -288,11 +288,13 @@ def test_f32_hex_conv(epi, cin, cout):
 
 @pytest.mark.parametrize("mode", ["qkv", "gelu", "resid", "plain"])
 @pytest.mark.parametrize("c,h", [(32, 4), (128, 8), (96, 4), (192, 3)])
-def test_f32_linear_modes(mode, c, h):
+@pytest.mark.parametrize("B,S", [(3, 37), (1, 9)])
+def test_f32_linear_modes(mode, c, h, B, S):
+    """Every linear mode against float64. 9 rows leave three of a workgroup's
+    four waves without rows (they still take part in the weight staging)."""
     from shrimp import _lib
 
-    rng = np.random.default_rng(c + len(mode))
-    B, S = 3, 37
+    rng = np.random.default_rng(c + len(mode) + S)
     d = c // h
     rows = B * S
     n_in = 2 * c if mode == "resid" else c
