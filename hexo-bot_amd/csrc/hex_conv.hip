@@ -512,7 +512,9 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
 
   for (int tile0 = (int)blockIdx.y * TILE; tile0 < N; tile0 += (int)gridDim.y * TILE) {
     const int row_base = tile0 + wave * MB * 16;
-    if (row_base >= N) break;
+    // BIGORDER waves meet at barriers in the K loop, so a wave without rows
+    // runs it (on the zero row) and skips only the epilogue.
+    if (!BIGORDER && row_base >= N) break;
     int rb[MB], rn[MB];
     bool rv[MB];
 #pragma unroll
@@ -552,16 +554,35 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) sa[t][mb] = row_addr(j[mb]);
       }
-      // Weight fragments run two steps ahead through a ring of three (a small
-      // tile has few products per step to cover the L2 latency), row fragments
-      // one step ahead.
+      // A step's weight fragments (NB x 1 KiB, contiguous) are loaded once per
+      // workgroup, 16 bytes per thread and piece, D steps ahead in registers,
+      // and handed to the waves through one LDS buffer: each wave reads its
+      // fragments, a barrier, the next step's pieces are stored, a barrier.
+      // (Per wave, the same fragments in the same MFMA order as a per-wave
+      // load, so the same bits; a quarter of the L2 reads, and a prefetch
+      // deep enough for a step's 8 MFMAs to cover the L2 latency.) Row
+      // fragments run one step ahead from the staged rows.
       constexpr int NS = T * KC;
-      u32x4 wq[3][NB], xq[2][MB];
-      auto load_w = [&](int s, u32x4 (&w)[NB]) {
+      constexpr int WP = NB * 64;            // 16-byte pieces per step
+      constexpr int WPT = (WP + 255) / 256;  // per thread
+      constexpr int D = 6;                   // steps in flight
+      __shared__ u32x4 wls[WP];
+      u32x4 stg[D][WPT], wq[NB], xq[2][MB];
+      auto gload = [&](int s, u32x4 (&r)[WPT]) {
         const int kc = s / T, t = s % T;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          w[nb] = buf_load16(wr, (uint32_t)((((t * KC + kc) * NB + nb) * 64 + lane) * 16));
+        for (int k = 0; k < WPT; ++k) {
+          const int i = (int)threadIdx.x + k * 256;
+          if (WP % 256 == 0 || i < WP)
+            r[k] = buf_load16(wr, (uint32_t)(((t * KC + kc) * WP + i) * 16));
+        }
+      };
+      auto sstore = [&](const u32x4 (&r)[WPT]) {
+#pragma unroll
+        for (int k = 0; k < WPT; ++k) {
+          const int i = (int)threadIdx.x + k * 256;
+          if (WP % 256 == 0 || i < WP) wls[i] = r[k];
+        }
       };
       auto load_x = [&](int s, u32x4 (&x)[MB]) {
         const int kc = s / T, t = s % T;
@@ -569,20 +590,32 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) x[mb] = *reinterpret_cast<const u32x4*>(xs + (sa[t][mb] ^ cs));
       };
-      load_w(0, wq[0]);
-      load_w(1, wq[1]);
+#pragma unroll
+      for (int d = 0; d < D && d < NS; ++d) gload(d, stg[d]);
+      __syncthreads();  // the previous tile's last fragments are read
+      sstore(stg[0]);
+      if (D < NS) gload(D, stg[0]);
       load_x(0, xq[0]);
+      __syncthreads();
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        if (s + 2 < NS) load_w(s + 2, wq[(s + 2) % 3]);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) wq[nb] = wls[nb * 64 + lane];
         if (s + 1 < NS) load_x(s + 1, xq[(s + 1) % 2]);
+        if (s + 1 < NS) __syncthreads();  // every wave holds step s's fragments
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb)
-            acc[nb][mb] = mfma16x16x32(wq[s % 3][nb], xq[s % 2][mb], acc[nb][mb]);
+            acc[nb][mb] = mfma16x16x32(wq[nb], xq[s % 2][mb], acc[nb][mb]);
+        if (s + 1 < NS) {
+          sstore(stg[(s + 1) % D]);
+          if (s + 1 + D < NS) gload(s + 1 + D, stg[(s + 1) % D]);
+          __syncthreads();  // step s + 1's fragments are visible
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
+      if (row_base >= N) continue;
       lds_conv_epilogue<COUT, MB, BA ? (EPI | EPI_BACC) : EPI, B16>(a, acc, rb, rn, rv, lg, lp,
                                                                    o_bytes, r_bytes);
       continue;
@@ -1314,8 +1347,10 @@ static int launch_conv(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, size
   // tile of 64 rows per workgroup, (B, N / 64) workgroups, instead of one
   // workgroup per position; where the big-tile kernel would run, with its
   // arithmetic (same bits).
+  // (The big-tile order adds a static 16 * COUT-byte weight buffer to the LDS.)
   if (COUT == 128 && lds_ok && (a->cin_pad == 32 || a->cin_pad == 128) &&
-      (int64_t)a->B * 2 <= cu_count() && g_conv_variant == 0) {
+      (int64_t)a->B * 2 <= cu_count() && g_conv_variant == 0 &&
+      (!big || lds_p + (size_t)COUT * 64 <= (size_t)max_lds_per_block())) {
     const dim3 grid((unsigned)a->B, (unsigned)((a->N + 63) / 64));
     if (big) SHRIMP_LDS_LAUNCH(grid, 1, 128, true);
     else if (a->cin_pad == 32) SHRIMP_LDS_LAUNCH(grid, 1, 32, false);
