@@ -916,16 +916,26 @@ __global__ __launch_bounds__(A32_NW * 64) void attn32_mfma_kernel(const shrimp_a
         sc = mfma16x16x16(khi[fs], qh, sc);
         const int4 cl = *reinterpret_cast<const int4*>(kcls + key0);
         const int clv[4] = {cl.x, cl.y, cl.z, cl.w};
+        // every key's table entry is read (in the linear table any key's
+        // code gives an index inside it), then replaced for tokens and dead
+        // keys by selects, so the tile runs without branches
+        float tb[4];
+        if (linear) {
+          const int4 kc = *reinterpret_cast<const int4*>(kcode + key0);
+          tb[0] = tab[kc.x - qoff];
+          tb[1] = tab[kc.y - qoff];
+          tb[2] = tab[kc.z - qoff];
+          tb[3] = tab[kc.w - qoff];
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int key = key0 + j;
+            tb[j] = tab[(min(max(kq[key] - qq, -M), M) + M) * W + (min(max(kr[key] - qr, -M), M) + M)];
+          }
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int key = key0 + j;
-          float bias;
-          if (linear) {
-            bias = tab[kcode[key] - qoff];
-          } else {
-            const int pos = (min(max(kq[key] - qq, -M), M) + M) * W + (min(max(kr[key] - qr, -M), M) + M);
-            bias = tab[pos];
-          }
+          float bias = tb[j];
           bias = qtok ? t_tc : bias;
           bias = clv[j] == K_TOKEN ? (qtok ? t_tt : t_ct) : bias;
           s[j] = clv[j] == K_DEAD ? SHRIMP_NEG_BIG_F32 : sc[j] + bias;
