@@ -81,8 +81,9 @@ struct Gemm32 {
   int S, H, dpad;  // QKV split: row = b * N + n is sequence row (r / S, r % S)
 };
 
-// One wave: MB x 16 rows by NB x 16 outputs (blockIdx.y selects the output
-// blocks); four waves per workgroup.
+// One wave: MB x 16 rows by NB x 16 outputs at a time (blockIdx.y selects the
+// output blocks, or the workgroup walks them all: YLOOP); four waves per
+// workgroup.
 // X3 (kin a multiple of 32): the products on bf16 MFMA with each fp32 operand
 // split as x = hi + lo (hi = bf16(x), lo = bf16(x - hi)), a 16 x 16 x 32 tile
 // taken as hi·lo + lo·hi + hi·hi (the lo·lo term is below 2^-16 of the
@@ -102,7 +103,7 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
   const int lg = lane >> 4;
   const int64_t R = (int64_t)g.B * g.N;
   const int64_t row_base = ((int64_t)blockIdx.x * 4 + wave) * (MB * 16);
-  // X3 waves share weight fragments through LDS with a barrier per chunk, so
+  // X3 waves share weight fragments through LDS with a barrier per stage, so
   // a wave past the last row stays until the K loop ends.
   if (!X3 && row_base >= R) return;
   // With a LayerNorm prologue the split kernel walks all output blocks itself
@@ -313,8 +314,10 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
     }
     if (c < NC) step(c, true, xa, xb);
   }
+  if constexpr (!X3) {
+  // fp32 fragments on v_mfma_f32_16x16x4f32, 16 input channels per k-chunk
   const f32x4* wp = reinterpret_cast<const f32x4*>(g.w);
-  for (int t = 0; t < (X3 ? 0 : T); ++t) {
+  for (int t = 0; t < T; ++t) {
     uint32_t xoff[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -350,6 +353,7 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
           for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = mfma16x16x4f32(aw[nb][s], bx[mb][s], acc[nb][mb]);
     }
   }
+  }  // !X3
 
   if (row_base >= R) {
     if constexpr (YLOOP) continue;  // the next output block's barriers need the wave
