@@ -132,6 +132,29 @@ def _wide_batch(npad):
     return collate_rows([(s, f) for _, s, f in rows], pad_to=npad)
 
 
+def test_forward_c128_ragged_pad_matches_oracle():
+    """C=128, H=8 at Npad 464 (7 x 64 + 16): a small batch runs the row-split
+    convs, whose last 64-row tile holds 16 rows, so three of its four waves
+    have no rows (they still take part in the shared weight staging)."""
+
+    from shrimp import synthetic
+    from shrimp.batching import collate_rows
+
+    rows = [r for r in synthetic.positions("cfg4_spec", 24, seed=34) if r[1].num_nodes <= 464][:3]
+    assert len(rows) == 3
+    b = collate_rows([(s, f) for _, s, f in rows], pad_to=464)
+    c, h, layout = 128, 8, "CCA"
+    net = _net(c, h, layout, seed=11, mode="heads")
+    out = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"], trunk=True)
+    want = ofwd.forward_policy_value(
+        weights.make_state_dict(c, h, layout, seed=11, mode="heads"), layout, h, b["feats"],
+        b["nbr"], b["mask"], b["coords"], request_moves_left=True, dtype=torch.float32,
+        return_trunk=True,
+    )
+    _check(out, want, b["mask"], "C=128 H=8 Npad=464")
+    _check_trunk(out, want, b["mask"], "C=128 H=8 Npad=464")
+
+
 @pytest.mark.parametrize("c,h,npad", [(96, 4, 256), (96, 4, 512), (192, 3, 256), (192, 3, 512),
                                       (192, 3, 576)])
 def test_forward_other_widths_match_oracle(c, h, npad):
