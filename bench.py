@@ -13,8 +13,9 @@ dominant kernel (the fused ConvBlock, timed live with HIP events on the
 launch stream, re-launched alone and inside the forward), the attention
 kernel's figures, per-kernel times inside real forwards, configs 1-3 as
 standalone ops at B=1024 with their rooflines, the fp32 serve mode's
-forward, and the CPU baseline (the oracle's fp32 eager forward on a bounded
-sample, rank 0 only).
+forward, and the CPU baseline (the reference CPU forward restated in the
+oracle, fp32 eager with sdpa, on the same 512 positions: the median of five
+forwards, rank 0 only).
 """
 
 from __future__ import annotations
@@ -446,31 +447,51 @@ def hexfield_timing(reps: int = 50, cpu_sample: int = 16) -> dict:
 
 
 def _host_cpu() -> dict:
-    """CPU model and the cores this process may use (lscpu / sched affinity)."""
+    """CPU model (every model string lscpu and /proc/cpuinfo report, the
+    longest kept), sockets and cores from lscpu, and the cores this process
+    may use (sched affinity)."""
 
-    model = None
+    names, info = [], {}
     try:
         import subprocess
 
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
         for ln in out.splitlines():
-            if ln.startswith("Model name:"):
-                model = ln.split(":", 1)[1].strip()
-    except Exception:  # lscpu missing: model stays unknown
+            key, _, val = ln.partition(":")
+            info.setdefault(key.strip(), val.strip())
+            if key.strip() in ("Model name", "BIOS Model name"):
+                names.append(val.strip())
+    except Exception:  # lscpu missing: the model comes from /proc/cpuinfo or stays unknown
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.lower().startswith("model name"):
+                    names.append(ln.split(":", 1)[1].strip())
+                    break
+    except OSError:
         pass
     try:
         usable = len(os.sched_getaffinity(0))
     except AttributeError:
         usable = os.cpu_count() or 1
-    return {"model": model, "cores_visible": os.cpu_count(), "cores_usable": usable}
+    return {"model": max(names, key=len) if names else None,
+            "sockets": info.get("Socket(s)"), "cores_per_socket": info.get("Core(s) per socket"),
+            "threads_per_core": info.get("Thread(s) per core"),
+            "cores_visible": os.cpu_count(), "cores_usable": usable}
 
 
-def cpu_baseline(batch, seconds: float, sample: int = 64):
-    """Oracle fp32 eager forward (the reference CPU path, restated) on a
-    bounded sample of the same workload (the first `sample` of the 512 cfg4
-    positions, one forward per batch of `sample`); positions/s on the host
-    cores this process may use, capped by OMP_NUM_THREADS where the host sets
-    it (the GPU box allots 16 threads per GPU)."""
+def cpu_baseline(batch, seconds: float, sample: int = 512, runs: int = 5, warmup: int = 2):
+    """The reference CPU forward restated (oracle.forward: the pair rows built
+    in torch as model.py:677-716 does, the fp16 bias per block, sdpa with that
+    mask, fp32 eager) on the same cfg4 workload: the first `sample` of the 512
+    positions as one batch, `warmup` untimed forwards, then the median of
+    `runs` timed forwards (more while the timed total stays under `seconds`);
+    positions/s on the host cores this process may use, capped by
+    OMP_NUM_THREADS where the host sets it (the GPU box allots 16 threads per
+    GPU)."""
+
+    import statistics
 
     import torch
 
@@ -485,23 +506,29 @@ def cpu_baseline(batch, seconds: float, sample: int = 64):
     torch.set_num_threads(threads)
     sd = weights.make_state_dict(C, H, LAYOUT, seed=0, mode="fresh")
     args = [batch[k][:sample] for k in ("feats", "nbr", "mask", "coords")]
-    ofwd.forward_policy_value(sd, LAYOUT, H, *args, dtype=torch.float32)
-    runs = 0
-    t0 = time.perf_counter()
-    while True:
+    n = int(args[0].shape[0])
+    for _ in range(warmup):
         ofwd.forward_policy_value(sd, LAYOUT, H, *args, dtype=torch.float32)
-        runs += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
+    times = []
+    while len(times) < runs or sum(times) < seconds:
+        t0 = time.perf_counter()
+        ofwd.forward_policy_value(sd, LAYOUT, H, *args, dtype=torch.float32)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 4 * runs:
             break
+    med = statistics.median(times)
     return {
-        "value": round(sample * runs / el, 3),
+        "value": round(n / med, 3),
         "unit": "positions/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{runs} forwards x {sample} cfg4 positions (fp32 eager oracle, {el:.1f} s, "
-                  f"torch threads {threads})",
+        "sample": f"median of {len(times)} forwards of {n} cfg4 positions after {warmup} warm-ups "
+                  f"(fp32 eager oracle: torch pair rows, fp16 bias, sdpa; "
+                  f"{min(times):.2f}-{max(times):.2f} s per forward, torch threads {threads})",
         "cpu_model": host["model"],
+        "sockets": host["sockets"],
+        "cores_per_socket": host["cores_per_socket"],
+        "threads_per_core": host["threads_per_core"],
         "cores_visible": host["cores_visible"],
         "cores_usable": host["cores_usable"],
     }
@@ -706,7 +733,7 @@ def main() -> int:
     # run), then 100 timed ones (about 0.13 s)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=30)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run 5 plain device copies of this many MiB (the "

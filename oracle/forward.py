@@ -1,7 +1,9 @@
 """Eager-torch CPU restatement of the Shrimp serve forward (test infrastructure).
 
 Follows the reference's CPU path (no Triton, no flex): the materialised
-gather + GEMM conv and the materialised bias + softmax attention of
+gather + GEMM conv, the pair rows built in torch (model.py:677-716), the fp16
+bias gathered per block (model.py:737-760) and ``scaled_dot_product_attention``
+with that bias as its mask (model.py:481-485) of
 ``packages/shrimp/python/shrimp/model.py``. All functions take a ``dtype``
 (float64 for pinning, float32 for the CPU baseline) and plain tensors;
 weights come as a state dict with the reference's keys.
@@ -119,9 +121,12 @@ def attn_offset_table(q, k, v, coords, mask, table, m):
 
 def block_bias(table, pair, key_live, dtype):
     """Reference no-grad bias (model.py:737-760): the table is rounded to
-    float16, gathered per pair, and dead keys get +(-3e4) (also in fp16)."""
+    float16, gathered per pair from its transposed (heads, rows) copy, and
+    dead keys get +(-3e4) (also in fp16). pair: (B, S, S) row indices of
+    any integer dtype."""
 
-    bias = table.to(torch.float16)[pair].permute(0, 3, 1, 2)  # (B, H, S, S)
+    bias_t = table.to(torch.float16).t().contiguous()  # (H, rows)
+    bias = bias_t[:, pair.to(torch.int64)].permute(1, 0, 2, 3)  # (B, H, S, S) view
     fill = torch.where(key_live, 0.0, PAD_KEY_MASK_VALUE).to(torch.float16)
     return (bias + fill[:, None, None, :]).to(dtype)
 
@@ -162,7 +167,7 @@ def forward_policy_value(sd, layout, heads, feats, nbr, mask, coords, *,
     gidx = torch.from_numpy(tables.gather_index(nbr.numpy()))
 
     x = F.relu(_ln(sd, "stem_ln", _conv(sd, "stem", feats, gidx, mask))) * m
-    pair = torch.from_numpy(tables.pair_rows(coords_np, mask.numpy()))
+    pair = tables.pair_rows_torch(coords_np, mask)
     key_live = torch.cat([torch.ones(b, NUM_TOKENS, dtype=torch.bool), mask], dim=1)
     seq_mask = key_live.unsqueeze(-1).to(dtype)
     tokens = sd["tokens"].unsqueeze(0).expand(b, -1, -1)
@@ -185,7 +190,9 @@ def forward_policy_value(sd, layout, heads, feats, nbr, mask, coords, *,
             q = _lin(sd, p + ".attn.q_proj", z).reshape(b, s, h, d).transpose(1, 2)
             k = _lin(sd, p + ".attn.k_proj", z).reshape(b, s, h, d).transpose(1, 2)
             v = _lin(sd, p + ".attn.v_proj", z).reshape(b, s, h, d).transpose(1, 2)
-            a = attention(q, k, v, bias).transpose(1, 2).reshape(b, s, c)
+            # the reference's default attention impl "sdpa" (model.py:481-485)
+            a = F.scaled_dot_product_attention(q, k, v, attn_mask=bias)
+            a = a.transpose(1, 2).reshape(b, s, c)
             a = _lin(sd, p + ".attn.out_proj", a)
             seq = seq + sd[p + ".ls_attn.gamma"] * (a * seq_mask)
             z = _ln(sd, p + ".ln2", seq)

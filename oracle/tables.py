@@ -3,7 +3,10 @@
 - ``rel_bias_row``  packages/shrimp/python/shrimp/geometry.py:97-131
 - ``cell_lut``      model.py:625-641 (35 x 35, clamp +-17)
 - ``gather_index``  model.py:861-863
-- ``pair_rows``     model.py:677-716 / 762-792 (key - query offsets)
+- ``pair_rows``     model.py:677-716 / 762-792 (key - query offsets); numpy, the
+                    pinned checker
+- ``pair_rows_torch`` the same rows built in torch the way the reference's CPU
+                    path builds them (the forward oracle and the CPU baseline)
 - ``seq_lens``      model.py:884-892
 - ``ray_index``     hexfield_eq/_triton_ray.py:131-152 (slot table), 221-281 (join)
 """
@@ -92,6 +95,35 @@ def pair_rows(coords: np.ndarray, mask: np.ndarray, pad_row: int | None = None) 
     if pad_row is not None:
         dead = np.concatenate([np.zeros((b, NUM_TOKENS), bool), ~mask.astype(bool)], axis=1)
         pair = np.where(dead[:, None, :], pad_row, pair)
+    return pair
+
+
+def pair_rows_torch(coords, mask, pad_row: int | None = None):
+    """``pair_rows`` vectorised in torch, as the reference builds it on its CPU
+    path (model.py:677-716 ``_build_pair``; the uint8 variant with the pad
+    row at model.py:762-792): int16 offsets, clamp to +-17, one LUT gather.
+    Returns a (B, S, S) uint8 tensor (every row index is below 256); equal
+    to ``pair_rows`` element for element (tests/test_oracle_tables.py)."""
+
+    import torch
+
+    c = torch.as_tensor(coords).to(torch.int16)
+    b, n, _ = c.shape
+    lut = torch.from_numpy(cell_lut())
+    dq = c[:, None, :, 0] - c[:, :, None, 0]
+    dr = c[:, None, :, 1] - c[:, :, None, 1]
+    qi = (dq.clamp(-LUT_M, LUT_M) + LUT_M).to(torch.int32)
+    ri = (dr.clamp(-LUT_M, LUT_M) + LUT_M).to(torch.int32)
+    cell = lut[(qi * LUT_W + ri).reshape(-1).to(torch.int64)].reshape(b, n, n)
+    s = NUM_TOKENS + n
+    pair = torch.full((b, s, s), ROW_TOKEN_TOKEN, dtype=torch.uint8)
+    pair[:, :NUM_TOKENS, NUM_TOKENS:] = ROW_TOKEN_CELL
+    pair[:, NUM_TOKENS:, :NUM_TOKENS] = ROW_CELL_TOKEN
+    pair[:, NUM_TOKENS:, NUM_TOKENS:] = cell
+    if pad_row is not None:
+        m = torch.as_tensor(mask).to(torch.bool)
+        dead = torch.cat([torch.zeros(b, NUM_TOKENS, dtype=torch.bool), ~m], dim=1)
+        pair = pair.masked_fill(dead[:, None, :], pad_row)
     return pair
 
 

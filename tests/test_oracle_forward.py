@@ -101,11 +101,13 @@ def test_forward_fp32_close_to_fp64(golden):
         assert (a[k].double() - b[k]).abs().max().item() < 1e-4
 
 
-def test_hex_conv_equals_dense_grid_conv():
-    """Tap 0 = centre (1,1) of a 3x3 kernel, axial (dq, dr) at (dr+1, dq+1)."""
+def _dense_grid_case(seed, cin, cout):
+    """A random cell set (axial coordinates within +-6), its neighbour table,
+    inputs, weights, and the same convolution as a dense F.conv2d over a
+    41 x 41 grid: tap 0 = centre (1, 1) of a 3x3 kernel, axial (dq, dr) at
+    (dr + 1, dq + 1). Returns (cells, gidx, x, w, b, dense)."""
 
-    torch.manual_seed(1)
-    rng = np.random.default_rng(3)
+    rng = np.random.default_rng(seed)
     cells = sorted({(int(q), int(r)) for q, r in rng.integers(-6, 7, size=(40, 2))})
     n = len(cells)
     index = {c: i for i, c in enumerate(cells)}
@@ -113,13 +115,10 @@ def test_hex_conv_equals_dense_grid_conv():
     for i, (q, r) in enumerate(cells):
         for k, (dq, dr) in enumerate(tables.DIRECTIONS):
             nbr[0, i, k] = index.get((q + dq, r + dr), n)
-    cin, cout = 5, 4
-    w = torch.randn(7, cin, cout, dtype=torch.float64)
-    b = torch.randn(cout, dtype=torch.float64)
-    x = torch.randn(1, n, cin, dtype=torch.float64)
+    w = torch.from_numpy(rng.standard_normal((7, cin, cout)))
+    b = torch.from_numpy(rng.standard_normal(cout))
+    x = torch.from_numpy(rng.standard_normal((1, n, cin)))
     gidx = torch.from_numpy(tables.gather_index(nbr))
-    mask = torch.ones(1, n, dtype=torch.bool)
-    out = forward.hex_conv(x, gidx, mask, w, b)
     kern = torch.zeros(cout, cin, 3, 3, dtype=torch.float64)
     kern[:, :, 1, 1] = w[0].T
     for k, (dq, dr) in enumerate(tables.DIRECTIONS):
@@ -128,8 +127,39 @@ def test_hex_conv_equals_dense_grid_conv():
     for i, (q, r) in enumerate(cells):
         grid[0, :, r + 20, q + 20] = x[0, i]
     dense = F.conv2d(grid, kern, bias=b, padding=1)
-    for i, (q, r) in enumerate(cells):
-        assert torch.allclose(out[0, i], dense[0, :, r + 20, q + 20], atol=1e-12)
+    rows = torch.stack([dense[0, :, r + 20, q + 20] for q, r in cells])  # (n, cout)
+    return cells, gidx, x, w, b, rows
+
+
+def test_hex_conv_equals_dense_grid_conv():
+    cells, gidx, x, w, b, dense = _dense_grid_case(3, 5, 4)
+    mask = torch.ones(1, len(cells), dtype=torch.bool)
+    out = forward.hex_conv(x, gidx, mask, w, b)
+    assert torch.allclose(out[0], dense, atol=1e-12)
+
+
+@pytest.mark.parametrize("relu", [False, True])
+def test_hex_conv_ln_equals_dense_grid_conv_then_layer_norm(relu):
+    """hex_conv_ln (shrimp::hex_conv_ln, _triton_conv.py:139-196) against the
+    dense-grid convolution followed by torch's F.layer_norm over the output
+    channels, the optional ReLU and the row mask; a LayerNorm over the wrong
+    axis, a dropped affine or an unmasked row each fail."""
+
+    cells, gidx, x, w, b, dense = _dense_grid_case(7, 6, 8)
+    n = len(cells)
+    rng = np.random.default_rng(8)
+    ln_w = torch.from_numpy(rng.uniform(0.5, 1.5, 8))
+    ln_b = torch.from_numpy(rng.normal(0, 0.3, 8))
+    mask = torch.from_numpy(rng.random(n) > 0.25)[None]
+    out = forward.hex_conv_ln(x, gidx, mask, w, b, ln_w, ln_b, 1e-5, relu)
+    want = F.layer_norm(dense, (8,), ln_w, ln_b, 1e-5)
+    if relu:
+        want = F.relu(want)
+    want = want * mask[0, :, None].double()
+    assert torch.allclose(out[0], want, atol=1e-12)
+    assert (out[0][~mask[0]] == 0).all()
+    plain = forward.hex_conv(x, gidx, mask, w, b)[0]
+    assert (plain - want).abs().max().item() > 1e-1  # the LayerNorm is not a no-op here
 
 
 def test_raytap_conv_reduces_to_hex_conv():

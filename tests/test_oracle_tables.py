@@ -40,6 +40,29 @@ def test_pair_rows_match_reference_pair_tensors(golden):
     np.testing.assert_array_equal(pl, g["pair_long"])
 
 
+def test_pair_rows_torch_equals_numpy(golden):
+    """The torch pair builder (the forward oracle's and the CPU baseline's)
+    equals the pinned numpy rows bit for bit: golden positions with and
+    without the pad row, and wide random boards whose offsets pass the
+    +-17 clamp."""
+
+    import torch
+
+    g = golden("pair")
+    for pad in (None, 237):
+        got = tables.pair_rows_torch(g["coords"], g["mask"], pad_row=pad)
+        assert got.dtype == torch.uint8
+        np.testing.assert_array_equal(got.numpy().astype(np.int64),
+                                      tables.pair_rows(g["coords"], g["mask"], pad_row=pad))
+    rng = np.random.default_rng(11)
+    coords = rng.integers(-30, 31, size=(3, 50, 2))
+    mask = rng.random((3, 50)) > 0.3
+    for pad in (None, 237):
+        np.testing.assert_array_equal(
+            tables.pair_rows_torch(coords, mask, pad_row=pad).numpy().astype(np.int64),
+            tables.pair_rows(coords, mask, pad_row=pad))
+
+
 def test_pair_rows_brute_force_on_small_board():
     rng = np.random.default_rng(0)
     coords = rng.integers(-20, 21, size=(2, 9, 2))
