@@ -1177,6 +1177,8 @@ SHRIMP_DEV void tail_ln_lds(const BigTile& t, unsigned char* xs, const shrimp_ta
   const int sub = tid & 15, c0 = sub * 8;
   const uint32_t koff = (uint32_t)((sub >> 2) * t.NR * 64), piece = (uint32_t)(sub & 3);
   const uint16_t* seq = static_cast<const uint16_t*>(ta.seq) + (int64_t)t.b * ta.s_sb;
+  const uint16_t* tlo =
+      ta.tok_lo ? static_cast<const uint16_t*>(ta.tok_lo) + (int64_t)t.b * nt * C : nullptr;
   float* vin = ta.workspace + (int64_t)t.b * 6 * C;
   float w[8], bb[8];
 #pragma unroll
@@ -1196,12 +1198,15 @@ SHRIMP_DEV void tail_ln_lds(const BigTile& t, unsigned char* xs, const shrimp_ta
       const uint32_t addr = koff + (uint32_t)j * 64 + ((piece ^ (uint32_t)((j >> 2) & 3)) << 4);
       const u32x4 raw = cell ? *reinterpret_cast<const u32x4*>(xs + addr)
                              : *reinterpret_cast<const u32x4*>(seq + (int64_t)r * C + c0);
+      // a token row's low part (final_ln_kernel adds it the same way)
+      const u32x4 lo = !cell && tlo ? *reinterpret_cast<const u32x4*>(tlo + (int64_t)r * C + c0)
+                                    : u32x4{0u, 0u, 0u, 0u};
       float x[8];
       float sm = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        x[2 * e] = bf16_lo(raw[e]);
-        x[2 * e + 1] = bf16_hi(raw[e]);
+        x[2 * e] = bf16_lo(raw[e]) + bf16_lo(lo[e]);
+        x[2 * e + 1] = bf16_hi(raw[e]) + bf16_hi(lo[e]);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) sm += x[e];

@@ -128,14 +128,24 @@ __global__ __launch_bounds__(256, 2) void linear_kernel(const shrimp_linear_args
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] = gelu_erf(o[j]);
       }
+      unsigned short* lo_p = nullptr;  // this row's token low part (RESID mode)
       if (MODE == SHRIMP_LIN_RESID) {
         const u32x2 rw = *reinterpret_cast<const u32x2*>(
             static_cast<const unsigned short*>(a.resid) + (int64_t)r * a.r_sr + n);
+        u32x2 lw = u32x2{0u, 0u};
+        if (a.tok_lo != nullptr) {
+          const int bp = r / a.S, sp = r - bp * a.S;
+          if (sp < a.n_tokens) {
+            lo_p = static_cast<unsigned short*>(a.tok_lo) +
+                   ((int64_t)bp * a.n_tokens + sp) * a.out_features + n;
+            lw = *reinterpret_cast<const u32x2*>(lo_p);
+          }
+        }
         const f32x4 g = *reinterpret_cast<const f32x4*>(a.gamma + n);
-        o[0] = bf16_lo(rw.x) + g[0] * (live * o[0]);
-        o[1] = bf16_hi(rw.x) + g[1] * (live * o[1]);
-        o[2] = bf16_lo(rw.y) + g[2] * (live * o[2]);
-        o[3] = bf16_hi(rw.y) + g[3] * (live * o[3]);
+        o[0] = (bf16_lo(rw.x) + bf16_lo(lw.x)) + g[0] * (live * o[0]);
+        o[1] = (bf16_hi(rw.x) + bf16_hi(lw.x)) + g[1] * (live * o[1]);
+        o[2] = (bf16_lo(rw.y) + bf16_lo(lw.y)) + g[2] * (live * o[2]);
+        o[3] = (bf16_hi(rw.y) + bf16_hi(lw.y)) + g[3] * (live * o[3]);
       }
       if (MODE == SHRIMP_LIN_QKV) {
         const int which = n / C3;
@@ -152,6 +162,11 @@ __global__ __launch_bounds__(256, 2) void linear_kernel(const shrimp_linear_args
       pk.x = pack_bf16x2(o[0], o[1]);
       pk.y = pack_bf16x2(o[2], o[3]);
       *reinterpret_cast<u32x2*>(dst) = pk;
+      if (MODE == SHRIMP_LIN_RESID && lo_p != nullptr) {
+        *reinterpret_cast<u32x2*>(lo_p) =
+            u32x2{pack_bf16x2(o[0] - bf16_lo(pk.x), o[1] - bf16_hi(pk.x)),
+                  pack_bf16x2(o[2] - bf16_lo(pk.y), o[3] - bf16_hi(pk.y))};
+      }
     }
   }
 }
@@ -217,6 +232,9 @@ extern "C" int shrimp_linear(const shrimp_linear_args* a, void* stream) {
       SHRIMP_REQUIRE(a->resid && a->gamma, "linear: residual mode needs resid and gamma");
       SHRIMP_REQUIRE(!ln, "linear: residual mode takes no LayerNorm prologue");
       SHRIMP_REQUIRE(a->o_sr % 4 == 0 && a->r_sr % 4 == 0, "linear: row strides %% 4");
+      SHRIMP_REQUIRE(!a->tok_lo || (a->S > 0 && a->rows % a->S == 0 && a->n_tokens >= 0 &&
+                                    a->n_tokens <= a->S),
+                     "linear: token low parts need rows = whole positions of S rows");
       return dispatch_k<SHRIMP_LIN_RESID, false>(a, xb, wb, st);
     case SHRIMP_LIN_QKV:
       SHRIMP_REQUIRE(a->out_features % 3 == 0, "linear: qkv out_features %% 3");

@@ -4,6 +4,12 @@
 //   s1  = seq + g_attn * (m * (att . Wo^T + bo))          (out_proj, LayerScale)
 //   h   = GELU_erf(LN2(s1) . W1^T + b1)                   (fc1, hidden 2C)
 //   seq = s1 + g_mlp * (m * (h . W2^T + b2))              (fc2, LayerScale)
+// s1 stays in fp32 inside the kernel: it is the fc2 accumulators' starting
+// value, so only the block's result is rounded to bf16. The summary-token
+// rows carry the rounding remainder as a second bf16 (tok_lo), so their
+// residual stream keeps about 16 significant bits across the blocks (the
+// reference's autocast serve keeps the stream in fp32; the tokens feed the
+// value heads).
 //
 // The per-channel factors are folded into the weights once, at pack time
 // (shrimp_pack_attn_mlp):
@@ -11,8 +17,9 @@
 //   W1' = W1 diag(ln_w),    b1' = b1 + W1 ln_b
 //   W2' = diag(g_mlp) W2,   b2' = g_mlp * b2
 // so per row the kernel computes
-//   s1 = seq + (att . Wo'^T + bo'),  n = (s1 - mean) * rstd,
-//   h = GELU(n . W1'^T + b1'),       seq = bf16(s1) + (h . W2'^T + b2')
+//   s1 = seq + lo + (att . Wo'^T + bo'),  n = (s1 - mean) * rstd,
+//   h = GELU(n . W1'^T + b1'),            v = (s1 + b2') + h . W2'^T,
+//   seq = bf16(v), token rows: lo = bf16(v - seq)
 // with n and h in bf16 as MFMA inputs. Rows with m = 0 are left untouched
 // (their updates are multiplied by 0), so the math runs unmasked and only
 // live rows store.
@@ -103,16 +110,20 @@ SHRIMP_DEV void load_s(const shrimp_mlp_args& a, __amdgpu_buffer_rsrc_t sr, int 
 }
 
 // One block of 16 rows (lane: row lane % 16, channel group lane / 16); xf:
-// the block's attention-output fragments.
+// the block's attention-output fragments; loff: this lane's byte offset in
+// the token low parts (lor), past the resource for cell rows.
 SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, const MlpBias& bias,
-                          __amdgpu_buffer_rsrc_t sr, const u32x4 (&xf)[MC / 32], int row,
-                          int lane, bool store) {
+                          __amdgpu_buffer_rsrc_t sr, __amdgpu_buffer_rsrc_t lor, uint32_t loff,
+                          const u32x4 (&xf)[MC / 32], int row, int lane, bool store) {
   constexpr int KS1 = MC / 32, NB1 = MC / 16, NBH = MH / 16, KT = MH / 32, NB2 = MC / 16;
   constexpr int TB1 = NB1, TB2 = NB1 + NBH;  // first bias block of b1', b2'
   const int lg = lane >> 4;
-  // the block's residual rows, consumed after out_proj
-  u32x2 sin[MC / 16];
+  // the block's residual rows and their low parts (zeros for cells), consumed
+  // after out_proj
+  u32x2 sin[MC / 16], slo[MC / 16];
   load_s(a, sr, row, lg, sin);
+#pragma unroll
+  for (int nb = 0; nb < NB1; ++nb) slo[nb] = buf_load8(lor, loff + nb * 32);
 
   // accumulators start at the biases
   f32x4 acc[NB1];
@@ -133,17 +144,18 @@ SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, con
   }
 
   // ---- residual 1, LayerNorm 2 (affine folded into W1', b1') ---------------
-  // s1 is kept as bf16 for the second residual; LayerNorm reads its fp32 value.
-  u32x2 sp[NB1];
+  // s1 (fp32) is the fc2 accumulators' starting value, added to b2'.
+  f32x4 acc2[NB2];
   float v[NB1][4];
 #pragma unroll
   for (int nb = 0; nb < NB1; ++nb) {
-    v[nb][0] = acc[nb][0] + bf16_lo(sin[nb].x);
-    v[nb][1] = acc[nb][1] + bf16_hi(sin[nb].x);
-    v[nb][2] = acc[nb][2] + bf16_lo(sin[nb].y);
-    v[nb][3] = acc[nb][3] + bf16_hi(sin[nb].y);
-    sp[nb].x = pack_bf16x2(v[nb][0], v[nb][1]);
-    sp[nb].y = pack_bf16x2(v[nb][2], v[nb][3]);
+    v[nb][0] = acc[nb][0] + (bf16_lo(sin[nb].x) + bf16_lo(slo[nb].x));
+    v[nb][1] = acc[nb][1] + (bf16_hi(sin[nb].x) + bf16_hi(slo[nb].x));
+    v[nb][2] = acc[nb][2] + (bf16_lo(sin[nb].y) + bf16_lo(slo[nb].y));
+    v[nb][3] = acc[nb][3] + (bf16_hi(sin[nb].y) + bf16_hi(slo[nb].y));
+    const f32x4 b2 = bias.rows(TB2 + nb);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc2[nb][j] = b2[j] + v[nb][j];
   }
   float s = 0.f;
 #pragma unroll
@@ -172,9 +184,6 @@ SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, con
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- fc1 -> GELU -> fc2, one 32-wide hidden slice at a time ---------------
-  f32x4 acc2[NB2];
-#pragma unroll
-  for (int nb = 0; nb < NB2; ++nb) acc2[nb] = bias.rows(TB2 + nb);
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt) {
     f32x4 ah[2];
@@ -207,15 +216,18 @@ SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, con
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // ---- residual 2 -> seq ----------------------------------------------------
+  // ---- residual 2 -> seq (and the token rows' low parts) ----------------------
   if (store) {
     unsigned short* op = static_cast<unsigned short*>(a.seq) + (int64_t)row * a.s_sr + lg * 4;
 #pragma unroll
     for (int nb = 0; nb < NB2; ++nb) {
-      u32x2 pk;
-      pk.x = pack_bf16x2(acc2[nb][0] + bf16_lo(sp[nb].x), acc2[nb][1] + bf16_hi(sp[nb].x));
-      pk.y = pack_bf16x2(acc2[nb][2] + bf16_lo(sp[nb].y), acc2[nb][3] + bf16_hi(sp[nb].y));
+      u32x2 pk, lo;
+      pk.x = pack_bf16x2(acc2[nb][0], acc2[nb][1]);
+      pk.y = pack_bf16x2(acc2[nb][2], acc2[nb][3]);
+      lo.x = pack_bf16x2(acc2[nb][0] - bf16_lo(pk.x), acc2[nb][1] - bf16_hi(pk.x));
+      lo.y = pack_bf16x2(acc2[nb][2] - bf16_lo(pk.y), acc2[nb][3] - bf16_hi(pk.y));
       *reinterpret_cast<u32x2*>(op + nb * 16) = pk;
+      __builtin_amdgcn_raw_buffer_store_b64(lo, lor, loff + nb * 32, 0, 0);
     }
   }
 }
@@ -224,7 +236,8 @@ SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, con
 
 __global__ __launch_bounds__(MWAVES * 64, 1) void attn_mlp_kernel(const shrimp_mlp_args a,
                                                                   uint32_t x_bytes,
-                                                                  uint32_t s_bytes) {
+                                                                  uint32_t s_bytes,
+                                                                  uint32_t lo_bytes) {
   extern __shared__ __attribute__((aligned(16))) unsigned char wl[];
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
@@ -250,6 +263,9 @@ __global__ __launch_bounds__(MWAVES * 64, 1) void attn_mlp_kernel(const shrimp_m
             lane);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes);
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.seq, s_bytes);
+  // token low parts: lo_bytes is 0 without them (every access reads zeros /
+  // is dropped)
+  const __amdgpu_buffer_rsrc_t lor = make_rsrc(a.tok_lo, lo_bytes);
   // row mask bytes: rows at or past `rows` read as 0 (not stored)
   const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.mask, (uint32_t)a.rows);
   // Contiguous, balanced range of 16-row blocks per wave; the next block's
@@ -274,8 +290,13 @@ __global__ __launch_bounds__(MWAVES * 64, 1) void attn_mlp_kernel(const shrimp_m
     // the next block's mask byte ahead of this block's rows: a wait for it
     // never waits for them
     mnxt = load_m(nrow);
-    load_x(a, xr, blk * 16 + lr, lg, cur);
-    mlp_block(a, wl, bias, sr, cur, blk * 16 + lr, lane, mcur != 0);
+    const int row = blk * 16 + lr;
+    const int pos = row / a.S, srow = row - pos * a.S;
+    const uint32_t loff = row < a.rows && srow < a.n_tokens
+                              ? (uint32_t)(((pos * a.n_tokens + srow) * MC + lg * 4) * 2)
+                              : SHRIMP_OOB_OFFSET;
+    load_x(a, xr, row, lg, cur);
+    mlp_block(a, wl, bias, sr, lor, loff, cur, row, lane, mcur != 0);
   }
 }
 
@@ -361,6 +382,11 @@ extern "C" int shrimp_attn_mlp(const shrimp_mlp_args* a, void* stream) {
   const int64_t se = ((int64_t)(a->rows - 1) * a->s_sr + MC) * 2;
   SHRIMP_REQUIRE(xe < (int64_t)0x7FFF0000 && se < (int64_t)0x7FFF0000,
                  "attn_mlp: activation buffer too large");
+  SHRIMP_REQUIRE(a->S > 0 && a->rows % a->S == 0 && a->n_tokens >= 0 && a->n_tokens <= a->S,
+                 "attn_mlp: rows must be whole positions of S rows (rows %d, S %d, tokens %d)",
+                 a->rows, a->S, a->n_tokens);
+  const int64_t lob = a->tok_lo ? (int64_t)(a->rows / a->S) * a->n_tokens * MC * 2 : 0;
+  SHRIMP_REQUIRE(lob < (int64_t)0x7FFF0000, "attn_mlp: token low parts too large");
   SHRIMP_REQUIRE((size_t)max_lds_per_block() >= W_LDS,
                  "attn_mlp: needs %u bytes of LDS per workgroup", (unsigned)W_LDS);
   int dev = 0, cus = 0;
@@ -373,6 +399,6 @@ extern "C" int shrimp_attn_mlp(const shrimp_mlp_args* a, void* stream) {
   // row counts spread over more units, each staging the weights once
   const int grid = (int)std::min<int64_t>(cus, std::max<int64_t>((nblk + MWAVES - 1) / MWAVES, (nblk + 3) / 4));
   hipLaunchKernelGGL(attn_mlp_kernel, dim3(grid), dim3(MWAVES * 64), W_LDS, as_stream(stream), *a,
-                     (uint32_t)xe, (uint32_t)se);
+                     (uint32_t)xe, (uint32_t)se, (uint32_t)lob);
   return check_launch("attn_mlp");
 }

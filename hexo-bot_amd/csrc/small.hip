@@ -196,10 +196,15 @@ __global__ __launch_bounds__(256) void prep_csr_kernel(const uint16_t* __restric
 }
 
 __global__ void fill_tokens_kernel(const float* __restrict__ tokens, int n_tokens, int C,
-                                   uint16_t* __restrict__ seq, int64_t seq_sb) {
+                                   uint16_t* __restrict__ seq, int64_t seq_sb,
+                                   uint16_t* __restrict__ tok_lo) {
   const int b = blockIdx.x;
-  for (int i = threadIdx.x; i < n_tokens * C; i += blockDim.x)
-    seq[(int64_t)b * seq_sb + i] = f32_to_bf16_bits(tokens[i]);
+  for (int i = threadIdx.x; i < n_tokens * C; i += blockDim.x) {
+    const float t = tokens[i];
+    const uint16_t hi = f32_to_bf16_bits(t);
+    seq[(int64_t)b * seq_sb + i] = hi;
+    if (tok_lo) tok_lo[(int64_t)b * n_tokens * C + i] = f32_to_bf16_bits(t - bf16_bits_to_f32(hi));
+  }
 }
 
 // ---- trunk tail + value heads (model.py:927-935, 990-1002) --------------------
@@ -229,7 +234,8 @@ SHRIMP_DEV float row_group_sum(float v) {
 // F32: seq and out_seq hold fp32 rows instead of bf16 (the fp32 serve mode).
 template <int TPR, bool F32>
 __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a, uint32_t seq_bytes,
-                                                       uint32_t mask_bytes, uint32_t ws_bytes) {
+                                                       uint32_t mask_bytes, uint32_t ws_bytes,
+                                                       uint32_t lo_bytes) {
   constexpr int RPP = 256 / TPR;  // rows per pass
   constexpr int U = F32 ? 4 : 17;  // passes per chunk (bf16, C = 128: a position of up to 272 rows)
   constexpr int EB = F32 ? 4 : 2;  // bytes per element
@@ -245,6 +251,9 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a,
   const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.out_seq, seq_bytes);
   const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.mask, mask_bytes);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.workspace, ws_bytes);
+  // token rows' low parts (lo_bytes 0 without them: reads give zeros); the
+  // tokens are rows 0 .. nt - 1, all in the first pass (nt <= RPP)
+  const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.tok_lo, lo_bytes);
   const uint32_t pos_off = (uint32_t)((int64_t)b * a.s_sb * EB);
   const uint32_t vin_off = (uint32_t)((int64_t)b * 6 * C * 4);
   float w[8], bb[8], pool[8];
@@ -262,7 +271,10 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a,
     return row < S && cv ? pos_off + (uint32_t)((row * C + c0) * EB) : SHRIMP_OOB_OFFSET;
   };
   constexpr int U2 = F32 ? U : 1;  // second 16 bytes of an fp32 row chunk
-  auto load = [&](int chunk, u32x4 (&raw)[U], u32x4 (&raw2)[U2], unsigned (&mk)[U]) {
+  auto load = [&](int chunk, u32x4 (&raw)[U], u32x4 (&raw2)[U2], unsigned (&mk)[U], u32x4& lo0) {
+    lo0 = buf_load16(lr, chunk == 0 && rs < nt && cv
+                             ? (uint32_t)((((int64_t)b * nt + rs) * C + c0) * 2)
+                             : SHRIMP_OOB_OFFSET);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int row = chunk * U * RPP + u * RPP + rs;
@@ -275,9 +287,9 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a,
     }
   };
   for (int ch = 0; ch < nchunk; ++ch) {
-    u32x4 raw[U], raw2[U2];
+    u32x4 raw[U], raw2[U2], lo0;
     unsigned mk[U];
-    load(ch, raw, raw2, mk);
+    load(ch, raw, raw2, mk, lo0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int row = ch * U * RPP + u * RPP + rs;
@@ -288,6 +300,9 @@ __global__ __launch_bounds__(256) void final_ln_kernel(const shrimp_tail_args a,
         if constexpr (F32) {
           x[e] = __uint_as_float(raw[u][e]);
           x[4 + e] = __uint_as_float(raw2[u][e]);
+        } else if (u == 0) {
+          x[2 * e] = bf16_lo(raw[u][e]) + bf16_lo(lo0[e]);
+          x[2 * e + 1] = bf16_hi(raw[u][e]) + bf16_hi(lo0[e]);
         } else {
           x[2 * e] = bf16_lo(raw[u][e]);
           x[2 * e + 1] = bf16_hi(raw[u][e]);
@@ -642,11 +657,12 @@ extern "C" int shrimp_prep_csr(const void* node_feats, int nfeat, const int16_t*
 }
 
 extern "C" int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void* seq,
-                                  int64_t seq_sb, int B, void* stream) {
+                                  int64_t seq_sb, void* tok_lo, int B, void* stream) {
   SHRIMP_REQUIRE(tokens && seq, "fill_tokens: null pointer");
   if (B == 0 || n_tokens == 0) return SHRIMP_OK;
   hipLaunchKernelGGL(fill_tokens_kernel, dim3(B), dim3(256), 0, as_stream(stream), tokens,
-                     n_tokens, C, static_cast<uint16_t*>(seq), seq_sb);
+                     n_tokens, C, static_cast<uint16_t*>(seq), seq_sb,
+                     static_cast<uint16_t*>(tok_lo));
   return check_launch("fill_tokens");
 }
 
@@ -666,11 +682,15 @@ static int launch_trunk_tail(const shrimp_tail_args* a, float* ws, hipStream_t s
   SHRIMP_REQUIRE(a->C % 8 == 0 && a->C <= 256 && a->s_sb % 8 == 0,
                  "trunk_tail: C %d must be a multiple of 8 (<= 256), position stride of 8", a->C);
   SHRIMP_REQUIRE(a->bins > 0 && a->bins <= 256, "trunk_tail: bins %d", a->bins);
+  SHRIMP_REQUIRE(!a->tok_lo || !f32, "trunk_tail_f32: token low parts apply to the bf16 stream only");
+  SHRIMP_REQUIRE(a->n_tokens <= 8 * (256 / a->C), "trunk_tail: %d tokens exceed one pass of rows",
+                 a->n_tokens);
   shrimp_tail_args k = *a;
   k.workspace = ws;
   const int64_t seq_bytes = ((int64_t)(k.B - 1) * k.s_sb + (int64_t)k.S * k.C) * (f32 ? 4 : 2);
   const int64_t mask_bytes = (int64_t)k.B * (k.S - k.n_tokens);
   const int64_t ws_bytes = (int64_t)k.B * 6 * k.C * 4;
+  const int64_t lo_bytes = k.tok_lo ? (int64_t)k.B * k.n_tokens * k.C * 2 : 0;
   SHRIMP_REQUIRE(seq_bytes < (int64_t)0x7FFF0000 && ws_bytes < (int64_t)0x7FFF0000,
                  "trunk_tail: buffers too large for 32-bit offsets");
   const int tpr = k.C / 8;
@@ -680,10 +700,12 @@ static int launch_trunk_tail(const shrimp_tail_args* a, float* ws, hipStream_t s
   do {                                                                                       \
     if (f32)                                                                                 \
       hipLaunchKernelGGL((final_ln_kernel<T, true>), dim3(k.B), dim3(256), lsm, st, k,         \
-                         (uint32_t)seq_bytes, (uint32_t)mask_bytes, (uint32_t)ws_bytes);       \
+                         (uint32_t)seq_bytes, (uint32_t)mask_bytes, (uint32_t)ws_bytes,        \
+                         (uint32_t)lo_bytes);                                                  \
     else                                                                                     \
       hipLaunchKernelGGL((final_ln_kernel<T, false>), dim3(k.B), dim3(256), lsm, st, k,        \
-                         (uint32_t)seq_bytes, (uint32_t)mask_bytes, (uint32_t)ws_bytes);       \
+                         (uint32_t)seq_bytes, (uint32_t)mask_bytes, (uint32_t)ws_bytes,        \
+                         (uint32_t)lo_bytes);                                                  \
   } while (0)
   if (tpr <= 4) SHRIMP_FLN(4);
   else if (tpr <= 8) SHRIMP_FLN(8);

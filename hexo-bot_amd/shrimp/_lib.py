@@ -45,6 +45,7 @@ class LinearArgs(ctypes.Structure):
         ("out", _vp), ("o_sr", _i64),
         ("rows", _i32), ("in_features", _i32), ("out_features", _i32),
         ("B", _i32), ("S", _i32), ("H", _i32), ("dpad", _i32),
+        ("tok_lo", _vp), ("n_tokens", _i32),
     ]
 
 
@@ -74,6 +75,7 @@ class TailArgs(ctypes.Structure):
         ("mr_w", _vp), ("mr_b", _vp), ("mh_w", _vp), ("mh_b", _vp), ("moves_left", _vp),
         ("workspace", _vp),
         ("B", _i32), ("S", _i32), ("n_tokens", _i32), ("C", _i32), ("bins", _i32),
+        ("tok_lo", _vp),
     ]
 
 
@@ -96,6 +98,7 @@ class MlpArgs(ctypes.Structure):
     _fields_ = [
         ("x", _vp), ("x_sr", _i64), ("seq", _vp), ("s_sr", _i64), ("mask", _vp),
         ("packed", _vp), ("eps", _f32), ("rows", _i32), ("C", _i32), ("hidden", _i32),
+        ("tok_lo", _vp), ("S", _i32), ("n_tokens", _i32),
     ]
 
 
@@ -174,7 +177,7 @@ SIGNATURES: dict = {
         + [_vp] * 7,
     ),
     "shrimp_fill_tokens": (
-        ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _i64, ctypes.c_int, _vp]
+        ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _i64, _vp, ctypes.c_int, _vp]
     ),
     "shrimp_trunk_tail": (ctypes.c_int, [ctypes.POINTER(TailArgs), _vp]),
     "shrimp_policy_tail_supported": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),

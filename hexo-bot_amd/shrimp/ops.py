@@ -244,14 +244,18 @@ def launch_conv_block_pair(*, x, x_sb, x_sn, idx, idx_stride, mask8, B, N, C, bl
 
 def launch_linear(
     *, x, x_sr, wpack, bias, rows, n_in, n_out, mode, out, o_sr=0, ln_w=None, ln_b=None,
-    eps=1e-5, resid=None, r_sr=0, gamma=None, mask=None, B=0, S=0, H=0, dpad=0, stream=None,
+    eps=1e-5, resid=None, r_sr=0, gamma=None, mask=None, B=0, S=0, H=0, dpad=0,
+    tok_lo=None, n_tokens=0, stream=None,
 ):
+    """shrimp_linear; in the RESID mode ``tok_lo`` (B, n_tokens, n_out) bf16
+    carries the low parts of the token rows (rows r with r % S < n_tokens)."""
+
     a = _lib.LinearArgs(
         x=x.data_ptr(), x_sr=x_sr, w=wpack.data_ptr(), bias=bias.data_ptr(),
         ln_w=_lib.ptr(ln_w), ln_b=_lib.ptr(ln_b), eps=float(eps), mode=mode,
         resid=_lib.ptr(resid), r_sr=r_sr, gamma=_lib.ptr(gamma), mask=_lib.ptr(mask),
         out=out.data_ptr(), o_sr=o_sr, rows=rows, in_features=n_in, out_features=n_out,
-        B=B, S=S, H=H, dpad=dpad,
+        B=B, S=S, H=H, dpad=dpad, tok_lo=_lib.ptr(tok_lo), n_tokens=n_tokens,
     )
     s = _lib.stream_handle() if stream is None else stream
     _lib.check(_lib.load().shrimp_linear(ctypes_ref(a), s), "linear")
@@ -266,12 +270,17 @@ def launch_attn_qkv(*, x, x_sr, qkv, packed, eps, rows, B, S, H, C, dpad, stream
     _lib.check(_lib.load().shrimp_attn_qkv(ctypes_ref(a), s), "attn_qkv")
 
 
-def launch_attn_mlp(*, x, x_sr, seq, s_sr, mask, packed, eps, rows, C, hidden, stream=None):
-    """Fused out_proj + residual + LN2 + fc1 + GELU + fc2 + residual, seq in place."""
+def launch_attn_mlp(*, x, x_sr, seq, s_sr, mask, packed, eps, rows, C, hidden, tok_lo=None,
+                    S=None, n_tokens=0, stream=None):
+    """Fused out_proj + residual + LN2 + fc1 + GELU + fc2 + residual, seq in
+    place; ``tok_lo`` (B, n_tokens, C) bf16 carries the low parts of the token
+    rows (the first n_tokens of every S rows). Without S the rows are one
+    position."""
 
     a = _lib.MlpArgs(
         x=x.data_ptr(), x_sr=x_sr, seq=seq.data_ptr(), s_sr=s_sr, mask=mask.data_ptr(),
         packed=packed.data_ptr(), eps=float(eps), rows=rows, C=C, hidden=hidden,
+        tok_lo=_lib.ptr(tok_lo), S=rows if S is None else S, n_tokens=n_tokens,
     )
     s = _lib.stream_handle() if stream is None else stream
     _lib.check(_lib.load().shrimp_attn_mlp(ctypes_ref(a), s), "attn_mlp")

@@ -588,8 +588,12 @@ class HipForward:
         idx, mask8, coords32 = pb.idx, pb.mask8, pb.coords32
         seq_lens, seq_mask, xin = pb.seq_lens, pb.seq_mask, pb.xin
         seq = torch.empty((B, S, C), dtype=bf, device=dev)
+        # the token rows' residual stream is seq (bf16) + tok_lo (bf16): the
+        # rounding remainder of every update, kept by the residual kernels
+        tok_lo = torch.empty((B, NUM_TOKENS, C), dtype=bf, device=dev)
         _lib.check(
-            lib.shrimp_fill_tokens(P.tokens.data_ptr(), NUM_TOKENS, C, seq.data_ptr(), S * C, B, st),
+            lib.shrimp_fill_tokens(P.tokens.data_ptr(), NUM_TOKENS, C, seq.data_ptr(), S * C,
+                                   tok_lo.data_ptr(), B, st),
             "fill_tokens",
         )
         cells = seq[:, NUM_TOKENS:]
@@ -711,14 +715,15 @@ class HipForward:
                 if fused:
                     launch_attn_mlp(
                         x=att, x_sr=C, seq=seq, s_sr=C, mask=seq_mask, packed=a.mlp,
-                        eps=a.eps2, rows=rows, C=C, hidden=2 * C, stream=st,
+                        eps=a.eps2, rows=rows, C=C, hidden=2 * C, tok_lo=tok_lo, S=S,
+                        n_tokens=NUM_TOKENS, stream=st,
                     )
                     self._mark("mlp")
                     continue
                 launch_linear(
                     x=att, x_sr=C, wpack=a.out_w, bias=a.out_b, rows=rows, n_in=C, n_out=C,
                     mode=_lib.LIN_RESID, out=seq, o_sr=C, resid=seq, r_sr=C, gamma=a.g_attn,
-                    mask=seq_mask, stream=st,
+                    mask=seq_mask, S=S, tok_lo=tok_lo, n_tokens=NUM_TOKENS, stream=st,
                 )
                 launch_linear(
                     x=seq, x_sr=C, wpack=a.fc1_w, bias=a.fc1_b, rows=rows, n_in=C, n_out=2 * C,
@@ -728,7 +733,8 @@ class HipForward:
                 launch_linear(
                     x=hid, x_sr=2 * C, wpack=a.fc2_w, bias=a.fc2_b, rows=rows, n_in=2 * C,
                     n_out=C, mode=_lib.LIN_RESID, out=seq, o_sr=C, resid=seq, r_sr=C,
-                    gamma=a.g_mlp, mask=seq_mask, stream=st,
+                    gamma=a.g_mlp, mask=seq_mask, S=S, tok_lo=tok_lo, n_tokens=NUM_TOKENS,
+                    stream=st,
                 )
                 self._mark("mlp")
 
@@ -743,7 +749,7 @@ class HipForward:
             vh_b=P.value.hb.data_ptr(), value=value.data_ptr(),
             mr_w=P.ml.rw.data_ptr(), mr_b=P.ml.rb.data_ptr(), mh_w=P.ml.hw.data_ptr(),
             mh_b=P.ml.hb.data_ptr(), moves_left=_lib.ptr(ml), workspace=tail_ws.data_ptr(),
-            B=B, S=S, n_tokens=NUM_TOKENS, C=C, bins=VALUE_BINS,
+            B=B, S=S, n_tokens=NUM_TOKENS, C=C, bins=VALUE_BINS, tok_lo=tok_lo.data_ptr(),
         )
         policy = torch.empty((B, N), dtype=torch.float32, device=dev)
         if (self.use_fused_tail and not self.keep_buffers and 2 * B > self._cus(dev)
@@ -774,6 +780,7 @@ class HipForward:
                 P=P, B=B, N=N, S=S, idx=idx, mask8=mask8, coords32=coords32, seq_lens=seq_lens,
                 seq_mask=seq_mask, seq=seq, y1=y1, qkv=qkv, att=att, hid=hid, seqf=seqf,
                 stream=st, attn_fused=attn_fused, staged=staged, kvf=kvf, meta=meta,
+                tok_lo=tok_lo,
             )
         return out
 

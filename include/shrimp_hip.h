@@ -165,6 +165,10 @@ int shrimp_conv_block_pair(const shrimp_conv_args* c1, const shrimp_conv_args* c
  *   y = a @ W^T + bias                                      (fp32 acc)
  *   mode PLAIN: out = y (bf16)          mode GELU: out = gelu_erf(y)
  *   mode RESID: out[r] = resid[r] + gamma * (mask[r] ? y : 0)   (out may alias resid)
+ *               with tok_lo set, the token rows (r % S < n_tokens) carry a low part:
+ *               v = resid[r] + lo[r] + gamma * y, out[r] = bf16(v),
+ *               lo[r] = bf16(v - out[r]), lo[r] = tok_lo[((r / S) * n_tokens +
+ *               r % S) * out_features ..] (bf16; may alias its input)
  *   mode QKV:  y split into q/k/v, heads, stored to qkv (3, B, H, S, dpad)
  * Rows r = (b, s) over B positions x S rows; x, out, resid strides per row
  * are given in elements; mask is per (b, s) (seq mask) or NULL.
@@ -190,8 +194,11 @@ typedef struct {
   void* out;
   int64_t o_sr;
   int32_t rows, in_features, out_features;
-  /* QKV mode */
+  /* QKV mode (and S for the RESID mode's token rows) */
   int32_t B, S, H, dpad;
+  /* RESID mode: low parts of the token rows (B, n_tokens, out_features) bf16, or NULL */
+  void* tok_lo;
+  int32_t n_tokens;
 } shrimp_linear_args;
 
 int shrimp_linear(const shrimp_linear_args* a, void* stream);
@@ -227,13 +234,19 @@ int shrimp_attn_qkv(const shrimp_qkv_args* a, void* stream);
  * Fused attention-block tail (AttnBlock.forward after the attention core,
  * model.py:508-514; replaces the out_proj / fc1 / fc2 nn.Linear calls, LN2
  * and the two LayerScale residuals):
- *   s1  = seq + g_attn * (mask ? x @ Wo^T + bo : 0)
+ *   s1  = seq + lo + g_attn * (mask ? x @ Wo^T + bo : 0)          (fp32)
  *   h   = bf16(gelu_erf(LN2(s1) @ W1^T + b1))
- *   seq = bf16(bf16(s1) + g_mlp * (mask ? h @ W2^T + b2 : 0))   (in place)
+ *   v   = s1 + g_mlp * (mask ? h @ W2^T + b2 : 0)                (fp32)
+ *   seq = bf16(v) (in place);  token rows: lo = bf16(v - seq)
  * x: attention output rows (bf16), seq: residual stream rows (bf16), both
  * with element row strides; mask: per-row live flag (rows with mask 0 are
- * not written: their update is 0). C = 128, hidden = 256: the packed weights
- * (160 KiB of fragments) fill one workgroup's LDS.
+ * not written: their update is 0). lo: the low part of a token row (row r
+ * with r % S < n_tokens) at tok_lo[((r / S) * n_tokens + r % S) * C ..]
+ * (bf16, read and written in place), 0 for cell rows and when tok_lo is NULL;
+ * the summary tokens feed the value heads, so their residual stream is kept
+ * to about 16 significant bits, as the reference's autocast serve keeps it in
+ * fp32. C = 128, hidden = 256: the packed weights (160 KiB of fragments) fill
+ * one workgroup's LDS.
  *
  * shrimp_pack_attn_mlp folds g_attn into Wo / bo, LN2's affine into W1 / b1
  * and g_mlp into W2 / b2, then writes MFMA fragments and the folded biases to
@@ -264,6 +277,8 @@ typedef struct {
   const void* packed;   /* shrimp_pack_attn_mlp output */
   float eps;            /* LN2 epsilon */
   int32_t rows, C, hidden;
+  void* tok_lo;         /* (B, n_tokens, C) bf16 low parts of the token rows, or NULL */
+  int32_t S, n_tokens;  /* rows per position, token rows per position */
 } shrimp_mlp_args;
 
 size_t shrimp_attn_mlp_pack_bytes(int C, int hidden);
@@ -409,10 +424,12 @@ int shrimp_prep_csr(const void* node_feats, int nfeat, const int16_t* node_qr, c
                     uint8_t* mask8, int32_t* coords32, int32_t* seq_lens, uint8_t* seq_mask,
                     void* xin, void* stream);
 
-/* seq[b, t, :] = tokens[t, :] (bf16) for t < n_tokens; seq rows are C apart,
- * positions seq_sb apart. */
-int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void* seq, int64_t seq_sb, int B,
-                       void* stream);
+/* seq[b, t, :] = bf16(tokens[t, :]) for t < n_tokens; seq rows are C apart,
+ * positions seq_sb apart. tok_lo (optional, (B, n_tokens, C) bf16):
+ * tok_lo[b, t, :] = bf16(tokens[t, :] - seq[b, t, :]), the low parts that the
+ * residual kernels carry for the token rows. */
+int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void* seq, int64_t seq_sb,
+                       void* tok_lo, int B, void* stream);
 
 /* ------------------------------------------------------------------------
  * Featurizer on the device (support.py:84-205 build_support, features.py:80-240
@@ -443,7 +460,8 @@ int shrimp_featurize(const int32_t* rec_qr, const uint8_t* rec_owner, const int3
 
 /* ------------------------------------------------------------------------
  * Trunk tail + value head (model.py:927-935, 990-1002):
- *   seq_f = LayerNorm(seq) (all S rows, fp32 stats), cell rows * mask -> out_seq (bf16)
+ *   seq_f = LayerNorm(seq) (all S rows, fp32 stats), cell rows * mask -> out_seq (bf16);
+ *           token rows are seq + tok_lo when tok_lo is set (bf16 seq only)
  *   pooled = masked mean of the normalized cells (count clamped to 1)
  *   value = value_head(relu(value_reduction([T0, T1, pooled])))  -> value (B, 65) fp32
  *   moves_left likewise from [T4, T5, pooled] when moves_left is non-NULL.
@@ -467,6 +485,7 @@ typedef struct {
   float* moves_left;
   float* workspace; /* (B, 6C) */
   int32_t B, S, n_tokens, C, bins;
+  const void* tok_lo; /* (B, n_tokens, C) bf16 low parts of the token rows, or NULL */
 } shrimp_tail_args;
 
 int shrimp_trunk_tail(const shrimp_tail_args* a, void* stream);

@@ -27,7 +27,7 @@ int main(void) {
   F(shrimp_linear_args, out); F(shrimp_linear_args, o_sr); F(shrimp_linear_args, rows);
   F(shrimp_linear_args, in_features); F(shrimp_linear_args, out_features);
   F(shrimp_linear_args, B); F(shrimp_linear_args, S); F(shrimp_linear_args, H);
-  F(shrimp_linear_args, dpad);
+  F(shrimp_linear_args, dpad); F(shrimp_linear_args, tok_lo); F(shrimp_linear_args, n_tokens);
   Z(shrimp_attn_args);
   F(shrimp_attn_args, q); F(shrimp_attn_args, k); F(shrimp_attn_args, v);
   F(shrimp_attn_args, qkv_sb); F(shrimp_attn_args, qkv_sh); F(shrimp_attn_args, seq_lens);
@@ -50,7 +50,7 @@ int main(void) {
   F(shrimp_tail_args, mh_b); F(shrimp_tail_args, moves_left); F(shrimp_tail_args, workspace);
   F(shrimp_tail_args, B);
   F(shrimp_tail_args, S); F(shrimp_tail_args, n_tokens); F(shrimp_tail_args, C);
-  F(shrimp_tail_args, bins);
+  F(shrimp_tail_args, bins); F(shrimp_tail_args, tok_lo);
   Z(shrimp_qkv_args);
   F(shrimp_qkv_args, x); F(shrimp_qkv_args, x_sr); F(shrimp_qkv_args, qkv);
   F(shrimp_qkv_args, packed); F(shrimp_qkv_args, eps); F(shrimp_qkv_args, rows);
@@ -65,7 +65,8 @@ int main(void) {
   F(shrimp_mlp_args, x); F(shrimp_mlp_args, x_sr); F(shrimp_mlp_args, seq);
   F(shrimp_mlp_args, s_sr); F(shrimp_mlp_args, mask); F(shrimp_mlp_args, packed);
   F(shrimp_mlp_args, eps); F(shrimp_mlp_args, rows); F(shrimp_mlp_args, C);
-  F(shrimp_mlp_args, hidden);
+  F(shrimp_mlp_args, hidden); F(shrimp_mlp_args, tok_lo); F(shrimp_mlp_args, S);
+  F(shrimp_mlp_args, n_tokens);
   Z(shrimp_ray_attn_args);
   F(shrimp_ray_attn_args, q); F(shrimp_ray_attn_args, k); F(shrimp_ray_attn_args, v);
   F(shrimp_ray_attn_args, q_sb); F(shrimp_ray_attn_args, q_sh); F(shrimp_ray_attn_args, q_sn);

@@ -118,6 +118,36 @@ def test_forward_cfg4_matches_oracle(cfg4_batch):
     _check_trunk(out, want, b["mask"], "cfg4 B=32")
 
 
+def test_forward_cfg4_b512_matches_oracle():
+    """Config 4 at the batch the benchmark is quoted on: the bench's own 512
+    positions (seeded L256 generator, Npad 256), C=128, H=8, 12 blocks, the
+    "heads" weights (O(1) logits), through forward_policy_value against the
+    fp32 oracle (the reference's CPU path restated). Prints each output's
+    largest error and the share of its gate it uses."""
+
+    from shrimp import synthetic
+
+    b = synthetic.position_batch("cfg4", 512)
+    assert b["mask"].shape == (512, 256)
+    layout = "CCACCACCACCA"
+    sd = weights.make_state_dict(128, 8, layout, seed=5, mode="heads")
+    net = _net(128, 8, layout, seed=5, mode="heads")
+    print("cfg4 B=512 forward", flush=True)
+    out = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"], trunk=True)
+    print("cfg4 B=512 oracle", flush=True)
+    want = ofwd.forward_policy_value(sd, layout, 8, b["feats"], b["nbr"], b["mask"], b["coords"],
+                                     request_moves_left=True, dtype=torch.float32,
+                                     return_trunk=True)
+    for key in ("policy", "value", "moves_left"):
+        err = (out[key] - want[key].double()).abs().max().item()
+        print(f"cfg4 B=512 {key}: max abs err {err:.3e} = {100 * err / TOL:.0f}% of the "
+              f"{TOL:g} gate", flush=True)
+    v_err = (odec.decode_value(out["value"]) - odec.decode_value(want["value"].double())).abs()
+    print(f"cfg4 B=512 decoded value: max abs err {v_err.max().item():.3e}", flush=True)
+    _check(out, want, b["mask"], "cfg4 B=512")
+    _check_trunk(out, want, b["mask"], "cfg4 B=512")
+
+
 def _wide_batch(npad):
     """Three positions padded to npad: L256 positions for 256, spec-variant
     positions (supports of 280-512 cells) for 512."""
@@ -220,14 +250,6 @@ def test_fused_and_unfused_mlp_paths_agree(cfg4_batch):
     net = _net(128, 8, "CCACCACCACCA", seed=5)
     fused = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
     rt = net.hip_runtime()
-    # the one-launch ConvBlock repeats the two-launch arithmetic exactly
-    rt.use_fused_block = False
-    try:
-        two = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
-    finally:
-        rt.use_fused_block = True
-    for key in ("policy", "value", "moves_left"):
-        assert torch.equal(fused[key], two[key]), key
     rt.use_fused_mlp = rt.use_fused_qkv = rt.use_fused_block = False
     try:
         plain = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
@@ -245,7 +267,9 @@ def test_large_batch_launch_fusions_are_bit_identical():
     final LayerNorm, pooling and policy conv as one launch; both hand rows over
     inside the workgroup instead of through HBM and must give the same bits as
     the separate launches (one ConvBlock launch per block, shrimp_trunk_tail
-    and the policy conv)."""
+    and the policy conv), and as ConvBlocks run as two conv launches each
+    (conv1 + LN + ReLU to HBM, conv2 + LN + residual). The launch names each
+    forward recorded show which kernels ran."""
 
     from shrimp import synthetic
 
@@ -253,16 +277,34 @@ def test_large_batch_launch_fusions_are_bit_identical():
     net = _net(128, 8, "CCACCACCACCA", seed=6)
     rt = net.hip_runtime()
     print("large batch fusions B=160", flush=True)
-    fused = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
-    rt.use_block_pair = rt.use_fused_tail = False
-    try:
-        plain = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
-    finally:
-        rt.use_block_pair = rt.use_fused_tail = True
-    for key in ("policy", "value", "moves_left"):
-        err = (fused[key] - plain[key]).abs().max().item()
-        print(f"fused launches vs separate {key}: {err:.3e}", flush=True)
-        assert torch.equal(fused[key], plain[key]), key
+
+    def run(**flags):
+        old = {k: getattr(rt, k) for k in flags}
+        for k, v in flags.items():
+            setattr(rt, k, v)
+        rt.timeline = []
+        try:
+            out = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"])
+            names = [n for n, _ in rt.timeline]
+        finally:
+            rt.timeline = None
+            for k, v in old.items():
+                setattr(rt, k, v)
+        return out, names
+
+    fused, n_fused = run()
+    assert n_fused.count("conv_block_pair") == 4 and "policy_tail" in n_fused, n_fused
+    plain, n_plain = run(use_block_pair=False, use_fused_tail=False)
+    assert n_plain.count("conv_block") == 8 and "conv_block_pair" not in n_plain, n_plain
+    assert "tail" in n_plain and "policy" in n_plain, n_plain
+    # one ConvBlock as two conv launches: the same arithmetic as the fused block
+    two, n_two = run(use_fused_block=False, use_fused_tail=False)
+    assert n_two.count("conv1") == 8 and n_two.count("conv2") == 8, n_two
+    for other, what in ((plain, "block launches"), (two, "two-conv blocks")):
+        for key in ("policy", "value", "moves_left"):
+            err = (fused[key] - other[key]).abs().max().item()
+            print(f"fused launches vs {what} {key}: {err:.3e}", flush=True)
+            assert torch.equal(fused[key], other[key]), (what, key)
     assert fused["value"].abs().max() > 0 and fused["policy"].abs().max() > 0
 
 

@@ -522,19 +522,8 @@ def test_linear_modes(mode, c):
         close(out, y, what="plain")
 
 
-@pytest.mark.parametrize("rows", [1, 37, 4096 + 5])
-def test_attn_mlp_fused(rows):
-    """Fused out_proj + LayerScale residual + LN2 + fc1 + GELU(erf) + fc2 +
-    residual (C=128) against a float64 restatement of AttnBlock's tail with
-    the kernel's bf16 points (MFMA inputs, s1 kept as bf16 for the second
-    residual). The kernel folds the LayerScales and LN2's affine into the
-    weights before rounding them to bf16, so the reference rounds the folded
-    weights the same way. Row counts cover a single row, a ragged block and
-    several blocks per wave; masked rows must keep their residual exactly."""
-
-    from shrimp import ops
-
-    torch.manual_seed(2)
+def _mlp_case(rows, seed=2):
+    torch.manual_seed(seed)
     c, hdim = 128, 256
     x = torch.randn(rows, c)
     seq = torch.randn(rows, c)
@@ -544,12 +533,41 @@ def test_attn_mlp_fused(rows):
     w2, b2 = torch.randn(c, hdim) * 0.06, torch.randn(c) * 0.1
     ga, gm = torch.rand(c) * 0.5 + 0.25, torch.rand(c) * 0.5 + 0.25
     lnw, lnb = torch.rand(c) + 0.5, torch.randn(c) * 0.1
+    return x, seq, m, (wo, bo, ga, lnw, lnb, w1, b1, w2, b2, gm)
 
+
+def _mlp_restated(x, s_in, m, p):
+    """AttnBlock's tail in float64 with the kernel's bf16 points (MFMA inputs:
+    x, the LayerNorm output, the GELU output and the folded weights); s1 and
+    the result stay unrounded (the kernel rounds only its stores)."""
+
+    wo, bo, ga, lnw, lnb, w1, b1, w2, b2, gm = p
+    c = x.shape[1]
     d = lambda t: t.double()
-    s1 = bf(seq) + (bf(x) @ bf(ga[:, None] * wo).T + d(ga * bo)) * d(m)[:, None]
+    s1 = d(s_in) + (bf(x) @ bf(ga[:, None] * wo).T + d(ga * bo)) * d(m)[:, None]
     n = bf(torch.nn.functional.layer_norm(s1, (c,), None, None, 1e-5))
     hid = bf(torch.nn.functional.gelu(n @ bf(w1 * lnw[None, :]).T + d(b1) + d(w1) @ d(lnb)))
-    want = bf(s1) + (hid @ bf(gm[:, None] * w2).T + d(gm * b2)) * d(m)[:, None]
+    return s1 + (hid @ bf(gm[:, None] * w2).T + d(gm * b2)) * d(m)[:, None]
+
+
+@pytest.mark.parametrize("rows", [1, 37, 4096 + 5])
+def test_attn_mlp_fused(rows):
+    """Fused out_proj + LayerScale residual + LN2 + fc1 + GELU(erf) + fc2 +
+    residual (C=128) against a float64 restatement of AttnBlock's tail with
+    the kernel's bf16 points (MFMA inputs; s1 stays fp32 inside the kernel as
+    the fc2 accumulators' start, and only the stored result is rounded). The
+    kernel folds the LayerScales and LN2's affine into the weights before
+    rounding them to bf16, so the reference rounds the folded weights the
+    same way. Row counts cover a single row, a ragged block and several
+    blocks per wave; masked rows must keep their residual exactly."""
+
+    from shrimp import ops
+
+    x, seq, m, p = _mlp_case(rows)
+    wo, bo, ga, lnw, lnb, w1, b1, w2, b2, gm = p
+    c, hdim = 128, 256
+    d = lambda t: t.double()
+    want = _mlp_restated(x, bf(seq), m, p)
     # the same block in the model's own terms (unfolded fp64): within bf16 noise
     s1u = d(seq) + d(ga) * ((d(x) @ d(wo).T + d(bo)) * d(m)[:, None])
     hu = torch.nn.functional.gelu(
@@ -565,6 +583,57 @@ def test_attn_mlp_fused(rows):
     close(seq_d, want, what=f"attn_mlp rows={rows}")
     close(seq_d, model, atol=5e-2, rtol=2e-2, what=f"attn_mlp vs model rows={rows}")
     assert torch.equal(seq_d.cpu()[~m].double(), bf(seq)[~m])
+
+
+def test_attn_mlp_token_low_parts():
+    """The token rows (the first n_tokens of every S rows) carry a second
+    bf16, their rounding remainder: the kernel reads seq + tok_lo as the
+    residual and writes the new remainder, so hi + lo follows the fp64
+    restatement to about 2^-16 relative (a bf16 stream alone: 2^-9), while
+    cell rows are exactly the same as without tok_lo and tok_lo bytes of
+    cells are never touched. Masked token rows keep hi and lo."""
+
+    from shrimp import ops
+
+    B, S, nt, c = 5, 24, 8, 128
+    rows = B * S
+    x, seq, m, p = _mlp_case(rows, seed=3)
+    m[S + 2] = False  # a masked token row
+    hi = seq.to(torch.bfloat16)
+    lo = (seq - hi.float()).to(torch.bfloat16)
+    tok = (torch.arange(rows) % S) < nt
+    d_in = hi.double() + torch.where(tok[:, None], lo.double(), torch.zeros(1).double())
+    want = _mlp_restated(x, d_in, m, p)
+    wo, bo, ga, lnw, lnb, w1, b1, w2, b2, gm = p
+    g = lambda t: t.to(DEV)
+    packed = ops.pack_attn_mlp(g(wo), g(bo), g(ga), g(lnw), g(lnb), g(w1), g(b1), g(w2), g(b2), g(gm))
+    xd = x.to(DEV, torch.bfloat16).contiguous()
+    md = m.to(DEV, torch.uint8)
+
+    seq_a = hi.to(DEV).contiguous()
+    lo_d = lo.reshape(B, S, c)[:, :nt].to(DEV).contiguous()
+    ops.launch_attn_mlp(x=xd, x_sr=c, seq=seq_a, s_sr=c, mask=md, packed=packed, eps=1e-5,
+                        rows=rows, C=c, hidden=256, tok_lo=lo_d, S=S, n_tokens=nt)
+    seq_b = hi.to(DEV).contiguous()
+    ops.launch_attn_mlp(x=xd, x_sr=c, seq=seq_b, s_sr=c, mask=md, packed=packed, eps=1e-5,
+                        rows=rows, C=c, hidden=256)
+    got_hi = seq_a.cpu().double()
+    got_lo = torch.zeros(rows, c, dtype=torch.float64)
+    got_lo.view(B, S, c)[:, :nt] = lo_d.cpu().double()
+    got = got_hi + got_lo
+    tw = want[tok]
+    err = ((got[tok] - tw).abs() / tw.abs().clamp(min=1.0)).max().item()
+    err_hi = ((got_hi[tok] - tw).abs() / tw.abs().clamp(min=1.0)).max().item()
+    print(f"token rows: hi + lo rel err {err:.3e}, hi alone {err_hi:.3e}", flush=True)
+    # hi + lo: fp32 accumulation and the odd bf16 rounding flip of a hidden
+    # value (~1e-4); hi alone: up to half a bf16 ulp (~2e-3 relative)
+    assert err <= 5e-4 and err_hi >= 3 * err
+    # cell rows: identical to the call without low parts
+    assert torch.equal(seq_a.cpu()[~tok], seq_b.cpu()[~tok])
+    close(seq_a[~tok.to(DEV)], want[~tok], what="attn_mlp cells with tok_lo")
+    # the masked token row keeps its hi and lo
+    assert torch.equal(seq_a.cpu()[S + 2], hi[S + 2])
+    assert torch.equal(lo_d.cpu()[1, 2], lo.reshape(B, S, c)[1, 2])
 
 
 @pytest.mark.parametrize("h,dpad", [(8, 16), (4, 32), (2, 64)])
