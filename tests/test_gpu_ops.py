@@ -622,12 +622,16 @@ def test_attn_mlp_token_low_parts():
     got_lo.view(B, S, c)[:, :nt] = lo_d.cpu().double()
     got = got_hi + got_lo
     tw = want[tok]
-    err = ((got[tok] - tw).abs() / tw.abs().clamp(min=1.0)).max().item()
-    err_hi = ((got_hi[tok] - tw).abs() / tw.abs().clamp(min=1.0)).max().item()
-    print(f"token rows: hi + lo rel err {err:.3e}, hi alone {err_hi:.3e}", flush=True)
-    # hi + lo: fp32 accumulation and the odd bf16 rounding flip of a hidden
-    # value (~1e-4); hi alone: up to half a bf16 ulp (~2e-3 relative)
-    assert err <= 5e-4 and err_hi >= 3 * err
+    e_both = (got[tok] - tw).abs() / tw.abs().clamp(min=1.0)
+    e_hi = (got_hi[tok] - tw).abs() / tw.abs().clamp(min=1.0)
+    print(f"token rows: hi + lo rel err mean {e_both.mean().item():.3e} max "
+          f"{e_both.max().item():.3e}; hi alone mean {e_hi.mean().item():.3e} max "
+          f"{e_hi.max().item():.3e}", flush=True)
+    # hi + lo: fp32 accumulation, plus the odd element where the kernel and the
+    # restatement round a LayerNorm or GELU value to different bf16 neighbours;
+    # hi alone: a quarter of a bf16 ulp on average (~1e-3 relative)
+    assert e_both.max().item() <= 2e-3
+    assert e_both.mean().item() * 8 <= e_hi.mean().item()
     # cell rows: identical to the call without low parts
     assert torch.equal(seq_a.cpu()[~tok], seq_b.cpu()[~tok])
     close(seq_a[~tok.to(DEV)], want[~tok], what="attn_mlp cells with tok_lo")
