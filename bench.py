@@ -560,6 +560,41 @@ def forward_timeline(net, inputs, reps: int = 10) -> dict:
                    "ms_per_forward": round(sum(v) / reps, 5)} for name, v in per.items()}
 
 
+def _device_gather_index(batch, dev):
+    """(B, N, 7) gather index and (B, N) mask bytes of a position batch, built by
+    the product's input-preparation kernel (shrimp_prep_inputs) from the batch's
+    neighbour rows, as the forward builds them."""
+
+    import torch
+
+    from shrimp import _lib
+    from shrimp.constants import NUM_TOKENS
+
+    lib = _lib.load()
+    feats = batch["feats"].to(dev, torch.float16).contiguous()
+    nbr = batch["nbr"].to(dev, torch.int32).contiguous()
+    mask = batch["mask"].to(dev, torch.bool).contiguous()
+    coords = batch["coords"].to(dev, torch.int32).contiguous()
+    b, n, f = feats.shape
+    i32, u8 = torch.int32, torch.uint8
+    idx = torch.empty((b, n, 7), dtype=i32, device=dev)
+    m8 = torch.empty((b, n), dtype=u8, device=dev)
+    coords32 = torch.empty((b, n, 2), dtype=i32, device=dev)
+    seq_lens = torch.empty((b,), dtype=i32, device=dev)
+    seq_mask = torch.empty((b, n + NUM_TOKENS), dtype=u8, device=dev)
+    xin = torch.empty((b, n, 32), dtype=torch.bfloat16, device=dev)
+    _lib.check(
+        lib.shrimp_prep_inputs(
+            nbr.data_ptr(), _lib.DT_I32, mask.data_ptr(), coords.data_ptr(), _lib.DT_I32,
+            feats.data_ptr(), _lib.DT_F16, f, b, n, NUM_TOKENS, idx.data_ptr(), m8.data_ptr(),
+            coords32.data_ptr(), seq_lens.data_ptr(), seq_mask.data_ptr(), _lib.ptr(xin),
+            _lib.stream_handle(dev),
+        ),
+        "prep_inputs",
+    )
+    return idx, m8
+
+
 def ops_timing(reps: int = 30) -> dict:
     """Configs 1-3 as standalone ops at their own shapes (B = 1024, Npad = 256),
     HIP events around back-to-back launches on the launch stream:
@@ -578,7 +613,6 @@ def ops_timing(reps: int = 30) -> dict:
 
     import torch
 
-    from oracle import tables
     from shrimp import _lib, ops, synthetic
 
     dev = torch.device("cuda")
@@ -593,8 +627,7 @@ def ops_timing(reps: int = 30) -> dict:
     x = torch.from_numpy(case["x"]).to(dev, torch.bfloat16).contiguous()
     wp = ops.pack_conv_weight(torch.from_numpy(case["w"]).to(dev))
     bias = torch.from_numpy(case["bias"]).to(dev)
-    idx = torch.from_numpy(tables.gather_index(b["nbr"].numpy())).to(dev, torch.int32).contiguous()
-    m8 = b["mask"].to(dev, torch.uint8).contiguous()
+    idx, m8 = _device_gather_index(b, dev)
     out = torch.empty((bb, n, 128), dtype=torch.bfloat16, device=dev)
     run = lambda: ops.launch_conv(x=x, x_sb=n * 128, x_sn=128, idx=idx, taps=7, idx_stride=7,
                                   mask8=m8, wpack=wp, bias=bias, B=bb, N=n, cin_pad=128, cout=128,
@@ -726,6 +759,26 @@ def fp32_timing(net, inputs, steps: int = 10) -> dict:
     }
 
 
+def _block_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed
+    FETCH_SIZE / WRITE_SIZE passes (profiles/block_traffic.json), used only when
+    they were taken on this build's kernel source: the file records the sha256
+    of hex_conv.hip it was measured on, and a different source gives
+    (None, reason) instead of a stale figure."""
+
+    import hashlib
+
+    tfile = ROOT / "profiles" / "block_traffic.json"
+    src = ROOT / "hexo-bot_amd" / "csrc" / "hex_conv.hip"
+    if not tfile.exists():
+        return None, "no counter passes recorded"
+    rec = json.loads(tfile.read_text())
+    sha = hashlib.sha256(src.read_bytes()).hexdigest()
+    if rec.get("kernel_source_sha256") != sha:
+        return None, "counter passes were taken on another hex_conv.hip; not measured for this build"
+    return rec.get("bytes_per_launch"), f"{rec.get('source')} (hex_conv.hip sha256 {sha[:12]})"
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -792,10 +845,7 @@ def main() -> int:
     a_flops = kt["attn_flops"] + (kt["proj_flops"] if fused else 0.0)
     a_bytes = kt["proj_bytes"] if fused else kt["attn_bytes"]
     attn_tflops = a_flops / (a_ms * 1e-3) / 1e12
-    traffic = None
-    tfile = ROOT / "profiles" / "block_traffic.json"
-    if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
+    traffic, traffic_source = _block_traffic()
     line = {
         "metric": METRIC,
         "value": round(B / (ms * 1e-3), 1),
@@ -824,6 +874,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(pair_tflops / PEAK_BF16_TFLOPS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
             "algorithmic_bytes": kt["pair_bytes"],
             "launch_ms": round(kt["pair_ms"], 5),
             "flops_per_launch": kt["pair_flops"],

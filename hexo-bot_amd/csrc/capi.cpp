@@ -17,8 +17,8 @@ int set_error(int code, const char* fmt, ...) {
   return code;
 }
 
-int g_conv_variant = 0;
-int g_attn_variant = 0;
+std::atomic<int> g_conv_variant{0};
+std::atomic<int> g_attn_variant{0};
 
 int max_lds_per_block() {
   static std::atomic<int> cache[64];
@@ -54,15 +54,13 @@ extern "C" const char* shrimp_last_error(void) { return shrimp::g_last_error.c_s
 extern "C" int shrimp_abi_version(void) { return SHRIMP_ABI_VERSION; }
 
 extern "C" int shrimp_conv_variant(int variant) {
-  const int prev = shrimp::g_conv_variant;
-  if (variant >= 0 && variant <= 3) shrimp::g_conv_variant = variant;
-  return prev;
+  if (variant < 0 || variant > 3) return shrimp::g_conv_variant.load();
+  return shrimp::g_conv_variant.exchange(variant);
 }
 
 extern "C" int shrimp_attn_variant(int variant) {
-  const int prev = shrimp::g_attn_variant;
-  if (variant >= 0 && variant <= 3) shrimp::g_attn_variant = variant;
-  return prev;
+  if (variant < 0 || variant > 3) return shrimp::g_attn_variant.load();
+  return shrimp::g_attn_variant.exchange(variant);
 }
 
 extern "C" int shrimp_max_lds_per_block(void) { return shrimp::max_lds_per_block(); }

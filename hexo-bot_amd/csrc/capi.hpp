@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -37,12 +38,12 @@ int cu_count();
 // LDS-staged when the position fits, else global gather), 1 = always the
 // global-gather kernel, 2 = LDS-staged (no big tiles), 3 = as 0 without the
 // small-batch row split.
-extern int g_conv_variant;
+extern std::atomic<int> g_conv_variant;
 // Attention: 0 = automatic (two heads per workgroup when they fit), 1 = one
 // head per workgroup, 2 = two heads on four waves, 3 = the chunked kernel
 // (keys streamed through LDS; otherwise used only for sequences that do not
 // fit one workgroup's LDS).
-extern int g_attn_variant;
+extern std::atomic<int> g_attn_variant;
 
 }  // namespace shrimp
 

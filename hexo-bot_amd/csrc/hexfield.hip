@@ -37,7 +37,7 @@ constexpr uint32_t RA_STAGE_MAX_LDS = 64 * 1024;
 constexpr uint32_t RA_BIAS_LDS = 96;  // the head pair's 22 fp32 slot biases, padded
 constexpr float LOG2E_F = 1.4426950408889634f;
 
-int g_ray_variant = 0;
+std::atomic<int> g_ray_variant{0};
 
 SHRIMP_DEV f16x2 as_h2(unsigned u) { return __builtin_bit_cast(f16x2, u); }
 
@@ -609,9 +609,8 @@ bool raytap_shape_ok(int C, int Cout) {
 }  // namespace
 
 extern "C" int shrimp_ray_attn_variant(int v) {
-  const int prev = g_ray_variant;
-  if (v == 0 || v == 1) g_ray_variant = v;
-  return prev;
+  if (v != 0 && v != 1) return g_ray_variant.load();
+  return g_ray_variant.exchange(v);
 }
 
 extern "C" int shrimp_ray_attn(const shrimp_ray_attn_args* a, void* stream) {

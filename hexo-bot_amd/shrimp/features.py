@@ -3,14 +3,13 @@
 Restates ``packages/shrimp/python/shrimp/features.py``: the
 ``PositionFacts`` record (:54-77), turn bookkeeping (:80-93), the
 single-colour window scan for hot / standing-win cells (:99-159), the feature
-build (:165-210), the opponent's last full turn (:213-233) and D6 transforms
-of facts (:246-266). The HIP forward consumes these planes unchanged, so the
-values must be exact.
+build (:165-210) and the opponent's last full turn (:213-233). The HIP
+forward consumes these planes unchanged, so the values must be exact.
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass, replace
+from dataclasses import dataclass
 
 import numpy as np
 
@@ -37,7 +36,6 @@ from .constants import (
     WIN_NOW_COUNT,
     WINDOW_LEN,
 )
-from .geometry import apply_d6
 from .support import Support, build_support
 
 PHASE_OPENING = "Opening"
@@ -194,20 +192,3 @@ def build_position(facts: PositionFacts, *, radius: int | None = None):
 
     sup = build_support(facts.stones(), radius=radius)
     return sup, build_features(facts, sup)
-
-
-def transform_facts(facts: PositionFacts, sym: int) -> PositionFacts:
-    """Apply D6 element ``sym`` to every coordinate in ``facts``."""
-
-    def t(cell):
-        return apply_d6(sym, cell[0], cell[1])
-
-    return replace(
-        facts,
-        records=tuple((*t((q, r)), o, i) for q, r, o, i in facts.records),
-        first_stone=t(facts.first_stone) if facts.first_stone is not None else None,
-        own_hot=tuple(sorted(t(c) for c in facts.own_hot)),
-        opp_hot=tuple(sorted(t(c) for c in facts.opp_hot)),
-        own_win=tuple(sorted(t(c) for c in facts.own_win)),
-        opp_win=tuple(sorted(t(c) for c in facts.opp_win)),
-    )

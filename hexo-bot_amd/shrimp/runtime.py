@@ -26,9 +26,13 @@ any parameter changes (tracked through tensor version counters).
 
 precision "fp32" (the reference's serve with autocast off,
 inference.py:50-68) runs the same sequence on the fp32 kernels: fp32
-activations end to end (seq, y1, qkv, att, hid, seqf all fp32), fp32 MFMA
-products, the attention on the chunked fp32 kernel, the bias tables rounded
-to fp16 as the reference's no-grad bias is (model.py:737-760).
+activations end to end (seq, y1, qkv, att, hid, seqf all fp32); the GEMMs
+whose input width is a multiple of 32 on bf16 MFMA over hi / lo split
+operands (three products per tile, about 2^-16 relative error per product),
+only the 16-channel stem on fp32 MFMA; the head-dim-16 coords attention on
+the split-operand MFMA kernel, other head dims and pair mode on the chunked
+fp32 kernel; the bias tables rounded to fp16 as the reference's no-grad bias
+is (model.py:737-760).
 """
 
 from __future__ import annotations
@@ -513,18 +517,22 @@ class HipForward:
     BUFFER_LIMIT = 0x7FFF0000
 
     def batch_limit(self, N: int) -> int:
-        """Positions one forward can take at Npad = N: the widest per-position
-        activation buffer (the MLP hidden (S, 2C), q/k/v (H, S, dpad) or the K / V
-        fragments (H, 2, SP, 16)) times the batch stays under BUFFER_LIMIT
-        bytes; max_batch caps it further."""
+        """Positions one forward can take at Npad = N: every per-batch buffer
+        whose byte extent a kernel checks against BUFFER_LIMIT stays under it at
+        that batch. The widest per position are the MLP hidden rows (S, 2C), the
+        three q / k / v planes (3, H, S, dpad) of the unstaged attention (the
+        fused q/k/v kernel checks all three planes as one extent; the fp32 mode
+        keeps the same planes in fp32) and the staged attention's K / V
+        fragments (H, 2, SP, 16); the bound takes the largest of them whichever
+        attention path the forward takes. max_batch caps it further."""
 
         net = self.net
         c, h = net.channels, net.heads
-        width = max(2 * c, h * head_dim_pad(c // h))
+        dpad = head_dim_pad(c // h)
         elem = 4 if self.fp32 else 2
-        # the staged attention's K / V fragments: (H, 2, SP, 16) bf16 per position
-        sp = (N + NUM_TOKENS + 15) // 16 * 16
-        per = max((N + NUM_TOKENS) * width * elem, h * sp * 64)
+        s = N + NUM_TOKENS
+        sp = (s + 15) // 16 * 16
+        per = max(s * 2 * c * elem, 3 * h * s * dpad * elem, h * sp * 64)
         lim = max(1, (self.BUFFER_LIMIT - 1) // per)
         return lim if self.max_batch is None else max(1, min(lim, int(self.max_batch)))
 

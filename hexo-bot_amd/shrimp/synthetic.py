@@ -141,7 +141,7 @@ def position_batch(name: str, count: int, seed: int | None = None) -> dict:
 def serve_payload(name: str, count: int, seed: int | None = None, *,
                   request_moves_left: bool = False, request_logits: bool = False) -> tuple:
     """ABI-1 evaluator payload of ``count`` positions of config ``name``, built
-    as the Rust bridge builds it (``crates/shrimp/src/payload.rs:108-160``):
+    as the Rust bridge builds it (``packages/shrimp/rust/src/payload.rs:108-160``):
     rows sorted by support size, descending (ties in request order), f16
     features, i16 coordinates, u16 row-local neighbour ids with 0xFFFF for
     absent. Returns (payload, order): order[k] is the request index of row k."""

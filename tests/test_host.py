@@ -145,20 +145,42 @@ def test_serve_payload_matches_the_oracle_builder():
 
 
 def test_batch_limit_keeps_buffers_under_32_bit_offsets():
-    """One forward launch sequence takes at most as many positions as keep its
-    widest activation buffer (MLP hidden (S, 2C), q/k/v (H, S, dpad)) below the
-    32-bit buffer-offset limit; max_batch lowers it further."""
+    """One forward launch sequence takes at most as many positions as keep every
+    buffer extent that a kernel checks below the 32-bit buffer-offset limit,
+    whichever attention path runs (staged: q plane + K/V fragments; unstaged:
+    the three q/k/v planes the fused q/k/v kernel writes as one extent);
+    max_batch lowers it further. The extents are recomputed here the way the
+    kernels' argument checks compute them (qkv.hip, attn.hip, mlp.hip)."""
 
     from shrimp.model import ShrimpNet
     from shrimp.runtime import HipForward
 
-    rt = HipForward(ShrimpNet(channels=128, attention_heads=8, trunk_layout="CCACCACCACCA"))
+    limit = HipForward.BUFFER_LIMIT
+    C, H, dpad = 128, 8, 16
+    rt = HipForward(ShrimpNet(channels=C, attention_heads=H, trunk_layout="CCACCACCACCA"))
+    for precision, elem in (("bf16", 2), ("fp32", 4)):
+        rt.precision = precision
+        for npad in (256, 464, 512, 576):
+            for staged in (True, False):
+                rt.use_staged_attn = staged
+                B = rt.batch_limit(npad)
+                S = npad + 8
+                SP = (S + 15) // 16 * 16
+                extents = {
+                    "attn_qkv qe (3 planes)": 3 * B * H * S * dpad * elem,
+                    "attn q/k/v plane": ((B - 1) * H * S * dpad + (H - 1) * S * dpad + S * dpad) * elem,
+                    "attn_staged kvf": B * H * SP * 64,
+                    "attn out": ((B - 1) * S * C + (H - 1) * 16 + (S - 1) * C + 16) * elem,
+                    "mlp hidden rows": ((B * S - 1) * 2 * C + 2 * C) * elem,
+                    "seq rows": ((B * S - 1) * C + C) * elem,
+                }
+                for name, e in extents.items():
+                    assert e < limit, (precision, npad, staged, B, name, e)
+                # and the bound is tight: one more position would overflow a buffer
+                per = max(3 * H * S * dpad * elem, S * 2 * C * elem, H * SP * 64)
+                assert (B + 1) * per >= limit, (precision, npad, B)
     rt.precision = "bf16"
-    lim = rt.batch_limit(256)
-    assert lim == (HipForward.BUFFER_LIMIT - 1) // (8 * 272 * 64)
-    assert lim * 8 * 272 * 64 < 2 ** 31 and lim * 264 * 256 * 2 < 2 ** 31
-    rt.precision = "fp32"
-    assert rt.batch_limit(256) == (HipForward.BUFFER_LIMIT - 1) // (264 * 256 * 4)
+    assert rt.batch_limit(256) == (limit - 1) // (3 * H * 264 * dpad * 2)
     rt.max_batch = 7
     assert rt.batch_limit(256) == 7
     assert rt.batch_limit(10 ** 7) == 1
