@@ -478,6 +478,8 @@ def _host_cpu() -> dict:
     return {"model": max(names, key=len) if names else None,
             "sockets": info.get("Socket(s)"), "cores_per_socket": info.get("Core(s) per socket"),
             "threads_per_core": info.get("Thread(s) per core"),
+            "vendor": info.get("Vendor ID"), "family": info.get("CPU family"),
+            "model_id": info.get("Model"), "flags_avx512f": "avx512f" in info.get("Flags", ""),
             "cores_visible": os.cpu_count(), "cores_usable": usable}
 
 
@@ -526,12 +528,80 @@ def cpu_baseline(batch, seconds: float, sample: int = 512, runs: int = 5, warmup
                   f"(fp32 eager oracle: torch pair rows, fp16 bias, sdpa; "
                   f"{min(times):.2f}-{max(times):.2f} s per forward, torch threads {threads})",
         "cpu_model": host["model"],
+        "cpu_vendor_family_model": f"{host['vendor']} family {host['family']} model {host['model_id']}",
+        "cpu_avx512f": host["flags_avx512f"],
         "sockets": host["sockets"],
         "cores_per_socket": host["cores_per_socket"],
         "threads_per_core": host["threads_per_core"],
         "cores_visible": host["cores_visible"],
         "cores_usable": host["cores_usable"],
     }
+
+
+def forward_flops(N: int, c: int = C, layout: str = LAYOUT, features: int = 15) -> float:
+    """Padded-dense FLOPs of one position's forward at Npad = N (S = N + 8):
+    per ConvBlock two 7-tap convs (2 * 2 * 7 * C^2 * N); per attention block
+    q/k/v (6 C^2 S), QK^T and PV over all heads (4 S^2 C), out_proj
+    (2 C^2 S) and the MLP (8 C^2 S); the stem (2 * 7 * features * C * N) and
+    the policy conv (2 * 7 * C^2 * N). 1.425 GFLOP at N = 256, C = 128."""
+
+    s = N + 8
+    f = layout.count("C") * 28.0 * c * c * N
+    f += layout.count("A") * (16.0 * c * c * s + 4.0 * s * s * c)
+    return f + 14.0 * c * c * N + 14.0 * features * c * N
+
+
+def spec_timing(net, reps: int = 10) -> dict:
+    """The spec-faithful positions (all 10-80 stones, supports of 280-544
+    cells: shrimp.synthetic "cfg4_spec", 512 positions) on the same network,
+    inputs device-resident: (a) the whole batch padded to one Npad
+    (ceil64 of its largest support: 576) in one forward; (b) the batch as
+    the evaluator serves it: rows sorted by size and cut by plan_groups
+    (padding to the 64-quantized anchor, the reference's pair ceiling and
+    waste fraction), one forward per group. positions/s over the 512, HIP
+    events on the launch stream, and the padded-dense TFLOP/s."""
+
+    import torch
+
+    from shrimp import synthetic
+    from shrimp.batching import collate_rows
+    from shrimp.inference import plan_groups
+
+    dev = torch.device("cuda")
+    stream = torch.cuda.current_stream(dev)
+    batch = synthetic.position_batch("cfg4_spec", B)
+    rows = batch["rows"]
+    npad = int(batch["mask"].shape[1])
+    sizes = sorted((s.num_nodes for _, s, _ in rows), reverse=True)
+
+    def dev_inputs(b):
+        return (b["feats"].to(dev, torch.float16), b["nbr"].to(dev, torch.int32),
+                b["mask"].to(dev), b["coords"].to(dev, torch.int32))
+
+    one = dev_inputs(batch)
+    order = sorted(range(len(rows)), key=lambda i: -rows[i][1].num_nodes)
+    groups = []
+    for g0, g1, pad in plan_groups(sizes):
+        sel = [rows[order[i]] for i in range(g0, g1)]
+        groups.append((pad, g1 - g0, dev_inputs(collate_rows([(s, f) for _, s, f in sel], pad_to=pad))))
+    run_one = lambda: net.forward_policy_value(*one)
+    run_groups = lambda: [net.forward_policy_value(*g[2]) for g in groups]
+    res = {"workload": f"B={B} cfg4_spec positions, supports {min(sizes)}-{max(sizes)} cells",
+           "generator": "spec seed 20261205"}
+    for name, fn, flops in (
+        ("one_batch", run_one, B * forward_flops(npad)),
+        ("grouped", run_groups, sum(n * forward_flops(pad) for pad, n, _ in groups)),
+    ):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize(dev)
+        ms = _events_time(fn, reps, stream)
+        res[name] = {"ms_per_512": round(ms, 4), "positions_per_s": round(B / (ms * 1e-3), 1),
+                     "tflops_padded": round(flops / (ms * 1e-3) / 1e12, 2),
+                     "bf16_mfma_frac_padded": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    res["one_batch"]["npad"] = npad
+    res["grouped"]["groups"] = [{"npad": pad, "positions": n} for pad, n, _ in groups]
+    return res
 
 
 def forward_timeline(net, inputs, reps: int = 10) -> dict:
@@ -788,6 +858,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--spec-only", action="store_true",
+                    help="only time the spec-faithful positions (spec_timing) and print that")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run 5 plain device copies of this many MiB (the "
                          "calibration kernel for HBM traffic counters) and exit")
@@ -818,6 +890,9 @@ def main() -> int:
     _lib.load()
     torch.manual_seed(0)
     net = ShrimpNet(channels=C, attention_heads=H, trunk_layout=LAYOUT).to(dev).eval()
+    if args.spec_only:
+        print(json.dumps({"spec": spec_timing(net, reps=args.steps)}), flush=True)
+        return 0
     batch = synthetic.position_batch("cfg4", B)
     inputs = (
         batch["feats"].to(dev, torch.float16),
@@ -913,7 +988,8 @@ def main() -> int:
         "in_forward": timeline,
         "ops": ops_timing(),
         "fp32": fp32_timing(net, inputs),
-        "forward_tflops_padded": round(1.425e9 * B / (ms * 1e-3) / 1e12, 2),
+        "forward_tflops_padded": round(forward_flops(NPAD) * B / (ms * 1e-3) / 1e12, 2),
+        "spec": spec_timing(net),
         "featurize": featurize_timing(batch["rows"]),
         "hexfield": hexfield_timing(),
         "evaluator": evaluator_timing(net),

@@ -404,7 +404,7 @@ SHRIMP_DEV u32x2 opaque2(u32x2 v) {
 }
 
 template <int DP, int HG, bool PAIR, int PROJ, int NW>
-__global__ __launch_bounds__(64 * NW, NW == 8 ? 4 : 1) void attn_kernel(const shrimp_attn_args a, float qk_scale,
+__global__ __launch_bounds__(64 * NW, NW == 8 ? (PROJ == 3 ? 2 : 4) : 1) void attn_kernel(const shrimp_attn_args a, float qk_scale,
                                                    uint32_t qkv_bytes, int npos,
                                                    const shrimp_attn_proj_args p, uint32_t x_bytes,
                                                    uint32_t o_bytes) {
@@ -1446,10 +1446,14 @@ extern "C" int shrimp_attn_keys(const int32_t* coords, const uint8_t* mask, cons
   return check_launch("attn_keys");
 }
 
+// The staged kernel runs four waves per workgroup while its LDS fits the
+// 64 KiB budget (three workgroups per compute unit), and eight waves with the
+// unit's LDS to itself past it (two waves per SIMD, up to 256 registers each):
+// supports of 368 cells and more, as the evaluator pads spec-sized positions.
 extern "C" int shrimp_attn_staged_supported(int H, int S, int dpad) {
   const int SP = (S + 15) & ~15;
   return dpad == 16 && H > 0 && H % 2 == 0 && S > 0 && S % 4 == 0 && SP <= 1024 &&
-         attn_smem_bytes(16, 2, S, 0, false) <= kAttnSmemCap;
+         attn_smem_bytes(16, 2, S, 0, false) <= (size_t)max_lds_per_block();
 }
 
 extern "C" int shrimp_attn_staged(const shrimp_attn_args* a, const void* kvf, const int32_t* meta,
@@ -1482,15 +1486,20 @@ extern "C" int shrimp_attn_staged(const shrimp_attn_args* a, const void* kvf, co
   const float qk_scale = SHRIMP_LOG2E / sqrtf((float)a->d);
   const size_t smem = attn_smem_bytes(16, 2, a->S, 0, false);
   // four waves per workgroup (three workgroups per compute unit): measured
-  // faster than eight here
+  // faster than eight where the 64 KiB budget holds; past it eight waves
+  const bool big = smem > kAttnSmemCap;
+  const int NW = big ? 8 : 4;
   const int groups = a->H / 2 * a->B;
-  constexpr int NW = 4;
   const int rounds = ((a->S + 15) / 16) / NW;
   int z = 1;
   while (z < 4 && groups * z * 2 <= 2 * cu_count() && rounds >= 2 * z) z *= 2;
   dim3 grid(a->H / 2, a->B, z);
   const shrimp_attn_proj_args none{};
-  hipLaunchKernelGGL((attn_kernel<16, 2, false, 3, NW>), grid, dim3(64 * NW), smem, as_stream(stream),
-                     s, qk_scale, (uint32_t)qe, 0, none, 0u, attn_out_bytes(a));
+  if (big)
+    hipLaunchKernelGGL((attn_kernel<16, 2, false, 3, 8>), grid, dim3(64 * 8), smem,
+                       as_stream(stream), s, qk_scale, (uint32_t)qe, 0, none, 0u, attn_out_bytes(a));
+  else
+    hipLaunchKernelGGL((attn_kernel<16, 2, false, 3, 4>), grid, dim3(64 * 4), smem,
+                       as_stream(stream), s, qk_scale, (uint32_t)qe, 0, none, 0u, attn_out_bytes(a));
   return check_launch("attn_staged");
 }

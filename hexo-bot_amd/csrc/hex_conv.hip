@@ -690,6 +690,12 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
 // retires in issue order and every weight load issued after a row DMA waits
 // for it. The K loop runs chunk-major (kc, then the 7 taps).
 constexpr int BIG_MAX_N = 512;
+// Two workgroups of three waves per position (hex_conv_big_kernel with
+// gridDim.y = 2): up to 3 * 128 rows per half, and ceil((N + 1) / 16) <= 3 *
+// BIG_SPLIT_GPW row groups staged by each.
+constexpr int BIG_SPLIT_MAX_N = 576;
+constexpr int BIG_SPLIT_GPW = 13;
+constexpr int BIG_SPLIT_MIN_B = 32;
 constexpr int BIG_PARAMS = 5 * 128;  // floats: [bias | ln_w | ln_b | gamma or head_w | zeros]
 
 __host__ __device__ inline int big_rows_padded(int N) { return ((N + 1 + 15) / 16) * 16; }
@@ -756,16 +762,21 @@ struct BigParams {
 // Requests all four chunks by DMA and turns the neighbour indices of this wave's rows
 // into swizzled 16-bit LDS row addresses j * 64 | ((j >> 2) & 3) << 4.
 // The indices are requested before the rows (three loads per row block, absent
-// rows reading zeros past the resource), and every wave issues the same nine
+// rows reading zeros past the resource), and every wave issues the same GPW
 // DMAs per chunk (a wave with fewer groups repeats its first one: the same
 // bytes to the same place), so the wait for the indices counts the DMAs
 // instead of waiting for them and the row addresses are computed while the
-// rows arrive. Needs idx_stride >= 7 and N <= BIG_MAX_N.
+// rows arrive. Needs idx_stride >= 7 and ceil((N + 1) / 16) <= GPW * waves.
+// The workgroup computes rows [rbase, rend) (128 per wave from rbase); every
+// workgroup stages all rows of its position, since the taps reach anywhere in
+// it.
+template <int GPW = 9>
 SHRIMP_DEV void big_setup(BigTile& t, const shrimp_conv_args& a, unsigned char* xs,
-                          uint32_t x_bytes) {
-  // DMAs per chunk and wave: with ceil(N / 128) waves a wave owns at most
-  // ceil((8 nw + 1) / nw) = 9 of the ceil((N + 1) / 16) row groups
-  constexpr int T = 7, MB = 8, GPW = 9;
+                          uint32_t x_bytes, int rbase = 0, int rend = 1 << 30) {
+  // DMAs per chunk and wave: with ceil(N / 128) waves over the whole position
+  // a wave owns at most ceil((8 nw + 1) / nw) = 9 of the ceil((N + 1) / 16)
+  // row groups (GPW = 9)
+  constexpr int T = 7, MB = 8;
   t.lane = threadIdx.x & 63;
   t.wave = wave_id();
   t.nw = blockDim.x >> 6;
@@ -777,12 +788,13 @@ SHRIMP_DEV void big_setup(BigTile& t, const shrimp_conv_args& a, unsigned char* 
   t.xr = make_rsrc(a.x, x_bytes);
   t.xbase = (uint32_t)((int64_t)t.b * a.x_sb * 2);
   t.xsn2 = (uint32_t)(a.x_sn * 2);
-  const int row0 = t.wave * (MB * 16);
+  const int row0 = rbase + t.wave * (MB * 16);
+  const int rlim = rend < t.N ? rend : t.N;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     t.rb[mb] = t.b;
     t.rn[mb] = row0 + mb * 16 + (t.lane & 15);
-    t.rv[mb] = t.rn[mb] < t.N;
+    t.rv[mb] = t.rn[mb] < rlim;
   }
   const __amdgpu_buffer_rsrc_t ir =
       make_rsrc(a.idx + (int64_t)t.b * t.N * a.idx_stride, (uint32_t)(t.N * a.idx_stride * 4));
@@ -881,14 +893,19 @@ SHRIMP_DEV void big_pass(f32x4 (&acc)[8][8], u32x4 (&wf)[8], const BigTile& t,
   }
 }
 
-template <int EPI>
+// Workgroup (b, y) computes rows [y rp, (y + 1) rp) of position b: gridDim.y
+// is 1 (rp = N) up to BIG_MAX_N rows, 2 past it (GPW DMAs per chunk and wave
+// then cover the position with three waves).
+template <int EPI, int GPW = 9>
 __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_args a,
-                                                              uint32_t x_bytes, uint32_t w_bytes) {
+                                                              uint32_t x_bytes, uint32_t w_bytes,
+                                                              int rp) {
   extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
   BigParams<1> bp;
   bp.load(0, a.bias, a.ln_w, a.ln_b, (EPI & EPI_HEAD) ? a.head_w : a.gamma);
   BigTile t;
-  big_setup(t, a, xs, x_bytes);
+  const int rbase = (int)blockIdx.y * rp;
+  big_setup<GPW>(t, a, xs, x_bytes, rbase, rbase + rp);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, w_bytes);
   u32x4 wf[8];
   big_wload(wr, 0, t.lane, wf);
@@ -1348,6 +1365,21 @@ static int launch_conv(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, size
                          lds_p, st, *a, wb, ob, rbb);                                              \
     return check_launch("hex_conv");                                                               \
   } while (0)
+  // Past BIG_MAX_N rows a position's rows split over two workgroups of three
+  // waves (rows [0, rp) and [rp, N), rp = ceil(N / 32) * 16), each staging the
+  // whole position: the big-tile arithmetic (same bits per row) with one
+  // round of workgroups for up to a compute unit's worth of halves, where the
+  // row-split kernel stages the position once per 64-row tile. Batches under
+  // BIG_SPLIT_MIN_B positions keep the row split (more workgroups).
+  if (COUT == 128 && lds && a->cin_pad == 128 && a->taps == 7 && a->N > BIG_MAX_N &&
+      a->B >= BIG_SPLIT_MIN_B &&
+      a->N <= BIG_SPLIT_MAX_N && out16 && (g_conv_variant == 0 || g_conv_variant == 3) &&
+      big_lds <= (size_t)max_lds_per_block()) {
+    const int rp = (a->N + 31) / 32 * 16;
+    hipLaunchKernelGGL((hex_conv_big_kernel<EPI, BIG_SPLIT_GPW>), dim3(a->B, 2), dim3(64 * 3),
+                       big_lds, st, *a, xb, wb, rp);
+    return check_launch("hex_conv");
+  }
   // Small batches (at most half as many positions as compute units): one row
   // tile of 64 rows per workgroup, (B, N / 64) workgroups, instead of one
   // workgroup per position; where the big-tile kernel would run, with its
@@ -1365,10 +1397,11 @@ static int launch_conv(const shrimp_conv_args* a, uint32_t xb, uint32_t wb, size
     const int waves = (a->N + 127) / 128;
     {
       hipLaunchKernelGGL((hex_conv_big_kernel<EPI>), dim3(a->B), dim3(64 * waves), big_lds, st, *a,
-                         xb, wb);
+                         xb, wb, a->N);
       return check_launch("hex_conv");
     }
   }
+
   if (lds_ok) {
     switch (a->cin_pad) {
       case 32: SHRIMP_LDS_LAUNCH(dim3(a->B), MB, 32, false);

@@ -139,6 +139,9 @@ class HipForward:
         # ConvBlock as one launch (conv1's output kept in LDS) where a fused
         # kernel exists; off runs the two convolutions.
         self.use_fused_block = True
+        # Batch size from which the one-workgroup-per-position kernels run
+        # (None: above half the compute units).
+        self.fused_min_batch = None
         self._cu_cache: dict = {}
         # Captured forwards (graph_forward_csr), keyed by (batch bucket, Npad,
         # moves-left, device); dropped when a parameter changes.
@@ -171,6 +174,25 @@ class HipForward:
         if dev.index not in self._cu_cache:
             self._cu_cache[dev.index] = torch.cuda.get_device_properties(dev).multi_processor_count
         return self._cu_cache[dev.index]
+
+    def _fused_batch(self, B: int, N: int, dev) -> bool:
+        """Whether a batch of B positions at Npad = N takes the
+        one-workgroup-per-position kernels (fused ConvBlock, block pair, policy
+        tail), or ``fused_min_batch`` positions when that is set. Up to 256
+        cells a fused workgroup is two waves and two fit a compute unit, so the
+        row-split convolutions win until the batch passes half the compute
+        units. Past 256 cells a fused workgroup is three or four waves with the
+        unit's LDS to itself, while the row split stages the whole position
+        once per 64-row tile and runs ceil(B N / 64 / CUs) rounds of those:
+        measured at Npad 512 (whole forward), 40 positions 0.91 ms either way,
+        98 positions 1.15 ms fused against 1.67 ms split, 128 positions 1.25
+        against 1.71 ms; 16 positions 0.73 against 0.54 ms."""
+
+        if self.fused_min_batch is not None:
+            return B >= self.fused_min_batch
+        if N > 256:
+            return B >= 40
+        return 2 * B > self._cus(dev)
 
     def invalidate(self) -> None:
         self._packed = None
@@ -636,7 +658,7 @@ class HipForward:
         self._mark("stem")
         ci = ai = 0
         rows = B * S
-        fused_block = self.use_fused_block and 2 * B > self._cus(dev) and conv_block_supported(7, N, C, C)
+        fused_block = self.use_fused_block and self._fused_batch(B, N, dev) and conv_block_supported(7, N, C, C)
         pair_ok = fused_block and self.use_block_pair and conv_block_pair_supported(7, N, C, C)
         skip = False
         for li, kind in enumerate(P.layout):
@@ -760,7 +782,7 @@ class HipForward:
             B=B, S=S, n_tokens=NUM_TOKENS, C=C, bins=VALUE_BINS, tok_lo=tok_lo.data_ptr(),
         )
         policy = torch.empty((B, N), dtype=torch.float32, device=dev)
-        if (self.use_fused_tail and not self.keep_buffers and 2 * B > self._cus(dev)
+        if (self.use_fused_tail and not self.keep_buffers and self._fused_batch(B, N, dev)
                 and lib.shrimp_policy_tail_supported(N, C)):
             pa = _lib.ConvArgs(
                 x=seq.data_ptr() + NUM_TOKENS * C * seq.element_size(), x_sb=S * C, x_sn=C,

@@ -213,6 +213,39 @@ def test_forward_other_widths_match_oracle(c, h, npad):
     _check_trunk(out, want, b["mask"], f"C={c} H={h} Npad={npad}")
 
 
+@pytest.mark.parametrize("npad,count", [(512, 136), (576, 136), (576, 24)])
+def test_forward_c128_spec_sizes_match_oracle(npad, count):
+    """C=128, H=8, the full 12-block trunk on spec-faithful positions (supports
+    of 280-544 cells, as the evaluator groups them) padded to Npad 512 and
+    576, against the oracle. 136 positions run the large-batch kernels (the
+    fused ConvBlock pair at 512; at 576, past one workgroup's fused-block
+    LDS, the two-launch convs); 24 positions run the small-batch row split."""
+
+    from shrimp import synthetic
+    from shrimp.batching import collate_rows
+
+    rows = [r for r in synthetic.positions("cfg4_spec", 3 * count, seed=41 + npad)
+            if r[1].num_nodes <= npad]
+    if npad == 576:
+        big = [r for r in rows if r[1].num_nodes > 512]
+        rows = big[: count // 4] + [r for r in rows if r[1].num_nodes <= 512]
+    rows = rows[:count]
+    assert len(rows) == count and max(r[1].num_nodes for r in rows) > npad - 64
+    b = collate_rows([(s, f) for _, s, f in rows], pad_to=npad)
+    layout = "CCACCACCACCA"
+    net = _net(128, 8, layout, seed=13, mode="heads")
+    what = f"C=128 H=8 Npad={npad} B={count}"
+    print(what, flush=True)
+    out = _run(net, b["feats"], b["nbr"], b["mask"], b["coords"], trunk=True)
+    want = ofwd.forward_policy_value(
+        weights.make_state_dict(128, 8, layout, seed=13, mode="heads"), layout, 8, b["feats"],
+        b["nbr"], b["mask"], b["coords"], request_moves_left=True, dtype=torch.float32,
+        return_trunk=True,
+    )
+    _check(out, want, b["mask"], what)
+    _check_trunk(out, want, b["mask"], what)
+
+
 def test_forward_feature_and_index_dtypes(cfg4_batch):
     """f16 features + int32 nbr/coords (the evaluator wire types) give the
     same result as f32 + int64 up to the f16 rounding of the features."""

@@ -162,6 +162,84 @@ def test_conv_residual_and_head_epilogues(conv_case, conv_variant):
     assert (head.cpu()[~mask] == 0).all()
 
 
+@pytest.fixture(scope="module")
+def spec576_case():
+    """36 spec-sized positions (supports past 512 cells among them) padded to
+    576 cells, with N(0, 1) rows and a 7-tap 128 -> 128 weight."""
+
+    from shrimp import synthetic
+    from shrimp.batching import collate_rows
+
+    rows = [r for r in synthetic.positions("cfg4_spec", 80, seed=57) if r[1].num_nodes <= 576]
+    big = [r for r in rows if r[1].num_nodes > 512]
+    rows = (big[:6] + [r for r in rows if r[1].num_nodes <= 512])[:36]
+    b = collate_rows([(s, f) for _, s, f in rows], pad_to=576)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(36, 576, 128, generator=g) * b["mask"][..., None]
+    w = torch.randn(7, 128, 128, generator=g) / math.sqrt(7 * 128)
+    bias = torch.randn(128, generator=g) * 0.02
+    return b, x, w, bias
+
+
+def test_conv_past_512_rows_split_over_two_workgroups(spec576_case):
+    """Npad 576 at a batch of 36 positions runs the big-tile conv with each
+    position's rows split over two workgroups of three waves (each staging the
+    whole position): conv + LN + ReLU, the LayerScale residual and the policy
+    head against the fp64 oracle; the same rows through two batches of 18
+    (the row-split kernel) agree to the bf16 tolerance."""
+
+    from shrimp import ops
+
+    b, x, w, bias = spec576_case
+    mask = b["mask"]
+    B, N = mask.shape
+    assert B >= 32 and N == 576 and int(mask.sum(1).max()) > 512
+    gidx = _gidx(b)
+    g = torch.rand(128) * 0.5 + 0.5
+    lnw = torch.rand(128) + 0.5
+    lnb = torch.randn(128) * 0.1
+    xd = x.to(DEV, torch.bfloat16).contiguous()
+    idx = gidx.to(DEV, torch.int32).contiguous()
+    m8 = mask.to(DEV, torch.uint8)
+    wp = ops.pack_conv_weight(w.to(DEV))
+    common = dict(x_sb=N * 128, x_sn=128, taps=7, idx_stride=7, wpack=wp, bias=bias.to(DEV),
+                  cin_pad=128, cout=128)
+    print("spec576 conv ln_relu", flush=True)
+    y1 = torch.empty(B, N, 128, dtype=torch.bfloat16, device=DEV)
+    ops.launch_conv(x=xd, idx=idx, mask8=m8, B=B, N=N, ln_w=lnw.to(DEV), ln_b=lnb.to(DEV),
+                    relu=True, out=y1, o_sb=N * 128, o_sn=128, **common)
+    want = ofwd.hex_conv_ln(bf(x), gidx, mask, bf(w), bias.double(), lnw.double(), lnb.double(),
+                            1e-5, True)
+    close(y1, want, what="ln_relu N=576")
+    assert (y1.cpu()[~mask] == 0).all()
+    # the same positions in two batches of 18 (row-split kernel)
+    halves = torch.empty_like(y1)
+    for h0 in (0, 18):
+        ops.launch_conv(x=xd[h0:h0 + 18], idx=idx[h0:h0 + 18], mask8=m8[h0:h0 + 18], B=18, N=N,
+                        ln_w=lnw.to(DEV), ln_b=lnb.to(DEV), relu=True, out=halves[h0:h0 + 18],
+                        o_sb=N * 128, o_sn=128, **common)
+    close(halves, y1.double().cpu(), what="split vs row-split N=576")
+    print("spec576 conv residual", flush=True)
+    resid = torch.randn(B, N, 128) * mask[..., None]
+    out = resid.to(DEV, torch.bfloat16).contiguous()
+    ops.launch_conv(x=xd, idx=idx, mask8=m8, B=B, N=N, ln_w=lnw.to(DEV), ln_b=lnb.to(DEV),
+                    resid=out, r_sb=N * 128, r_sn=128, gamma=g.to(DEV), out=out, o_sb=N * 128,
+                    o_sn=128, **common)
+    y = ofwd.hex_conv_ln(bf(x), gidx, mask, bf(w), bias.double(), lnw.double(), lnb.double(),
+                         1e-5, False)
+    close(out, torch.relu(bf(resid) + g.double() * y), what="residual N=576")
+    print("spec576 conv head", flush=True)
+    hw = torch.randn(128) * 0.1
+    hb = torch.randn(1)
+    head = torch.empty(B, N, device=DEV)
+    ops.launch_conv(x=xd, idx=idx, mask8=m8, B=B, N=N, relu=True, head_w=hw.to(DEV),
+                    head_b=hb.to(DEV), head_out=head, **common)
+    yc = torch.relu(ofwd.hex_conv(bf(x), gidx, mask, bf(w), bias.double()))
+    close(head, (yc @ hw.double() + hb.double()) * mask.double(), atol=1e-2, rtol=1e-3,
+          what="head N=576")
+    assert (head.cpu()[~mask] == 0).all()
+
+
 def _block_case(conv_case, n):
     """conv_case cut (n < 256) or zero-padded (n > 256) to n cells per position;
     neighbours outside [0, n) become the sentinel n."""
