@@ -277,7 +277,7 @@ def test_fused_and_unfused_mlp_paths_agree(cfg4_batch):
     """The fused LN1 + q/k/v and attention-block MLP kernels (per-channel
     factors folded into bf16 weights) and the separate linear kernels give the
     same forward up to bf16 rounding points, fp32 summation order and the
-    GELU's erf evaluation (|error| <= 1.5e-7)."""
+    GELU evaluation (|error| <= 3.8e-6)."""
 
     b = cfg4_batch
     net = _net(128, 8, "CCACCACCACCA", seed=5)
