@@ -194,34 +194,47 @@ constexpr uint32_t QKV_PACK_BYTES = QKV_CS_OFF + QKV_N * 4;
 
 // ---- per-channel biases held in registers -------------------------------------
 //
-// NT blocks of 16 channels kept in NT / 4 registers: register r holds at lane
-// (lr, lg) channel lr of block 4 r + lg. An accumulator starts at bias block t
-// with one fp32 MFMA against a one-hot operand (lane (lr, lg): 1 when
-// lg = t % 4), exactly: the products are bias * 1 and bias * 0. This keeps
-// bias loads out of loops whose global loads would otherwise make each bias
-// wait for every earlier load and store (memory operations retire in order).
+// NT blocks of 16 channels kept in NT / 4 registers. A 16x16 accumulator
+// fragment with rows = channels wants, at lane (lr, lg), channels
+// 16 t + 4 lg + j (j = 0..3) of block t, the same four values across each
+// 16-lane row lg. Register r therefore holds at lane (lr, lg) channel
+// 16 (4 r + lr / 4) + 4 lg + lr % 4: row lg keeps exactly the values its
+// lanes need, and rows(t) takes them with four DPP row broadcasts
+// (row_newbcast of lane 4 (t % 4) + j of register t / 4): exact copies, four
+// VALU moves per block. This keeps bias loads out of loops whose global loads
+// would otherwise make each bias wait for every earlier load and store
+// (memory operations retire in order).
 template <int NT>
 struct BiasRegs {
   static_assert(NT % 4 == 0, "bias blocks come in fours");
   float reg[NT / 4];
-  float onehot[4];
 
   SHRIMP_DEV void load(const float* bias, int lane) {
     const int lr = lane & 15, lg = lane >> 4;
 #pragma unroll
-    for (int r = 0; r < NT / 4; ++r) reg[r] = bias[(4 * r + lg) * 16 + lr];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) onehot[t] = lg == t ? 1.0f : 0.0f;
+    for (int r = 0; r < NT / 4; ++r) reg[r] = bias[16 * (4 * r + lr / 4) + 4 * lg + lr % 4];
   }
   // 16x16 fragment with rows = channels: lane (lr, lg) gets bias[16 t + 4 lg + j]
+  // (t is a constant once the caller's loops are unrolled)
   SHRIMP_DEV f32x4 rows(int t) const {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(reg[t >> 2], onehot[t & 3],
-                                                 f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    const int v = __builtin_bit_cast(int, reg[t >> 2]);
+    switch (t & 3) {
+      case 0: return bcast4<0>(v);
+      case 1: return bcast4<4>(v);
+      case 2: return bcast4<8>(v);
+      default: return bcast4<12>(v);
+    }
   }
-  // 16x16 fragment with columns = channels: lane (lr, lg) gets bias[16 t + lr]
-  SHRIMP_DEV f32x4 cols(int t) const {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(onehot[t & 3], reg[t >> 2],
-                                                 f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+
+ private:
+  // lanes S .. S + 3 of each 16-lane row, broadcast over the row
+  template <int S>
+  SHRIMP_DEV static f32x4 bcast4(int v) {
+    return f32x4{
+        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x150 + S, 0xF, 0xF, false)),
+        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x151 + S, 0xF, 0xF, false)),
+        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x152 + S, 0xF, 0xF, false)),
+        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x153 + S, 0xF, 0xF, false))};
   }
 };
 

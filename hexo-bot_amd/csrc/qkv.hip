@@ -86,7 +86,13 @@ __global__ __launch_bounds__(QWAVES * 64, 1) void attn_qkv_kernel(const shrimp_q
 
   // the folded biases in registers: the block loop issues no bias loads
   BiasRegs<QN / 16> bias;
-  bias.load(reinterpret_cast<const float*>(static_cast<const unsigned char*>(a.packed) + QB_OFF), lane);
+  const float* pb = reinterpret_cast<const float*>(static_cast<const unsigned char*>(a.packed) + QB_OFF);
+  bias.load(pb, lane);
+  // the v blocks with columns = channels (KVF: V written transposed): lane
+  // (lr, lg) starts all four of its accumulators at bias[16 nb + lr]
+  float vcol[QC / 16];
+#pragma unroll
+  for (int t = 0; t < QC / 16; ++t) vcol[t] = KVF ? pb[16 * (2 * (QC / 16) + t) + lr] : 0.f;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes);
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.qkv, q_bytes);
   const __amdgpu_buffer_rsrc_t kr = make_rsrc(kvf, kvf_bytes);
@@ -134,7 +140,8 @@ __global__ __launch_bounds__(QWAVES * 64, 1) void attn_qkv_kernel(const shrimp_q
       const int which = nb / (QC / 16);
       if (KVF && which == 2) {
         // rows 16 blk + 4 lg .. + 3 of output channel 16 (nb - 16) + lr = head nb - 16, dim lr
-        f32x4 acc = bias.cols(nb);
+        const float vb = vcol[nb - 2 * (QC / 16)];
+        f32x4 acc = f32x4{vb, vb, vb, vb};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) acc = mfma16x16x32(hf[ks], w[ks], acc);
         const int r0 = blk * 16 + lg * 4;
