@@ -159,32 +159,37 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
       }
     }
     if constexpr (LN) {
-      float s = 0.f;
+      // one pass for the row statistics: sum and sum of squares in four
+      // independent chains (one per element j), variance = E[v^2] - mean^2
+      // (the pre-LN conv outputs have |mean| of the order of their spread, so
+      // fp32 keeps the difference to about 2^-22 relative); each value then
+      // takes two FMAs: (v * rstd - mean * rstd) * ln_w + ln_b
+      float sj[4], qj[4];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+      for (int j = 0; j < 4; ++j) {
+        sj[j] = v[0][j];
+        qj[j] = v[0][j] * v[0][j];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s += v[nb][j];
-      const float mean = sum_groups_swap(s) * (1.0f / COUT);
-      float q = 0.f;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[nb][j] -= mean;
-          q += v[nb][j] * v[nb][j];
+        for (int nb = 1; nb < NB; ++nb) {
+          sj[j] += v[nb][j];
+          qj[j] = fmaf(v[nb][j], v[nb][j], qj[j]);
         }
-      float rstd = rsqrtf(sum_groups_swap(q) * (1.0f / COUT) + a.eps);
+      }
+      const float mean = sum_groups_swap((sj[0] + sj[1]) + (sj[2] + sj[3])) * (1.0f / COUT);
+      const float ex2 = sum_groups_swap((qj[0] + qj[1]) + (qj[2] + qj[3])) * (1.0f / COUT);
+      float rstd = rsqrtf(fmaxf(fmaf(-mean, mean, ex2), 0.f) + a.eps);
       int bslot = 2;
       if constexpr (LNMASK) {
         rstd = live[mb] ? rstd : 0.f;
         bslot = live[mb] ? 2 : 4;
       }
+      const float nmr = -mean * rstd;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const f32x4 gw = P_w(nb);
         const f32x4 gb = LNMASK ? prm(lp + bslot * COUT, nb) : P_l(nb);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[nb][j] = fmaf(v[nb][j] * rstd, gw[j], gb[j]);
+        for (int j = 0; j < 4; ++j) v[nb][j] = fmaf(fmaf(v[nb][j], rstd, nmr), gw[j], gb[j]);
       }
     }
     if constexpr (HEAD) {
