@@ -374,7 +374,10 @@ int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_proj_args* p,
  *     a->k, a->v, a->coords and a->mask are not read. Results equal
  *     shrimp_attn's up to the bf16 rounding of P (the softmax offsets may
  *     differ). shrimp_attn_staged_supported(H, S, dpad): dpad = 16, even H,
- *     S % 4 == 0 and the LDS budget.
+ *     S % 4 == 0, S <= 1024 and the workgroup's LDS within the device's
+ *     per-workgroup limit: four waves while it fits 64 KiB (three workgroups
+ *     per compute unit), eight waves with a compute unit's LDS past it
+ *     (S >= 368, the spec-sized supports the evaluator pads to 384-576).
  * ---------------------------------------------------------------------- */
 size_t shrimp_attn_keys_bytes(int S);
 int shrimp_attn_keys(const int32_t* coords, const uint8_t* mask, const int32_t* seq_lens, int B,
