@@ -159,29 +159,33 @@ SHRIMP_DEV void mlp_block(const shrimp_mlp_args& a, const unsigned char* wl, con
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc2[nb][j] = b2[j] + v[nb][j];
   }
-  float s = 0.f;
+  // one pass for the row statistics: four independent sum / sum-of-squares
+  // chains, var = E[v^2] - mean^2, then one FMA per value
+  float sj[4], qj[4];
 #pragma unroll
-  for (int nb = 0; nb < NB1; ++nb)
+  for (int j = 0; j < 4; ++j) {
+    sj[j] = v[0][j];
+    qj[j] = v[0][j] * v[0][j];
+  }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) s += v[nb][j];
-  const float mean = sum_groups_swap(s) * (1.0f / MC);
-  float q = 0.f;
-#pragma unroll
-  for (int nb = 0; nb < NB1; ++nb)
+  for (int nb = 1; nb < NB1; ++nb)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      v[nb][j] -= mean;
-      q = fmaf(v[nb][j], v[nb][j], q);
+      sj[j] += v[nb][j];
+      qj[j] = fmaf(v[nb][j], v[nb][j], qj[j]);
     }
-  const float rstd = rsqrtf(sum_groups_swap(q) * (1.0f / MC) + a.eps);
+  const float mean = sum_groups_swap((sj[0] + sj[1]) + (sj[2] + sj[3])) * (1.0f / MC);
+  const float ex2 = sum_groups_swap((qj[0] + qj[1]) + (qj[2] + qj[3])) * (1.0f / MC);
+  const float rstd = rsqrtf(fmaxf(fmaf(-mean, mean, ex2), 0.f) + a.eps);
+  const float nmr = -mean * rstd;
   u32x4 hf[KS1];
 #pragma unroll
   for (int ks = 0; ks < KS1; ++ks) {
     const int n0 = 2 * ks, n1 = 2 * ks + 1;
-    hf[ks] = u32x4{pack_bf16x2(v[n0][0] * rstd, v[n0][1] * rstd),
-                   pack_bf16x2(v[n0][2] * rstd, v[n0][3] * rstd),
-                   pack_bf16x2(v[n1][0] * rstd, v[n1][1] * rstd),
-                   pack_bf16x2(v[n1][2] * rstd, v[n1][3] * rstd)};
+    hf[ks] = u32x4{pack_bf16x2(fmaf(v[n0][0], rstd, nmr), fmaf(v[n0][1], rstd, nmr)),
+                   pack_bf16x2(fmaf(v[n0][2], rstd, nmr), fmaf(v[n0][3], rstd, nmr)),
+                   pack_bf16x2(fmaf(v[n1][0], rstd, nmr), fmaf(v[n1][1], rstd, nmr)),
+                   pack_bf16x2(fmaf(v[n1][2], rstd, nmr), fmaf(v[n1][3], rstd, nmr))};
   }
   __builtin_amdgcn_sched_barrier(0);
 
