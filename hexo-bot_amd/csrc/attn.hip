@@ -431,6 +431,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? (PROJ == 3 ? 2 : 4) : 1) void at
   const int S = a.S;
   const int SP = (S + 15) & ~15;
   int L = a.seq_lens[b];
+  SHRIMP_DCHECK(L >= 0 && L <= S, SHRIMP_DBG_SEQ_LEN);
   L = L < 0 ? 0 : (L > S ? S : L);
   const int LP = (L + 15) & ~15;
   const int nt = a.n_tokens;
@@ -1159,7 +1160,9 @@ static int64_t attn_out_extent(const shrimp_attn_args* a) {
   return ((int64_t)(a->B - 1) * a->o_sb + (int64_t)(a->H - 1) * a->o_sh + (int64_t)(a->S - 1) * a->o_sr +
           a->d) * 2;
 }
-static bool attn_out_fits(const shrimp_attn_args* a) { return attn_out_extent(a) < (int64_t)0x7FFF0000; }
+static bool attn_out_fits(const shrimp_attn_args* a) {
+  return strides_ok({a->o_sb, a->o_sh, a->o_sr}) && attn_out_extent(a) < (int64_t)0x7FFF0000;
+}
 static uint32_t attn_out_bytes(const shrimp_attn_args* a) { return (uint32_t)attn_out_extent(a); }
 
 // LDS bytes of one workgroup; npos = pair-table rows (pair mode only).
@@ -1228,6 +1231,7 @@ __global__ void attn_bias_table_kernel(const float* __restrict__ table, int tabl
   int row;
   if (pos < npos_lut) row = lut[pos];
   else row = pos == npos_lut ? r_ct : (pos == npos_lut + 1 ? r_tc : r_tt);
+  SHRIMP_DCHECK(row < table_rows, SHRIMP_DBG_TABLE_ROW);
   row = row < table_rows ? row : table_rows - 1;
   btab[i] = table[row * H + h] * SHRIMP_LOG2E;
 }
@@ -1260,6 +1264,7 @@ __global__ __launch_bounds__(256) void attn_keys_kernel(const int32_t* __restric
   const int b = blockIdx.x, tid = threadIdx.x;
   const int SP = (S + 15) & ~15, NKB = SP / 16, NC = S - nt;
   int L = seq_lens[b];
+  SHRIMP_DCHECK(L >= 0 && L <= S, SHRIMP_DBG_SEQ_LEN);
   L = L < 0 ? 0 : (L > S ? S : L);
   const int mi = attn_meta_ints(SP);
   int* m = meta + (int64_t)b * mi;
@@ -1347,7 +1352,13 @@ extern "C" int shrimp_attn_bias_table(const float* table, int table_rows, int H,
                                       int tok_row_tc, int tok_row_tt, float* btab, void* xtab,
                                       void* stream) {
   SHRIMP_REQUIRE(table && lut && btab, "attn_bias_table: null pointer");
-  SHRIMP_REQUIRE(table_rows > 0 && H > 0 && lut_m >= 0, "attn_bias_table: bad sizes");
+  SHRIMP_REQUIRE(table_rows > 0 && table_rows <= kMaxDim && H > 0 && H <= 1024 && lut_m >= 0 &&
+                     lut_m <= 64,
+                 "attn_bias_table: bad sizes (rows %d, H %d, lut_m %d)", table_rows, H, lut_m);
+  SHRIMP_REQUIRE(tok_row_ct >= 0 && tok_row_ct < table_rows && tok_row_tc >= 0 &&
+                     tok_row_tc < table_rows && tok_row_tt >= 0 && tok_row_tt < table_rows,
+                 "attn_bias_table: token rows (%d, %d, %d) outside the %d table rows", tok_row_ct,
+                 tok_row_tc, tok_row_tt, table_rows);
   const int w = 2 * lut_m + 1;
   const int total = (w * w + 3) * H;
   hipLaunchKernelGGL(attn_bias_table_kernel, dim3((total + 255) / 256), dim3(256), 0,
@@ -1363,7 +1374,8 @@ extern "C" int shrimp_attn_bias_table(const float* table, int table_rows, int H,
 
 extern "C" int shrimp_attn(const shrimp_attn_args* a, void* stream) {
   SHRIMP_REQUIRE(a != nullptr, "attn: null args");
-  SHRIMP_REQUIRE(a->B >= 0 && a->S > 0 && a->H > 0, "attn: bad shape");
+  SHRIMP_REQUIRE(a->B >= 0 && a->S > 0 && a->S <= kMaxDim && a->H > 0 && a->H <= kMaxDim,
+                 "attn: bad shape");
   if (a->B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(a->q && a->k && a->v && a->o && a->seq_lens, "attn: null pointer");
   SHRIMP_REQUIRE(a->d > 0 && a->d % 4 == 0 && a->d <= a->dpad, "attn: head dim %d / pad %d",
@@ -1372,6 +1384,7 @@ extern "C" int shrimp_attn(const shrimp_attn_args* a, void* stream) {
                  "attn: output strides must be multiples of 4");
   SHRIMP_REQUIRE(attn_out_fits(a), "attn: output buffer too large");
   SHRIMP_REQUIRE(a->n_tokens >= 0 && a->n_tokens <= a->S, "attn: bad n_tokens");
+  SHRIMP_REQUIRE(strides_ok({a->qkv_sb, a->qkv_sh, a->p_sb, a->p_sq}), "attn: strides outside [0, 2^31)");
   const int64_t extent =
       (int64_t)(a->B - 1) * a->qkv_sb + (int64_t)(a->H - 1) * a->qkv_sh + (int64_t)a->S * a->dpad;
   SHRIMP_REQUIRE(extent * 2 < (int64_t)0x7FFF0000, "attn: q/k/v buffers too large");
@@ -1396,11 +1409,13 @@ extern "C" int shrimp_attn_fused_supported(int C, int H, int S, int dpad) {
 extern "C" int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_proj_args* p,
                                  void* stream) {
   SHRIMP_REQUIRE(a != nullptr && p != nullptr, "attn_fused: null args");
-  SHRIMP_REQUIRE(a->B >= 0 && a->S > 0 && a->H > 0, "attn_fused: bad shape");
+  SHRIMP_REQUIRE(a->B >= 0 && a->S > 0 && a->S <= kMaxDim && a->H > 0 && a->H <= kMaxDim,
+                 "attn_fused: bad shape");
   if (a->B == 0) return SHRIMP_OK;
-  SHRIMP_REQUIRE(shrimp_attn_fused_supported(a->H * a->d, a->H, a->S, a->dpad),
-                 "attn_fused: covers C = %d, H = 8, dpad = 16, S <= %d (got C = %d, H = %d, "
-                 "dpad = %d, S = %d)", QKV_C, PROJ_MAX_S, a->H * a->d, a->H, a->dpad, a->S);
+  const long long fc = (long long)a->H * a->d;
+  SHRIMP_REQUIRE(fc == QKV_C && shrimp_attn_fused_supported(QKV_C, a->H, a->S, a->dpad),
+                 "attn_fused: covers C = %d, H = 8, dpad = 16, S <= %d (got C = %lld, H = %d, "
+                 "dpad = %d, S = %d)", QKV_C, PROJ_MAX_S, fc, a->H, a->dpad, a->S);
   SHRIMP_REQUIRE(a->pair == nullptr, "attn_fused: coords mode only");
   SHRIMP_REQUIRE(a->o && a->seq_lens && p->x && p->packed, "attn_fused: null pointer");
   SHRIMP_REQUIRE(a->o_sb % 4 == 0 && a->o_sh % 4 == 0 && a->o_sr % 4 == 0,
@@ -1410,6 +1425,7 @@ extern "C" int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_pr
   SHRIMP_REQUIRE(a->btab && a->lut_m >= 0 && a->lut_m <= 64, "attn_fused: needs btab");
   SHRIMP_REQUIRE(a->n_tokens == a->S || (a->coords && a->mask),
                  "attn_fused: needs coords and mask");
+  SHRIMP_REQUIRE(strides_ok({p->x_sb, p->x_sr}), "attn_fused: x strides outside [0, 2^31)");
   SHRIMP_REQUIRE(p->x_sr >= QKV_C && p->x_sr % 8 == 0 && p->x_sb % 8 == 0 &&
                      p->x_sb >= (int64_t)(a->S - 1) * p->x_sr + QKV_C,
                  "attn_fused: x strides (row %lld, position %lld)", (long long)p->x_sr,
@@ -1431,12 +1447,13 @@ extern "C" int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_pr
 }
 
 extern "C" size_t shrimp_attn_keys_bytes(int S) {
-  return S > 0 ? (size_t)attn_meta_ints((S + 15) & ~15) * 4 : 0;
+  return S > 0 && S <= kMaxDim ? (size_t)attn_meta_ints((S + 15) & ~15) * 4 : 0;
 }
 
 extern "C" int shrimp_attn_keys(const int32_t* coords, const uint8_t* mask, const int32_t* seq_lens,
                                 int B, int S, int n_tokens, int32_t* meta, void* stream) {
-  SHRIMP_REQUIRE(B >= 0 && S > 0 && n_tokens >= 0 && n_tokens <= S, "attn_keys: bad shape");
+  SHRIMP_REQUIRE(B >= 0 && S > 0 && S <= 4096 && n_tokens >= 0 && n_tokens <= S,
+                 "attn_keys: bad shape (S = %d, at most 4096)", S);
   if (B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(seq_lens && meta && (n_tokens == S || (coords && mask)), "attn_keys: null pointer");
   const int SP = (S + 15) & ~15;
@@ -1451,6 +1468,7 @@ extern "C" int shrimp_attn_keys(const int32_t* coords, const uint8_t* mask, cons
 // unit's LDS to itself past it (two waves per SIMD, up to 256 registers each):
 // supports of 368 cells and more, as the evaluator pads spec-sized positions.
 extern "C" int shrimp_attn_staged_supported(int H, int S, int dpad) {
+  if (S <= 0 || S > 1024) return 0;
   const int SP = (S + 15) & ~15;
   return dpad == 16 && H > 0 && H % 2 == 0 && S > 0 && S % 4 == 0 && SP <= 1024 &&
          attn_smem_bytes(16, 2, S, 0, false) <= (size_t)max_lds_per_block();
@@ -1474,8 +1492,9 @@ extern "C" int shrimp_attn_staged(const shrimp_attn_args* a, const void* kvf, co
   SHRIMP_REQUIRE(a->n_tokens >= 0 && a->n_tokens <= a->S, "attn_staged: bad n_tokens");
   SHRIMP_REQUIRE(a->lut_m >= 0 && a->lut_m <= 64, "attn_staged: lut_m");
   const int SP = (a->S + 15) & ~15;
-  const int64_t kvb = (int64_t)a->B * a->H * SP * 64;
-  const int64_t mb = (int64_t)a->B * shrimp_attn_keys_bytes(a->S);
+  SHRIMP_REQUIRE(strides_ok({a->qkv_sb, a->qkv_sh}), "attn_staged: q strides outside [0, 2^31)");
+  const int64_t kvb = mul_sat({a->B, a->H, SP, 64});
+  const int64_t mb = mul_sat({a->B, (int64_t)shrimp_attn_keys_bytes(a->S)});
   const int64_t qe = ((int64_t)(a->B - 1) * a->qkv_sb + (int64_t)(a->H - 1) * a->qkv_sh +
                       (int64_t)a->S * a->dpad) * 2;
   SHRIMP_REQUIRE(kvb < (int64_t)0x7FFF0000 && mb < (int64_t)0x7FFF0000 && qe < (int64_t)0x7FFF0000,

@@ -7,21 +7,64 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <initializer_list>
 #include <string>
 
 #include "shrimp_hip.h"
+
+// Checked builds (SHRIMP_DEBUG=1) compile the kernels' input checks
+// (SHRIMP_DCHECK, common.hpp) and synchronise after every launch.
+#ifndef SHRIMP_DEBUG
+#define SHRIMP_DEBUG 0
+#endif
 
 namespace shrimp {
 
 int set_error(int code, const char* fmt, ...);
 
-inline int check_launch(const char* what) {
+#if SHRIMP_DEBUG
+// Waits for the device, then reads and clears the fault word of the calling
+// source file's kernels (defined beside that word in common.hpp).
+static int debug_sync(const char* what);
+#endif
+
+static inline int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(SHRIMP_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+#if SHRIMP_DEBUG
+  return debug_sync(what);
+#else
   return SHRIMP_OK;
+#endif
 }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Strides (in elements) that the buffer-extent checks accept: non-negative and
+// below 2^31, so an extent (count - 1) * stride + width stays far inside
+// int64_t for any int32 count and width (larger strides could not pass the
+// 32-bit buffer-offset limit anyway).
+inline bool strides_ok(std::initializer_list<int64_t> strides) {
+  for (int64_t v : strides)
+    if (v < 0 || v >= ((int64_t)1 << 31)) return false;
+  return true;
+}
+
+// Largest row / sequence count an entry point takes: past it no buffer of the
+// shape fits a 32-bit offset, and rounding it up stays inside int.
+constexpr int kMaxDim = 1 << 24;
+
+// Product of non-negative factors, INT64_MAX when it overflows (a negative
+// factor gives -1): byte counts checked against a limit without signed
+// overflow.
+inline int64_t mul_sat(std::initializer_list<int64_t> factors) {
+  int64_t r = 1;
+  for (int64_t v : factors) {
+    if (v < 0) return -1;
+    if (__builtin_mul_overflow(r, v, &r)) return INT64_MAX;
+  }
+  return r;
+}
 
 // Largest dynamic LDS allocation one workgroup may request on the current
 // device (queried once per device).

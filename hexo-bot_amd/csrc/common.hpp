@@ -45,6 +45,54 @@ SHRIMP_DEV unsigned buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0);
 }
 
+// ---- input checks of checked builds (SHRIMP_DEBUG=1) ---------------------------
+//
+// SHRIMP_DCHECK(cond, bit) compiles to nothing in release builds. In checked
+// builds a failed condition sets `bit` in this source file's device fault word
+// (a relaxed device-scope atomic OR; the kernel then goes on exactly as a
+// release build does, so an absent row still reads zeros), and the launch
+// wrapper's check_launch synchronises and reports the word as SHRIMP_ECHECK.
+#define SHRIMP_DBG_CONV_INDEX 0x1u  // conv neighbour index outside [-1, N]
+#define SHRIMP_DBG_SEQ_LEN 0x2u     // sequence length outside [0, S]
+#define SHRIMP_DBG_RAY_INDEX 0x4u   // ray-tap / gather index outside [-1, N]
+#define SHRIMP_DBG_LEGAL 0x8u       // legal count outside [0, row]
+#define SHRIMP_DBG_NBR 0x10u        // packed neighbour id neither absent nor in the row
+#define SHRIMP_DBG_TABLE_ROW 0x20u  // bias LUT entry past the bias table's rows
+
+#if SHRIMP_DEBUG
+namespace shrimp {
+static __device__ unsigned g_debug_fault;
+
+SHRIMP_DEV void debug_fault(unsigned bit) {
+  __hip_atomic_fetch_or(&g_debug_fault, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+static int debug_sync(const char* what) {
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return set_error(SHRIMP_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+  unsigned f = 0;
+  e = hipMemcpyFromSymbol(&f, HIP_SYMBOL(g_debug_fault), sizeof(f));
+  if (e != hipSuccess) return set_error(SHRIMP_ELAUNCH, "%s: fault word: %s", what, hipGetErrorString(e));
+  if (f == 0) return SHRIMP_OK;
+  const unsigned zero = 0;
+  (void)hipMemcpyToSymbol(HIP_SYMBOL(g_debug_fault), &zero, sizeof(zero));
+  return set_error(SHRIMP_ECHECK, "%s: input checks failed (0x%x:%s%s%s%s%s%s)", what, f,
+                   (f & SHRIMP_DBG_CONV_INDEX) ? " conv index" : "",
+                   (f & SHRIMP_DBG_SEQ_LEN) ? " sequence length" : "",
+                   (f & SHRIMP_DBG_RAY_INDEX) ? " ray/gather index" : "",
+                   (f & SHRIMP_DBG_LEGAL) ? " legal count" : "",
+                   (f & SHRIMP_DBG_NBR) ? " neighbour id" : "",
+                   (f & SHRIMP_DBG_TABLE_ROW) ? " bias table row" : "");
+}
+}  // namespace shrimp
+#define SHRIMP_DCHECK(cond, bit)                  \
+  do {                                            \
+    if (!(cond)) ::shrimp::debug_fault(bit);      \
+  } while (0)
+#else
+#define SHRIMP_DCHECK(cond, bit) ((void)0)
+#endif
+
 // ---- bf16 <-> f32 -----------------------------------------------------------
 
 SHRIMP_DEV float bf16_lo(unsigned w) { return __uint_as_float(w << 16); }

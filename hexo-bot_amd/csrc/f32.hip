@@ -220,6 +220,7 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
       for (int mb = 0; mb < MB; ++mb) {
         jn[mb] = rn[mb];
         if (GATHER) jn[mb] = rv[mb] ? g.idx[((int64_t)rb[mb] * g.N + rn[mb]) * g.idx_stride + t] : -1;
+        SHRIMP_DCHECK(!GATHER || (jn[mb] >= -1 && jn[mb] <= g.N), SHRIMP_DBG_CONV_INDEX);
       }
     };
     auto tap_off = [&]() {
@@ -323,6 +324,7 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
     for (int mb = 0; mb < MB; ++mb) {
       int j = rn[mb];
       if (GATHER) j = rv[mb] ? g.idx[((int64_t)rb[mb] * g.N + rn[mb]) * g.idx_stride + t] : -1;
+      SHRIMP_DCHECK(!GATHER || (j >= -1 && j <= g.N), SHRIMP_DBG_CONV_INDEX);
       const bool ok = rv[mb] && j >= 0 && j < g.N;
       xoff[mb] = ok ? (uint32_t)(((int64_t)rb[mb] * g.x_sb + (int64_t)j * g.x_sr) * 4) +
                           (uint32_t)(lg * 16)
@@ -602,6 +604,7 @@ __global__ __launch_bounds__(AR_THREADS) void attn_rows_kernel(const shrimp_attn
   const int i = blockIdx.x * AR_THREADS + tid;
   const int S = a.S, d = a.d, nt = a.n_tokens, NC = S - nt;
   int L = a.seq_lens[b];
+  SHRIMP_DCHECK(L >= 0 && L <= S, SHRIMP_DBG_SEQ_LEN);
   L = L < 0 ? 0 : (L > S ? S : L);
   const bool qv = i < L;
   const T* q = static_cast<const T*>(a.q) + (int64_t)b * a.qkv_sb + (int64_t)h * a.qkv_sh;
@@ -738,6 +741,7 @@ __global__ __launch_bounds__(A32_NW * 64) void attn32_mfma_kernel(const shrimp_a
   const int S = a.S, H = a.H, nt = a.n_tokens, NC = S - nt;
   const int SP = (S + 15) & ~15, NKB = SP / 16;
   int L = a.seq_lens[b];
+  SHRIMP_DCHECK(L >= 0 && L <= S, SHRIMP_DBG_SEQ_LEN);
   L = L < 0 ? 0 : (L > S ? S : L);
   const int M = a.lut_m, W = 2 * M + 1;
 
@@ -1076,8 +1080,10 @@ using namespace shrimp;
 
 // ---- C ABI ------------------------------------------------------------------------------
 
+// 0 for a shape whose packed weights would not fit a 32-bit buffer offset
 extern "C" size_t shrimp_conv_wpack_bytes_f32(int taps, int cin_pad, int cout) {
-  return (size_t)taps * cin_pad * cout * 4;
+  const int64_t n = mul_sat({taps, cin_pad, cout, 4});
+  return taps > 0 && cin_pad > 0 && cout > 0 && n < (int64_t)0x7FFF0000 ? (size_t)n : 0;
 }
 
 extern "C" int shrimp_pack_conv_weight_f32(const float* w, float* packed, int taps, int cin,
@@ -1085,7 +1091,8 @@ extern "C" int shrimp_pack_conv_weight_f32(const float* w, float* packed, int ta
   SHRIMP_REQUIRE(w && packed, "pack_conv_weight_f32: null pointer");
   SHRIMP_REQUIRE(taps > 0 && cin > 0 && cin <= cin_pad && cin_pad % 16 == 0,
                  "pack_conv_weight_f32: bad taps/cin (%d, %d, %d)", taps, cin, cin_pad);
-  SHRIMP_REQUIRE(cout > 0 && cout % 16 == 0, "pack_conv_weight_f32: cout %d", cout);
+  SHRIMP_REQUIRE(cout > 0 && cout % 16 == 0 && shrimp_conv_wpack_bytes_f32(taps, cin_pad, cout) > 0,
+                 "pack_conv_weight_f32: cout %d", cout);
   pack_w32(w, packed, taps, cin, cin_pad, cout, (int64_t)cin * cout, (int64_t)cout, (int64_t)1,
            as_stream(stream));
   return check_launch("pack_conv_weight_f32");
@@ -1095,7 +1102,7 @@ extern "C" int shrimp_pack_linear_weight_f32(const float* w, float* packed, int 
                                              int out_features, void* stream) {
   SHRIMP_REQUIRE(w && packed, "pack_linear_weight_f32: null pointer");
   SHRIMP_REQUIRE(in_features > 0 && in_features % 16 == 0 && out_features > 0 &&
-                     out_features % 16 == 0,
+                     out_features % 16 == 0 && shrimp_conv_wpack_bytes_f32(1, in_features, out_features) > 0,
                  "pack_linear_weight_f32: shape (%d -> %d) needs multiples of 16", in_features,
                  out_features);
   pack_w32(w, packed, 1, in_features, in_features, out_features, (int64_t)0, (int64_t)1,
@@ -1105,12 +1112,14 @@ extern "C" int shrimp_pack_linear_weight_f32(const float* w, float* packed, int 
 
 extern "C" int shrimp_hex_conv_f32(const shrimp_conv_args* a, void* stream) {
   SHRIMP_REQUIRE(a != nullptr, "hex_conv_f32: null args");
-  SHRIMP_REQUIRE(a->B >= 0 && a->N > 0, "hex_conv_f32: bad shape");
+  SHRIMP_REQUIRE(a->B >= 0 && a->N > 0 && a->N <= kMaxDim, "hex_conv_f32: bad shape");
   if (a->B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(a->x && a->idx && a->mask && a->w && a->bias, "hex_conv_f32: null pointer");
   SHRIMP_REQUIRE(a->taps > 0 && a->taps <= a->idx_stride, "hex_conv_f32: taps / idx stride");
   SHRIMP_REQUIRE(a->cin_pad > 0 && a->cin_pad % 16 == 0 && a->cout > 0 && a->cout % 16 == 0,
                  "hex_conv_f32: cin_pad %d / cout %d must be multiples of 16", a->cin_pad, a->cout);
+  SHRIMP_REQUIRE(strides_ok({a->x_sb, a->x_sn, a->o_sb, a->o_sn, a->r_sb, a->r_sn}),
+                 "hex_conv_f32: strides outside [0, 2^31)");
   SHRIMP_REQUIRE(a->x_sn >= a->cin_pad && a->x_sn % 4 == 0 && a->x_sb % 4 == 0,
                  "hex_conv_f32: x strides");
   const bool ln = a->ln_w != nullptr, resid = a->resid != nullptr, head = a->head_w != nullptr;
@@ -1171,6 +1180,7 @@ extern "C" int shrimp_linear_f32(const shrimp_linear_args* a, void* stream) {
   SHRIMP_REQUIRE(a->in_features % 16 == 0 && a->out_features % 16 == 0,
                  "linear_f32: in %d / out %d must be multiples of 16", a->in_features,
                  a->out_features);
+  SHRIMP_REQUIRE(strides_ok({a->x_sr, a->o_sr, a->r_sr}), "linear_f32: row strides outside [0, 2^31)");
   SHRIMP_REQUIRE(a->x_sr >= a->in_features && a->x_sr % 4 == 0, "linear_f32: x row stride");
   const bool ln = a->ln_w != nullptr;
   SHRIMP_REQUIRE(!ln || a->ln_b, "linear_f32: ln_w without ln_b");
@@ -1230,7 +1240,8 @@ extern "C" int shrimp_linear_f32(const shrimp_linear_args* a, void* stream) {
 
 extern "C" int shrimp_attn_f32(const shrimp_attn_args* a, void* stream) {
   SHRIMP_REQUIRE(a != nullptr, "attn_f32: null args");
-  SHRIMP_REQUIRE(a->B >= 0 && a->S > 0 && a->H > 0, "attn_f32: bad shape");
+  SHRIMP_REQUIRE(a->B >= 0 && a->S > 0 && a->S <= kMaxDim && a->H > 0 && a->H <= kMaxDim,
+                 "attn_f32: bad shape");
   if (a->B == 0) return SHRIMP_OK;
   int npos = 0;
   if (int rc = check_attn_rows(a, 4, &npos)) return rc;
@@ -1253,7 +1264,7 @@ extern "C" int shrimp_attn_f32(const shrimp_attn_args* a, void* stream) {
 
 extern "C" int shrimp_prep_feats_f32(const void* feats, int feats_dt, int nfeat, int B, int N,
                                      float* xin, void* stream) {
-  SHRIMP_REQUIRE(B >= 0 && N > 0, "prep_feats_f32: bad shape");
+  SHRIMP_REQUIRE(B >= 0 && N > 0 && N <= kMaxDim, "prep_feats_f32: bad shape");
   if (B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(feats && xin && nfeat > 0 && nfeat <= 16, "prep_feats_f32: feats (nfeat %d)",
                  nfeat);
@@ -1274,7 +1285,7 @@ extern "C" int shrimp_prep_feats_f32(const void* feats, int feats_dt, int nfeat,
 extern "C" int shrimp_prep_csr_feats_f32(const void* node_feats, int nfeat,
                                          const int64_t* row_offsets, int row0, int B, int N,
                                          float* xin, void* stream) {
-  SHRIMP_REQUIRE(B >= 0 && N > 0 && row0 >= 0, "prep_csr_feats_f32: bad sizes");
+  SHRIMP_REQUIRE(B >= 0 && N > 0 && N <= kMaxDim && row0 >= 0, "prep_csr_feats_f32: bad sizes");
   if (B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(node_feats && row_offsets && xin && nfeat > 0 && nfeat <= 16,
                  "prep_csr_feats_f32: null pointer or nfeat %d", nfeat);

@@ -371,6 +371,7 @@ __global__ __launch_bounds__(256, 2) void hex_conv_kernel(const shrimp_conv_args
     for (int mb = 0; mb < MB; ++mb) {
       int j = -1;
       if (rv[mb]) j = a.idx[(int64_t)(rb[mb] * N + rn[mb]) * a.idx_stride + t];
+      SHRIMP_DCHECK(j >= -1 && j <= N, SHRIMP_DBG_CONV_INDEX);
       const bool ok = (j >= 0) && (j < N);
       const int64_t e = (int64_t)rb[mb] * a.x_sb + (int64_t)j * a.x_sn;
       off[mb] = ok ? (uint32_t)(e * 2) + (uint32_t)(lg * 16) : SHRIMP_OOB_OFFSET;
@@ -533,6 +534,7 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         int v = rv[mb] ? idxb[rn[mb] * a.idx_stride + t] : N;
+        SHRIMP_DCHECK(v >= -1 && v <= N, SHRIMP_DBG_CONV_INDEX);
         j[mb] = (v >= 0 && v < N) ? v : N;
       }
     };
@@ -830,6 +832,7 @@ SHRIMP_DEV void big_setup(BigTile& t, const shrimp_conv_args& a, unsigned char* 
         const int mb = 2 * m2 + h;
         const unsigned raw = tp < 4 ? i0[mb][tp] : (tp < 6 ? i1[mb][tp - 4] : i2[mb]);
         const int j = t.rv[mb] ? (int)raw : t.N;
+        SHRIMP_DCHECK(j >= -1 && j <= t.N, SHRIMP_DBG_CONV_INDEX);
         const int jj = (j >= 0 && j < t.N) ? j : t.N;
         pk |= (uint32_t)(jj * 64 + (((jj >> 2) & 3) << 4)) << (16 * h);
       }
@@ -1452,12 +1455,15 @@ static size_t conv_lds_bytes(const shrimp_conv_args* a) {
 
 using namespace shrimp;
 
+// 0 for a shape whose packed weights would not fit a 32-bit buffer offset
 extern "C" size_t shrimp_conv_wpack_bytes(int taps, int cin_pad, int cout) {
-  return (size_t)taps * cin_pad * cout * 2;
+  const int64_t n = mul_sat({taps, cin_pad, cout, 2});
+  return taps > 0 && cin_pad > 0 && cout > 0 && n < (int64_t)0x7FFF0000 ? (size_t)n : 0;
 }
 
 extern "C" size_t shrimp_linear_wpack_bytes(int in_features, int out_features) {
-  return (size_t)in_features * out_features * 2;
+  const int64_t n = mul_sat({in_features, out_features, 2});
+  return in_features > 0 && out_features > 0 && n < (int64_t)0x7FFF0000 ? (size_t)n : 0;
 }
 
 extern "C" int shrimp_pack_conv_weight(const float* w, void* packed, int taps, int cin,
@@ -1467,6 +1473,7 @@ extern "C" int shrimp_pack_conv_weight(const float* w, void* packed, int taps, i
                  "pack_conv_weight: bad taps/cin (%d, %d, %d)", taps, cin, cin_pad);
   SHRIMP_REQUIRE(cout > 0 && cout % 16 == 0, "pack_conv_weight: cout %d not a multiple of 16",
                  cout);
+  SHRIMP_REQUIRE(shrimp_conv_wpack_bytes(taps, cin_pad, cout) > 0, "pack_conv_weight: too large");
   const int K = taps * cin_pad;
   const int64_t frags = (int64_t)(K / 32) * (cout / 16) * 64;
   const int grid = (int)((frags + 255) / 256);
@@ -1479,7 +1486,8 @@ extern "C" int shrimp_pack_conv_weight(const float* w, void* packed, int taps, i
 static int pack_linear(const float* w, void* packed, int in_features, int out_features,
                        void* stream, int interleaved) {
   SHRIMP_REQUIRE(w && packed, "pack_linear_weight: null pointer");
-  SHRIMP_REQUIRE(in_features % 32 == 0 && out_features % 16 == 0,
+  SHRIMP_REQUIRE(in_features % 32 == 0 && out_features % 16 == 0 &&
+                     shrimp_linear_wpack_bytes(in_features, out_features) > 0,
                  "pack_linear_weight: shape (%d -> %d) needs in %% 32 == 0, out %% 16 == 0",
                  in_features, out_features);
   const int64_t frags = (int64_t)(in_features / 32) * (out_features / 16) * 64;
@@ -1498,13 +1506,15 @@ extern "C" int shrimp_pack_linear_weight(const float* w, void* packed, int in_fe
 
 extern "C" int shrimp_hex_conv(const shrimp_conv_args* a, void* stream) {
   SHRIMP_REQUIRE(a != nullptr, "hex_conv: null args");
-  SHRIMP_REQUIRE(a->B >= 0 && a->N > 0, "hex_conv: bad B/N (%d, %d)", a->B, a->N);
+  SHRIMP_REQUIRE(a->B >= 0 && a->N > 0 && a->N <= kMaxDim, "hex_conv: bad B/N (%d, %d)", a->B, a->N);
   if (a->B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(a->x && a->idx && a->mask && a->w && a->bias, "hex_conv: null input pointer");
   SHRIMP_REQUIRE(a->taps > 0 && a->idx_stride >= a->taps, "hex_conv: bad taps %d / stride %d",
                  a->taps, a->idx_stride);
   SHRIMP_REQUIRE(a->cin_pad > 0 && a->cin_pad % 32 == 0, "hex_conv: cin_pad %d %% 32 != 0",
                  a->cin_pad);
+  SHRIMP_REQUIRE(strides_ok({a->x_sb, a->x_sn, a->o_sb, a->o_sn, a->r_sb, a->r_sn}),
+                 "hex_conv: strides outside [0, 2^31)");
   SHRIMP_REQUIRE(a->x_sn >= a->cin_pad && a->x_sn % 8 == 0,
                  "hex_conv: row stride %lld must be >= cin_pad and a multiple of 8",
                  (long long)a->x_sn);
@@ -1564,6 +1574,7 @@ static int check_block(const shrimp_conv_args* c1, const shrimp_conv_args* c2, s
   SHRIMP_REQUIRE(c1->x && c1->idx && c1->mask && c1->w && c1->bias && c2->w && c2->bias,
                  "conv_block: null input pointer");
   SHRIMP_REQUIRE(c1->idx_stride >= 7, "conv_block: idx_stride %d < 7", c1->idx_stride);
+  SHRIMP_REQUIRE(strides_ok({c1->x_sb, c1->x_sn, c2->o_sb, c2->o_sn}), "conv_block: strides outside [0, 2^31)");
   SHRIMP_REQUIRE(c1->ln_w && c1->ln_b && c1->relu && !c1->resid && !c1->head_w,
                  "conv_block: conv1 must be conv + LN + ReLU");
   SHRIMP_REQUIRE(c2->ln_w && c2->ln_b && !c2->relu && c2->gamma && !c2->head_w && c2->out,
@@ -1683,6 +1694,7 @@ extern "C" int shrimp_policy_tail(const shrimp_conv_args* p, const shrimp_tail_a
   SHRIMP_REQUIRE(p->x == static_cast<const uint16_t*>(ta->seq) + (int64_t)ta->n_tokens * 128 &&
                      p->x_sb == ta->s_sb && p->x_sn == 128 && p->mask == ta->mask,
                  "policy_tail: the policy conv must read the cell rows of tail.seq with its mask");
+  SHRIMP_REQUIRE(strides_ok({p->x_sb}), "policy_tail: position stride outside [0, 2^31)");
   const int64_t x_extent = (int64_t)(p->B - 1) * p->x_sb + (int64_t)(N - 1) * p->x_sn + 128;
   SHRIMP_REQUIRE(x_extent * 2 < (int64_t)0x7FFF0000, "policy_tail: activation buffer too large");
   const int waves = (N + 127) / 128;

@@ -124,6 +124,7 @@ __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_a
   }
   const int N = a.N;
   const int nh = min(2, a.H - 2 * p);
+  SHRIMP_DCHECK(a.seq_lens[b] >= 0 && a.seq_lens[b] <= N, SHRIMP_DBG_SEQ_LEN);
   const int live_rows = min(max(a.seq_lens[b], 0), N);
   const int nst = STAGE ? live_rows : 0;
   const int part = (int)threadIdx.x % LPR;
@@ -203,6 +204,8 @@ __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_a
     js[0] = ir[0];
 #pragma unroll
     for (int t = 0; t < 10; ++t) js[1 + t] = axis ? ir[1 + 10 * p + t] : -1;
+#pragma unroll
+    for (int t = 0; t < 11; ++t) SHRIMP_DCHECK(js[t] >= -1 && js[t] <= N, SHRIMP_DBG_RAY_INDEX);
     uint32_t rl4 = 0x05050505u;  // reach (own dir 0, own dir 1, opp dir 0, opp dir 1)
     if (a.blockers && axis) {
       const uint8_t* rl = a.raylen + (int64_t)b * a.rl_sb + (int64_t)r * a.rl_sn + 2 * p;
@@ -366,6 +369,7 @@ __global__ __launch_bounds__(64 * RT_MAX_WAVES) void conv_ln_raytap_kernel(
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int j = rv[mb] ? a.gather_idx[(int64_t)b * a.g_sb + (int64_t)rn[mb] * a.g_sn] : N;
+    SHRIMP_DCHECK(j >= -1 && j <= N, SHRIMP_DBG_RAY_INDEX);
     crow[mb] = (unsigned)j < (unsigned)N ? (uint32_t)j : (uint32_t)N;
   }
   // Side of the lane's two 4-channel halves of chunk kc, (c % corb) >= corb / 2:
@@ -391,7 +395,10 @@ __global__ __launch_bounds__(64 * RT_MAX_WAVES) void conv_ln_raytap_kernel(
     if (trow < N) {
       const int32_t* ir = rib + (int64_t)trow * a.r_sn + RT_SLOT_BASE[t];
 #pragma unroll
-      for (int k = 0; k < RAY_STEPS; ++k) pj[k] = ir[k];
+      for (int k = 0; k < RAY_STEPS; ++k) {
+        pj[k] = ir[k];
+        SHRIMP_DCHECK(pj[k] >= -1 && pj[k] <= N, SHRIMP_DBG_RAY_INDEX);
+      }
       const uint8_t* re = reb + (int64_t)trow * a.re_sn;
       preach = (uint32_t)re[t] | ((uint32_t)re[6 + t] << 8);
     }
@@ -615,7 +622,7 @@ extern "C" int shrimp_ray_attn_variant(int v) {
 
 extern "C" int shrimp_ray_attn(const shrimp_ray_attn_args* a, void* stream) {
   SHRIMP_REQUIRE(a, "ray_attn: null args");
-  SHRIMP_REQUIRE(a->B >= 0 && a->H >= 1 && a->N >= 1, "ray_attn: bad shape B=%d H=%d N=%d", a->B,
+  SHRIMP_REQUIRE(a->B >= 0 && a->H >= 1 && a->H <= kMaxDim && a->N >= 1 && a->N <= kMaxDim, "ray_attn: bad shape B=%d H=%d N=%d", a->B,
                  a->H, a->N);
   SHRIMP_REQUIRE(a->D == 16 || a->D == 32 || a->D == 64 || a->D == 128,
                  "ray_attn: head dim %d not in {16, 32, 64, 128}", a->D);
@@ -628,7 +635,10 @@ extern "C" int shrimp_ray_attn(const shrimp_ray_attn_args* a, void* stream) {
   const int64_t st[12] = {a->q_sb, a->q_sh, a->q_sn, a->k_sb, a->k_sh, a->k_sn,
                           a->v_sb, a->v_sh, a->v_sn, a->o_sb, a->o_sh, a->o_sn};
   for (int i = 0; i < 12; ++i)
-    SHRIMP_REQUIRE(st[i] % 8 == 0, "ray_attn: q/k/v/out strides must be multiples of 8 elements");
+    SHRIMP_REQUIRE(st[i] % 8 == 0 && st[i] > -(1LL << 31) && st[i] < (1LL << 31),
+                   "ray_attn: q/k/v/out strides must be multiples of 8 elements below 2^31");
+  SHRIMP_REQUIRE(strides_ok({a->idx_sb, a->idx_sn, a->rl_sb, a->rl_sn}),
+                 "ray_attn: idx / raylen strides outside [0, 2^31)");
   SHRIMP_REQUIRE(a->idx_sn >= RAY_SLOT_COUNT && a->idx_sb >= (int64_t)a->N * a->idx_sn - a->idx_sn + RAY_SLOT_COUNT,
                  "ray_attn: idx rows must hold 32 slots");
   SHRIMP_REQUIRE(!a->blockers || a->rl_sn >= 12, "ray_attn: raylen rows must hold 12 slots");
@@ -674,6 +684,9 @@ extern "C" int shrimp_conv_ln_raytap(const shrimp_raytap_args* a, void* stream) 
   SHRIMP_REQUIRE(a->x && a->gather_idx && a->mask && a->packed_w && a->bias && a->ln_w && a->ln_b &&
                      a->ray_idx && a->reach && a->alpha && a->out,
                  "conv_ln_raytap: null pointer");
+  SHRIMP_REQUIRE(strides_ok({a->x_sb, a->x_sn, a->o_sb, a->o_sn, a->g_sb, a->g_sn, a->r_sb, a->r_sn,
+                             a->re_sb, a->re_sn}),
+                 "conv_ln_raytap: strides outside [0, 2^31)");
   SHRIMP_REQUIRE(a->corb >= 8 && a->corb % 8 == 0 && a->C % a->corb == 0,
                  "conv_ln_raytap: corb=%d must divide C=%d and be a multiple of 8", a->corb, a->C);
   SHRIMP_REQUIRE(aligned16(a->x) && a->x_sb % 8 == 0 && a->x_sn % 8 == 0 && a->x_sn >= a->C,

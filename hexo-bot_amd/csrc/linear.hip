@@ -211,6 +211,7 @@ extern "C" int shrimp_linear(const shrimp_linear_args* a, void* stream) {
   SHRIMP_REQUIRE(a->x && a->w && a->bias && a->out, "linear: null pointer");
   SHRIMP_REQUIRE(a->out_features % 32 == 0, "linear: out_features %d %% 32 != 0",
                  a->out_features);
+  SHRIMP_REQUIRE(strides_ok({a->x_sr, a->o_sr, a->r_sr}), "linear: row strides outside [0, 2^31)");
   SHRIMP_REQUIRE(a->x_sr >= a->in_features && a->x_sr % 8 == 0, "linear: x row stride");
   const bool ln = a->ln_w != nullptr;
   SHRIMP_REQUIRE(!ln || a->ln_b, "linear: ln_w without ln_b");
@@ -238,7 +239,7 @@ extern "C" int shrimp_linear(const shrimp_linear_args* a, void* stream) {
       return dispatch_k<SHRIMP_LIN_RESID, false>(a, xb, wb, st);
     case SHRIMP_LIN_QKV:
       SHRIMP_REQUIRE(a->out_features % 3 == 0, "linear: qkv out_features %% 3");
-      SHRIMP_REQUIRE(a->B > 0 && a->S > 0 && a->H > 0 && a->B * a->S == a->rows,
+      SHRIMP_REQUIRE(a->B > 0 && a->S > 0 && a->H > 0 && (int64_t)a->B * a->S == a->rows,
                      "linear: qkv needs B*S == rows");
       SHRIMP_REQUIRE((a->out_features / 3) % a->H == 0, "linear: qkv C %% H != 0");
       SHRIMP_REQUIRE(((a->out_features / 3) / a->H) % 4 == 0 &&

@@ -382,6 +382,7 @@ extern "C" int shrimp_attn_mlp(const shrimp_mlp_args* a, void* stream) {
                  "attn_mlp: fused kernel covers C=%d, hidden=%d (got C=%d, hidden=%d)", MC, MH,
                  a->C, a->hidden);
   SHRIMP_REQUIRE(a->x && a->seq && a->mask && a->packed, "attn_mlp: null pointer");
+  SHRIMP_REQUIRE(strides_ok({a->x_sr, a->s_sr}), "attn_mlp: row strides outside [0, 2^31)");
   SHRIMP_REQUIRE(a->x_sr >= MC && a->x_sr % 8 == 0 && a->s_sr >= MC && a->s_sr % 8 == 0,
                  "attn_mlp: row strides must be >= C and multiples of 8");
   const int64_t xe = ((int64_t)(a->rows - 1) * a->x_sr + MC) * 2;

@@ -246,10 +246,10 @@ extern "C" int shrimp_attn_qkv(const shrimp_qkv_args* a, void* stream) {
   const int d = QC / a->H;
   SHRIMP_REQUIRE(d >= 4 && (d & (d - 1)) == 0 && a->dpad >= d && a->dpad % 4 == 0,
                  "attn_qkv: head dim %d must be a power of two >= 4 with dpad %d >= d", d, a->dpad);
-  SHRIMP_REQUIRE(a->x_sr >= QC && a->x_sr % 8 == 0, "attn_qkv: x row stride");
+  SHRIMP_REQUIRE(strides_ok({a->x_sr}) && a->x_sr >= QC && a->x_sr % 8 == 0, "attn_qkv: x row stride");
   const int64_t xe = ((int64_t)(a->rows - 1) * a->x_sr + QC) * 2;
   SHRIMP_REQUIRE(xe < (int64_t)0x7FFF0000, "attn_qkv: activation buffer too large");
-  const int64_t qe = (int64_t)3 * a->B * a->H * a->S * a->dpad * 2;  // q, k and v planes
+  const int64_t qe = mul_sat({3, a->B, a->H, a->S, a->dpad, 2});  // q, k and v planes
   SHRIMP_REQUIRE(qe < (int64_t)0x7FFF0000, "attn_qkv: q/k/v buffer too large");
   SHRIMP_REQUIRE((size_t)max_lds_per_block() >= QW_LDS, "attn_qkv: needs %u bytes of LDS",
                  (unsigned)QW_LDS);
@@ -279,7 +279,7 @@ extern "C" int shrimp_attn_qkv_kvf(const shrimp_qkv_args* a, void* kvf, void* st
   SHRIMP_REQUIRE(a->x && a->qkv && a->packed && kvf, "attn_qkv_kvf: null pointer");
   SHRIMP_REQUIRE(a->B > 0 && a->S > 0 && a->S % 4 == 0 && (int64_t)a->B * a->S == a->rows,
                  "attn_qkv_kvf: rows must be B * S with S %% 4 == 0");
-  SHRIMP_REQUIRE(a->x_sr >= QC && a->x_sr % 8 == 0, "attn_qkv_kvf: x row stride");
+  SHRIMP_REQUIRE(strides_ok({a->x_sr}) && a->x_sr >= QC && a->x_sr % 8 == 0, "attn_qkv_kvf: x row stride");
   const int SP = (a->S + 15) & ~15;
   const int64_t xe = ((int64_t)(a->rows - 1) * a->x_sr + QC) * 2;
   const int64_t qe = (int64_t)a->B * a->H * a->S * 16 * 2;  // the q plane

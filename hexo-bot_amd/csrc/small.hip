@@ -39,6 +39,7 @@ SHRIMP_DEV void prep_idx(const void* __restrict__ nbr, int64_t base, int N, int3
     int32_t v = n;
     if (k > 0) {
       const int64_t j = load_index_t<DT>(nbr, (base + n) * 6 + k - 1);
+      SHRIMP_DCHECK((j >= -1 && j <= N) || (DT == SHRIMP_DT_U16 && j == 0xFFFF), SHRIMP_DBG_NBR);
       v = (j >= 0 && j < N) ? (int32_t)j : N;
     }
     ib[i] = v;
@@ -165,6 +166,7 @@ __global__ __launch_bounds__(256) void prep_csr_kernel(const uint16_t* __restric
       int32_t v = r;
       if (k > 0) {
         const unsigned j = r < n ? nbr[(o + r) * 6 + k - 1] : 0xFFFFu;
+        SHRIMP_DCHECK(j == 0xFFFFu || (int)j < n, SHRIMP_DBG_NBR);
         v = (int)j < N ? (int32_t)j : N;
       }
       ib[i] = v;
@@ -503,6 +505,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const float* value_logits,
     if (threadIdx.x == 0) ml[b] = (u + 1.0f) * 0.5f * ml_cap;
   }
   // The legal prefix never extends past the row (pol_sb == Npad here).
+  SHRIMP_DCHECK(legal[b] >= 0 && legal[b] <= pol_sb, SHRIMP_DBG_LEGAL);
   const int L = max(0, min(legal[b], (int)pol_sb));
   const float* row = policy + (int64_t)b * pol_sb;
   float* dst = priors + out_off[b];
@@ -620,9 +623,10 @@ extern "C" int shrimp_prep_inputs(const void* nbr, int nbr_dt, const void* mask,
                                   int N, int n_tokens, int32_t* idx, uint8_t* mask8,
                                   int32_t* coords32, int32_t* seq_lens, uint8_t* seq_mask,
                                   void* xin, void* stream) {
-  SHRIMP_REQUIRE(B >= 0 && N > 0, "prep_inputs: bad shape (%d, %d)", B, N);
+  SHRIMP_REQUIRE(B >= 0 && N > 0 && N <= kMaxDim, "prep_inputs: bad shape (%d, %d)", B, N);
   if (B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(mask != nullptr, "prep_inputs: mask required");
+  SHRIMP_REQUIRE(n_tokens >= 0 && n_tokens <= 4096, "prep_inputs: n_tokens %d", n_tokens);
   SHRIMP_REQUIRE(!idx || (nbr && (nbr_dt == SHRIMP_DT_I64 || nbr_dt == SHRIMP_DT_I32 ||
                                   nbr_dt == SHRIMP_DT_U16)),
                  "prep_inputs: nbr dtype");
@@ -642,7 +646,8 @@ extern "C" int shrimp_prep_csr(const void* node_feats, int nfeat, const int16_t*
                                const uint16_t* nbr, const int64_t* row_offsets, int row0, int B,
                                int N, int n_tokens, int32_t* idx, uint8_t* mask8, int32_t* coords32,
                                int32_t* seq_lens, uint8_t* seq_mask, void* xin, void* stream) {
-  SHRIMP_REQUIRE(B >= 0 && N > 0 && row0 >= 0 && n_tokens >= 0, "prep_csr: bad sizes");
+  SHRIMP_REQUIRE(B >= 0 && N > 0 && N <= kMaxDim && row0 >= 0 && n_tokens >= 0 && n_tokens <= 4096,
+                 "prep_csr: bad sizes");
   if (B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(row_offsets, "prep_csr: null row offsets");
   SHRIMP_REQUIRE(!idx || nbr, "prep_csr: idx needs nbr");
@@ -658,8 +663,12 @@ extern "C" int shrimp_prep_csr(const void* node_feats, int nfeat, const int16_t*
 
 extern "C" int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void* seq,
                                   int64_t seq_sb, void* tok_lo, int B, void* stream) {
-  SHRIMP_REQUIRE(tokens && seq, "fill_tokens: null pointer");
+  SHRIMP_REQUIRE(B >= 0 && n_tokens >= 0 && n_tokens <= 4096 && C > 0 && C <= 4096,
+                 "fill_tokens: bad sizes (B %d, tokens %d, C %d)", B, n_tokens, C);
   if (B == 0 || n_tokens == 0) return SHRIMP_OK;
+  SHRIMP_REQUIRE(tokens && seq, "fill_tokens: null pointer");
+  SHRIMP_REQUIRE(strides_ok({seq_sb}) && seq_sb >= (int64_t)n_tokens * C,
+                 "fill_tokens: position stride %lld", (long long)seq_sb);
   hipLaunchKernelGGL(fill_tokens_kernel, dim3(B), dim3(256), 0, as_stream(stream), tokens,
                      n_tokens, C, static_cast<uint16_t*>(seq), seq_sb,
                      static_cast<uint16_t*>(tok_lo));
@@ -670,11 +679,13 @@ extern "C" int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void
 // passes with the head inputs in `ws` ((B, 6C) fp32, device memory).
 static int launch_trunk_tail(const shrimp_tail_args* a, float* ws, hipStream_t st,
                              bool f32 = false) {
+  SHRIMP_REQUIRE(a->B > 0 && a->S > 0 && a->S <= kMaxDim, "trunk_tail: bad shape (B %d, S %d)", a->B,
+                 a->S);
   SHRIMP_REQUIRE(a->seq && a->mask && a->ln_w && a->ln_b && a->out_seq,
                  "trunk_tail: null pointer");
   SHRIMP_REQUIRE(a->C > 0 && a->C <= 256 && a->C % 2 == 0, "trunk_tail: C %d outside (0, 256]",
                  a->C);
-  SHRIMP_REQUIRE(a->s_sb % 2 == 0, "trunk_tail: position stride must be even");
+  SHRIMP_REQUIRE(strides_ok({a->s_sb}) && a->s_sb % 2 == 0, "trunk_tail: position stride must be even");
   SHRIMP_REQUIRE(a->n_tokens >= 6 && a->S > a->n_tokens, "trunk_tail: needs >= 6 tokens");
   SHRIMP_REQUIRE(!a->value || (a->vr_w && a->vr_b && a->vh_w && a->vh_b), "trunk_tail: value head");
   SHRIMP_REQUIRE(!a->moves_left || (a->mr_w && a->mr_b && a->mh_w && a->mh_b),
@@ -776,7 +787,7 @@ extern "C" int shrimp_trunk_tail_noalloc(const shrimp_tail_args* a, void* stream
   SHRIMP_REQUIRE(a != nullptr, "trunk_tail_noalloc: null args");
   if (a->B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(a->B > 0 && a->C > 0, "trunk_tail_noalloc: bad shape (B %d, C %d)", a->B, a->C);
-  const int64_t need = (int64_t)a->B * 6 * a->C;
+  const int64_t need = mul_sat({a->B, 6, a->C});
   SHRIMP_REQUIRE(need <= (int64_t)SHRIMP_TAIL_SCRATCH_FLOATS,
                  "trunk_tail_noalloc: B * 6 * C = %lld floats exceeds the fixed scratch of %d "
                  "floats (use shrimp_trunk_tail with a workspace)",
@@ -790,11 +801,13 @@ extern "C" int shrimp_decode(const float* value_logits, const float* ml_logits,
                              const float* policy, int64_t pol_sb, const int32_t* legal,
                              const int64_t* out_off, int B, int bins, float ml_cap, float* value,
                              float* ml, float* priors, float* logits_out, void* stream) {
+  SHRIMP_REQUIRE(B >= 0, "decode: B %d", B);
   if (B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(value_logits && policy && legal && out_off && value && priors,
                  "decode: null pointer");
   SHRIMP_REQUIRE(!ml_logits || ml, "decode: ml output missing");
-  SHRIMP_REQUIRE(bins >= 2, "decode: bins %d", bins);
+  SHRIMP_REQUIRE(bins >= 2 && bins <= 4096, "decode: bins %d", bins);
+  SHRIMP_REQUIRE(pol_sb >= 1 && strides_ok({pol_sb}), "decode: policy row stride %lld", (long long)pol_sb);
   hipLaunchKernelGGL(decode_kernel, dim3(B), dim3(256), 0, as_stream(stream), value_logits,
                      ml_logits, policy, pol_sb, legal, out_off, bins, ml_cap, value, ml, priors,
                      logits_out);
@@ -804,6 +817,12 @@ extern "C" int shrimp_decode(const float* value_logits, const float* ml_logits,
 extern "C" int shrimp_build_pair_u8(const int32_t* coords, const uint8_t* mask, const uint8_t* lut,
                                     int lut_m, int B, int N, int n_tokens, int row_ct, int row_tc,
                                     int row_tt, int pad_row, uint8_t* pair, void* stream) {
+  SHRIMP_REQUIRE(B >= 0 && N > 0 && N <= 65535 && n_tokens >= 0 && n_tokens <= 4096 && lut_m >= 0 &&
+                     lut_m <= 64,
+                 "build_pair_u8: bad sizes (B %d, N %d, tokens %d, lut_m %d)", B, N, n_tokens, lut_m);
+  SHRIMP_REQUIRE(row_ct >= 0 && row_ct < 256 && row_tc >= 0 && row_tc < 256 && row_tt >= 0 &&
+                     row_tt < 256 && pad_row >= 0 && pad_row < 256,
+                 "build_pair_u8: rows must fit a byte");
   if (B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(coords && mask && lut && pair, "build_pair_u8: null pointer");
   dim3 grid(n_tokens + N, B);
@@ -814,9 +833,10 @@ extern "C" int shrimp_build_pair_u8(const int32_t* coords, const uint8_t* mask, 
 
 extern "C" int shrimp_build_ray_index(const int32_t* coords, const uint8_t* mask, int B, int N,
                                       int32_t* idx, void* stream) {
+  SHRIMP_REQUIRE(B >= 0, "build_ray_index: B %d", B);
   if (B == 0) return SHRIMP_OK;
   SHRIMP_REQUIRE(coords && mask && idx, "build_ray_index: null pointer");
-  SHRIMP_REQUIRE(N > 0 && 2 * N <= RAY_TABLE, "build_ray_index: N %d exceeds %d", N, RAY_TABLE / 2);
+  SHRIMP_REQUIRE(N > 0 && N <= RAY_TABLE / 2, "build_ray_index: N %d exceeds %d", N, RAY_TABLE / 2);
   hipLaunchKernelGGL(ray_index_kernel, dim3(B), dim3(256), 0, as_stream(stream), coords, mask, N,
                      idx);
   return check_launch("build_ray_index");

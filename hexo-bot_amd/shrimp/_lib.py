@@ -4,6 +4,11 @@ The library is built in-tree (``hexo-bot_amd/shrimp/_lib/``) by
 ``__graft_entry__.build()`` / ``make -C hexo-bot_amd/csrc``. There is no
 fallback: if the library is missing every GPU entry point raises, naming the
 build step.
+
+``SHRIMP_HIP_LIB`` (a path) loads another build of the same ABI in its place,
+e.g. the checked build ``libshrimp_hip_check.so`` (``make -C hexo-bot_amd/csrc
+check``: the kernels' input checks, and a device synchronisation after every
+launch that reports a failed check as status -3).
 """
 
 from __future__ import annotations
@@ -14,6 +19,7 @@ from pathlib import Path
 
 LIB_DIR = Path(__file__).resolve().parent / "_lib"
 LIB_PATH = LIB_DIR / "libshrimp_hip.so"
+CHECK_LIB_PATH = LIB_DIR / "libshrimp_hip_check.so"
 
 DT_BF16, DT_F32, DT_F16, DT_I64, DT_I32, DT_U16, DT_U8 = range(7)
 LIN_PLAIN, LIN_GELU, LIN_RESID, LIN_QKV = range(4)
@@ -226,7 +232,7 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     global _LIB
     if _LIB is not None and path is None:
         return _LIB
-    p = Path(path) if path is not None else LIB_PATH
+    p = Path(path) if path is not None else Path(os.environ.get("SHRIMP_HIP_LIB") or LIB_PATH)
     if not p.exists():
         raise HipLibraryMissing(
             f"{p} is not built: run `python -c 'import __graft_entry__ as g; g.build()'` "

@@ -30,6 +30,12 @@ extern "C" {
 #define SHRIMP_OK 0
 #define SHRIMP_EINVAL (-1)   /* bad argument / unsupported shape */
 #define SHRIMP_ELAUNCH (-2)  /* HIP launch error */
+/* Checked builds only (libshrimp_hip_check.so, built with SHRIMP_DEBUG=1): a
+ * kernel found an input outside its contract (an index past the rows, a length
+ * past the sequence). Every launch of such a build is followed by a device
+ * synchronisation and a read of the kernels' fault word, so it cannot be
+ * captured into a graph; shrimp_last_error names the failed checks. */
+#define SHRIMP_ECHECK (-3)
 
 /* Element types for the few entry points that accept several. */
 #define SHRIMP_DT_BF16 0

@@ -168,6 +168,26 @@ def test_variant_switches(lib):
         lib.shrimp_conv_variant(prev)
 
 
+def test_host_side_under_address_and_ub_sanitizers():
+    """The host side of every entry point (argument checks, extent arithmetic,
+    launch wrappers, error text) built with -fsanitize=address,undefined and
+    driven by tests/abi_asan.cpp: known rejections with their messages, null
+    argument structs, and 2 x 20000 rounds of boundary-value argument sets
+    (every call OK, EINVAL with a message or ELAUNCH; no sanitizer report)."""
+    import os
+
+    csrc = ROOT / "hexo-bot_amd" / "csrc"
+    exe = ROOT / "_build" / "asan" / "abi_asan"
+    subprocess.run(["make", "-C", str(csrc), "-j8", "asan"], check=True, capture_output=True)
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0", UBSAN_OPTIONS="print_stacktrace=1")
+    for seed in (20261202, 7):
+        r = subprocess.run([str(exe), "20000", str(seed)], capture_output=True, text=True, env=env)
+        if r.returncode == 2 and "GPU(s) visible" in r.stderr:
+            pytest.skip("the sanitizer driver runs only where no GPU is visible")
+        assert r.returncode == 0, r.stdout + r.stderr
+        assert "0 failures" in r.stdout and "runtime error" not in r.stderr, r.stdout + r.stderr
+
+
 def test_missing_library_raises(tmp_path):
     with pytest.raises(_lib.HipLibraryMissing):
         _lib.load(tmp_path / "nope.so")
