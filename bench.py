@@ -829,6 +829,144 @@ def fp32_timing(net, inputs, steps: int = 10) -> dict:
     }
 
 
+def _phase_stats(starts, ends, nbytes, resident):
+    """One phase over all workgroups: start and end stamps (10 ns ticks) and the
+    phase's algorithmic HBM bytes per workgroup. gbs_over_span: every
+    workgroup's bytes over the span (first start to last end), a lower bound on
+    what the chip moved while the phase ran; gbs_resident: `resident`
+    workgroups (as many as the chip holds at once) each moving its bytes in the
+    mean per-workgroup duration, the rate while all resident workgroups are in
+    the phase together."""
+
+    import numpy as np
+
+    d = (ends - starts).astype(np.float64) * 1e-2  # us
+    span = float(ends.max() - starts.min()) * 1e-2
+    total = float(nbytes) * len(starts)
+    r = {
+        "workgroups": int(len(starts)),
+        "mean_us": round(float(d.mean()), 2),
+        "median_us": round(float(np.median(d)), 2),
+        "max_us": round(float(d.max()), 2),
+        "span_us": round(span, 2),
+        "bytes_per_workgroup": int(nbytes),
+    }
+    if nbytes:
+        r["gbs_over_span"] = round(total / (span * 1e-6) / 1e9, 1)
+        r["resident_workgroups"] = int(min(resident, len(starts)))
+        r["gbs_resident"] = round(min(resident, len(starts)) * float(nbytes) / (float(d.mean()) * 1e-6) / 1e9, 1)
+    return r
+
+
+def phase_report(net, inputs, dev) -> dict:
+    """Phase timings and per-phase HBM rates of three kernels, from the phase
+    build (libshrimp_hip_phase.so, SHRIMP_PHASE_CLOCK=1: the kernels store the
+    100 MHz constant clock at their phase boundaries; the release build has no
+    such code):
+
+    - hex_block_pair_kernel, the fourth pair launch of one cfg4 forward (B=512,
+      Npad 256, 2 waves per workgroup): gather (rows and indices staged into
+      LDS: 256 rows x 256 B + 7 indices x 4 B per row), the four convs (no HBM
+      beyond L2-resident weights), the LDS-only epilogue 1 of each block, and
+      the two residual epilogues (256 rows x 256 B read + 256 B stored each);
+    - hex_conv_big_kernel<bias+ReLU>, the cfg1 op (B=1024, Npad 256): gather,
+      conv, epilogue (256 B stored per row);
+    - the staged attention kernel, the fourth attention launch of the same
+      forward (2048 workgroups of one position and two heads): staging (the
+      pair's K/V fragments, 2 x 2 x SP x 32 B, and a quarter of the position's
+      key table, which its four workgroups share), then the query blocks (q
+      fragments in, outputs stored: 2 x 2 x S x 16 x 2 B). The staging rate is
+      given for the first generation of resident workgroups (those starting
+      within 2 us of the first), which stage together.
+    Rates: over each phase's span, and for the workgroups the chip holds at
+    once (two per CU for the conv kernels, three for the attention) each moving
+    its bytes in the mean per-workgroup duration. The stamps (a clock read and
+    a wait for it) slow the kernels by 5-15 %; compare the launch spans with
+    the release kernels' launch times."""
+
+    import numpy as np
+    import torch
+
+    from shrimp import _lib, ops, synthetic
+
+    release = _lib.load()
+    phase = _lib.load(_lib.PHASE_LIB_PATH)
+    _lib._LIB = phase
+    rt = net.hip_runtime()
+    rt.invalidate()
+    res = {}
+    try:
+        conv_st = torch.zeros(1 << 20, dtype=torch.int64, device=dev)
+        attn_st = torch.zeros(1 << 20, dtype=torch.int64, device=dev)
+        _lib.check(phase.shrimp_phase_clock(conv_st.data_ptr(), 0), "phase_clock")
+        _lib.check(phase.shrimp_phase_clock(attn_st.data_ptr(), 1), "phase_clock")
+        for _ in range(5):
+            net.forward_policy_value(*inputs)
+        torch.cuda.synchronize(dev)
+        nb, npad = inputs[2].shape
+        S = npad + 8
+        SP = (S + 15) // 16 * 16
+        c = conv_st[: nb * 32].view(nb, 32).cpu().numpy()
+        row, idx = 256, 7 * 4
+        waves = (npad + 127) // 128
+        w_epi4 = c[:, 16:16 + waves].min(1)
+        w_end = c[:, 24:24 + waves].max(1)
+        bounds = [("gather", 0, 1, npad * (row + idx)), ("conv1", 1, 2, 0), ("epilogue1", 2, 3, 0),
+                  ("conv2", 3, 4, 0), ("epilogue2", 4, 5, 2 * npad * row), ("conv3", 5, 6, 0),
+                  ("epilogue3", 6, 7, 0)]
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        pair = {name: _phase_stats(c[:, s], c[:, e], by, 2 * cus) for name, s, e, by in bounds}
+        pair["conv4"] = _phase_stats(c[:, 7], w_epi4, 0, 2 * cus)
+        pair["epilogue4"] = _phase_stats(w_epi4, w_end, 2 * npad * row, 2 * cus)
+        pair["launch_span_us"] = round(float(w_end.max() - c[:, 0].min()) * 1e-2, 2)
+        res["hex_block_pair_kernel"] = pair
+
+        hb = attn_st[: nb * 4 * 32].view(nb * 4, 32).cpu().numpy()
+        nw = 8 if hb[:, 16 + 4:24].max() > 0 else 4
+        a_end = hb[:, 16:16 + nw].max(1)
+        mbytes = int(release.shrimp_attn_keys_bytes(S))
+        stage_b = 2 * 2 * SP * 32 + mbytes // 4
+        first = hb[:, 0] < hb[:, 0].min() + 200
+        att = {
+            "staging_first_generation": _phase_stats(hb[first, 0], hb[first, 1], stage_b, 3 * cus),
+            "staging_all": _phase_stats(hb[:, 0], hb[:, 1], stage_b, 3 * cus),
+            "query_blocks": _phase_stats(hb[:, 1], a_end, 2 * 2 * S * 16 * 2, 3 * cus),
+            "launch_span_us": round(float(a_end.max() - hb[:, 0].min()) * 1e-2, 2),
+            "waves_per_workgroup": nw,
+        }
+        res["attn_kernel_staged"] = att
+
+        conv_st.zero_()
+        case = synthetic.conv_inputs(1024, channels=128)
+        b1 = case["batch"]
+        bb, n = b1["mask"].shape
+        x = torch.from_numpy(case["x"]).to(dev, torch.bfloat16).contiguous()
+        wp = ops.pack_conv_weight(torch.from_numpy(case["w"]).to(dev))
+        bias = torch.from_numpy(case["bias"]).to(dev)
+        gi, m8 = _device_gather_index(b1, dev)
+        out = torch.empty((bb, n, 128), dtype=torch.bfloat16, device=dev)
+        for _ in range(3):
+            ops.launch_conv(x=x, x_sb=n * 128, x_sn=128, idx=gi, taps=7, idx_stride=7, mask8=m8,
+                            wpack=wp, bias=bias, B=bb, N=n, cin_pad=128, cout=128, relu=True,
+                            out=out, o_sb=n * 128, o_sn=128)
+        torch.cuda.synchronize(dev)
+        c1 = conv_st[: bb * 32].view(bb, 32).cpu().numpy()
+        wv = (n + 127) // 128
+        e0, e1 = c1[:, 16:16 + wv].min(1), c1[:, 24:24 + wv].max(1)
+        res["hex_conv_big_kernel_cfg1"] = {
+            "gather": _phase_stats(c1[:, 0], c1[:, 1], n * (row + idx), 2 * cus),
+            "conv": _phase_stats(c1[:, 1], e0, 0, 2 * cus),
+            "epilogue": _phase_stats(e0, e1, n * row, 2 * cus),
+            "launch_span_us": round(float(e1.max() - c1[:, 0].min()) * 1e-2, 2),
+        }
+        _lib.check(phase.shrimp_phase_clock(None, 0), "phase_clock")
+        _lib.check(phase.shrimp_phase_clock(None, 1), "phase_clock")
+    finally:
+        _lib._LIB = release
+        rt.invalidate()
+    return res
+
+
 def _block_traffic():
     """HBM bytes per launch of the dominant kernel from the committed
     FETCH_SIZE / WRITE_SIZE passes (profiles/block_traffic.json), used only when
@@ -860,6 +998,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--spec-only", action="store_true",
                     help="only time the spec-faithful positions (spec_timing) and print that")
+    ap.add_argument("--phases", action="store_true",
+                    help="only print the phase build's per-phase timings and HBM rates "
+                         "(phase_report) and exit")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run 5 plain device copies of this many MiB (the "
                          "calibration kernel for HBM traffic counters) and exit")
@@ -900,6 +1041,9 @@ def main() -> int:
         batch["mask"].to(dev),
         batch["coords"].to(dev, torch.int32),
     )
+    if args.phases:
+        print(json.dumps({"phases": phase_report(net, inputs, dev)}), flush=True)
+        return 0
     for _ in range(args.warmup):
         net.forward_policy_value(*inputs)
     torch.cuda.synchronize(dev)

@@ -420,6 +420,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? (PROJ == 3 ? 2 : 4) : 1) void at
   constexpr int NT = 64 * NW;  // threads per workgroup
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int KD = DP / 16;
+  if constexpr (STG) SHRIMP_PHASE_WG(0);  // phase builds: staging starts
   int b = blockIdx.y;
   int h0 = blockIdx.x * HG;
   if (PROJ == 2) {
@@ -548,6 +549,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? (PROJ == 3 ? 2 : 4) : 1) void at
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    SHRIMP_PHASE_WG(1);  // phase builds: K, V and the key table are in LDS
     linear_ok = hdr[HDR_SPAN_OK] != 0;
     safe_q = hdr[HDR_SAFE_Q];
     safe_r = hdr[HDR_SAFE_R];
@@ -1152,6 +1154,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? (PROJ == 3 ? 2 : 4) : 1) void at
                            (int64_t)(h0 + h) * a.o_sh + (int64_t)row * a.o_sr;
     *reinterpret_cast<u32x2*>(orow + e) = u32x2{0u, 0u};
   }
+  if constexpr (STG) SHRIMP_PHASE_WAVE(0);  // phase builds: this wave's stores are issued
 }
 
 // Bytes spanned by the output rows (a.o); callers have checked them against
@@ -1445,6 +1448,17 @@ extern "C" int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_pr
                        *a, qk_scale, 0u, w * w, *p, (uint32_t)xe, attn_out_bytes(a));
   return check_launch("attn_fused");
 }
+
+namespace shrimp {
+int attn_phase_set(void* stamps) {
+#if SHRIMP_PHASE_CLOCK
+  return phase_set(stamps);
+#else
+  (void)stamps;
+  return set_error(SHRIMP_EINVAL, "phase_clock: phase stamps need the phase build (SHRIMP_PHASE_CLOCK=1)");
+#endif
+}
+}  // namespace shrimp
 
 extern "C" size_t shrimp_attn_keys_bytes(int S) {
   return S > 0 && S <= kMaxDim ? (size_t)attn_meta_ints((S + 15) & ~15) * 4 : 0;

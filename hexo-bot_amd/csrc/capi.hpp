@@ -76,6 +76,10 @@ int launch_value_heads(const shrimp_tail_args* a, hipStream_t st);
 // Compute units of the current device (queried once per device).
 int cu_count();
 
+// Stamp buffer of the attention kernels in phase builds (attn.hip; the conv
+// kernels' is set in hex_conv.hip); SHRIMP_EINVAL in other builds.
+int attn_phase_set(void* stamps);
+
 // Conv kernel selection: 0 = automatic (small batches: one 64-row tile per
 // workgroup; else big-tile LDS kernel for the 128-channel 7-tap shape, else
 // LDS-staged when the position fits, else global gather), 1 = always the

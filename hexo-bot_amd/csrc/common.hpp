@@ -93,6 +93,41 @@ static int debug_sync(const char* what) {
 #define SHRIMP_DCHECK(cond, bit) ((void)0)
 #endif
 
+// ---- phase stamps of measurement builds (SHRIMP_PHASE_CLOCK=1) -----------------
+//
+// SHRIMP_PHASE_WG(slot) and SHRIMP_PHASE_WAVE(k) compile to nothing in other
+// builds. In a phase build, while shrimp_phase_clock has set a stamp buffer
+// for the source file's kernels, they store the 100 MHz constant clock
+// (s_memrealtime) into 32 u64 slots per workgroup (workgroup blockIdx.x +
+// gridDim.x blockIdx.y; blockIdx.z is not told apart): slots 0-15 from thread 0 at workgroup-wide points
+// (after a barrier), slot 16 + 8 k + wave from lane 0 of each wave (k = 0, 1;
+// waves < 8).
+#ifndef SHRIMP_PHASE_CLOCK
+#define SHRIMP_PHASE_CLOCK 0
+#endif
+#if SHRIMP_PHASE_CLOCK
+namespace shrimp {
+static __device__ unsigned long long* g_phase_buf;
+
+static int phase_set(void* buf) {
+  const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_phase_buf), &buf, sizeof(buf));
+  return e == hipSuccess ? SHRIMP_OK : set_error(SHRIMP_ELAUNCH, "phase_clock: %s", hipGetErrorString(e));
+}
+
+SHRIMP_DEV void phase_stamp(int slot, bool writer) {
+  unsigned long long* p = g_phase_buf;
+  if (p != nullptr && writer)
+    p[(size_t)(blockIdx.x + gridDim.x * blockIdx.y) * 32 + slot] = __builtin_amdgcn_s_memrealtime();
+}
+}  // namespace shrimp
+#define SHRIMP_PHASE_WG(slot) ::shrimp::phase_stamp((slot), threadIdx.x == 0)
+#define SHRIMP_PHASE_WAVE(k) \
+  ::shrimp::phase_stamp(16 + 8 * (k) + (int)(threadIdx.x >> 6), (threadIdx.x & 63) == 0)
+#else
+#define SHRIMP_PHASE_WG(slot) ((void)0)
+#define SHRIMP_PHASE_WAVE(k) ((void)0)
+#endif
+
 // ---- bf16 <-> f32 -----------------------------------------------------------
 
 SHRIMP_DEV float bf16_lo(unsigned w) { return __uint_as_float(w << 16); }

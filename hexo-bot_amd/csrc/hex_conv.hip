@@ -909,6 +909,7 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
                                                               uint32_t x_bytes, uint32_t w_bytes,
                                                               int rp) {
   extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
+  SHRIMP_PHASE_WG(0);  // phase builds: the gather (row staging) starts
   BigParams<1> bp;
   bp.load(0, a.bias, a.ln_w, a.ln_b, (EPI & EPI_HEAD) ? a.head_w : a.gamma);
   BigTile t;
@@ -934,13 +935,16 @@ __global__ __launch_bounds__(256, 1) void hex_conv_big_kernel(const shrimp_conv_
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  SHRIMP_PHASE_WG(1);  // phase builds: the position's rows are in LDS
   big_pass(acc, wf, t, xs, wr);
+  SHRIMP_PHASE_WAVE(0);  // phase builds: this wave's epilogue starts
   if constexpr ((EPI & EPI_HEAD) != 0) {
     conv_epilogue<128, 8, EPI | BA, PS_LDS>(a, acc, t.rb, t.rn, t.rv, t.lg, lp);
   } else {
     conv_epilogue<128, 8, EPI | BA, PS_LDS>(a, acc, t.rb, t.rn, t.rv, t.lg, lp,
                                             GlobalRowStore16<8>(a, t.rb, t.rn, t.lg));
   }
+  SHRIMP_PHASE_WAVE(1);  // phase builds: this wave's stores are issued
 }
 
 // Epilogue store of a ConvBlock that another ConvBlock follows in the same
@@ -1002,6 +1006,10 @@ SHRIMP_DEV void block_convs(BigTile& t, unsigned char* xs, const shrimp_conv_arg
   const float* lp2 = lp1 + BIG_PARAMS;
   f32x4 acc[8][8];
   big_acc_init(acc, c1.bias, t.lg);
+  // phase builds: workgroup stamps ps + 0..3 (ps = 1 for the first block of a
+  // pair, 5 for the second), per-wave stamps at the last block's epilogue
+  const int ps = first ? 1 : 5;
+  (void)ps;
   if (first) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -1010,10 +1018,12 @@ SHRIMP_DEV void block_convs(BigTile& t, unsigned char* xs, const shrimp_conv_arg
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
   }
+  SHRIMP_PHASE_WG(ps);  // rows in LDS: conv1 starts
   // conv2's first weights are loaded after conv1's epilogue, whose bias and
   // ln_w then fit in registers
   big_pass(acc, wf, t, xs, wr1);
   __syncthreads();  // every wave is done reading x from LDS
+  SHRIMP_PHASE_WG(ps + 1);  // epilogue 1 starts
   {
     const uint32_t nr64 = (uint32_t)t.NR * 64;
     const uint32_t lo = (uint32_t)(t.lg & 1) * 8;
@@ -1038,6 +1048,7 @@ SHRIMP_DEV void block_convs(BigTile& t, unsigned char* xs, const shrimp_conv_arg
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   __syncthreads();  // y1 is complete
+  SHRIMP_PHASE_WG(ps + 2);  // conv2 starts
   big_wload(wr2, 0, t.lane, wf);
   // Hide the per-lane addresses from the optimizer: otherwise it keeps conv1's
   // LDS row and weight offsets alive (spilled) for reuse by conv2 instead of
@@ -1053,12 +1064,15 @@ SHRIMP_DEV void block_convs(BigTile& t, unsigned char* xs, const shrimp_conv_arg
     // every wave is done reading y1 before the output rows replace it
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
+    SHRIMP_PHASE_WG(ps + 3);  // epilogue 2 (residual reads, row stores) starts
     conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(a2, acc, t.rb, t.rn, t.rv, t.lg, lp2,
                                                       BlockOutStore(a2, t, xs, o_bytes, r_bytes));
   } else {
+    SHRIMP_PHASE_WAVE(0);  // this wave's epilogue 2 starts
     conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(
         a2, acc, t.rb, t.rn, t.rv, t.lg, lp2,
         BufRowStore16<8>(a2, t.rb, t.rn, t.rv, t.lg, o_bytes, r_bytes));
+    SHRIMP_PHASE_WAVE(1);  // this wave's stores are issued
   }
 }
 
@@ -1163,6 +1177,7 @@ __global__ __launch_bounds__(256, 1) void hex_block_pair_kernel(
     const shrimp_conv_args c1, const shrimp_conv_args c2, const PairSecond p2, uint32_t x_bytes,
     uint32_t w_bytes, uint32_t o_bytes) {
   extern __shared__ __attribute__((aligned(16))) unsigned char xs[];
+  SHRIMP_PHASE_WG(0);  // phase builds: the gather (row staging) starts
   BigParams<4> bp;
   bp.load(0, c1.bias, c1.ln_w, c1.ln_b, nullptr);
   bp.load(1, c2.bias, c2.ln_w, c2.ln_b, c2.gamma);
@@ -1464,6 +1479,17 @@ extern "C" size_t shrimp_conv_wpack_bytes(int taps, int cin_pad, int cout) {
 extern "C" size_t shrimp_linear_wpack_bytes(int in_features, int out_features) {
   const int64_t n = mul_sat({in_features, out_features, 2});
   return in_features > 0 && out_features > 0 && n < (int64_t)0x7FFF0000 ? (size_t)n : 0;
+}
+
+extern "C" int shrimp_phase_clock(void* stamps, int unit) {
+  SHRIMP_REQUIRE(unit == 0 || unit == 1, "phase_clock: unit %d (0 conv kernels, 1 attention)", unit);
+  if (unit == 1) return attn_phase_set(stamps);
+#if SHRIMP_PHASE_CLOCK
+  return phase_set(stamps);
+#else
+  (void)stamps;
+  return set_error(SHRIMP_EINVAL, "phase_clock: phase stamps need the phase build (SHRIMP_PHASE_CLOCK=1)");
+#endif
 }
 
 extern "C" int shrimp_pack_conv_weight(const float* w, void* packed, int taps, int cin,

@@ -20,6 +20,7 @@ from pathlib import Path
 LIB_DIR = Path(__file__).resolve().parent / "_lib"
 LIB_PATH = LIB_DIR / "libshrimp_hip.so"
 CHECK_LIB_PATH = LIB_DIR / "libshrimp_hip_check.so"
+PHASE_LIB_PATH = LIB_DIR / "libshrimp_hip_phase.so"
 
 DT_BF16, DT_F32, DT_F16, DT_I64, DT_I32, DT_U16, DT_U8 = range(7)
 LIN_PLAIN, LIN_GELU, LIN_RESID, LIN_QKV = range(4)
@@ -214,6 +215,7 @@ SIGNATURES: dict = {
                                              ctypes.c_int, _vp, _vp]),
     "shrimp_prep_csr_feats_f32": (ctypes.c_int, [_vp, ctypes.c_int, _vp] + [ctypes.c_int] * 3
                                   + [_vp, _vp]),
+    "shrimp_phase_clock": (ctypes.c_int, [_vp, ctypes.c_int]),
     "shrimp_fill_tokens_f32": (
         ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _i64, ctypes.c_int, _vp]
     ),

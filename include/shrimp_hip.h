@@ -72,6 +72,17 @@ int shrimp_conv_variant(int variant);
 int shrimp_attn_variant(int variant);
 int shrimp_max_lds_per_block(void);
 
+/* Phase stamps (measurement builds only; no counterpart in the reference).
+ * In libshrimp_hip_phase.so (built with SHRIMP_PHASE_CLOCK=1) every later
+ * launch of the unit's instrumented kernels (unit 0: the big-tile conv and the
+ * ConvBlock pair; unit 1: the staged attention) stores the 100 MHz constant
+ * clock at its phase boundaries into `stamps` (device memory, 32 uint64 per
+ * workgroup, workgroup blockIdx.x + gridDim.x * blockIdx.y, blockIdx.z not
+ * told apart; slots 0-15 from
+ * the workgroup after a barrier, 16 + 8 k + wave from each wave); NULL stops.
+ * Other builds return SHRIMP_EINVAL. Process-wide. */
+int shrimp_phase_clock(void* stamps, int unit);
+
 /* ------------------------------------------------------------------------
  * Weight packing (device -> device). MFMA operands are read in fragment
  * order: for K-step ks (32 rows of K) and output block nb (16 outputs), 64

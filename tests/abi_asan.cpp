@@ -319,6 +319,8 @@ void fuzz_scalars(uint64_t seed, int iters) {
     check_rc(shrimp_prep_feats_f32(P(), (int)fz.u(7), i0, i1, i2, (float*)P(), nullptr), "prep_feats_f32");
     check_rc(shrimp_prep_csr_feats_f32(P(), i0, (const int64_t*)P(), i1, i2, i3, (float*)P(), nullptr),
              "prep_csr_feats_f32");
+    // the release host side has no phase stamps: every unit is refused
+    expect_einval(shrimp_phase_clock(P(), (int)fz.u(4) - 1), "phase", "phase_clock");
     // process-wide switches: out-of-range values only query
     const int cv = shrimp_conv_variant(-1), av = shrimp_attn_variant(-1), rv = shrimp_ray_attn_variant(-1);
     expect(shrimp_conv_variant(i0 > 3 || i0 < 0 ? i0 : 99) == cv, "conv_variant query");
