@@ -52,9 +52,12 @@ SHRIMP_DEV unsigned buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
 // (a relaxed device-scope atomic OR; the kernel then goes on exactly as a
 // release build does, so an absent row still reads zeros), and the launch
 // wrapper's check_launch synchronises and reports the word as SHRIMP_ECHECK.
-#define SHRIMP_DBG_CONV_INDEX 0x1u  // conv neighbour index outside [-1, N]
+// The index checks follow the reference kernels' contract: an index at or past
+// the rows is absent (their `idx < Npad` test), -1 is absent here too, and a
+// more negative one would gather before the rows there.
+#define SHRIMP_DBG_CONV_INDEX 0x1u  // conv neighbour index below -1
 #define SHRIMP_DBG_SEQ_LEN 0x2u     // sequence length outside [0, S]
-#define SHRIMP_DBG_RAY_INDEX 0x4u   // ray-tap / gather index outside [-1, N]
+#define SHRIMP_DBG_RAY_INDEX 0x4u   // ray-tap / gather index below -1
 #define SHRIMP_DBG_LEGAL 0x8u       // legal count outside [0, row]
 #define SHRIMP_DBG_NBR 0x10u        // packed neighbour id neither absent nor in the row
 #define SHRIMP_DBG_TABLE_ROW 0x20u  // bias LUT entry past the bias table's rows

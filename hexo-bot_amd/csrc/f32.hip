@@ -220,7 +220,7 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
       for (int mb = 0; mb < MB; ++mb) {
         jn[mb] = rn[mb];
         if (GATHER) jn[mb] = rv[mb] ? g.idx[((int64_t)rb[mb] * g.N + rn[mb]) * g.idx_stride + t] : -1;
-        SHRIMP_DCHECK(!GATHER || (jn[mb] >= -1 && jn[mb] <= g.N), SHRIMP_DBG_CONV_INDEX);
+        SHRIMP_DCHECK(!GATHER || jn[mb] >= -1, SHRIMP_DBG_CONV_INDEX);
       }
     };
     auto tap_off = [&]() {
@@ -324,7 +324,7 @@ SHRIMP_DEV void gemm32_body(const Gemm32& g) {
     for (int mb = 0; mb < MB; ++mb) {
       int j = rn[mb];
       if (GATHER) j = rv[mb] ? g.idx[((int64_t)rb[mb] * g.N + rn[mb]) * g.idx_stride + t] : -1;
-      SHRIMP_DCHECK(!GATHER || (j >= -1 && j <= g.N), SHRIMP_DBG_CONV_INDEX);
+      SHRIMP_DCHECK(!GATHER || j >= -1, SHRIMP_DBG_CONV_INDEX);
       const bool ok = rv[mb] && j >= 0 && j < g.N;
       xoff[mb] = ok ? (uint32_t)(((int64_t)rb[mb] * g.x_sb + (int64_t)j * g.x_sr) * 4) +
                           (uint32_t)(lg * 16)

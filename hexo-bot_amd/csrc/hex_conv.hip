@@ -371,7 +371,7 @@ __global__ __launch_bounds__(256, 2) void hex_conv_kernel(const shrimp_conv_args
     for (int mb = 0; mb < MB; ++mb) {
       int j = -1;
       if (rv[mb]) j = a.idx[(int64_t)(rb[mb] * N + rn[mb]) * a.idx_stride + t];
-      SHRIMP_DCHECK(j >= -1 && j <= N, SHRIMP_DBG_CONV_INDEX);
+      SHRIMP_DCHECK(j >= -1, SHRIMP_DBG_CONV_INDEX);
       const bool ok = (j >= 0) && (j < N);
       const int64_t e = (int64_t)rb[mb] * a.x_sb + (int64_t)j * a.x_sn;
       off[mb] = ok ? (uint32_t)(e * 2) + (uint32_t)(lg * 16) : SHRIMP_OOB_OFFSET;
@@ -534,7 +534,7 @@ __global__ __launch_bounds__(256, 2) void hex_conv_lds_kernel(const shrimp_conv_
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         int v = rv[mb] ? idxb[rn[mb] * a.idx_stride + t] : N;
-        SHRIMP_DCHECK(v >= -1 && v <= N, SHRIMP_DBG_CONV_INDEX);
+        SHRIMP_DCHECK(v >= -1, SHRIMP_DBG_CONV_INDEX);
         j[mb] = (v >= 0 && v < N) ? v : N;
       }
     };
@@ -832,7 +832,7 @@ SHRIMP_DEV void big_setup(BigTile& t, const shrimp_conv_args& a, unsigned char* 
         const int mb = 2 * m2 + h;
         const unsigned raw = tp < 4 ? i0[mb][tp] : (tp < 6 ? i1[mb][tp - 4] : i2[mb]);
         const int j = t.rv[mb] ? (int)raw : t.N;
-        SHRIMP_DCHECK(j >= -1 && j <= t.N, SHRIMP_DBG_CONV_INDEX);
+        SHRIMP_DCHECK(j >= -1, SHRIMP_DBG_CONV_INDEX);
         const int jj = (j >= 0 && j < t.N) ? j : t.N;
         pk |= (uint32_t)(jj * 64 + (((jj >> 2) & 3) << 4)) << (16 * h);
       }
@@ -870,12 +870,13 @@ SHRIMP_DEV void big_pass(f32x4 (&acc)[8][8], u32x4 (&wf)[8], const BigTile& t,
       x[mb] = *reinterpret_cast<const u32x4*>(xs + kbase + (v ^ ls));
     }
   };
-  // The chunk loop is fully unrolled so that no value crosses a branch.
+  // The chunk loop is fully unrolled so that no value crosses a branch. The
+  // last tap of a chunk requests the next chunk's first rows and weights.
+  u32x4 xf[MB];
+  xload(0, 0, xf);
 #pragma unroll
   for (int kc = 0; kc < KC; ++kc) {
     const bool more = kc + 1 < KC;
-    u32x4 xf[MB];
-    xload(0, kc, xf);
 #pragma unroll
     for (int tp = 0; tp < T; ++tp) {
       u32x4 xc[MB], wc[NB];
@@ -887,6 +888,7 @@ SHRIMP_DEV void big_pass(f32x4 (&acc)[8][8], u32x4 (&wf)[8], const BigTile& t,
         xload(tp + 1, kc, xf);
         big_wload(wr, (tp + 1) * KC + kc, t.lane, wf);
       } else if (more) {
+        xload(0, kc + 1, xf);
         big_wload(wr, kc + 1, t.lane, wf);
       }
       // Keep the next step's loads ahead of this step's MFMAs (the scheduler

@@ -205,7 +205,7 @@ __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_a
 #pragma unroll
     for (int t = 0; t < 10; ++t) js[1 + t] = axis ? ir[1 + 10 * p + t] : -1;
 #pragma unroll
-    for (int t = 0; t < 11; ++t) SHRIMP_DCHECK(js[t] >= -1 && js[t] <= N, SHRIMP_DBG_RAY_INDEX);
+    for (int t = 0; t < 11; ++t) SHRIMP_DCHECK(js[t] >= -1, SHRIMP_DBG_RAY_INDEX);
     uint32_t rl4 = 0x05050505u;  // reach (own dir 0, own dir 1, opp dir 0, opp dir 1)
     if (a.blockers && axis) {
       const uint8_t* rl = a.raylen + (int64_t)b * a.rl_sb + (int64_t)r * a.rl_sn + 2 * p;
@@ -369,7 +369,7 @@ __global__ __launch_bounds__(64 * RT_MAX_WAVES) void conv_ln_raytap_kernel(
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int j = rv[mb] ? a.gather_idx[(int64_t)b * a.g_sb + (int64_t)rn[mb] * a.g_sn] : N;
-    SHRIMP_DCHECK(j >= -1 && j <= N, SHRIMP_DBG_RAY_INDEX);
+    SHRIMP_DCHECK(j >= -1, SHRIMP_DBG_RAY_INDEX);
     crow[mb] = (unsigned)j < (unsigned)N ? (uint32_t)j : (uint32_t)N;
   }
   // Side of the lane's two 4-channel halves of chunk kc, (c % corb) >= corb / 2:
@@ -397,7 +397,7 @@ __global__ __launch_bounds__(64 * RT_MAX_WAVES) void conv_ln_raytap_kernel(
 #pragma unroll
       for (int k = 0; k < RAY_STEPS; ++k) {
         pj[k] = ir[k];
-        SHRIMP_DCHECK(pj[k] >= -1 && pj[k] <= N, SHRIMP_DBG_RAY_INDEX);
+        SHRIMP_DCHECK(pj[k] >= -1, SHRIMP_DBG_RAY_INDEX);
       }
       const uint8_t* re = reb + (int64_t)trow * a.re_sn;
       preach = (uint32_t)re[t] | ((uint32_t)re[6 + t] << 8);

@@ -4,9 +4,11 @@ word after every launch.
 
 On valid inputs it gives the release build's forward bit for bit (the checks
 only read). Inputs outside a kernel's contract that the release kernels clamp
-(a neighbour index past the zero row reads zeros, a sequence length past S is
+(a neighbour index below -1 reads the zero row, a sequence length past S is
 cut to S) come back from the checked build as status -3 naming the failed
 check, and the checked build still returns the release build's output for them.
+The release library is loaded by its own path, so these tests also hold when
+SHRIMP_HIP_LIB points the package at the checked build.
 """
 
 import ctypes
@@ -27,10 +29,19 @@ def libs():
 
     if not _lib.CHECK_LIB_PATH.exists():
         pytest.fail(f"{_lib.CHECK_LIB_PATH} not built; run __graft_entry__.build()")
-    release = _lib.load()
-    checked = _lib.load(_lib.CHECK_LIB_PATH)
-    yield _lib, release, checked
-    _lib._LIB = release
+    _lib.load()
+    return _lib, _lib.load(_lib.LIB_PATH), _lib.load(_lib.CHECK_LIB_PATH)
+
+
+@pytest.fixture(autouse=True)
+def _restore_library():
+    """Each test switches the package's library; the next one starts from the
+    default again."""
+    from shrimp import _lib
+
+    default = _lib.load()
+    yield
+    _lib._LIB = default
 
 
 def _use(_lib, lib):
@@ -55,7 +66,6 @@ def test_checked_forward_is_bit_identical(libs):
         out = net.forward_policy_value(*args, request_moves_left=True)
         torch.cuda.synchronize()
         outs.append({k: v.clone() for k, v in out.items()})
-    _use(_lib, release)
     net.hip_runtime().invalidate()
     for key in outs[0]:
         assert torch.equal(outs[0][key], outs[1][key]), key
@@ -70,9 +80,10 @@ def _conv_args(_lib, x, idx, mask8, w, bias, out, B, N):
     )
 
 
-def test_checked_build_reports_an_index_past_the_zero_row(libs):
-    """One gathered neighbour index is N + 5 (past the zero row N): the release
-    conv reads a zero row for it, the checked build returns the same output and
+def test_checked_build_reports_a_negative_neighbour_index(libs):
+    """One gathered neighbour index is -7 (the reference's kernels would gather
+    before the rows; absent is -1 or any index at or past N): the release conv
+    reads the zero row for it, the checked build returns the same output and
     status -3 naming the conv index check."""
     from shrimp import ops
 
@@ -85,7 +96,7 @@ def test_checked_build_reports_an_index_past_the_zero_row(libs):
     clean = idx.clone()
     clean[1, 17, 3] = N  # the zero row
     bad = idx.clone()
-    bad[1, 17, 3] = N + 5
+    bad[1, 17, 3] = -7
     mask8 = torch.ones(B, N, dtype=torch.uint8, device=DEV)
     w = ops.pack_conv_weight((torch.randn(7, 128, 128, generator=g) / 30).to(DEV))
     bias = (torch.randn(128, generator=g) * 0.02).to(DEV)
@@ -134,7 +145,6 @@ def test_checked_build_reports_a_length_past_the_sequence(libs):
         except RuntimeError as e:
             torch.cuda.synchronize()
             res[name] = (str(e), None)
-    _use(_lib, release)
     assert res["release_bad"][0] is None and res["checked_good"][0] is None, res
     assert torch.equal(res["release_bad"][1], res["checked_good"][1])
     err = res["checked_bad"][0]

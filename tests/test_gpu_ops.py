@@ -826,9 +826,10 @@ def _attn_block_ref(x, w, b, lnw, lnb, coords, mask, lens, table, H, eps=1e-5):
 
 
 @pytest.mark.parametrize("S,lens,wide", [
-    # 17 query blocks (the last one split over the waves), ragged bounds, a
-    # bound inside the tokens, tokens only, an empty position
-    (264, [264, 251, 8 + 16 * 16 + 1, 40, 5, 8, 0], False),
+    # 17 query blocks (the last one split over the waves), ragged bounds (one
+    # inside the split block), a bound inside the tokens, tokens only, an
+    # empty position
+    (264, [264, 251, 8 + 16 * 15 + 3, 40, 5, 8, 0], False),
     # coordinates wider than the unclamped table: clamped-LUT path
     (264, [264, 200, 137], True),
     (40, [40, 33, 17], False),
