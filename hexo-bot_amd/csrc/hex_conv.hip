@@ -297,30 +297,35 @@ struct GlobalRowStore16 {
 
 // GlobalRowStore16 through buffer resources (see is_buffered_store): `out`
 // spans o_bytes, the residual rows `rres` r_bytes.
+// A row block's byte offset is computed at its first store (nb = 0), so only
+// the current block's offset is held in a register through the epilogue.
 template <int MB>
 struct BufRowStore16 {
   static constexpr bool kBuffered = true;
   __amdgpu_buffer_rsrc_t orr, rres;
-  uint32_t off[MB];
+  const int (&rb)[MB];
+  const int (&rn)[MB];
+  const bool (&rv)[MB];
+  int64_t o_sb, o_sn;
+  int sub;
+  uint32_t cur = 0;
   u32x2 pend;
-  SHRIMP_DEV BufRowStore16(const shrimp_conv_args& a, const int (&rb)[MB], const int (&rn)[MB],
-                           const bool (&rv)[MB], int lg, uint32_t o_bytes, uint32_t r_bytes)
-      : orr(make_rsrc(a.out, o_bytes)), rres(make_rsrc(a.resid, r_bytes)) {
-    const int sub = (lg & 1) * 16 + (lg >> 1) * 8;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-      off[mb] = rv[mb] ? (uint32_t)(((int64_t)rb[mb] * a.o_sb + (int64_t)rn[mb] * a.o_sn + sub) * 2)
-                       : SHRIMP_OOB_OFFSET;
-  }
+  SHRIMP_DEV BufRowStore16(const shrimp_conv_args& a, const int (&rb_)[MB], const int (&rn_)[MB],
+                           const bool (&rv_)[MB], int lg, uint32_t o_bytes, uint32_t r_bytes)
+      : orr(make_rsrc(a.out, o_bytes)), rres(make_rsrc(a.resid, r_bytes)), rb(rb_), rn(rn_),
+        rv(rv_), o_sb(a.o_sb), o_sn(a.o_sn), sub((lg & 1) * 16 + (lg >> 1) * 8) {}
   SHRIMP_DEV void operator()(int mb, int nb, u32x2 pk) {
     if ((nb & 1) == 0) {
+      if (nb == 0)
+        cur = rv[mb] ? (uint32_t)(((int64_t)rb[mb] * o_sb + (int64_t)rn[mb] * o_sn + sub) * 2)
+                     : SHRIMP_OOB_OFFSET;
       pend = pk;
       return;
     }
     const auto sx = __builtin_amdgcn_permlane16_swap(pend.x, pk.x, false, false);
     const auto sy = __builtin_amdgcn_permlane16_swap(pend.y, pk.y, false, false);
     __builtin_amdgcn_raw_buffer_store_b128(u32x4{sx[0], sy[0], sx[1], sy[1]}, orr,
-                                           off[mb] + (uint32_t)((nb >> 1) * 64), 0, 0);
+                                           cur + (uint32_t)((nb >> 1) * 64), 0, 0);
   }
 };
 
@@ -719,6 +724,20 @@ struct BigTile {
   uint32_t sw2[7][4];  // neighbour row addresses, two 16-bit values per register
 };
 
+// Row ids and validity of a whole-position workgroup's wave (rows 128 wave ..
+// + 127 below N), recomputed from an opaque copy of the lane id before an
+// epilogue, so they are not held in registers across the conv passes.
+SHRIMP_DEV void big_rows(BigTile& t) {
+  int lane = t.lane;
+  asm volatile("" : "+v"(lane));
+  const int row0 = t.wave * 128;
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) {
+    t.rn[mb] = row0 + mb * 16 + (lane & 15);
+    t.rv[mb] = t.rn[mb] < t.N;
+  }
+}
+
 // DMA of chunk kc, rows [16 g, 16 g + 16): lane -> row 16 g + lane / 4, slot lane % 4.
 SHRIMP_DEV void big_dma(unsigned char* xs, const BigTile& t, int kc, int g) {
   const int r = g * 16 + (t.lane >> 2);
@@ -1036,6 +1055,7 @@ SHRIMP_DEV void block_convs(BigTile& t, unsigned char* xs, const shrimp_conv_arg
       swz[mb] = (uint32_t)((t.rn[mb] >> 2) & 3);
     }
     const int lg = t.lg;
+    big_rows(t);
     conv_epilogue<128, 8, EPI_LN | EPI_RELU | EPI_BACC, PS_LDSREG>(
         c1, acc, t.rb, t.rn, t.rv, t.lg, lp1, [&](int mb, int nb, u32x2 pk) {
           const uint32_t piece = (uint32_t)((nb & 1) * 2 + (lg >> 1));
@@ -1067,10 +1087,16 @@ SHRIMP_DEV void block_convs(BigTile& t, unsigned char* xs, const shrimp_conv_arg
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     SHRIMP_PHASE_WG(ps + 3);  // epilogue 2 (residual reads, row stores) starts
+    big_rows(t);
     conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(a2, acc, t.rb, t.rn, t.rv, t.lg, lp2,
                                                       BlockOutStore(a2, t, xs, o_bytes, r_bytes));
   } else {
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) asm volatile("" : "+a"(acc[nb][mb]));
     SHRIMP_PHASE_WAVE(0);  // this wave's epilogue 2 starts
+    big_rows(t);
     conv_epilogue<128, 8, EPI_LN | EPI_RESID, PS_LDS>(
         a2, acc, t.rb, t.rn, t.rv, t.lg, lp2,
         BufRowStore16<8>(a2, t.rb, t.rn, t.rv, t.lg, o_bytes, r_bytes));
