@@ -558,14 +558,17 @@ def spec_timing(net, reps: int = 10) -> dict:
     (ceil64 of its largest support: 576) in one forward; (b) the batch as
     the evaluator serves it: rows sorted by size and cut by plan_groups
     (padding to the 64-quantized anchor, the reference's pair ceiling and
-    waste fraction), one forward per group. positions/s over the 512, HIP
-    events on the launch stream, and the padded-dense TFLOP/s."""
+    waste fraction), one forward per group, the groups spread over two
+    streams as ShrimpEvaluator does (assign_group_streams); (c) the same
+    groups one after another on one stream. positions/s over the 512, HIP
+    events on the launch stream (which waits for the side streams), and the
+    padded-dense TFLOP/s."""
 
     import torch
 
     from shrimp import synthetic
     from shrimp.batching import collate_rows
-    from shrimp.inference import plan_groups
+    from shrimp.inference import assign_group_streams, plan_groups
 
     dev = torch.device("cuda")
     stream = torch.cuda.current_stream(dev)
@@ -585,12 +588,28 @@ def spec_timing(net, reps: int = 10) -> dict:
         sel = [rows[order[i]] for i in range(g0, g1)]
         groups.append((pad, g1 - g0, dev_inputs(collate_rows([(s, f) for _, s, f in sel], pad_to=pad))))
     run_one = lambda: net.forward_policy_value(*one)
-    run_groups = lambda: [net.forward_policy_value(*g[2]) for g in groups]
+    run_seq = lambda: [net.forward_policy_value(*g[2]) for g in groups]
+    side = [torch.cuda.Stream(dev), torch.cuda.Stream(dev)]
+    slots = assign_group_streams([n * (pad + 8) ** 2 for pad, n, _ in groups], len(side))
+
+    def run_groups():
+        for s in side:
+            s.wait_stream(stream)
+        outs = []
+        for (pad, n, inp), k in zip(groups, slots):
+            with torch.cuda.stream(side[k]):
+                outs.append(net.forward_policy_value(*inp))
+        for s in side:
+            stream.wait_stream(s)
+        return outs
+
     res = {"workload": f"B={B} cfg4_spec positions, supports {min(sizes)}-{max(sizes)} cells",
            "generator": "spec seed 20261205"}
+    gflops = sum(n * forward_flops(pad) for pad, n, _ in groups)
     for name, fn, flops in (
         ("one_batch", run_one, B * forward_flops(npad)),
-        ("grouped", run_groups, sum(n * forward_flops(pad) for pad, n, _ in groups)),
+        ("grouped", run_groups, gflops),
+        ("grouped_one_stream", run_seq, gflops),
     ):
         for _ in range(3):
             fn()
@@ -600,7 +619,8 @@ def spec_timing(net, reps: int = 10) -> dict:
                      "tflops_padded": round(flops / (ms * 1e-3) / 1e12, 2),
                      "bf16_mfma_frac_padded": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
     res["one_batch"]["npad"] = npad
-    res["grouped"]["groups"] = [{"npad": pad, "positions": n} for pad, n, _ in groups]
+    res["grouped"]["groups"] = [{"npad": pad, "positions": n, "stream": k}
+                                for (pad, n, _), k in zip(groups, slots)]
     return res
 
 

@@ -58,6 +58,21 @@ def _ceil_quant(n: int) -> int:
     return max(QUANT_NODES, -(-int(n) // QUANT_NODES) * QUANT_NODES)
 
 
+def assign_group_streams(costs, n_streams: int) -> list:
+    """Stream slot of each group when independent group forwards are spread
+    over n_streams streams: groups in order, each to the slot with the least
+    work so far (cost: positions x (Npad + tokens)^2, the attention's share),
+    so the large first groups land on different streams."""
+
+    load = [0.0] * max(1, int(n_streams))
+    out = []
+    for c in costs:
+        k = min(range(len(load)), key=lambda i: load[i])
+        out.append(k)
+        load[k] += float(c)
+    return out
+
+
 def plan_groups(sizes) -> list:
     """(start, end, pad_to) groups over size-descending rows: a group is
     anchored at its first (largest) row, padded to the 64-quantized anchor, and
@@ -144,7 +159,15 @@ class ShrimpEvaluator:
     """graphs: replay each group's forward from a captured HIP graph keyed by
     (batch bucket, Npad, moves-left) instead of launching its kernels one by
     one; None follows SHRIMP_CUDA_GRAPHS=1 as the reference does
-    (inference.py:463-467). Groups above the largest bucket run eagerly."""
+    (inference.py:463-467). Groups above the largest bucket run eagerly.
+
+    group_streams (SHRIMP_GROUP_STREAMS, default 2): the eager forwards of a
+    payload's groups are independent, so when a payload has several they are
+    spread over this many side streams (default priority; assign_group_streams)
+    and run concurrently; small groups at large Npad leave most compute units
+    idle on their own. Results are bit-identical to one stream. 1 keeps every
+    group on the compute stream; captured graphs always replay in order (their
+    buffers share one memory pool)."""
 
     def __init__(self, model: ShrimpNet, device="cuda", graphs: bool | None = None):
         self.graphs = os.environ.get("SHRIMP_CUDA_GRAPHS") == "1" if graphs is None else bool(graphs)
@@ -162,6 +185,8 @@ class ShrimpEvaluator:
         self._copy_stream = None
         self._inflight = 0
         self._perf = GpuBusyTrace() if os.environ.get("SHRIMP_PERF_TRACE") == "1" else None
+        self.group_streams = max(1, int(os.environ.get("SHRIMP_GROUP_STREAMS", 0) or 2))
+        self._group_streams: list = []
 
     def _copies(self) -> torch.cuda.Stream:
         if self._copy_stream is None:
@@ -238,29 +263,49 @@ class ShrimpEvaluator:
             for t in (d_legal, d_off, d_feats, d_qr, d_nbr, d_rows):
                 t.record_stream(compute)
         lib = _lib.load()
-        stream = _lib.stream_handle(dev)
         rt = self.model.hip_runtime()
         perf = self._perf.begin(compute) if self._perf is not None else None
-        for start, end, pad_to in plan_groups(sizes):
+        groups = plan_groups(sizes)
+        side = []
+        if not self.graphs and self.group_streams > 1 and len(groups) > 1:
+            while len(self._group_streams) < self.group_streams:
+                self._group_streams.append(torch.cuda.Stream(dev))
+            side = self._group_streams[: self.group_streams]
+            rt.weights(dev)  # packed on the compute stream, before the side streams fork
+            slots = assign_group_streams(
+                [(e - s) * (p + NUM_TOKENS) ** 2 for s, e, p in groups], len(side))
+            for s in side:
+                s.wait_stream(compute)
+                # this payload's inputs and outputs stay allocated until the
+                # side streams are done with them
+                for t in (d_legal, d_off, d_feats, d_qr, d_nbr, d_rows, values, ml, priors, logits):
+                    if t is not None:
+                        t.record_stream(s)
+        for i, (start, end, pad_to) in enumerate(groups):
             g = end - start
             csr = (d_feats, d_qr, d_nbr, d_rows)
-            out = rt.graph_forward_csr(*csr, start, g, pad_to, request_moves_left=request_ml) \
-                if self.graphs else None
-            if out is None:
-                out = rt.forward_csr(*csr, start, g, pad_to, request_moves_left=request_ml)
-            pol = out["policy"]
-            _lib.check(
-                lib.shrimp_decode(
-                    out["value"].data_ptr(),
-                    out["moves_left"].data_ptr() if request_ml else None,
-                    pol.data_ptr(), pol.stride(0),
-                    d_legal[start:].data_ptr(), d_off[start:].data_ptr(), g, VALUE_BINS,
-                    float(MOVES_LEFT_CAP), values[start:].data_ptr(),
-                    ml[start:].data_ptr() if request_ml else None,
-                    priors.data_ptr(), logits.data_ptr() if request_logits else None, stream,
-                ),
-                "decode",
-            )
+            launch = side[slots[i]] if side else compute
+            with torch.cuda.stream(launch):
+                stream = _lib.stream_handle(dev)
+                out = rt.graph_forward_csr(*csr, start, g, pad_to, request_moves_left=request_ml) \
+                    if self.graphs else None
+                if out is None:
+                    out = rt.forward_csr(*csr, start, g, pad_to, request_moves_left=request_ml)
+                pol = out["policy"]
+                _lib.check(
+                    lib.shrimp_decode(
+                        out["value"].data_ptr(),
+                        out["moves_left"].data_ptr() if request_ml else None,
+                        pol.data_ptr(), pol.stride(0),
+                        d_legal[start:].data_ptr(), d_off[start:].data_ptr(), g, VALUE_BINS,
+                        float(MOVES_LEFT_CAP), values[start:].data_ptr(),
+                        ml[start:].data_ptr() if request_ml else None,
+                        priors.data_ptr(), logits.data_ptr() if request_logits else None, stream,
+                    ),
+                    "decode",
+                )
+        for s in side:
+            compute.wait_stream(s)
         if perf is not None:
             perf[1].record(compute)
         done = torch.cuda.Event()

@@ -548,6 +548,34 @@ def test_evaluator_multi_group_matches_oracle(graphs):
         assert err <= tol, key
 
 
+def test_evaluator_group_streams_are_bit_identical():
+    """A spec-variant payload of 300 positions (groups of 111, 140, 45 and 4
+    rows at Npad 576, 512, 448 and 384; C = 128, H = 8): its groups' forwards
+    spread over two side streams (the default) give the same reply bytes as
+    one stream, twice in a row (the second payload reuses the streams and the
+    memory the first one freed on them)."""
+
+    from shrimp import synthetic
+    from shrimp.inference import ShrimpEvaluator, plan_groups
+
+    payload, _ = synthetic.serve_payload("cfg4_spec", 300, seed=5, request_moves_left=True,
+                                         request_logits=True)
+    offs = np.asarray(payload["node_row_offsets"], dtype=np.int64)
+    groups = plan_groups(offs[1:] - offs[:-1])
+    print(f"group streams: groups {[(e - s, p) for s, e, p in groups]}", flush=True)
+    assert len(groups) >= 3
+    net = _net(128, 8, "CCACCACCACCA", seed=6, mode="heads")
+    ev = ShrimpEvaluator(net, DEV, graphs=False)
+    ev.group_streams = 1
+    want = ev.evaluate_payload(payload)
+    ev.group_streams = 2
+    for rep in range(2):
+        got = ev.evaluate_payload(payload)
+        assert len(ev._group_streams) == 2
+        for key in want:
+            assert got[key] == want[key], (rep, key)
+
+
 def test_graph_replays_match_eager():
     """Captured forwards (graphs=True) against the eager evaluator, payload by
     payload, with eager work and synchronizations between the replays: a

@@ -97,6 +97,17 @@ def test_plan_groups_matches_reference(golden):
     assert plan_groups(g["sizes"]) == [tuple(x) for x in g["groups"].tolist()]
 
 
+def test_group_stream_assignment():
+    """Groups go in order to the stream with the least work so far."""
+
+    from shrimp.inference import assign_group_streams
+
+    assert assign_group_streams([5, 5, 4, 3, 1], 2) == [0, 1, 0, 1, 1]
+    assert assign_group_streams([9, 1, 1, 1], 2) == [0, 1, 1, 1]
+    assert assign_group_streams([3, 2, 1], 1) == [0, 0, 0]
+    assert assign_group_streams([], 2) == []
+
+
 def test_synthetic_l256_generator():
     from shrimp import synthetic
 
