@@ -558,7 +558,7 @@ def spec_timing(net, reps: int = 10) -> dict:
     (ceil64 of its largest support: 576) in one forward; (b) the batch as
     the evaluator serves it: rows sorted by size and cut by plan_groups
     (padding to the 64-quantized anchor, the reference's pair ceiling and
-    waste fraction), one forward per group, the groups spread over two
+    waste fraction), one forward per group, the groups spread over three
     streams as ShrimpEvaluator does (assign_group_streams); (c) the same
     groups one after another on one stream. positions/s over the 512, HIP
     events on the launch stream (which waits for the side streams), and the
@@ -589,7 +589,7 @@ def spec_timing(net, reps: int = 10) -> dict:
         groups.append((pad, g1 - g0, dev_inputs(collate_rows([(s, f) for _, s, f in sel], pad_to=pad))))
     run_one = lambda: net.forward_policy_value(*one)
     run_seq = lambda: [net.forward_policy_value(*g[2]) for g in groups]
-    side = [torch.cuda.Stream(dev), torch.cuda.Stream(dev)]
+    side = [torch.cuda.Stream(dev) for _ in range(3)]
     slots = assign_group_streams([n * (pad + 8) ** 2 for pad, n, _ in groups], len(side))
 
     def run_groups():

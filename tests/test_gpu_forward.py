@@ -551,8 +551,8 @@ def test_evaluator_multi_group_matches_oracle(graphs):
 def test_evaluator_group_streams_are_bit_identical():
     """A spec-variant payload of 300 positions (groups of 111, 140, 45 and 4
     rows at Npad 576, 512, 448 and 384; C = 128, H = 8): its groups' forwards
-    spread over two side streams (the default) give the same reply bytes as
-    one stream, twice in a row (the second payload reuses the streams and the
+    spread over two or three side streams give the same reply bytes as one
+    stream, twice in a row (the second payload reuses the streams and the
     memory the first one freed on them)."""
 
     from shrimp import synthetic
@@ -568,12 +568,12 @@ def test_evaluator_group_streams_are_bit_identical():
     ev = ShrimpEvaluator(net, DEV, graphs=False)
     ev.group_streams = 1
     want = ev.evaluate_payload(payload)
-    ev.group_streams = 2
-    for rep in range(2):
+    for n in (2, 3, 3):
+        ev.group_streams = n
         got = ev.evaluate_payload(payload)
-        assert len(ev._group_streams) == 2
+        assert len(ev._group_streams) >= n
         for key in want:
-            assert got[key] == want[key], (rep, key)
+            assert got[key] == want[key], (n, key)
 
 
 def test_graph_replays_match_eager():
