@@ -878,6 +878,22 @@ def _phase_stats(starts, ends, nbytes, resident):
     return r
 
 
+def _clock_stats(stamps, s, e, mfma_cycles=0):
+    """Core clock of a phase between workgroup stamps s and e, from a run that
+    stored the core clock counter at slot + 8 beside each: cycles over 10 ns
+    ticks summed over the workgroups, and, for a phase with mfma_cycles of MFMA
+    issue per wave, the MFMA pipe's busy share at that clock."""
+
+    import numpy as np
+
+    ticks = (stamps[:, e] - stamps[:, s]).astype(np.float64)
+    cyc = (stamps[:, e + 8] - stamps[:, s + 8]).astype(np.float64)
+    r = {"core_clock_ghz": round(float(cyc.sum() / (ticks.sum() * 10.0)), 3)}
+    if mfma_cycles:
+        r["mfma_busy_at_clock"] = round(float(mfma_cycles / cyc.mean()), 3)
+    return r
+
+
 def phase_report(net, inputs, dev) -> dict:
     """Phase timings and per-phase HBM rates of three kernels, from the phase
     build (libshrimp_hip_phase.so, SHRIMP_PHASE_CLOCK=1: the kernels store the
@@ -902,7 +918,10 @@ def phase_report(net, inputs, dev) -> dict:
     once (two per CU for the conv kernels, three for the attention) each moving
     its bytes in the mean per-workgroup duration. The stamps (a clock read and
     a wait for it) slow the kernels by 5-15 %; compare the launch spans with
-    the release kernels' launch times."""
+    the release kernels' launch times. Timings and rates come from a run with
+    the constant clock only; the core clock columns (core_clock_ghz, and the
+    MFMA pipe's busy share in the conv phases) from a second run that also
+    reads the core clock counter at each workgroup stamp."""
 
     import numpy as np
     import torch
@@ -911,79 +930,97 @@ def phase_report(net, inputs, dev) -> dict:
 
     release = _lib.load()
     phase = _lib.load(_lib.PHASE_LIB_PATH)
-    _lib._LIB = phase
-    rt = net.hip_runtime()
-    rt.invalidate()
-    res = {}
-    try:
-        conv_st = torch.zeros(1 << 20, dtype=torch.int64, device=dev)
-        attn_st = torch.zeros(1 << 20, dtype=torch.int64, device=dev)
-        _lib.check(phase.shrimp_phase_clock(conv_st.data_ptr(), 0), "phase_clock")
-        _lib.check(phase.shrimp_phase_clock(attn_st.data_ptr(), 1), "phase_clock")
+    nb, npad = inputs[2].shape
+    case = synthetic.conv_inputs(1024, channels=128)
+    b1 = case["batch"]
+    bb, n = b1["mask"].shape
+    x = torch.from_numpy(case["x"]).to(dev, torch.bfloat16).contiguous()
+    wp = ops.pack_conv_weight(torch.from_numpy(case["w"]).to(dev))
+    bias = torch.from_numpy(case["bias"]).to(dev)
+    gi, m8 = _device_gather_index(b1, dev)
+    out = torch.empty((bb, n, 128), dtype=torch.bfloat16, device=dev)
+    conv_st = torch.zeros(1 << 20, dtype=torch.int64, device=dev)
+    attn_st = torch.zeros(1 << 20, dtype=torch.int64, device=dev)
+
+    def collect(clock):
+        """Stamps of the fourth pair launch, the fourth attention launch and the
+        cfg1 op; clock adds the core clock counter to the workgroup stamps."""
+        conv_st.zero_()
+        attn_st.zero_()
+        _lib.check(phase.shrimp_phase_clock(conv_st.data_ptr(), 0 | (4 if clock else 0)), "phase_clock")
+        _lib.check(phase.shrimp_phase_clock(attn_st.data_ptr(), 1 | (4 if clock else 0)), "phase_clock")
         for _ in range(5):
             net.forward_policy_value(*inputs)
         torch.cuda.synchronize(dev)
-        nb, npad = inputs[2].shape
-        S = npad + 8
-        SP = (S + 15) // 16 * 16
         c = conv_st[: nb * 32].view(nb, 32).cpu().numpy()
-        row, idx = 256, 7 * 4
-        waves = (npad + 127) // 128
-        w_epi4 = c[:, 16:16 + waves].min(1)
-        w_end = c[:, 24:24 + waves].max(1)
-        bounds = [("gather", 0, 1, npad * (row + idx)), ("conv1", 1, 2, 0), ("epilogue1", 2, 3, 0),
-                  ("conv2", 3, 4, 0), ("epilogue2", 4, 5, 2 * npad * row), ("conv3", 5, 6, 0),
-                  ("epilogue3", 6, 7, 0)]
-        cus = torch.cuda.get_device_properties(dev).multi_processor_count
-        pair = {name: _phase_stats(c[:, s], c[:, e], by, 2 * cus) for name, s, e, by in bounds}
-        pair["conv4"] = _phase_stats(c[:, 7], w_epi4, 0, 2 * cus)
-        pair["epilogue4"] = _phase_stats(w_epi4, w_end, 2 * npad * row, 2 * cus)
-        pair["launch_span_us"] = round(float(w_end.max() - c[:, 0].min()) * 1e-2, 2)
-        res["hex_block_pair_kernel"] = pair
-
         hb = attn_st[: nb * 4 * 32].view(nb * 4, 32).cpu().numpy()
-        nw = 8 if hb[:, 16 + 4:24].max() > 0 else 4
-        a_end = hb[:, 16:16 + nw].max(1)
-        mbytes = int(release.shrimp_attn_keys_bytes(S))
-        stage_b = 2 * 2 * SP * 32 + mbytes // 4
-        first = hb[:, 0] < hb[:, 0].min() + 200
-        att = {
-            "staging_first_generation": _phase_stats(hb[first, 0], hb[first, 1], stage_b, 3 * cus),
-            "staging_all": _phase_stats(hb[:, 0], hb[:, 1], stage_b, 3 * cus),
-            "query_blocks": _phase_stats(hb[:, 1], a_end, 2 * 2 * S * 16 * 2, 3 * cus),
-            "launch_span_us": round(float(a_end.max() - hb[:, 0].min()) * 1e-2, 2),
-            "waves_per_workgroup": nw,
-        }
-        res["attn_kernel_staged"] = att
-
         conv_st.zero_()
-        case = synthetic.conv_inputs(1024, channels=128)
-        b1 = case["batch"]
-        bb, n = b1["mask"].shape
-        x = torch.from_numpy(case["x"]).to(dev, torch.bfloat16).contiguous()
-        wp = ops.pack_conv_weight(torch.from_numpy(case["w"]).to(dev))
-        bias = torch.from_numpy(case["bias"]).to(dev)
-        gi, m8 = _device_gather_index(b1, dev)
-        out = torch.empty((bb, n, 128), dtype=torch.bfloat16, device=dev)
         for _ in range(3):
             ops.launch_conv(x=x, x_sb=n * 128, x_sn=128, idx=gi, taps=7, idx_stride=7, mask8=m8,
                             wpack=wp, bias=bias, B=bb, N=n, cin_pad=128, cout=128, relu=True,
                             out=out, o_sb=n * 128, o_sn=128)
         torch.cuda.synchronize(dev)
         c1 = conv_st[: bb * 32].view(bb, 32).cpu().numpy()
-        wv = (n + 127) // 128
-        e0, e1 = c1[:, 16:16 + wv].min(1), c1[:, 24:24 + wv].max(1)
-        res["hex_conv_big_kernel_cfg1"] = {
-            "gather": _phase_stats(c1[:, 0], c1[:, 1], n * (row + idx), 2 * cus),
-            "conv": _phase_stats(c1[:, 1], e0, 0, 2 * cus),
-            "epilogue": _phase_stats(e0, e1, n * row, 2 * cus),
-            "launch_span_us": round(float(e1.max() - c1[:, 0].min()) * 1e-2, 2),
-        }
         _lib.check(phase.shrimp_phase_clock(None, 0), "phase_clock")
         _lib.check(phase.shrimp_phase_clock(None, 1), "phase_clock")
+        return c, hb, c1
+
+    _lib._LIB = phase
+    rt = net.hip_runtime()
+    rt.invalidate()
+    try:
+        c, hb, c1 = collect(False)
+        kc, khb, kc1 = collect(True)
     finally:
         _lib._LIB = release
         rt.invalidate()
+
+    res = {}
+    S = npad + 8
+    SP = (S + 15) // 16 * 16
+    row, idx = 256, 7 * 4
+    waves = (npad + 127) // 128
+    w_epi4 = c[:, 16:16 + waves].min(1)
+    w_end = c[:, 24:24 + waves].max(1)
+    bounds = [("gather", 0, 1, npad * (row + idx)), ("conv1", 1, 2, 0), ("epilogue1", 2, 3, 0),
+              ("conv2", 3, 4, 0), ("epilogue2", 4, 5, 2 * npad * row), ("conv3", 5, 6, 0),
+              ("epilogue3", 6, 7, 0)]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    conv_mfma = 7 * 4 * 64 * 16  # MFMA issue cycles of one 7-tap conv per wave
+    pair = {}
+    for name, s, e, by in bounds:
+        pair[name] = _phase_stats(c[:, s], c[:, e], by, 2 * cus)
+        pair[name].update(_clock_stats(kc, s, e, conv_mfma if name.startswith("conv") else 0))
+    pair["conv4"] = _phase_stats(c[:, 7], w_epi4, 0, 2 * cus)
+    pair["epilogue4"] = _phase_stats(w_epi4, w_end, 2 * npad * row, 2 * cus)
+    pair["launch_span_us"] = round(float(w_end.max() - c[:, 0].min()) * 1e-2, 2)
+    res["hex_block_pair_kernel"] = pair
+
+    nw = 8 if hb[:, 16 + 4:24].max() > 0 else 4
+    a_end = hb[:, 16:16 + nw].max(1)
+    mbytes = int(release.shrimp_attn_keys_bytes(S))
+    stage_b = 2 * 2 * SP * 32 + mbytes // 4
+    first = hb[:, 0] < hb[:, 0].min() + 200
+    kfirst = khb[:, 0] < khb[:, 0].min() + 200
+    att = {
+        "staging_first_generation": _phase_stats(hb[first, 0], hb[first, 1], stage_b, 3 * cus),
+        "staging_all": _phase_stats(hb[:, 0], hb[:, 1], stage_b, 3 * cus),
+        "query_blocks": _phase_stats(hb[:, 1], a_end, 2 * 2 * S * 16 * 2, 3 * cus),
+        "launch_span_us": round(float(a_end.max() - hb[:, 0].min()) * 1e-2, 2),
+        "waves_per_workgroup": nw,
+    }
+    att["staging_first_generation"].update(_clock_stats(khb[kfirst], 0, 1))
+    att["staging_all"].update(_clock_stats(khb, 0, 1))
+    res["attn_kernel_staged"] = att
+
+    wv = (n + 127) // 128
+    e0, e1 = c1[:, 16:16 + wv].min(1), c1[:, 24:24 + wv].max(1)
+    res["hex_conv_big_kernel_cfg1"] = {
+        "gather": {**_phase_stats(c1[:, 0], c1[:, 1], n * (row + idx), 2 * cus), **_clock_stats(kc1, 0, 1)},
+        "conv": _phase_stats(c1[:, 1], e0, 0, 2 * cus),
+        "epilogue": _phase_stats(e0, e1, n * row, 2 * cus),
+        "launch_span_us": round(float(e1.max() - c1[:, 0].min()) * 1e-2, 2),
+    }
     return res
 
 

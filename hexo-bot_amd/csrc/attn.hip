@@ -1450,11 +1450,12 @@ extern "C" int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_pr
 }
 
 namespace shrimp {
-int attn_phase_set(void* stamps) {
+int attn_phase_set(void* stamps, int cycles) {
 #if SHRIMP_PHASE_CLOCK
-  return phase_set(stamps);
+  return phase_set(stamps, cycles);
 #else
   (void)stamps;
+  (void)cycles;
   return set_error(SHRIMP_EINVAL, "phase_clock: phase stamps need the phase build (SHRIMP_PHASE_CLOCK=1)");
 #endif
 }

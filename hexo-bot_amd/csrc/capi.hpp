@@ -77,8 +77,9 @@ int launch_value_heads(const shrimp_tail_args* a, hipStream_t st);
 int cu_count();
 
 // Stamp buffer of the attention kernels in phase builds (attn.hip; the conv
-// kernels' is set in hex_conv.hip); SHRIMP_EINVAL in other builds.
-int attn_phase_set(void* stamps);
+// kernels' is set in hex_conv.hip), cycles != 0 to record the core clock too;
+// SHRIMP_EINVAL in other builds.
+int attn_phase_set(void* stamps, int cycles);
 
 // Conv kernel selection: 0 = automatic (small batches: one 64-row tile per
 // workgroup; else big-tile LDS kernel for the 128-channel 7-tap shape, else

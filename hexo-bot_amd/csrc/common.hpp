@@ -102,25 +102,33 @@ static int debug_sync(const char* what) {
 // builds. In a phase build, while shrimp_phase_clock has set a stamp buffer
 // for the source file's kernels, they store the 100 MHz constant clock
 // (s_memrealtime) into 32 u64 slots per workgroup (workgroup blockIdx.x +
-// gridDim.x blockIdx.y; blockIdx.z is not told apart): slots 0-15 from thread 0 at workgroup-wide points
-// (after a barrier), slot 16 + 8 k + wave from lane 0 of each wave (k = 0, 1;
-// waves < 8).
+// gridDim.x blockIdx.y; blockIdx.z is not told apart): slots 0-7 from thread 0
+// at workgroup-wide points (after a barrier), and when asked for, each with the
+// core clock counter (s_memtime) at slot + 8, so a phase's cycles over its wall
+// time give the clock the compute unit ran at (a second counter read per stamp,
+// so timings are taken from runs without it); slot 16 + 8 k + wave from lane 0
+// of each wave (k = 0, 1; waves < 8).
 #ifndef SHRIMP_PHASE_CLOCK
 #define SHRIMP_PHASE_CLOCK 0
 #endif
 #if SHRIMP_PHASE_CLOCK
 namespace shrimp {
 static __device__ unsigned long long* g_phase_buf;
+static __device__ int g_phase_cycles;
 
-static int phase_set(void* buf) {
-  const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_phase_buf), &buf, sizeof(buf));
+static int phase_set(void* buf, int cycles) {
+  hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_phase_buf), &buf, sizeof(buf));
+  if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(g_phase_cycles), &cycles, sizeof(cycles));
   return e == hipSuccess ? SHRIMP_OK : set_error(SHRIMP_ELAUNCH, "phase_clock: %s", hipGetErrorString(e));
 }
 
 SHRIMP_DEV void phase_stamp(int slot, bool writer) {
   unsigned long long* p = g_phase_buf;
-  if (p != nullptr && writer)
-    p[(size_t)(blockIdx.x + gridDim.x * blockIdx.y) * 32 + slot] = __builtin_amdgcn_s_memrealtime();
+  if (p != nullptr && writer) {
+    unsigned long long* w = p + (size_t)(blockIdx.x + gridDim.x * blockIdx.y) * 32;
+    w[slot] = __builtin_amdgcn_s_memrealtime();
+    if (slot < 8 && g_phase_cycles) w[slot + 8] = __builtin_amdgcn_s_memtime();
+  }
 }
 }  // namespace shrimp
 #define SHRIMP_PHASE_WG(slot) ::shrimp::phase_stamp((slot), threadIdx.x == 0)

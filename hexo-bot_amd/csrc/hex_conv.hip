@@ -1510,11 +1510,14 @@ extern "C" size_t shrimp_linear_wpack_bytes(int in_features, int out_features) {
 }
 
 extern "C" int shrimp_phase_clock(void* stamps, int unit) {
-  SHRIMP_REQUIRE(unit == 0 || unit == 1, "phase_clock: unit %d (0 conv kernels, 1 attention)", unit);
-  if (unit == 1) return attn_phase_set(stamps);
+  SHRIMP_REQUIRE(unit >= 0 && unit <= 5 && (unit & 3) <= 1,
+                 "phase_clock: unit %d (0 conv kernels, 1 attention, + 4 for the core clock)", unit);
+  const int cycles = unit & 4;
+  if ((unit & 3) == 1) return attn_phase_set(stamps, cycles);
 #if SHRIMP_PHASE_CLOCK
-  return phase_set(stamps);
+  return phase_set(stamps, cycles);
 #else
+  (void)cycles;
   (void)stamps;
   return set_error(SHRIMP_EINVAL, "phase_clock: phase stamps need the phase build (SHRIMP_PHASE_CLOCK=1)");
 #endif

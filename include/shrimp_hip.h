@@ -78,8 +78,10 @@ int shrimp_max_lds_per_block(void);
  * ConvBlock pair; unit 1: the staged attention) stores the 100 MHz constant
  * clock at its phase boundaries into `stamps` (device memory, 32 uint64 per
  * workgroup, workgroup blockIdx.x + gridDim.x * blockIdx.y, blockIdx.z not
- * told apart; slots 0-15 from
- * the workgroup after a barrier, 16 + 8 k + wave from each wave); NULL stops.
+ * told apart; slots 0-7 from the workgroup after a barrier, 16 + 8 k + wave
+ * from each wave); unit + 4 also stores the core clock counter of each
+ * workgroup stamp at slot + 8 (a second counter read per stamp: take timings
+ * from runs without it); NULL stops.
  * Other builds return SHRIMP_EINVAL. Process-wide. */
 int shrimp_phase_clock(void* stamps, int unit);
 
