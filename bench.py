@@ -694,7 +694,9 @@ def ops_timing(reps: int = 30) -> dict:
           bytes (Cin + Cout)*2 + 7*4 per row + weights (141.8 MB);
     cfg2  rel-biased masked attention, H = 8, d = 16, lengths U[64, 256], the
           33x33 per-head offset table, no tokens; work 4*d*H*sum n_b^2, bytes
-          8*d*H*sum n_b (Q, K, V in, O out) + coordinates + table;
+          8*d*H*sum n_b (Q, K, V in, O out) + coordinates + table; timed as
+          the key table plus the staged kernel over the K / V rows, with the
+          row-layout kernel (shrimp_attn) beside it;
     cfg3  31 independent tap weights over the 32-slot ray index (built on
           the device), 128 -> 128; work 2*31*C*C per row (266.3 GFLOP), bytes
           2*C*2 + 32*4 per row + weights."""
@@ -749,10 +751,23 @@ def ops_timing(reps: int = 30) -> dict:
     mask2 = torch.from_numpy(c2["mask"]).to(dev, torch.uint8).contiguous()
     lens = torch.from_numpy(c2["lens"]).to(dev)
     o = torch.empty((B2, H2, S2, d2), dtype=torch.bfloat16, device=dev)
-    run = lambda: ops.launch_attn(q=q, k=k, v=v, qkv_sb=H2 * S2 * d2, qkv_sh=S2 * d2, seq_lens=lens,
-                                  o=o, o_sb=H2 * S2 * d2, o_sh=S2 * d2, o_sr=d2, B=B2, S=S2, H=H2,
-                                  d=d2, dpad=16, coords=coords, mask8=mask2, btab=btab, xtab=xtab,
-                                  lut_m=16, n_tokens=0)
+    rows = lambda: ops.launch_attn(q=q, k=k, v=v, qkv_sb=H2 * S2 * d2, qkv_sh=S2 * d2, seq_lens=lens,
+                                   o=o, o_sb=H2 * S2 * d2, o_sh=S2 * d2, o_sr=d2, B=B2, S=S2, H=H2,
+                                   d=d2, dpad=16, coords=coords, mask8=mask2, btab=btab, xtab=xtab,
+                                   lut_m=16, n_tokens=0)
+    rows()
+    ms_rows = _events_time(rows, reps, stream)
+    # the op as served: the key table (attn_keys) and the staged kernel over the
+    # K / V rows, both launches timed
+    meta = torch.empty(B2 * ops.attn_keys_ints(S2), dtype=torch.int32, device=dev)
+
+    def run():
+        ops.launch_attn_keys(coords=coords, mask8=mask2, seq_lens=lens, B=B2, S=S2, n_tokens=0,
+                             meta=meta)
+        ops.launch_attn_staged(q=q, k=k, v=v, qkv_sb=H2 * S2 * d2, qkv_sh=S2 * d2, meta=meta,
+                               seq_lens=lens, o=o, o_sb=H2 * S2 * d2, o_sh=S2 * d2, o_sr=d2, B=B2,
+                               S=S2, H=H2, d=d2, dpad=16, btab=btab, xtab=xtab, lut_m=16, n_tokens=0)
+
     run()
     ms = _events_time(run, reps, stream)
     nb = c2["lens"].astype("float64")
@@ -766,6 +781,8 @@ def ops_timing(reps: int = 30) -> dict:
         "launch_ms": round(ms, 5), "flops": flops, "algorithmic_bytes": nbytes, "bound": "hbm",
         "achieved_gbs": round(gbs, 1), "peak_gbs": PEAK_HBM_GBS, "frac": round(gbs / PEAK_HBM_GBS, 4),
         "tflops": round(tfl, 2), "mfma_frac": round(tfl / PEAK_BF16_TFLOPS, 4),
+        "path": "attn_keys + attn_staged over the K / V rows",
+        "row_layout_launch_ms": round(ms_rows, 5),
     }
     del q, k, v, o
 

@@ -404,14 +404,16 @@ SHRIMP_DEV u32x2 opaque2(u32x2 v) {
 }
 
 template <int DP, int HG, bool PAIR, int PROJ, int NW>
-__global__ __launch_bounds__(64 * NW, NW == 8 ? (PROJ == 3 ? 2 : 4) : 1) void attn_kernel(const shrimp_attn_args a, float qk_scale,
+__global__ __launch_bounds__(64 * NW, NW == 8 ? (PROJ >= 3 ? 2 : 4) : 1) void attn_kernel(const shrimp_attn_args a, float qk_scale,
                                                    uint32_t qkv_bytes, int npos,
                                                    const shrimp_attn_proj_args p, uint32_t x_bytes,
                                                    uint32_t o_bytes) {
   // PROJ 1, 2: q/k/v projected in the kernel; 3: staged (K and V fragments
-  // and the key table by DMA from shrimp_attn_qkv_kvf / shrimp_attn_keys)
+  // and the key table by DMA from shrimp_attn_qkv_kvf / shrimp_attn_keys);
+  // 4: staged from K and V rows in the q layout (K permuted into fragment
+  // order by the DMA, V rows transposed in LDS), key table in a.coords
   constexpr bool PJ = PROJ == 1 || PROJ == 2;
-  constexpr bool STG = PROJ == 3;
+  constexpr bool STG = PROJ == 3 || PROJ == 4;
   static_assert(!PJ || (DP == 16 && HG == 2 && !PAIR && NW == 4),
                 "projection covers d = 16, two heads, coords, four waves");
   static_assert(!STG || (DP == 16 && HG == 2 && !PAIR), "staged path covers d = 16, two heads, coords");
@@ -507,25 +509,68 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? (PROJ == 3 ? 2 : 4) : 1) void at
     // instructions). Fragment pieces of keys >= S read past the buffer and
     // land as zeros.
     const int H = a.H;
-    const __amdgpu_buffer_rsrc_t kvr = make_rsrc(a.k, (uint32_t)((int64_t)a.B * H * SP * 64));
     const int mbytes = attn_meta_ints(SP) * 4;
-    const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.v, (uint32_t)((int64_t)a.B * mbytes));
-    // fragments f = (tensor, h, kb) in LDS order, two per 1 KiB DMA
-    const int nfr = 2 * HG * NKB;
-    const int half = lane >> 5, sub = lane & 31;
-    for (int i = wave; 2 * i < nfr; i += NW) {
-      const int f = 2 * i + half;
-      const int tensor = f >= HG * NKB ? 1 : 0;
-      const int r = f - tensor * HG * NKB;
-      const int h = r >= NKB ? 1 : 0;
-      const int kb = r - h * NKB;
-      // first key of this lane's 16 bytes: K slots (lg, lr), (lg, lr + 1) with
-      // lr = 2 (sub % 8) hold keys lr, lr + 1; V slots hold keys 4 lg .. + 3
-      const int key = kb * 16 + (tensor ? 4 * (sub >> 3) : 2 * (sub & 7));
-      const uint32_t off =
-          key < S ? (uint32_t)((((int64_t)b * H + h0 + h) * 2 + tensor) * SP * 32 + kb * 512 + sub * 16)
-                  : SHRIMP_OOB_OFFSET;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(kvr, (lds_dst_t*)(smem + i * 1024), 16, off, 0, 0, 0);
+    const __amdgpu_buffer_rsrc_t mr =
+        make_rsrc(PROJ == 4 ? static_cast<const void*>(a.coords) : a.v, (uint32_t)((int64_t)a.B * mbytes));
+    if constexpr (PROJ == 3) {
+      const __amdgpu_buffer_rsrc_t kvr = make_rsrc(a.k, (uint32_t)((int64_t)a.B * H * SP * 64));
+      // fragments f = (tensor, h, kb) in LDS order, two per 1 KiB DMA
+      const int nfr = 2 * HG * NKB;
+      const int half = lane >> 5, sub = lane & 31;
+      for (int i = wave; 2 * i < nfr; i += NW) {
+        const int f = 2 * i + half;
+        const int tensor = f >= HG * NKB ? 1 : 0;
+        const int r = f - tensor * HG * NKB;
+        const int h = r >= NKB ? 1 : 0;
+        const int kb = r - h * NKB;
+        // first key of this lane's 16 bytes: K slots (lg, lr), (lg, lr + 1) with
+        // lr = 2 (sub % 8) hold keys lr, lr + 1; V slots hold keys 4 lg .. + 3
+        const int key = kb * 16 + (tensor ? 4 * (sub >> 3) : 2 * (sub & 7));
+        const uint32_t off =
+            key < S ? (uint32_t)((((int64_t)b * H + h0 + h) * 2 + tensor) * SP * 32 + kb * 512 + sub * 16)
+                    : SHRIMP_OOB_OFFSET;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kvr, (lds_dst_t*)(smem + i * 1024), 16, off, 0, 0, 0);
+      }
+    } else {
+      // Only the nkb = LP / 16 key blocks the chunks read are copied.
+      // K rows into fragment order one dword per lane, two DMAs per fragment:
+      // DMA i fills half i % 2 of fragment (h, kb), i / 2 = h nkb + kb; its
+      // dword w = 64 (i % 2) + lane is half w % 2 of slot w / 2 = 16 lg + lr,
+      // i.e. K[kb*16 + lr][4 lg + 2 (w % 2) .. + 1]. Keys past the bound land
+      // as zeros.
+      const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.k, qkv_bytes);
+      for (int i = wave; i < HG * nkb * 2; i += NW) {
+        const int f = i >> 1;
+        const int h = HG == 2 && f >= nkb ? 1 : 0;
+        const int kb = f - h * nkb;
+        const int w = (i & 1) * 64 + lane;
+        const int slot = w >> 1;
+        const int key = kb * 16 + (slot & 15);
+        const int dim = 4 * (slot >> 4) + 2 * (w & 1);
+        const uint32_t off =
+            key < L ? (uint32_t)((pos_base + (int64_t)(h0 + h) * a.qkv_sh + key * 16 + dim) * 2)
+                    : SHRIMP_OOB_OFFSET;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            kr, (lds_dst_t*)(smem + (h * NKB + kb) * 512 + (i & 1) * 256), 4, off, 0, 0, 0);
+      }
+      // V rows as they are: head h's key rows at Vt + h SP 32 bytes, 32 bytes
+      // each, i.e. the 128 bytes of keys 4 g .. 4 g + 3 exactly where their
+      // four-key V-fragment slots go (transposed below). One DMA is 32 keys;
+      // lanes past the head's LP keys stay idle.
+      const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.v, qkv_bytes);
+      unsigned char* vdst = reinterpret_cast<unsigned char*>(s.Vt);
+      const int vper = (LP + 31) >> 5;  // DMAs per head
+      for (int i = wave; i < HG * vper; i += NW) {
+        const int h = HG == 2 && i >= vper ? 1 : 0;
+        const int piece = (i - h * vper) * 64 + lane;
+        const int key = piece >> 1;
+        const uint32_t off =
+            key < L ? (uint32_t)((pos_base + (int64_t)(h0 + h) * a.qkv_sh + key * 16 + (piece & 1) * 8) * 2)
+                    : SHRIMP_OOB_OFFSET;
+        if (key < LP)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              vr, (lds_dst_t*)(vdst + h * SP * 32 + (i - h * vper) * 1024), 16, off, 0, 0, 0);
+      }
     }
     unsigned char* mdst = reinterpret_cast<unsigned char*>(s.kqr);
     for (int i = wave; i * 1024 < mbytes; i += NW) {
@@ -549,6 +594,47 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? (PROJ == 3 ? 2 : 4) : 1) void at
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if constexpr (PROJ == 4) {
+      // V rows -> V fragments in place: one thread per four keys of one head
+      // reads their rows (128 bytes) and writes their 16 slots (lg, lr), which
+      // hold V[4 g + j][lr] for j = 0..3, into the same 128 bytes. Dead keys
+      // (masked cells, past the bound) get zero V rows, as in the row-layout
+      // path, and zero K slots, so no value a caller left there reaches the
+      // products.
+      for (int g = tid; g < HG * LP / 4; g += NT) {
+        const int h = HG == 2 && g >= LP / 4 ? 1 : 0;
+        const int key0 = (g - h * (LP / 4)) * 4;
+        unsigned char* blk = reinterpret_cast<unsigned char*>(s.Vt) + h * SP * 32 + key0 * 32;
+        const int4 cls = *reinterpret_cast<const int4*>(s.kcls + key0);
+        const int clv[4] = {cls.x, cls.y, cls.z, cls.w};
+        // K slots (lg', key0 % 16 + j) of fragment (h, key0 / 16)
+        unsigned char* kfr = reinterpret_cast<unsigned char*>(s.Ks) + h * SP * 32 + (key0 >> 4) * 512;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (clv[j] == KEY_DEAD)
+#pragma unroll
+            for (int g2 = 0; g2 < 4; ++g2)
+              *reinterpret_cast<u32x2*>(kfr + (g2 * 16 + (key0 & 15) + j) * 8) = u32x2{0u, 0u};
+        u32x4 r[4][2];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            r[j][c] = *reinterpret_cast<const u32x4*>(blk + j * 32 + c * 16);
+            if (clv[j] == KEY_DEAD) r[j][c] = u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+#pragma unroll
+        for (int lr = 0; lr < 16; ++lr) {
+          const int c = lr >> 3, d = (lr & 7) >> 1;
+          const bool hi = (lr & 1) != 0;
+          auto elem = [&](int j) { return hi ? r[j][c][d] >> 16 : r[j][c][d] & 0xFFFFu; };
+          *reinterpret_cast<u32x2*>(blk + lr * 8) =
+              u32x2{elem(0) | (elem(1) << 16), elem(2) | (elem(3) << 16)};
+        }
+      }
+      __syncthreads();
+    }
     SHRIMP_PHASE_WG(1);  // phase builds: K, V and the key table are in LDS
     linear_ok = hdr[HDR_SPAN_OK] != 0;
     safe_q = hdr[HDR_SAFE_Q];
@@ -1498,7 +1584,9 @@ extern "C" int shrimp_attn_staged(const shrimp_attn_args* a, const void* kvf, co
                  "attn_staged: covers dpad = 16, even H, S %% 4 == 0 (got H = %d, S = %d, dpad = %d)",
                  a->H, a->S, a->dpad);
   SHRIMP_REQUIRE(a->pair == nullptr, "attn_staged: coords mode only");
-  SHRIMP_REQUIRE(a->q && kvf && meta && a->o && a->seq_lens && a->btab && a->xtab,
+  // kvf NULL: K and V rows from a->k, a->v in the layout of a->q
+  const bool rows = kvf == nullptr;
+  SHRIMP_REQUIRE(a->q && meta && a->o && a->seq_lens && a->btab && a->xtab && (!rows || (a->k && a->v)),
                  "attn_staged: null pointer");
   SHRIMP_REQUIRE(a->d > 0 && a->d % 4 == 0 && a->d <= 16, "attn_staged: head dim %d", a->d);
   SHRIMP_REQUIRE(a->o_sb % 4 == 0 && a->o_sh % 4 == 0 && a->o_sr % 4 == 0,
@@ -1515,8 +1603,12 @@ extern "C" int shrimp_attn_staged(const shrimp_attn_args* a, const void* kvf, co
   SHRIMP_REQUIRE(kvb < (int64_t)0x7FFF0000 && mb < (int64_t)0x7FFF0000 && qe < (int64_t)0x7FFF0000,
                  "attn_staged: buffers too large");
   shrimp_attn_args s = *a;
-  s.k = kvf;
-  s.v = meta;
+  if (rows) {
+    s.coords = meta;
+  } else {
+    s.k = kvf;
+    s.v = meta;
+  }
   const float qk_scale = SHRIMP_LOG2E / sqrtf((float)a->d);
   const size_t smem = attn_smem_bytes(16, 2, a->S, 0, false);
   // four waves per workgroup (three workgroups per compute unit): measured
@@ -1529,7 +1621,13 @@ extern "C" int shrimp_attn_staged(const shrimp_attn_args* a, const void* kvf, co
   while (z < 4 && groups * z * 2 <= 2 * cu_count() && rounds >= 2 * z) z *= 2;
   dim3 grid(a->H / 2, a->B, z);
   const shrimp_attn_proj_args none{};
-  if (big)
+  if (rows && big)
+    hipLaunchKernelGGL((attn_kernel<16, 2, false, 4, 8>), grid, dim3(64 * 8), smem,
+                       as_stream(stream), s, qk_scale, (uint32_t)qe, 0, none, 0u, attn_out_bytes(a));
+  else if (rows)
+    hipLaunchKernelGGL((attn_kernel<16, 2, false, 4, 4>), grid, dim3(64 * 4), smem,
+                       as_stream(stream), s, qk_scale, (uint32_t)qe, 0, none, 0u, attn_out_bytes(a));
+  else if (big)
     hipLaunchKernelGGL((attn_kernel<16, 2, false, 3, 8>), grid, dim3(64 * 8), smem,
                        as_stream(stream), s, qk_scale, (uint32_t)qe, 0, none, 0u, attn_out_bytes(a));
   else

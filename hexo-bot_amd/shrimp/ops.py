@@ -334,21 +334,24 @@ def attn_staged_supported(H: int, S: int, dpad: int) -> bool:
 
 
 def launch_attn_staged(
-    *, q, qkv_sb, qkv_sh, kvf, meta, seq_lens, o, o_sb, o_sh, o_sr, B, S, H, d, dpad, btab, xtab,
-    lut_m=CELL_LUT_M, n_tokens=NUM_TOKENS, stream=None,
+    *, q, qkv_sb, qkv_sh, meta, seq_lens, o, o_sb, o_sh, o_sr, B, S, H, d, dpad, btab, xtab,
+    kvf=None, k=None, v=None, lut_m=CELL_LUT_M, n_tokens=NUM_TOKENS, stream=None,
 ):
-    """Attention over K / V fragments from launch_attn_qkv_kvf and the key table
-    from launch_attn_keys (coords mode, LINEAR table required)."""
+    """Attention over K / V fragments from launch_attn_qkv_kvf (``kvf``), or over
+    K / V rows ``k``, ``v`` in the layout of ``q`` (``kvf`` None), with the key
+    table from launch_attn_keys (coords mode, LINEAR table required)."""
 
+    if kvf is None and (k is None or v is None):
+        raise ValueError("launch_attn_staged: kvf, or k and v rows, required")
     a = _lib.AttnArgs(
-        q=q.data_ptr(), k=None, v=None, qkv_sb=qkv_sb, qkv_sh=qkv_sh,
+        q=q.data_ptr(), k=_lib.ptr(k), v=_lib.ptr(v), qkv_sb=qkv_sb, qkv_sh=qkv_sh,
         seq_lens=seq_lens.data_ptr(), pair=None, p_sb=0, p_sq=0, table2=None, table_rows=0,
         coords=None, mask=None, btab=btab.data_ptr(), xtab=xtab.data_ptr(), lut_m=lut_m,
         n_tokens=n_tokens, o=o.data_ptr(), o_sb=o_sb, o_sh=o_sh, o_sr=o_sr,
         B=B, S=S, H=H, d=d, dpad=dpad,
     )
     s = _lib.stream_handle() if stream is None else stream
-    _lib.check(_lib.load().shrimp_attn_staged(ctypes_ref(a), kvf.data_ptr(), meta.data_ptr(), s),
+    _lib.check(_lib.load().shrimp_attn_staged(ctypes_ref(a), _lib.ptr(kvf), meta.data_ptr(), s),
                "attn_staged")
 
 

@@ -390,7 +390,12 @@ int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_proj_args* p,
  *     16 (slots of keys >= S are not written and not read).
  *   shrimp_attn_staged: a->q, a->qkv_sb / qkv_sh the q layout above, kvf and
  *     meta from the two calls above, btab and xtab required, pair NULL;
- *     a->k, a->v, a->coords and a->mask are not read. Results equal
+ *     a->k, a->v, a->coords and a->mask are not read. With kvf NULL, K and V
+ *     are the rows a->k, a->v in the layout of a->q ((B, H, S, 16) with the
+ *     same strides, as shrimp_attn reads them; the operator path of config 2):
+ *     the kernel permutes K into fragment order as it copies it and
+ *     transposes V in LDS, with rows of dead keys (masked cells, keys past
+ *     seq_lens) taken as zeros. Results equal
  *     shrimp_attn's up to the bf16 rounding of P (the softmax offsets may
  *     differ). shrimp_attn_staged_supported(H, S, dpad): dpad = 16, even H,
  *     S % 4 == 0, S <= 1024 and the workgroup's LDS within the device's

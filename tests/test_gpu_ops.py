@@ -1025,6 +1025,70 @@ def test_cfg2_attention_full_shape(cfg2_full, attn_variant, linear):
     assert torch.equal(full[rows], run(rows))
 
 
+def test_cfg2_staged_rows_path(cfg2_full):
+    """Config 2's op as bench.py times it: the key table (shrimp_attn_keys) and
+    the staged kernel over the K / V rows (shrimp_attn_staged with kvf NULL).
+    Bit-identical to the row-layout kernel at the same wave count (four waves,
+    two heads per workgroup), against the oracle on sampled positions, and
+    unchanged when the K and V rows of dead keys (masked cells, rows past each
+    length) hold NaN."""
+
+    from bench import cfg2_xtab
+    from shrimp import _lib, ops
+
+    c = cfg2_full
+    q, k, v = (torch.from_numpy(c[n]) for n in ("q", "k", "v"))
+    B, H, S, d = q.shape
+    table = torch.from_numpy(c["table"])
+    btab = (torch.cat([table, torch.zeros(3, H)]) * (1.0 / math.log(2.0))).to(DEV).contiguous()
+    xtab = cfg2_xtab(btab, 16)
+    coords, mask, lens = (torch.from_numpy(c[n]) for n in ("coords", "mask", "lens"))
+    assert ops.attn_staged_supported(H, S, 16)
+    dead = ~mask.bool() | (torch.arange(S)[None, :] >= lens[:, None].long())  # (B, S)
+    assert dead.any() and (~mask.bool()).any()
+    cd = coords.to(DEV, torch.int32).contiguous()
+    md = mask.to(DEV, torch.uint8).contiguous()
+    ld = lens.to(DEV)
+    qd = q.to(DEV, torch.bfloat16).contiguous()
+    meta = torch.empty(B * ops.attn_keys_ints(S), dtype=torch.int32, device=DEV)
+    kw = dict(qkv_sb=H * S * d, qkv_sh=S * d, seq_lens=ld, o_sb=H * S * d, o_sh=S * d, o_sr=d, B=B,
+              S=S, H=H, d=d, dpad=16, btab=btab, xtab=xtab, lut_m=16, n_tokens=0)
+
+    def staged(kt, vt):
+        out = torch.full((B, H, S, d), 5.0, dtype=torch.bfloat16, device=DEV)
+        ops.launch_attn_keys(coords=cd, mask8=md, seq_lens=ld, B=B, S=S, n_tokens=0, meta=meta)
+        ops.launch_attn_staged(q=qd, k=kt.to(DEV, torch.bfloat16).contiguous(),
+                               v=vt.to(DEV, torch.bfloat16).contiguous(), meta=meta, o=out, **kw)
+        return out.cpu()
+
+    print(f"cfg2 staged rows B={B}", flush=True)
+    got = staged(k, v)
+    lib = _lib.load()
+    prev = lib.shrimp_attn_variant(2)
+    try:
+        print("cfg2 row-layout kernel, four waves", flush=True)
+        ref = torch.empty((B, H, S, d), dtype=torch.bfloat16, device=DEV)
+        ops.launch_attn(q=qd, k=k.to(DEV, torch.bfloat16).contiguous(),
+                        v=v.to(DEV, torch.bfloat16).contiguous(), o=ref, coords=cd, mask8=md, **kw)
+        ref = ref.cpu()
+    finally:
+        lib.shrimp_attn_variant(prev)
+    assert torch.isfinite(got.float()).all()
+    for i in range(B):
+        assert (got[i, :, int(lens[i]):] == 0).all(), i
+    assert torch.equal(got, ref)
+    rows = _sample_rows(B)
+    want = ofwd.attn_offset_table(bf(q[rows]), bf(k[rows]), bf(v[rows]), coords[rows], mask[rows],
+                                  table.double(), 16)
+    close(got[rows], want, atol=1e-2, what="cfg2 staged rows")
+    kn, vn = k.clone(), v.clone()
+    dm = dead[:, None, :, None].expand_as(kn)
+    kn[dm] = float("nan")
+    vn[dm] = float("nan")
+    print("cfg2 staged rows, NaN in dead keys' rows", flush=True)
+    assert torch.equal(staged(kn, vn), got)
+
+
 @pytest.fixture(scope="module")
 def cfg3_full():
     from shrimp import synthetic
