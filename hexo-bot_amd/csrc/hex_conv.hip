@@ -1255,57 +1255,67 @@ SHRIMP_DEV void tail_ln_lds(const BigTile& t, unsigned char* xs, const shrimp_ta
     bb[e] = ta.ln_b[c0 + e];
   }
   const float invc = 1.0f / (float)C;
+  // One row: x = raw + lo (the low part of a token row, zeros for a cell row:
+  // final_ln_kernel adds it the same way), normalised into y (zeros where not
+  // live).
+  auto norm_row = [&](const u32x4& raw, const u32x4& lo, bool live, float (&y)[8]) {
+    float x[8];
+    float sm = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = bf16_lo(raw[e]) + bf16_lo(lo[e]);
+      x[2 * e + 1] = bf16_hi(raw[e]) + bf16_hi(lo[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sm += x[e];
+    sm = group_sum_dpp<16>(sm);
+    const float mean = sm * invc;
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = x[e] - mean;
+      q = fmaf(x[e], x[e], q);
+    }
+    q = group_sum_dpp<16>(q);
+    const float rstd = rsqrtf(q * invc + ta.eps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = live ? fmaf(x[e] * rstd, w[e], bb[e]) : 0.f;
+  };
   for (int rs = tid >> 4; rs < 16; rs += ngrp) {
     float pool[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) pool[e] = 0.f;
     int cnt = 0;
-    for (int r = rs; r < S; r += 16) {
-      const bool cell = r >= nt;
+    // Token rows (r < nt) from global memory, then the cell rows from LDS, in
+    // row order. Two loops, so the cell rows are plain LDS reads: one loop
+    // over both kinds compiled to a flat load through a selected pointer,
+    // which gave every LDS row the global-memory latency.
+    int r = rs;
+    for (; r < nt && r < S; r += 16) {
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(seq + (int64_t)r * C + c0);
+      const u32x4 lo = tlo ? *reinterpret_cast<const u32x4*>(tlo + (int64_t)r * C + c0)
+                           : u32x4{0u, 0u, 0u, 0u};
+      float y[8];
+      norm_row(raw, lo, true, y);
+      const int slot = r == 0 ? 0 : r == 1 ? 1 : r == 4 ? 3 : r == 5 ? 4 : -1;
+      if (slot >= 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vin[slot * C + c0 + e] = y[e];
+      }
+    }
+    for (; r < S; r += 16) {
       const int j = r - nt;
       const uint32_t addr = koff + (uint32_t)j * 64 + ((piece ^ (uint32_t)((j >> 2) & 3)) << 4);
-      const u32x4 raw = cell ? *reinterpret_cast<const u32x4*>(xs + addr)
-                             : *reinterpret_cast<const u32x4*>(seq + (int64_t)r * C + c0);
-      // a token row's low part (final_ln_kernel adds it the same way)
-      const u32x4 lo = !cell && tlo ? *reinterpret_cast<const u32x4*>(tlo + (int64_t)r * C + c0)
-                                    : u32x4{0u, 0u, 0u, 0u};
-      float x[8];
-      float sm = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        x[2 * e] = bf16_lo(raw[e]) + bf16_lo(lo[e]);
-        x[2 * e + 1] = bf16_hi(raw[e]) + bf16_hi(lo[e]);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sm += x[e];
-      sm = group_sum_dpp<16>(sm);
-      const float mean = sm * invc;
-      float q = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        x[e] = x[e] - mean;
-        q = fmaf(x[e], x[e], q);
-      }
-      q = group_sum_dpp<16>(q);
-      const float rstd = rsqrtf(q * invc + ta.eps);
-      const bool live = !cell || mk[j] != 0;
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(xs + addr);
+      const bool live = mk[j] != 0;
       float y[8];
+      norm_row(raw, u32x4{0u, 0u, 0u, 0u}, live, y);
+      *reinterpret_cast<u32x4*>(xs + addr) =
+          u32x4{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]),
+                pack_bf16x2(y[6], y[7])};
+      if (live && sub == 0) ++cnt;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) y[e] = live ? fmaf(x[e] * rstd, w[e], bb[e]) : 0.f;
-      if (cell) {
-        *reinterpret_cast<u32x4*>(xs + addr) =
-            u32x4{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]),
-                  pack_bf16x2(y[6], y[7])};
-        if (live && sub == 0) ++cnt;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pool[e] += y[e];
-      } else {
-        const int slot = r == 0 ? 0 : r == 1 ? 1 : r == 4 ? 3 : r == 5 ? 4 : -1;
-        if (slot >= 0) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) vin[slot * C + c0 + e] = y[e];
-        }
-      }
+      for (int e = 0; e < 8; ++e) pool[e] += y[e];
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) red[rs * C + c0 + e] = pool[e];
