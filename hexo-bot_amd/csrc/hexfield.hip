@@ -101,9 +101,11 @@ SHRIMP_DEV void fma_row16(float (&acc)[16], float p, const Row16& v) {
 
 // Workgroup: (position b, head pair p), 256 threads, D / 16 lanes per query row
 // (each owning 16 of its D channels). LDS: the pair's 22 slot biases (fp32),
-// then (STAGE) [K | V][head of pair][row][D] fp16. Head rows are addressed
-// from per-head base pointers with 32-bit byte offsets (the host checks that
-// a position's rows of one head span less than 2 GiB).
+// then (STAGE) [K | V][head of pair][row][D] fp16. Rows are buffer accesses
+// from the head pair's first head with 32-bit byte offsets (head h adds
+// h times the head stride; the host checks that the strides are not negative
+// and that a head pair's rows of a position span less than 2 GiB), so no
+// access goes through a generic pointer chosen by the head index.
 template <int D, bool STAGE>
 __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_attn_args a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
@@ -155,6 +157,12 @@ __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_a
     const int hh = 2 * p + min(hl, nh - 1);
     sbias[threadIdx.x] = (float)__builtin_bit_cast(_Float16, a.slot_bias[slot * a.H + hh]);
   }
+  const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qb[0], 0x7FFFFFFFu);
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kb[0], 0x7FFFFFFFu);
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vb[0], 0x7FFFFFFFu);
+  const __amdgpu_buffer_rsrc_t ors = make_rsrc(ob[0], 0x7FFFFFFFu);
+  const uint32_t qhs = (uint32_t)(qb[1] - qb[0]), khs = (uint32_t)(kb[1] - kb[0]);
+  const uint32_t vhs = (uint32_t)(vb[1] - vb[0]), ohs = (uint32_t)(ob[1] - ob[0]);
   unsigned char* rows = lds + RA_BIAS_LDS;
   if constexpr (STAGE) {
     constexpr int CPR = D / 8;  // 16-byte chunks per row and head
@@ -162,13 +170,13 @@ __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_a
 #pragma unroll
     for (int tsr = 0; tsr < 2; ++tsr)
       for (int hl = 0; hl < nh; ++hl) {
-        const unsigned char* src = tsr ? vb[hl] : kb[hl];
+        const uint32_t base = (uint32_t)hl * (tsr ? vhs : khs);
         const uint32_t sn = tsr ? vsn : ksn;
         unsigned char* dst = rows + (size_t)(tsr * 2 + hl) * N * D * 2;
         for (int c = (int)threadIdx.x; c < per; c += RA_THREADS) {
           const int j = c / CPR, ch = c % CPR;
           *reinterpret_cast<u32x4*>(dst + (uint32_t)(j * D + ch * 8) * 2) =
-              *reinterpret_cast<const u32x4*>(src + (uint32_t)j * sn + ch * 16);
+              buf_load16(tsr ? vrs : krs, base + (uint32_t)j * sn + ch * 16);
         }
       }
   }
@@ -177,9 +185,6 @@ __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_a
   // Key row fetch: the lane's 16 channels of row j of head (2p + hl). Rows
   // not staged in LDS are buffer loads from the head pair's base (a distinct
   // load kind, so the two paths never merge into one generic-pointer load).
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kb[0], 0x7FFFFFFFu);
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vb[0], 0x7FFFFFFFu);
-  const uint32_t khs = (uint32_t)(kb[1] - kb[0]), vhs = (uint32_t)(vb[1] - vb[0]);
   auto fetch = [&](int tsr, int hl, int j) -> Row16 {
     if (STAGE && j < nst)
       return load_row16(rows + (((size_t)(tsr * 2 + hl) * N + j) * D + part * 16) * 2);
@@ -193,9 +198,9 @@ __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_a
   for (int r = (int)threadIdx.x / LPR; r < N; r += RPP) {
     if (r >= live_rows) {
       for (int hl = 0; hl < nh; ++hl) {
-        u32x4* dst = reinterpret_cast<u32x4*>(ob[hl] + (uint32_t)r * osn + part * 32);
-        dst[0] = u32x4{0u, 0u, 0u, 0u};
-        dst[1] = u32x4{0u, 0u, 0u, 0u};
+        const uint32_t off = (uint32_t)hl * ohs + (uint32_t)r * osn + part * 32;
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, ors, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, ors, off + 16, 0, 0);
       }
       continue;
     }
@@ -223,7 +228,12 @@ __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_a
         live |= ((unsigned)js[1 + t] < (unsigned)N && (t % 5 + 1) <= (t < 5 ? reach0 : reach1) ? 1u : 0u)
                 << (1 + t);
 
-      const Row16 q = load_row16(qb[hl] + (uint32_t)r * qsn + part * 32);
+      Row16 q;
+      {
+        const uint32_t off = (uint32_t)hl * qhs + (uint32_t)r * qsn + part * 32;
+        q.p0 = buf_load16(qrs, off);
+        q.p1 = buf_load16(qrs, off + 16);
+      }
       float s[11];
       float m = -INFINITY;
 #pragma unroll
@@ -256,9 +266,9 @@ __global__ __launch_bounds__(RA_THREADS) void ray_attn_kernel(const shrimp_ray_a
         o0[w] = pack_f16x2(acc[2 * w] * inv, acc[2 * w + 1] * inv);
         o1[w] = pack_f16x2(acc[8 + 2 * w] * inv, acc[8 + 2 * w + 1] * inv);
       }
-      u32x4* dst = reinterpret_cast<u32x4*>(ob[hl] + (uint32_t)r * osn + part * 32);
-      dst[0] = o0;
-      dst[1] = o1;
+      const uint32_t off = (uint32_t)hl * ohs + (uint32_t)r * osn + part * 32;
+      __builtin_amdgcn_raw_buffer_store_b128(o0, ors, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(o1, ors, off + 16, 0, 0);
     }
   }
 }
@@ -635,8 +645,8 @@ extern "C" int shrimp_ray_attn(const shrimp_ray_attn_args* a, void* stream) {
   const int64_t st[12] = {a->q_sb, a->q_sh, a->q_sn, a->k_sb, a->k_sh, a->k_sn,
                           a->v_sb, a->v_sh, a->v_sn, a->o_sb, a->o_sh, a->o_sn};
   for (int i = 0; i < 12; ++i)
-    SHRIMP_REQUIRE(st[i] % 8 == 0 && st[i] > -(1LL << 31) && st[i] < (1LL << 31),
-                   "ray_attn: q/k/v/out strides must be multiples of 8 elements below 2^31");
+    SHRIMP_REQUIRE(st[i] % 8 == 0 && st[i] >= 0 && st[i] < (1LL << 31),
+                   "ray_attn: q/k/v/out strides must be multiples of 8 elements in [0, 2^31)");
   SHRIMP_REQUIRE(strides_ok({a->idx_sb, a->idx_sn, a->rl_sb, a->rl_sn}),
                  "ray_attn: idx / raylen strides outside [0, 2^31)");
   SHRIMP_REQUIRE(a->idx_sn >= RAY_SLOT_COUNT && a->idx_sb >= (int64_t)a->N * a->idx_sn - a->idx_sn + RAY_SLOT_COUNT,
@@ -645,8 +655,7 @@ extern "C" int shrimp_ray_attn(const shrimp_ray_attn_args* a, void* stream) {
   const int64_t rsn[4] = {a->q_sn, a->k_sn, a->v_sn, a->o_sn};
   const int64_t rsh[4] = {a->q_sh, a->k_sh, a->v_sh, a->o_sh};
   for (int i = 0; i < 4; ++i)
-    SHRIMP_REQUIRE(rsn[i] >= a->D && ((int64_t)a->N * rsn[i] + (rsh[i] < 0 ? -rsh[i] : rsh[i])) * 2 <
-                                         (1LL << 31),
+    SHRIMP_REQUIRE(rsn[i] >= a->D && ((int64_t)a->N * rsn[i] + rsh[i]) * 2 < (1LL << 31),
                    "ray_attn: a head pair's rows of a position must span less than 2 GiB");
   SHRIMP_REQUIRE((int64_t)a->B * ((a->H + 1) / 2) < (1LL << 31), "ray_attn: grid too large");
   const bool stage = g_ray_variant == 0 && 8u * (uint64_t)a->N * a->D <= RA_STAGE_MAX_LDS;

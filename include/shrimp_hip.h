@@ -575,9 +575,10 @@ int shrimp_build_ray_index(const int32_t* coords, const uint8_t* mask, int B, in
  * hexfield_eq::ray_attn (hexfield_eq/_triton_ray.py:681-715; kernel :378-501):
  * gathered ray attention over the 32-slot index above.
  *   q, k, v, out: (B, H, N, D) fp16, D in {16, 32, 64, 128}, element strides
- *     *_sb / *_sh / *_sn (multiples of 8, bases 16-byte aligned; the head
- *     dimension is contiguous). The (B, N, H, D).transpose(1, 2) views the
- *     reference passes satisfy this.
+ *     *_sb / *_sh / *_sn (multiples of 8 in [0, 2^31), bases 16-byte aligned;
+ *     the head dimension is contiguous; a head pair's rows of a position span
+ *     less than 2 GiB). The (B, N, H, D).transpose(1, 2) views the reference
+ *     passes satisfy this.
  *   idx (B, N, 32) int32, strides idx_sb / idx_sn, slot stride 1; an entry
  *     outside [0, N) is an absent key.
  *   slot_bias (32, H) fp16 (the reference rounds its fp32 slot bias to fp16).
