@@ -121,6 +121,9 @@ def test_bad_arguments_fail_with_message(lib):
     ra.q_sn = 12
     assert lib.shrimp_ray_attn(ctypes.byref(ra), None) == -1
     assert b"multiples of 8" in lib.shrimp_last_error()
+    ra.q_sn = -96  # the kernel's 32-bit row offsets take no negative strides
+    assert lib.shrimp_ray_attn(ctypes.byref(ra), None) == -1
+    assert b"[0, 2^31)" in lib.shrimp_last_error()
     ra.q_sn = 96
     ra.blockers = 1
     assert lib.shrimp_ray_attn(ctypes.byref(ra), None) == -1
