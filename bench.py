@@ -820,18 +820,19 @@ def ops_timing(reps: int = 30) -> dict:
 
 def cfg2_xtab(btab, m: int):
     """The attention kernel's unclamped offset table for a (2m+1)^2 per-offset
-    table: xtab[(dq + XD)(2 XD + 1) + dr + XD, h] = fp16(btab[clamped (dq, dr), h])
-    over |dq|, |dr| <= XD (what shrimp_attn_bias_table writes for the model's
-    LUT), so compact cell sets take the kernel's linear-offset path."""
+    table: fp16(btab[clamped (dq, dr), h]) at offset x = (dq + XD)(2 XD + 1) +
+    dr + XD over |dq|, |dr| <= XD, in the head pair major layout (what
+    shrimp_attn_bias_table writes for the model's LUT), so compact cell sets
+    take the kernel's linear-offset path."""
 
     import torch
 
-    from shrimp.ops import ATTN_XD
+    from shrimp.ops import ATTN_XD, xtab_pairs
 
     r = torch.arange(-ATTN_XD, ATTN_XD + 1, device=btab.device)
     dq, dr = torch.meshgrid(r, r, indexing="ij")
     pos = (dq.clamp(-m, m) + m) * (2 * m + 1) + dr.clamp(-m, m) + m
-    return btab[pos.reshape(-1)].half().contiguous()
+    return xtab_pairs(btab[pos.reshape(-1)].half())
 
 
 def fp32_timing(net, inputs, steps: int = 10) -> dict:

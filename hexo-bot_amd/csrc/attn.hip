@@ -41,9 +41,13 @@ namespace shrimp {
 enum : int { KEY_CELL = 0, KEY_TOKEN = 1, KEY_DEAD = 2 };
 enum : int { PATH_GENERAL = 0, PATH_CLAMP = 1, PATH_LINEAR = 2 };
 
-// Unclamped offset table: offsets with |dq|, |dr| <= XD.
+// Unclamped offset table: offsets with |dq|, |dr| <= XD. In memory it is head
+// pair major, ((H + 1) / 2, XP, 2) fp16: each head pair's XW*XW dwords padded
+// to XP, so a workgroup copies its pair's table in whole 1 KiB DMAs.
 constexpr int XD = SHRIMP_ATTN_XD;
 constexpr int XW = 2 * XD + 1;
+constexpr int XP = SHRIMP_ATTN_XP;
+static_assert(XP >= XW * XW && XP % 256 == 0, "XP: XW*XW dwords in whole 1 KiB pieces");
 
 SHRIMP_DEV int clampi(int x, int m) { return min(max(x, -m), m); }
 
@@ -453,7 +457,9 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? (PROJ >= 3 ? 2 : 4) : 1) void at
   const int* hdr = s.blk_dead + NKB;
   s.tokb = reinterpret_cast<float*>(reinterpret_cast<int*>(s.kqr) + attn_meta_ints(SP));
   int* span_red = reinterpret_cast<int*>(s.tokb + 3 * HG);  // [NW][4]
-  float* tail = reinterpret_cast<float*>(span_red + 4 * NW);
+  // the tables (16-byte aligned: the offset table arrives in 16-byte DMA pieces)
+  float* tail = reinterpret_cast<float*>((reinterpret_cast<uintptr_t>(span_red + 4 * NW) + 15) &
+                                         ~static_cast<uintptr_t>(15));
   s.tab = tail;
   s.xtab = reinterpret_cast<_Float16*>(tail);
 
@@ -579,15 +585,13 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? (PROJ >= 3 ? 2 : 4) : 1) void at
         __builtin_amdgcn_raw_ptr_buffer_load_lds(mr, (lds_dst_t*)(mdst + i * 1024), 16,
                                                  (uint32_t)((int64_t)b * mbytes + o), 0, 0, 0);
     }
-    // (XW*XW, H) fp16 table: the head pair's dword of each offset
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xtab, (uint32_t)(XW * XW * H * 2));
+    // the head pair's XP dwords of the pair-major table, 1 KiB per DMA
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xtab, (uint32_t)((H + 1) / 2 * XP * 4));
     unsigned char* xdst = reinterpret_cast<unsigned char*>(s.xtab);
-    for (int i = wave; i * 64 < XW * XW; i += NW) {
-      const int x = i * 64 + lane;
-      if (x < XW * XW)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_dst_t*)(xdst + i * 256), 4,
-                                                 (uint32_t)((x * H + h0) * 2), 0, 0, 0);
-    }
+    for (int i = wave; i * 256 < XP; i += NW)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xr, (lds_dst_t*)(xdst + i * 1024), 16,
+          (uint32_t)((h0 / 2) * XP * 4 + i * 1024 + lane * 16), 0, 0, 0);
     if (tid < 3 * HG) {
       const int W2 = (2 * a.lut_m + 1) * (2 * a.lut_m + 1);
       s.tokb[tid] = a.btab[(W2 + tid / HG) * H + h0 + tid % HG];
@@ -659,16 +663,17 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? (PROJ >= 3 ? 2 : 4) : 1) void at
       }
     }
   }
-  // the (XW*XW, HG) offset table of this head pair: XW*XW dwords, one pass
+  // the (XW*XW, HG) offset table of this head pair: XW*XW dwords of its pair
+  // in the pair-major table, one pass
   constexpr int UX = (XW * XW + NT - 1) / NT;
   unsigned xv[UX];
   const bool xstage = !PAIR && HG == 2 && a.xtab != nullptr;
   if (xstage) {
-    const unsigned short* xg = static_cast<const unsigned short*>(a.xtab);
+    const unsigned* xg = static_cast<const unsigned*>(a.xtab) + (int64_t)(h0 / 2) * XP;
 #pragma unroll
     for (int u = 0; u < UX; ++u) {
       const int x = tid + u * NT;
-      xv[u] = x < XW * XW ? *reinterpret_cast<const unsigned*>(xg + (int64_t)x * a.H + h0) : 0u;
+      xv[u] = x < XW * XW ? xg[x] : 0u;
     }
   }
 
@@ -808,9 +813,11 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? (PROJ >= 3 ? 2 : 4) : 1) void at
         if (x < XW * XW) reinterpret_cast<unsigned*>(s.xtab)[x] = xv[u];
       }
     } else {
+      // one head: its half of each dword of its pair
+      const unsigned short* xh = xg + (int64_t)(h0 / 2) * XP * 2 + (h0 & 1);
       for (int i = tid; i < XW * XW * HG; i += NT) {
         const int x = i / HG;
-        reinterpret_cast<unsigned short*>(s.xtab)[i] = xg[(int64_t)x * a.H + h0 + (i - x * HG)];
+        reinterpret_cast<unsigned short*>(s.xtab)[i] = xh[(int64_t)x * 2 + (i - x * HG)];
       }
     }
   }
@@ -1258,7 +1265,8 @@ static uint32_t attn_out_bytes(const shrimp_attn_args* a) { return (uint32_t)att
 static size_t attn_smem_bytes(int DP, int HG, int S, int npos, bool pair) {
   const size_t SP = (size_t)((S + 15) & ~15);
   size_t bytes = 2 * HG * SP * DP * 2 + (size_t)attn_meta_ints((int)SP) * 4 + 3 * HG * 4 + 4 * 8 * 4;
-  bytes += pair ? (size_t)npos * HG * 4 : (size_t)XW * XW * HG * 2;
+  bytes += 16;  // alignment of the tables
+  bytes += pair ? (size_t)npos * HG * 4 : (size_t)(HG == 2 ? XP : XW * XW) * HG * 2;
   return bytes;
 }
 
@@ -1325,19 +1333,26 @@ __global__ void attn_bias_table_kernel(const float* __restrict__ table, int tabl
   btab[i] = table[row * H + h] * SHRIMP_LOG2E;
 }
 
-// xtab[x, h] = fp16(btab[clamped LUT position of (dq, dr), h]), x over the
-// unclamped (2 XD + 1)^2 offsets.
+// xtab[p, x, j] = fp16(btab[clamped LUT position of (dq, dr), 2 p + j]), x over
+// the unclamped (2 XD + 1)^2 offsets; the padding (x >= XW*XW) and the missing
+// second head of an odd H are zeros.
 __global__ void attn_xtab_kernel(const float* __restrict__ btab, int H, int M,
                                  unsigned short* __restrict__ xtab) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= XW * XW * H) return;
-  const int x = i / H;
-  const int h = i - x * H;
-  const int dq = x / XW - XD;
-  const int dr = x - (x / XW) * XW - XD;
-  const int W = 2 * M + 1;
-  const int pos = (clampi(dq, M) + M) * W + (clampi(dr, M) + M);
-  xtab[i] = __builtin_bit_cast(unsigned short, (_Float16)btab[pos * H + h]);
+  if (i >= (H + 1) / 2 * XP * 2) return;
+  const int p = i / (XP * 2);
+  const int rem = i - p * XP * 2;
+  const int x = rem >> 1;
+  const int h = 2 * p + (rem & 1);
+  float v = 0.f;
+  if (x < XW * XW && h < H) {
+    const int dq = x / XW - XD;
+    const int dr = x - (x / XW) * XW - XD;
+    const int W = 2 * M + 1;
+    const int pos = (clampi(dq, M) + M) * W + (clampi(dr, M) + M);
+    v = btab[pos * H + h];
+  }
+  xtab[i] = __builtin_bit_cast(unsigned short, (_Float16)v);
 }
 
 // Key table of every position for the staged attention (layout at
@@ -1454,7 +1469,7 @@ extern "C" int shrimp_attn_bias_table(const float* table, int table_rows, int H,
                      as_stream(stream), table, table_rows, H, lut, w * w, tok_row_ct, tok_row_tc,
                      tok_row_tt, btab);
   if (xtab != nullptr) {
-    const int nx = XW * XW * H;
+    const int nx = (H + 1) / 2 * XP * 2;
     hipLaunchKernelGGL(attn_xtab_kernel, dim3((nx + 255) / 256), dim3(256), 0, as_stream(stream),
                        btab, H, lut_m, static_cast<unsigned short*>(xtab));
   }

@@ -119,20 +119,21 @@ def pack_attn_mlp(out_w, out_b, g_attn, ln_w, ln_b, fc1_w, fc1_b, fc2_w, fc2_b, 
 
 
 ATTN_XD = 26  # SHRIMP_ATTN_XD of the C ABI
+ATTN_XP = 2816  # SHRIMP_ATTN_XP: (2 XD + 1)^2 offsets per head pair, padded
 
 
 def attn_bias_table(table: torch.Tensor, lut_u8: torch.Tensor, lut_m: int = CELL_LUT_M):
     """Per-block (BIAS_ROWS, H) table -> (btab, xtab): btab ((2M+1)^2 + 3, H)
-    fp32, the LUT-indexed table with log2(e) folded in; xtab ((2 XD + 1)^2, H)
-    fp16, the same values indexed by unclamped offsets (|dq|, |dr| <= XD)."""
+    fp32, the LUT-indexed table with log2(e) folded in; xtab ((H + 1) // 2,
+    ATTN_XP, 2) fp16, the same values indexed by unclamped offsets (|dq|, |dr|
+    <= XD), head pair major (see xtab_pairs)."""
 
     require_device(table, "attn_bias_table")
     rows, h = table.shape
     w = 2 * lut_m + 1
-    xw = 2 * ATTN_XD + 1
     t32 = table.detach().to(torch.float32).contiguous()
     btab = torch.empty((w * w + 3, h), dtype=torch.float32, device=table.device)
-    xtab = torch.empty((xw * xw, h), dtype=torch.float16, device=table.device)
+    xtab = torch.empty(((h + 1) // 2, ATTN_XP, 2), dtype=torch.float16, device=table.device)
     _lib.check(
         _lib.load().shrimp_attn_bias_table(
             t32.data_ptr(), rows, h, lut_u8.data_ptr(), lut_m, BIAS_CELL_TOKEN_ROW,
@@ -142,6 +143,21 @@ def attn_bias_table(table: torch.Tensor, lut_u8: torch.Tensor, lut_m: int = CELL
         "attn_bias_table",
     )
     return btab, xtab
+
+
+def xtab_pairs(xh: torch.Tensor) -> torch.Tensor:
+    """((2 XD + 1)^2, H) fp16 offset table -> the head pair major layout the
+    kernels read, ((H + 1) // 2, ATTN_XP, 2): entry [p, x, j] is xh[x, 2 p + j],
+    zeros for the padding offsets and the missing second head of an odd H."""
+
+    n, h = xh.shape
+    xw = 2 * ATTN_XD + 1
+    if n != xw * xw:
+        raise ValueError(f"xtab_pairs: {n} offsets, expected {xw * xw}")
+    hp = (h + 1) // 2
+    out = xh.new_zeros((ATTN_XP, 2 * hp))
+    out[:n, :h] = xh
+    return out.view(ATTN_XP, hp, 2).permute(1, 0, 2).contiguous()
 
 
 # ---- raw launches ----------------------------------------------------------------------

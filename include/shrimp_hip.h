@@ -322,8 +322,9 @@ int shrimp_attn_mlp(const shrimp_mlp_args* a, void* stream);
  *       (token q, token k); keys whose mask is 0 get weight exactly 0.
  *   btab is produced by shrimp_attn_bias_table (with log2(e) folded in).
  *   xtab (optional, same source): the LUT re-indexed without clamping over
- *       |dq|, |dr| <= SHRIMP_ATTN_XD, fp16 [(2 XD + 1)^2][H]; positions whose
- *       live cells span <= XD in q and r then index it linearly.
+ *       |dq|, |dr| <= SHRIMP_ATTN_XD, fp16, head pair major
+ *       [(H + 1) / 2][SHRIMP_ATTN_XP][2] (layout at shrimp_attn_bias_table);
+ *       positions whose live cells span <= XD in q and r index it linearly.
  * q, k, v: (B, H, S, dpad) bf16 with head-dim zero padding; o element
  * (b, h, s, e) at o[b*o_sb + h*o_sh + s*o_sr + e], e < d (o_sh = d, o_sr = C
  * gives the (B, S, C) layout out_proj reads; o_sh = S*d, o_sr = d gives
@@ -344,7 +345,7 @@ typedef struct {
   const int32_t* coords; /* (B, S - n_tokens, 2) */
   const uint8_t* mask;   /* (B, S - n_tokens) */
   const float* btab;     /* ((2M+1)^2 + 3, H), log2e folded */
-  const void* xtab;      /* ((2 XD + 1)^2, H) fp16, log2e folded, or NULL */
+  const void* xtab;      /* ((H+1)/2, XP, 2) fp16, log2e folded, or NULL */
   int32_t lut_m, n_tokens;
   void* o;
   int64_t o_sb, o_sh, o_sr;
@@ -412,11 +413,17 @@ int shrimp_attn_staged(const shrimp_attn_args* a, const void* kvf, const int32_t
                        void* stream);
 
 #define SHRIMP_ATTN_XD 26
+/* offsets per head pair in xtab: (2 XD + 1)^2 = 2809 padded to 2816 (11 KiB of
+ * dwords, which the staged kernel copies in whole 1 KiB DMAs) */
+#define SHRIMP_ATTN_XP 2816
 
 /* btab[pos, h] = log2(e) * table[lut[pos], h] for pos < (2M+1)^2 and the 3
  * token rows from table rows tok_rows[0..2]; table (rows, H) fp32.
- * xtab (if not NULL) [x, h] = fp16(btab[clamped pos of (dq, dr)], h) with
- * x = (dq + XD) * (2 XD + 1) + dr + XD. */
+ * xtab (if not NULL), ((H + 1) / 2) * SHRIMP_ATTN_XP * 2 fp16:
+ * xtab[p, x, j] = fp16(btab[clamped pos of (dq, dr)], 2 p + j) with
+ * x = (dq + XD) * (2 XD + 1) + dr + XD < (2 XD + 1)^2; zeros for the padding
+ * x and for j = 1 of the last pair of an odd H. The two heads of a pair share
+ * a dword per offset. */
 int shrimp_attn_bias_table(const float* table, int table_rows, int H, const uint8_t* lut,
                            int lut_m, int tok_row_ct, int tok_row_tc, int tok_row_tt,
                            float* btab, void* xtab, void* stream);
