@@ -1089,6 +1089,61 @@ def test_cfg2_staged_rows_path(cfg2_full):
     assert torch.equal(staged(kn, vn), got)
 
 
+def test_staged_rows_eight_waves():
+    """shrimp_attn_staged over K / V rows past the 64 KiB LDS budget (S = 384:
+    eight waves with a compute unit's LDS), masked cells scattered inside each
+    length and a length of 17: live query rows against the oracle, rows past
+    each length zero, and the same output with NaN in the K / V rows of dead
+    keys (masked cells, rows past the length)."""
+
+    from bench import cfg2_xtab
+    from shrimp import ops
+
+    g = torch.Generator().manual_seed(23)
+    B, H, S, d = 12, 8, 384, 16
+    assert ops.attn_staged_supported(H, S, 16)
+    grid = torch.stack(torch.meshgrid(torch.arange(20), torch.arange(20), indexing="ij"), -1)
+    grid = grid.reshape(-1, 2)
+    coords = torch.stack([grid[torch.randperm(400, generator=g)[:S]] for _ in range(B)])
+    lens = torch.randint(200, S + 1, (B,), generator=g, dtype=torch.int32)
+    lens[0], lens[1] = S, 17
+    inside = torch.arange(S)[None, :] < lens[:, None].long()
+    mask = inside & (torch.rand(B, S, generator=g) > 0.1)
+    q, k, v = (torch.randn(B, H, S, d, generator=g) for _ in range(3))
+    table = torch.randn(33 * 33, H, generator=g) * 0.7
+    btab = (torch.cat([table, torch.zeros(3, H)]) * (1.0 / math.log(2.0))).to(DEV).contiguous()
+    xtab = cfg2_xtab(btab, 16)
+    cd = coords.to(DEV, torch.int32).contiguous()
+    md = mask.to(DEV, torch.uint8).contiguous()
+    ld = lens.to(DEV)
+    meta = torch.empty(B * ops.attn_keys_ints(S), dtype=torch.int32, device=DEV)
+
+    def staged(kt, vt):
+        out = torch.full((B, H, S, d), 5.0, dtype=torch.bfloat16, device=DEV)
+        ops.launch_attn_keys(coords=cd, mask8=md, seq_lens=ld, B=B, S=S, n_tokens=0, meta=meta)
+        ops.launch_attn_staged(
+            q=q.to(DEV, torch.bfloat16).contiguous(), k=kt.to(DEV, torch.bfloat16).contiguous(),
+            v=vt.to(DEV, torch.bfloat16).contiguous(), qkv_sb=H * S * d, qkv_sh=S * d, meta=meta,
+            seq_lens=ld, o=out, o_sb=H * S * d, o_sh=S * d, o_sr=d, B=B, S=S, H=H, d=d, dpad=16,
+            btab=btab, xtab=xtab, lut_m=16, n_tokens=0)
+        return out.cpu()
+
+    print(f"staged rows, eight waves, B={B} S={S}", flush=True)
+    got = staged(k, v)
+    assert torch.isfinite(got.float()).all()
+    for i in range(B):
+        assert (got[i, :, int(lens[i]):] == 0).all(), i
+    want = ofwd.attn_offset_table(bf(q), bf(k), bf(v), coords, mask, table.double(), 16)
+    sel = mask[:, None, :, None].expand_as(want)
+    close(got[sel], want[sel], atol=1e-2, what="staged rows S=384")
+    dead = ~mask[:, None, :, None].expand_as(k)
+    kn, vn = k.clone(), v.clone()
+    kn[dead] = float("nan")
+    vn[dead] = float("nan")
+    print("staged rows, eight waves, NaN in dead keys' rows", flush=True)
+    assert torch.equal(staged(kn, vn), got)
+
+
 @pytest.fixture(scope="module")
 def cfg3_full():
     from shrimp import synthetic
