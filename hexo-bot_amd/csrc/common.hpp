@@ -188,6 +188,14 @@ SHRIMP_DEV int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx
 
 SHRIMP_DEV float xor_shfl(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// max(v, 0) as a signed integer max of the bit pattern: one instruction where
+// fmaxf(v, 0) on a value the compiler cannot prove canonical (an MFMA result)
+// takes two. Equal to fmaxf(v, 0) for every v except a NaN with the sign bit
+// clear, which it passes through (fmaxf returns 0).
+SHRIMP_DEV float relu_bits(float v) {
+  return __builtin_bit_cast(float, max(__builtin_bit_cast(int, v), 0));
+}
+
 // Sum over the 4 lane groups (l/16 = 0..3) sharing the same l % 16.
 SHRIMP_DEV float sum_lane_groups(float v) {
   v += xor_shfl(v, 16);

@@ -197,7 +197,7 @@ SHRIMP_DEV void conv_epilogue(const shrimp_conv_args& a, f32x4 (&acc)[COUT / 16]
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) v[nb][j] = fmaxf(v[nb][j], 0.f);
+          for (int j = 0; j < 4; ++j) v[nb][j] = relu_bits(v[nb][j]);
       }
       float h = 0.f;
 #pragma unroll

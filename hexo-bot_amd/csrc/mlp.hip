@@ -66,20 +66,23 @@ constexpr uint32_t PACK_BYTES = B2_OFF + MC * 4;
 // 5 (h(5) = 2.9e-7): one transcendental and seven fused multiply-adds per
 // value. Against float64 erf-GELU the error is at most 3.8e-6 absolute over
 // [-12, 12] (a tenth of a bf16 rounding step of the output near 0.1), and the
-// kernel rounds the result to bf16 for fc2.
+// kernel rounds the result to bf16 for fc2. The clamp is one med3 and max(x, 0)
+// one integer max (relu_bits): fminf / fmaxf on an MFMA result cost a second
+// instruction each, a canonicalisation of the operand the compiler cannot
+// prove canonical.
 SHRIMP_DEV float gelu_ex2(float x) {
   constexpr float g0 = 1.0001733303070068f, g1 = 1.149885654449463f, g2 = 0.461910218000412f;
   constexpr float g3 = 0.05010765790939331f, g4 = -0.006412093993276358f;
   constexpr float g5 = 0.00037955178413540125f;
   const float ax = fabsf(x);
-  const float a = fminf(ax, 5.0f);
+  const float a = __builtin_amdgcn_fmed3f(ax, 0.0f, 5.0f);
   float g = fmaf(g5, a, g4);
   g = fmaf(g, a, g3);
   g = fmaf(g, a, g2);
   g = fmaf(g, a, g1);
   g = fmaf(g, a, g0);
   const float h = __builtin_amdgcn_exp2f(-g);
-  return fmaf(-ax, h, fmaxf(x, 0.f));
+  return fmaf(-ax, h, relu_bits(x));
 }
 
 SHRIMP_DEV u32x4 lds_frag(const unsigned char* wl, uint32_t base, int ks, int nb, int nbt,
