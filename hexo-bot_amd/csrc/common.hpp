@@ -330,13 +330,16 @@ struct BiasRegs {
 
  private:
   // lanes S .. S + 3 of each 16-lane row, broadcast over the row
+  // (row_newbcast with every row and bank enabled writes every lane, so no
+  // old value is needed: update_dpp with an old value of 0 costs a v_mov of
+  // 0 per broadcast)
   template <int S>
   SHRIMP_DEV static f32x4 bcast4(int v) {
     return f32x4{
-        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x150 + S, 0xF, 0xF, false)),
-        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x151 + S, 0xF, 0xF, false)),
-        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x152 + S, 0xF, 0xF, false)),
-        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, v, 0x153 + S, 0xF, 0xF, false))};
+        __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0x150 + S, 0xF, 0xF, false)),
+        __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0x151 + S, 0xF, 0xF, false)),
+        __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0x152 + S, 0xF, 0xF, false)),
+        __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0x153 + S, 0xF, 0xF, false))};
   }
 };
 
