@@ -1092,9 +1092,9 @@ def test_cfg2_staged_rows_path(cfg2_full):
 def test_staged_rows_eight_waves():
     """shrimp_attn_staged over K / V rows past the 64 KiB LDS budget (S = 384:
     eight waves with a compute unit's LDS), masked cells scattered inside each
-    length and a length of 17: live query rows against the oracle, rows past
-    each length zero, and the same output with NaN in the K / V rows of dead
-    keys (masked cells, rows past the length)."""
+    length, a length of 17 and an empty position: live query rows against the
+    oracle, rows past each length zero, and the same output with NaN in the
+    K / V rows of dead keys (masked cells, rows past the length)."""
 
     from bench import cfg2_xtab
     from shrimp import ops
@@ -1106,7 +1106,7 @@ def test_staged_rows_eight_waves():
     grid = grid.reshape(-1, 2)
     coords = torch.stack([grid[torch.randperm(400, generator=g)[:S]] for _ in range(B)])
     lens = torch.randint(200, S + 1, (B,), generator=g, dtype=torch.int32)
-    lens[0], lens[1] = S, 17
+    lens[0], lens[1], lens[2] = S, 17, 0
     inside = torch.arange(S)[None, :] < lens[:, None].long()
     mask = inside & (torch.rand(B, S, generator=g) > 0.1)
     q, k, v = (torch.randn(B, H, S, d, generator=g) for _ in range(3))
