@@ -58,24 +58,45 @@ SHRIMP_DEV void prep_feats(const void* __restrict__ feats, int nfeat, int64_t ba
     xb[i] = pack_bf16x2(v0, v1);
   }
 }
-template <int DT>
-SHRIMP_DEV void prep_coords(const void* __restrict__ coords, int64_t base, int N,
-                            int32_t* __restrict__ c32, int i0, int step) {
-#pragma unroll 4
-  for (int i = i0; i < N * 2; i += step)
-    c32[base * 2 + i] = (int32_t)load_index_t<DT>(coords, base * 2 + i);
+// Mask, coords, seq_mask and seq_lens of one position: each thread loads a
+// cell's mask byte and coordinates together (CDT: the coords dtype, 0 when
+// coords32 is not wanted) and keeps 1 + the index of its last live cell.
+template <int CDT>
+SHRIMP_DEV int prep_cells(const uint8_t* __restrict__ mask, const void* __restrict__ coords,
+                          int64_t base, int64_t sbase, int N, int n_tokens,
+                          uint8_t* __restrict__ mask8, int32_t* __restrict__ c32,
+                          uint8_t* __restrict__ seq_mask) {
+  int last = 0;
+#pragma unroll 2
+  for (int n = threadIdx.x; n < N; n += blockDim.x) {
+    const int64_t r = base + n;
+    const bool live = mask[r] != 0;
+    if constexpr (CDT != 0) {
+      const int32_t c0 = (int32_t)load_index_t<CDT>(coords, r * 2);
+      const int32_t c1 = (int32_t)load_index_t<CDT>(coords, r * 2 + 1);
+      c32[r * 2] = c0;
+      c32[r * 2 + 1] = c1;
+    }
+    if (mask8) mask8[r] = live ? 1 : 0;
+    if (seq_mask) seq_mask[sbase + n_tokens + n] = live ? 1 : 0;
+    if (live) last = n + 1;
+  }
+  return last;
 }
 
-// A position's flat loops are spread over PREP_PARTS workgroups (blockIdx.y),
-// so each thread has one or two rounds of loads in flight; the first
-// workgroup of a position also writes its token rows and seq_lens.
-constexpr int PREP_PARTS = 4;
+// A position's outputs are written by PREP_PARTS workgroups (blockIdx.y), each
+// with one kind of output, so a thread issues a single round of loads before
+// its stores: parts [0, PREP_FEAT) the stem input rows, the next PREP_IDX the
+// idx rows, the last one the mask, coords, seq_mask and seq_lens.
+constexpr int PREP_FEAT = 4, PREP_IDX = 2, PREP_PARTS = PREP_FEAT + PREP_IDX + 1;
+// prep_csr_kernel spreads its flat loops over PREP_CSR_PARTS workgroups per row
+constexpr int PREP_CSR_PARTS = 4;
 
 // ---- input preparation (model.py:861-863, 884-892; batching.py:264-276) --------
-// One workgroup per position; each output array is written by a flat loop over
-// its elements, so consecutive lanes touch consecutive addresses.
-// The pointers are __restrict__ and the loops unrolled, so each thread keeps
-// several loads in flight instead of one load / wait / store per element.
+// Each output array is written by a flat loop over its elements, so
+// consecutive lanes touch consecutive addresses. The pointers are __restrict__
+// and the loops unrolled, so each thread keeps its loads in flight together
+// instead of one load / wait / store per element.
 __global__ __launch_bounds__(256) void prep_kernel(const void* __restrict__ nbr, int nbr_dt,
                                                    const void* __restrict__ mask,
                                                    const void* __restrict__ coords, int coords_dt,
@@ -88,38 +109,35 @@ __global__ __launch_bounds__(256) void prep_kernel(const void* __restrict__ nbr,
                                                    uint8_t* __restrict__ seq_mask,
                                                    uint16_t* __restrict__ xin) {
   const int b = blockIdx.x;
+  const int part = blockIdx.y;  // uniform over the workgroup
   const int64_t base = (int64_t)b * N;
-  const int i0 = blockIdx.y * blockDim.x + threadIdx.x;
-  const int step = PREP_PARTS * blockDim.x;
-  if (idx) {
-    int32_t* ib = idx + base * 7;
-    if (nbr_dt == SHRIMP_DT_I64) prep_idx<SHRIMP_DT_I64>(nbr, base, N, ib, i0, step);
-    else if (nbr_dt == SHRIMP_DT_I32) prep_idx<SHRIMP_DT_I32>(nbr, base, N, ib, i0, step);
-    else prep_idx<SHRIMP_DT_U16>(nbr, base, N, ib, i0, step);
-  }
-  if (xin) {
+  if (part < PREP_FEAT) {
+    if (!xin) return;
+    const int i0 = part * blockDim.x + threadIdx.x, step = PREP_FEAT * blockDim.x;
     unsigned* xb = reinterpret_cast<unsigned*>(xin + base * 32);
     if (feats_dt == SHRIMP_DT_F32) prep_feats<SHRIMP_DT_F32>(feats, nfeat, base, N, xb, i0, step);
     else if (feats_dt == SHRIMP_DT_F16) prep_feats<SHRIMP_DT_F16>(feats, nfeat, base, N, xb, i0, step);
     else prep_feats<SHRIMP_DT_BF16>(feats, nfeat, base, N, xb, i0, step);
+    return;
   }
-  if (coords32) {
-    if (coords_dt == SHRIMP_DT_I64) prep_coords<SHRIMP_DT_I64>(coords, base, N, coords32, i0, step);
-    else prep_coords<SHRIMP_DT_I32>(coords, base, N, coords32, i0, step);
+  if (part < PREP_FEAT + PREP_IDX) {
+    if (!idx) return;
+    const int i0 = (part - PREP_FEAT) * blockDim.x + threadIdx.x, step = PREP_IDX * blockDim.x;
+    int32_t* ib = idx + base * 7;
+    if (nbr_dt == SHRIMP_DT_I64) prep_idx<SHRIMP_DT_I64>(nbr, base, N, ib, i0, step);
+    else if (nbr_dt == SHRIMP_DT_I32) prep_idx<SHRIMP_DT_I32>(nbr, base, N, ib, i0, step);
+    else prep_idx<SHRIMP_DT_U16>(nbr, base, N, ib, i0, step);
+    return;
   }
-  for (int n = i0; n < N; n += step) {
-    const int64_t r = base + n;
-    const bool live = static_cast<const uint8_t*>(mask)[r] != 0;
-    if (mask8) mask8[r] = live ? 1 : 0;
-    if (seq_mask) seq_mask[(int64_t)b * (n_tokens + N) + n_tokens + n] = live ? 1 : 0;
-  }
-  if (blockIdx.y != 0) return;  // uniform
+  const uint8_t* m = static_cast<const uint8_t*>(mask);
+  const int64_t sbase = (int64_t)b * (n_tokens + N);
+  int last;
+  if (!coords32) last = prep_cells<0>(m, coords, base, sbase, N, n_tokens, mask8, coords32, seq_mask);
+  else if (coords_dt == SHRIMP_DT_I64)
+    last = prep_cells<SHRIMP_DT_I64>(m, coords, base, sbase, N, n_tokens, mask8, coords32, seq_mask);
+  else last = prep_cells<SHRIMP_DT_I32>(m, coords, base, sbase, N, n_tokens, mask8, coords32, seq_mask);
   if (seq_mask)
-    for (int t = threadIdx.x; t < n_tokens; t += blockDim.x)
-      seq_mask[(int64_t)b * (n_tokens + N) + t] = 1;
-  int last = 0;  // 1 + index of the last live cell
-  for (int n = threadIdx.x; n < N; n += blockDim.x)
-    if (static_cast<const uint8_t*>(mask)[base + n] != 0) last = n + 1;
+    for (int t = threadIdx.x; t < n_tokens; t += blockDim.x) seq_mask[sbase + t] = 1;
   if (seq_lens) {
     __shared__ int red[256];
     red[threadIdx.x] = last;
@@ -153,7 +171,7 @@ __global__ __launch_bounds__(256) void prep_csr_kernel(const uint16_t* __restric
   const int n = cnt < 0 ? 0 : (cnt > N ? N : (int)cnt);
   const int64_t base = (int64_t)b * N;
   const int i0 = blockIdx.y * blockDim.x + threadIdx.x;
-  const int step = PREP_PARTS * blockDim.x;
+  const int step = PREP_CSR_PARTS * blockDim.x;
   if (seq_mask && blockIdx.y == 0)
     for (int t = threadIdx.x; t < n_tokens; t += blockDim.x)
       seq_mask[(int64_t)b * (n_tokens + N) + t] = 1;
@@ -675,7 +693,7 @@ extern "C" int shrimp_prep_csr(const void* node_feats, int nfeat, const int16_t*
   SHRIMP_REQUIRE(!coords32 || node_qr, "prep_csr: coords need node_qr");
   SHRIMP_REQUIRE(!xin || (node_feats && nfeat > 0 && nfeat <= 32), "prep_csr: feats (nfeat %d)",
                  nfeat);
-  hipLaunchKernelGGL(prep_csr_kernel, dim3(B, PREP_PARTS), dim3(256), 0, as_stream(stream),
+  hipLaunchKernelGGL(prep_csr_kernel, dim3(B, PREP_CSR_PARTS), dim3(256), 0, as_stream(stream),
                      static_cast<const uint16_t*>(node_feats), nfeat, node_qr, nbr, row_offsets,
                      row0, N, n_tokens, idx, mask8, coords32, seq_lens, seq_mask,
                      static_cast<uint16_t*>(xin));
