@@ -1358,14 +1358,22 @@ __global__ void attn_xtab_kernel(const float* __restrict__ btab, int H, int M,
 // Key table of every position for the staged attention (layout at
 // attn_meta_ints): the classes, coordinates, LINEAR codes, per-block flags
 // and span of the in-kernel setup, once per forward instead of once per
-// (position, head pair, attention block). One workgroup per position.
+// (position, head pair, attention block). One workgroup per position; when
+// `tokens` is given it also writes the position's token rows (as
+// fill_tokens_kernel does) before its key work.
 __global__ __launch_bounds__(256) void attn_keys_kernel(const int32_t* __restrict__ coords,
                                                         const uint8_t* __restrict__ mask,
                                                         const int32_t* __restrict__ seq_lens, int S,
-                                                        int nt, int* __restrict__ meta) {
+                                                        int nt, int* __restrict__ meta,
+                                                        const float* __restrict__ tokens, int C,
+                                                        unsigned short* __restrict__ seq,
+                                                        int64_t seq_sb,
+                                                        unsigned short* __restrict__ tok_lo,
+                                                        int vec4) {
   extern __shared__ int ks[];  // [3][SP]: class, q, r
   __shared__ int red[4][4];
   const int b = blockIdx.x, tid = threadIdx.x;
+  if (tokens) fill_token_rows(b, tokens, nt, C, seq, seq_sb, tok_lo, vec4);
   const int SP = (S + 15) & ~15, NKB = SP / 16, NC = S - nt;
   int L = seq_lens[b];
   SHRIMP_DCHECK(L >= 0 && L <= S, SHRIMP_DBG_SEQ_LEN);
@@ -1575,8 +1583,28 @@ extern "C" int shrimp_attn_keys(const int32_t* coords, const uint8_t* mask, cons
   const int SP = (S + 15) & ~15;
   SHRIMP_REQUIRE(SP <= 4096, "attn_keys: S = %d too large", S);
   hipLaunchKernelGGL(attn_keys_kernel, dim3(B), dim3(256), (size_t)3 * SP * 4, as_stream(stream),
-                     coords, mask, seq_lens, S, n_tokens, meta);
+                     coords, mask, seq_lens, S, n_tokens, meta, nullptr, 0, nullptr, (int64_t)0,
+                     nullptr, 0);
   return check_launch("attn_keys");
+}
+
+extern "C" int shrimp_attn_keys_tokens(const int32_t* coords, const uint8_t* mask,
+                                       const int32_t* seq_lens, int B, int S, int n_tokens,
+                                       int32_t* meta, const float* tokens, int C, void* seq,
+                                       int64_t seq_sb, void* tok_lo, void* stream) {
+  SHRIMP_REQUIRE(B >= 0 && S > 0 && S <= 4096 && n_tokens >= 0 && n_tokens <= S,
+                 "attn_keys_tokens: bad shape (S = %d, at most 4096)", S);
+  SHRIMP_REQUIRE(seq_lens && meta && (n_tokens == S || (coords && mask)),
+                 "attn_keys_tokens: null pointer");
+  const int vec4 = fill_tokens_check(tokens, n_tokens, C, seq, seq_sb, tok_lo);
+  if (vec4 < 0) return vec4;
+  if (B == 0) return SHRIMP_OK;
+  const int SP = (S + 15) & ~15;
+  hipLaunchKernelGGL(attn_keys_kernel, dim3(B), dim3(256), (size_t)3 * SP * 4, as_stream(stream),
+                     coords, mask, seq_lens, S, n_tokens, meta, tokens, C,
+                     static_cast<unsigned short*>(seq), seq_sb, static_cast<unsigned short*>(tok_lo),
+                     vec4);
+  return check_launch("attn_keys_tokens");
 }
 
 // The staged kernel runs four waves per workgroup while its LDS fits the

@@ -80,6 +80,8 @@ int cu_count();
 // kernels' is set in hex_conv.hip), cycles != 0 to record the core clock too;
 // SHRIMP_EINVAL in other builds.
 int attn_phase_set(void* stamps, int cycles);
+int fill_tokens_check(const float* tokens, int n_tokens, int C, const void* seq, int64_t seq_sb,
+                      const void* tok_lo);
 
 // Conv kernel selection: 0 = automatic (small batches: one 64-row tile per
 // workgroup; else big-tile LDS kernel for the 128-channel 7-tap shape, else

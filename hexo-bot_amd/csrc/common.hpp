@@ -166,6 +166,40 @@ SHRIMP_DEV float bf16_bits_to_f32(unsigned short h) {
   return __uint_as_float(((unsigned)h) << 16);
 }
 
+// Token rows of position b: seq[b, t, :] = bf16(tokens[t, :]) and, when tok_lo
+// is given, tok_lo[b, t, :] = bf16(tokens[t, :] - that), by the workgroup's
+// threads. vec4: four elements per thread and iteration (a 16-byte load, 8-byte
+// stores); the host sets it when the element count is a multiple of 4 and the
+// tables and rows are aligned for it. The same arithmetic per element.
+SHRIMP_DEV void fill_token_rows(int b, const float* __restrict__ tokens, int n_tokens, int C,
+                                unsigned short* __restrict__ seq, int64_t seq_sb,
+                                unsigned short* __restrict__ tok_lo, int vec4) {
+  const int n = n_tokens * C;
+  if (vec4) {
+    for (int i = 4 * (int)threadIdx.x; i < n; i += 4 * (int)blockDim.x) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(tokens + i);
+      unsigned short hi[4], lo[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        hi[e] = f32_to_bf16_bits(t[e]);
+        lo[e] = f32_to_bf16_bits(t[e] - bf16_bits_to_f32(hi[e]));
+      }
+      *reinterpret_cast<u32x2*>(seq + (int64_t)b * seq_sb + i) =
+          u32x2{hi[0] | ((unsigned)hi[1] << 16), hi[2] | ((unsigned)hi[3] << 16)};
+      if (tok_lo)
+        *reinterpret_cast<u32x2*>(tok_lo + (int64_t)b * n + i) =
+            u32x2{lo[0] | ((unsigned)lo[1] << 16), lo[2] | ((unsigned)lo[3] << 16)};
+    }
+    return;
+  }
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const float t = tokens[i];
+    const unsigned short hi = f32_to_bf16_bits(t);
+    seq[(int64_t)b * seq_sb + i] = hi;
+    if (tok_lo) tok_lo[(int64_t)b * n + i] = f32_to_bf16_bits(t - bf16_bits_to_f32(hi));
+  }
+}
+
 // ---- MFMA wrappers -------------------------------------------------------------
 
 SHRIMP_DEV f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {

@@ -215,37 +215,10 @@ __global__ __launch_bounds__(256) void prep_csr_kernel(const uint16_t* __restric
   if (seq_lens && blockIdx.y == 0 && threadIdx.x == 0) seq_lens[b] = n_tokens + n;
 }
 
-// vec4: four elements per thread and iteration (a 16-byte load, 8-byte
-// stores); the host sets it when the element count is a multiple of 4 and the
-// tables and rows are aligned for it. The same arithmetic per element.
 __global__ void fill_tokens_kernel(const float* __restrict__ tokens, int n_tokens, int C,
                                    uint16_t* __restrict__ seq, int64_t seq_sb,
                                    uint16_t* __restrict__ tok_lo, int vec4) {
-  const int b = blockIdx.x;
-  const int n = n_tokens * C;
-  if (vec4) {
-    for (int i = 4 * (int)threadIdx.x; i < n; i += 4 * (int)blockDim.x) {
-      const f32x4 t = *reinterpret_cast<const f32x4*>(tokens + i);
-      uint16_t hi[4], lo[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        hi[e] = f32_to_bf16_bits(t[e]);
-        lo[e] = f32_to_bf16_bits(t[e] - bf16_bits_to_f32(hi[e]));
-      }
-      *reinterpret_cast<u32x2*>(seq + (int64_t)b * seq_sb + i) =
-          u32x2{hi[0] | ((unsigned)hi[1] << 16), hi[2] | ((unsigned)hi[3] << 16)};
-      if (tok_lo)
-        *reinterpret_cast<u32x2*>(tok_lo + (int64_t)b * n + i) =
-            u32x2{lo[0] | ((unsigned)lo[1] << 16), lo[2] | ((unsigned)lo[3] << 16)};
-    }
-    return;
-  }
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const float t = tokens[i];
-    const uint16_t hi = f32_to_bf16_bits(t);
-    seq[(int64_t)b * seq_sb + i] = hi;
-    if (tok_lo) tok_lo[(int64_t)b * n + i] = f32_to_bf16_bits(t - bf16_bits_to_f32(hi));
-  }
+  fill_token_rows(blockIdx.x, tokens, n_tokens, C, seq, seq_sb, tok_lo, vec4);
 }
 
 // ---- trunk tail + value heads (model.py:927-935, 990-1002) --------------------
@@ -700,17 +673,26 @@ extern "C" int shrimp_prep_csr(const void* node_feats, int nfeat, const int16_t*
   return check_launch("prep_csr");
 }
 
-extern "C" int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void* seq,
-                                  int64_t seq_sb, void* tok_lo, int B, void* stream) {
-  SHRIMP_REQUIRE(B >= 0 && n_tokens >= 0 && n_tokens <= 4096 && C > 0 && C <= 4096,
-                 "fill_tokens: bad sizes (B %d, tokens %d, C %d)", B, n_tokens, C);
-  if (B == 0 || n_tokens == 0) return SHRIMP_OK;
+// Checks the token-row arguments and returns the vec4 switch of
+// fill_token_rows (0 or 1), or SHRIMP_EINVAL with the error set.
+int shrimp::fill_tokens_check(const float* tokens, int n_tokens, int C, const void* seq,
+                              int64_t seq_sb, const void* tok_lo) {
+  SHRIMP_REQUIRE(n_tokens >= 0 && n_tokens <= 4096 && C > 0 && C <= 4096,
+                 "fill_tokens: bad sizes (tokens %d, C %d)", n_tokens, C);
   SHRIMP_REQUIRE(tokens && seq, "fill_tokens: null pointer");
   SHRIMP_REQUIRE(strides_ok({seq_sb}) && seq_sb >= (int64_t)n_tokens * C,
                  "fill_tokens: position stride %lld", (long long)seq_sb);
   const int n = n_tokens * C;
-  const int vec4 = n % 4 == 0 && seq_sb % 4 == 0 && (uintptr_t)tokens % 16 == 0 &&
-                   (uintptr_t)seq % 8 == 0 && (uintptr_t)tok_lo % 8 == 0;
+  return n % 4 == 0 && seq_sb % 4 == 0 && (uintptr_t)tokens % 16 == 0 &&
+         (uintptr_t)seq % 8 == 0 && (uintptr_t)tok_lo % 8 == 0;
+}
+
+extern "C" int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void* seq,
+                                  int64_t seq_sb, void* tok_lo, int B, void* stream) {
+  SHRIMP_REQUIRE(B >= 0, "fill_tokens: bad batch %d", B);
+  const int vec4 = fill_tokens_check(tokens, n_tokens, C, seq, seq_sb, tok_lo);
+  if (vec4 < 0) return vec4;
+  if (B == 0 || n_tokens == 0) return SHRIMP_OK;
   hipLaunchKernelGGL(fill_tokens_kernel, dim3(B), dim3(256), 0, as_stream(stream), tokens,
                      n_tokens, C, static_cast<uint16_t*>(seq), seq_sb,
                      static_cast<uint16_t*>(tok_lo), vec4);

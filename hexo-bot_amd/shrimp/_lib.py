@@ -157,6 +157,11 @@ SIGNATURES: dict = {
     "shrimp_attn_qkv_kvf": (ctypes.c_int, [ctypes.POINTER(QkvArgs), _vp, _vp]),
     "shrimp_attn_keys_bytes": (ctypes.c_size_t, [ctypes.c_int]),
     "shrimp_attn_keys": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+    "shrimp_attn_keys_tokens": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp, ctypes.c_int, _vp, _i64,
+         _vp, _vp],
+    ),
     "shrimp_attn_staged_supported": (ctypes.c_int, [ctypes.c_int] * 3),
     "shrimp_attn_staged": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _vp, _vp, _vp]),
     "shrimp_attn_qkv_pack_bytes": (ctypes.c_size_t, [ctypes.c_int]),

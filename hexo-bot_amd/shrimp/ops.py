@@ -336,13 +336,24 @@ def attn_keys_ints(S: int) -> int:
     return int(_lib.load().shrimp_attn_keys_bytes(S)) // 4
 
 
-def launch_attn_keys(*, coords, mask8, seq_lens, B, S, n_tokens, meta, stream=None):
-    """Key table of every position for the staged attention (once per forward)."""
+def launch_attn_keys(*, coords, mask8, seq_lens, B, S, n_tokens, meta, tokens=None, seq=None,
+                     seq_sb=0, tok_lo=None, stream=None):
+    """Key table of every position for the staged attention (once per forward).
+    With ``tokens`` ((n_tokens, C) fp32) the same launch also writes the token
+    rows of ``seq`` (positions ``seq_sb`` elements apart) and ``tok_lo``, as
+    shrimp_fill_tokens does."""
 
     s = _lib.stream_handle() if stream is None else stream
-    _lib.check(_lib.load().shrimp_attn_keys(
-        _lib.ptr(coords), _lib.ptr(mask8), seq_lens.data_ptr(), B, S, n_tokens, meta.data_ptr(), s),
-        "attn_keys")
+    lib = _lib.load()
+    if tokens is None:
+        _lib.check(lib.shrimp_attn_keys(
+            _lib.ptr(coords), _lib.ptr(mask8), seq_lens.data_ptr(), B, S, n_tokens,
+            meta.data_ptr(), s), "attn_keys")
+        return
+    _lib.check(lib.shrimp_attn_keys_tokens(
+        _lib.ptr(coords), _lib.ptr(mask8), seq_lens.data_ptr(), B, S, n_tokens, meta.data_ptr(),
+        tokens.data_ptr(), tokens.shape[-1], seq.data_ptr(), seq_sb, _lib.ptr(tok_lo), s),
+        "attn_keys_tokens")
 
 
 def attn_staged_supported(H: int, S: int, dpad: int) -> bool:

@@ -621,11 +621,6 @@ class HipForward:
         # the token rows' residual stream is seq (bf16) + tok_lo (bf16): the
         # rounding remainder of every update, kept by the residual kernels
         tok_lo = torch.empty((B, NUM_TOKENS, C), dtype=bf, device=dev)
-        _lib.check(
-            lib.shrimp_fill_tokens(P.tokens.data_ptr(), NUM_TOKENS, C, seq.data_ptr(), S * C,
-                                   tok_lo.data_ptr(), B, st),
-            "fill_tokens",
-        )
         cells = seq[:, NUM_TOKENS:]
         y1 = torch.empty((B, N, C), dtype=bf, device=dev)
         attn_fused = (P.fused_qkv and self.use_fused_qkv and self.use_fused_attn
@@ -647,9 +642,18 @@ class HipForward:
         conv_common = dict(idx=idx, taps=7, idx_stride=7, mask8=mask8, B=B, N=N, stream=st)
         self._mark("start")
         if staged:
+            # the key table and the token rows in one launch
             launch_attn_keys(coords=coords32, mask8=mask8, seq_lens=seq_lens, B=B, S=S,
-                             n_tokens=NUM_TOKENS, meta=meta, stream=st)
+                             n_tokens=NUM_TOKENS, meta=meta, tokens=P.tokens, seq=seq,
+                             seq_sb=S * C, tok_lo=tok_lo, stream=st)
             self._mark("attn_keys")
+        else:
+            _lib.check(
+                lib.shrimp_fill_tokens(P.tokens.data_ptr(), NUM_TOKENS, C, seq.data_ptr(), S * C,
+                                       tok_lo.data_ptr(), B, st),
+                "fill_tokens",
+            )
+            self._mark("fill_tokens")
         launch_conv(
             x=xin, x_sb=N * 32, x_sn=32, wpack=P.stem.w, bias=P.stem.b, cin_pad=32, cout=C,
             ln_w=P.stem.lnw, ln_b=P.stem.lnb, eps=P.stem.eps, relu=True,

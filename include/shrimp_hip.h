@@ -407,6 +407,13 @@ int shrimp_attn_fused(const shrimp_attn_args* a, const shrimp_attn_proj_args* p,
 size_t shrimp_attn_keys_bytes(int S);
 int shrimp_attn_keys(const int32_t* coords, const uint8_t* mask, const int32_t* seq_lens, int B,
                      int S, int n_tokens, int32_t* meta, void* stream);
+/* shrimp_attn_keys and shrimp_fill_tokens(tokens, n_tokens, C, seq, seq_sb,
+ * tok_lo, B) in one launch, with the same outputs and argument rules: the
+ * forward writes its token rows and key table together (neither has a
+ * counterpart in the reference; the token rows are model.py:905-926). */
+int shrimp_attn_keys_tokens(const int32_t* coords, const uint8_t* mask, const int32_t* seq_lens,
+                            int B, int S, int n_tokens, int32_t* meta, const float* tokens, int C,
+                            void* seq, int64_t seq_sb, void* tok_lo, void* stream);
 int shrimp_attn_qkv_kvf(const shrimp_qkv_args* a, void* kvf, void* stream);
 int shrimp_attn_staged_supported(int H, int S, int dpad);
 int shrimp_attn_staged(const shrimp_attn_args* a, const void* kvf, const int32_t* meta,

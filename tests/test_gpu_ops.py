@@ -1192,3 +1192,59 @@ def test_cfg3_raytap_full_shape(cfg3_full):
     want = ofwd.raytap_conv(bf(x[rows]), ridx, mask[rows], bf(w), bias.double())
     close(full[rows], want, what="cfg3 B=1024")
     assert torch.equal(full[rows], run(rows)[0])
+
+
+def test_attn_keys_tokens_equals_separate_launches():
+    """shrimp_attn_keys_tokens writes the same key table as shrimp_attn_keys
+    and the same token rows as shrimp_fill_tokens (both vec4 and scalar token
+    paths), and leaves the cell rows alone; bad token arguments are refused
+    before anything runs."""
+
+    from shrimp import _lib, ops
+
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(11)
+    for B, N, C, off in ((37, 61, 128, 0), (5, 20, 24, 1)):
+        nt = 4
+        S = N + nt
+        mask = (torch.rand(B, N, generator=g) < 0.7).to(torch.uint8)
+        mask[1] = 0  # a position with no live cell
+        coords = torch.randint(-9, 9, (B, N, 2), generator=g, dtype=torch.int32)
+        last = torch.where(mask.bool(), torch.arange(1, N + 1), torch.zeros(N, dtype=torch.int64))
+        lens = (nt + last.max(1).values).to(torch.int32)
+        cd, md, ld = coords.to(DEV), mask.to(DEV), lens.to(DEV)
+        # off = 1: tokens one float into an allocation (not 16-byte aligned: scalar path)
+        tok = torch.randn(nt * C + off, generator=g).to(DEV)[off:].view(nt, C)
+        out = {}
+        for fused in (False, True):
+            print(f"attn_keys_tokens B={B} N={N} C={C} off={off} fused={fused}", flush=True)
+            meta = torch.full((B, ops.attn_keys_ints(S)), -7, dtype=torch.int32, device=DEV)
+            seq = torch.full((B, S, C), 3.0, dtype=torch.bfloat16, device=DEV)
+            lo = torch.full((B, nt, C), 3.0, dtype=torch.bfloat16, device=DEV)
+            if fused:
+                ops.launch_attn_keys(coords=cd, mask8=md, seq_lens=ld, B=B, S=S, n_tokens=nt,
+                                     meta=meta, tokens=tok, seq=seq, seq_sb=S * C, tok_lo=lo)
+            else:
+                ops.launch_attn_keys(coords=cd, mask8=md, seq_lens=ld, B=B, S=S, n_tokens=nt,
+                                     meta=meta)
+                _lib.check(lib.shrimp_fill_tokens(tok.data_ptr(), nt, C, seq.data_ptr(), S * C,
+                                                  lo.data_ptr(), B, _lib.stream_handle()),
+                           "fill_tokens")
+            torch.cuda.synchronize()
+            out[fused] = (meta.cpu(), seq.cpu(), lo.cpu())
+        for a, b in zip(out[False], out[True]):
+            assert torch.equal(a, b)
+        seq = out[True][1].float()
+        assert torch.equal(seq[:, :nt], tok.cpu().to(torch.bfloat16).float().expand(B, nt, C))
+        assert (seq[:, nt:] == 3.0).all()
+        lo = out[True][2].float()
+        assert torch.equal(lo, (tok.cpu() - seq[0, :nt]).to(torch.bfloat16).float().expand(B, nt, C))
+    meta = torch.empty((2, ops.attn_keys_ints(8)), dtype=torch.int32, device=DEV)
+    seq = torch.empty((2, 8, 16), dtype=torch.bfloat16, device=DEV)
+    ln = torch.full((2,), 4, dtype=torch.int32, device=DEV)
+    tok = torch.zeros((4, 16), device=DEV)
+    # a position stride shorter than the token rows is refused
+    assert lib.shrimp_attn_keys_tokens(None, None, ln.data_ptr(), 2, 4, 4, meta.data_ptr(),
+                                       tok.data_ptr(), 16, seq.data_ptr(), 16, None,
+                                       _lib.stream_handle()) == -1
+    assert "position stride" in lib.shrimp_last_error().decode()
