@@ -1596,7 +1596,7 @@ extern "C" int shrimp_attn_keys_tokens(const int32_t* coords, const uint8_t* mas
                  "attn_keys_tokens: bad shape (S = %d, at most 4096)", S);
   SHRIMP_REQUIRE(seq_lens && meta && (n_tokens == S || (coords && mask)),
                  "attn_keys_tokens: null pointer");
-  const int vec4 = fill_tokens_check(tokens, n_tokens, C, seq, seq_sb, tok_lo);
+  const int vec4 = fill_tokens_check(tokens, n_tokens, C, seq, seq_sb, tok_lo, B);
   if (vec4 < 0) return vec4;
   if (B == 0) return SHRIMP_OK;
   const int SP = (S + 15) & ~15;

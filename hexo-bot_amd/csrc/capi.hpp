@@ -81,7 +81,7 @@ int cu_count();
 // SHRIMP_EINVAL in other builds.
 int attn_phase_set(void* stamps, int cycles);
 int fill_tokens_check(const float* tokens, int n_tokens, int C, const void* seq, int64_t seq_sb,
-                      const void* tok_lo);
+                      const void* tok_lo, int B);
 
 // Conv kernel selection: 0 = automatic (small batches: one 64-row tile per
 // workgroup; else big-tile LDS kernel for the 128-channel 7-tap shape, else

@@ -674,11 +674,13 @@ extern "C" int shrimp_prep_csr(const void* node_feats, int nfeat, const int16_t*
 }
 
 // Checks the token-row arguments and returns the vec4 switch of
-// fill_token_rows (0 or 1), or SHRIMP_EINVAL with the error set.
+// fill_token_rows (0 or 1), or SHRIMP_EINVAL with the error set. With no rows
+// to write (B or n_tokens 0) only the sizes are checked.
 int shrimp::fill_tokens_check(const float* tokens, int n_tokens, int C, const void* seq,
-                              int64_t seq_sb, const void* tok_lo) {
-  SHRIMP_REQUIRE(n_tokens >= 0 && n_tokens <= 4096 && C > 0 && C <= 4096,
-                 "fill_tokens: bad sizes (tokens %d, C %d)", n_tokens, C);
+                              int64_t seq_sb, const void* tok_lo, int B) {
+  SHRIMP_REQUIRE(B >= 0 && n_tokens >= 0 && n_tokens <= 4096 && C > 0 && C <= 4096,
+                 "fill_tokens: bad sizes (B %d, tokens %d, C %d)", B, n_tokens, C);
+  if (B == 0 || n_tokens == 0) return 0;
   SHRIMP_REQUIRE(tokens && seq, "fill_tokens: null pointer");
   SHRIMP_REQUIRE(strides_ok({seq_sb}) && seq_sb >= (int64_t)n_tokens * C,
                  "fill_tokens: position stride %lld", (long long)seq_sb);
@@ -689,8 +691,7 @@ int shrimp::fill_tokens_check(const float* tokens, int n_tokens, int C, const vo
 
 extern "C" int shrimp_fill_tokens(const float* tokens, int n_tokens, int C, void* seq,
                                   int64_t seq_sb, void* tok_lo, int B, void* stream) {
-  SHRIMP_REQUIRE(B >= 0, "fill_tokens: bad batch %d", B);
-  const int vec4 = fill_tokens_check(tokens, n_tokens, C, seq, seq_sb, tok_lo);
+  const int vec4 = fill_tokens_check(tokens, n_tokens, C, seq, seq_sb, tok_lo, B);
   if (vec4 < 0) return vec4;
   if (B == 0 || n_tokens == 0) return SHRIMP_OK;
   hipLaunchKernelGGL(fill_tokens_kernel, dim3(B), dim3(256), 0, as_stream(stream), tokens,

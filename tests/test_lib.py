@@ -146,6 +146,17 @@ def test_bad_arguments_fail_with_message(lib):
                          re_sn=12, g_sn=7)
     assert lib.shrimp_conv_ln_raytap(ctypes.byref(rt), None) == -1
     assert b"corb=12" in lib.shrimp_last_error()
+    # token rows: nothing to write takes no pointers; a position stride shorter
+    # than the token rows is refused, by the key-table launch that writes them too
+    assert lib.shrimp_fill_tokens(None, 4, 128, None, 0, None, 0, None) == 0
+    assert lib.shrimp_fill_tokens(None, 0, 128, None, 0, None, 3, None) == 0
+    assert lib.shrimp_fill_tokens(None, 4, 128, None, 0, None, 3, None) == -1
+    assert b"null pointer" in lib.shrimp_last_error()
+    assert lib.shrimp_fill_tokens(16, 4, 128, 16, 256, None, 3, None) == -1
+    assert b"position stride" in lib.shrimp_last_error()
+    assert lib.shrimp_attn_keys_tokens(16, 16, 16, 3, 68, 4, 16, 16, 128, 16, 256, None,
+                                       None) == -1
+    assert b"position stride" in lib.shrimp_last_error()
 
 
 def test_variant_switches(lib):
